@@ -1,0 +1,178 @@
+/*
+ * ns2.h -- C ABI of the MI355X (gfx950) kernel library for one Nanosaur2 DiT pass.
+ *
+ * This library replaces the WebGPU runtime and the WGSL kernels behind the reference's
+ * ops layer (app/gpu/device.js, app/gpu/ops.js, app/gpu/kernels.js, app/gpu/gemm.js).
+ * A Node.js N-API addon (nanosaur2-web_amd/addon/ns2_addon.cc) exposes exactly these
+ * entry points to the JavaScript host; Python binds them through ctypes.
+ *
+ * Conventions
+ *  - Every entry point returns an int status: NS2_OK (0) or an error code; the message of
+ *    the last error on the calling thread is returned by ns2_last_error().
+ *  - Pointers named like tensors are DEVICE pointers (from ns2_malloc / ns2_pool_get, or
+ *    any other HIP device allocation). Host pointers are only taken by ns2_h2d / ns2_d2h.
+ *  - Activations are fp32, row-major. Strides (ld*) and offsets (*Off) are in ELEMENTS,
+ *    exactly as in the reference's dispatch parameters.
+ *  - All launches are asynchronous and ordered on one HIP stream (ns2_set_stream; the
+ *    default is the null stream). ns2_sync / ns2_d2h wait for completion.
+ *  - int8 weights are "int8_tensorwise + convrot": W_q int8 [N, K] row-major with one fp32
+ *    scale per output row; the layer computes (x H) W_q^T diag(scale), where H is the
+ *    normalized 256-point regular Hadamard matrix applied per 256-feature group
+ *    (tools/quant.py:21-64).
+ *  - bf16 weights are raw bfloat16 bit patterns [N, K] row-major (uint16_t).
+ */
+#ifndef NS2_H
+#define NS2_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------------------ */
+#define NS2_OK 0
+#define NS2_ERR_INVALID 1 /* bad argument or unsupported shape/alignment */
+#define NS2_ERR_HIP 2     /* HIP runtime / launch error */
+#define NS2_ERR_OOM 3     /* device allocation failed */
+#define NS2_ERR_STATE 4   /* library not initialised */
+
+/* activation codes (gemm.js:163, kernels.js:9-17) */
+#define NS2_ACT_NONE 0
+#define NS2_ACT_SILU 1
+#define NS2_ACT_GELU_TANH 2
+
+/* elementwise op codes (kernels.js:496-518) */
+#define NS2_EW_ADD 0
+#define NS2_EW_SUB 1
+#define NS2_EW_SILU 2
+#define NS2_EW_COPY 3
+
+/* ---- runtime: replaces GPU / BufferPool / Profiler of app/gpu/device.js -------------- */
+
+/* GPU.create (app/gpu/device.js:61-81): select and initialise a device. */
+int ns2_init(int device);
+/* Message of the last failed call on this thread ("" if none). */
+const char* ns2_last_error(void);
+/* gpu.info (app/gpu/device.js:77): device name, compute units, HBM bytes. */
+int ns2_device_info(char* name, size_t cap, int* compute_units, size_t* hbm_bytes);
+/* Use a caller-owned hipStream_t for every later launch (NULL = null stream). */
+int ns2_set_stream(void* hip_stream);
+void* ns2_get_stream(void);
+
+/* GPU.upload (app/gpu/device.js:134-139): persistent (non-pooled) device buffer. */
+int ns2_malloc(void** ptr, size_t bytes);
+int ns2_free(void* ptr);
+/* BufferPool.round (app/gpu/device.js:33-39): 1/8-power-of-two size buckets, >= 256 B. */
+size_t ns2_pool_round(size_t bytes);
+/* BufferPool.get (app/gpu/device.js:40-48); *rounded receives the bucket size. */
+int ns2_pool_get(size_t bytes, void** ptr, size_t* rounded);
+/* BufferPool.put / Tensor.release (app/gpu/device.js:20-23, 49-52). */
+int ns2_pool_put(void* ptr, size_t rounded);
+/* BufferPool.trim (app/gpu/device.js:53-56). */
+int ns2_pool_trim(void);
+/* BufferPool.allocated / .peak (app/gpu/device.js:30-31). */
+int ns2_pool_stats(size_t* allocated, size_t* peak);
+
+/* GPU.write (app/gpu/device.js:122-131): host -> device, ordered on the stream. */
+int ns2_h2d(void* dst, const void* src, size_t bytes);
+/* GPU.read (app/gpu/device.js:141-154): device -> host, waits for prior work. */
+int ns2_d2h(void* dst, const void* src, size_t bytes);
+/* GPU.sync (app/gpu/device.js:218-222): wait for all queued work, surface errors. */
+int ns2_sync(void);
+/* Fill count 32-bit words with value (a kernel, safe inside graph capture).
+ * ops.zero (app/gpu/ops.js:89-93) is value = 0. */
+int ns2_fill_u32(void* dst, uint32_t value, size_t count);
+
+/* Profiler (app/gpu/device.js:234-288): stream-ordered timing events. */
+int ns2_event_create(void** ev);
+int ns2_event_record(void* ev);
+int ns2_event_elapsed(void* start, void* end, float* ms);
+int ns2_event_destroy(void* ev);
+
+/* ---- ConvRot rotation --------------------------------------------------------------- */
+
+/* ops.rotate + hadamardShader (app/gpu/ops.js:38-44, app/gpu/kernels.js:378-407):
+ * y = x H per contiguous group of 256 fp32 values, groups = size / 256. y may equal x. */
+int ns2_hadamard256(const float* x, float* y, long long groups);
+/* Same rotation on a strided [rows, cols] view (cols % 256 == 0), written as fp16
+ * (the pre-rotated `xr` operand of ns2_linear_i8, ldy in fp16 elements). */
+int ns2_rotate_f16(const float* x, int ldx, uint16_t* y, int ldy, int rows, int cols);
+
+/* ---- linear layers (ops.linear, app/gpu/ops.js:50-66; runMatmul :14-32;
+ *      matmulShader epilogue app/gpu/gemm.js:159-164) -------------------------------------
+ * C[cOff + m*ldc + n] (=|+=) epilogue(alpha * sum_k A[m,k] W[n,k]) for m < M, n < N with
+ *   r = acc*alpha; r *= scale[n] (int8 only); r += bias[n]; r += add[m*N + n]; r = act(r);
+ *   resid == 0: C = r;  resid != 0 && gate == NULL: C += r;  else C += gate[gOff + n] * r.
+ * bias, add and gate may be NULL. */
+
+/* int8 ConvRot weights. a_fmt selects the activation operand:
+ *   a_fmt = 0: A is fp32 [M, lda], NOT rotated; the call rotates it (ops.linear without xr).
+ *   a_fmt = 1: A is fp16 [M, lda] already rotated (ops.linear with opts.xr).
+ * Requires K % 256 == 0. */
+int ns2_linear_i8(const void* A, int a_fmt, int lda, const int8_t* W, const float* scale,
+                  const float* bias, const float* add, float* C, int M, int N, int K, int ldc,
+                  long long cOff, float alpha, int act, int resid, const float* gate,
+                  long long gOff);
+/* bf16 weights (gemm.js:98-118), fp32 activations [M, lda]. Requires K % 16 == 0. */
+int ns2_linear_bf16(const float* A, int lda, const uint16_t* W, const float* bias,
+                    const float* add, float* C, int M, int N, int K, int ldc, long long cOff,
+                    float alpha, int act, int resid, const float* gate, long long gOff);
+
+/* ---- attention (ops.attention, app/gpu/ops.js:199-209; flashAttentionShader,
+ *      app/gpu/kernels.js:119-305) ----------------------------------------------------------
+ * For every batch element b and head h < H, with q_i = Q[qOff + b*qBatch + i*ldq + h*D ..],
+ * k_j, v_j likewise and
+ *   s_ij = scale * <q_i, k_j> + (j >= biasStart ? key_bias[b*biasBatch + j - biasStart] : 0)
+ *   O[oOff + b*oBatch + i*ldo + h*D ..] = sum_j softmax_j(s_ij) v_j      (non-causal, group 1)
+ * Optional fused prologue, applied to the operands before the product (the work the DiT
+ * does with headNorm, app/gpu/kernels.js:307-342, app/models/nanosaur2.js:199-204):
+ *   q_norm / k_norm: per-head RMSNorm x * rsqrt(mean x^2 + eps) * w[D] on every q / k row;
+ *   rope_cs: split-half RoPE (pair i, i + D/2) on q rows and k rows with index < rope_rows,
+ *            cos at rope_cs[row*D/2 + i], sin at rope_cs[sin_off + row*D/2 + i].
+ * key_bias may be NULL. D must be 32, 64, 96 or 128. */
+int ns2_attention(const float* q, const float* k, const float* v, float* o, int batch,
+                  int Lq, int Lk, int H, int D, int ldq, int ldk, int ldv, int ldo,
+                  long long qOff, long long kOff, long long vOff, long long oOff,
+                  long long qBatch, long long kBatch, long long vBatch, long long oBatch,
+                  float scale, const float* key_bias, int biasStart, long long biasBatch,
+                  const float* q_norm, const float* k_norm, float eps, const float* rope_cs,
+                  long long sin_off, int rope_rows);
+
+/* ---- row kernels ---------------------------------------------------------------------- */
+
+/* ops.headNorm + headNormShader (app/gpu/ops.js:133-138, app/gpu/kernels.js:307-342):
+ * in place on X[(rowOff + l)*ld + colOff + h*D ..] for l < L, h < H; cs may be NULL. */
+int ns2_head_norm(float* X, const float* w, int L, int H, int D, int ld, long long colOff,
+                  long long rowOff, const float* cs, long long sinOff, float eps);
+/* ops.normMod + normModShader (app/gpu/ops.js:121-129, app/gpu/kernels.js:82-117):
+ * y = norm(x) * (1 + mod[scaleOff + c]) + mod[shiftOff + c]; weight != NULL: RMSNorm * w,
+ * weight == NULL: LayerNorm without affine. */
+int ns2_norm_mod(const float* x, const float* mod, long long shiftOff, long long scaleOff,
+                 int rows, int cols, const float* weight, float eps, float* y);
+/* ns2_norm_mod followed by the ConvRot rotation, written as fp16 (cols % 256 == 0):
+ * the pre-rotated input of the int8 linear that consumes it. */
+int ns2_norm_mod_rotate_f16(const float* x, const float* mod, long long shiftOff,
+                            long long scaleOff, int rows, int cols, const float* weight,
+                            float eps, uint16_t* y);
+/* ops.glu + gluShader (app/gpu/ops.js:141-148, app/gpu/kernels.js:344-360):
+ * y[r, j] = act(x[r, j]) * x[r, I + j] for x [rows, 2I]. */
+int ns2_glu(const float* x, float* y, int rows, int I, int act);
+/* ns2_glu followed by the ConvRot rotation, written as fp16 (I % 256 == 0). */
+int ns2_glu_rotate_f16(const float* x, uint16_t* y, int rows, int I, int act);
+/* ops.elementwise (app/gpu/ops.js:179-185, kernels.js:496-518): op in NS2_EW_*;
+ * b is ignored for silu/copy. */
+int ns2_elementwise(int op, const float* a, const float* b, float* y, long long n);
+/* ops.accumulate (app/gpu/ops.js:188-192): y += a. */
+int ns2_accumulate(float* y, const float* a, long long n);
+/* ops.rowSum (app/gpu/ops.js:151-156, kernels.js:362-376): y[n] = scale*sum_r w[r] x[r, n]. */
+int ns2_row_sum(const float* x, const float* w, float* y, int rows, int N, float scale);
+/* ops.rmsnorm (app/gpu/ops.js:111-117, kernels.js:60-80): y = x * rsqrt(mean x^2 + eps) * w. */
+int ns2_rmsnorm(const float* x, const float* w, float* y, int rows, int cols, float eps);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NS2_H */

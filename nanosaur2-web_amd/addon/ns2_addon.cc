@@ -1,0 +1,502 @@
+// Node.js N-API addon over the ns2 C ABI (include/ns2.h).
+//
+// Device buffers cross into JavaScript as BigInt addresses; sizes, strides and offsets as
+// Numbers; null/undefined stands for a NULL pointer. Every wrapper calls exactly one C entry
+// point and turns a non-zero status into a thrown JS Error carrying ns2_last_error(), the
+// way the reference's WebGPU runtime surfaces validation and device-loss errors
+// (app/gpu/device.js:97-102, 171, 224-231).
+#include <node_api.h>
+#include <stdint.h>
+#include <string.h>
+
+#include <string>
+
+#include "ns2.h"
+
+namespace {
+
+struct Ctx {
+  napi_env env;
+  napi_value* argv;
+  size_t argc;
+  bool failed = false;
+
+  void fail(const std::string& msg) {
+    if (!failed) napi_throw_error(env, nullptr, msg.c_str());
+    failed = true;
+  }
+  napi_valuetype type(size_t i) {
+    napi_valuetype t = napi_undefined;
+    if (i < argc) napi_typeof(env, argv[i], &t);
+    return t;
+  }
+  void* ptr(size_t i) {
+    napi_valuetype t = type(i);
+    if (t == napi_null || t == napi_undefined) return nullptr;
+    if (t != napi_bigint) {
+      fail("argument " + std::to_string(i) + ": expected a BigInt device address or null");
+      return nullptr;
+    }
+    uint64_t v = 0;
+    bool lossless = true;
+    napi_get_value_bigint_uint64(env, argv[i], &v, &lossless);
+    return reinterpret_cast<void*>(static_cast<uintptr_t>(v));
+  }
+  int64_t i64(size_t i) {
+    napi_valuetype t = type(i);
+    if (t == napi_bigint) {
+      int64_t v = 0;
+      bool lossless = true;
+      napi_get_value_bigint_int64(env, argv[i], &v, &lossless);
+      return v;
+    }
+    if (t != napi_number) {
+      fail("argument " + std::to_string(i) + ": expected a number");
+      return 0;
+    }
+    int64_t v = 0;
+    napi_get_value_int64(env, argv[i], &v);
+    return v;
+  }
+  int i32(size_t i) { return static_cast<int>(i64(i)); }
+  double f64(size_t i) {
+    if (type(i) != napi_number) {
+      fail("argument " + std::to_string(i) + ": expected a number");
+      return 0;
+    }
+    double v = 0;
+    napi_get_value_double(env, argv[i], &v);
+    return v;
+  }
+  float f32(size_t i) { return static_cast<float>(f64(i)); }
+};
+
+template <size_t N>
+bool get_args(napi_env env, napi_callback_info info, napi_value (&argv)[N], size_t* argc) {
+  *argc = N;
+  return napi_get_cb_info(env, info, argc, argv, nullptr, nullptr) == napi_ok;
+}
+
+napi_value undef(napi_env env) {
+  napi_value u;
+  napi_get_undefined(env, &u);
+  return u;
+}
+
+napi_value check(napi_env env, Ctx& c, int rc) {
+  if (c.failed) return nullptr;
+  if (rc != NS2_OK) {
+    napi_throw_error(env, nullptr, ns2_last_error());
+    return nullptr;
+  }
+  return undef(env);
+}
+
+napi_value bigint(napi_env env, void* p) {
+  napi_value v;
+  napi_create_bigint_uint64(env, reinterpret_cast<uintptr_t>(p), &v);
+  return v;
+}
+
+napi_value number(napi_env env, double d) {
+  napi_value v;
+  napi_create_double(env, d, &v);
+  return v;
+}
+
+#define ARGS(n)              \
+  napi_value argv[n];        \
+  size_t argc;               \
+  get_args(env, info, argv, &argc); \
+  Ctx c{env, argv, argc};
+
+// ---- runtime ------------------------------------------------------------------------------
+
+napi_value Init(napi_env env, napi_callback_info info) {
+  ARGS(1);
+  int dev = c.type(0) == napi_number ? c.i32(0) : 0;
+  return check(env, c, ns2_init(dev));
+}
+
+napi_value DeviceInfo(napi_env env, napi_callback_info info) {
+  char name[256];
+  int cus = 0;
+  size_t hbm = 0;
+  if (ns2_device_info(name, sizeof(name), &cus, &hbm) != NS2_OK) {
+    napi_throw_error(env, nullptr, ns2_last_error());
+    return nullptr;
+  }
+  napi_value o, s;
+  napi_create_object(env, &o);
+  napi_create_string_utf8(env, name, NAPI_AUTO_LENGTH, &s);
+  napi_set_named_property(env, o, "name", s);
+  napi_set_named_property(env, o, "computeUnits", number(env, cus));
+  napi_set_named_property(env, o, "hbmBytes", number(env, (double)hbm));
+  return o;
+}
+
+napi_value Malloc(napi_env env, napi_callback_info info) {
+  ARGS(1);
+  size_t bytes = (size_t)c.i64(0);
+  void* p = nullptr;
+  if (!check(env, c, c.failed ? 0 : ns2_malloc(&p, bytes))) return nullptr;
+  return bigint(env, p);
+}
+
+napi_value Free(napi_env env, napi_callback_info info) {
+  ARGS(1);
+  void* p = c.ptr(0);
+  return check(env, c, c.failed ? 0 : ns2_free(p));
+}
+
+napi_value PoolRound(napi_env env, napi_callback_info info) {
+  ARGS(1);
+  size_t b = (size_t)c.i64(0);
+  if (c.failed) return nullptr;
+  return number(env, (double)ns2_pool_round(b));
+}
+
+napi_value PoolGet(napi_env env, napi_callback_info info) {
+  ARGS(1);
+  size_t bytes = (size_t)c.i64(0);
+  void* p = nullptr;
+  size_t rounded = 0;
+  if (!check(env, c, c.failed ? 0 : ns2_pool_get(bytes, &p, &rounded))) return nullptr;
+  napi_value arr;
+  napi_create_array_with_length(env, 2, &arr);
+  napi_set_element(env, arr, 0, bigint(env, p));
+  napi_set_element(env, arr, 1, number(env, (double)rounded));
+  return arr;
+}
+
+napi_value PoolPut(napi_env env, napi_callback_info info) {
+  ARGS(2);
+  void* p = c.ptr(0);
+  size_t r = (size_t)c.i64(1);
+  return check(env, c, c.failed ? 0 : ns2_pool_put(p, r));
+}
+
+napi_value PoolTrim(napi_env env, napi_callback_info info) {
+  Ctx c{env, nullptr, 0};
+  return check(env, c, ns2_pool_trim());
+}
+
+napi_value PoolStats(napi_env env, napi_callback_info info) {
+  size_t a = 0, p = 0;
+  ns2_pool_stats(&a, &p);
+  napi_value o;
+  napi_create_object(env, &o);
+  napi_set_named_property(env, o, "allocated", number(env, (double)a));
+  napi_set_named_property(env, o, "peak", number(env, (double)p));
+  return o;
+}
+
+// h2d(dst, typedArrayOrBuffer[, dstByteOffset])
+napi_value H2D(napi_env env, napi_callback_info info) {
+  ARGS(3);
+  char* dst = static_cast<char*>(c.ptr(0));
+  int64_t off = c.type(2) == napi_number ? c.i64(2) : 0;
+  if (c.failed) return nullptr;
+  void* data = nullptr;
+  size_t bytes = 0;
+  bool is_ta = false, is_ab = false, is_dv = false;
+  napi_is_typedarray(env, argv[1], &is_ta);
+  napi_is_arraybuffer(env, argv[1], &is_ab);
+  napi_is_dataview(env, argv[1], &is_dv);
+  if (is_ta) {
+    napi_typedarray_type t;
+    size_t len, boff;
+    napi_value ab;
+    napi_get_typedarray_info(env, argv[1], &t, &len, &data, &ab, &boff);
+    size_t es = 1;
+    switch (t) {
+      case napi_int16_array: case napi_uint16_array: es = 2; break;
+      case napi_int32_array: case napi_uint32_array: case napi_float32_array: es = 4; break;
+      case napi_float64_array: case napi_bigint64_array: case napi_biguint64_array: es = 8; break;
+      default: es = 1;
+    }
+    bytes = len * es;
+  } else if (is_ab) {
+    napi_get_arraybuffer_info(env, argv[1], &data, &bytes);
+  } else if (is_dv) {
+    napi_value ab;
+    size_t boff;
+    napi_get_dataview_info(env, argv[1], &bytes, &data, &ab, &boff);
+  } else {
+    c.fail("h2d: expected a TypedArray, ArrayBuffer or DataView");
+    return nullptr;
+  }
+  return check(env, c, ns2_h2d(dst + off, data, bytes));
+}
+
+// d2h(src, dstTypedArray) or d2h(src, bytes) -> ArrayBuffer
+napi_value D2H(napi_env env, napi_callback_info info) {
+  ARGS(2);
+  const void* src = c.ptr(0);
+  if (c.failed) return nullptr;
+  bool is_ta = false;
+  napi_is_typedarray(env, argv[1], &is_ta);
+  if (is_ta) {
+    napi_typedarray_type t;
+    size_t len, boff;
+    void* data;
+    napi_value ab;
+    napi_get_typedarray_info(env, argv[1], &t, &len, &data, &ab, &boff);
+    size_t es = (t == napi_float32_array || t == napi_int32_array || t == napi_uint32_array) ? 4
+                : (t == napi_int16_array || t == napi_uint16_array) ? 2
+                : (t == napi_float64_array) ? 8 : 1;
+    if (!check(env, c, ns2_d2h(data, src, len * es))) return nullptr;
+    return argv[1];
+  }
+  size_t bytes = (size_t)c.i64(1);
+  if (c.failed) return nullptr;
+  void* data = nullptr;
+  napi_value ab;
+  napi_create_arraybuffer(env, bytes, &data, &ab);
+  if (!check(env, c, ns2_d2h(data, src, bytes))) return nullptr;
+  return ab;
+}
+
+napi_value Sync(napi_env env, napi_callback_info info) {
+  Ctx c{env, nullptr, 0};
+  return check(env, c, ns2_sync());
+}
+
+napi_value Fill(napi_env env, napi_callback_info info) {
+  ARGS(3);
+  void* p = c.ptr(0);
+  uint32_t v = (uint32_t)c.i64(1);
+  size_t n = (size_t)c.i64(2);
+  return check(env, c, c.failed ? 0 : ns2_fill_u32(p, v, n));
+}
+
+napi_value EventCreate(napi_env env, napi_callback_info info) {
+  void* ev = nullptr;
+  if (ns2_event_create(&ev) != NS2_OK) {
+    napi_throw_error(env, nullptr, ns2_last_error());
+    return nullptr;
+  }
+  return bigint(env, ev);
+}
+
+napi_value EventRecord(napi_env env, napi_callback_info info) {
+  ARGS(1);
+  void* ev = c.ptr(0);
+  return check(env, c, c.failed ? 0 : ns2_event_record(ev));
+}
+
+napi_value EventElapsed(napi_env env, napi_callback_info info) {
+  ARGS(2);
+  void* a = c.ptr(0);
+  void* b = c.ptr(1);
+  float ms = 0;
+  if (!check(env, c, c.failed ? 0 : ns2_event_elapsed(a, b, &ms))) return nullptr;
+  return number(env, ms);
+}
+
+napi_value EventDestroy(napi_env env, napi_callback_info info) {
+  ARGS(1);
+  void* ev = c.ptr(0);
+  return check(env, c, c.failed ? 0 : ns2_event_destroy(ev));
+}
+
+// ---- ops ------------------------------------------------------------------------------------
+
+napi_value Hadamard256(napi_env env, napi_callback_info info) {
+  ARGS(3);
+  auto x = (const float*)c.ptr(0);
+  auto y = (float*)c.ptr(1);
+  long long g = c.i64(2);
+  return check(env, c, c.failed ? 0 : ns2_hadamard256(x, y, g));
+}
+
+napi_value RotateF16(napi_env env, napi_callback_info info) {
+  ARGS(6);
+  auto x = (const float*)c.ptr(0);
+  int ldx = c.i32(1);
+  auto y = (uint16_t*)c.ptr(2);
+  int ldy = c.i32(3), rows = c.i32(4), cols = c.i32(5);
+  return check(env, c, c.failed ? 0 : ns2_rotate_f16(x, ldx, y, ldy, rows, cols));
+}
+
+// linearI8(A, aFmt, lda, W, scale, bias, add, C, M, N, K, ldc, cOff, alpha, act, resid, gate, gOff)
+napi_value LinearI8(napi_env env, napi_callback_info info) {
+  ARGS(18);
+  const void* A = c.ptr(0);
+  int aFmt = c.i32(1), lda = c.i32(2);
+  auto W = (const int8_t*)c.ptr(3);
+  auto scale = (const float*)c.ptr(4);
+  auto bias = (const float*)c.ptr(5);
+  auto add = (const float*)c.ptr(6);
+  auto C = (float*)c.ptr(7);
+  int M = c.i32(8), N = c.i32(9), K = c.i32(10), ldc = c.i32(11);
+  long long cOff = c.i64(12);
+  float alpha = c.f32(13);
+  int act = c.i32(14), resid = c.i32(15);
+  auto gate = (const float*)c.ptr(16);
+  long long gOff = c.i64(17);
+  if (c.failed) return nullptr;
+  return check(env, c, ns2_linear_i8(A, aFmt, lda, W, scale, bias, add, C, M, N, K, ldc, cOff, alpha, act, resid, gate, gOff));
+}
+
+// linearBf16(A, lda, W, bias, add, C, M, N, K, ldc, cOff, alpha, act, resid, gate, gOff)
+napi_value LinearBf16(napi_env env, napi_callback_info info) {
+  ARGS(16);
+  auto A = (const float*)c.ptr(0);
+  int lda = c.i32(1);
+  auto W = (const uint16_t*)c.ptr(2);
+  auto bias = (const float*)c.ptr(3);
+  auto add = (const float*)c.ptr(4);
+  auto C = (float*)c.ptr(5);
+  int M = c.i32(6), N = c.i32(7), K = c.i32(8), ldc = c.i32(9);
+  long long cOff = c.i64(10);
+  float alpha = c.f32(11);
+  int act = c.i32(12), resid = c.i32(13);
+  auto gate = (const float*)c.ptr(14);
+  long long gOff = c.i64(15);
+  if (c.failed) return nullptr;
+  return check(env, c, ns2_linear_bf16(A, lda, W, bias, add, C, M, N, K, ldc, cOff, alpha, act, resid, gate, gOff));
+}
+
+// attention(q, k, v, o, batch, Lq, Lk, H, D, ldq, ldk, ldv, ldo, qOff, kOff, vOff, oOff,
+//           qBatch, kBatch, vBatch, oBatch, scale, keyBias, biasStart, biasBatch,
+//           qNorm, kNorm, eps, ropeCs, sinOff, ropeRows)
+napi_value Attention(napi_env env, napi_callback_info info) {
+  ARGS(31);
+  auto q = (const float*)c.ptr(0);
+  auto k = (const float*)c.ptr(1);
+  auto v = (const float*)c.ptr(2);
+  auto o = (float*)c.ptr(3);
+  int batch = c.i32(4), Lq = c.i32(5), Lk = c.i32(6), H = c.i32(7), D = c.i32(8);
+  int ldq = c.i32(9), ldk = c.i32(10), ldv = c.i32(11), ldo = c.i32(12);
+  long long qOff = c.i64(13), kOff = c.i64(14), vOff = c.i64(15), oOff = c.i64(16);
+  long long qB = c.i64(17), kB = c.i64(18), vB = c.i64(19), oB = c.i64(20);
+  float scale = c.f32(21);
+  auto kb = (const float*)c.ptr(22);
+  int biasStart = c.i32(23);
+  long long biasBatch = c.i64(24);
+  auto qn = (const float*)c.ptr(25);
+  auto kn = (const float*)c.ptr(26);
+  float eps = c.f32(27);
+  auto cs = (const float*)c.ptr(28);
+  long long sinOff = c.i64(29);
+  int ropeRows = c.i32(30);
+  if (c.failed) return nullptr;
+  return check(env, c, ns2_attention(q, k, v, o, batch, Lq, Lk, H, D, ldq, ldk, ldv, ldo, qOff, kOff, vOff, oOff,
+                                     qB, kB, vB, oB, scale, kb, biasStart, biasBatch, qn, kn, eps, cs, sinOff, ropeRows));
+}
+
+// headNorm(X, w, L, H, D, ld, colOff, rowOff, cs, sinOff, eps)
+napi_value HeadNorm(napi_env env, napi_callback_info info) {
+  ARGS(11);
+  auto X = (float*)c.ptr(0);
+  auto w = (const float*)c.ptr(1);
+  int L = c.i32(2), H = c.i32(3), D = c.i32(4), ld = c.i32(5);
+  long long colOff = c.i64(6), rowOff = c.i64(7);
+  auto cs = (const float*)c.ptr(8);
+  long long sinOff = c.i64(9);
+  float eps = c.f32(10);
+  if (c.failed) return nullptr;
+  return check(env, c, ns2_head_norm(X, w, L, H, D, ld, colOff, rowOff, cs, sinOff, eps));
+}
+
+// normMod(x, mod, shiftOff, scaleOff, rows, cols, weight, eps, y) / normModRotateF16(...)
+template <bool ROT>
+napi_value NormModT(napi_env env, napi_callback_info info) {
+  ARGS(9);
+  auto x = (const float*)c.ptr(0);
+  auto mod = (const float*)c.ptr(1);
+  long long sh = c.i64(2), sc = c.i64(3);
+  int rows = c.i32(4), cols = c.i32(5);
+  auto w = (const float*)c.ptr(6);
+  float eps = c.f32(7);
+  void* y = c.ptr(8);
+  if (c.failed) return nullptr;
+  int rc = ROT ? ns2_norm_mod_rotate_f16(x, mod, sh, sc, rows, cols, w, eps, (uint16_t*)y)
+               : ns2_norm_mod(x, mod, sh, sc, rows, cols, w, eps, (float*)y);
+  return check(env, c, rc);
+}
+
+// glu(x, y, rows, I, act) / gluRotateF16(...)
+template <bool ROT>
+napi_value GluT(napi_env env, napi_callback_info info) {
+  ARGS(5);
+  auto x = (const float*)c.ptr(0);
+  void* y = c.ptr(1);
+  int rows = c.i32(2), I = c.i32(3), act = c.i32(4);
+  if (c.failed) return nullptr;
+  int rc = ROT ? ns2_glu_rotate_f16(x, (uint16_t*)y, rows, I, act) : ns2_glu(x, (float*)y, rows, I, act);
+  return check(env, c, rc);
+}
+
+// elementwise(op, a, b, y, n)
+napi_value Elementwise(napi_env env, napi_callback_info info) {
+  ARGS(5);
+  int op = c.i32(0);
+  auto a = (const float*)c.ptr(1);
+  auto b = (const float*)c.ptr(2);
+  auto y = (float*)c.ptr(3);
+  long long n = c.i64(4);
+  if (c.failed) return nullptr;
+  return check(env, c, ns2_elementwise(op, a, b, y, n));
+}
+
+napi_value Accumulate(napi_env env, napi_callback_info info) {
+  ARGS(3);
+  auto y = (float*)c.ptr(0);
+  auto a = (const float*)c.ptr(1);
+  long long n = c.i64(2);
+  if (c.failed) return nullptr;
+  return check(env, c, ns2_accumulate(y, a, n));
+}
+
+// rowSum(x, w, y, rows, N, scale)
+napi_value RowSum(napi_env env, napi_callback_info info) {
+  ARGS(6);
+  auto x = (const float*)c.ptr(0);
+  auto w = (const float*)c.ptr(1);
+  auto y = (float*)c.ptr(2);
+  int rows = c.i32(3), N = c.i32(4);
+  float s = c.f32(5);
+  if (c.failed) return nullptr;
+  return check(env, c, ns2_row_sum(x, w, y, rows, N, s));
+}
+
+// rmsnorm(x, w, y, rows, cols, eps)
+napi_value Rmsnorm(napi_env env, napi_callback_info info) {
+  ARGS(6);
+  auto x = (const float*)c.ptr(0);
+  auto w = (const float*)c.ptr(1);
+  auto y = (float*)c.ptr(2);
+  int rows = c.i32(3), cols = c.i32(4);
+  float eps = c.f32(5);
+  if (c.failed) return nullptr;
+  return check(env, c, ns2_rmsnorm(x, w, y, rows, cols, eps));
+}
+
+napi_value Module(napi_env env, napi_value exports) {
+  struct Fn {
+    const char* name;
+    napi_callback cb;
+  } fns[] = {
+      {"init", Init}, {"deviceInfo", DeviceInfo}, {"malloc", Malloc}, {"free", Free},
+      {"poolRound", PoolRound}, {"poolGet", PoolGet}, {"poolPut", PoolPut}, {"poolTrim", PoolTrim},
+      {"poolStats", PoolStats}, {"h2d", H2D}, {"d2h", D2H}, {"sync", Sync}, {"fill", Fill},
+      {"eventCreate", EventCreate}, {"eventRecord", EventRecord}, {"eventElapsed", EventElapsed},
+      {"eventDestroy", EventDestroy}, {"hadamard256", Hadamard256}, {"rotateF16", RotateF16},
+      {"linearI8", LinearI8}, {"linearBf16", LinearBf16}, {"attention", Attention},
+      {"headNorm", HeadNorm}, {"normMod", NormModT<false>}, {"normModRotateF16", NormModT<true>},
+      {"glu", GluT<false>}, {"gluRotateF16", GluT<true>}, {"elementwise", Elementwise},
+      {"accumulate", Accumulate}, {"rowSum", RowSum}, {"rmsnorm", Rmsnorm},
+  };
+  for (const Fn& f : fns) {
+    napi_value fn;
+    napi_create_function(env, f.name, NAPI_AUTO_LENGTH, f.cb, nullptr, &fn);
+    napi_set_named_property(env, exports, f.name, fn);
+  }
+  return exports;
+}
+
+}  // namespace
+
+NAPI_MODULE(NODE_GYP_MODULE_NAME, Module)

@@ -1,0 +1,125 @@
+// Internal helpers shared by the ns2 HIP sources (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include "../../include/ns2.h"
+
+namespace ns2 {
+
+// ---- host side -------------------------------------------------------------------------
+
+// Record an error message for ns2_last_error() and return code.
+int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+void clear_error();
+hipStream_t stream();
+bool initialised();
+// Stream-ordered scratch owned by the library, grown on demand and reused by later calls
+// (one slot per concurrent use inside a single entry point).
+void* workspace(int slot, size_t bytes);
+constexpr int kWorkspaceSlots = 6;
+
+}  // namespace ns2
+
+#define NS2_REQUIRE(cond, ...)                                   \
+  do {                                                           \
+    if (!(cond)) return ns2::set_error(NS2_ERR_INVALID, __VA_ARGS__); \
+  } while (0)
+
+#define NS2_HIP(expr)                                                                   \
+  do {                                                                                  \
+    hipError_t e_ = (expr);                                                             \
+    if (e_ != hipSuccess)                                                               \
+      return ns2::set_error(NS2_ERR_HIP, "%s: %s", #expr, hipGetErrorString(e_));      \
+  } while (0)
+
+#define NS2_LAUNCHED(name)                                                              \
+  do {                                                                                  \
+    hipError_t e_ = hipGetLastError();                                                  \
+    if (e_ != hipSuccess)                                                               \
+      return ns2::set_error(NS2_ERR_HIP, "launch %s: %s", name, hipGetErrorString(e_)); \
+  } while (0)
+
+#define NS2_READY()                                                             \
+  do {                                                                          \
+    if (!ns2::initialised())                                                    \
+      return ns2::set_error(NS2_ERR_STATE, "ns2_init has not been called");      \
+  } while (0)
+
+// ---- device side -------------------------------------------------------------------------
+
+typedef _Float16 half_t;
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef float float16_t __attribute__((ext_vector_type(16)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+
+namespace ns2dev {
+
+__device__ __forceinline__ float silu(float x) { return x / (1.0f + __expf(-x)); }
+
+// tanh-approximated GELU (PyTorch approximate="tanh"), tanh from exp of -2|u| so it
+// cannot overflow (kernels.js:11-17).
+__device__ __forceinline__ float gelu_tanh(float x) {
+  float u = 0.7978845608028654f * (x + 0.044715f * x * x * x);
+  float e = __expf(-2.0f * fabsf(u));
+  float t = copysignf((1.0f - e) / (1.0f + e), u);
+  return 0.5f * x * (1.0f + t);
+}
+
+__device__ __forceinline__ float apply_act(float x, int act) {
+  if (act == NS2_ACT_SILU) return silu(x);
+  if (act == NS2_ACT_GELU_TANH) return gelu_tanh(x);
+  return x;
+}
+
+// Sum over the 64 lanes of a wave.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+
+// One radix-4 stage of the regular Hadamard H4 = [[1,1,1,-1],[1,1,-1,1],[1,-1,1,1],[-1,1,1,1]]
+// across 4 lanes whose lane bits (lo, lo<<1) index the 4 inputs: output position i is
+// (a+b+c+e) - 2 * input[3 - i], and position 3 - i is lane ^ (3 * lo).
+__device__ __forceinline__ float h4_lanes(float v, int lo) {
+  float s = v + __shfl_xor(v, lo, 64);
+  s += __shfl_xor(s, 2 * lo, 64);
+  float partner = __shfl_xor(v, 3 * lo, 64);
+  return s - 2.0f * partner;
+}
+
+// In-wave fast Walsh-Hadamard transform of one 256-group: lane t holds elements 4t..4t+3
+// in v[0..3]. Computes y = x H with H = kron(H4, H4, H4, H4) / 16 (tools/quant.py:21-29):
+// radix-4 stages at strides 1 (in registers), 4, 16 and 64 (across lanes).
+__device__ __forceinline__ void fwht256_wave(float v[4]) {
+  {
+    float a = v[0], b = v[1], c = v[2], e = v[3];
+    float s = a + b + c + e;
+    v[0] = s - 2.0f * e;
+    v[1] = s - 2.0f * c;
+    v[2] = s - 2.0f * b;
+    v[3] = s - 2.0f * a;
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) v[j] = h4_lanes(v[j], 1);   // stride 4: lane bits 0-1
+#pragma unroll
+  for (int j = 0; j < 4; ++j) v[j] = h4_lanes(v[j], 4);   // stride 16: lane bits 2-3
+#pragma unroll
+  for (int j = 0; j < 4; ++j) v[j] = h4_lanes(v[j], 16);  // stride 64: lane bits 4-5
+#pragma unroll
+  for (int j = 0; j < 4; ++j) v[j] *= 0.0625f;
+}
+
+__device__ __forceinline__ uint32_t pack_half2(float a, float b) {
+  half2_t h;
+  h[0] = (half_t)a;
+  h[1] = (half_t)b;
+  return __builtin_bit_cast(uint32_t, h);
+}
+
+}  // namespace ns2dev

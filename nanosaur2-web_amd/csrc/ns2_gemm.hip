@@ -1,0 +1,370 @@
+// Linear layers: C = epilogue(alpha * A W^T) with int8 ConvRot or bf16 weights.
+//
+// Large M runs on MFMA (v_mfma_f32_32x32x16_f16): both operands are fp16 in LDS, fp32
+// accumulation. int8 weights are exact in fp16 and are decoded from bytes in the tile
+// loader (bias trick: 0x6400 | (b ^ 0x80) is the half 1024 + b + 128); bf16 weights are
+// converted through fp32. Activations arrive either as the rotated fp16 operand written
+// by the producing row kernel (int8 layers) or as fp32 (bf16 layers), converted in the
+// loader. The per-row int8 scale is applied in the epilogue, in the reference's order
+// (app/gpu/gemm.js:159-164). Small M (GEMV-like, e.g. the adaLN projections of one
+// conditioning vector) runs on a fp32-FMA kernel that streams the weights once.
+#include "ns2_common.h"
+
+using namespace ns2dev;
+
+namespace {
+
+struct GemmArgs {
+  const void* A;
+  const void* W;
+  const float* scale;
+  const float* bias;
+  const float* add;
+  float* C;
+  const float* gate;
+  long long cOff;
+  long long gOff;
+  int lda, ldc;
+  int M, N, K;
+  float alpha;
+  int act, resid;
+};
+
+constexpr int BK = 64;        // k per LDS tile
+constexpr int LDS_PAD = 8;    // halfs of padding per LDS row (bank spread)
+constexpr int LROW = BK + LDS_PAD;
+
+// Epilogue of one output element (gemm.js:159-164).
+__device__ __forceinline__ void epilogue_store(const GemmArgs& p, int m, int n, float acc,
+                                               float rs, float bi, float gt) {
+  float r = acc * p.alpha;
+  r *= rs;
+  r += bi;
+  if (p.add) r += p.add[(long long)m * p.N + n];
+  r = apply_act(r, p.act);
+  float* c = p.C + p.cOff + (long long)m * p.ldc + n;
+  if (!p.resid) *c = r;
+  else if (!p.gate) *c = *c + r;
+  else *c = *c + gt * r;
+}
+
+// 4 signed bytes -> 4 halfs (exact): half(0x6400 | u) = 1024 + u with u = b + 128.
+__device__ __forceinline__ uint2 i8x4_to_h4(uint32_t w) {
+  const uint32_t x = w ^ 0x80808080u;
+  const uint32_t lo = (x & 0xffu) | ((x & 0xff00u) << 8) | 0x64006400u;
+  const uint32_t hi = ((x >> 16) & 0xffu) | ((x >> 8) & 0xff0000u) | 0x64006400u;
+  const half2_t off = {(half_t)1152.0f, (half_t)1152.0f};
+  half2_t l = __builtin_bit_cast(half2_t, lo) - off;
+  half2_t h = __builtin_bit_cast(half2_t, hi) - off;
+  return make_uint2(__builtin_bit_cast(uint32_t, l), __builtin_bit_cast(uint32_t, h));
+}
+
+__device__ __forceinline__ uint32_t bf16x2_to_h2(uint32_t w) {
+  const float a = __builtin_bit_cast(float, w << 16);
+  const float b = __builtin_bit_cast(float, w & 0xffff0000u);
+  return pack_half2(a, b);
+}
+
+// Tile loaders: global -> registers (prefetch) -> LDS (fp16, [rows][LROW]).
+template <int ROWS, int NT, bool A_F32>
+struct ALoader {
+  // fp16 operand: 16-byte chunks of 8 k; fp32 operand: 16-byte chunks of 4 k
+  static constexpr int KPC = A_F32 ? 4 : 8;
+  static constexpr int CPR = BK / KPC;
+  static constexpr int CHUNKS = ROWS * CPR / NT;
+  static_assert(ROWS * CPR % NT == 0, "A tile not divisible");
+  uint4 r[CHUNKS];
+  __device__ __forceinline__ void load(const GemmArgs& p, int row0, int k0, int tid) {
+#pragma unroll
+    for (int i = 0; i < CHUNKS; ++i) {
+      const int c = tid + i * NT;
+      const int row = c / CPR, kc = (c % CPR) * KPC;
+      const int m = row0 + row, k = k0 + kc;
+      if (m < p.M && k < p.K) {
+        if (A_F32)
+          r[i] = *reinterpret_cast<const uint4*>(static_cast<const float*>(p.A) + (long long)m * p.lda + k);
+        else
+          r[i] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.A) + (long long)m * p.lda + k);
+      } else {
+        r[i] = make_uint4(0, 0, 0, 0);
+      }
+    }
+  }
+  __device__ __forceinline__ void store(half_t* lds, int tid) const {
+#pragma unroll
+    for (int i = 0; i < CHUNKS; ++i) {
+      const int c = tid + i * NT;
+      const int row = c / CPR, kc = (c % CPR) * KPC;
+      half_t* dst = lds + row * LROW + kc;
+      if (A_F32) {
+        uint2 h;
+        h.x = pack_half2(__builtin_bit_cast(float, r[i].x), __builtin_bit_cast(float, r[i].y));
+        h.y = pack_half2(__builtin_bit_cast(float, r[i].z), __builtin_bit_cast(float, r[i].w));
+        *reinterpret_cast<uint2*>(dst) = h;
+      } else {
+        *reinterpret_cast<uint4*>(dst) = r[i];
+      }
+    }
+  }
+};
+
+template <int ROWS, int NT, bool W_BF16>
+struct WLoader {
+  // int8: 16-byte chunks of 16 k; bf16: 16-byte chunks of 8 k
+  static constexpr int KPC = W_BF16 ? 8 : 16;
+  static constexpr int CPR = BK / KPC;
+  static constexpr int CHUNKS = ROWS * CPR / NT;
+  static_assert(ROWS * CPR % NT == 0, "W tile not divisible");
+  uint4 r[CHUNKS];
+  __device__ __forceinline__ void load(const GemmArgs& p, int row0, int k0, int tid) {
+#pragma unroll
+    for (int i = 0; i < CHUNKS; ++i) {
+      const int c = tid + i * NT;
+      const int row = c / CPR, kc = (c % CPR) * KPC;
+      const int n = row0 + row, k = k0 + kc;
+      if (n < p.N && k < p.K) {
+        if (W_BF16)
+          r[i] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.W) + (long long)n * p.K + k);
+        else
+          r[i] = *reinterpret_cast<const uint4*>(static_cast<const int8_t*>(p.W) + (long long)n * p.K + k);
+      } else {
+        r[i] = make_uint4(0, 0, 0, 0);
+      }
+    }
+  }
+  __device__ __forceinline__ void store(half_t* lds, int tid) const {
+#pragma unroll
+    for (int i = 0; i < CHUNKS; ++i) {
+      const int c = tid + i * NT;
+      const int row = c / CPR, kc = (c % CPR) * KPC;
+      half_t* dst = lds + row * LROW + kc;
+      if (W_BF16) {
+        uint4 h;
+        h.x = bf16x2_to_h2(r[i].x);
+        h.y = bf16x2_to_h2(r[i].y);
+        h.z = bf16x2_to_h2(r[i].z);
+        h.w = bf16x2_to_h2(r[i].w);
+        *reinterpret_cast<uint4*>(dst) = h;
+      } else {
+        const uint2 a = i8x4_to_h4(r[i].x), b = i8x4_to_h4(r[i].y);
+        const uint2 c2 = i8x4_to_h4(r[i].z), d = i8x4_to_h4(r[i].w);
+        *reinterpret_cast<uint4*>(dst) = make_uint4(a.x, a.y, b.x, b.y);
+        *reinterpret_cast<uint4*>(dst + 8) = make_uint4(c2.x, c2.y, d.x, d.y);
+      }
+    }
+  }
+};
+
+// Block tile BM x BN, wave tile WM x WN of 32x32 MFMA tiles, BK = 64 per LDS stage,
+// double-buffered LDS with register prefetch of the next stage.
+// MFMA 32x32x16 operand layout: lane l supplies row (l % 32) of A and column (l % 32) of B,
+// each with 8 consecutive k of the 16 (k = 8 * (l / 32) + e); accumulator element r of lane
+// l is C[8 * (r / 4) + 4 * (l / 32) + r % 4][l % 32].
+template <int BM, int BN, int WM, int WN, bool A_F32, bool W_BF16>
+__global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_kernel(GemmArgs p) {
+  constexpr int WAVES_N = BN / WN;
+  constexpr int NT = (BM / WM) * WAVES_N * 64;
+  constexpr int TM = WM / 32, TN = WN / 32;
+  __shared__ __attribute__((aligned(16))) half_t lds_a[2][BM * LROW];
+  __shared__ __attribute__((aligned(16))) half_t lds_b[2][BN * LROW];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+
+  ALoader<BM, NT, A_F32> la;
+  WLoader<BN, NT, W_BF16> lw;
+
+  float16_t acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  const int nk = (p.K + BK - 1) / BK;
+  la.load(p, m0, 0, tid);
+  lw.load(p, n0, 0, tid);
+  la.store(lds_a[0], tid);
+  lw.store(lds_b[0], tid);
+  __syncthreads();
+
+  const int lrow = lane & 31, lk = (lane >> 5) * 8;
+  for (int kt = 0; kt < nk; ++kt) {
+    const int cur = kt & 1;
+    if (kt + 1 < nk) {
+      la.load(p, m0, (kt + 1) * BK, tid);
+      lw.load(p, n0, (kt + 1) * BK, tid);
+    }
+    const half_t* A = lds_a[cur] + (wm * WM + lrow) * LROW + lk;
+    const half_t* B = lds_b[cur] + (wn * WN + lrow) * LROW + lk;
+#pragma unroll
+    for (int ks = 0; ks < BK / 16; ++ks) {
+      half8_t a[TM], b[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) a[i] = *reinterpret_cast<const half8_t*>(A + i * 32 * LROW + ks * 16);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) b[j] = *reinterpret_cast<const half8_t*>(B + j * 32 * LROW + ks * 16);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+    }
+    if (kt + 1 < nk) {
+      la.store(lds_a[cur ^ 1], tid);
+      lw.store(lds_b[cur ^ 1], tid);
+    }
+    __syncthreads();
+  }
+
+  // epilogue
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int n = n0 + wn * WN + j * 32 + lrow;
+    if (n >= p.N) continue;
+    const float rs = p.scale ? p.scale[n] : 1.0f;
+    const float bi = p.bias ? p.bias[n] : 0.0f;
+    const float gt = p.gate ? p.gate[p.gOff + n] : 1.0f;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = m0 + wm * WM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        if (m < p.M) epilogue_store(p, m, n, acc[i][j][r], rs, bi, gt);
+      }
+    }
+  }
+}
+
+// Small-M path: one wave per output column n, all M (<= 8) rows, fp32 FMA.
+// A: fp32 [M, lda] (bf16 layers) or rotated fp16 [M, lda] (int8 layers).
+template <bool W_BF16>
+__global__ __launch_bounds__(256) void gemv_kernel(GemmArgs p) {
+  const int lane = threadIdx.x & 63;
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (n >= p.N) return;
+  float acc[8];
+#pragma unroll
+  for (int m = 0; m < 8; ++m) acc[m] = 0.f;
+  for (int k = lane * 8; k < p.K; k += 512) {
+    float w[8];
+    if (W_BF16) {
+      const uint4 q = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.W) + (long long)n * p.K + k);
+      const uint32_t qq[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        w[2 * j] = __builtin_bit_cast(float, qq[j] << 16);
+        w[2 * j + 1] = __builtin_bit_cast(float, qq[j] & 0xffff0000u);
+      }
+    } else {
+      const uint2 q = *reinterpret_cast<const uint2*>(static_cast<const int8_t*>(p.W) + (long long)n * p.K + k);
+      const uint32_t qq[2] = {q.x, q.y};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) w[j] = (float)(int8_t)((qq[j >> 2] >> (8 * (j & 3))) & 0xff);
+    }
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      if (m < p.M) {
+        float a[8];
+        if (W_BF16) {
+          const float* ap = static_cast<const float*>(p.A) + (long long)m * p.lda + k;
+          const float4 x0 = *reinterpret_cast<const float4*>(ap);
+          const float4 x1 = *reinterpret_cast<const float4*>(ap + 4);
+          a[0] = x0.x; a[1] = x0.y; a[2] = x0.z; a[3] = x0.w;
+          a[4] = x1.x; a[5] = x1.y; a[6] = x1.z; a[7] = x1.w;
+        } else {
+          const half8_t h = *reinterpret_cast<const half8_t*>(static_cast<const uint16_t*>(p.A) + (long long)m * p.lda + k);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) a[j] = (float)h[j];
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[m] = fmaf(a[j], w[j], acc[m]);
+      }
+    }
+  }
+  const float rs = p.scale ? p.scale[n] : 1.0f;
+  const float bi = p.bias ? p.bias[n] : 0.0f;
+  const float gt = p.gate ? p.gate[p.gOff + n] : 1.0f;
+#pragma unroll
+  for (int m = 0; m < 8; ++m) {
+    if (m < p.M) {
+      const float s = wave_sum(acc[m]);
+      if (lane == 0) epilogue_store(p, m, n, s, rs, bi, gt);
+    }
+  }
+}
+
+constexpr int kGemvMaxM = 8;
+
+template <bool A_F32, bool W_BF16>
+int launch_gemm(const GemmArgs& p, const char* name) {
+  hipStream_t s = ns2::stream();
+  if (p.M <= kGemvMaxM) {
+    gemv_kernel<W_BF16><<<(p.N + 3) / 4, 256, 0, s>>>(p);
+  } else {
+    constexpr int BM = 128, BN = 128, WM = 64, WN = 64;
+    dim3 grid((p.N + BN - 1) / BN, (p.M + BM - 1) / BM);
+    gemm_mfma_kernel<BM, BN, WM, WN, A_F32, W_BF16><<<grid, (BM / WM) * (BN / WN) * 64, 0, s>>>(p);
+  }
+  NS2_LAUNCHED(name);
+  return NS2_OK;
+}
+
+inline bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+int check_common(const GemmArgs& p, const char* name) {
+  NS2_REQUIRE(p.A && p.W && p.C, "%s: null A, W or C", name);
+  NS2_REQUIRE(p.M >= 0 && p.N > 0 && p.K > 0, "%s: bad sizes M=%d N=%d K=%d", name, p.M, p.N, p.K);
+  NS2_REQUIRE(p.K % 16 == 0, "%s: K=%d must be a multiple of 16", name, p.K);
+  NS2_REQUIRE(p.lda >= p.K && p.lda % 8 == 0, "%s: lda=%d must be >= K and a multiple of 8", name, p.lda);
+  NS2_REQUIRE(p.ldc >= p.N, "%s: ldc=%d must be >= N=%d", name, p.ldc, p.N);
+  NS2_REQUIRE(aligned16(p.A) && aligned16(p.W), "%s: A and W must be 16-byte aligned", name);
+  NS2_REQUIRE(p.cOff >= 0 && p.gOff >= 0, "%s: negative offset", name);
+  NS2_REQUIRE(p.act >= NS2_ACT_NONE && p.act <= NS2_ACT_GELU_TANH, "%s: unknown act %d", name, p.act);
+  return NS2_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ns2_linear_i8(const void* A, int a_fmt, int lda, const int8_t* W, const float* scale,
+                  const float* bias, const float* add, float* C, int M, int N, int K, int ldc,
+                  long long cOff, float alpha, int act, int resid, const float* gate,
+                  long long gOff) {
+  NS2_READY();
+  if (M == 0) return NS2_OK;
+  GemmArgs p{A, W, scale, bias, add, C, gate, cOff, gOff, lda, ldc, M, N, K, alpha, act, resid};
+  NS2_REQUIRE(a_fmt == 0 || a_fmt == 1, "ns2_linear_i8: a_fmt must be 0 (fp32) or 1 (rotated fp16)");
+  NS2_REQUIRE(scale != nullptr, "ns2_linear_i8: null scale");
+  NS2_REQUIRE(K % 256 == 0, "ns2_linear_i8: K=%d must be a multiple of 256 (ConvRot groups)", K);
+  if (a_fmt == 0) {
+    // ops.linear without xr: rotate into library scratch first (app/gpu/ops.js:54)
+    NS2_REQUIRE(A && lda >= K && lda % 4 == 0, "ns2_linear_i8: bad fp32 A / lda=%d", lda);
+    uint16_t* xr = static_cast<uint16_t*>(ns2::workspace(0, (size_t)M * K * sizeof(uint16_t)));
+    if (!xr) return ns2::set_error(NS2_ERR_OOM, "ns2_linear_i8: workspace allocation failed");
+    int rc = ns2_rotate_f16(static_cast<const float*>(A), lda, xr, K, M, K);
+    if (rc) return rc;
+    p.A = xr;
+    p.lda = K;
+  }
+  int rc = check_common(p, "ns2_linear_i8");
+  if (rc) return rc;
+  return launch_gemm<false, false>(p, "linear_i8");
+}
+
+int ns2_linear_bf16(const float* A, int lda, const uint16_t* W, const float* bias,
+                    const float* add, float* C, int M, int N, int K, int ldc, long long cOff,
+                    float alpha, int act, int resid, const float* gate, long long gOff) {
+  NS2_READY();
+  if (M == 0) return NS2_OK;
+  GemmArgs p{A, W, nullptr, bias, add, C, gate, cOff, gOff, lda, ldc, M, N, K, alpha, act, resid};
+  int rc = check_common(p, "ns2_linear_bf16");
+  if (rc) return rc;
+  return launch_gemm<true, true>(p, "linear_bf16");
+}
+
+}  // extern "C"

@@ -1,0 +1,355 @@
+// Row kernels of the DiT pass: ConvRot rotation (FWHT), normMod, headNorm (+RoPE), GLU,
+// elementwise, rowSum and RMSNorm. All are HBM-bound; each reads and writes its row once.
+// Fused variants write the rotated fp16 operand of the int8 GEMM directly, so the
+// standalone rotation pass of app/gpu/ops.js:38-44 never touches HBM on the DiT path.
+#include "ns2_common.h"
+
+using namespace ns2dev;
+
+namespace {
+
+// Block-wide sum for blockDim.x == 64 * nwaves (<= 1024); every thread gets the total.
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  v = wave_sum(v);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  __syncthreads();  // red may still be read by a previous call
+  if (lane == 0) red[w] = v;
+  __syncthreads();
+  float t = 0.f;
+  for (int i = 0; i < nw; ++i) t += red[i];
+  return t;
+}
+
+// ---- rotation ------------------------------------------------------------------------------
+
+// y = x H per contiguous 256-group (kernels.js:378-407). One wave per group.
+__global__ __launch_bounds__(256) void hadamard256_kernel(const float* __restrict__ x,
+                                                           float* __restrict__ y,
+                                                           long long groups) {
+  long long g = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (g >= groups) return;
+  const int lane = threadIdx.x & 63;
+  const float4 in = *reinterpret_cast<const float4*>(x + g * 256 + lane * 4);
+  float v[4] = {in.x, in.y, in.z, in.w};
+  fwht256_wave(v);
+  *reinterpret_cast<float4*>(y + g * 256 + lane * 4) = make_float4(v[0], v[1], v[2], v[3]);
+}
+
+// Strided [rows, cols] fp32 -> rotated fp16. One wave per 256-group.
+__global__ __launch_bounds__(256) void rotate_f16_kernel(const float* __restrict__ x, int ldx,
+                                                          uint16_t* __restrict__ y, int ldy,
+                                                          int rows, int gpr) {
+  long long g = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (g >= (long long)rows * gpr) return;
+  const int r = (int)(g / gpr), c = (int)(g % gpr) * 256;
+  const int lane = threadIdx.x & 63;
+  const float4 in = *reinterpret_cast<const float4*>(x + (long long)r * ldx + c + lane * 4);
+  float v[4] = {in.x, in.y, in.z, in.w};
+  fwht256_wave(v);
+  uint2 o;
+  o.x = pack_half2(v[0], v[1]);
+  o.y = pack_half2(v[2], v[3]);
+  *reinterpret_cast<uint2*>(y + (long long)r * ldy + c + lane * 4) = o;
+}
+
+// ---- normMod ----------------------------------------------------------------------------
+
+// Reference-layout normMod, any cols (kernels.js:82-117): 256 threads per row.
+__global__ __launch_bounds__(256) void norm_mod_kernel(const float* __restrict__ x,
+                                                        const float* __restrict__ mod,
+                                                        long long shiftOff, long long scaleOff,
+                                                        int cols, const float* __restrict__ w,
+                                                        float eps, float* __restrict__ y) {
+  __shared__ float red[16];
+  const long long base = (long long)blockIdx.x * cols;
+  float mean = 0.f;
+  if (!w) {
+    float s = 0.f;
+    for (int c = threadIdx.x; c < cols; c += 256) s += x[base + c];
+    mean = block_sum(s, red) / (float)cols;
+  }
+  float v = 0.f;
+  for (int c = threadIdx.x; c < cols; c += 256) {
+    float d = x[base + c] - mean;
+    v += d * d;
+  }
+  const float r = rsqrtf(block_sum(v, red) / (float)cols + eps);
+  for (int c = threadIdx.x; c < cols; c += 256) {
+    float n = (x[base + c] - mean) * r;
+    if (w) n *= w[c];
+    y[base + c] = n * (1.0f + mod[scaleOff + c]) + mod[shiftOff + c];
+  }
+}
+
+// normMod + rotation + fp16: one wave per 256-group of the row, the row in registers.
+__global__ __launch_bounds__(1024) void norm_mod_rot_kernel(const float* __restrict__ x,
+                                                             const float* __restrict__ mod,
+                                                             long long shiftOff,
+                                                             long long scaleOff, int cols,
+                                                             const float* __restrict__ w,
+                                                             float eps,
+                                                             uint16_t* __restrict__ y) {
+  __shared__ float red[16];
+  const long long base = (long long)blockIdx.x * cols;
+  const int c = threadIdx.x * 4;  // blockDim.x * 4 == cols
+  const float4 in = *reinterpret_cast<const float4*>(x + base + c);
+  float v[4] = {in.x, in.y, in.z, in.w};
+  float mean = 0.f;
+  if (!w) mean = block_sum(v[0] + v[1] + v[2] + v[3], red) / (float)cols;
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    v[j] -= mean;
+    ss += v[j] * v[j];
+  }
+  const float r = rsqrtf(block_sum(ss, red) / (float)cols + eps);
+  const float4 sc = *reinterpret_cast<const float4*>(mod + scaleOff + c);
+  const float4 sh = *reinterpret_cast<const float4*>(mod + shiftOff + c);
+  float4 ww = make_float4(1.f, 1.f, 1.f, 1.f);
+  if (w) ww = *reinterpret_cast<const float4*>(w + c);
+  v[0] = v[0] * r * ww.x * (1.0f + sc.x) + sh.x;
+  v[1] = v[1] * r * ww.y * (1.0f + sc.y) + sh.y;
+  v[2] = v[2] * r * ww.z * (1.0f + sc.z) + sh.z;
+  v[3] = v[3] * r * ww.w * (1.0f + sc.w) + sh.w;
+  fwht256_wave(v);
+  uint2 o;
+  o.x = pack_half2(v[0], v[1]);
+  o.y = pack_half2(v[2], v[3]);
+  *reinterpret_cast<uint2*>(y + base + c) = o;
+}
+
+// ---- headNorm -------------------------------------------------------------------------------
+
+// In-place per-head RMSNorm (+ split-half RoPE), kernels.js:307-342. One wave per (row, head).
+__global__ __launch_bounds__(256) void head_norm_kernel(float* __restrict__ X,
+                                                         const float* __restrict__ w, int L,
+                                                         int H, int D, int ld, long long colOff,
+                                                         long long rowOff,
+                                                         const float* __restrict__ cs,
+                                                         long long sinOff, float eps) {
+  long long id = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (id >= (long long)L * H) return;
+  const int lane = threadIdx.x & 63;
+  const int l = (int)(id / H), h = (int)(id % H);
+  float* row = X + (rowOff + l) * (long long)ld + colOff + (long long)h * D;
+  float ss = 0.f;
+  for (int i = lane; i < D; i += 64) ss += row[i] * row[i];
+  const float r = rsqrtf(wave_sum(ss) / (float)D + eps);
+  if (cs) {
+    const int half = D / 2;
+    for (int i = lane; i < half; i += 64) {
+      const float y1 = row[i] * r * w[i];
+      const float y2 = row[i + half] * r * w[i + half];
+      const float c = cs[(long long)l * half + i];
+      const float s = cs[sinOff + (long long)l * half + i];
+      row[i] = y1 * c - y2 * s;
+      row[i + half] = y2 * c + y1 * s;
+    }
+  } else {
+    for (int i = lane; i < D; i += 64) row[i] = row[i] * r * w[i];
+  }
+}
+
+// ---- GLU ----------------------------------------------------------------------------------
+
+__global__ __launch_bounds__(256) void glu_kernel(const float* __restrict__ x,
+                                                   float* __restrict__ y, long long n, int I,
+                                                   int act) {
+  long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const long long r = i / I, j = i % I;
+  const long long base = r * 2 * I + j;
+  y[i] = apply_act(x[base], act) * x[base + I];
+}
+
+// GLU + rotation + fp16: one wave per 256 output columns.
+__global__ __launch_bounds__(256) void glu_rot_kernel(const float* __restrict__ x,
+                                                       uint16_t* __restrict__ y, int rows,
+                                                       int I, int act) {
+  const int gpr = I / 256;
+  long long g = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (g >= (long long)rows * gpr) return;
+  const int lane = threadIdx.x & 63;
+  const long long r = g / gpr;
+  const int c = (int)(g % gpr) * 256 + lane * 4;
+  const float4 a = *reinterpret_cast<const float4*>(x + r * 2 * I + c);
+  const float4 b = *reinterpret_cast<const float4*>(x + r * 2 * I + I + c);
+  float v[4] = {apply_act(a.x, act) * b.x, apply_act(a.y, act) * b.y,
+                apply_act(a.z, act) * b.z, apply_act(a.w, act) * b.w};
+  fwht256_wave(v);
+  uint2 o;
+  o.x = pack_half2(v[0], v[1]);
+  o.y = pack_half2(v[2], v[3]);
+  *reinterpret_cast<uint2*>(y + r * I + c) = o;
+}
+
+// ---- elementwise / accumulate / rowSum / RMSNorm ---------------------------------------------
+
+__global__ __launch_bounds__(256) void elementwise_kernel(int op, const float* __restrict__ a,
+                                                           const float* __restrict__ b,
+                                                           float* __restrict__ y, long long n) {
+  long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  float v = a[i];
+  if (op == NS2_EW_ADD) v = v + b[i];
+  else if (op == NS2_EW_SUB) v = v - b[i];
+  else if (op == NS2_EW_SILU) v = silu(v);
+  y[i] = v;
+}
+
+__global__ __launch_bounds__(256) void accumulate_kernel(float* __restrict__ y,
+                                                          const float* __restrict__ a,
+                                                          long long n) {
+  long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) y[i] += a[i];
+}
+
+// Y[n] = scale * sum_r w[r] X[r][n]: one thread per column, rows in order (kernels.js:362-376).
+__global__ __launch_bounds__(64) void row_sum_kernel(const float* __restrict__ x,
+                                                      const float* __restrict__ w,
+                                                      float* __restrict__ y, int rows, int N,
+                                                      float scale) {
+  int n = blockIdx.x * 64 + threadIdx.x;
+  if (n >= N) return;
+  float s = 0.f;
+  for (int r = 0; r < rows; ++r) s += w[r] * x[(long long)r * N + n];
+  y[n] = s * scale;
+}
+
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ x,
+                                                       const float* __restrict__ w,
+                                                       float* __restrict__ y, int cols,
+                                                       float eps) {
+  __shared__ float red[16];
+  const long long base = (long long)blockIdx.x * cols;
+  float ss = 0.f;
+  for (int c = threadIdx.x; c < cols; c += 256) ss += x[base + c] * x[base + c];
+  const float r = rsqrtf(block_sum(ss, red) / (float)cols + eps);
+  for (int c = threadIdx.x; c < cols; c += 256) y[base + c] = x[base + c] * r * w[c];
+}
+
+inline bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+inline bool aligned8(const void* p) { return ((uintptr_t)p & 7) == 0; }
+
+inline unsigned blocks_for(long long n, int per) { return (unsigned)((n + per - 1) / per); }
+
+}  // namespace
+
+extern "C" {
+
+int ns2_hadamard256(const float* x, float* y, long long groups) {
+  NS2_READY();
+  if (groups <= 0) return NS2_OK;
+  NS2_REQUIRE(x && y && aligned16(x) && aligned16(y), "ns2_hadamard256: null or unaligned buffer");
+  hadamard256_kernel<<<blocks_for(groups, 4), 256, 0, ns2::stream()>>>(x, y, groups);
+  NS2_LAUNCHED("hadamard256");
+  return NS2_OK;
+}
+
+int ns2_rotate_f16(const float* x, int ldx, uint16_t* y, int ldy, int rows, int cols) {
+  NS2_READY();
+  if (rows <= 0) return NS2_OK;
+  NS2_REQUIRE(cols > 0 && cols % 256 == 0, "ns2_rotate_f16: cols=%d must be a multiple of 256", cols);
+  NS2_REQUIRE(ldx % 4 == 0 && ldy % 4 == 0 && ldx >= cols && ldy >= cols,
+              "ns2_rotate_f16: ldx=%d ldy=%d must be multiples of 4 and >= cols", ldx, ldy);
+  NS2_REQUIRE(x && y && aligned16(x) && aligned8(y), "ns2_rotate_f16: null or unaligned buffer");
+  const int gpr = cols / 256;
+  rotate_f16_kernel<<<blocks_for((long long)rows * gpr, 4), 256, 0, ns2::stream()>>>(x, ldx, y, ldy, rows, gpr);
+  NS2_LAUNCHED("rotate_f16");
+  return NS2_OK;
+}
+
+int ns2_norm_mod(const float* x, const float* mod, long long shiftOff, long long scaleOff,
+                 int rows, int cols, const float* weight, float eps, float* y) {
+  NS2_READY();
+  if (rows <= 0) return NS2_OK;
+  NS2_REQUIRE(x && mod && y && cols > 0, "ns2_norm_mod: bad arguments");
+  norm_mod_kernel<<<rows, 256, 0, ns2::stream()>>>(x, mod, shiftOff, scaleOff, cols, weight, eps, y);
+  NS2_LAUNCHED("norm_mod");
+  return NS2_OK;
+}
+
+int ns2_norm_mod_rotate_f16(const float* x, const float* mod, long long shiftOff,
+                            long long scaleOff, int rows, int cols, const float* weight,
+                            float eps, uint16_t* y) {
+  NS2_READY();
+  if (rows <= 0) return NS2_OK;
+  NS2_REQUIRE(cols % 256 == 0 && cols >= 256 && cols <= 4096,
+              "ns2_norm_mod_rotate_f16: cols=%d must be a multiple of 256 in [256, 4096]", cols);
+  NS2_REQUIRE(x && mod && y && aligned16(x) && aligned8(y) && shiftOff % 4 == 0 && scaleOff % 4 == 0 &&
+                  aligned16(mod) && (!weight || aligned16(weight)),
+              "ns2_norm_mod_rotate_f16: null or unaligned buffer/offset");
+  norm_mod_rot_kernel<<<rows, cols / 4, 0, ns2::stream()>>>(x, mod, shiftOff, scaleOff, cols, weight, eps, y);
+  NS2_LAUNCHED("norm_mod_rotate_f16");
+  return NS2_OK;
+}
+
+int ns2_head_norm(float* X, const float* w, int L, int H, int D, int ld, long long colOff,
+                  long long rowOff, const float* cs, long long sinOff, float eps) {
+  NS2_READY();
+  if (L <= 0 || H <= 0) return NS2_OK;
+  NS2_REQUIRE(X && w && D > 0 && D % 2 == 0, "ns2_head_norm: bad arguments");
+  head_norm_kernel<<<blocks_for((long long)L * H, 4), 256, 0, ns2::stream()>>>(X, w, L, H, D, ld, colOff, rowOff, cs, sinOff, eps);
+  NS2_LAUNCHED("head_norm");
+  return NS2_OK;
+}
+
+int ns2_glu(const float* x, float* y, int rows, int I, int act) {
+  NS2_READY();
+  if (rows <= 0) return NS2_OK;
+  NS2_REQUIRE(x && y && I > 0, "ns2_glu: bad arguments");
+  const long long n = (long long)rows * I;
+  glu_kernel<<<blocks_for(n, 256), 256, 0, ns2::stream()>>>(x, y, n, I, act);
+  NS2_LAUNCHED("glu");
+  return NS2_OK;
+}
+
+int ns2_glu_rotate_f16(const float* x, uint16_t* y, int rows, int I, int act) {
+  NS2_READY();
+  if (rows <= 0) return NS2_OK;
+  NS2_REQUIRE(I > 0 && I % 256 == 0, "ns2_glu_rotate_f16: I=%d must be a multiple of 256", I);
+  NS2_REQUIRE(x && y && aligned16(x) && aligned8(y), "ns2_glu_rotate_f16: null or unaligned buffer");
+  const long long groups = (long long)rows * (I / 256);
+  glu_rot_kernel<<<blocks_for(groups, 4), 256, 0, ns2::stream()>>>(x, y, rows, I, act);
+  NS2_LAUNCHED("glu_rotate_f16");
+  return NS2_OK;
+}
+
+int ns2_elementwise(int op, const float* a, const float* b, float* y, long long n) {
+  NS2_READY();
+  if (n <= 0) return NS2_OK;
+  NS2_REQUIRE(op >= NS2_EW_ADD && op <= NS2_EW_COPY, "ns2_elementwise: unknown op %d", op);
+  NS2_REQUIRE(a && y && (b || op == NS2_EW_SILU || op == NS2_EW_COPY), "ns2_elementwise: null buffer");
+  elementwise_kernel<<<blocks_for(n, 256), 256, 0, ns2::stream()>>>(op, a, b, y, n);
+  NS2_LAUNCHED("elementwise");
+  return NS2_OK;
+}
+
+int ns2_accumulate(float* y, const float* a, long long n) {
+  NS2_READY();
+  if (n <= 0) return NS2_OK;
+  NS2_REQUIRE(a && y, "ns2_accumulate: null buffer");
+  accumulate_kernel<<<blocks_for(n, 256), 256, 0, ns2::stream()>>>(y, a, n);
+  NS2_LAUNCHED("accumulate");
+  return NS2_OK;
+}
+
+int ns2_row_sum(const float* x, const float* w, float* y, int rows, int N, float scale) {
+  NS2_READY();
+  if (N <= 0) return NS2_OK;
+  NS2_REQUIRE(x && w && y && rows >= 0, "ns2_row_sum: bad arguments");
+  row_sum_kernel<<<blocks_for(N, 64), 64, 0, ns2::stream()>>>(x, w, y, rows, N, scale);
+  NS2_LAUNCHED("row_sum");
+  return NS2_OK;
+}
+
+int ns2_rmsnorm(const float* x, const float* w, float* y, int rows, int cols, float eps) {
+  NS2_READY();
+  if (rows <= 0) return NS2_OK;
+  NS2_REQUIRE(x && w && y && cols > 0, "ns2_rmsnorm: bad arguments");
+  rmsnorm_kernel<<<rows, 256, 0, ns2::stream()>>>(x, w, y, cols, eps);
+  NS2_LAUNCHED("rmsnorm");
+  return NS2_OK;
+}
+
+}  // extern "C"

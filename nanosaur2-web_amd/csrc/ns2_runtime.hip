@@ -1,0 +1,263 @@
+// Runtime half of the C ABI: device selection, errors, stream, buffer pool, workspace,
+// copies and timing events. Replaces the WebGPU runtime of app/gpu/device.js.
+#include <math.h>
+#include <stdarg.h>
+#include <string.h>
+
+#include <map>
+#include <mutex>
+#include <vector>
+
+#include "ns2_common.h"
+
+namespace ns2 {
+
+static thread_local char g_error[1024] = "";
+static bool g_init = false;
+static int g_device = 0;
+static hipStream_t g_stream = nullptr;
+
+int set_error(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_error, sizeof(g_error), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+void clear_error() { g_error[0] = 0; }
+hipStream_t stream() { return g_stream; }
+bool initialised() { return g_init; }
+
+// ---- buffer pool: size buckets of app/gpu/device.js:33-39 ------------------------------
+struct Pool {
+  std::mutex mu;
+  std::map<size_t, std::vector<void*>> free_lists;
+  size_t allocated = 0;
+  size_t peak = 0;
+};
+static Pool g_pool;
+
+// ---- workspace ----------------------------------------------------------------------------
+struct Workspace {
+  void* ptr = nullptr;
+  size_t bytes = 0;
+};
+static Workspace g_ws[kWorkspaceSlots];
+
+void* workspace(int slot, size_t bytes) {
+  if (slot < 0 || slot >= kWorkspaceSlots) return nullptr;
+  Workspace& w = g_ws[slot];
+  if (w.bytes >= bytes && w.ptr) return w.ptr;
+  // the old buffer may still be read by queued kernels: wait before freeing it
+  if (w.ptr) {
+    if (hipStreamSynchronize(g_stream) != hipSuccess) return nullptr;
+    if (hipFree(w.ptr) != hipSuccess) return nullptr;
+    w.ptr = nullptr;
+    w.bytes = 0;
+  }
+  size_t want = bytes + bytes / 4 + 4096;
+  if (hipMalloc(&w.ptr, want) != hipSuccess) {
+    w.ptr = nullptr;
+    return nullptr;
+  }
+  w.bytes = want;
+  return w.ptr;
+}
+
+__global__ void fill_u32_kernel(uint32_t* __restrict__ p, uint32_t value, size_t count) {
+  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (; i < count; i += stride) p[i] = value;
+}
+
+}  // namespace ns2
+
+using namespace ns2;
+
+extern "C" {
+
+const char* ns2_last_error(void) { return g_error; }
+
+int ns2_init(int device) {
+  clear_error();
+  int n = 0;
+  NS2_HIP(hipGetDeviceCount(&n));
+  NS2_REQUIRE(device >= 0 && device < n, "ns2_init: device %d out of range (%d devices)", device, n);
+  NS2_HIP(hipSetDevice(device));
+  g_device = device;
+  g_init = true;
+  return NS2_OK;
+}
+
+int ns2_device_info(char* name, size_t cap, int* compute_units, size_t* hbm_bytes) {
+  NS2_READY();
+  hipDeviceProp_t p;
+  NS2_HIP(hipGetDeviceProperties(&p, g_device));
+  if (name && cap) {
+    snprintf(name, cap, "%s (%s)", p.name, p.gcnArchName);
+  }
+  if (compute_units) *compute_units = p.multiProcessorCount;
+  if (hbm_bytes) *hbm_bytes = p.totalGlobalMem;
+  return NS2_OK;
+}
+
+int ns2_set_stream(void* hip_stream) {
+  g_stream = (hipStream_t)hip_stream;
+  return NS2_OK;
+}
+
+void* ns2_get_stream(void) { return (void*)g_stream; }
+
+int ns2_malloc(void** ptr, size_t bytes) {
+  NS2_READY();
+  NS2_REQUIRE(ptr != nullptr, "ns2_malloc: null out-pointer");
+  // padded to 16 bytes like app/gpu/device.js:135 (vector-loadable tails)
+  size_t size = bytes < 16 ? 16 : (bytes + 15) / 16 * 16;
+  if (hipMalloc(ptr, size) != hipSuccess) {
+    *ptr = nullptr;
+    (void)hipGetLastError();
+    return set_error(NS2_ERR_OOM, "ns2_malloc: out of device memory for %zu bytes", size);
+  }
+  return NS2_OK;
+}
+
+int ns2_free(void* ptr) {
+  if (!ptr) return NS2_OK;
+  NS2_READY();
+  // a kernel still queued may read the buffer
+  NS2_HIP(hipStreamSynchronize(g_stream));
+  NS2_HIP(hipFree(ptr));
+  return NS2_OK;
+}
+
+size_t ns2_pool_round(size_t bytes) {
+  size_t b = bytes < 256 ? 256 : bytes;
+  size_t p = 1;
+  while (p <= b / 2) p <<= 1;  // largest power of two <= b
+  size_t step = p / 8 < 256 ? 256 : p / 8;
+  return (b + step - 1) / step * step;
+}
+
+int ns2_pool_get(size_t bytes, void** ptr, size_t* rounded) {
+  NS2_READY();
+  NS2_REQUIRE(ptr != nullptr, "ns2_pool_get: null out-pointer");
+  size_t size = ns2_pool_round(bytes);
+  if (rounded) *rounded = size;
+  {
+    std::lock_guard<std::mutex> lk(g_pool.mu);
+    auto it = g_pool.free_lists.find(size);
+    if (it != g_pool.free_lists.end() && !it->second.empty()) {
+      *ptr = it->second.back();
+      it->second.pop_back();
+      return NS2_OK;
+    }
+  }
+  if (hipMalloc(ptr, size) != hipSuccess) {
+    *ptr = nullptr;
+    (void)hipGetLastError();
+    return set_error(NS2_ERR_OOM, "ns2_pool_get: out of device memory for %zu bytes", size);
+  }
+  std::lock_guard<std::mutex> lk(g_pool.mu);
+  g_pool.allocated += size;
+  if (g_pool.allocated > g_pool.peak) g_pool.peak = g_pool.allocated;
+  return NS2_OK;
+}
+
+int ns2_pool_put(void* ptr, size_t rounded) {
+  if (!ptr) return NS2_OK;
+  NS2_REQUIRE(rounded == ns2_pool_round(rounded), "ns2_pool_put: %zu is not a bucket size", rounded);
+  std::lock_guard<std::mutex> lk(g_pool.mu);
+  g_pool.free_lists[rounded].push_back(ptr);
+  return NS2_OK;
+}
+
+int ns2_pool_trim(void) {
+  NS2_READY();
+  NS2_HIP(hipStreamSynchronize(g_stream));
+  std::lock_guard<std::mutex> lk(g_pool.mu);
+  for (auto& kv : g_pool.free_lists) {
+    for (void* p : kv.second) {
+      NS2_HIP(hipFree(p));
+      g_pool.allocated -= kv.first;
+    }
+  }
+  g_pool.free_lists.clear();
+  return NS2_OK;
+}
+
+int ns2_pool_stats(size_t* allocated, size_t* peak) {
+  std::lock_guard<std::mutex> lk(g_pool.mu);
+  if (allocated) *allocated = g_pool.allocated;
+  if (peak) *peak = g_pool.peak;
+  return NS2_OK;
+}
+
+int ns2_h2d(void* dst, const void* src, size_t bytes) {
+  NS2_READY();
+  if (!bytes) return NS2_OK;
+  NS2_REQUIRE(dst && src, "ns2_h2d: null pointer");
+  // pageable source: the copy has completed reading src when this returns
+  NS2_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, g_stream));
+  NS2_HIP(hipStreamSynchronize(g_stream));
+  return NS2_OK;
+}
+
+int ns2_d2h(void* dst, const void* src, size_t bytes) {
+  NS2_READY();
+  if (!bytes) return NS2_OK;
+  NS2_REQUIRE(dst && src, "ns2_d2h: null pointer");
+  NS2_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, g_stream));
+  NS2_HIP(hipStreamSynchronize(g_stream));
+  return NS2_OK;
+}
+
+int ns2_sync(void) {
+  NS2_READY();
+  NS2_HIP(hipStreamSynchronize(g_stream));
+  NS2_HIP(hipGetLastError());
+  return NS2_OK;
+}
+
+int ns2_fill_u32(void* dst, uint32_t value, size_t count) {
+  NS2_READY();
+  if (!count) return NS2_OK;
+  NS2_REQUIRE(dst != nullptr, "ns2_fill_u32: null pointer");
+  size_t blocks = (count + 255) / 256;
+  if (blocks > 8192) blocks = 8192;
+  fill_u32_kernel<<<dim3((unsigned)blocks), dim3(256), 0, g_stream>>>((uint32_t*)dst, value, count);
+  NS2_LAUNCHED("fill_u32");
+  return NS2_OK;
+}
+
+int ns2_event_create(void** ev) {
+  NS2_READY();
+  NS2_REQUIRE(ev != nullptr, "ns2_event_create: null out-pointer");
+  hipEvent_t e;
+  NS2_HIP(hipEventCreate(&e));
+  *ev = (void*)e;
+  return NS2_OK;
+}
+
+int ns2_event_record(void* ev) {
+  NS2_READY();
+  NS2_REQUIRE(ev != nullptr, "ns2_event_record: null event");
+  NS2_HIP(hipEventRecord((hipEvent_t)ev, g_stream));
+  return NS2_OK;
+}
+
+int ns2_event_elapsed(void* start, void* end, float* ms) {
+  NS2_READY();
+  NS2_REQUIRE(start && end && ms, "ns2_event_elapsed: null argument");
+  NS2_HIP(hipEventSynchronize((hipEvent_t)end));
+  NS2_HIP(hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)end));
+  return NS2_OK;
+}
+
+int ns2_event_destroy(void* ev) {
+  if (!ev) return NS2_OK;
+  NS2_HIP(hipEventDestroy((hipEvent_t)ev));
+  return NS2_OK;
+}
+
+}  // extern "C"

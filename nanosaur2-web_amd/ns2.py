@@ -1,0 +1,204 @@
+"""ctypes binding of the ns2 C ABI (include/ns2.h) for Python callers (tests, bench).
+
+Device buffers are passed as integer addresses (e.g. ``tensor.data_ptr()`` of a HIP tensor);
+every call checks the status code and raises NS2Error with the library's message. The library
+must have been built (``make -C nanosaur2-web_amd``); importing this module never falls back
+to anything else.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "lib", "libns2.so")
+ADDON_PATH = os.path.join(HERE, "lib", "ns2.node")
+
+ACT = {"none": 0, "silu": 1, "gelu_tanh": 2}
+EW = {"add": 0, "sub": 1, "silu": 2, "copy": 3}
+
+c_int, c_ll, c_float, c_size, c_vp = ctypes.c_int, ctypes.c_longlong, ctypes.c_float, ctypes.c_size_t, ctypes.c_void_p
+
+# name -> argtypes (all return int status unless listed in _RESTYPES)
+SIGNATURES = {
+    "ns2_init": [c_int],
+    "ns2_last_error": [],
+    "ns2_device_info": [ctypes.c_char_p, c_size, ctypes.POINTER(c_int), ctypes.POINTER(c_size)],
+    "ns2_set_stream": [c_vp],
+    "ns2_get_stream": [],
+    "ns2_malloc": [ctypes.POINTER(c_vp), c_size],
+    "ns2_free": [c_vp],
+    "ns2_pool_round": [c_size],
+    "ns2_pool_get": [c_size, ctypes.POINTER(c_vp), ctypes.POINTER(c_size)],
+    "ns2_pool_put": [c_vp, c_size],
+    "ns2_pool_trim": [],
+    "ns2_pool_stats": [ctypes.POINTER(c_size), ctypes.POINTER(c_size)],
+    "ns2_h2d": [c_vp, c_vp, c_size],
+    "ns2_d2h": [c_vp, c_vp, c_size],
+    "ns2_sync": [],
+    "ns2_fill_u32": [c_vp, ctypes.c_uint32, c_size],
+    "ns2_event_create": [ctypes.POINTER(c_vp)],
+    "ns2_event_record": [c_vp],
+    "ns2_event_elapsed": [c_vp, c_vp, ctypes.POINTER(c_float)],
+    "ns2_event_destroy": [c_vp],
+    "ns2_hadamard256": [c_vp, c_vp, c_ll],
+    "ns2_rotate_f16": [c_vp, c_int, c_vp, c_int, c_int, c_int],
+    "ns2_linear_i8": [c_vp, c_int, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int,
+                      c_ll, c_float, c_int, c_int, c_vp, c_ll],
+    "ns2_linear_bf16": [c_vp, c_int, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_ll,
+                        c_float, c_int, c_int, c_vp, c_ll],
+    "ns2_attention": [c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
+                      c_int, c_ll, c_ll, c_ll, c_ll, c_ll, c_ll, c_ll, c_ll, c_float, c_vp, c_int,
+                      c_ll, c_vp, c_vp, c_float, c_vp, c_ll, c_int],
+    "ns2_head_norm": [c_vp, c_vp, c_int, c_int, c_int, c_int, c_ll, c_ll, c_vp, c_ll, c_float],
+    "ns2_norm_mod": [c_vp, c_vp, c_ll, c_ll, c_int, c_int, c_vp, c_float, c_vp],
+    "ns2_norm_mod_rotate_f16": [c_vp, c_vp, c_ll, c_ll, c_int, c_int, c_vp, c_float, c_vp],
+    "ns2_glu": [c_vp, c_vp, c_int, c_int, c_int],
+    "ns2_glu_rotate_f16": [c_vp, c_vp, c_int, c_int, c_int],
+    "ns2_elementwise": [c_int, c_vp, c_vp, c_vp, c_ll],
+    "ns2_accumulate": [c_vp, c_vp, c_ll],
+    "ns2_row_sum": [c_vp, c_vp, c_vp, c_int, c_int, c_float],
+    "ns2_rmsnorm": [c_vp, c_vp, c_vp, c_int, c_int, c_float],
+}
+_RESTYPES = {"ns2_last_error": ctypes.c_char_p, "ns2_get_stream": c_vp, "ns2_pool_round": c_size}
+
+
+class NS2Error(RuntimeError):
+    pass
+
+
+def _ptr(x):
+    """Device address of a tensor-like (``data_ptr()``), an int, or None -> NULL."""
+    if x is None:
+        return None
+    if isinstance(x, int):
+        return x
+    return x.data_ptr()
+
+
+class Lib:
+    """Loaded libns2.so with checked calls."""
+
+    def __init__(self, path: str = LIB_PATH):
+        if not os.path.exists(path):
+            raise NS2Error(f"{path} is not built: run `make -C nanosaur2-web_amd`")
+        self.path = path
+        self.dll = ctypes.CDLL(path)
+        for name, args in SIGNATURES.items():
+            fn = getattr(self.dll, name)
+            fn.argtypes = args
+            fn.restype = _RESTYPES.get(name, c_int)
+
+    def exported(self):
+        return [n for n in SIGNATURES if hasattr(self.dll, n)]
+
+    def error(self) -> str:
+        return self.dll.ns2_last_error().decode()
+
+    def call(self, name, *args):
+        rc = getattr(self.dll, name)(*args)
+        if rc != 0:
+            raise NS2Error(f"{name} failed ({rc}): {self.error()}")
+        return rc
+
+    # ---- runtime
+    def init(self, device: int = 0):
+        self.call("ns2_init", device)
+
+    def set_stream(self, stream_handle: int | None):
+        self.call("ns2_set_stream", stream_handle)
+
+    def sync(self):
+        self.call("ns2_sync")
+
+    def device_info(self):
+        name = ctypes.create_string_buffer(256)
+        cus, hbm = c_int(), c_size()
+        self.call("ns2_device_info", name, 256, ctypes.byref(cus), ctypes.byref(hbm))
+        return {"name": name.value.decode(), "compute_units": cus.value, "hbm_bytes": hbm.value}
+
+    def event(self):
+        ev = c_vp()
+        self.call("ns2_event_create", ctypes.byref(ev))
+        return ev.value
+
+    def record(self, ev):
+        self.call("ns2_event_record", ev)
+
+    def elapsed_ms(self, a, b) -> float:
+        ms = c_float()
+        self.call("ns2_event_elapsed", a, b, ctypes.byref(ms))
+        return ms.value
+
+    # ---- ops (argument meaning as in include/ns2.h)
+    def hadamard256(self, x, y, groups):
+        self.call("ns2_hadamard256", _ptr(x), _ptr(y), groups)
+
+    def rotate_f16(self, x, ldx, y, ldy, rows, cols):
+        self.call("ns2_rotate_f16", _ptr(x), ldx, _ptr(y), ldy, rows, cols)
+
+    def linear_i8(self, A, a_fmt, lda, W, scale, C, M, N, K, *, bias=None, add=None, ldc=None,
+                  cOff=0, alpha=1.0, act="none", resid=False, gate=None, gOff=0):
+        self.call("ns2_linear_i8", _ptr(A), a_fmt, lda, _ptr(W), _ptr(scale), _ptr(bias), _ptr(add),
+                  _ptr(C), M, N, K, N if ldc is None else ldc, cOff, alpha, ACT[act], int(resid),
+                  _ptr(gate), gOff)
+
+    def linear_bf16(self, A, lda, W, C, M, N, K, *, bias=None, add=None, ldc=None, cOff=0,
+                    alpha=1.0, act="none", resid=False, gate=None, gOff=0):
+        self.call("ns2_linear_bf16", _ptr(A), lda, _ptr(W), _ptr(bias), _ptr(add), _ptr(C), M, N, K,
+                  N if ldc is None else ldc, cOff, alpha, ACT[act], int(resid), _ptr(gate), gOff)
+
+    def attention(self, q, k, v, o, *, Lq, Lk, H, D, ldq, ldk, ldv, ldo, qOff=0, kOff=0, vOff=0,
+                  oOff=0, batch=1, qBatch=0, kBatch=0, vBatch=0, oBatch=0, scale=None,
+                  key_bias=None, biasStart=0, biasBatch=0, q_norm=None, k_norm=None, eps=1e-6,
+                  rope_cs=None, sin_off=0, rope_rows=0):
+        if scale is None:
+            scale = 1.0 / D ** 0.5
+        self.call("ns2_attention", _ptr(q), _ptr(k), _ptr(v), _ptr(o), batch, Lq, Lk, H, D, ldq, ldk,
+                  ldv, ldo, qOff, kOff, vOff, oOff, qBatch, kBatch, vBatch, oBatch, scale,
+                  _ptr(key_bias), biasStart, biasBatch, _ptr(q_norm), _ptr(k_norm), eps,
+                  _ptr(rope_cs), sin_off, rope_rows)
+
+    def head_norm(self, X, w, L, H, D, ld, colOff=0, rowOff=0, cs=None, sinOff=0, eps=1e-6):
+        self.call("ns2_head_norm", _ptr(X), _ptr(w), L, H, D, ld, colOff, rowOff, _ptr(cs), sinOff, eps)
+
+    def norm_mod(self, x, mod, shiftOff, scaleOff, rows, cols, weight, y, eps=1e-6):
+        self.call("ns2_norm_mod", _ptr(x), _ptr(mod), shiftOff, scaleOff, rows, cols, _ptr(weight), eps, _ptr(y))
+
+    def norm_mod_rotate_f16(self, x, mod, shiftOff, scaleOff, rows, cols, weight, y, eps=1e-6):
+        self.call("ns2_norm_mod_rotate_f16", _ptr(x), _ptr(mod), shiftOff, scaleOff, rows, cols,
+                  _ptr(weight), eps, _ptr(y))
+
+    def glu(self, x, y, rows, I, act="silu"):
+        self.call("ns2_glu", _ptr(x), _ptr(y), rows, I, ACT[act])
+
+    def glu_rotate_f16(self, x, y, rows, I, act="silu"):
+        self.call("ns2_glu_rotate_f16", _ptr(x), _ptr(y), rows, I, ACT[act])
+
+    def elementwise(self, op, a, b, y, n):
+        self.call("ns2_elementwise", EW[op], _ptr(a), _ptr(b), _ptr(y), n)
+
+    def accumulate(self, y, a, n):
+        self.call("ns2_accumulate", _ptr(y), _ptr(a), n)
+
+    def row_sum(self, x, w, y, rows, N, scale=1.0):
+        self.call("ns2_row_sum", _ptr(x), _ptr(w), _ptr(y), rows, N, scale)
+
+    def rmsnorm(self, x, w, y, rows, cols, eps=1e-6):
+        self.call("ns2_rmsnorm", _ptr(x), _ptr(w), _ptr(y), rows, cols, eps)
+
+
+_LIB = None
+
+
+def load(device: int = 0, stream_handle: int | None = None) -> Lib:
+    """The process-wide library handle, initialised on `device`."""
+    global _LIB
+    if _LIB is None:
+        lib = Lib()
+        lib.init(device)
+        _LIB = lib
+    if stream_handle is not None:
+        _LIB.set_stream(stream_handle)
+    return _LIB

@@ -1,0 +1,371 @@
+"""Parity of every HIP op against the CPU oracle, called through the C ABI (ctypes).
+
+Tolerances: 2e-3 (max|d|/max|ref| and rel-L2) for GEMM/attention outputs computed on fp16
+MFMA operands; 1e-5 for the fp32-only row kernels.
+"""
+
+import math
+
+import pytest
+import torch
+
+import oracle.nanosaur2_oracle as O
+from conftest import assert_close
+
+pytestmark = pytest.mark.gpu
+dev = "cuda"
+TOL = 2e-3        # north_star tolerance for attention / GEMM outputs
+TOL_F32 = 1e-5    # kernels that compute in fp32 end to end
+TOL_F16_OUT = 2e-3  # fp32 math, fp16-rounded output
+
+
+def gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def int8_weight(N, K, g):
+    q = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int32).to(torch.int8)
+    s = torch.rand(N, 1, generator=g) * 9e-3 + 1e-3
+    return q, s
+
+
+def f16_as_float(t):
+    return t.view(torch.float16).float()
+
+
+# ----------------------------------------------------------------------------- rotation
+
+@pytest.mark.parametrize("rows,cols", [(1, 256), (7, 1536), (2432, 1536), (300, 4096)])
+def test_hadamard256(ns2lib, rows, cols):
+    g = gen(rows + cols)
+    x = torch.randn(rows, cols, generator=g)
+    xd = x.to(dev)
+    y = torch.empty_like(xd)
+    ns2lib.hadamard256(xd, y, rows * cols // 256)
+    torch.cuda.synchronize()
+    assert_close(y.cpu(), O.rotate(x.double()), TOL_F32, f"hadamard256 {rows}x{cols}")
+
+
+def test_hadamard256_in_place(ns2lib):
+    x = torch.randn(64, 512, generator=gen(3))
+    xd = x.to(dev)
+    ns2lib.hadamard256(xd, xd, 128)
+    torch.cuda.synchronize()
+    assert_close(xd.cpu(), O.rotate(x.double()), TOL_F32, "hadamard256 in place")
+
+
+def test_rotate_f16_strided(ns2lib):
+    x = torch.randn(100, 1024, generator=gen(4))
+    xd = x.to(dev)
+    y = torch.zeros(100, 640, dtype=torch.int16, device=dev)
+    # columns [256, 768) of x into columns [0, 512) of a wider fp16 buffer
+    ns2lib.rotate_f16(xd.data_ptr() + 256 * 4, 1024, y, 640, 100, 512)
+    torch.cuda.synchronize()
+    got = f16_as_float(y.cpu())[:, :512]
+    assert_close(got, O.rotate(x[:, 256:768].double()), TOL_F16_OUT, "rotate_f16 strided")
+    assert (f16_as_float(y.cpu())[:, 512:] == 0).all()
+
+
+# ----------------------------------------------------------------------------- int8 ConvRot linear
+
+@pytest.mark.parametrize("M,N,K", [
+    (2432, 4608, 1536),   # fused QKV
+    (2432, 1536, 1536),   # out projection
+    (2432, 6144, 1536),   # MLP up
+    (2432, 1536, 6144),   # MLP down
+    (3952, 8192, 1536),   # real-model w12
+    (97, 300, 512),       # ragged tails
+    (1, 1536, 1536),      # GEMV path
+    (5, 3072, 1536),
+])
+def test_linear_i8_shapes(ns2lib, M, N, K):
+    g = gen(M * 7 + N + K)
+    x = torch.randn(M, K, generator=g)
+    q, s = int8_weight(N, K, g)
+    ref = O.linear_i8(x.double(), q, s.double())
+    # equals x @ W_deq^T (tools/quant.py:59-64)
+    if M * N * K <= 2e9:
+        assert_close(ref, x.double() @ O.dequantize(q, s, torch.float64).T, 1e-9, "oracle identity")
+    xd, qd, sd = x.to(dev), q.to(dev), s.reshape(-1).to(dev)
+    out = torch.empty(M, N, device=dev)
+    ns2lib.linear_i8(xd, 0, K, qd, sd, out, M, N, K)
+    torch.cuda.synchronize()
+    assert_close(out.cpu(), ref, TOL, f"linear_i8 a_fmt=0 {M}x{N}x{K}")
+    # pre-rotated fp16 input (ops.linear with opts.xr)
+    xr = torch.empty(M, K, dtype=torch.int16, device=dev)
+    ns2lib.rotate_f16(xd, K, xr, K, M, K)
+    out2 = torch.empty(M, N, device=dev)
+    ns2lib.linear_i8(xr, 1, K, qd, sd, out2, M, N, K)
+    torch.cuda.synchronize()
+    assert torch.equal(out.cpu(), out2.cpu())
+
+
+def test_linear_i8_epilogues(ns2lib):
+    M, N, K = 300, 384, 768
+    g = gen(11)
+    x = torch.randn(M, K, generator=g)
+    q, s = int8_weight(N, K, g)
+    bias = torch.randn(N, generator=g)
+    add = torch.randn(M, N, generator=g)
+    gate = torch.randn(4 * N, generator=g)
+    base = torch.randn(M, N, generator=g)
+    xd, qd, sd = x.to(dev), q.to(dev), s.reshape(-1).to(dev)
+
+    # bias + add + silu + alpha
+    out = torch.empty(M, N, device=dev)
+    ns2lib.linear_i8(xd, 0, K, qd, sd, out, M, N, K, bias=bias.to(dev), add=add.to(dev), alpha=0.5, act="silu")
+    ref = O.linear_i8(x.double(), q, s.double(), alpha=0.5, bias=bias.double(), add=add.double(), act="silu")
+    torch.cuda.synchronize()
+    assert_close(out.cpu(), ref, TOL, "bias+add+silu+alpha")
+
+    # residual
+    outd = base.to(dev)
+    ns2lib.linear_i8(xd, 0, K, qd, sd, outd, M, N, K, resid=True)
+    ref = O.linear_i8(x.double(), q, s.double(), out=base.double().clone(), resid=True)
+    torch.cuda.synchronize()
+    assert_close(outd.cpu(), ref, TOL, "resid")
+
+    # gated residual (gate at an offset, app/models/nanosaur2.js:210)
+    outd = base.to(dev)
+    ns2lib.linear_i8(xd, 0, K, qd, sd, outd, M, N, K, resid=True, gate=gate.to(dev), gOff=2 * N)
+    ref = O.linear_i8(x.double(), q, s.double(), out=base.double().clone(), resid=True, gate=gate.double(), gOff=2 * N)
+    torch.cuda.synchronize()
+    assert_close(outd.cpu(), ref, TOL, "gated resid")
+
+
+def test_linear_i8_column_window(ns2lib):
+    """kv_y writes rows [L, L+T), cols [D, 3D) of the packed qkv (app/models/nanosaur2.js:202)."""
+    L, T, Dm = 40, 24, 256
+    g = gen(12)
+    txt = torch.randn(T, Dm, generator=g)
+    q, s = int8_weight(2 * Dm, Dm, g)
+    qkv = torch.randn(L + T, 3 * Dm, generator=g)
+    qkvd = qkv.to(dev)
+    ns2lib.linear_i8(txt.to(dev), 0, Dm, q.to(dev), s.reshape(-1).to(dev), qkvd, T, 2 * Dm, Dm,
+                     ldc=3 * Dm, cOff=L * 3 * Dm + Dm)
+    ref = qkv.double().clone()
+    O.linear_i8(txt.double(), q, s.double(), out=ref, ldc=3 * Dm, cOff=L * 3 * Dm + Dm)
+    torch.cuda.synchronize()
+    got = qkvd.cpu()
+    assert torch.equal(got[:L], qkv[:L]) and torch.equal(got[L:, :Dm], qkv[L:, :Dm])
+    assert_close(got, ref, TOL, "kv_y column window")
+
+
+# ----------------------------------------------------------------------------- bf16 linear
+
+@pytest.mark.parametrize("M,N,K", [(3952, 1536, 64), (3952, 1536, 1536), (3952, 64, 1536),
+                                   (256, 1536, 640), (1, 9216, 1536), (1, 1536, 256), (3, 3072, 1536)])
+def test_linear_bf16(ns2lib, M, N, K):
+    g = gen(M + N + K)
+    x = torch.randn(M, K, generator=g)
+    w = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
+    bias = torch.randn(N, generator=g) * 0.1
+    ref = O.linear_bf16(x.double(), w, bias=bias.double())
+    out = torch.empty(M, N, device=dev)
+    ns2lib.linear_bf16(x.to(dev), K, w.view(torch.int16).to(dev), out, M, N, K, bias=bias.to(dev))
+    torch.cuda.synchronize()
+    assert_close(out.cpu(), ref, TOL, f"linear_bf16 {M}x{N}x{K}")
+
+
+def test_linear_bf16_gemv_silu_resid(ns2lib):
+    g = gen(21)
+    x = torch.randn(1, 256, generator=g)
+    w = (torch.randn(1536, 256, generator=g) * 0.05).to(torch.bfloat16)
+    out = torch.empty(1, 1536, device=dev)
+    ns2lib.linear_bf16(x.to(dev), 256, w.view(torch.int16).to(dev), out, 1, 1536, 256, act="silu")
+    torch.cuda.synchronize()
+    assert_close(out.cpu(), O.linear_bf16(x.double(), w, act="silu"), TOL_F32 * 10, "gemv silu")
+    base = torch.randn(1, 1536, generator=g)
+    outd = base.to(dev)
+    ns2lib.linear_bf16(x.to(dev), 256, w.view(torch.int16).to(dev), outd, 1, 1536, 256, resid=True)
+    torch.cuda.synchronize()
+    assert_close(outd.cpu(), O.linear_bf16(x.double(), w, out=base.double().clone(), resid=True), TOL_F32 * 10, "gemv resid")
+
+
+# ----------------------------------------------------------------------------- attention
+
+def _attn_inputs(seed, Lq_img, T, heads=16, hd=96):
+    g = gen(seed)
+    Dm = heads * hd
+    Lk = Lq_img + T
+    q = torch.randn(Lq_img, Dm, generator=g)
+    k = torch.randn(Lk, Dm, generator=g)
+    v = torch.randn(Lk, Dm, generator=g)
+    w = torch.rand(T, generator=g) + 0.5
+    return q, k, v, torch.log(w)
+
+
+@pytest.mark.parametrize("hgrid,wgrid,T", [(48, 48, 128), (76, 52, 256), (5, 7, 3), (16, 16, 0)])
+def test_joint_attention_rope_bias(ns2lib, hgrid, wgrid, T):
+    """Config 0/2 op: RoPE on image q/k rows, log-weight bias on text keys."""
+    L = hgrid * wgrid
+    q, k, v, lb = _attn_inputs(L + T, L, T)
+    cs, sin_off = O.rope2d_table(hgrid, wgrid)
+    half = 48
+    cos = cs[:sin_off].reshape(L, half).double()
+    sin = cs[sin_off:].reshape(L, half).double()
+    ref = O.joint_attention_op(q.double(), k.double(), v.double(), L, cos, sin,
+                               key_bias=lb.double() if T else None, bias_start=L)
+    o = torch.empty(L, 1536, device=dev)
+    ns2lib.attention(q.to(dev), k.to(dev), v.to(dev), o, Lq=L, Lk=L + T, H=16, D=96, ldq=1536,
+                     ldk=1536, ldv=1536, ldo=1536, key_bias=lb.to(dev) if T else None, biasStart=L,
+                     rope_cs=cs.to(dev), sin_off=sin_off, rope_rows=L)
+    torch.cuda.synchronize()
+    assert_close(o.cpu(), ref, TOL, f"joint attention {hgrid}x{wgrid}+{T}")
+
+
+def test_attention_batch2_config2(ns2lib):
+    """Config 2: 832x1216 (76x52 latent), 256 text tokens, batch 2 in one call."""
+    L, T = 76 * 52, 256
+    qs, ks, vs, bs = zip(*[_attn_inputs(100 + b, L, T) for b in range(2)])
+    cs, sin_off = O.rope2d_table(76, 52)
+    q = torch.stack(qs).to(dev)
+    k = torch.stack(ks).to(dev)
+    v = torch.stack(vs).to(dev)
+    bias = torch.stack(bs).to(dev)
+    o = torch.empty(2, L, 1536, device=dev)
+    ns2lib.attention(q, k, v, o, Lq=L, Lk=L + T, H=16, D=96, ldq=1536, ldk=1536, ldv=1536, ldo=1536,
+                     batch=2, qBatch=L * 1536, kBatch=(L + T) * 1536, vBatch=(L + T) * 1536,
+                     oBatch=L * 1536, key_bias=bias, biasStart=L, biasBatch=T,
+                     rope_cs=cs.to(dev), sin_off=sin_off, rope_rows=L)
+    torch.cuda.synchronize()
+    cos = cs[:sin_off].reshape(L, 48)
+    sin = cs[sin_off:].reshape(L, 48)
+    heads = [0, 7, 15]  # oracle on a subset of heads keeps the CPU time small
+    for b in range(2):
+        for h in heads:
+            sl = slice(h * 96, (h + 1) * 96)
+            ref = O.joint_attention_op(qs[b][:, sl], ks[b][:, sl], vs[b][:, sl], L, cos, sin,
+                                       key_bias=bs[b], bias_start=L, heads=1)
+            assert_close(o[b, :, sl].cpu(), ref, TOL, f"config2 batch {b} head {h}")
+
+
+def test_attention_strided_qkv_views(ns2lib):
+    """q/k/v as column windows of one packed [Lk, 3D] buffer, like the DiT's qkv
+    (app/models/nanosaur2.js:205-208), with fused per-head norms (the headNorm calls)."""
+    L, T, Dm = 130, 20, 1536
+    g = gen(31)
+    qkv = torch.randn(L + T, 3 * Dm, generator=g)
+    qn = torch.randn(96, generator=g) * 0.5 + 1
+    kn = torch.randn(96, generator=g) * 0.5 + 1
+    cs, sin_off = O.rope2d_table(10, 13)
+    lb = torch.log(torch.rand(T, generator=g) + 0.5)
+    o = torch.empty(L, Dm, device=dev)
+    ns2lib.attention(qkv.to(dev), qkv.to(dev), qkv.to(dev), o, Lq=L, Lk=L + T, H=16, D=96, ldq=3 * Dm,
+                     ldk=3 * Dm, ldv=3 * Dm, ldo=Dm, qOff=0, kOff=Dm, vOff=2 * Dm, key_bias=lb.to(dev),
+                     biasStart=L, q_norm=qn.to(dev), k_norm=kn.to(dev), rope_cs=cs.to(dev),
+                     sin_off=sin_off, rope_rows=L)
+    torch.cuda.synchronize()
+    ref_buf = qkv.double().clone()
+    O.head_norm_rope(ref_buf, qn.double(), L, 16, 96, 3 * Dm, colOff=0, cs=cs, sinOff=sin_off)
+    O.head_norm_rope(ref_buf, kn.double(), L, 16, 96, 3 * Dm, colOff=Dm, cs=cs, sinOff=sin_off)
+    O.head_norm_rope(ref_buf, kn.double(), T, 16, 96, 3 * Dm, colOff=Dm, rowOff=L)
+    bias = torch.cat([torch.zeros(L, dtype=torch.float64), lb.double()])
+    ref = O.attention_heads(ref_buf[:L, :Dm], ref_buf[:, Dm:2 * Dm], ref_buf[:, 2 * Dm:], 16, 96, bias)
+    assert_close(o.cpu(), ref, TOL, "strided qkv + fused head norms")
+
+
+@pytest.mark.parametrize("Dh", [32, 64, 128])
+def test_attention_head_dims(ns2lib, Dh):
+    g = gen(Dh)
+    Lq, Lk, H = 200, 333, 3
+    q = torch.randn(Lq, H * Dh, generator=g)
+    k = torch.randn(Lk, H * Dh, generator=g)
+    v = torch.randn(Lk, H * Dh, generator=g)
+    o = torch.empty(Lq, H * Dh, device=dev)
+    ns2lib.attention(q.to(dev), k.to(dev), v.to(dev), o, Lq=Lq, Lk=Lk, H=H, D=Dh, ldq=H * Dh,
+                     ldk=H * Dh, ldv=H * Dh, ldo=H * Dh)
+    torch.cuda.synchronize()
+    assert_close(o.cpu(), O.attention_heads(q.double(), k.double(), v.double(), H, Dh), TOL, f"D={Dh}")
+
+
+# ----------------------------------------------------------------------------- row kernels
+
+@pytest.mark.parametrize("rms", [True, False])
+def test_norm_mod(ns2lib, rms):
+    g = gen(41)
+    rows, cols = 517, 1536
+    x = torch.randn(rows, cols, generator=g) * 3 + 0.5
+    mod = torch.randn(6 * cols, generator=g) * 0.1
+    w = torch.randn(cols, generator=g) * 0.02 if rms else None
+    y = torch.empty(rows, cols, device=dev)
+    ns2lib.norm_mod(x.to(dev), mod.to(dev), 3 * cols, 4 * cols, rows, cols, w.to(dev) if rms else None, y)
+    torch.cuda.synchronize()
+    ref = O.norm_mod(x.double(), mod.double(), 3 * cols, 4 * cols, w.double() if rms else None)
+    assert_close(y.cpu(), ref, TOL_F32, f"norm_mod rms={rms}")
+    yr = torch.empty(rows, cols, dtype=torch.int16, device=dev)
+    ns2lib.norm_mod_rotate_f16(x.to(dev), mod.to(dev), 3 * cols, 4 * cols, rows, cols, w.to(dev) if rms else None, yr)
+    torch.cuda.synchronize()
+    assert_close(f16_as_float(yr.cpu()), O.rotate(ref), TOL_F16_OUT, f"norm_mod_rotate rms={rms}")
+
+
+def test_head_norm(ns2lib):
+    g = gen(51)
+    L, T, Dm = 77, 9, 1536
+    X = torch.randn(L + T, 3 * Dm, generator=g)
+    w = torch.randn(96, generator=g)
+    cs, sin_off = O.rope2d_table(7, 11)
+    Xd = X.to(dev)
+    ns2lib.head_norm(Xd, w.to(dev), L, 16, 96, 3 * Dm, colOff=Dm, cs=cs.to(dev), sinOff=sin_off)
+    ns2lib.head_norm(Xd, w.to(dev), T, 16, 96, 3 * Dm, colOff=Dm, rowOff=L)
+    torch.cuda.synchronize()
+    ref = X.double().clone()
+    O.head_norm_rope(ref, w.double(), L, 16, 96, 3 * Dm, colOff=Dm, cs=cs, sinOff=sin_off)
+    O.head_norm_rope(ref, w.double(), T, 16, 96, 3 * Dm, colOff=Dm, rowOff=L)
+    assert_close(Xd.cpu(), ref, TOL_F32, "head_norm")
+
+
+@pytest.mark.parametrize("act", ["silu", "gelu_tanh"])
+def test_glu(ns2lib, act):
+    g = gen(61)
+    rows, I = 123, 4096
+    x = torch.randn(rows, 2 * I, generator=g) * 2
+    y = torch.empty(rows, I, device=dev)
+    ns2lib.glu(x.to(dev), y, rows, I, act)
+    torch.cuda.synchronize()
+    ref = O.glu(x.double(), act)
+    assert_close(y.cpu(), ref, TOL_F32, f"glu {act}")
+    yr = torch.empty(rows, I, dtype=torch.int16, device=dev)
+    ns2lib.glu_rotate_f16(x.to(dev), yr, rows, I, act)
+    torch.cuda.synchronize()
+    assert_close(f16_as_float(yr.cpu()), O.rotate(ref), TOL_F16_OUT, f"glu_rotate {act}")
+
+
+def test_elementwise_accumulate_rowsum_rmsnorm(ns2lib):
+    g = gen(71)
+    a = torch.randn(9216, generator=g)
+    b = torch.randn(9216, generator=g)
+    ad, bd = a.to(dev), b.to(dev)
+    y = torch.empty_like(ad)
+    for op, ref in [("add", a + b), ("sub", a - b), ("silu", torch.nn.functional.silu(a)), ("copy", a)]:
+        ns2lib.elementwise(op, ad, bd, y, a.numel())
+        torch.cuda.synchronize()
+        assert_close(y.cpu(), ref, TOL_F32, f"elementwise {op}")
+    yd = a.to(dev)
+    ns2lib.accumulate(yd, bd, a.numel())
+    torch.cuda.synchronize()
+    assert_close(yd.cpu(), a + b, TOL_F32, "accumulate")
+    x = torch.randn(256, 1536, generator=g)
+    w = torch.rand(256, generator=g) + 0.5
+    out = torch.empty(1, 1536, device=dev)
+    ns2lib.row_sum(x.to(dev), w.to(dev), out, 256, 1536, 1 / w.sum().item())
+    torch.cuda.synchronize()
+    assert_close(out.cpu(), O.row_sum(x.double(), w.double(), 1 / w.sum().item()), TOL_F32, "row_sum")
+    nw = torch.randn(1536, generator=g) * 0.02
+    out = torch.empty(256, 1536, device=dev)
+    ns2lib.rmsnorm(x.to(dev), nw.to(dev), out, 256, 1536)
+    torch.cuda.synchronize()
+    assert_close(out.cpu(), O.rms_norm(x.double(), nw.double()), TOL_F32, "rmsnorm")
+
+
+def test_fill_and_errors(ns2lib):
+    import ns2
+
+    buf = torch.full((1000,), 7, dtype=torch.int32, device=dev)
+    ns2lib.call("ns2_fill_u32", buf.data_ptr(), 0, 1000)
+    torch.cuda.synchronize()
+    assert (buf.cpu() == 0).all()
+    with pytest.raises(ns2.NS2Error, match="multiple of 256"):
+        ns2lib.linear_i8(buf, 0, 100, buf, buf, buf, 4, 4, 100)
+    with pytest.raises(ns2.NS2Error, match="head dim"):
+        ns2lib.attention(buf, buf, buf, buf, Lq=4, Lk=4, H=1, D=80, ldq=80, ldk=80, ldv=80, ldo=80)
