@@ -109,7 +109,8 @@ int ns2_rotate_f16(const float* x, int ldx, uint16_t* y, int ldy, int rows, int 
 
 /* int8 ConvRot weights. a_fmt selects the activation operand:
  *   a_fmt = 0: A is fp32 [M, lda], NOT rotated; the call rotates it (ops.linear without xr).
- *   a_fmt = 1: A is fp16 [M, lda] already rotated (ops.linear with opts.xr).
+ *   a_fmt = 1: A is fp16 [M, lda] already rotated (the fused producers' output).
+ *   a_fmt = 2: A is fp32 [M, lda] already rotated (ops.linear with opts.xr = ops.rotate(x)).
  * Requires K % 256 == 0. */
 int ns2_linear_i8(const void* A, int a_fmt, int lda, const int8_t* W, const float* scale,
                   const float* bias, const float* add, float* C, int M, int N, int K, int ldc,

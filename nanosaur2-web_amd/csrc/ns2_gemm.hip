@@ -297,6 +297,20 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemmArgs p) {
   }
 }
 
+// fp32 [rows, lda] (already rotated) -> fp16 [rows, cols]
+__global__ __launch_bounds__(256) void cast_f16_kernel(const float* __restrict__ x, int ldx,
+                                                        uint16_t* __restrict__ y, int rows,
+                                                        int cols) {
+  const long long i = ((long long)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (i >= (long long)rows * cols) return;
+  const long long r = i / cols, c = i % cols;
+  const float4 v = *reinterpret_cast<const float4*>(x + r * ldx + c);
+  uint2 o;
+  o.x = pack_half2(v.x, v.y);
+  o.y = pack_half2(v.z, v.w);
+  *reinterpret_cast<uint2*>(y + i) = o;
+}
+
 constexpr int kGemvMaxM = 8;
 
 template <bool A_F32, bool W_BF16>
@@ -338,16 +352,24 @@ int ns2_linear_i8(const void* A, int a_fmt, int lda, const int8_t* W, const floa
   NS2_READY();
   if (M == 0) return NS2_OK;
   GemmArgs p{A, W, scale, bias, add, C, gate, cOff, gOff, lda, ldc, M, N, K, alpha, act, resid};
-  NS2_REQUIRE(a_fmt == 0 || a_fmt == 1, "ns2_linear_i8: a_fmt must be 0 (fp32) or 1 (rotated fp16)");
+  NS2_REQUIRE(a_fmt >= 0 && a_fmt <= 2,
+              "ns2_linear_i8: a_fmt must be 0 (fp32), 1 (rotated fp16) or 2 (rotated fp32)");
   NS2_REQUIRE(scale != nullptr, "ns2_linear_i8: null scale");
   NS2_REQUIRE(K % 256 == 0, "ns2_linear_i8: K=%d must be a multiple of 256 (ConvRot groups)", K);
-  if (a_fmt == 0) {
-    // ops.linear without xr: rotate into library scratch first (app/gpu/ops.js:54)
-    NS2_REQUIRE(A && lda >= K && lda % 4 == 0, "ns2_linear_i8: bad fp32 A / lda=%d", lda);
+  if (a_fmt != 1) {
+    // fp32 input: rotate (ops.linear without xr, app/gpu/ops.js:54) or just cast a
+    // pre-rotated xr, into library scratch
+    NS2_REQUIRE(A && lda >= K && lda % 4 == 0 && aligned16(A), "ns2_linear_i8: bad fp32 A / lda=%d", lda);
     uint16_t* xr = static_cast<uint16_t*>(ns2::workspace(0, (size_t)M * K * sizeof(uint16_t)));
     if (!xr) return ns2::set_error(NS2_ERR_OOM, "ns2_linear_i8: workspace allocation failed");
-    int rc = ns2_rotate_f16(static_cast<const float*>(A), lda, xr, K, M, K);
-    if (rc) return rc;
+    if (a_fmt == 0) {
+      int rc = ns2_rotate_f16(static_cast<const float*>(A), lda, xr, K, M, K);
+      if (rc) return rc;
+    } else {
+      const long long quads = (long long)M * K / 4;
+      cast_f16_kernel<<<(unsigned)((quads + 255) / 256), 256, 0, ns2::stream()>>>(static_cast<const float*>(A), lda, xr, M, K);
+      NS2_LAUNCHED("cast_f16");
+    }
     p.A = xr;
     p.lda = K;
   }

@@ -1,0 +1,301 @@
+// Nanosaur2 DiT (1536 wide, 18 blocks, 16 heads of 96) on the ns2 ops: one pass from a
+// latent [64, h, w] to the x0 prediction, with the composition of the reference's
+// Nanosaur2DiT (app/models/nanosaur2.js:38-258; tools/reference.py:248-329):
+//   text:   y_embedder (+RMSNorm) -> 2 text-refine blocks conditioned on the timestep;
+//           prompt weights pool the refined text and become log-biases on the text keys
+//   blocks: adaLN-single modulation (shared projection + per-block offset), QK-norm, 2-D RoPE,
+//           joint image+text attention on even blocks (kv_y), image-only on odd blocks,
+//           SwiGLU MLP, gated residuals; blocks 2..15 form the SPRINT residual path.
+//
+// fused (default): normMod and GLU write the rotated fp16 operand of the next int8 linear,
+// and the per-head norms and RoPE run inside the attention call. fused = false issues the
+// reference's op sequence (separate headNorm / rotate / glu ops) on the same kernels' API.
+
+import * as ops from "./ops.js";
+import { rope2dTable } from "./common.js";
+
+const D = 1536;
+const HEADS = 16;
+const HD = D / HEADS;
+const BLOCKS = 18;
+const SPRINT_F = 2;
+const SPRINT_H = 2;
+const CH = 64;
+
+// Sinusoidal embedding of sigma * 1000, cos half then sin half, 256 dims, computed in fp32
+// steps (app/models/nanosaur2.js:24-36; tools/reference.py:213-217).
+export function timestepEmbedding(sigma) {
+  const dim = 256;
+  const half = dim / 2;
+  const t = Math.fround(sigma * 1000);
+  const out = new Float32Array(dim);
+  for (let i = 0; i < half; i++) {
+    const f = Math.fround(Math.exp(Math.fround((-Math.log(10000) * i) / half)));
+    const a = Math.fround(t * f);
+    out[i] = Math.cos(a);
+    out[half + i] = Math.sin(a);
+  }
+  return out;
+}
+
+export class Nanosaur2DiT {
+  // st: { linear(gpu, base), vector(gpu, name), has(name) } (weights.js SafeTensors)
+  static async load(gpu, st, onProgress, { fused = true } = {}) {
+    const m = new Nanosaur2DiT(gpu, fused);
+    const lin = (n) => st.linear(gpu, n);
+    const vec = (n) => st.vector(gpu, n);
+    m.sEmbed = await lin("s_embedder.proj.");
+    m.t1 = await lin("t_embedder.mlp.0.");
+    m.t2 = await lin("t_embedder.mlp.2.");
+    m.yEmbed = await lin("y_embedder.proj.");
+    m.yNorm = await vec("y_embedder.norm.weight");
+    m.yPool = await lin("y_pool_proj.");
+    m.sharedAda = await lin("shared_encoder_adaLN.0.");
+    m.sprintOut = await lin("sprint_out_proj.");
+    m.text = [];
+    for (let i = 0; st.has(`text_refine_blocks.${i}.norm1.weight`); i++) {
+      const p = `text_refine_blocks.${i}.`;
+      m.text.push({
+        ada: await lin(p + "adaLN_modulation.0."), n1: await vec(p + "norm1.weight"), n2: await vec(p + "norm2.weight"),
+        qkv: await lin(p + "attn.qkv."), qn: await vec(p + "attn.q_norm.weight"), kn: await vec(p + "attn.k_norm.weight"),
+        proj: await lin(p + "attn.proj."), w12: await lin(p + "mlp.w12."), w3: await lin(p + "mlp.w3."),
+      });
+    }
+    m.blocks = [];
+    for (let i = 0; i < BLOCKS; i++) {
+      const p = `blocks.${i}.`;
+      m.blocks.push({
+        offset: await vec(`encoder_adaLN_offsets.${i}`), n1: await vec(p + "norm1.weight"), n2: await vec(p + "norm2.weight"),
+        qkv: await lin(p + "attn.qkv_x."), kvY: st.has(p + "attn.kv_y.weight") ? await lin(p + "attn.kv_y.") : null,
+        qn: await vec(p + "attn.q_norm.weight"), kn: await vec(p + "attn.k_norm.weight"),
+        proj: await lin(p + "attn.proj."), w12: await lin(p + "mlp.w12."), w3: await lin(p + "mlp.w3."),
+      });
+      if (onProgress) onProgress((i + 1) / BLOCKS);
+    }
+    m.finalAda = await lin("final_layer.adaLN_modulation.");
+    m.finalLinear = await lin("final_layer.linear.");
+    return m;
+  }
+
+  constructor(gpu, fused = true) {
+    this.gpu = gpu;
+    this.fused = fused;
+  }
+
+  // Release every persistent weight buffer.
+  unload() {
+    const seen = new Set();
+    const walk = (o) => {
+      if (!o || typeof o !== "object" || seen.has(o)) return;
+      seen.add(o);
+      if (typeof o.destroy === "function" && o.ptr !== undefined) { o.destroy(); return; }
+      for (const k of Object.keys(o)) if (k !== "gpu") walk(o[k]);
+    };
+    walk(this);
+  }
+
+  // ------------------------------------------------------------------ text
+
+  // hidden: Float32Array [L, 640]; weights: per-token prompt weights. Tokens with weight <= 0
+  // are masked in the reference (no key, zeroed text row, no pooling contribution), so they
+  // are dropped; they still count in the pooling denominator (app/models/nanosaur2.js:94-118).
+  prepareText(hidden, weights) {
+    const gpu = this.gpu;
+    const keep = [];
+    weights.forEach((w, i) => { if (w > 0) keep.push(i); });
+    const L = keep.length;
+    const denom = Math.max(1, weights.reduce((a, b) => a + b, 0));
+    if (!L) return { L: 0, release() {} };
+    const ctx = new Float32Array(L * 640);
+    keep.forEach((src, i) => ctx.set(hidden.subarray(src * 640, (src + 1) * 640), i * 640));
+    const x = gpu.fromArray(ctx, [L, 640]);
+    const h = ops.linear(gpu, x, this.yEmbed, { name: "dit.y_embed" });
+    x.release();
+    const y = ops.rmsnorm(gpu, h, this.yNorm, D);
+    h.release();
+    const w = keep.map((i) => weights[i]);
+    const pool = gpu.fromArray(new Float32Array(w), [L]);
+    const bias = w.some((v) => v !== 1)
+      ? gpu.fromArray(new Float32Array(w.map((v) => Math.log(Math.max(v, 1e-4)))), [L]) : null;
+    return {
+      L, y, pool, poolScale: 1 / denom, bias,
+      release() { y.release(); pool.release(); if (bias) bias.release(); },
+    };
+  }
+
+  // Attention over a packed qkv [Lk, 3D] buffer; fused: per-head norms (and RoPE on the
+  // first ropeRows rows) inside the attention call, else the reference's headNorm ops.
+  attend(qkv, L, Lk, b, { cs = null, textRows = 0, bias = null } = {}) {
+    const gpu = this.gpu;
+    const common = { q: qkv, k: qkv, v: qkv, Lq: L, Lk, H: HEADS, D: HD, ldq: 3 * D, ldk: 3 * D, ldv: 3 * D,
+      qOff: 0, kOff: D, vOff: 2 * D, bias, biasStart: L };
+    if (this.fused) return ops.attention(gpu, { ...common, qNorm: b.qn, kNorm: b.kn, cs, ropeRows: L });
+    ops.headNorm(gpu, qkv, b.qn, { L, H: HEADS, D: HD, ld: 3 * D, colOff: 0, cs });
+    ops.headNorm(gpu, qkv, b.kn, { L, H: HEADS, D: HD, ld: 3 * D, colOff: D, cs });
+    if (textRows) ops.headNorm(gpu, qkv, b.kn, { L: textRows, H: HEADS, D: HD, ld: 3 * D, colOff: D, rowOff: L });
+    return ops.attention(gpu, common);
+  }
+
+  // x += gate_mlp * w3(silu(x1) * x2), [x1 x2] = w12(modulate(norm2(x))) (app/models/nanosaur2.js:142-152)
+  mlp(x, b, mod) {
+    const gpu = this.gpu;
+    if (this.fused) {
+      const nr = ops.normModRotated(gpu, x, mod, 3 * D, 4 * D, D, b.n2);
+      const h = ops.linear(gpu, null, b.w12, { xr: nr, name: "dit.mlp.w12" });
+      nr.release();
+      const gr = ops.gluRotated(gpu, h, "silu");
+      h.release();
+      ops.linear(gpu, null, b.w3, { xr: gr, out: x, resid: true, gate: mod, gOff: 5 * D, name: "dit.mlp.w3" });
+      gr.release();
+      return;
+    }
+    const n = ops.normMod(gpu, x, mod, 3 * D, 4 * D, D, b.n2);
+    const h = ops.linear(gpu, n, b.w12, { name: "dit.mlp.w12" });
+    n.release();
+    const g = ops.glu(gpu, h, "silu");
+    h.release();
+    ops.linear(gpu, g, b.w3, { out: x, resid: true, gate: mod, gOff: 5 * D, name: "dit.mlp.w3" });
+    g.release();
+  }
+
+  // qkv projection of modulate(norm1(x)) into rows [0, L) of qkv
+  qkvProj(x, mod, b, qkv, name) {
+    const gpu = this.gpu;
+    if (this.fused) {
+      const nr = ops.normModRotated(gpu, x, mod, 0, D, D, b.n1);
+      ops.linear(gpu, null, b.qkv, { xr: nr, out: qkv, name });
+      nr.release();
+      return;
+    }
+    const n = ops.normMod(gpu, x, mod, 0, D, D, b.n1);
+    ops.linear(gpu, n, b.qkv, { out: qkv, name });
+    n.release();
+  }
+
+  // Text refine blocks for one timestep: Tensor [L, D] (app/models/nanosaur2.js:120-140)
+  refineText(text, tc) {
+    const gpu = this.gpu;
+    const L = text.L;
+    const txt = ops.elementwise(gpu, "copy", text.y);
+    for (const b of this.text) {
+      const mod = ops.linear(gpu, tc, b.ada, { name: "dit.text.ada" });
+      const qkv = gpu.empty([L, 3 * D]);
+      this.qkvProj(txt, mod, b, qkv, "dit.text.qkv");
+      const a = this.attend(qkv, L, L, b);
+      qkv.release();
+      ops.linear(gpu, a, b.proj, { out: txt, resid: true, gate: mod, gOff: 2 * D, name: "dit.text.proj" });
+      a.release();
+      this.mlp(txt, b, mod);
+      mod.release();
+    }
+    return txt;
+  }
+
+  // ------------------------------------------------------------------ conditioning
+
+  // Everything that depends on sigma and the prompt but not on the latent
+  // (app/models/nanosaur2.js:154-184).
+  condition(text, sigma) {
+    const gpu = this.gpu;
+    const temb = gpu.fromArray(timestepEmbedding(sigma), [1, 256]);
+    const h = ops.linear(gpu, temb, this.t1, { act: "silu", name: "dit.t_embed" });
+    temb.release();
+    const t = ops.linear(gpu, h, this.t2, { name: "dit.t_embed" });
+    h.release();
+    const tc = ops.elementwise(gpu, "silu", t);
+    let txt = null;
+    let txtR = null;
+    if (text.L) {
+      txt = this.refineText(text, tc);
+      // the int8 kv_y projections take rotated inputs: rotate the text once for all blocks
+      if (this.blocks.some((b) => b.kvY && ops.needsRotation(b.kvY))) {
+        txtR = this.fused ? ops.rotateHalf(gpu, txt) : ops.rotate(gpu, txt);
+      }
+      const pooled = ops.rowSum(gpu, txt, text.pool, text.poolScale);
+      ops.linear(gpu, pooled, this.yPool, { out: t, resid: true, name: "dit.y_pool" });
+      pooled.release();
+    }
+    tc.release();
+    const cond = ops.elementwise(gpu, "silu", t);
+    t.release();
+    const mod = ops.linear(gpu, cond, this.sharedAda, { name: "dit.shared_ada" });
+    const final = ops.linear(gpu, cond, this.finalAda, { name: "dit.final_ada" });
+    cond.release();
+    return {
+      txt, txtR, mod, final,
+      release() { if (txt) txt.release(); if (txtR) txtR.release(); mod.release(); final.release(); },
+    };
+  }
+
+  // ------------------------------------------------------------------ forward
+
+  // One DiT block in place on x [L, D] (app/models/nanosaur2.js:186-214).
+  block(i, x, L, text, c, cs) {
+    const gpu = this.gpu;
+    const b = this.blocks[i];
+    const mod = ops.elementwise(gpu, "add", c.mod, b.offset); // [1, 6D]
+    const cross = !!(b.kvY && text.L);
+    // rows [0, L): image q|k|v; rows [L, L + text): text k|v (q columns unused)
+    const Lk = L + (cross ? text.L : 0);
+    const qkv = gpu.empty([Lk, 3 * D]);
+    this.qkvProj(x, mod, b, qkv, "dit.qkv");
+    if (cross) {
+      ops.linear(gpu, c.txt, b.kvY, { xr: c.txtR, out: qkv, ldc: 3 * D, cOff: L * 3 * D + D, name: "dit.kv_y" });
+    }
+    const a = this.attend(qkv, L, Lk, b, { cs, textRows: cross ? text.L : 0, bias: cross ? text.bias : null });
+    qkv.release();
+    ops.linear(gpu, a, b.proj, { out: x, resid: true, gate: mod, gOff: 2 * D, name: "dit.proj" });
+    a.release();
+    this.mlp(x, b, mod);
+    mod.release();
+  }
+
+  // Device-resident pass: tokens [L, 64] (Tensor) -> out [L, 64] (Tensor, caller releases).
+  async forwardTokens(tokens, h, w, text, sigma, { pathDrop = false, onBlock } = {}) {
+    const gpu = this.gpu;
+    const L = h * w;
+    const x = ops.linear(gpu, tokens, this.sEmbed, { name: "dit.s_embed" });
+    const cs = rope2dTable(gpu, h, w, HD);
+    const c = this.condition(text, sigma);
+    const total = pathDrop ? SPRINT_F + SPRINT_H : BLOCKS;
+    let done = 0;
+    const run = async (i, s) => {
+      this.block(i, s, L, text, c, cs);
+      if (onBlock) await onBlock(++done / total);
+    };
+    for (let i = 0; i < SPRINT_F; i++) await run(i, x);
+    if (!pathDrop) {
+      const g = ops.elementwise(gpu, "copy", x);
+      for (let i = SPRINT_F; i < BLOCKS - SPRINT_H; i++) await run(i, g);
+      const d = ops.elementwise(gpu, "sub", g, x);
+      g.release();
+      ops.linear(gpu, d, this.sprintOut, { out: x, resid: true, name: "dit.sprint_out" });
+      d.release();
+    }
+    for (let i = BLOCKS - SPRINT_H; i < BLOCKS; i++) await run(i, x);
+    cs.release();
+    const n = ops.normMod(gpu, x, c.final, 0, D, D);
+    x.release();
+    c.release();
+    const out = ops.linear(gpu, n, this.finalLinear, { name: "dit.final" });
+    n.release();
+    return out;
+  }
+
+  // latent: Float32Array [64, h, w]; text: prepareText(...). Returns x0 [64, h, w]
+  // (app/models/nanosaur2.js:216-258).
+  async forward(latent, h, w, text, sigma, opts = {}) {
+    const gpu = this.gpu;
+    const L = h * w;
+    const tokens = new Float32Array(L * CH);
+    for (let ch = 0; ch < CH; ch++) for (let l = 0; l < L; l++) tokens[l * CH + ch] = latent[ch * L + l];
+    const xin = gpu.fromArray(tokens, [L, CH]);
+    const out = await this.forwardTokens(xin, h, w, text, sigma, opts);
+    xin.release();
+    const o = await gpu.read(out);
+    out.release();
+    const x0 = new Float32Array(CH * L);
+    for (let l = 0; l < L; l++) for (let ch = 0; ch < CH; ch++) x0[ch * L + l] = o[l * CH + ch];
+    return x0;
+  }
+}

@@ -1,0 +1,165 @@
+// Tensor ops with the call surface of the reference's app/gpu/ops.js, launched as HIP kernels
+// through the ns2 addon. Activations are fp32 Tensors (row-major); offsets and strides are in
+// elements. Three fused producers are added for the int8 layers: normModRotated,
+// gluRotated and rotateHalf write the rotated fp16 operand that linear() takes as opts.xr,
+// so the separate rotation pass of the reference never runs on the DiT path.
+
+import { addr } from "./device.js";
+import { native, ACT, EW } from "./native.js";
+
+const opt = (v, d) => (v === undefined || v === null ? d : v);
+
+// int8 weights are ConvRot-quantized: they take Hadamard-rotated inputs (app/gpu/ops.js:34-35)
+export const needsRotation = (W) => W.kind === "i8";
+
+// ConvRot input rotation, fp32 -> fp32 (app/gpu/ops.js:37-44).
+export function rotate(gpu, x) {
+  const y = gpu.empty(x.shape);
+  const groups = x.size / 256;
+  gpu.run("hadamard", 0, () => native.hadamard256(addr(x), addr(y), groups));
+  return y;
+}
+
+// Rotation written as the fp16 GEMM operand ([rows, cols], cols % 256 == 0).
+export function rotateHalf(gpu, x, cols = x.shape[x.shape.length - 1]) {
+  const rows = x.size / cols;
+  const y = gpu.empty([rows, cols], "f16");
+  gpu.run("rotate_f16", 0, () => native.rotateF16(addr(x), cols, addr(y), cols, rows, cols));
+  return y;
+}
+
+// y = x @ W^T (+ bias) (act) (app/gpu/ops.js:46-66). opts: out, resid, gate, gOff, ldc, cOff,
+// bias, act, xr (pre-rotated input of an int8 weight: fp32 from rotate() or fp16 from a fused
+// producer), name. x may be null when xr is given.
+export function linear(gpu, x, W, opts = {}) {
+  const src = opts.xr || x;
+  const M = src.size / W.K;
+  if (W.lora && W.lora.length) throw new Error(`${W.name}: LoRA side paths are not part of this build`);
+  const out = opts.out || gpu.empty([M, W.N]);
+  const ldc = opt(opts.ldc, W.N);
+  const cOff = opt(opts.cOff, 0);
+  const gOff = opt(opts.gOff, 0);
+  const bias = opts.bias || W.bias || null;
+  const act = ACT[opts.act || "none"];
+  if (act === undefined) throw new Error(`linear: unknown activation ${opts.act}`);
+  const resid = opts.resid ? 1 : 0;
+  const flops = 2 * M * W.N * W.K;
+  if (W.kind === "i8") {
+    const aFmt = opts.xr ? (opts.xr.dtype === "f16" ? 1 : 2) : 0;
+    gpu.run(opts.name || "gemm.i8", flops, () =>
+      native.linearI8(addr(src), aFmt, W.K, addr(W.buf), addr(W.scale), addr(bias), null, addr(out),
+        M, W.N, W.K, ldc, cOff, 1, act, resid, addr(opts.gate), gOff));
+  } else if (W.kind === "bf16") {
+    gpu.run(opts.name || "gemm.bf16", flops, () =>
+      native.linearBf16(addr(x), W.K, addr(W.buf), addr(bias), null, addr(out), M, W.N, W.K, ldc, cOff,
+        1, act, resid, addr(opts.gate), gOff));
+  } else {
+    throw new Error(`linear: weight kind ${W.kind} is not part of this build`);
+  }
+  return out;
+}
+
+export function zero(gpu, t) {
+  const words = t.dtype === "f16" ? Math.ceil(t.size / 2) : t.size;
+  gpu.run("zero", 0, () => native.fill(addr(t), 0, words));
+}
+
+export function rmsnorm(gpu, x, weight, cols, eps = 1e-6, out) {
+  const rows = x.size / cols;
+  const y = out || gpu.empty(x.shape);
+  gpu.run("rmsnorm", 0, () => native.rmsnorm(addr(x), addr(weight), addr(y), rows, cols, eps));
+  return y;
+}
+
+// norm(x) * (1 + mod[scaleOff..]) + mod[shiftOff..]; RMSNorm*weight, or LayerNorm without
+// affine when weight is null (app/gpu/ops.js:119-129).
+export function normMod(gpu, x, mod, shiftOff, scaleOff, cols, weight = null, eps = 1e-6) {
+  const rows = x.size / cols;
+  const y = gpu.empty(x.shape);
+  gpu.run(weight ? "rmsnorm_mod" : "layernorm_mod", 0, () =>
+    native.normMod(addr(x), addr(mod), shiftOff, scaleOff, rows, cols, addr(weight), eps, addr(y)));
+  return y;
+}
+
+// normMod followed by the ConvRot rotation, as the fp16 operand of an int8 linear.
+export function normModRotated(gpu, x, mod, shiftOff, scaleOff, cols, weight = null, eps = 1e-6) {
+  const rows = x.size / cols;
+  const y = gpu.empty([rows, cols], "f16");
+  gpu.run(weight ? "rmsnorm_mod_rot" : "layernorm_mod_rot", 0, () =>
+    native.normModRotateF16(addr(x), addr(mod), shiftOff, scaleOff, rows, cols, addr(weight), eps, addr(y)));
+  return y;
+}
+
+// In-place per-head RMSNorm (+ RoPE with a table from common.js) on L rows x H heads of D
+// values at X[(rowOff + l) * ld + colOff + h * D] (app/gpu/ops.js:131-138).
+export function headNorm(gpu, X, weight, { L, H, D, ld, colOff = 0, rowOff = 0, cs = null, eps = 1e-6 }) {
+  gpu.run(cs ? "head_norm_rope" : "head_norm", 0, () =>
+    native.headNorm(addr(X), addr(weight), L, H, D, ld, colOff, rowOff, cs ? addr(cs) : null, cs ? cs.sinOff : 0, eps));
+}
+
+// [rows, 2I] -> [rows, I]: act(first half) * second half (app/gpu/ops.js:140-148)
+export function glu(gpu, x, act) {
+  const I = x.shape[1] / 2;
+  const y = gpu.empty([x.shape[0], I]);
+  gpu.run("glu." + act, 0, () => native.glu(addr(x), addr(y), x.shape[0], I, ACT[act]));
+  return y;
+}
+
+// glu followed by the ConvRot rotation, as the fp16 operand of an int8 linear.
+export function gluRotated(gpu, x, act) {
+  const I = x.shape[1] / 2;
+  const y = gpu.empty([x.shape[0], I], "f16");
+  gpu.run("glu_rot." + act, 0, () => native.gluRotateF16(addr(x), addr(y), x.shape[0], I, ACT[act]));
+  return y;
+}
+
+// [1, N] = scale * sum_r w[r] * x[r] (app/gpu/ops.js:150-156)
+export function rowSum(gpu, x, w, scale = 1) {
+  const [rows, N] = x.shape;
+  const y = gpu.empty([1, N]);
+  gpu.run("rowsum", 0, () => native.rowSum(addr(x), addr(w), addr(y), rows, N, scale));
+  return y;
+}
+
+export function elementwise(gpu, op, a, b, out) {
+  const y = out || gpu.empty(a.shape);
+  if (EW[op] === undefined) throw new Error(`elementwise: unknown op ${op}`);
+  gpu.run("elementwise." + op, 0, () => native.elementwise(EW[op], addr(a), b ? addr(b) : null, addr(y), y.size));
+  return y;
+}
+
+// y += a (in place) (app/gpu/ops.js:187-192)
+export function accumulate(gpu, y, a) {
+  gpu.run("accumulate", 0, () => native.accumulate(addr(y), addr(a), y.size));
+}
+
+// Multi-head attention (app/gpu/ops.js:194-209), fused kernel only.
+//  q: [Lq, ldq] with head h at column qOff + h*D; k, v: [Lk, ldk]/[Lk, ldv]. Output [Lq, H*D].
+//  bias: optional Tensor of additive score biases for keys biasStart...
+// Fused prologue options of this build: qNorm/kNorm (per-head RMSNorm weights, the DiT's
+// headNorm), cs (RoPE table with .sinOff) applied to q/k rows < ropeRows, eps.
+export function attention(gpu, { q, k, v, Lq, Lk, H, D, ldq, ldk, ldv, qOff = 0, kOff = 0, vOff = 0, group = 1,
+  causal = false, bias = null, biasStart = 0, out, qNorm = null, kNorm = null, cs = null, ropeRows = 0, eps = 1e-6 }) {
+  if (causal || group !== 1) {
+    throw new Error("attention: causal / grouped-query attention (the reference's unfused text-encoder path) is not part of this build");
+  }
+  if (D % 32 || D > 128) throw new Error(`flash attention: unsupported head dim ${D}`);
+  const o = out || gpu.empty([Lq, H * D]);
+  gpu.run("attn.flash", 4 * Lq * Lk * D * H, () =>
+    native.attention(addr(q), addr(k), addr(v), addr(o), 1, Lq, Lk, H, D, ldq, ldk, ldv, H * D, qOff, kOff, vOff, 0,
+      0, 0, 0, 0, 1 / Math.sqrt(D), addr(bias), biasStart, 0, addr(qNorm), addr(kNorm), eps,
+      cs ? addr(cs) : null, cs ? cs.sinOff : 0, cs ? ropeRows : 0));
+  return o;
+}
+
+export function conv3x3() {
+  throw new Error("conv3x3 (VAE decoder) is not part of this build");
+}
+
+export function conv3x3Into() {
+  throw new Error("conv3x3 (VAE decoder) is not part of this build");
+}
+
+export function groupNorm() {
+  throw new Error("groupNorm (VAE decoder) is not part of this build");
+}

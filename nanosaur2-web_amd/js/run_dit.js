@@ -1,0 +1,149 @@
+// Command-line driver for one Nanosaur2 DiT pass on the MI355X through the Node host.
+//
+//   node run_dit.js (--weights FILE.safetensors | --synthetic SEED)
+//                   (--inputs DIR | --shape H,W,T[,SEED])
+//                   [--out FILE.f32] [--reference-ops] [--path-drop]
+//                   [--warmup N] [--reps N] [--profile]
+//
+// --inputs DIR holds inputs.json {h, w, sigma, T} and latent.f32 [64*h*w], context.f32
+// [T*640], weights.f32 [T]. --out writes the x0 prediction [64, h, w] as raw fp32.
+// With --reps, the pass is timed with the latent resident in device memory (stream events
+// and wall clock), and once more host-to-host (upload, pass, readback); one JSON line with
+// the timings (and the per-op profile with --profile) is printed.
+
+import fs from "fs";
+import path from "path";
+import { GPU } from "./device.js";
+import { native } from "./native.js";
+import { Nanosaur2DiT } from "./nanosaur2.js";
+import { SafeTensors } from "./weights.js";
+import { SyntheticWeights } from "./synthetic.js";
+
+function parseArgs(argv) {
+  const a = { warmup: 0, reps: 0 };
+  for (let i = 0; i < argv.length; i++) {
+    const k = argv[i];
+    const next = () => argv[++i];
+    if (k === "--weights") a.weights = next();
+    else if (k === "--synthetic") a.synthetic = Number(next());
+    else if (k === "--inputs") a.inputs = next();
+    else if (k === "--shape") a.shape = next().split(",").map(Number);
+    else if (k === "--out") a.out = next();
+    else if (k === "--reference-ops") a.referenceOps = true;
+    else if (k === "--path-drop") a.pathDrop = true;
+    else if (k === "--warmup") a.warmup = Number(next());
+    else if (k === "--reps") a.reps = Number(next());
+    else if (k === "--profile") a.profile = true;
+    else throw new Error(`unknown argument ${k}`);
+  }
+  return a;
+}
+
+function readF32(file) {
+  const b = fs.readFileSync(file);
+  return new Float32Array(b.buffer.slice(b.byteOffset, b.byteOffset + b.byteLength));
+}
+
+// Seeded inputs of the benchmark shape (values only matter for timing).
+function syntheticInputs([h, w, T, seed = 1]) {
+  let s = (seed * 2654435761) >>> 0 || 1;
+  const u = () => {
+    s ^= s << 13; s >>>= 0; s ^= s >>> 17; s ^= s << 5; s >>>= 0;
+    return s / 4294967296;
+  };
+  const gauss = (n) => {
+    const o = new Float32Array(n);
+    for (let i = 0; i < n; i++) o[i] = Math.sqrt(-2 * Math.log(u() + 1e-12)) * Math.cos(2 * Math.PI * u());
+    return o;
+  };
+  const weights = new Float32Array(T);
+  for (let i = 0; i < T; i++) weights[i] = 0.5 + u();
+  return { h, w, T, sigma: u(), latent: gauss(64 * h * w), context: gauss(T * 640), weights };
+}
+
+function loadInputs(dir) {
+  const meta = JSON.parse(fs.readFileSync(path.join(dir, "inputs.json"), "utf8"));
+  return {
+    h: meta.h, w: meta.w, T: meta.T, sigma: meta.sigma,
+    latent: readF32(path.join(dir, "latent.f32")),
+    context: readF32(path.join(dir, "context.f32")),
+    weights: readF32(path.join(dir, "weights.f32")),
+  };
+}
+
+const median = (xs) => {
+  const s = [...xs].sort((p, q) => p - q);
+  return s.length ? s[Math.floor(s.length / 2)] : null;
+};
+
+async function main() {
+  const a = parseArgs(process.argv.slice(2));
+  const t0 = Date.now();
+  const gpu = await GPU.create({ profile: !!a.profile });
+  const st = a.weights ? await SafeTensors.open(a.weights) : new SyntheticWeights(a.synthetic || 3);
+  const dit = await Nanosaur2DiT.load(gpu, st, null, { fused: !a.referenceOps });
+  if (st.close) st.close();
+  const inp = a.inputs ? loadInputs(a.inputs) : syntheticInputs(a.shape || [76, 52, 256]);
+  const { h, w, sigma } = inp;
+  const text = dit.prepareText(inp.context, Array.from(inp.weights));
+  const loadMs = Date.now() - t0;
+  const report = { h, w, T: inp.T, tokens: h * w, fused: !a.referenceOps, pathDrop: !!a.pathDrop, load_ms: loadMs, device: gpu.info };
+
+  if (a.out) {
+    const x0 = await dit.forward(inp.latent, h, w, text, sigma, { pathDrop: !!a.pathDrop });
+    fs.writeFileSync(a.out, Buffer.from(x0.buffer));
+    report.out = a.out;
+  }
+
+  if (a.reps > 0) {
+    // device-resident latent tokens [L, 64]
+    const L = h * w;
+    const tok = new Float32Array(L * 64);
+    for (let ch = 0; ch < 64; ch++) for (let l = 0; l < L; l++) tok[l * 64 + ch] = inp.latent[ch * L + l];
+    const tokens = gpu.fromArray(tok, [L, 64]);
+    const pass = async () => (await dit.forwardTokens(tokens, h, w, text, sigma, { pathDrop: !!a.pathDrop })).release();
+    for (let i = 0; i < a.warmup; i++) await pass();
+    await gpu.sync();
+    if (gpu.profiler) gpu.profiler.reset();
+    const evA = native.eventCreate();
+    const evB = native.eventCreate();
+    const dev = [];
+    const wall = [];
+    for (let i = 0; i < a.reps; i++) {
+      const w0 = process.hrtime.bigint();
+      native.eventRecord(evA);
+      await pass();
+      native.eventRecord(evB);
+      await gpu.sync();
+      wall.push(Number(process.hrtime.bigint() - w0) / 1e6);
+      dev.push(native.eventElapsed(evA, evB));
+      process.stderr.write(`[run_dit] pass ${i + 1}/${a.reps}: ${dev[dev.length - 1].toFixed(3)} ms\n`);
+    }
+    const host = [];
+    for (let i = 0; i < Math.min(3, a.reps); i++) {
+      const w0 = process.hrtime.bigint();
+      await dit.forward(inp.latent, h, w, text, sigma, { pathDrop: !!a.pathDrop });
+      host.push(Number(process.hrtime.bigint() - w0) / 1e6);
+    }
+    tokens.release();
+    native.eventDestroy(evA);
+    native.eventDestroy(evB);
+    Object.assign(report, {
+      reps: a.reps, warmup: a.warmup, ms_device: dev, ms_wall: wall, ms_host_to_host: host,
+      ms_device_median: median(dev), ms_wall_median: median(wall), ms_host_to_host_median: median(host),
+    });
+    if (gpu.profiler) {
+      const rows = await gpu.profiler.report();
+      report.profile = rows.map((r) => ({ name: r.name, count: r.count / a.reps, ms: r.ms / a.reps, tflops: r.flops ? r.flops / (r.ms / 1e3) / 1e12 : null }));
+    }
+  }
+  report.pool_peak_bytes = gpu.pool.peak;
+  text.release();
+  dit.unload();
+  process.stdout.write(JSON.stringify(report) + "\n");
+}
+
+main().catch((e) => {
+  process.stderr.write(`[run_dit] error: ${e && e.stack ? e.stack : e}\n`);
+  process.exit(1);
+});

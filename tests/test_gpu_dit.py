@@ -1,0 +1,61 @@
+"""Full DiT pass through the Node host (run_dit.js -> N-API addon -> C ABI -> HIP) against the
+oracle's restatement of tools/reference.py DiT.forward, on seeded real-architecture weights
+(D=1536, 18 blocks, I=4096, int8 ConvRot block linears). Tolerance 1e-2 (max|d|/max|ref| and
+rel-L2) for the full 18-block pass.
+"""
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import dit_fixture as F
+from conftest import assert_close
+
+pytestmark = pytest.mark.gpu
+TOL_PASS = 1e-2
+
+
+@pytest.fixture(scope="module")
+def weights_file(tmp_path_factory):
+    d = tmp_path_factory.mktemp("dit")
+    tensors = F.make_weights(seed=3)
+    path = str(d / "dit_int8.safetensors")
+    F.save_weights(tensors, path)
+    print(f"[dit] wrote {os.path.getsize(path) / 2**20:.0f} MiB of seeded weights", flush=True)
+    return tensors, path, d
+
+
+def _run_case(weights_file, name, h, w, T, *, zero=(), path_drop=False, reference_ops=False, seed=7):
+    tensors, path, d = weights_file
+    inp = F.make_inputs(h, w, T, seed=seed, zero_weight_tokens=zero)
+    idir = str(d / f"in_{name}")
+    F.write_inputs(inp, idir)
+    out = str(d / f"x0_{name}.f32")
+    args = ["--weights", path, "--inputs", idir, "--out", out]
+    if path_drop:
+        args.append("--path-drop")
+    if reference_ops:
+        args.append("--reference-ops")
+    rep = F.run_node(args)
+    got = torch.from_numpy(np.fromfile(out, dtype=np.float32).reshape(64, h, w))
+    ref = F.oracle_forward(tensors, inp, path_drop=path_drop)
+    assert_close(got, ref, TOL_PASS, f"DiT pass {name} ({h}x{w}, T={T})")
+    return rep
+
+
+def test_dit_pass_fused(weights_file):
+    _run_case(weights_file, "fused", 6, 8, 16)
+
+
+def test_dit_pass_reference_op_sequence(weights_file):
+    """The reference's op sequence (separate headNorm / rotate / glu) on the same ops API."""
+    _run_case(weights_file, "refops", 6, 8, 16, reference_ops=True)
+
+
+def test_dit_pass_masked_token_and_path_drop(weights_file):
+    """A zero-weight prompt token (dropped by the host, masked by the reference) and the
+    path-drop pass that skips the SPRINT blocks."""
+    _run_case(weights_file, "masked", 5, 7, 12, zero=(3,), seed=11)
+    _run_case(weights_file, "pathdrop", 5, 7, 12, path_drop=True, seed=12)
