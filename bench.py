@@ -1,0 +1,295 @@
+#!/usr/bin/env python3
+"""Benchmark: ms per 832x1216 int8 DiT pass + joint-attention TFLOP/s on one MI355X.
+
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-dit]
+
+1. DiT pass (the metric): the Node host (nanosaur2-web_amd/js/run_dit.js) runs one full pass
+   of the 18-block Nanosaur2 DiT at 832x1216 (latent 76 rows x 52 cols = 3952 image tokens,
+   256 text tokens, batch 1) on seeded random-init weights of the real architecture (int8
+   ConvRot block linears, bf16 elsewhere). W untimed passes, then K timed passes with the
+   latent tokens resident in device memory, bracketed by stream events and a device sync.
+   `value` is the median device time per pass in ms.
+2. Joint attention at the production shape (3952 queries x 4208 keys, 16 heads x 96, batch 2,
+   2-D RoPE on image rows, log-weight bias on the text keys) through the C ABI (ctypes);
+   the library's kernel profiler times each launch of the flash kernel with stream events,
+   which gives the roofline entry (algorithmic 4*Lq*Lk*D*H*B flops per launch / mean launch
+   time, against the 2516.6 TFLOP/s dense fp16 MFMA peak).
+3. CPU baseline: the oracle (a PyTorch-CPU restatement of tools/reference.py) on a bounded
+   sample -- one joint block and one image-only block at the full 3952-token shape -- scaled
+   to 18 blocks, on this host's cores.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import subprocess
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "nanosaur2-web_amd")
+RUN_DIT = os.path.join(PKG, "js", "run_dit.js")
+METRIC = "ms per 832x1216 DiT pass (int8) + joint-attention TFLOP/s, 1 MI355X"
+PUBLISHED_PASS_MS = 1730.0   # README.md:86-88 of the reference (WebGPU, laptop GPU)
+FP16_PEAK_TFLOPS = 2516.6    # MI355X dense fp16 MFMA
+H_IMG, W_IMG, T_TXT, D, HEADS, HD, I_MLP, BLOCKS = 76, 52, 256, 1536, 16, 96, 4096, 18
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def pass_flops(L=H_IMG * W_IMG, T=T_TXT):
+    """Algorithmic FLOPs of one DiT pass: GEMMs 2MNK, attention 4*Lq*Lk*D*H
+    (app/gpu/ops.js:30, 207)."""
+    g = lambda M, N, K: 2 * M * N * K  # noqa: E731
+    blk = g(L, 3 * D, D) + g(L, D, D) + g(L, 2 * I_MLP, D) + g(L, D, I_MLP)
+    total = BLOCKS * blk
+    total += (BLOCKS // 2) * (g(T, 2 * D, D) + 4 * L * (L + T) * HD * HEADS)   # joint blocks
+    total += (BLOCKS // 2) * 4 * L * L * HD * HEADS                              # image-only blocks
+    txt = g(T, 3 * D, D) + g(T, D, D) + g(T, 2 * I_MLP, D) + g(T, D, I_MLP) + 4 * T * T * HD * HEADS + g(1, 6 * D, D)
+    total += 2 * txt
+    total += g(L, D, 64) + g(L, D, D) + g(L, 64, D)                              # s_embed, sprint, final
+    total += g(T, D, 640) + g(1, D, 256) + g(1, D, D) * 2 + g(1, 6 * D, D) + g(1, 2 * D, D)
+    return total
+
+
+def run_dit(steps, warmup):
+    cmd = ["node", RUN_DIT, "--synthetic", "3", "--shape", f"{H_IMG},{W_IMG},{T_TXT}",
+           "--warmup", str(warmup), "--reps", str(steps)]
+    log(" ".join(cmd))
+    p = subprocess.run(cmd, capture_output=True, text=True, timeout=900)
+    sys.stderr.write(p.stderr[-3000:])
+    if p.returncode != 0:
+        raise SystemExit(f"run_dit.js failed with {p.returncode}")
+    return json.loads(p.stdout.strip().splitlines()[-1])
+
+
+def run_dit_profile():
+    cmd = ["node", RUN_DIT, "--synthetic", "3", "--shape", f"{H_IMG},{W_IMG},{T_TXT}",
+           "--warmup", "1", "--reps", "2", "--profile"]
+    log(" ".join(cmd))
+    p = subprocess.run(cmd, capture_output=True, text=True, timeout=900)
+    if p.returncode != 0:
+        sys.stderr.write(p.stderr[-3000:])
+        raise SystemExit(f"run_dit.js --profile failed with {p.returncode}")
+    return json.loads(p.stdout.strip().splitlines()[-1]).get("profile", [])
+
+
+def bench_attention(reps, warmup):
+    """Joint attention at the production shape, batch 2 (cond + uncond)."""
+    import torch
+
+    sys.path.insert(0, PKG)
+    import ns2
+
+    lib = ns2.load(0, torch.cuda.current_stream().cuda_stream)
+    dev = "cuda"
+    L, B = H_IMG * W_IMG, 2
+    Lk = L + T_TXT
+    g = torch.Generator(device=dev).manual_seed(2)
+    q = torch.randn(B, L, D, device=dev, generator=g)
+    k = torch.randn(B, Lk, D, device=dev, generator=g)
+    v = torch.randn(B, Lk, D, device=dev, generator=g)
+    bias = torch.log(torch.rand(B, T_TXT, device=dev, generator=g) + 0.5)
+    o = torch.empty(B, L, D, device=dev)
+    cs = rope_table(H_IMG, W_IMG).to(dev)
+    sin_off = L * HD // 2
+
+    def call():
+        lib.attention(q, k, v, o, Lq=L, Lk=Lk, H=HEADS, D=HD, ldq=D, ldk=D, ldv=D, ldo=D, batch=B,
+                      qBatch=L * D, kBatch=Lk * D, vBatch=Lk * D, oBatch=L * D, key_bias=bias,
+                      biasStart=L, biasBatch=T_TXT, rope_cs=cs, sin_off=sin_off, rope_rows=L)
+
+    for _ in range(warmup):
+        call()
+    torch.cuda.synchronize()
+    lib.profile_reset()
+    lib.profile(True)
+    a, b = lib.event(), lib.event()
+    lib.record(a)
+    for _ in range(reps):
+        call()
+    lib.record(b)
+    torch.cuda.synchronize()
+    total_ms = lib.elapsed_ms(a, b) / reps
+    prof = lib.profile_report()
+    lib.profile(False)
+    flops = 4 * L * Lk * HD * HEADS * B
+    flash = prof.get("attn_flash", {"count": 0, "ms": 0})
+    pack = prof.get("attn_pack", {"count": 0, "ms": 0})
+    flash_ms = flash["ms"] / max(1, flash["count"])
+    pack_ms = pack["ms"] / max(1, pack["count"])
+    return {
+        "config": f"{L} queries x {Lk} keys ({L} image + {T_TXT} text), {HEADS} heads x {HD}, batch {B}, "
+                  "2-D RoPE on image rows, log-weight bias on text keys, fp32 in/out",
+        "gflop": flops / 1e9,
+        "ms": total_ms,
+        "tflops": flops / (total_ms / 1e3) / 1e12,
+        "flash_ms": flash_ms,
+        "flash_tflops": flops / (flash_ms / 1e3) / 1e12 if flash_ms else None,
+        "pack_ms": pack_ms,
+        "launches": flash["count"],
+        "flops_per_launch": flops,
+    }
+
+
+def rope_table(h, w):
+    """cos|sin table of the centred 2-D RoPE (app/models/common.js:28-43 layout)."""
+    import math
+
+    import torch
+
+    half = HD // 2
+    f = torch.tensor([float(torch.tensor(1.0 / math.pow(10000.0, float(torch.tensor(2.0 * i / half, dtype=torch.float32))),
+                                         dtype=torch.float32)) for i in range(half // 2)], dtype=torch.float64)
+    ys = torch.arange(h, dtype=torch.float64) - (h - 1) / 2
+    xs = torch.arange(w, dtype=torch.float64) - (w - 1) / 2
+    yy, xx = torch.meshgrid(ys, xs, indexing="ij")
+    ang = torch.cat([torch.outer(xx.flatten(), f), torch.outer(yy.flatten(), f)], dim=-1).float().double()
+    return torch.cat([ang.cos().reshape(-1), ang.sin().reshape(-1)]).float()
+
+
+def cpu_baseline():
+    """Oracle (PyTorch CPU, fp32) on one joint and one image-only block at full size."""
+    import torch
+
+    sys.path.insert(0, ROOT)
+    import oracle.nanosaur2_oracle as O
+
+    torch.manual_seed(0)
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    L, T = H_IMG * W_IMG, T_TXT
+    gen = torch.Generator().manual_seed(5)
+    t = {}
+
+    def i8(name, N, K):
+        t[name + ".weight"] = torch.randint(-127, 128, (N, K), generator=gen, dtype=torch.int32).to(torch.int8)
+        t[name + ".weight_scale"] = torch.rand(N, 1, generator=gen) * 9e-3 + 1e-3
+
+    def vec(name, n):
+        t[name] = (torch.randn(n, generator=gen) * 0.02).to(torch.bfloat16)
+
+    for i in (0, 1):
+        p = f"blocks.{i}."
+        vec(f"encoder_adaLN_offsets.{i}", 6 * D)
+        vec(p + "norm1.weight", D)
+        vec(p + "norm2.weight", D)
+        i8(p + "attn.qkv_x", 3 * D, D)
+        if i == 0:
+            i8(p + "attn.kv_y", 2 * D, D)
+        vec(p + "attn.q_norm.weight", HD)
+        vec(p + "attn.k_norm.weight", HD)
+        i8(p + "attn.proj", D, D)
+        i8(p + "mlp.w12", 2 * I_MLP, D)
+        i8(p + "mlp.w3", D, I_MLP)
+    W = O.TensorWeights(t)
+    dit = O.DiT(W)
+    x = torch.randn(L, D, generator=gen)
+    txt = torch.randn(T, D, generator=gen)
+    mod = torch.randn(1, 6 * D, generator=gen) * 0.02
+    tb = torch.log(torch.rand(T, generator=gen) + 0.5)
+    cos, sin = O.rope_2d(H_IMG, W_IMG)
+    with torch.no_grad():
+        for name in list(t):
+            if name.endswith(".weight"):
+                W(name)  # dequantize once (weights are loaded before the pass in the reference too)
+        times = []
+        for i in (0, 1):
+            dit.block(i, x, txt, cos, sin, mod, tb)  # untimed: thread-pool and allocator warmup
+            t0 = time.perf_counter()
+            dit.block(i, x, txt, cos, sin, mod, tb)
+            times.append(time.perf_counter() - t0)
+    per_pass_ms = (BLOCKS // 2) * (times[0] + times[1]) * 1e3
+    return {
+        "value": per_pass_ms,
+        "unit": "ms per DiT pass",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"oracle block 0 (joint, {L}+{T} keys: {times[0]*1e3:.0f} ms) and block 1 (image-only: "
+                  f"{times[1]*1e3:.0f} ms) at 3952 tokens, fp32 PyTorch CPU, x9 each for 18 blocks "
+                  "(conditioning, embeddings and final layer, <1% of the FLOPs, not included)",
+        "cpu": cpu_model(),
+    }
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-dit", action="store_true", help="only the joint-attention measurement")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
+              file=sys.stderr)
+        sys.exit(2)
+
+    flops = pass_flops()
+    dit, kernels = None, None
+    if not args.no_dit:
+        # the Node runs come first, before this process initialises the GPU
+        dit = run_dit(args.steps, args.warmup)
+        kernels = run_dit_profile()
+    attn = bench_attention(reps=max(10, args.steps), warmup=max(2, args.warmup))
+    log(f"attention: {attn['ms']:.3f} ms/call, flash {attn['flash_ms']:.3f} ms ({attn['flash_tflops']:.1f} TFLOP/s)")
+    cpu = None if args.no_cpu else cpu_baseline()
+
+    ms = dit["ms_device_median"] if dit else None
+    out = {
+        "metric": METRIC,
+        "value": ms,
+        "unit": "ms",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": (ms / PUBLISHED_PASS_MS) if ms else None,
+        "dtype": "fp16",
+        "data": "synthetic (seeded random-init weights of the real architecture; N(0,1) latent/context)",
+        "config": {
+            "workload": "one Nanosaur2 DiT pass at 832x1216: 76x52 latent = 3952 image tokens + 256 text tokens, "
+                        "18 blocks (9 joint, 9 image-only), dim 1536, 16 heads x 96, MLP 4096, int8 ConvRot "
+                        "block linears, batch 1",
+            "tokens": H_IMG * W_IMG, "text_tokens": T_TXT, "blocks": BLOCKS, "parallelism": "none (1 GPU)",
+        },
+        "pass_tflop": flops / 1e12,
+        "pass_tflops": (flops / (ms / 1e3) / 1e12) if ms else None,
+        "pass_ms_wall": dit["ms_wall_median"] if dit else None,
+        "pass_ms_host_to_host": dit["ms_host_to_host_median"] if dit else None,
+        "joint_attention": attn,
+        "roofline": {
+            "kernel": "attn_flash (joint attention, 3952x4208, batch 2)",
+            "bound": "mfma",
+            "achieved": attn["flash_tflops"],
+            "peak": FP16_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": attn["flash_tflops"] / FP16_PEAK_TFLOPS if attn["flash_tflops"] else None,
+            "traffic": None,
+        },
+        "cpu_baseline": cpu,
+        "kernels": kernels,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -90,6 +90,12 @@ int ns2_event_create(void** ev);
 int ns2_event_record(void* ev);
 int ns2_event_elapsed(void* start, void* end, float* ms);
 int ns2_event_destroy(void* ev);
+/* Kernel-level Profiler: while enabled, stream events bracket every kernel launch of the
+ * library; ns2_profile_report writes JSON {"<kernel>": {"count": n, "ms": total}, ...} with
+ * the sums since the last ns2_profile_reset (waits for the recorded events). */
+int ns2_profile_enable(int on);
+int ns2_profile_reset(void);
+int ns2_profile_report(char* buf, size_t cap);
 
 /* ---- ConvRot rotation --------------------------------------------------------------- */
 

@@ -300,6 +300,29 @@ napi_value EventDestroy(napi_env env, napi_callback_info info) {
   return check(env, c, c.failed ? 0 : ns2_event_destroy(ev));
 }
 
+napi_value ProfileEnable(napi_env env, napi_callback_info info) {
+  ARGS(1);
+  int on = c.i32(0);
+  return check(env, c, c.failed ? 0 : ns2_profile_enable(on));
+}
+
+napi_value ProfileReset(napi_env env, napi_callback_info info) {
+  Ctx c{env, nullptr, 0};
+  return check(env, c, ns2_profile_reset());
+}
+
+// profileReport() -> JSON text {"kernel": {"count", "ms"}}
+napi_value ProfileReport(napi_env env, napi_callback_info info) {
+  std::string buf(1 << 16, '\0');
+  if (ns2_profile_report(&buf[0], buf.size()) != NS2_OK) {
+    napi_throw_error(env, nullptr, ns2_last_error());
+    return nullptr;
+  }
+  napi_value s;
+  napi_create_string_utf8(env, buf.c_str(), NAPI_AUTO_LENGTH, &s);
+  return s;
+}
+
 // ---- ops ------------------------------------------------------------------------------------
 
 napi_value Hadamard256(napi_env env, napi_callback_info info) {
@@ -483,7 +506,8 @@ napi_value Module(napi_env env, napi_value exports) {
       {"poolRound", PoolRound}, {"poolGet", PoolGet}, {"poolPut", PoolPut}, {"poolTrim", PoolTrim},
       {"poolStats", PoolStats}, {"h2d", H2D}, {"d2h", D2H}, {"sync", Sync}, {"fill", Fill},
       {"eventCreate", EventCreate}, {"eventRecord", EventRecord}, {"eventElapsed", EventElapsed},
-      {"eventDestroy", EventDestroy}, {"hadamard256", Hadamard256}, {"rotateF16", RotateF16},
+      {"eventDestroy", EventDestroy}, {"profileEnable", ProfileEnable}, {"profileReset", ProfileReset},
+      {"profileReport", ProfileReport}, {"hadamard256", Hadamard256}, {"rotateF16", RotateF16},
       {"linearI8", LinearI8}, {"linearBf16", LinearBf16}, {"attention", Attention},
       {"headNorm", HeadNorm}, {"normMod", NormModT<false>}, {"normModRotateF16", NormModT<true>},
       {"glu", GluT<false>}, {"gluRotateF16", GluT<true>}, {"elementwise", Elementwise},

@@ -367,8 +367,12 @@ template <int D>
 int run_attention(PackArgs pa, FlashArgs fa, int batch) {
   hipStream_t s = ns2::stream();
   const int rows = pa.Lq_pad > pa.Lk_pad ? pa.Lq_pad : pa.Lk_pad;
-  attn_pack_kernel<D><<<dim3(rows / KB, pa.H, batch), 256, 0, s>>>(pa);
-  NS2_LAUNCHED("attn_pack");
+  {
+    ns2::ProfScope prof_("attn_pack");
+    attn_pack_kernel<D><<<dim3(rows / KB, pa.H, batch), 256, 0, s>>>(pa);
+    NS2_LAUNCHED("attn_pack");
+  }
+  ns2::ProfScope prof_("attn_flash");
   // 2 query tiles of 32 per wave; 4 waves per workgroup when that still gives every CU
   // a workgroup, else 2.
   const long long units4 = (long long)((pa.Lq + 255) / 256) * pa.H * batch;

@@ -21,6 +21,15 @@ bool initialised();
 void* workspace(int slot, size_t bytes);
 constexpr int kWorkspaceSlots = 6;
 
+// Kernel profiler (ns2_profile_*): when enabled, stream events bracket every launch and are
+// aggregated by kernel name on ns2_profile_report.
+void prof_begin(const char* name);
+void prof_end();
+struct ProfScope {
+  explicit ProfScope(const char* name) { prof_begin(name); }
+  ~ProfScope() { prof_end(); }
+};
+
 }  // namespace ns2
 
 #define NS2_REQUIRE(cond, ...)                                   \

@@ -316,6 +316,7 @@ constexpr int kGemvMaxM = 8;
 template <bool A_F32, bool W_BF16>
 int launch_gemm(const GemmArgs& p, const char* name) {
   hipStream_t s = ns2::stream();
+  ns2::ProfScope prof_(p.M <= kGemvMaxM ? (W_BF16 ? "gemv_bf16" : "gemv_i8") : (W_BF16 ? "gemm_bf16" : "gemm_i8"));
   if (p.M <= kGemvMaxM) {
     gemv_kernel<W_BF16><<<(p.N + 3) / 4, 256, 0, s>>>(p);
   } else {
@@ -367,6 +368,7 @@ int ns2_linear_i8(const void* A, int a_fmt, int lda, const int8_t* W, const floa
       if (rc) return rc;
     } else {
       const long long quads = (long long)M * K / 4;
+      ns2::ProfScope prof_("cast_f16");
       cast_f16_kernel<<<(unsigned)((quads + 255) / 256), 256, 0, ns2::stream()>>>(static_cast<const float*>(A), lda, xr, M, K);
       NS2_LAUNCHED("cast_f16");
     }

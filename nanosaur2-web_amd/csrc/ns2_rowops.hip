@@ -241,6 +241,7 @@ int ns2_hadamard256(const float* x, float* y, long long groups) {
   NS2_READY();
   if (groups <= 0) return NS2_OK;
   NS2_REQUIRE(x && y && aligned16(x) && aligned16(y), "ns2_hadamard256: null or unaligned buffer");
+  ns2::ProfScope prof_("hadamard256");
   hadamard256_kernel<<<blocks_for(groups, 4), 256, 0, ns2::stream()>>>(x, y, groups);
   NS2_LAUNCHED("hadamard256");
   return NS2_OK;
@@ -254,6 +255,7 @@ int ns2_rotate_f16(const float* x, int ldx, uint16_t* y, int ldy, int rows, int 
               "ns2_rotate_f16: ldx=%d ldy=%d must be multiples of 4 and >= cols", ldx, ldy);
   NS2_REQUIRE(x && y && aligned16(x) && aligned8(y), "ns2_rotate_f16: null or unaligned buffer");
   const int gpr = cols / 256;
+  ns2::ProfScope prof_("rotate_f16");
   rotate_f16_kernel<<<blocks_for((long long)rows * gpr, 4), 256, 0, ns2::stream()>>>(x, ldx, y, ldy, rows, gpr);
   NS2_LAUNCHED("rotate_f16");
   return NS2_OK;
@@ -264,6 +266,7 @@ int ns2_norm_mod(const float* x, const float* mod, long long shiftOff, long long
   NS2_READY();
   if (rows <= 0) return NS2_OK;
   NS2_REQUIRE(x && mod && y && cols > 0, "ns2_norm_mod: bad arguments");
+  ns2::ProfScope prof_("norm_mod");
   norm_mod_kernel<<<rows, 256, 0, ns2::stream()>>>(x, mod, shiftOff, scaleOff, cols, weight, eps, y);
   NS2_LAUNCHED("norm_mod");
   return NS2_OK;
@@ -279,6 +282,7 @@ int ns2_norm_mod_rotate_f16(const float* x, const float* mod, long long shiftOff
   NS2_REQUIRE(x && mod && y && aligned16(x) && aligned8(y) && shiftOff % 4 == 0 && scaleOff % 4 == 0 &&
                   aligned16(mod) && (!weight || aligned16(weight)),
               "ns2_norm_mod_rotate_f16: null or unaligned buffer/offset");
+  ns2::ProfScope prof_("norm_mod_rotate_f16");
   norm_mod_rot_kernel<<<rows, cols / 4, 0, ns2::stream()>>>(x, mod, shiftOff, scaleOff, cols, weight, eps, y);
   NS2_LAUNCHED("norm_mod_rotate_f16");
   return NS2_OK;
@@ -289,6 +293,7 @@ int ns2_head_norm(float* X, const float* w, int L, int H, int D, int ld, long lo
   NS2_READY();
   if (L <= 0 || H <= 0) return NS2_OK;
   NS2_REQUIRE(X && w && D > 0 && D % 2 == 0, "ns2_head_norm: bad arguments");
+  ns2::ProfScope prof_("head_norm");
   head_norm_kernel<<<blocks_for((long long)L * H, 4), 256, 0, ns2::stream()>>>(X, w, L, H, D, ld, colOff, rowOff, cs, sinOff, eps);
   NS2_LAUNCHED("head_norm");
   return NS2_OK;
@@ -299,6 +304,7 @@ int ns2_glu(const float* x, float* y, int rows, int I, int act) {
   if (rows <= 0) return NS2_OK;
   NS2_REQUIRE(x && y && I > 0, "ns2_glu: bad arguments");
   const long long n = (long long)rows * I;
+  ns2::ProfScope prof_("glu");
   glu_kernel<<<blocks_for(n, 256), 256, 0, ns2::stream()>>>(x, y, n, I, act);
   NS2_LAUNCHED("glu");
   return NS2_OK;
@@ -310,6 +316,7 @@ int ns2_glu_rotate_f16(const float* x, uint16_t* y, int rows, int I, int act) {
   NS2_REQUIRE(I > 0 && I % 256 == 0, "ns2_glu_rotate_f16: I=%d must be a multiple of 256", I);
   NS2_REQUIRE(x && y && aligned16(x) && aligned8(y), "ns2_glu_rotate_f16: null or unaligned buffer");
   const long long groups = (long long)rows * (I / 256);
+  ns2::ProfScope prof_("glu_rotate_f16");
   glu_rot_kernel<<<blocks_for(groups, 4), 256, 0, ns2::stream()>>>(x, y, rows, I, act);
   NS2_LAUNCHED("glu_rotate_f16");
   return NS2_OK;
@@ -320,6 +327,7 @@ int ns2_elementwise(int op, const float* a, const float* b, float* y, long long 
   if (n <= 0) return NS2_OK;
   NS2_REQUIRE(op >= NS2_EW_ADD && op <= NS2_EW_COPY, "ns2_elementwise: unknown op %d", op);
   NS2_REQUIRE(a && y && (b || op == NS2_EW_SILU || op == NS2_EW_COPY), "ns2_elementwise: null buffer");
+  ns2::ProfScope prof_("elementwise");
   elementwise_kernel<<<blocks_for(n, 256), 256, 0, ns2::stream()>>>(op, a, b, y, n);
   NS2_LAUNCHED("elementwise");
   return NS2_OK;
@@ -329,6 +337,7 @@ int ns2_accumulate(float* y, const float* a, long long n) {
   NS2_READY();
   if (n <= 0) return NS2_OK;
   NS2_REQUIRE(a && y, "ns2_accumulate: null buffer");
+  ns2::ProfScope prof_("accumulate");
   accumulate_kernel<<<blocks_for(n, 256), 256, 0, ns2::stream()>>>(y, a, n);
   NS2_LAUNCHED("accumulate");
   return NS2_OK;
@@ -338,6 +347,7 @@ int ns2_row_sum(const float* x, const float* w, float* y, int rows, int N, float
   NS2_READY();
   if (N <= 0) return NS2_OK;
   NS2_REQUIRE(x && w && y && rows >= 0, "ns2_row_sum: bad arguments");
+  ns2::ProfScope prof_("row_sum");
   row_sum_kernel<<<blocks_for(N, 64), 64, 0, ns2::stream()>>>(x, w, y, rows, N, scale);
   NS2_LAUNCHED("row_sum");
   return NS2_OK;
@@ -347,6 +357,7 @@ int ns2_rmsnorm(const float* x, const float* w, float* y, int rows, int cols, fl
   NS2_READY();
   if (rows <= 0) return NS2_OK;
   NS2_REQUIRE(x && w && y && cols > 0, "ns2_rmsnorm: bad arguments");
+  ns2::ProfScope prof_("rmsnorm");
   rmsnorm_kernel<<<rows, 256, 0, ns2::stream()>>>(x, w, y, cols, eps);
   NS2_LAUNCHED("rmsnorm");
   return NS2_OK;

@@ -5,6 +5,7 @@
 #include <string.h>
 
 #include <map>
+#include <string>
 #include <mutex>
 #include <vector>
 
@@ -63,6 +64,64 @@ void* workspace(int slot, size_t bytes) {
   }
   w.bytes = want;
   return w.ptr;
+}
+
+// ---- kernel profiler -----------------------------------------------------------------------
+struct ProfPending {
+  const char* name;
+  hipEvent_t a, b;
+};
+struct ProfStat {
+  long long count = 0;
+  double ms = 0;
+};
+static bool g_prof_on = false;
+static std::vector<ProfPending> g_prof_pending;
+static std::vector<hipEvent_t> g_prof_spare;
+static std::map<std::string, ProfStat> g_prof_stats;
+
+static hipEvent_t prof_event() {
+  if (!g_prof_spare.empty()) {
+    hipEvent_t e = g_prof_spare.back();
+    g_prof_spare.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  return e;
+}
+
+void prof_begin(const char* name) {
+  if (!g_prof_on) return;
+  hipEvent_t a = prof_event();
+  if (!a) return;
+  (void)hipEventRecord(a, g_stream);
+  g_prof_pending.push_back({name, a, nullptr});
+}
+
+void prof_end() {
+  if (!g_prof_on || g_prof_pending.empty() || g_prof_pending.back().b) return;
+  hipEvent_t b = prof_event();
+  if (!b) return;
+  (void)hipEventRecord(b, g_stream);
+  g_prof_pending.back().b = b;
+}
+
+static int prof_collect() {
+  for (auto& p : g_prof_pending) {
+    if (p.b) {
+      float ms = 0;
+      NS2_HIP(hipEventSynchronize(p.b));
+      NS2_HIP(hipEventElapsedTime(&ms, p.a, p.b));
+      ProfStat& s = g_prof_stats[p.name];
+      s.count++;
+      s.ms += ms;
+      g_prof_spare.push_back(p.b);
+    }
+    g_prof_spare.push_back(p.a);
+  }
+  g_prof_pending.clear();
+  return NS2_OK;
 }
 
 __global__ void fill_u32_kernel(uint32_t* __restrict__ p, uint32_t value, size_t count) {
@@ -257,6 +316,44 @@ int ns2_event_elapsed(void* start, void* end, float* ms) {
 int ns2_event_destroy(void* ev) {
   if (!ev) return NS2_OK;
   NS2_HIP(hipEventDestroy((hipEvent_t)ev));
+  return NS2_OK;
+}
+
+int ns2_profile_enable(int on) {
+  NS2_READY();
+  if (!on) {
+    int rc = prof_collect();
+    if (rc) return rc;
+  }
+  g_prof_on = on != 0;
+  return NS2_OK;
+}
+
+int ns2_profile_reset(void) {
+  NS2_READY();
+  int rc = prof_collect();
+  if (rc) return rc;
+  g_prof_stats.clear();
+  return NS2_OK;
+}
+
+int ns2_profile_report(char* buf, size_t cap) {
+  NS2_READY();
+  NS2_REQUIRE(buf && cap > 2, "ns2_profile_report: null or tiny buffer");
+  int rc = prof_collect();
+  if (rc) return rc;
+  std::string s = "{";
+  bool first = true;
+  for (const auto& kv : g_prof_stats) {
+    char line[256];
+    snprintf(line, sizeof(line), "%s\"%s\": {\"count\": %lld, \"ms\": %.6f}", first ? "" : ", ",
+             kv.first.c_str(), kv.second.count, kv.second.ms);
+    s += line;
+    first = false;
+  }
+  s += "}";
+  NS2_REQUIRE(s.size() < cap, "ns2_profile_report: buffer of %zu bytes too small (%zu needed)", cap, s.size() + 1);
+  memcpy(buf, s.c_str(), s.size() + 1);
   return NS2_OK;
 }
 

@@ -119,6 +119,10 @@ async function main() {
       dev.push(native.eventElapsed(evA, evB));
       process.stderr.write(`[run_dit] pass ${i + 1}/${a.reps}: ${dev[dev.length - 1].toFixed(3)} ms\n`);
     }
+    if (gpu.profiler) {
+      const rows = await gpu.profiler.report();
+      report.profile = rows.map((r) => ({ name: r.name, count: r.count / a.reps, ms: r.ms / a.reps, tflops: r.flops ? r.flops / (r.ms / 1e3) / 1e12 : null }));
+    }
     const host = [];
     for (let i = 0; i < Math.min(3, a.reps); i++) {
       const w0 = process.hrtime.bigint();
@@ -132,10 +136,6 @@ async function main() {
       reps: a.reps, warmup: a.warmup, ms_device: dev, ms_wall: wall, ms_host_to_host: host,
       ms_device_median: median(dev), ms_wall_median: median(wall), ms_host_to_host_median: median(host),
     });
-    if (gpu.profiler) {
-      const rows = await gpu.profiler.report();
-      report.profile = rows.map((r) => ({ name: r.name, count: r.count / a.reps, ms: r.ms / a.reps, tflops: r.flops ? r.flops / (r.ms / 1e3) / 1e12 : null }));
-    }
   }
   report.pool_peak_bytes = gpu.pool.peak;
   text.release();

@@ -42,6 +42,9 @@ SIGNATURES = {
     "ns2_event_record": [c_vp],
     "ns2_event_elapsed": [c_vp, c_vp, ctypes.POINTER(c_float)],
     "ns2_event_destroy": [c_vp],
+    "ns2_profile_enable": [c_int],
+    "ns2_profile_reset": [],
+    "ns2_profile_report": [ctypes.c_char_p, c_size],
     "ns2_hadamard256": [c_vp, c_vp, c_ll],
     "ns2_rotate_f16": [c_vp, c_int, c_vp, c_int, c_int, c_int],
     "ns2_linear_i8": [c_vp, c_int, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int,
@@ -130,6 +133,20 @@ class Lib:
         ms = c_float()
         self.call("ns2_event_elapsed", a, b, ctypes.byref(ms))
         return ms.value
+
+    def profile(self, on: bool):
+        self.call("ns2_profile_enable", int(on))
+
+    def profile_reset(self):
+        self.call("ns2_profile_reset")
+
+    def profile_report(self) -> dict:
+        """{kernel: {"count": n, "ms": total}} since the last reset."""
+        import json
+
+        buf = ctypes.create_string_buffer(1 << 16)
+        self.call("ns2_profile_report", buf, 1 << 16)
+        return json.loads(buf.value.decode())
 
     # ---- ops (argument meaning as in include/ns2.h)
     def hadamard256(self, x, y, groups):
