@@ -59,3 +59,24 @@ def test_dit_pass_masked_token_and_path_drop(weights_file):
     path-drop pass that skips the SPRINT blocks."""
     _run_case(weights_file, "masked", 5, 7, 12, zero=(3,), seed=11)
     _run_case(weights_file, "pathdrop", 5, 7, 12, path_drop=True, seed=12)
+
+
+def test_dit_pass_against_reference_golden(tmp_path):
+    """The HIP path against x0 written by the reference implementation itself
+    (tests/golden/dit_composition.npz; MLP width 256)."""
+    import json
+
+    z = np.load(os.path.join(os.path.dirname(__file__), "golden", "dit_composition.npz"), allow_pickle=False)
+    meta = json.loads(bytes(z["meta"]).decode())
+    tensors = F.make_weights(seed=meta["weight_seed"], I=meta["mlp_width"])
+    path = str(tmp_path / "golden_w.safetensors")
+    F.save_weights(tensors, path)
+    for c in meta["cases"]:
+        inp = F.make_inputs(c["h"], c["w"], c["T"], seed=c["input_seed"], zero_weight_tokens=c["zero_weight_tokens"])
+        idir = str(tmp_path / c["name"])
+        F.write_inputs(inp, idir)
+        out = str(tmp_path / f"{c['name']}.f32")
+        args = ["--weights", path, "--inputs", idir, "--out", out] + (["--path-drop"] if c["path_drop"] else [])
+        F.run_node(args)
+        got = torch.from_numpy(np.fromfile(out, dtype=np.float32).reshape(64, c["h"], c["w"]))
+        assert_close(got, torch.from_numpy(z[f"{c['name']}.x0"]), TOL_PASS, f"HIP pass vs reference golden {c['name']}")
