@@ -137,6 +137,22 @@ def bench_attention(reps, warmup):
     }
 
 
+def copy_calibration(n=64 << 20, reps=3):
+    """ns2_elementwise copy of n fp32 values: 4n bytes read + 4n bytes written per launch,
+    the known-size kernel that HBM byte counters are scaled against."""
+    import torch
+
+    import ns2
+
+    lib = ns2.load(0)
+    a = torch.ones(n, device="cuda")
+    b = torch.empty(n, device="cuda")
+    for _ in range(reps):
+        lib.elementwise("copy", a, None, b, n)
+    torch.cuda.synchronize()
+    return {"kernel": "elementwise_kernel (copy)", "bytes_read": 4 * n, "bytes_written": 4 * n, "launches": reps}
+
+
 def rope_table(h, w):
     """cos|sin table of the centred 2-D RoPE (app/models/common.js:28-43 layout)."""
     import math
@@ -235,6 +251,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-dit", action="store_true", help="only the joint-attention measurement")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run a 256 MiB -> 256 MiB copy kernel (reference point for HBM counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
@@ -248,6 +266,8 @@ def main():
         dit = run_dit(args.steps, args.warmup)
         kernels = run_dit_profile()
     attn = bench_attention(reps=max(10, args.steps), warmup=max(2, args.warmup))
+    if args.copy_calibration:
+        attn["copy_calibration"] = copy_calibration()
     log(f"attention: {attn['ms']:.3f} ms/call, flash {attn['flash_ms']:.3f} ms ({attn['flash_tflops']:.1f} TFLOP/s)")
     cpu = None if args.no_cpu else cpu_baseline()
 
