@@ -3,18 +3,26 @@
 // Two kernels per call:
 //  1. pack: reads the fp32 q/k/v views, applies the optional per-head RMSNorm and split-half
 //     RoPE (the DiT's headNorm, kernels.js:307-342), folds scale*log2(e) into q, and writes
-//     head-major fp16 operands: Qp [B*H][Lq_pad][D], Kp [B*H][Lk_pad][D], Vt [B*H][D][Lk_pad]
-//     (V transposed), plus one fp32 bias per key in log2 units (0 on image keys, the
-//     log-prompt-weight on text keys, -1e30 on padding keys).
-//  2. flash: one workgroup per (query block, head, batch); K/V tiles of 64 keys are staged in
-//     LDS (double-buffered, register prefetch). Each wave owns QT x 32 queries and works in
-//     the transposed domain so no register shuffles are needed between the two products:
-//        S^T = K Q^T       (A = K rows from LDS, B = Q^T held in registers)
-//        O^T += V^T P^T    (A = V^T rows from LDS, B = P^T straight from the S^T registers)
+//     fp16 operands. Q is row-major per head, Qp [B*H][Lq_pad][D]. K and V are written per
+//     64-key tile as the exact byte image of the flash kernel's LDS stage, so a tile moves
+//     into LDS with direct global->LDS loads (no registers, no LDS store instructions):
+//        Kc [B*H][tile][D/8 chunks][64 keys][8 dims]        (chunk-major K)
+//        Vc [B*H][tile][8 key-chunks][D dims][8 keys]       (V transposed, chunk-major)
+//     plus one fp32 bias per key in log2 units (0 on image keys, the log-prompt-weight on
+//     text keys, -1e30 on padding keys).
+//  2. flash: one workgroup per (query block, head, batch). Each wave owns QT x 32 queries and
+//     works in the transposed domain, so no register shuffles are needed between products:
+//        S^T = K Q^T       (A = K fragments from LDS, B = Q^T held in registers)
+//        O^T += V^T P^T    (A = V^T fragments from LDS, B = P^T straight from S^T registers)
 //     The 32x32 MFMA accumulator of S^T gives every lane one query column and 16 keys, which
 //     is exactly the k-slice a lane supplies as B operand of the next product (the k order
 //     inside an MFMA is free as long as A and B agree), and the online-softmax statistics
-//     of a query live in the same lanes as its output column.
+//     of a query live in the same lanes as its output column. In the chunk-major LDS images
+//     the 32 lanes of a half-wave read 32 consecutive 16-byte rows: no bank conflicts.
+#include <stdlib.h>
+
+#include <type_traits>
+
 #include "ns2_common.h"
 
 using namespace ns2dev;
@@ -25,7 +33,11 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kMaskBias = -1.0e30f;
 constexpr int KB = 64;          // keys per tile
 constexpr int QPAD = 256;       // Lq padding granule (largest query block)
-constexpr int KPAD_LDS = 8;     // halfs of padding per LDS row
+
+// Position of key k (within a 16-key step) in the stored V^T order: bits 2 and 3 swapped, so
+// the 8 keys one lane feeds to a PV product, {4hi..4hi+3, 8+4hi..8+4hi+3}, are 8 adjacent
+// stored keys (one 16-byte chunk). The map is its own inverse.
+__device__ __forceinline__ int vkey_pos(int k) { return (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1); }
 
 struct PackArgs {
   const float* q;
@@ -36,8 +48,8 @@ struct PackArgs {
   const float* k_norm;
   const float* cs;
   half_t* Qp;
-  half_t* Kp;
-  half_t* Vt;
+  half_t* Kc;
+  half_t* Vc;
   float* bias2;
   long long qOff, kOff, vOff, qBatch, kBatch, vBatch, biasBatch, sinOff;
   int Lq, Lk, Lq_pad, Lk_pad, H, ldq, ldk, ldv, biasStart, rope_rows;
@@ -90,18 +102,20 @@ __device__ __forceinline__ void prep_row(const float* __restrict__ src, const fl
   }
 }
 
-// grid: (rows / 64, H, batch), 256 threads: 64 rows x 4 parts.
+// grid: (rows / 64, H, batch), 256 threads: 64 rows x 4 parts. Block x handles key tile x.
 template <int D>
 __global__ __launch_bounds__(256) void attn_pack_kernel(PackArgs a) {
+  constexpr int KROW = D + 8;
+  __shared__ __attribute__((aligned(16))) half_t ktile[KB][KROW];
   __shared__ half_t vs[D][KB + 2];
   const int h = blockIdx.y, b = blockIdx.z;
   const int bh = b * a.H + h;
-  const int row0 = blockIdx.x * KB;
+  const int tile = blockIdx.x, row0 = tile * KB;
   const int tid = threadIdx.x;
   const int rl = tid >> 2, part = tid & 3;
   const int row = row0 + rl;
 
-  // Q rows
+  // Q rows (row-major per head)
   if (row0 < a.Lq_pad) {
     half_t* dst = a.Qp + ((long long)bh * a.Lq_pad + row) * D;
     if (row < a.Lq) {
@@ -112,77 +126,109 @@ __global__ __launch_bounds__(256) void attn_pack_kernel(PackArgs a) {
       for (int j = 0; j < D / 4; ++j) dst[part * (D / 4) + j] = (half_t)0.f;
     }
   }
-  if (row0 < a.Lk_pad) {
-    // K rows
-    half_t* dst = a.Kp + ((long long)bh * a.Lk_pad + row) * D;
-    if (row < a.Lk) {
-      const float* src = a.k + a.kOff + b * a.kBatch + (long long)row * a.ldk + (long long)h * D;
-      prep_row<D>(src, a.k_norm, a.cs, a.sinOff, row, a.cs && row < a.rope_rows, 1.0f, a.eps, part, dst);
-    } else {
+  if (row0 >= a.Lk_pad) return;  // uniform per block
+
+  // K rows -> LDS, V rows -> LDS transposed
+  if (row < a.Lk) {
+    const float* src = a.k + a.kOff + b * a.kBatch + (long long)row * a.ldk + (long long)h * D;
+    prep_row<D>(src, a.k_norm, a.cs, a.sinOff, row, a.cs && row < a.rope_rows, 1.0f, a.eps, part, &ktile[rl][0]);
+  } else {
 #pragma unroll
-      for (int j = 0; j < D / 4; ++j) dst[part * (D / 4) + j] = (half_t)0.f;
-    }
-    // V rows -> transposed through LDS
-    {
-      const float* src = a.v + a.vOff + b * a.vBatch + (long long)row * a.ldv + (long long)h * D;
+    for (int j = 0; j < D / 4; ++j) ktile[rl][part * (D / 4) + j] = (half_t)0.f;
+  }
+  {
+    const float* src = a.v + a.vOff + b * a.vBatch + (long long)row * a.ldv + (long long)h * D;
 #pragma unroll
-      for (int j = 0; j < D / 4; ++j) {
-        const int d = part * (D / 4) + j;
-        vs[d][rl] = (half_t)(row < a.Lk ? src[d] : 0.f);
-      }
+    for (int j = 0; j < D / 4; ++j) {
+      const int d = part * (D / 4) + j;
+      vs[d][rl] = (half_t)(row < a.Lk ? src[d] : 0.f);
     }
-    __syncthreads();
-    for (int e = tid; e < D * KB; e += 256) {
-      const int d = e / KB, kk = e % KB;
-      a.Vt[((long long)bh * D + d) * a.Lk_pad + row0 + kk] = vs[d][kk];
+  }
+  __syncthreads();
+
+  // chunk-major tile images, 16 bytes per thread and step
+  const long long tiles = a.Lk_pad / KB;
+  half_t* kdst = a.Kc + ((long long)bh * tiles + tile) * (KB * D);
+  for (int i = tid; i < (D / 8) * KB; i += 256) {
+    const int key = i % KB, chunk = i / KB;
+    *reinterpret_cast<uint4*>(kdst + (long long)i * 8) = *reinterpret_cast<const uint4*>(&ktile[key][chunk * 8]);
+  }
+  half_t* vdst = a.Vc + ((long long)bh * tiles + tile) * (KB * D);
+  for (int i = tid; i < 8 * D; i += 256) {
+    const int d = i % D, kc = i / D;
+    half8_t v8;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v8[e] = vs[d][vkey_pos(kc * 8 + e)];
+    *reinterpret_cast<half8_t*>(vdst + (long long)i * 8) = v8;
+  }
+  // per-key bias in log2 units (one head does it)
+  if (h == 0 && tid < KB) {
+    const int key = row0 + tid;
+    float bv = kMaskBias;
+    if (key < a.Lk) {
+      bv = 0.f;
+      if (a.key_bias && key >= a.biasStart) bv = a.key_bias[b * a.biasBatch + key - a.biasStart] * kLog2e;
     }
-    // per-key bias in log2 units (one head does it)
-    if (h == 0 && tid < KB) {
-      const int key = row0 + tid;
-      float bv = kMaskBias;
-      if (key < a.Lk) {
-        bv = 0.f;
-        if (a.key_bias && key >= a.biasStart) bv = a.key_bias[b * a.biasBatch + key - a.biasStart] * kLog2e;
-      }
-      a.bias2[(long long)b * a.Lk_pad + key] = bv;
-    }
+    a.bias2[(long long)b * a.Lk_pad + key] = bv;
   }
 }
 
 struct FlashArgs {
   const half_t* Qp;
-  const half_t* Kp;
-  const half_t* Vt;
+  const half_t* Kc;
+  const half_t* Vc;
   const float* bias2;
   float* O;
   long long oOff, oBatch;
   int Lq, Lk, Lq_pad, Lk_pad, H, ldo;
   int bias_block0;  // first key tile that needs the per-key bias (text or padding keys)
+  int qblocks;      // query blocks per (batch, head)
+  int pairs;        // batch * heads
+  int xcd_order;    // 1: block id -> (pair, query block) keeps a pair on one XCD
 };
+
+// Scores are kept relative to a per-query reference m_ref (log2 units) that only moves when a
+// score exceeds it by more than 2^kRebase; between moves the output accumulator needs no
+// rescale. Any reference gives the same softmax, and p <= 2^kRebase stays in fp16 range.
+constexpr float kRebase = 8.0f;
 
 template <int D, int QT, int NW>
 __global__ __launch_bounds__(NW * 64) void flash_kernel(FlashArgs a) {
-  constexpr int NT = NW * 64;
-  constexpr int KROW = D + KPAD_LDS;    // K tile row (halfs)
-  constexpr int VROW = KB + KPAD_LDS;   // V^T tile row (halfs)
-  constexpr int DC = D / 16;            // k-steps of S
-  constexpr int DT = D / 32;            // dim tiles of O
-  constexpr int K_CHUNKS = KB * D / 8;  // 16-byte chunks per K tile
-  constexpr int V_CHUNKS = D * KB / 8;
-  constexpr int KC_T = (K_CHUNKS + NT - 1) / NT;
-  constexpr int VC_T = (V_CHUNKS + NT - 1) / NT;
+  constexpr int DC = D / 16;             // k-steps of S
+  constexpr int DT = D / 32;             // dim tiles of O
+  constexpr int TILE = KB * D;           // halfs per K (or V) tile image
+  constexpr int BLOCKS = 2 * TILE / 512; // 1 KB direct-load blocks per stage (K then V)
 
-  __shared__ __attribute__((aligned(16))) half_t ks[2][KB * KROW];
-  __shared__ __attribute__((aligned(16))) half_t vts[2][D * VROW];
-  __shared__ float kbias[2][KB];
+  // three stages: K of tile t+1 and V of tile t are read while tile t+2 lands
+  __shared__ __attribute__((aligned(16))) half_t ks[3][TILE];
+  __shared__ __attribute__((aligned(16))) half_t vts[3][TILE];
+  __shared__ __attribute__((aligned(16))) float kbias[3][KB];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int h = blockIdx.y, b = blockIdx.z, bh = b * a.H + h;
-  const int q0 = blockIdx.x * (NW * QT * 32) + wave * QT * 32;
+  // Work unit: (pair = batch*H + head, query block). With xcd_order, consecutive block ids
+  // land on different XCDs (round-robin dispatch), so block id i is mapped to pair
+  // (i % 8) + 8 * ((i / 8) / qblocks): every query block of a pair runs on one XCD and its
+  // K/V tiles are fetched into that XCD's L2 once.
+  int pair, qb;
+  {
+    const int id = blockIdx.x;
+    if (a.xcd_order) {
+      const int local = id >> 3;
+      pair = (id & 7) + 8 * (local / a.qblocks);
+      qb = local % a.qblocks;
+    } else {
+      pair = id / a.qblocks;
+      qb = id % a.qblocks;
+    }
+  }
+  const int b = pair / a.H, h = pair % a.H, bh = pair;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int q0 = qb * (NW * QT * 32) + wave * QT * 32;
   const int lq = lane & 31, hi = lane >> 5;
+  const int ntiles = a.Lk_pad / KB;
 
-  const half_t* Kg = a.Kp + (long long)bh * a.Lk_pad * D;
-  const half_t* Vg = a.Vt + (long long)bh * D * a.Lk_pad;
+  const half_t* Kt = a.Kc + (long long)bh * ntiles * TILE;
+  const half_t* Vt = a.Vc + (long long)bh * ntiles * TILE;
   const float* Bg = a.bias2 + (long long)b * a.Lk_pad;
 
   // Q^T operands: lane holds query q0 + qt*32 + lq, dims c*16 + 8*hi .. +7
@@ -201,86 +247,58 @@ __global__ __launch_bounds__(NW * 64) void flash_kernel(FlashArgs a) {
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
       for (int r = 0; r < 16; ++r) o[qt][dt][r] = 0.f;
-  float m_run[QT], l_run[QT];
+  float m_ref[QT], l_run[QT];
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
-    m_run[qt] = kMaskBias;
+    m_ref[qt] = 0.f;
     l_run[qt] = 0.f;
   }
 
-  uint4 kreg[KC_T], vreg[VC_T];
-  float breg = 0.f;
-  auto gload = [&](int t) {
-    const int key0 = t * KB;
-#pragma unroll
-    for (int i = 0; i < KC_T; ++i) {
-      const int c = tid + i * NT;
-      if (c < K_CHUNKS) kreg[i] = *reinterpret_cast<const uint4*>(Kg + (long long)key0 * D + c * 8);
+  // Tile t -> LDS stage st with direct global->LDS loads: the stage image is BLOCKS blocks of
+  // 1 KB (K blocks, then V^T blocks) plus the 256-byte key bias; wave w moves blocks w, w+NW,
+  // ...; lane l moves bytes [16l, 16l+16) of a block (16 lanes for the bias). Every load goes
+  // through this one call site so the LDS base (M0) is set from its own destination.
+  auto dma = [&](int t, int st) {
+    for (int j = wave; j <= BLOCKS; j += NW) {
+      const int kind = j < BLOCKS / 2 ? 0 : (j < BLOCKS ? 1 : 2);
+      const half_t* src = kind == 0 ? Kt + (long long)t * TILE + j * 512 + lane * 8
+                        : kind == 1 ? Vt + (long long)t * TILE + (j - BLOCKS / 2) * 512 + lane * 8
+                                    : reinterpret_cast<const half_t*>(Bg + t * KB) + lane * 8;
+      half_t* dst = kind == 0 ? ks[st] + j * 512
+                  : kind == 1 ? vts[st] + (j - BLOCKS / 2) * 512
+                              : reinterpret_cast<half_t*>(kbias[st]);
+      if (kind < 2 || lane < KB / 4) __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
     }
-#pragma unroll
-    for (int i = 0; i < VC_T; ++i) {
-      const int c = tid + i * NT;
-      if (c < V_CHUNKS) {
-        const int d = c / (KB / 8), kc = (c % (KB / 8)) * 8;
-        vreg[i] = *reinterpret_cast<const uint4*>(Vg + (long long)d * a.Lk_pad + key0 + kc);
-      }
-    }
-    if (tid < KB) breg = Bg[key0 + tid];
-  };
-  auto sstore = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < KC_T; ++i) {
-      const int c = tid + i * NT;
-      if (c < K_CHUNKS) {
-        const int key = c / (D / 8), dc = (c % (D / 8)) * 8;
-        *reinterpret_cast<uint4*>(&ks[buf][key * KROW + dc]) = kreg[i];
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < VC_T; ++i) {
-      const int c = tid + i * NT;
-      if (c < V_CHUNKS) {
-        const int d = c / (KB / 8), kc = (c % (KB / 8)) * 8;
-        *reinterpret_cast<uint4*>(&vts[buf][d * VROW + kc]) = vreg[i];
-      }
-    }
-    if (tid < KB) kbias[buf][tid] = breg;
   };
 
-  const int ntiles = a.Lk_pad / KB;
-  gload(0);
-  sstore(0);
-  __syncthreads();
-
-  for (int t = 0; t < ntiles; ++t) {
-    const int cur = t & 1;
-    if (t + 1 < ntiles) gload(t + 1);
-
-    // ---- S^T = K Q^T: s[kt][qt][r] = score(key t*64 + kt*32 + 8(r/4) + 4hi + r%4, query lq)
-    float16_t s[2][QT];
+  // S^T = K Q^T for the 64-key tile in LDS stage `buf`, the two 32-key halves' MFMA chains
+  // interleaved: s[kt][qt][r] = score(key 64t + 32kt + 8(r/4) + 4hi + r%4, query lq).
+  // A fragment: chunk 2c + hi (dims 16c + 8hi .. +7) of key 32kt + lq.
+  auto qk = [&](float16_t (&s)[2][QT], int buf) {
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
+    for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
       for (int qt = 0; qt < QT; ++qt)
 #pragma unroll
         for (int r = 0; r < 16; ++r) s[kt][qt][r] = 0.f;
-      const half_t* krow = &ks[cur][(kt * 32 + lq) * KROW + 8 * hi];
 #pragma unroll
-      for (int c = 0; c < DC; ++c) {
-        const half8_t kf = *reinterpret_cast<const half8_t*>(krow + c * 16);
+    for (int c = 0; c < DC; ++c)
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+        const half8_t kf = *reinterpret_cast<const half8_t*>(&ks[buf][((2 * c + hi) * KB + kt * 32 + lq) * 8]);
 #pragma unroll
         for (int qt = 0; qt < QT; ++qt)
           s[kt][qt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[qt][c], s[kt][qt], 0, 0, 0);
       }
-    }
-
-    // ---- per-key bias (text keys and padding keys only)
-    if (t >= a.bias_block0) {
+  };
+  // per-key bias (text and padding keys), then the row maximum (both 32-key halves)
+  auto bias_max = [&](float16_t (&s)[2][QT], float (&mx)[QT], int buf, bool biased) {
+    if (biased) {
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          const float4 bb = *reinterpret_cast<const float4*>(&kbias[cur][kt * 32 + 8 * g + 4 * hi]);
+          const float4 bb = *reinterpret_cast<const float4*>(&kbias[buf][kt * 32 + 8 * g + 4 * hi]);
 #pragma unroll
           for (int qt = 0; qt < QT; ++qt) {
             s[kt][qt][4 * g + 0] += bb.x;
@@ -290,59 +308,135 @@ __global__ __launch_bounds__(NW * 64) void flash_kernel(FlashArgs a) {
           }
         }
     }
-
-    // ---- online softmax (log2 domain) and P^T operands
-    half8_t pf[QT][2][2];
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
-      float mx = s[0][qt][0];
+      float m = s[0][qt][0];
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kt][qt][r]);
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float m_new = fmaxf(m_run[qt], mx);
-      const float alpha = __builtin_amdgcn_exp2f(m_run[qt] - m_new);
-      m_run[qt] = m_new;
-      float ls = 0.f;
+        for (int r = 0; r < 16; ++r) m = fmaxf(m, s[kt][qt][r]);
+      mx[qt] = fmaxf(m, __shfl_xor(m, 32, 64));
+    }
+  };
+
+  // Software pipeline, one barrier per tile. Iteration t:
+  //   wait for this wave's loads, barrier (tile t+1 has landed; every wave is done with
+  //   iteration t-1), start loading tile t+2 into stage (t+2)%3 (it held tile t-1);
+  //   move the softmax reference if tile t needs it (rare);
+  //   phase A: scores of tile t+1 on the MFMA pipe, interleaved with exp/convert/sum of tile t;
+  //   phase B: O += V_t P_t on the MFMA pipe, interleaved with bias and row max of tile t+1.
+  float16_t s_cur[2][QT];
+  float mx_cur[QT];
+  dma(0, 0);
+  if (ntiles > 1) dma(1, 1);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  qk(s_cur, 0);
+  bias_max(s_cur, mx_cur, 0, 0 >= a.bias_block0);
+
+  auto step = [&](int t, auto more_c, auto bias_next_c) {
+    constexpr bool MORE = decltype(more_c)::value;
+    constexpr bool BIAS_NEXT = decltype(bias_next_c)::value;
+    const int vbuf = t % 3, kbuf = (t + 1) % 3;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (MORE && t + 2 < ntiles) dma(t + 2, (t + 2) % 3);
+
+    // ---- move the reference when a score exceeds it by more than 2^kRebase, or when nothing
+    // has been accumulated yet (l = 0: the tile maximum becomes the reference, so the largest
+    // p is 1 and l >= 1 afterwards); the running sum and output scale by 2^-shift
+    {
+      bool need = false;
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
+      for (int qt = 0; qt < QT; ++qt) need |= (mx_cur[qt] - m_ref[qt] > kRebase) || (l_run[qt] == 0.f);
+      if (__builtin_amdgcn_ballot_w64(need)) {
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) {
+          const float d = mx_cur[qt] - m_ref[qt];
+          const float shift = (l_run[qt] == 0.f) ? d : fmaxf(d, 0.f);
+          const float alpha = __builtin_amdgcn_exp2f(-shift);
+          m_ref[qt] += shift;
+          l_run[qt] *= alpha;
+#pragma unroll
+          for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o[qt][dt][r] *= alpha;
+        }
+      }
+    }
+
+    // ---- phase A (raised wave priority while this wave feeds the MFMA pipe)
+    __builtin_amdgcn_s_setprio(1);
+    float16_t s_next[2][QT];
+    if (MORE) qk(s_next, kbuf);
+    half8_t pf[2][QT][2];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) {
+        float ls = 0.f;
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const float pv = __builtin_amdgcn_exp2f(s[kt][qt][kk * 8 + e] - m_new);
-            const half_t ph = (half_t)pv;
-            pf[qt][kt][kk][e] = ph;
-            ls += (float)ph;
+          for (int e = 0; e < 8; e += 2) {
+            half2_t pp;
+            pp[0] = (half_t)__builtin_amdgcn_exp2f(s_cur[kt][qt][kk * 8 + e] - m_ref[qt]);
+            pp[1] = (half_t)__builtin_amdgcn_exp2f(s_cur[kt][qt][kk * 8 + e + 1] - m_ref[qt]);
+            pf[kt][qt][kk][e] = pp[0];
+            pf[kt][qt][kk][e + 1] = pp[1];
+            const half2_t one = {(half_t)1.0f, (half_t)1.0f};
+            ls = __builtin_amdgcn_fdot2(pp, one, ls, false);
           }
-      l_run[qt] = l_run[qt] * alpha + ls;
+        l_run[qt] += ls;
+      }
+    if (MORE) {
+      // 2*DC*QT score MFMAs, each after its K-fragment read, with the exp work between them
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) o[qt][dt][r] *= alpha;
+      for (int i = 0; i < 2 * DC; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, QT, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 6 * QT, 0);
+      }
     }
 
-    // ---- O^T += V^T P^T: A = V^T[dim dt*32 + lq][keys kt*32 + kk*16 + {4hi..4hi+3, 8+4hi..}]
+    // ---- phase B: O^T += V^T P^T, the DT accumulators interleaved.
+    // A fragment: stored key chunk 4kt + 2kk + hi of dim 32dt + lq.
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
-      const half_t* vrow = &vts[cur][(dt * 32 + lq) * VROW + 4 * hi];
+    for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
+      for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-          const half4_t v0 = *reinterpret_cast<const half4_t*>(vrow + kt * 32 + kk * 16);
-          const half4_t v1 = *reinterpret_cast<const half4_t*>(vrow + kt * 32 + kk * 16 + 8);
-          const half8_t vf = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+        for (int dt = 0; dt < DT; ++dt) {
+          const half8_t vf = *reinterpret_cast<const half8_t*>(&vts[vbuf][((4 * kt + 2 * kk + hi) * D + dt * 32 + lq) * 8]);
 #pragma unroll
           for (int qt = 0; qt < QT; ++qt)
-            o[qt][dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[qt][kt][kk], o[qt][dt], 0, 0, 0);
+            o[qt][dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[kt][qt][kk], o[qt][dt], 0, 0, 0);
         }
+    __builtin_amdgcn_s_setprio(0);
+    if (MORE) {
+      float mx_next[QT];
+      bias_max(s_next, mx_next, kbuf, BIAS_NEXT);
+#pragma unroll
+      for (int i = 0; i < 4 * DT; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, QT, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 4 * QT, 0);
+      }
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) {
+        mx_cur[qt] = mx_next[qt];
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) s_cur[kt][qt] = s_next[kt][qt];
+      }
     }
-
-    if (t + 1 < ntiles) sstore(cur ^ 1);
-    __syncthreads();
-  }
+  };
+  using T_ = std::integral_constant<bool, true>;
+  using F_ = std::integral_constant<bool, false>;
+  // the scores of tile t+1 need the bias when t+1 >= bias_block0
+  const int tb = a.bias_block0 - 1 < ntiles - 1 ? (a.bias_block0 - 1 > 0 ? a.bias_block0 - 1 : 0) : ntiles - 1;
+  for (int t = 0; t < tb; ++t) step(t, T_{}, F_{});
+  for (int t = tb; t < ntiles - 1; ++t) step(t, T_{}, T_{});
+  step(ntiles - 1, F_{}, F_{});
 
   // ---- normalise and store: o[qt][dt][r] = O[query lq][dim dt*32 + 8(r/4) + 4hi + r%4]
 #pragma unroll
@@ -363,6 +457,15 @@ __global__ __launch_bounds__(NW * 64) void flash_kernel(FlashArgs a) {
   }
 }
 
+template <int D, int QT, int NW>
+void launch_flash(FlashArgs fa, hipStream_t s) {
+  constexpr int BQ = NW * QT * 32;
+  fa.qblocks = (fa.Lq + BQ - 1) / BQ;
+  const int blocks = fa.qblocks * fa.pairs;
+  fa.xcd_order = (fa.pairs % 8 == 0) ? 1 : 0;
+  flash_kernel<D, QT, NW><<<blocks, NW * 64, 0, s>>>(fa);
+}
+
 template <int D>
 int run_attention(PackArgs pa, FlashArgs fa, int batch) {
   hipStream_t s = ns2::stream();
@@ -373,16 +476,10 @@ int run_attention(PackArgs pa, FlashArgs fa, int batch) {
     NS2_LAUNCHED("attn_pack");
   }
   ns2::ProfScope prof_("attn_flash");
-  // 2 query tiles of 32 per wave; 4 waves per workgroup when that still gives every CU
-  // a workgroup, else 2.
-  const long long units4 = (long long)((pa.Lq + 255) / 256) * pa.H * batch;
-  if (units4 >= 256) {
-    dim3 grid((pa.Lq + 255) / 256, pa.H, batch);
-    flash_kernel<D, 2, 4><<<grid, 256, 0, s>>>(fa);
-  } else {
-    dim3 grid((pa.Lq + 127) / 128, pa.H, batch);
-    flash_kernel<D, 2, 2><<<grid, 128, 0, s>>>(fa);
-  }
+  fa.pairs = pa.H * batch;
+  // 32 queries per wave, 8 waves (256 queries) per workgroup: two waves per SIMD, all
+  // accumulators in architectural VGPRs
+  launch_flash<D, 1, 8>(fa, s);
   NS2_LAUNCHED("attn_flash");
   return NS2_OK;
 }
@@ -405,7 +502,8 @@ extern "C" int ns2_attention(const float* q, const float* k, const float* v, flo
   NS2_REQUIRE(Lk > 0 && H > 0, "ns2_attention: Lk=%d H=%d", Lk, H);
   NS2_REQUIRE(ldo % 4 == 0 && oOff % 4 == 0 && oBatch % 4 == 0 && aligned16(o),
               "ns2_attention: the output view must be 16-byte aligned (ldo, oOff, oBatch multiples of 4)");
-  NS2_REQUIRE(ldq >= H * D || qOff > 0 || ldq >= D, "ns2_attention: bad ldq");
+  NS2_REQUIRE(ldq >= D && ldk >= D && ldv >= D, "ns2_attention: row strides must cover one head");
+  if (key_bias) NS2_REQUIRE(biasStart >= 0, "ns2_attention: negative biasStart");
   const int Lq_pad = (Lq + QPAD - 1) / QPAD * QPAD;
   const int Lk_pad = (Lk + KB - 1) / KB * KB;
   const long long bh = (long long)batch * H;
@@ -413,19 +511,18 @@ extern "C" int ns2_attention(const float* q, const float* k, const float* v, flo
   const size_t kbytes = (size_t)bh * Lk_pad * D * sizeof(half_t);
   const size_t bbytes = (size_t)batch * Lk_pad * sizeof(float);
   half_t* Qp = static_cast<half_t*>(ns2::workspace(1, qbytes));
-  half_t* Kp = static_cast<half_t*>(ns2::workspace(2, kbytes));
-  half_t* Vt = static_cast<half_t*>(ns2::workspace(3, kbytes));
+  half_t* Kc = static_cast<half_t*>(ns2::workspace(2, kbytes));
+  half_t* Vc = static_cast<half_t*>(ns2::workspace(3, kbytes));
   float* B2 = static_cast<float*>(ns2::workspace(4, bbytes));
-  if (!Qp || !Kp || !Vt || !B2) return ns2::set_error(NS2_ERR_OOM, "ns2_attention: workspace allocation failed");
+  if (!Qp || !Kc || !Vc || !B2) return ns2::set_error(NS2_ERR_OOM, "ns2_attention: workspace allocation failed");
 
-  PackArgs pa{q, k, v, key_bias, q_norm, k_norm, rope_cs, Qp, Kp, Vt, B2,
+  PackArgs pa{q, k, v, key_bias, q_norm, k_norm, rope_cs, Qp, Kc, Vc, B2,
               qOff, kOff, vOff, qBatch, kBatch, vBatch, biasBatch, sin_off,
               Lq, Lk, Lq_pad, Lk_pad, H, ldq, ldk, ldv, biasStart, rope_rows,
               scale * kLog2e, eps};
   int first_biased = Lk;  // padding keys need the mask bias too
-  if (key_bias && biasStart < Lk) first_biased = biasStart < 0 ? 0 : biasStart;
-  FlashArgs fa{Qp, Kp, Vt, B2, o, oOff, oBatch, Lq, Lk, Lq_pad, Lk_pad, H, ldo, first_biased / KB};
-  if (key_bias) NS2_REQUIRE(biasStart >= 0, "ns2_attention: negative biasStart");
+  if (key_bias && biasStart < Lk) first_biased = biasStart;
+  FlashArgs fa{Qp, Kc, Vc, B2, o, oOff, oBatch, Lq, Lk, Lq_pad, Lk_pad, H, ldo, first_biased / KB, 0, 0, 0};
   switch (D) {
     case 32: return run_attention<32>(pa, fa, batch);
     case 64: return run_attention<64>(pa, fa, batch);
