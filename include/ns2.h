@@ -102,9 +102,11 @@ int ns2_profile_report(char* buf, size_t cap);
 /* ops.rotate + hadamardShader (app/gpu/ops.js:38-44, app/gpu/kernels.js:378-407):
  * y = x H per contiguous group of 256 fp32 values, groups = size / 256. y may equal x. */
 int ns2_hadamard256(const float* x, float* y, long long groups);
-/* Same rotation on a strided [rows, cols] view (cols % 256 == 0), written as fp16
- * (the pre-rotated `xr` operand of ns2_linear_i8, ldy in fp16 elements). */
-int ns2_rotate_f16(const float* x, int ldx, uint16_t* y, int ldy, int rows, int cols);
+/* Same rotation on a strided [rows, cols] view (cols % 256 == 0), written as fp16: the
+ * pre-rotated operand of the int8 linear. tiled == 0: row-major with ldy (fp16 elements), the
+ * `xr` of ns2_linear_i8; tiled != 0: the tiled layout of ns2_linear_i8_tiled (ldy ignored;
+ * y holds ceil(rows/64)*64 rows). */
+int ns2_rotate_f16(const float* x, int ldx, uint16_t* y, int ldy, int rows, int cols, int tiled);
 
 /* ---- linear layers (ops.linear, app/gpu/ops.js:50-66; runMatmul :14-32;
  *      matmulShader epilogue app/gpu/gemm.js:159-164) -------------------------------------
@@ -122,6 +124,18 @@ int ns2_linear_i8(const void* A, int a_fmt, int lda, const int8_t* W, const floa
                   const float* bias, const float* add, float* C, int M, int N, int K, int ldc,
                   long long cOff, float alpha, int act, int resid, const float* gate,
                   long long gOff);
+/* The same int8 ConvRot linear on tiled operands (the fused DiT path): At is the rotated
+ * fp16 activation in the tiled layout [ceil(M/64)][K/64][8][64][8] written by the fused
+ * producers (tiled != 0), Wt the weight re-tiled by ns2_tile_i8_weight. Epilogue as above
+ * without `add`. Requires N % 64 == 0, K % 256 == 0. */
+int ns2_linear_i8_tiled(const uint16_t* At, const int8_t* Wt, const float* scale,
+                        const float* bias, float* C, int M, int N, int K, int ldc,
+                        long long cOff, float alpha, int act, int resid, const float* gate,
+                        long long gOff);
+/* Re-tile an int8 weight [N, K] row-major into Wt [N/64][K/64][4][64][16 bytes] for
+ * ns2_linear_i8_tiled, each byte stored biased as w + 128 (N % 64 == 0, K % 64 == 0).
+ * Done once when the weight is loaded. */
+int ns2_tile_i8_weight(const int8_t* W, int8_t* Wt, int N, int K);
 /* bf16 weights (gemm.js:98-118), fp32 activations [M, lda]. Requires K % 16 == 0. */
 int ns2_linear_bf16(const float* A, int lda, const uint16_t* W, const float* bias,
                     const float* add, float* C, int M, int N, int K, int ldc, long long cOff,
@@ -159,15 +173,17 @@ int ns2_head_norm(float* X, const float* w, int L, int H, int D, int ld, long lo
 int ns2_norm_mod(const float* x, const float* mod, long long shiftOff, long long scaleOff,
                  int rows, int cols, const float* weight, float eps, float* y);
 /* ns2_norm_mod followed by the ConvRot rotation, written as fp16 (cols % 256 == 0):
- * the pre-rotated input of the int8 linear that consumes it. */
+ * the pre-rotated input of the int8 linear that consumes it, row-major [rows, cols]
+ * (tiled == 0) or in the layout of ns2_linear_i8_tiled (tiled != 0). */
 int ns2_norm_mod_rotate_f16(const float* x, const float* mod, long long shiftOff,
                             long long scaleOff, int rows, int cols, const float* weight,
-                            float eps, uint16_t* y);
+                            float eps, uint16_t* y, int tiled);
 /* ops.glu + gluShader (app/gpu/ops.js:141-148, app/gpu/kernels.js:344-360):
  * y[r, j] = act(x[r, j]) * x[r, I + j] for x [rows, 2I]. */
 int ns2_glu(const float* x, float* y, int rows, int I, int act);
-/* ns2_glu followed by the ConvRot rotation, written as fp16 (I % 256 == 0). */
-int ns2_glu_rotate_f16(const float* x, uint16_t* y, int rows, int I, int act);
+/* ns2_glu followed by the ConvRot rotation, written as fp16 (I % 256 == 0), row-major or
+ * tiled as in ns2_norm_mod_rotate_f16. */
+int ns2_glu_rotate_f16(const float* x, uint16_t* y, int rows, int I, int act, int tiled);
 /* ops.elementwise (app/gpu/ops.js:179-185, kernels.js:496-518): op in NS2_EW_*;
  * b is ignored for silu/copy. */
 int ns2_elementwise(int op, const float* a, const float* b, float* y, long long n);

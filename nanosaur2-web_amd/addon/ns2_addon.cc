@@ -333,13 +333,41 @@ napi_value Hadamard256(napi_env env, napi_callback_info info) {
   return check(env, c, c.failed ? 0 : ns2_hadamard256(x, y, g));
 }
 
+// rotateF16(x, ldx, y, ldy, rows, cols, tiled)
 napi_value RotateF16(napi_env env, napi_callback_info info) {
-  ARGS(6);
+  ARGS(7);
   auto x = (const float*)c.ptr(0);
   int ldx = c.i32(1);
   auto y = (uint16_t*)c.ptr(2);
-  int ldy = c.i32(3), rows = c.i32(4), cols = c.i32(5);
-  return check(env, c, c.failed ? 0 : ns2_rotate_f16(x, ldx, y, ldy, rows, cols));
+  int ldy = c.i32(3), rows = c.i32(4), cols = c.i32(5), tiled = c.i32(6);
+  return check(env, c, c.failed ? 0 : ns2_rotate_f16(x, ldx, y, ldy, rows, cols, tiled));
+}
+
+// tileI8Weight(W, Wt, N, K)
+napi_value TileI8Weight(napi_env env, napi_callback_info info) {
+  ARGS(4);
+  auto W = (const int8_t*)c.ptr(0);
+  auto Wt = (int8_t*)c.ptr(1);
+  int N = c.i32(2), K = c.i32(3);
+  return check(env, c, c.failed ? 0 : ns2_tile_i8_weight(W, Wt, N, K));
+}
+
+// linearI8Tiled(At, Wt, scale, bias, C, M, N, K, ldc, cOff, alpha, act, resid, gate, gOff)
+napi_value LinearI8Tiled(napi_env env, napi_callback_info info) {
+  ARGS(15);
+  auto At = (const uint16_t*)c.ptr(0);
+  auto Wt = (const int8_t*)c.ptr(1);
+  auto scale = (const float*)c.ptr(2);
+  auto bias = (const float*)c.ptr(3);
+  auto C = (float*)c.ptr(4);
+  int M = c.i32(5), N = c.i32(6), K = c.i32(7), ldc = c.i32(8);
+  long long cOff = c.i64(9);
+  float alpha = c.f32(10);
+  int act = c.i32(11), resid = c.i32(12);
+  auto gate = (const float*)c.ptr(13);
+  long long gOff = c.i64(14);
+  if (c.failed) return nullptr;
+  return check(env, c, ns2_linear_i8_tiled(At, Wt, scale, bias, C, M, N, K, ldc, cOff, alpha, act, resid, gate, gOff));
 }
 
 // linearI8(A, aFmt, lda, W, scale, bias, add, C, M, N, K, ldc, cOff, alpha, act, resid, gate, gOff)
@@ -423,10 +451,11 @@ napi_value HeadNorm(napi_env env, napi_callback_info info) {
   return check(env, c, ns2_head_norm(X, w, L, H, D, ld, colOff, rowOff, cs, sinOff, eps));
 }
 
-// normMod(x, mod, shiftOff, scaleOff, rows, cols, weight, eps, y) / normModRotateF16(...)
+// normMod(x, mod, shiftOff, scaleOff, rows, cols, weight, eps, y) /
+// normModRotateF16(x, mod, shiftOff, scaleOff, rows, cols, weight, eps, y, tiled)
 template <bool ROT>
 napi_value NormModT(napi_env env, napi_callback_info info) {
-  ARGS(9);
+  ARGS(10);
   auto x = (const float*)c.ptr(0);
   auto mod = (const float*)c.ptr(1);
   long long sh = c.i64(2), sc = c.i64(3);
@@ -434,21 +463,23 @@ napi_value NormModT(napi_env env, napi_callback_info info) {
   auto w = (const float*)c.ptr(6);
   float eps = c.f32(7);
   void* y = c.ptr(8);
+  int tiled = ROT ? c.i32(9) : 0;
   if (c.failed) return nullptr;
-  int rc = ROT ? ns2_norm_mod_rotate_f16(x, mod, sh, sc, rows, cols, w, eps, (uint16_t*)y)
+  int rc = ROT ? ns2_norm_mod_rotate_f16(x, mod, sh, sc, rows, cols, w, eps, (uint16_t*)y, tiled)
                : ns2_norm_mod(x, mod, sh, sc, rows, cols, w, eps, (float*)y);
   return check(env, c, rc);
 }
 
-// glu(x, y, rows, I, act) / gluRotateF16(...)
+// glu(x, y, rows, I, act) / gluRotateF16(x, y, rows, I, act, tiled)
 template <bool ROT>
 napi_value GluT(napi_env env, napi_callback_info info) {
-  ARGS(5);
+  ARGS(6);
   auto x = (const float*)c.ptr(0);
   void* y = c.ptr(1);
   int rows = c.i32(2), I = c.i32(3), act = c.i32(4);
+  int tiled = ROT ? c.i32(5) : 0;
   if (c.failed) return nullptr;
-  int rc = ROT ? ns2_glu_rotate_f16(x, (uint16_t*)y, rows, I, act) : ns2_glu(x, (float*)y, rows, I, act);
+  int rc = ROT ? ns2_glu_rotate_f16(x, (uint16_t*)y, rows, I, act, tiled) : ns2_glu(x, (float*)y, rows, I, act);
   return check(env, c, rc);
 }
 
@@ -508,6 +539,7 @@ napi_value Module(napi_env env, napi_value exports) {
       {"eventCreate", EventCreate}, {"eventRecord", EventRecord}, {"eventElapsed", EventElapsed},
       {"eventDestroy", EventDestroy}, {"profileEnable", ProfileEnable}, {"profileReset", ProfileReset},
       {"profileReport", ProfileReport}, {"hadamard256", Hadamard256}, {"rotateF16", RotateF16},
+      {"tileI8Weight", TileI8Weight}, {"linearI8Tiled", LinearI8Tiled},
       {"linearI8", LinearI8}, {"linearBf16", LinearBf16}, {"attention", Attention},
       {"headNorm", HeadNorm}, {"normMod", NormModT<false>}, {"normModRotateF16", NormModT<true>},
       {"glu", GluT<false>}, {"gluRotateF16", GluT<true>}, {"elementwise", Elementwise},

@@ -131,4 +131,33 @@ __device__ __forceinline__ uint32_t pack_half2(float a, float b) {
   return __builtin_bit_cast(uint32_t, h);
 }
 
+// LDS byte address of a pointer into a __shared__ array, as a wave-uniform value.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return __builtin_amdgcn_readfirstlane(
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const char*)p)));
+}
+
+// Direct global->LDS copy of 16 bytes per lane: lane l's bytes land at LDS address
+// lds + 16 * l. Issued as inline assembly so that the compiler tracks neither the LDS
+// write nor the load counter (it would otherwise wait for every outstanding copy before
+// any LDS read): the caller waits with vm_wait<n>() and a barrier before reading the data.
+// M0 carries the LDS base; no other code in the kernels that use this sets M0. An LDS DMA
+// that reads M0 needs one wait state after the SALU write of M0 (the compiler's hazard
+// rule for this generation, which it cannot apply inside an asm statement): s_nop 0.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(const void* src, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// Wait until at most N vector-memory loads of this wave are outstanding (loads complete in
+// issue order, so every older one has landed).
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
 }  // namespace ns2dev

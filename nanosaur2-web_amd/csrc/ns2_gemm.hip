@@ -364,7 +364,7 @@ int ns2_linear_i8(const void* A, int a_fmt, int lda, const int8_t* W, const floa
     uint16_t* xr = static_cast<uint16_t*>(ns2::workspace(0, (size_t)M * K * sizeof(uint16_t)));
     if (!xr) return ns2::set_error(NS2_ERR_OOM, "ns2_linear_i8: workspace allocation failed");
     if (a_fmt == 0) {
-      int rc = ns2_rotate_f16(static_cast<const float*>(A), lda, xr, K, M, K);
+      int rc = ns2_rotate_f16(static_cast<const float*>(A), lda, xr, K, M, K, 0);
       if (rc) return rc;
     } else {
       const long long quads = (long long)M * K / 4;

@@ -1,0 +1,355 @@
+// int8 ConvRot linear on tiled operands: the DiT's fast path.
+//
+// Operand layouts (16-byte chunks; each 64x64 tile image is what one LDS stage holds per
+// 64-row block):
+//   A (rotated fp16 activations), written by the producing row kernel:
+//     At[ceil(M/64)][K/64][8 k-chunks][64 rows][8 halfs]       (8 KB per 64x64 tile)
+//   W (int8 ConvRot weights), re-tiled once after upload (ns2_tile_i8_weight), each byte
+//   stored biased as u = w + 128:
+//     Wt[N/64][K/64][4 k-chunks][64 rows][16 bytes]           (4 KB per 64x64 tile)
+// Tiles move into LDS as 1 KB blocks with direct global->LDS copies (no registers, no LDS
+// stores) into a three-stage ring, and the MFMA fragment reads are conflict-free: the 32
+// lanes of a half-wave read 32 consecutive 16-byte (A) or 8-of-16-byte (W) rows. The int8
+// weights are decoded to fp16 as they are read from LDS into the MFMA B operand (exact:
+// half(0x6400 | u) - 1152 = w for |w| <= 128), and the per-output-row scale is applied in
+// the epilogue, in the reference's order (app/gpu/gemm.js:159-164).
+#include "ns2_common.h"
+
+using namespace ns2dev;
+
+namespace {
+
+struct TGemmArgs {
+  const half_t* At;
+  const uint8_t* Wt;
+  const float* scale;
+  const float* bias;
+  float* C;
+  const float* gate;
+  long long cOff, gOff;
+  int M, N, K, ldc;
+  int mblocks, nblocks;  // 64-row blocks of A (rounded up) and W
+  int tiles_m, tiles_n;  // block tiles
+  float alpha;
+  int act, resid;
+};
+
+// 8 biased bytes (two dwords) -> 8 halfs: byte u -> half(0x6400 | u) - 1152 = u - 128 = w.
+// v_perm picks bytes of {x, 0x64646464}: selector bytes 4..7 are x's bytes, 0 is 0x64.
+__device__ __forceinline__ half8_t u8x8_to_h8(uint2 w) {
+  const half2_t off = {(half_t)1152.0f, (half_t)1152.0f};
+  half8_t r;
+  const uint32_t ws[2] = {w.x, w.y};
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const uint32_t lo = __builtin_amdgcn_perm(ws[i], 0x64646464u, 0x00050004u);
+    const uint32_t hi = __builtin_amdgcn_perm(ws[i], 0x64646464u, 0x00070006u);
+    const half2_t l = __builtin_bit_cast(half2_t, lo) - off;
+    const half2_t h = __builtin_bit_cast(half2_t, hi) - off;
+    r[4 * i + 0] = l[0];
+    r[4 * i + 1] = l[1];
+    r[4 * i + 2] = h[0];
+    r[4 * i + 3] = h[1];
+  }
+  return r;
+}
+
+__device__ __forceinline__ void epilogue(const TGemmArgs& p, int m, int n, float acc, float rs, float bi, float gt) {
+  float r = acc * p.alpha;
+  r *= rs;
+  r += bi;
+  r = apply_act(r, p.act);
+  float* c = p.C + p.cOff + (long long)m * p.ldc + n;
+  if (!p.resid) *c = r;
+  else if (!p.gate) *c = *c + r;
+  else *c = *c + gt * r;
+}
+
+// Block tile BM x BN (multiples of 64), BK = 64; WAVES_M x WAVES_N waves, each computing
+// (BM/WAVES_M) x (BN/WAVES_N) with v_mfma_f32_32x32x16_f16 tiles. Three LDS stages, one
+// barrier per k-tile: tile kt+2 is copied in while tile kt is multiplied, and the wait before
+// the barrier leaves tile kt+1's copies in flight.
+template <int BM, int BN, int WAVES_M, int WAVES_N, bool PIPE, int STAGES>
+__global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void gemm_tiled_kernel(TGemmArgs p) {
+  constexpr int NW = WAVES_M * WAVES_N;
+  constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
+  constexpr int TM = WTM / 32, TN = WTN / 32;
+  constexpr int A_BLOCKS = BM / 64 * 8, W_BLOCKS = BN / 64 * 4;  // 1 KB blocks per stage
+  constexpr int BLOCKS = A_BLOCKS + W_BLOCKS;
+  constexpr int PER_WAVE = BLOCKS / NW;
+  static_assert(BM % 64 == 0 && BN % 64 == 0 && WTM % 32 == 0 && WTN % 32 == 0, "tile shape");
+  static_assert(BLOCKS % NW == 0, "copies must split evenly over the waves");
+
+  static_assert(STAGES == 2 || STAGES == 3, "two or three LDS stages");
+  __shared__ __attribute__((aligned(16))) half_t as[STAGES][BM * 64];
+  __shared__ __attribute__((aligned(16))) uint8_t ws[STAGES][BN * 64];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+  const int lq = lane & 31, hi = lane >> 5;
+
+  // XCD-aware tile order: consecutive block ids go to different XCDs (round-robin dispatch);
+  // block i is given tile start(x) + i/8 of XCD x = i % 8, where XCD x owns the contiguous
+  // range of T/8 (+1 for the first T%8 XCDs) tiles, so neighbouring tiles (sharing A rows and
+  // W columns) run on the same XCD and meet in its L2.
+  const int tiles = p.tiles_m * p.tiles_n;
+  int tile;
+  {
+    const int x = blockIdx.x % 8, local = blockIdx.x / 8;
+    const int q = tiles / 8, rmd = tiles % 8;
+    tile = x * q + (x < rmd ? x : rmd) + local;
+  }
+  // tiles are walked with N fastest inside groups of 4 row-tiles (A reuse in L2)
+  const int group = 4;
+  const int gsize = group * p.tiles_n;
+  const int g = tile / gsize, rem = tile % gsize;
+  const int rows_in_g = (p.tiles_m - g * group) < group ? (p.tiles_m - g * group) : group;
+  const int tm = g * group + rem % rows_in_g, tn = rem / rows_in_g;
+  const int m0 = tm * BM, n0 = tn * BN;
+
+  const int kblocks = p.K / 64;
+  const uint32_t as_base = lds_addr(as), ws_base = lds_addr(ws);
+  // Stage image: A blocks (8 k-chunks of 1 KB per 64-row block), then W blocks (4 per block).
+  // Block ids past the last real 64-row block re-read the last one (their rows are dropped).
+  auto dma = [&](int kt, int st) {
+#pragma unroll
+    for (int i = 0; i < PER_WAVE; ++i) {
+      const int j = wave + i * NW;
+      const char* src;
+      uint32_t dst;
+      if (j < A_BLOCKS) {
+        const int mbi = j / 8, c = j % 8;
+        int mb = m0 / 64 + mbi;
+        mb = mb < p.mblocks ? mb : p.mblocks - 1;
+        src = reinterpret_cast<const char*>(p.At) + (((long long)mb * kblocks + kt) * 8 + c) * 1024;
+        dst = as_base + st * (BM * 64 * 2) + j * 1024;
+      } else {
+        const int jw = j - A_BLOCKS;
+        const int nbi = jw / 4, c = jw % 4;
+        int nb = n0 / 64 + nbi;
+        nb = nb < p.nblocks ? nb : p.nblocks - 1;
+        src = reinterpret_cast<const char*>(p.Wt) + (((long long)nb * kblocks + kt) * 4 + c) * 1024;
+        dst = ws_base + st * (BN * 64) + jw * 1024;
+      }
+      dma16(src + lane * 16, __builtin_amdgcn_readfirstlane(dst));
+    }
+  };
+
+  float16_t acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  dma(0, 0);
+  if (STAGES == 3 && kblocks > 1) dma(1, 1);
+
+  for (int kt = 0; kt < kblocks; ++kt) {
+    const int st = kt % STAGES;
+    // this wave's copies of tile kt have landed once at most tile kt+1's remain in flight
+    // (three stages); the barrier then covers every wave's copies, and every wave's reads of
+    // tile kt-1, whose stage the next copies overwrite
+    if (STAGES == 3 && kt + 1 < kblocks) vm_wait<PER_WAVE>();
+    else vm_wait<0>();
+    __syncthreads();
+    if (kt + STAGES - 1 < kblocks) dma(kt + STAGES - 1, (kt + STAGES - 1) % STAGES);
+    __builtin_amdgcn_s_setprio(1);
+    if constexpr (PIPE) {
+      // k-steps of 16, software-pipelined inside the k-tile: fragments are read from LDS two
+      // steps ahead and the weights decoded one step ahead, interleaved with the MFMAs.
+      half8_t a[3][TM];
+      uint2 w[3][TN];
+      half8_t b[2][TN];
+      auto read = [&](int s, int slot) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+          const int row = wm * WTM + 32 * i;
+          const int mbi = row / 64, r0 = row % 64;
+          a[slot][i] = *reinterpret_cast<const half8_t*>(&as[st][((mbi * 8 + 2 * s + hi) * 64 + r0 + lq) * 8]);
+        }
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          const int col = wn * WTN + 32 * j;
+          const int nbi = col / 64, c0 = col % 64;
+          w[slot][j] = *reinterpret_cast<const uint2*>(&ws[st][((nbi * 4 + s) * 64 + c0 + lq) * 16 + 8 * hi]);
+        }
+      };
+      read(0, 0);
+      read(1, 1);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) b[0][j] = u8x8_to_h8(w[0][j]);
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        if (s + 2 < 4) read(s + 2, (s + 2) % 3);
+        if (s + 1 < 4) {
+#pragma unroll
+          for (int j = 0; j < TN; ++j) b[(s + 1) & 1][j] = u8x8_to_h8(w[(s + 1) % 3][j]);
+        }
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[s % 3][i], b[s & 1][j], acc[i][j], 0, 0, 0);
+        // per MFMA: one LDS read and a share of the decode VALU work
+        constexpr int NMF = TM * TN, NRD = TM + TN, NVALU = TN * 8;
+#pragma unroll
+        for (int q = 0; q < NMF; ++q) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                       // MFMA
+          if (q < NRD && s + 2 < 4) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+          if (s + 1 < 4) __builtin_amdgcn_sched_group_barrier(0x002, (NVALU + NMF - 1) / NMF, 0);  // VALU
+        }
+      }
+    } else {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {  // k-steps of 16
+      half8_t a[TM], b[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int row = wm * WTM + 32 * i;  // within the block tile
+        const int mbi = row / 64, r0 = row % 64;
+        a[i] = *reinterpret_cast<const half8_t*>(&as[st][((mbi * 8 + 2 * s + hi) * 64 + r0 + lq) * 8]);
+      }
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int col = wn * WTN + 32 * j;
+        const int nbi = col / 64, c0 = col % 64;
+        const uint2 w8 = *reinterpret_cast<const uint2*>(&ws[st][((nbi * 4 + s) * 64 + c0 + lq) * 16 + 8 * hi]);
+        b[j] = u8x8_to_h8(w8);
+      }
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+    }
+    }
+    __builtin_amdgcn_s_setprio(0);
+  }
+
+  // epilogue: acc[i][j][r] = C[m0 + wm*WTM + 32i + 8(r/4) + 4hi + r%4][n0 + wn*WTN + 32j + lq]
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int n = n0 + wn * WTN + 32 * j + lq;
+    if (n >= p.N) continue;
+    const float rs = p.scale[n];
+    const float bi = p.bias ? p.bias[n] : 0.0f;
+    const float gt = p.gate ? p.gate[p.gOff + n] : 1.0f;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = m0 + wm * WTM + 32 * i + 8 * (r >> 2) + 4 * hi + (r & 3);
+        if (m < p.M) epilogue(p, m, n, acc[i][j][r], rs, bi, gt);
+      }
+  }
+}
+
+// W [N, K] row-major int8 -> Wt tiles of biased bytes (w + 128); one thread per 16-byte chunk.
+__global__ __launch_bounds__(256) void tile_w_kernel(const int8_t* __restrict__ W, uint8_t* __restrict__ Wt,
+                                                      int N, int K) {
+  const long long i = (long long)blockIdx.x * 256 + threadIdx.x;  // output chunk index
+  const long long chunks = (long long)N * K / 16;
+  if (i >= chunks) return;
+  // chunk order: [nb][kb][c 0..3][row 0..63]
+  const int row = (int)(i % 64);
+  const int c = (int)((i / 64) % 4);
+  const long long rest = i / 256;  // nb * (K/64) + kb
+  const int kb = (int)(rest % (K / 64));
+  const int nb = (int)(rest / (K / 64));
+  const int n = nb * 64 + row, kc = kb * 4 + c;
+  uint4 v = *reinterpret_cast<const uint4*>(W + (long long)n * K + kc * 16);
+  v.x ^= 0x80808080u;
+  v.y ^= 0x80808080u;
+  v.z ^= 0x80808080u;
+  v.w ^= 0x80808080u;
+  *reinterpret_cast<uint4*>(Wt + i * 16) = v;
+}
+
+template <int BM, int BN, int WM, int WN, bool PIPE = false, int STAGES = 3>
+int launch_tiled(TGemmArgs p) {
+  p.tiles_m = (p.M + BM - 1) / BM;
+  p.tiles_n = (p.N + BN - 1) / BN;
+  gemm_tiled_kernel<BM, BN, WM, WN, PIPE, STAGES><<<p.tiles_m * p.tiles_n, WM * WN * 64, 0, ns2::stream()>>>(p);
+  NS2_LAUNCHED("gemm_tiled");
+  return NS2_OK;
+}
+
+// Block-tile configurations: BM x BN, blocks resident per CU (LDS-bound), and relative
+// per-CU throughput of one resident tile set (larger tiles re-read less from LDS and L2).
+struct TileCfg {
+  int bm, bn, per_cu;
+  float rate;
+};
+constexpr TileCfg kCfgs[] = {
+    {256, 256, 1, 1.00f},  // 8 waves of 128x64, 144 KB LDS
+    {192, 192, 1, 0.97f},  // 4 waves of 96x96, 108 KB
+    {192, 128, 1, 0.93f},  // 4 waves of 96x64, 96 KB
+    {128, 128, 2, 0.85f},  // 4 waves of 64x64, 72 KB
+    {64, 128, 3, 0.60f},   // 4 waves of 64x32, 48 KB: small M
+};
+constexpr int kCUs = 256;
+
+// Estimated time of a configuration: rounds of resident tile sets times the work of a set
+// divided by its rate. The configuration with the least estimate is used.
+int pick_config(int M, int N) {
+  int best = -1;
+  double best_t = 0;
+  for (int i = 0; i < (int)(sizeof(kCfgs) / sizeof(kCfgs[0])); ++i) {
+    const TileCfg& c = kCfgs[i];
+    const long long tiles = (long long)((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn);
+    const long long slots = (long long)kCUs * c.per_cu;
+    const long long rounds = (tiles + slots - 1) / slots;
+    const double t = (double)rounds * c.per_cu * c.bm * c.bn / c.rate;
+    if (best < 0 || t < best_t) {
+      best = i;
+      best_t = t;
+    }
+  }
+  return best;
+}
+
+inline bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+}  // namespace
+
+extern "C" {
+
+int ns2_tile_i8_weight(const int8_t* W, int8_t* Wt, int N, int K) {
+  NS2_READY();
+  NS2_REQUIRE(W && Wt && aligned16(W) && aligned16(Wt), "ns2_tile_i8_weight: null or unaligned buffer");
+  NS2_REQUIRE(N > 0 && K > 0 && N % 64 == 0 && K % 64 == 0,
+              "ns2_tile_i8_weight: N=%d and K=%d must be multiples of 64", N, K);
+  const long long chunks = (long long)N * K / 16;
+  ns2::ProfScope prof_("tile_i8_weight");
+  tile_w_kernel<<<(unsigned)((chunks + 255) / 256), 256, 0, ns2::stream()>>>(W, reinterpret_cast<uint8_t*>(Wt), N, K);
+  NS2_LAUNCHED("tile_i8_weight");
+  return NS2_OK;
+}
+
+int ns2_linear_i8_tiled(const uint16_t* At, const int8_t* Wt, const float* scale, const float* bias,
+                        float* C, int M, int N, int K, int ldc, long long cOff, float alpha, int act,
+                        int resid, const float* gate, long long gOff) {
+  NS2_READY();
+  if (M == 0) return NS2_OK;
+  NS2_REQUIRE(At && Wt && scale && C, "ns2_linear_i8_tiled: null At, Wt, scale or C");
+  NS2_REQUIRE(M > 0 && N > 0 && N % 64 == 0 && K > 0 && K % 256 == 0,
+              "ns2_linear_i8_tiled: M=%d N=%d K=%d (N %% 64 == 0, K %% 256 == 0 required)", M, N, K);
+  NS2_REQUIRE(ldc >= N && cOff >= 0 && gOff >= 0, "ns2_linear_i8_tiled: bad ldc/offsets");
+  NS2_REQUIRE(aligned16(At) && aligned16(Wt), "ns2_linear_i8_tiled: operands must be 16-byte aligned");
+  NS2_REQUIRE(act >= NS2_ACT_NONE && act <= NS2_ACT_GELU_TANH, "ns2_linear_i8_tiled: unknown act %d", act);
+  TGemmArgs p{reinterpret_cast<const half_t*>(At), reinterpret_cast<const uint8_t*>(Wt), scale, bias, C, gate,
+              cOff, gOff, M, N, K, ldc, (M + 63) / 64, N / 64, 0, 0, alpha, act, resid};
+  ns2::ProfScope prof_("gemm_i8_tiled");
+  switch (pick_config(M, N)) {
+    case 0: return launch_tiled<256, 256, 2, 4>(p);
+    case 1: return launch_tiled<192, 192, 2, 2>(p);
+    case 2: return launch_tiled<192, 128, 2, 2>(p);
+    case 3: return launch_tiled<128, 128, 2, 2>(p);
+    default: return launch_tiled<64, 128, 1, 4>(p);
+  }
+}
+
+}  // extern "C"

@@ -20,6 +20,22 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
   return t;
 }
 
+// Offset (in halfs) of element (m, k) of an fp16 GEMM operand with K columns in the tiled
+// layout of the int8 GEMM: [M/64][K/64][8 k-chunks][64 rows][8 halfs] (ns2_linear_i8_tiled).
+__device__ __forceinline__ long long tiled_off(long long m, int k, int K) {
+  return (((m >> 6) * (K >> 6) + (k >> 6)) * 8 + ((k & 63) >> 3)) * 512 + (m & 63) * 8 + (k & 7);
+}
+
+// Store 4 consecutive rotated values (k..k+3, k % 4 == 0) as fp16, row-major or tiled.
+__device__ __forceinline__ void store4_f16(uint16_t* __restrict__ y, long long m, int k, int ldy, int K,
+                                           int tiled, const float v[4]) {
+  uint2 o;
+  o.x = pack_half2(v[0], v[1]);
+  o.y = pack_half2(v[2], v[3]);
+  const long long off = tiled ? tiled_off(m, k, K) : m * ldy + k;
+  *reinterpret_cast<uint2*>(y + off) = o;
+}
+
 // ---- rotation ------------------------------------------------------------------------------
 
 // y = x H per contiguous 256-group (kernels.js:378-407). One wave per group.
@@ -38,7 +54,7 @@ __global__ __launch_bounds__(256) void hadamard256_kernel(const float* __restric
 // Strided [rows, cols] fp32 -> rotated fp16. One wave per 256-group.
 __global__ __launch_bounds__(256) void rotate_f16_kernel(const float* __restrict__ x, int ldx,
                                                           uint16_t* __restrict__ y, int ldy,
-                                                          int rows, int gpr) {
+                                                          int rows, int gpr, int tiled) {
   long long g = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (g >= (long long)rows * gpr) return;
   const int r = (int)(g / gpr), c = (int)(g % gpr) * 256;
@@ -46,10 +62,7 @@ __global__ __launch_bounds__(256) void rotate_f16_kernel(const float* __restrict
   const float4 in = *reinterpret_cast<const float4*>(x + (long long)r * ldx + c + lane * 4);
   float v[4] = {in.x, in.y, in.z, in.w};
   fwht256_wave(v);
-  uint2 o;
-  o.x = pack_half2(v[0], v[1]);
-  o.y = pack_half2(v[2], v[3]);
-  *reinterpret_cast<uint2*>(y + (long long)r * ldy + c + lane * 4) = o;
+  store4_f16(y, r, c + lane * 4, ldy, gpr * 256, tiled, v);
 }
 
 // ---- normMod ----------------------------------------------------------------------------
@@ -88,7 +101,7 @@ __global__ __launch_bounds__(1024) void norm_mod_rot_kernel(const float* __restr
                                                              long long scaleOff, int cols,
                                                              const float* __restrict__ w,
                                                              float eps,
-                                                             uint16_t* __restrict__ y) {
+                                                             uint16_t* __restrict__ y, int tiled) {
   __shared__ float red[16];
   const long long base = (long long)blockIdx.x * cols;
   const int c = threadIdx.x * 4;  // blockDim.x * 4 == cols
@@ -112,10 +125,7 @@ __global__ __launch_bounds__(1024) void norm_mod_rot_kernel(const float* __restr
   v[2] = v[2] * r * ww.z * (1.0f + sc.z) + sh.z;
   v[3] = v[3] * r * ww.w * (1.0f + sc.w) + sh.w;
   fwht256_wave(v);
-  uint2 o;
-  o.x = pack_half2(v[0], v[1]);
-  o.y = pack_half2(v[2], v[3]);
-  *reinterpret_cast<uint2*>(y + base + c) = o;
+  store4_f16(y, blockIdx.x, c, cols, cols, tiled, v);
 }
 
 // ---- headNorm -------------------------------------------------------------------------------
@@ -165,7 +175,7 @@ __global__ __launch_bounds__(256) void glu_kernel(const float* __restrict__ x,
 // GLU + rotation + fp16: one wave per 256 output columns.
 __global__ __launch_bounds__(256) void glu_rot_kernel(const float* __restrict__ x,
                                                        uint16_t* __restrict__ y, int rows,
-                                                       int I, int act) {
+                                                       int I, int act, int tiled) {
   const int gpr = I / 256;
   long long g = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (g >= (long long)rows * gpr) return;
@@ -177,10 +187,7 @@ __global__ __launch_bounds__(256) void glu_rot_kernel(const float* __restrict__ 
   float v[4] = {apply_act(a.x, act) * b.x, apply_act(a.y, act) * b.y,
                 apply_act(a.z, act) * b.z, apply_act(a.w, act) * b.w};
   fwht256_wave(v);
-  uint2 o;
-  o.x = pack_half2(v[0], v[1]);
-  o.y = pack_half2(v[2], v[3]);
-  *reinterpret_cast<uint2*>(y + r * I + c) = o;
+  store4_f16(y, r, c, I, I, tiled, v);
 }
 
 // ---- elementwise / accumulate / rowSum / RMSNorm ---------------------------------------------
@@ -247,16 +254,16 @@ int ns2_hadamard256(const float* x, float* y, long long groups) {
   return NS2_OK;
 }
 
-int ns2_rotate_f16(const float* x, int ldx, uint16_t* y, int ldy, int rows, int cols) {
+int ns2_rotate_f16(const float* x, int ldx, uint16_t* y, int ldy, int rows, int cols, int tiled) {
   NS2_READY();
   if (rows <= 0) return NS2_OK;
   NS2_REQUIRE(cols > 0 && cols % 256 == 0, "ns2_rotate_f16: cols=%d must be a multiple of 256", cols);
-  NS2_REQUIRE(ldx % 4 == 0 && ldy % 4 == 0 && ldx >= cols && ldy >= cols,
+  NS2_REQUIRE(ldx % 4 == 0 && ldx >= cols && (tiled || (ldy % 4 == 0 && ldy >= cols)),
               "ns2_rotate_f16: ldx=%d ldy=%d must be multiples of 4 and >= cols", ldx, ldy);
   NS2_REQUIRE(x && y && aligned16(x) && aligned8(y), "ns2_rotate_f16: null or unaligned buffer");
   const int gpr = cols / 256;
   ns2::ProfScope prof_("rotate_f16");
-  rotate_f16_kernel<<<blocks_for((long long)rows * gpr, 4), 256, 0, ns2::stream()>>>(x, ldx, y, ldy, rows, gpr);
+  rotate_f16_kernel<<<blocks_for((long long)rows * gpr, 4), 256, 0, ns2::stream()>>>(x, ldx, y, ldy, rows, gpr, tiled);
   NS2_LAUNCHED("rotate_f16");
   return NS2_OK;
 }
@@ -274,7 +281,7 @@ int ns2_norm_mod(const float* x, const float* mod, long long shiftOff, long long
 
 int ns2_norm_mod_rotate_f16(const float* x, const float* mod, long long shiftOff,
                             long long scaleOff, int rows, int cols, const float* weight,
-                            float eps, uint16_t* y) {
+                            float eps, uint16_t* y, int tiled) {
   NS2_READY();
   if (rows <= 0) return NS2_OK;
   NS2_REQUIRE(cols % 256 == 0 && cols >= 256 && cols <= 4096,
@@ -283,7 +290,7 @@ int ns2_norm_mod_rotate_f16(const float* x, const float* mod, long long shiftOff
                   aligned16(mod) && (!weight || aligned16(weight)),
               "ns2_norm_mod_rotate_f16: null or unaligned buffer/offset");
   ns2::ProfScope prof_("norm_mod_rotate_f16");
-  norm_mod_rot_kernel<<<rows, cols / 4, 0, ns2::stream()>>>(x, mod, shiftOff, scaleOff, cols, weight, eps, y);
+  norm_mod_rot_kernel<<<rows, cols / 4, 0, ns2::stream()>>>(x, mod, shiftOff, scaleOff, cols, weight, eps, y, tiled);
   NS2_LAUNCHED("norm_mod_rotate_f16");
   return NS2_OK;
 }
@@ -310,14 +317,14 @@ int ns2_glu(const float* x, float* y, int rows, int I, int act) {
   return NS2_OK;
 }
 
-int ns2_glu_rotate_f16(const float* x, uint16_t* y, int rows, int I, int act) {
+int ns2_glu_rotate_f16(const float* x, uint16_t* y, int rows, int I, int act, int tiled) {
   NS2_READY();
   if (rows <= 0) return NS2_OK;
   NS2_REQUIRE(I > 0 && I % 256 == 0, "ns2_glu_rotate_f16: I=%d must be a multiple of 256", I);
   NS2_REQUIRE(x && y && aligned16(x) && aligned8(y), "ns2_glu_rotate_f16: null or unaligned buffer");
   const long long groups = (long long)rows * (I / 256);
   ns2::ProfScope prof_("glu_rotate_f16");
-  glu_rot_kernel<<<blocks_for(groups, 4), 256, 0, ns2::stream()>>>(x, y, rows, I, act);
+  glu_rot_kernel<<<blocks_for(groups, 4), 256, 0, ns2::stream()>>>(x, y, rows, I, act, tiled);
   NS2_LAUNCHED("glu_rotate_f16");
   return NS2_OK;
 }

@@ -74,6 +74,12 @@ export class Nanosaur2DiT {
     }
     m.finalAda = await lin("final_layer.adaLN_modulation.");
     m.finalLinear = await lin("final_layer.linear.");
+    if (fused) {
+      // the fused producers feed the block linears tiled operands: re-tile their weights once
+      for (const b of m.text.concat(m.blocks)) {
+        for (const W of [b.qkv, b.kvY, b.proj, b.w12, b.w3]) if (W && ops.tileable(W)) ops.tileWeight(gpu, W);
+      }
+    }
     return m;
   }
 
@@ -140,10 +146,10 @@ export class Nanosaur2DiT {
   mlp(x, b, mod) {
     const gpu = this.gpu;
     if (this.fused) {
-      const nr = ops.normModRotated(gpu, x, mod, 3 * D, 4 * D, D, b.n2);
+      const nr = ops.normModRotated(gpu, x, mod, 3 * D, 4 * D, D, b.n2, 1e-6, !!b.w12.tbuf);
       const h = ops.linear(gpu, null, b.w12, { xr: nr, name: "dit.mlp.w12" });
       nr.release();
-      const gr = ops.gluRotated(gpu, h, "silu");
+      const gr = ops.gluRotated(gpu, h, "silu", !!b.w3.tbuf);
       h.release();
       ops.linear(gpu, null, b.w3, { xr: gr, out: x, resid: true, gate: mod, gOff: 5 * D, name: "dit.mlp.w3" });
       gr.release();
@@ -158,11 +164,23 @@ export class Nanosaur2DiT {
     g.release();
   }
 
+  // x += gate_msa * proj(a); fused: a is rotated into the tiled operand of the int8 GEMM
+  projAdd(x, a, W, mod, name) {
+    const gpu = this.gpu;
+    if (this.fused && W.tbuf) {
+      const ar = ops.rotateHalf(gpu, a, D, true);
+      ops.linear(gpu, null, W, { xr: ar, out: x, resid: true, gate: mod, gOff: 2 * D, name });
+      ar.release();
+      return;
+    }
+    ops.linear(gpu, a, W, { out: x, resid: true, gate: mod, gOff: 2 * D, name });
+  }
+
   // qkv projection of modulate(norm1(x)) into rows [0, L) of qkv
   qkvProj(x, mod, b, qkv, name) {
     const gpu = this.gpu;
     if (this.fused) {
-      const nr = ops.normModRotated(gpu, x, mod, 0, D, D, b.n1);
+      const nr = ops.normModRotated(gpu, x, mod, 0, D, D, b.n1, 1e-6, !!b.qkv.tbuf);
       ops.linear(gpu, null, b.qkv, { xr: nr, out: qkv, name });
       nr.release();
       return;
@@ -183,7 +201,7 @@ export class Nanosaur2DiT {
       this.qkvProj(txt, mod, b, qkv, "dit.text.qkv");
       const a = this.attend(qkv, L, L, b);
       qkv.release();
-      ops.linear(gpu, a, b.proj, { out: txt, resid: true, gate: mod, gOff: 2 * D, name: "dit.text.proj" });
+      this.projAdd(txt, a, b.proj, mod, "dit.text.proj");
       a.release();
       this.mlp(txt, b, mod);
       mod.release();
@@ -209,7 +227,8 @@ export class Nanosaur2DiT {
       txt = this.refineText(text, tc);
       // the int8 kv_y projections take rotated inputs: rotate the text once for all blocks
       if (this.blocks.some((b) => b.kvY && ops.needsRotation(b.kvY))) {
-        txtR = this.fused ? ops.rotateHalf(gpu, txt) : ops.rotate(gpu, txt);
+        const tiled = this.blocks.every((b) => !b.kvY || b.kvY.tbuf);
+        txtR = this.fused ? ops.rotateHalf(gpu, txt, D, tiled) : ops.rotate(gpu, txt);
       }
       const pooled = ops.rowSum(gpu, txt, text.pool, text.poolScale);
       ops.linear(gpu, pooled, this.yPool, { out: t, resid: true, name: "dit.y_pool" });
@@ -244,7 +263,7 @@ export class Nanosaur2DiT {
     }
     const a = this.attend(qkv, L, Lk, b, { cs, textRows: cross ? text.L : 0, bias: cross ? text.bias : null });
     qkv.release();
-    ops.linear(gpu, a, b.proj, { out: x, resid: true, gate: mod, gOff: 2 * D, name: "dit.proj" });
+    this.projAdd(x, a, b.proj, mod, "dit.proj");
     a.release();
     this.mlp(x, b, mod);
     mod.release();

@@ -2,9 +2,11 @@
 // through the ns2 addon. Activations are fp32 Tensors (row-major); offsets and strides are in
 // elements. Three fused producers are added for the int8 layers: normModRotated,
 // gluRotated and rotateHalf write the rotated fp16 operand that linear() takes as opts.xr,
-// so the separate rotation pass of the reference never runs on the DiT path.
+// so the separate rotation pass of the reference never runs on the DiT path. With
+// tiled = true they write it in the tiled layout of the fast int8 GEMM (rows padded to a
+// multiple of 64), which linear() then multiplies with the weight re-tiled by tileWeight().
 
-import { addr } from "./device.js";
+import { addr, DeviceBuffer } from "./device.js";
 import { native, ACT, EW } from "./native.js";
 
 const opt = (v, d) => (v === undefined || v === null ? d : v);
@@ -20,12 +22,36 @@ export function rotate(gpu, x) {
   return y;
 }
 
-// Rotation written as the fp16 GEMM operand ([rows, cols], cols % 256 == 0).
-export function rotateHalf(gpu, x, cols = x.shape[x.shape.length - 1]) {
-  const rows = x.size / cols;
-  const y = gpu.empty([rows, cols], "f16");
-  gpu.run("rotate_f16", 0, () => native.rotateF16(addr(x), cols, addr(y), cols, rows, cols));
+// fp16 GEMM operand [rows, cols]: row-major, or tiled (tile images of 64 rows x 64 columns,
+// rows padded to a multiple of 64; y.rows keeps the real count).
+function rotatedOperand(gpu, rows, cols, tiled) {
+  const y = gpu.empty([tiled ? Math.ceil(rows / 64) * 64 : rows, cols], "f16");
+  if (tiled) {
+    y.tiled = true;
+    y.rows = rows;
+  }
   return y;
+}
+
+// Rotation written as the fp16 GEMM operand ([rows, cols], cols % 256 == 0).
+export function rotateHalf(gpu, x, cols = x.shape[x.shape.length - 1], tiled = false) {
+  const rows = x.size / cols;
+  const y = rotatedOperand(gpu, rows, cols, tiled);
+  gpu.run("rotate_f16", 0, () => native.rotateF16(addr(x), cols, addr(y), cols, rows, cols, tiled ? 1 : 0));
+  return y;
+}
+
+// Whether an int8 weight can take tiled operands (N % 64 == 0, K % 256 == 0).
+export const tileable = (W) => W.kind === "i8" && W.N % 64 === 0 && W.K % 256 === 0;
+
+// Re-tile an int8 weight for tiled operands (W.tbuf, kept next to the row-major W.buf).
+export function tileWeight(gpu, W) {
+  if (!tileable(W)) throw new Error(`${W.name}: [${W.N}, ${W.K}] int8 weight cannot be tiled`);
+  if (W.tbuf) return W;
+  const ptr = native.malloc(W.N * W.K);
+  W.tbuf = new DeviceBuffer(ptr, W.N * W.K, false);
+  gpu.run("tile_i8_weight", 0, () => native.tileI8Weight(addr(W.buf), addr(W.tbuf), W.N, W.K));
+  return W;
 }
 
 // y = x @ W^T (+ bias) (act) (app/gpu/ops.js:46-66). opts: out, resid, gate, gOff, ldc, cOff,
@@ -33,7 +59,7 @@ export function rotateHalf(gpu, x, cols = x.shape[x.shape.length - 1]) {
 // producer), name. x may be null when xr is given.
 export function linear(gpu, x, W, opts = {}) {
   const src = opts.xr || x;
-  const M = src.size / W.K;
+  const M = src.tiled ? src.rows : src.size / W.K;
   if (W.lora && W.lora.length) throw new Error(`${W.name}: LoRA side paths are not part of this build`);
   const out = opts.out || gpu.empty([M, W.N]);
   const ldc = opt(opts.ldc, W.N);
@@ -44,7 +70,12 @@ export function linear(gpu, x, W, opts = {}) {
   if (act === undefined) throw new Error(`linear: unknown activation ${opts.act}`);
   const resid = opts.resid ? 1 : 0;
   const flops = 2 * M * W.N * W.K;
-  if (W.kind === "i8") {
+  if (W.kind === "i8" && src.tiled) {
+    if (!W.tbuf) throw new Error(`${W.name}: a tiled operand needs the tiled weight (tileWeight)`);
+    gpu.run(opts.name || "gemm.i8", flops, () =>
+      native.linearI8Tiled(addr(src), addr(W.tbuf), addr(W.scale), addr(bias), addr(out), M, W.N, W.K, ldc,
+        cOff, 1, act, resid, addr(opts.gate), gOff));
+  } else if (W.kind === "i8") {
     const aFmt = opts.xr ? (opts.xr.dtype === "f16" ? 1 : 2) : 0;
     gpu.run(opts.name || "gemm.i8", flops, () =>
       native.linearI8(addr(src), aFmt, W.K, addr(W.buf), addr(W.scale), addr(bias), null, addr(out),
@@ -82,11 +113,12 @@ export function normMod(gpu, x, mod, shiftOff, scaleOff, cols, weight = null, ep
 }
 
 // normMod followed by the ConvRot rotation, as the fp16 operand of an int8 linear.
-export function normModRotated(gpu, x, mod, shiftOff, scaleOff, cols, weight = null, eps = 1e-6) {
+export function normModRotated(gpu, x, mod, shiftOff, scaleOff, cols, weight = null, eps = 1e-6, tiled = false) {
   const rows = x.size / cols;
-  const y = gpu.empty([rows, cols], "f16");
+  const y = rotatedOperand(gpu, rows, cols, tiled);
   gpu.run(weight ? "rmsnorm_mod_rot" : "layernorm_mod_rot", 0, () =>
-    native.normModRotateF16(addr(x), addr(mod), shiftOff, scaleOff, rows, cols, addr(weight), eps, addr(y)));
+    native.normModRotateF16(addr(x), addr(mod), shiftOff, scaleOff, rows, cols, addr(weight), eps, addr(y),
+      tiled ? 1 : 0));
   return y;
 }
 
@@ -106,10 +138,10 @@ export function glu(gpu, x, act) {
 }
 
 // glu followed by the ConvRot rotation, as the fp16 operand of an int8 linear.
-export function gluRotated(gpu, x, act) {
+export function gluRotated(gpu, x, act, tiled = false) {
   const I = x.shape[1] / 2;
-  const y = gpu.empty([x.shape[0], I], "f16");
-  gpu.run("glu_rot." + act, 0, () => native.gluRotateF16(addr(x), addr(y), x.shape[0], I, ACT[act]));
+  const y = rotatedOperand(gpu, x.shape[0], I, tiled);
+  gpu.run("glu_rot." + act, 0, () => native.gluRotateF16(addr(x), addr(y), x.shape[0], I, ACT[act], tiled ? 1 : 0));
   return y;
 }
 

@@ -46,7 +46,10 @@ SIGNATURES = {
     "ns2_profile_reset": [],
     "ns2_profile_report": [ctypes.c_char_p, c_size],
     "ns2_hadamard256": [c_vp, c_vp, c_ll],
-    "ns2_rotate_f16": [c_vp, c_int, c_vp, c_int, c_int, c_int],
+    "ns2_rotate_f16": [c_vp, c_int, c_vp, c_int, c_int, c_int, c_int],
+    "ns2_linear_i8_tiled": [c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_ll, c_float,
+                            c_int, c_int, c_vp, c_ll],
+    "ns2_tile_i8_weight": [c_vp, c_vp, c_int, c_int],
     "ns2_linear_i8": [c_vp, c_int, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int,
                       c_ll, c_float, c_int, c_int, c_vp, c_ll],
     "ns2_linear_bf16": [c_vp, c_int, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_ll,
@@ -56,9 +59,9 @@ SIGNATURES = {
                       c_ll, c_vp, c_vp, c_float, c_vp, c_ll, c_int],
     "ns2_head_norm": [c_vp, c_vp, c_int, c_int, c_int, c_int, c_ll, c_ll, c_vp, c_ll, c_float],
     "ns2_norm_mod": [c_vp, c_vp, c_ll, c_ll, c_int, c_int, c_vp, c_float, c_vp],
-    "ns2_norm_mod_rotate_f16": [c_vp, c_vp, c_ll, c_ll, c_int, c_int, c_vp, c_float, c_vp],
+    "ns2_norm_mod_rotate_f16": [c_vp, c_vp, c_ll, c_ll, c_int, c_int, c_vp, c_float, c_vp, c_int],
     "ns2_glu": [c_vp, c_vp, c_int, c_int, c_int],
-    "ns2_glu_rotate_f16": [c_vp, c_vp, c_int, c_int, c_int],
+    "ns2_glu_rotate_f16": [c_vp, c_vp, c_int, c_int, c_int, c_int],
     "ns2_elementwise": [c_int, c_vp, c_vp, c_vp, c_ll],
     "ns2_accumulate": [c_vp, c_vp, c_ll],
     "ns2_row_sum": [c_vp, c_vp, c_vp, c_int, c_int, c_float],
@@ -152,8 +155,16 @@ class Lib:
     def hadamard256(self, x, y, groups):
         self.call("ns2_hadamard256", _ptr(x), _ptr(y), groups)
 
-    def rotate_f16(self, x, ldx, y, ldy, rows, cols):
-        self.call("ns2_rotate_f16", _ptr(x), ldx, _ptr(y), ldy, rows, cols)
+    def rotate_f16(self, x, ldx, y, ldy, rows, cols, tiled=False):
+        self.call("ns2_rotate_f16", _ptr(x), ldx, _ptr(y), ldy, rows, cols, int(tiled))
+
+    def tile_i8_weight(self, W, Wt, N, K):
+        self.call("ns2_tile_i8_weight", _ptr(W), _ptr(Wt), N, K)
+
+    def linear_i8_tiled(self, At, Wt, scale, C, M, N, K, *, bias=None, ldc=None, cOff=0, alpha=1.0,
+                        act="none", resid=False, gate=None, gOff=0):
+        self.call("ns2_linear_i8_tiled", _ptr(At), _ptr(Wt), _ptr(scale), _ptr(bias), _ptr(C), M, N, K,
+                  N if ldc is None else ldc, cOff, alpha, ACT[act], int(resid), _ptr(gate), gOff)
 
     def linear_i8(self, A, a_fmt, lda, W, scale, C, M, N, K, *, bias=None, add=None, ldc=None,
                   cOff=0, alpha=1.0, act="none", resid=False, gate=None, gOff=0):
@@ -183,15 +194,15 @@ class Lib:
     def norm_mod(self, x, mod, shiftOff, scaleOff, rows, cols, weight, y, eps=1e-6):
         self.call("ns2_norm_mod", _ptr(x), _ptr(mod), shiftOff, scaleOff, rows, cols, _ptr(weight), eps, _ptr(y))
 
-    def norm_mod_rotate_f16(self, x, mod, shiftOff, scaleOff, rows, cols, weight, y, eps=1e-6):
+    def norm_mod_rotate_f16(self, x, mod, shiftOff, scaleOff, rows, cols, weight, y, eps=1e-6, tiled=False):
         self.call("ns2_norm_mod_rotate_f16", _ptr(x), _ptr(mod), shiftOff, scaleOff, rows, cols,
-                  _ptr(weight), eps, _ptr(y))
+                  _ptr(weight), eps, _ptr(y), int(tiled))
 
     def glu(self, x, y, rows, I, act="silu"):
         self.call("ns2_glu", _ptr(x), _ptr(y), rows, I, ACT[act])
 
-    def glu_rotate_f16(self, x, y, rows, I, act="silu"):
-        self.call("ns2_glu_rotate_f16", _ptr(x), _ptr(y), rows, I, ACT[act])
+    def glu_rotate_f16(self, x, y, rows, I, act="silu", tiled=False):
+        self.call("ns2_glu_rotate_f16", _ptr(x), _ptr(y), rows, I, ACT[act], int(tiled))
 
     def elementwise(self, op, a, b, y, n):
         self.call("ns2_elementwise", EW[op], _ptr(a), _ptr(b), _ptr(y), n)

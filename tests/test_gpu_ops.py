@@ -33,6 +33,22 @@ def f16_as_float(t):
     return t.view(torch.float16).float()
 
 
+def untile_a(t, M, K):
+    """Tiled fp16 operand [ceil(M/64)][K/64][8][64][8] -> row-major [M, K]."""
+    Mb = (M + 63) // 64
+    return t.reshape(Mb, K // 64, 8, 64, 8).permute(0, 3, 1, 2, 4).reshape(Mb * 64, K)[:M]
+
+
+def untile_w(t, N, K):
+    """Tiled weight [N/64][K/64][4][64][16] of biased bytes (w + 128) -> row-major int8 [N, K]."""
+    u = t.view(torch.uint8).reshape(N // 64, K // 64, 4, 64, 16).permute(0, 3, 1, 2, 4).reshape(N, K)
+    return (u.to(torch.int16) - 128).to(torch.int8)
+
+
+def tiled_operand(M, K):
+    return torch.empty((M + 63) // 64 * 64, K, dtype=torch.int16, device=dev)
+
+
 # ----------------------------------------------------------------------------- rotation
 
 @pytest.mark.parametrize("rows,cols", [(1, 256), (7, 1536), (2432, 1536), (300, 4096)])
@@ -149,6 +165,117 @@ def test_linear_i8_column_window(ns2lib):
     got = qkvd.cpu()
     assert torch.equal(got[:L], qkv[:L]) and torch.equal(got[L:, :Dm], qkv[L:, :Dm])
     assert_close(got, ref, TOL, "kv_y column window")
+
+
+# ----------------------------------------------------------------------------- tiled int8 linear
+
+def test_tile_i8_weight(ns2lib):
+    N, K = 320, 768
+    q, _ = int8_weight(N, K, gen(13))
+    qd = q.to(dev)
+    wt = torch.empty(N * K, dtype=torch.int8, device=dev)
+    ns2lib.tile_i8_weight(qd, wt, N, K)
+    torch.cuda.synchronize()
+    assert torch.equal(untile_w(wt.cpu(), N, K), q)
+
+
+@pytest.mark.parametrize("rows", [1, 100, 517])
+def test_tiled_producers(ns2lib, rows):
+    """The tiled forms of the three producers hold exactly the row-major results."""
+    g = gen(14 + rows)
+    cols, I = 1536, 4096
+    x = torch.randn(rows, cols, generator=g).to(dev)
+    mod = (torch.randn(6 * cols, generator=g) * 0.1).to(dev)
+    w = (torch.randn(cols, generator=g) * 0.02).to(dev)
+    h = (torch.randn(rows, 2 * I, generator=g) * 2).to(dev)
+    for name, call, K in [
+        ("rotate_f16", lambda y, t: ns2lib.rotate_f16(x, cols, y, cols, rows, cols, tiled=t), cols),
+        ("norm_mod_rotate_f16",
+         lambda y, t: ns2lib.norm_mod_rotate_f16(x, mod, 0, cols, rows, cols, w, y, tiled=t), cols),
+        ("glu_rotate_f16", lambda y, t: ns2lib.glu_rotate_f16(h, y, rows, I, "silu", tiled=t), I),
+    ]:
+        flat = torch.empty(rows, K, dtype=torch.int16, device=dev)
+        call(flat, False)
+        til = tiled_operand(rows, K)
+        call(til, True)
+        torch.cuda.synchronize()
+        assert torch.equal(untile_a(til.cpu(), rows, K), flat.cpu()), name
+
+
+def _tiled_linear_inputs(M, N, K, seed):
+    g = gen(seed)
+    x = torch.randn(M, K, generator=g)
+    q, s = int8_weight(N, K, g)
+    return g, x, q, s, x.to(dev), q.to(dev), tiled_operand(M, K)
+
+
+@pytest.mark.parametrize("M,N,K", [
+    (3952, 4608, 1536),   # fused QKV, 832x1216 image + text rows
+    (3952, 1536, 1536),   # out projection
+    (3952, 8192, 1536),   # MLP w12
+    (3952, 1536, 4096),   # MLP w3
+    (256, 3072, 1536),    # kv_y on the text rows
+    (2432, 6144, 1536),
+    (97, 320, 512),       # ragged rows, N not a multiple of 128
+    (1, 64, 256),
+])
+def test_linear_i8_tiled_shapes(ns2lib, M, N, K):
+    g, x, q, s, xd, qd, at = _tiled_linear_inputs(M, N, K, M * 3 + N + K)
+    wt = torch.empty(N * K, dtype=torch.int8, device=dev)
+    ns2lib.tile_i8_weight(qd, wt, N, K)
+    ns2lib.rotate_f16(xd, K, at, K, M, K, tiled=True)
+    out = torch.empty(M, N, device=dev)
+    ns2lib.linear_i8_tiled(at, wt, s.reshape(-1).to(dev), out, M, N, K)
+    torch.cuda.synchronize()
+    assert_close(out.cpu(), O.linear_i8(x.double(), q, s.double()), TOL, f"linear_i8_tiled {M}x{N}x{K}")
+
+
+def test_linear_i8_tiled_epilogues(ns2lib):
+    M, N, K = 300, 384, 768
+    g, x, q, s, xd, qd, at = _tiled_linear_inputs(M, N, K, 15)
+    bias = torch.randn(N, generator=g)
+    gate = torch.randn(4 * N, generator=g)
+    base = torch.randn(M, N, generator=g)
+    sd = s.reshape(-1).to(dev)
+    wt = torch.empty(N * K, dtype=torch.int8, device=dev)
+    ns2lib.tile_i8_weight(qd, wt, N, K)
+    ns2lib.rotate_f16(xd, K, at, K, M, K, tiled=True)
+
+    out = torch.empty(M, N, device=dev)
+    ns2lib.linear_i8_tiled(at, wt, sd, out, M, N, K, bias=bias.to(dev), alpha=0.5, act="silu")
+    ref = O.linear_i8(x.double(), q, s.double(), alpha=0.5, bias=bias.double(), act="silu")
+    torch.cuda.synchronize()
+    assert_close(out.cpu(), ref, TOL, "tiled bias+silu+alpha")
+
+    outd = base.to(dev)
+    ns2lib.linear_i8_tiled(at, wt, sd, outd, M, N, K, resid=True, gate=gate.to(dev), gOff=2 * N)
+    ref = O.linear_i8(x.double(), q, s.double(), out=base.double().clone(), resid=True, gate=gate.double(), gOff=2 * N)
+    torch.cuda.synchronize()
+    assert_close(outd.cpu(), ref, TOL, "tiled gated resid")
+
+    # column window of a wider output (kv_y into the packed qkv)
+    L = 40
+    qkv = torch.randn(L + M, 3 * N, generator=g)
+    qkvd = qkv.to(dev)
+    ns2lib.linear_i8_tiled(at, wt, sd, qkvd, M, N, K, ldc=3 * N, cOff=L * 3 * N + N)
+    ref = qkv.double().clone()
+    O.linear_i8(x.double(), q, s.double(), out=ref, ldc=3 * N, cOff=L * 3 * N + N)
+    torch.cuda.synchronize()
+    got = qkvd.cpu()
+    assert torch.equal(got[:L], qkv[:L]) and torch.equal(got[L:, :N], qkv[L:, :N])
+    assert torch.equal(got[L:, 2 * N:], qkv[L:, 2 * N:])
+    assert_close(got, ref, TOL, "tiled column window")
+
+
+def test_linear_i8_tiled_errors(ns2lib):
+    at = torch.empty(64, 256, dtype=torch.int16, device=dev)
+    wt = torch.empty(96 * 256, dtype=torch.int8, device=dev)
+    sc = torch.ones(96, device=dev)
+    out = torch.empty(64, 96, device=dev)
+    with pytest.raises(RuntimeError, match="N %"):
+        ns2lib.linear_i8_tiled(at, wt, sc, out, 64, 96, 256)
+    with pytest.raises(RuntimeError, match="multiples of 64"):
+        ns2lib.tile_i8_weight(wt, wt, 96, 256)
 
 
 # ----------------------------------------------------------------------------- bf16 linear
