@@ -9,11 +9,15 @@
    ConvRot block linears, bf16 elsewhere). W untimed passes, then K timed passes with the
    latent tokens resident in device memory, bracketed by stream events and a device sync.
    `value` is the median device time per pass in ms.
+   The dominant kernel of the pass is the tiled int8 ConvRot GEMM (qkv, proj, w12, w3, kv_y of
+   every block): a profiled run of the same pass times every launch with stream events on the
+   library's stream, and `roofline` is its algorithmic 2*M*N*K flops summed over the pass /
+   its summed launch time, against the 2516.6 TFLOP/s dense fp16 MFMA peak.
 2. Joint attention at the production shape (3952 queries x 4208 keys, 16 heads x 96, batch 2,
    2-D RoPE on image rows, log-weight bias on the text keys) through the C ABI (ctypes);
    the library's kernel profiler times each launch of the flash kernel with stream events,
-   which gives the roofline entry (algorithmic 4*Lq*Lk*D*H*B flops per launch / mean launch
-   time, against the 2516.6 TFLOP/s dense fp16 MFMA peak).
+   which gives `roofline_attention` (algorithmic 4*Lq*Lk*D*H*B flops per launch / mean launch
+   time).
 3. CPU baseline: the oracle (a PyTorch-CPU restatement of tools/reference.py) on a bounded
    sample -- one joint block and one image-only block at the full 3952-token shape -- scaled
    to 18 blocks, on this host's cores.
@@ -36,6 +40,10 @@ METRIC = "ms per 832x1216 DiT pass (int8) + joint-attention TFLOP/s, 1 MI355X"
 PUBLISHED_PASS_MS = 1730.0   # README.md:86-88 of the reference (WebGPU, laptop GPU)
 FP16_PEAK_TFLOPS = 2516.6    # MI355X dense fp16 MFMA
 H_IMG, W_IMG, T_TXT, D, HEADS, HD, I_MLP, BLOCKS = 76, 52, 256, 1536, 16, 96, 4096, 18
+# HBM bytes per launch from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE (scaled by the copy-kernel
+# calibration; see profiles/), or None where not collected for the current kernels
+GEMM_TRAFFIC_BYTES_PER_LAUNCH = None
+ATTN_TRAFFIC_BYTES_PER_LAUNCH = None
 
 
 def log(msg):
@@ -77,6 +85,24 @@ def run_dit_profile():
         sys.stderr.write(p.stderr[-3000:])
         raise SystemExit(f"run_dit.js --profile failed with {p.returncode}")
     return json.loads(p.stdout.strip().splitlines()[-1]).get("profile", [])
+
+
+# int8 ConvRot linears of the pass (tiled GEMM launches), by the op names the DiT driver uses
+GEMM_OPS = ("dit.qkv", "dit.proj", "dit.mlp.w12", "dit.mlp.w3", "dit.kv_y", "dit.text.qkv", "dit.text.proj")
+
+
+def gemm_roofline(kernels):
+    """Pass aggregate of the int8 GEMM launches: per-op rows and sum(2MNK) / sum(time)."""
+    rows = [r for r in kernels if r["name"] in GEMM_OPS and r.get("tflops")]
+    flop = sum(r["tflops"] * r["ms"] * 1e9 for r in rows)
+    ms = sum(r["ms"] for r in rows)
+    return {
+        "ops": [{"name": r["name"], "launches_per_pass": r["count"], "ms_per_pass": r["ms"],
+                 "tflops": r["tflops"]} for r in rows],
+        "gflop_per_pass": flop / 1e9, "ms_per_pass": ms,
+        "launches_per_pass": sum(r["count"] for r in rows),
+        "tflops": flop / (ms / 1e3) / 1e12 if ms else None,
+    }
 
 
 def bench_attention(reps, warmup):
@@ -260,11 +286,13 @@ def main():
         sys.exit(2)
 
     flops = pass_flops()
-    dit, kernels = None, None
+    dit, kernels, gemm = None, None, None
     if not args.no_dit:
         # the Node runs come first, before this process initialises the GPU
         dit = run_dit(args.steps, args.warmup)
         kernels = run_dit_profile()
+        gemm = gemm_roofline(kernels)
+        log(f"int8 GEMMs: {gemm['ms_per_pass']:.3f} ms/pass, {gemm['tflops']:.1f} TFLOP/s")
     attn = bench_attention(reps=max(10, args.steps), warmup=max(2, args.warmup))
     if args.copy_calibration:
         attn["copy_calibration"] = copy_calibration()
@@ -296,14 +324,24 @@ def main():
         "pass_ms_wall": dit["ms_wall_median"] if dit else None,
         "pass_ms_host_to_host": dit["ms_host_to_host_median"] if dit else None,
         "joint_attention": attn,
+        "gemm_i8": gemm,
         "roofline": {
-            "kernel": "attn_flash (joint attention, 3952x4208, batch 2)",
+            "kernel": "gemm_tiled_kernel (int8 ConvRot block linears of one pass: qkv, proj, w12, w3, kv_y)",
+            "bound": "mfma",
+            "achieved": gemm["tflops"] if gemm else None,
+            "peak": FP16_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": gemm["tflops"] / FP16_PEAK_TFLOPS if gemm and gemm["tflops"] else None,
+            "traffic": GEMM_TRAFFIC_BYTES_PER_LAUNCH,
+        },
+        "roofline_attention": {
+            "kernel": "flash_kernel (joint attention, 3952x4208, batch 2)",
             "bound": "mfma",
             "achieved": attn["flash_tflops"],
             "peak": FP16_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": attn["flash_tflops"] / FP16_PEAK_TFLOPS if attn["flash_tflops"] else None,
-            "traffic": None,
+            "traffic": ATTN_TRAFFIC_BYTES_PER_LAUNCH,
         },
         "cpu_baseline": cpu,
         "kernels": kernels,

@@ -192,17 +192,18 @@ struct FlashArgs {
 // rescale. Any reference gives the same softmax, and p <= 2^kRebase stays in fp16 range.
 constexpr float kRebase = 8.0f;
 
-template <int D, int QT, int NW>
+template <int D, int QT, int NW, int STAGES>
 __global__ __launch_bounds__(NW * 64) void flash_kernel(FlashArgs a) {
   constexpr int DC = D / 16;             // k-steps of S
   constexpr int DT = D / 32;             // dim tiles of O
   constexpr int TILE = KB * D;           // halfs per K (or V) tile image
   constexpr int BLOCKS = 2 * TILE / 512; // 1 KB direct-load blocks per stage (K then V)
+  static_assert(STAGES == 3 || STAGES == 4, "three or four LDS stages");
 
-  // three stages: K of tile t+1 and V of tile t are read while tile t+2 lands
-  __shared__ __attribute__((aligned(16))) half_t ks[3][TILE];
-  __shared__ __attribute__((aligned(16))) half_t vts[3][TILE];
-  __shared__ __attribute__((aligned(16))) float kbias[3][KB];
+  // K of tile t+1 and V of tile t are read while tiles t+2 .. t+STAGES-1 land
+  __shared__ __attribute__((aligned(16))) half_t ks[STAGES][TILE];
+  __shared__ __attribute__((aligned(16))) half_t vts[STAGES][TILE];
+  __shared__ __attribute__((aligned(16))) float kbias[STAGES][KB];
 
   // Work unit: (pair = batch*H + head, query block). With xcd_order, consecutive block ids
   // land on different XCDs (round-robin dispatch), so block id i is mapped to pair
@@ -256,20 +257,30 @@ __global__ __launch_bounds__(NW * 64) void flash_kernel(FlashArgs a) {
 
   // Tile t -> LDS stage st with direct global->LDS loads: the stage image is BLOCKS blocks of
   // 1 KB (K blocks, then V^T blocks) plus the 256-byte key bias; wave w moves blocks w, w+NW,
-  // ...; lane l moves bytes [16l, 16l+16) of a block (16 lanes for the bias). Every load goes
-  // through this one call site so the LDS base (M0) is set from its own destination.
+  // ..., BLOCKS (the bias); lane l moves bytes [16l, 16l+16) of a block (16 lanes for the bias).
+  const uint32_t ks_base = lds_addr(ks), vts_base = lds_addr(vts), kb_base = lds_addr(kbias);
   auto dma = [&](int t, int st) {
     for (int j = wave; j <= BLOCKS; j += NW) {
       const int kind = j < BLOCKS / 2 ? 0 : (j < BLOCKS ? 1 : 2);
       const half_t* src = kind == 0 ? Kt + (long long)t * TILE + j * 512 + lane * 8
                         : kind == 1 ? Vt + (long long)t * TILE + (j - BLOCKS / 2) * 512 + lane * 8
                                     : reinterpret_cast<const half_t*>(Bg + t * KB) + lane * 8;
-      half_t* dst = kind == 0 ? ks[st] + j * 512
-                  : kind == 1 ? vts[st] + (j - BLOCKS / 2) * 512
-                              : reinterpret_cast<half_t*>(kbias[st]);
-      if (kind < 2 || lane < KB / 4) __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
+      const uint32_t dst = kind == 0 ? ks_base + (st * TILE + j * 512) * 2
+                         : kind == 1 ? vts_base + (st * TILE + (j - BLOCKS / 2) * 512) * 2
+                                     : kb_base + st * KB * 4;
+      if (kind < 2 || lane < KB / 4) dma16(src, __builtin_amdgcn_readfirstlane(dst));
     }
   };
+  // Wait until at most the loads of the N most recent tiles are in flight for this wave
+  // (wave w issues (BLOCKS - w) / NW + 1 loads per tile).
+  auto wait_newer = [&](auto n_c) {
+    constexpr int N = decltype(n_c)::value;
+    if (wave <= BLOCKS % NW) vm_wait<N * (BLOCKS / NW + 1)>();
+    else vm_wait<N * (BLOCKS / NW)>();
+  };
+  using W0_ = std::integral_constant<int, 0>;
+  using W1_ = std::integral_constant<int, 1>;
+  using W2_ = std::integral_constant<int, 2>;
 
   // S^T = K Q^T for the 64-key tile in LDS stage `buf`, the two 32-key halves' MFMA chains
   // interleaved: s[kt][qt][r] = score(key 64t + 32kt + 8(r/4) + 4hi + r%4, query lq).
@@ -327,9 +338,14 @@ __global__ __launch_bounds__(NW * 64) void flash_kernel(FlashArgs a) {
   //   phase B: O += V_t P_t on the MFMA pipe, interleaved with bias and row max of tile t+1.
   float16_t s_cur[2][QT];
   float mx_cur[QT];
-  dma(0, 0);
-  if (ntiles > 1) dma(1, 1);
-  __builtin_amdgcn_s_waitcnt(0);
+  for (int i = 0; i < STAGES - 1 && i < ntiles; ++i) dma(i, i);
+  {
+    // tile 0 has landed once at most the tiles issued after it remain in flight
+    const int newer = (STAGES - 2 < ntiles - 1 ? STAGES - 2 : ntiles - 1);
+    if (newer >= 2) wait_newer(W2_{});
+    else if (newer == 1) wait_newer(W1_{});
+    else wait_newer(W0_{});
+  }
   __syncthreads();
   qk(s_cur, 0);
   bias_max(s_cur, mx_cur, 0, 0 >= a.bias_block0);
@@ -337,10 +353,12 @@ __global__ __launch_bounds__(NW * 64) void flash_kernel(FlashArgs a) {
   auto step = [&](int t, auto more_c, auto bias_next_c) {
     constexpr bool MORE = decltype(more_c)::value;
     constexpr bool BIAS_NEXT = decltype(bias_next_c)::value;
-    const int vbuf = t % 3, kbuf = (t + 1) % 3;
-    __builtin_amdgcn_s_waitcnt(0);
+    const int vbuf = t % STAGES, kbuf = (t + 1) % STAGES;
+    // tile t+1 has landed once at most the tiles issued after it (t+2 .. t+STAGES-2) remain
+    if (MORE && STAGES == 4 && t + 2 < ntiles) wait_newer(W1_{});
+    else wait_newer(W0_{});
     __syncthreads();
-    if (MORE && t + 2 < ntiles) dma(t + 2, (t + 2) % 3);
+    if (MORE && t + STAGES - 1 < ntiles) dma(t + STAGES - 1, (t + STAGES - 1) % STAGES);
 
     // ---- move the reference when a score exceeds it by more than 2^kRebase, or when nothing
     // has been accumulated yet (l = 0: the tile maximum becomes the reference, so the largest
@@ -457,13 +475,13 @@ __global__ __launch_bounds__(NW * 64) void flash_kernel(FlashArgs a) {
   }
 }
 
-template <int D, int QT, int NW>
+template <int D, int QT, int NW, int STAGES = 4>
 void launch_flash(FlashArgs fa, hipStream_t s) {
   constexpr int BQ = NW * QT * 32;
   fa.qblocks = (fa.Lq + BQ - 1) / BQ;
   const int blocks = fa.qblocks * fa.pairs;
   fa.xcd_order = (fa.pairs % 8 == 0) ? 1 : 0;
-  flash_kernel<D, QT, NW><<<blocks, NW * 64, 0, s>>>(fa);
+  flash_kernel<D, QT, NW, STAGES><<<blocks, NW * 64, 0, s>>>(fa);
 }
 
 template <int D>

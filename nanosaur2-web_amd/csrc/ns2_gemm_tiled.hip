@@ -277,32 +277,31 @@ int launch_tiled(TGemmArgs p) {
   return NS2_OK;
 }
 
-// Block-tile configurations: BM x BN, blocks resident per CU (LDS-bound), and relative
-// per-CU throughput of one resident tile set (larger tiles re-read less from LDS and L2).
+// Block-tile configurations (two LDS stages each): BM x BN, the waves' layout, and a per-CU
+// throughput factor fitted to measurements at the DiT shapes (3952 x {4608, 1536, 8192} x
+// {1536, 4096}, 256 x 3072 x 1536). Layouts with one wave row decode each weight fragment once.
 struct TileCfg {
-  int bm, bn, per_cu;
+  int bm, bn;
   float rate;
 };
 constexpr TileCfg kCfgs[] = {
-    {256, 256, 1, 1.00f},  // 8 waves of 128x64, 144 KB LDS
-    {192, 192, 1, 0.97f},  // 4 waves of 96x96, 108 KB
-    {192, 128, 1, 0.93f},  // 4 waves of 96x64, 96 KB
-    {128, 128, 2, 0.85f},  // 4 waves of 64x64, 72 KB
-    {64, 128, 3, 0.60f},   // 4 waves of 64x32, 48 KB: small M
+    {128, 256, 1.00f},  // 16 waves (2 x 8) of 64x32, 64 KB LDS
+    {64, 256, 0.95f},   // 8 waves (1 x 8) of 64x32, 48 KB
+    {64, 128, 0.70f},   // 4 waves (1 x 4) of 64x32, 32 KB
+    {64, 64, 0.40f},    // 4 waves (2 x 2) of 32x32, 24 KB: few rows (text tokens)
 };
 constexpr int kCUs = 256;
 
-// Estimated time of a configuration: rounds of resident tile sets times the work of a set
-// divided by its rate. The configuration with the least estimate is used.
+// Estimated time: the tiles the busiest CU runs, times the work of a tile over its rate.
+// The configuration with the least estimate is used.
 int pick_config(int M, int N) {
   int best = -1;
   double best_t = 0;
   for (int i = 0; i < (int)(sizeof(kCfgs) / sizeof(kCfgs[0])); ++i) {
     const TileCfg& c = kCfgs[i];
     const long long tiles = (long long)((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn);
-    const long long slots = (long long)kCUs * c.per_cu;
-    const long long rounds = (tiles + slots - 1) / slots;
-    const double t = (double)rounds * c.per_cu * c.bm * c.bn / c.rate;
+    const long long per_cu = (tiles + kCUs - 1) / kCUs;
+    const double t = (double)per_cu * c.bm * c.bn / c.rate;
     if (best < 0 || t < best_t) {
       best = i;
       best_t = t;
@@ -344,11 +343,10 @@ int ns2_linear_i8_tiled(const uint16_t* At, const int8_t* Wt, const float* scale
               cOff, gOff, M, N, K, ldc, (M + 63) / 64, N / 64, 0, 0, alpha, act, resid};
   ns2::ProfScope prof_("gemm_i8_tiled");
   switch (pick_config(M, N)) {
-    case 0: return launch_tiled<256, 256, 2, 4>(p);
-    case 1: return launch_tiled<192, 192, 2, 2>(p);
-    case 2: return launch_tiled<192, 128, 2, 2>(p);
-    case 3: return launch_tiled<128, 128, 2, 2>(p);
-    default: return launch_tiled<64, 128, 1, 4>(p);
+    case 0: return launch_tiled<128, 256, 2, 8, true, 2>(p);
+    case 1: return launch_tiled<64, 256, 1, 8, true, 2>(p);
+    case 2: return launch_tiled<64, 128, 1, 4, true, 2>(p);
+    default: return launch_tiled<64, 64, 2, 2, true, 2>(p);
   }
 }
 

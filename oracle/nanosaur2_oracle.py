@@ -12,7 +12,7 @@ CPU tensors; pass dtype=torch.float64 inputs where a tighter reference is wanted
 
 Parity status: every function here is pinned by tests/test_oracle.py (closed forms,
 invariants, brute force) and, for the DiT composition, by golden vectors written from the
-reference itself (tests/golden/). See DESIGN.md for the list.
+reference itself (tests/golden/).
 """
 
 from __future__ import annotations

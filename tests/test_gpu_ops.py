@@ -14,7 +14,7 @@ from conftest import assert_close
 
 pytestmark = pytest.mark.gpu
 dev = "cuda"
-TOL = 2e-3        # north_star tolerance for attention / GEMM outputs
+TOL = 2e-3        # parity tolerance for attention / GEMM outputs (max-abs / max|ref|, rel-L2)
 TOL_F32 = 1e-5    # kernels that compute in fp32 end to end
 TOL_F16_OUT = 2e-3  # fp32 math, fp16-rounded output
 
@@ -390,6 +390,26 @@ def test_attention_strided_qkv_views(ns2lib):
     bias = torch.cat([torch.zeros(L, dtype=torch.float64), lb.double()])
     ref = O.attention_heads(ref_buf[:L, :Dm], ref_buf[:, Dm:2 * Dm], ref_buf[:, 2 * Dm:], 16, 96, bias)
     assert_close(o.cpu(), ref, TOL, "strided qkv + fused head norms")
+
+
+@pytest.mark.parametrize("Lk", [64, 100, 150, 200, 257])
+def test_attention_few_key_tiles(ns2lib, Lk):
+    """1 to 5 key tiles of 64: the load pipeline's prologue and tail with fewer tiles than stages."""
+    g = gen(Lk)
+    Lq, H, Dh = 70, 2, 96
+    q = torch.randn(Lq, H * Dh, generator=g)
+    k = torch.randn(Lk, H * Dh, generator=g)
+    v = torch.randn(Lk, H * Dh, generator=g)
+    kb = torch.randn(Lk, generator=g)
+    o = torch.empty(Lq, H * Dh, device=dev)
+    # bias on keys [30, Lk): the biased tiles start inside the first tile
+    ns2lib.attention(q.to(dev), k.to(dev), v.to(dev), o, Lq=Lq, Lk=Lk, H=H, D=Dh, ldq=H * Dh,
+                     ldk=H * Dh, ldv=H * Dh, ldo=H * Dh, key_bias=kb[30:].to(dev), biasStart=30)
+    torch.cuda.synchronize()
+    bias = torch.zeros(Lk, dtype=torch.float64)
+    bias[30:] = kb[30:].double()
+    ref = O.attention_heads(q.double(), k.double(), v.double(), H, Dh, bias=bias)
+    assert_close(o.cpu(), ref, TOL, f"Lk={Lk}")
 
 
 @pytest.mark.parametrize("Dh", [32, 64, 128])
