@@ -258,17 +258,37 @@ __global__ __launch_bounds__(NW * 64) void flash_kernel(FlashArgs a) {
   // Tile t -> LDS stage st with direct global->LDS loads: the stage image is BLOCKS blocks of
   // 1 KB (K blocks, then V^T blocks) plus the 256-byte key bias; wave w moves blocks w, w+NW,
   // ..., BLOCKS (the bias); lane l moves bytes [16l, 16l+16) of a block (16 lanes for the bias).
-  const uint32_t ks_base = lds_addr(ks), vts_base = lds_addr(vts), kb_base = lds_addr(kbias);
+  // The per-wave sources and destinations are fixed up front; a tile adds its offsets.
+  constexpr int NJ = (BLOCKS + NW) / NW;  // loads per wave per tile, at most
+  const char* g_src[NJ];
+  uint32_t l_dst[NJ];
+  int g_step[NJ], l_step[NJ];
+  {
+    const uint32_t ks_base = lds_addr(ks), vts_base = lds_addr(vts), kb_base = lds_addr(kbias);
+#pragma unroll
+    for (int i = 0; i < NJ; ++i) {
+      const int j = wave + i * NW;
+      if (j < BLOCKS / 2) {
+        g_src[i] = reinterpret_cast<const char*>(Kt + j * 512);
+        l_dst[i] = ks_base + j * 1024;
+      } else if (j < BLOCKS) {
+        g_src[i] = reinterpret_cast<const char*>(Vt + (j - BLOCKS / 2) * 512);
+        l_dst[i] = vts_base + (j - BLOCKS / 2) * 1024;
+      } else {
+        g_src[i] = reinterpret_cast<const char*>(Bg);
+        l_dst[i] = kb_base;
+      }
+      g_step[i] = j < BLOCKS ? TILE * 2 : KB * 4;  // bytes per tile in global memory
+      l_step[i] = j < BLOCKS ? TILE * 2 : KB * 4;  // bytes per LDS stage
+    }
+  }
   auto dma = [&](int t, int st) {
-    for (int j = wave; j <= BLOCKS; j += NW) {
-      const int kind = j < BLOCKS / 2 ? 0 : (j < BLOCKS ? 1 : 2);
-      const half_t* src = kind == 0 ? Kt + (long long)t * TILE + j * 512 + lane * 8
-                        : kind == 1 ? Vt + (long long)t * TILE + (j - BLOCKS / 2) * 512 + lane * 8
-                                    : reinterpret_cast<const half_t*>(Bg + t * KB) + lane * 8;
-      const uint32_t dst = kind == 0 ? ks_base + (st * TILE + j * 512) * 2
-                         : kind == 1 ? vts_base + (st * TILE + (j - BLOCKS / 2) * 512) * 2
-                                     : kb_base + st * KB * 4;
-      if (kind < 2 || lane < KB / 4) dma16(src, __builtin_amdgcn_readfirstlane(dst));
+#pragma unroll
+    for (int i = 0; i < NJ; ++i) {
+      const int j = wave + i * NW;
+      if (j > BLOCKS) break;
+      if (j < BLOCKS || lane < KB / 4)
+        dma16(g_src[i] + (long long)t * g_step[i] + lane * 16, __builtin_amdgcn_readfirstlane(l_dst[i] + st * l_step[i]));
     }
   };
   // Wait until at most the loads of the N most recent tiles are in flight for this wave
@@ -282,62 +302,70 @@ __global__ __launch_bounds__(NW * 64) void flash_kernel(FlashArgs a) {
   using W1_ = std::integral_constant<int, 1>;
   using W2_ = std::integral_constant<int, 2>;
 
-  // S^T = K Q^T for the 64-key tile in LDS stage `buf`, the two 32-key halves' MFMA chains
-  // interleaved: s[kt][qt][r] = score(key 64t + 32kt + 8(r/4) + 4hi + r%4, query lq).
-  // A fragment: chunk 2c + hi (dims 16c + 8hi .. +7) of key 32kt + lq.
-  auto qk = [&](float16_t (&s)[2][QT], int buf) {
+  // S^T = K Q^T - m_ref for the 64-key tile in LDS stage `buf`: the accumulators start at
+  // -m_ref, so scores come out relative to the softmax reference (log2 units) and exp2 needs
+  // no subtraction. s[kt][qt][r] = score(key 64t + 32kt + 8(r/4) + 4hi + r%4, query lq).
+  // K fragment i = 2c + kt: chunk 2c + hi (dims 16c + 8hi .. +7) of key 32kt + lq.
+  constexpr int NK = 2 * DC;  // K fragments (and score MFMA groups) per tile
+  constexpr int NV = 4 * DT;  // V fragments (and output MFMA groups) per tile
+  auto read_k = [&](int i, int buf) {
+    const int c = i / 2, kt = i % 2;
+    return *reinterpret_cast<const half8_t*>(&ks[buf][((2 * c + hi) * KB + kt * 32 + lq) * 8]);
+  };
+  // V fragment i = (2kt + kk) * DT + dt: stored key chunk 4kt + 2kk + hi of dim 32dt + lq
+  auto read_v = [&](int i, int buf) {
+    const int kt = i / (2 * DT), kk = (i / DT) % 2, dt = i % DT;
+    return *reinterpret_cast<const half8_t*>(&vts[buf][((4 * kt + 2 * kk + hi) * D + dt * 32 + lq) * 8]);
+  };
+  auto init_scores = [&](float16_t (&s)[2][QT]) {
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
       for (int qt = 0; qt < QT; ++qt)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) s[kt][qt][r] = 0.f;
+        for (int r = 0; r < 16; ++r) s[kt][qt][r] = -m_ref[qt];
+  };
+  auto qk_mfma = [&](float16_t (&s)[2][QT], int i, const half8_t& kf) {
+    const int c = i / 2, kt = i % 2;
 #pragma unroll
-    for (int c = 0; c < DC; ++c)
+    for (int qt = 0; qt < QT; ++qt) s[kt][qt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[qt][c], s[kt][qt], 0, 0, 0);
+  };
+  // per-key bias of a tile (text and padding keys)
+  auto add_bias = [&](float16_t (&s)[2][QT], int buf) {
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
-        const half8_t kf = *reinterpret_cast<const half8_t*>(&ks[buf][((2 * c + hi) * KB + kt * 32 + lq) * 8]);
+    for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-        for (int qt = 0; qt < QT; ++qt)
-          s[kt][qt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[qt][c], s[kt][qt], 0, 0, 0);
+      for (int g = 0; g < 4; ++g) {
+        const float4 bb = *reinterpret_cast<const float4*>(&kbias[buf][kt * 32 + 8 * g + 4 * hi]);
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) {
+          s[kt][qt][4 * g + 0] += bb.x;
+          s[kt][qt][4 * g + 1] += bb.y;
+          s[kt][qt][4 * g + 2] += bb.z;
+          s[kt][qt][4 * g + 3] += bb.w;
+        }
       }
   };
-  // per-key bias (text and padding keys), then the row maximum (both 32-key halves)
-  auto bias_max = [&](float16_t (&s)[2][QT], float (&mx)[QT], int buf, bool biased) {
-    if (biased) {
+  // partial row maximum over one 32-key half (kt) of the tile, 16 values per lane
+  auto half_max = [&](float16_t (&s)[2][QT], int kt, int qt) {
+    float m = s[kt][qt][0];
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const float4 bb = *reinterpret_cast<const float4*>(&kbias[buf][kt * 32 + 8 * g + 4 * hi]);
-#pragma unroll
-          for (int qt = 0; qt < QT; ++qt) {
-            s[kt][qt][4 * g + 0] += bb.x;
-            s[kt][qt][4 * g + 1] += bb.y;
-            s[kt][qt][4 * g + 2] += bb.z;
-            s[kt][qt][4 * g + 3] += bb.w;
-          }
-        }
-    }
-#pragma unroll
-    for (int qt = 0; qt < QT; ++qt) {
-      float m = s[0][qt][0];
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) m = fmaxf(m, s[kt][qt][r]);
-      mx[qt] = fmaxf(m, __shfl_xor(m, 32, 64));
-    }
+    for (int r = 1; r < 16; ++r) m = fmaxf(m, s[kt][qt][r]);
+    return m;
   };
 
-  // Software pipeline, one barrier per tile. Iteration t:
-  //   wait for this wave's loads, barrier (tile t+1 has landed; every wave is done with
-  //   iteration t-1), start loading tile t+2 into stage (t+2)%3 (it held tile t-1);
+  // Software pipeline, one barrier per tile. Step t:
+  //   wait for this wave's loads of tile t+1, barrier (every wave's loads of tile t+1 have
+  //   landed; every wave is done with step t-1), start loading tile t+STAGES-1 into the stage
+  //   that held tile t-1;
   //   move the softmax reference if tile t needs it (rare);
-  //   phase A: scores of tile t+1 on the MFMA pipe, interleaved with exp/convert/sum of tile t;
-  //   phase B: O += V_t P_t on the MFMA pipe, interleaved with bias and row max of tile t+1.
-  float16_t s_cur[2][QT];
-  float mx_cur[QT];
+  //   phase A: scores of tile t+1 on the MFMA pipe, K fragments read two MFMA groups ahead,
+  //            the exp/convert/sum of tile t spread between the MFMA groups;
+  //   phase B: O += V_t P_t on the MFMA pipe, V fragments read two MFMA groups ahead, the key
+  //            bias (for the tiles that have one) and row max of tile t+1 between them.
+  // Steps alternate the two score buffers (A holds tile t, B receives tile t+1).
+  float16_t sA[2][QT], sB[2][QT];
+  float mA[QT], mB[QT];
   for (int i = 0; i < STAGES - 1 && i < ntiles; ++i) dma(i, i);
   {
     // tile 0 has landed once at most the tiles issued after it remain in flight
@@ -347,14 +375,21 @@ __global__ __launch_bounds__(NW * 64) void flash_kernel(FlashArgs a) {
     else wait_newer(W0_{});
   }
   __syncthreads();
-  qk(s_cur, 0);
-  bias_max(s_cur, mx_cur, 0, 0 >= a.bias_block0);
+  init_scores(sA);
+#pragma unroll
+  for (int i = 0; i < NK; ++i) qk_mfma(sA, i, read_k(i, 0));
+  if (0 >= a.bias_block0) add_bias(sA, 0);
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    const float m = fmaxf(half_max(sA, 0, qt), half_max(sA, 1, qt));
+    mA[qt] = fmaxf(m, __shfl_xor(m, 32, 64));
+  }
 
-  auto step = [&](int t, auto more_c, auto bias_next_c) {
+  auto step = [&](int t, float16_t (&s_cur)[2][QT], float16_t (&s_nxt)[2][QT], float (&mx_cur)[QT],
+                  float (&mx_nxt)[QT], auto more_c, auto bias_c) {
     constexpr bool MORE = decltype(more_c)::value;
-    constexpr bool BIAS_NEXT = decltype(bias_next_c)::value;
+    constexpr bool BIAS = decltype(bias_c)::value;  // tile t+1 carries a key bias
     const int vbuf = t % STAGES, kbuf = (t + 1) % STAGES;
-    // tile t+1 has landed once at most the tiles issued after it (t+2 .. t+STAGES-2) remain
     if (MORE && STAGES == 4 && t + 2 < ntiles) wait_newer(W1_{});
     else wait_newer(W0_{});
     __syncthreads();
@@ -362,16 +397,16 @@ __global__ __launch_bounds__(NW * 64) void flash_kernel(FlashArgs a) {
 
     // ---- move the reference when a score exceeds it by more than 2^kRebase, or when nothing
     // has been accumulated yet (l = 0: the tile maximum becomes the reference, so the largest
-    // p is 1 and l >= 1 afterwards); the running sum and output scale by 2^-shift
+    // p is 1 and l >= 1 afterwards); the running sum and output scale by 2^-shift and the
+    // tile's relative scores drop by shift
     {
       bool need = false;
 #pragma unroll
-      for (int qt = 0; qt < QT; ++qt) need |= (mx_cur[qt] - m_ref[qt] > kRebase) || (l_run[qt] == 0.f);
+      for (int qt = 0; qt < QT; ++qt) need |= (mx_cur[qt] > kRebase) || (l_run[qt] == 0.f);
       if (__builtin_amdgcn_ballot_w64(need)) {
 #pragma unroll
         for (int qt = 0; qt < QT; ++qt) {
-          const float d = mx_cur[qt] - m_ref[qt];
-          const float shift = (l_run[qt] == 0.f) ? d : fmaxf(d, 0.f);
+          const float shift = (l_run[qt] == 0.f) ? mx_cur[qt] : fmaxf(mx_cur[qt], 0.f);
           const float alpha = __builtin_amdgcn_exp2f(-shift);
           m_ref[qt] += shift;
           l_run[qt] *= alpha;
@@ -379,82 +414,114 @@ __global__ __launch_bounds__(NW * 64) void flash_kernel(FlashArgs a) {
           for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
             for (int r = 0; r < 16; ++r) o[qt][dt][r] *= alpha;
+#pragma unroll
+          for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) s_cur[kt][qt][r] -= shift;
         }
       }
     }
 
-    // ---- phase A (raised wave priority while this wave feeds the MFMA pipe)
+    // ---- phase A (raised wave priority while this wave feeds the MFMA pipe); the scheduling
+    // barriers keep each phase's reads and VALU work inside the phase
+    __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_setprio(1);
-    float16_t s_next[2][QT];
-    if (MORE) qk(s_next, kbuf);
+    // P of tile t in fp16, pair by pair: pair p = ((kt*QT + qt)*2 + kk)*4 + e/2
+    constexpr int NP = 2 * QT * 2 * 4;
     half8_t pf[2][QT][2];
+    float ls[2][QT];
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-      for (int qt = 0; qt < QT; ++qt) {
-        float ls = 0.f;
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-          for (int e = 0; e < 8; e += 2) {
-            half2_t pp;
-            pp[0] = (half_t)__builtin_amdgcn_exp2f(s_cur[kt][qt][kk * 8 + e] - m_ref[qt]);
-            pp[1] = (half_t)__builtin_amdgcn_exp2f(s_cur[kt][qt][kk * 8 + e + 1] - m_ref[qt]);
-            pf[kt][qt][kk][e] = pp[0];
-            pf[kt][qt][kk][e + 1] = pp[1];
-            const half2_t one = {(half_t)1.0f, (half_t)1.0f};
-            ls = __builtin_amdgcn_fdot2(pp, one, ls, false);
-          }
-        l_run[qt] += ls;
-      }
+      for (int qt = 0; qt < QT; ++qt) ls[kt][qt] = 0.f;
+    auto exp_pair = [&](int p) {
+      const int e = (p % 4) * 2, kk = (p / 4) % 2, qt = (p / 8) % QT, kt = p / (8 * QT);
+      half2_t pp;
+      pp[0] = (half_t)__builtin_amdgcn_exp2f(s_cur[kt][qt][kk * 8 + e]);
+      pp[1] = (half_t)__builtin_amdgcn_exp2f(s_cur[kt][qt][kk * 8 + e + 1]);
+      pf[kt][qt][kk][e] = pp[0];
+      pf[kt][qt][kk][e + 1] = pp[1];
+      const half2_t one = {(half_t)1.0f, (half_t)1.0f};
+      ls[kt][qt] = __builtin_amdgcn_fdot2(pp, one, ls[kt][qt], false);
+    };
     if (MORE) {
-      // 2*DC*QT score MFMAs, each after its K-fragment read, with the exp work between them
+      // K fragment i+2 is read before the MFMAs of fragment i; each slot also does its share
+      // of the exp work. Scheduling barriers pin this order (the default scheduler would put
+      // every read right before its MFMA to save registers).
+      init_scores(s_nxt);
+      half8_t kf[NK];
+      kf[0] = read_k(0, kbuf);
+      kf[1] = read_k(1, kbuf);
 #pragma unroll
-      for (int i = 0; i < 2 * DC; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, QT, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, 6 * QT, 0);
+      for (int i = 0; i < NK; ++i) {
+        if (i + 2 < NK) kf[i + 2] = read_k(i + 2, kbuf);
+        __builtin_amdgcn_sched_barrier(0);
+        qk_mfma(s_nxt, i, kf[i]);
+#pragma unroll
+        for (int p = i * NP / NK; p < (i + 1) * NP / NK; ++p) exp_pair(p);
+        __builtin_amdgcn_sched_barrier(0);
       }
+    } else {
+#pragma unroll
+      for (int p = 0; p < NP; ++p) exp_pair(p);
     }
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) l_run[qt] += ls[0][qt] + ls[1][qt];
 
-    // ---- phase B: O^T += V^T P^T, the DT accumulators interleaved.
-    // A fragment: stored key chunk 4kt + 2kk + hi of dim 32dt + lq.
+    __builtin_amdgcn_sched_barrier(0);
+    // ---- phase B: O^T += V^T P^T, the DT accumulators interleaved
+    if (BIAS) add_bias(s_nxt, kbuf);
+    {
+      // V fragment i+2 is read before the MFMAs of fragment i; the first 2*QT slots also take
+      // a half-row maximum of tile t+1
+      half8_t vf[NV];
+      float hm[2][QT];
+      vf[0] = read_v(0, vbuf);
+      vf[1] = read_v(1, vbuf);
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
+      for (int i = 0; i < NV; ++i) {
+        if (i + 2 < NV) vf[i + 2] = read_v(i + 2, vbuf);
+        __builtin_amdgcn_sched_barrier(0);
+        const int kt = i / (2 * DT), kk = (i / DT) % 2, dt = i % DT;
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-          const half8_t vf = *reinterpret_cast<const half8_t*>(&vts[vbuf][((4 * kt + 2 * kk + hi) * D + dt * 32 + lq) * 8]);
-#pragma unroll
-          for (int qt = 0; qt < QT; ++qt)
-            o[qt][dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[kt][qt][kk], o[qt][dt], 0, 0, 0);
-        }
-    __builtin_amdgcn_s_setprio(0);
-    if (MORE) {
-      float mx_next[QT];
-      bias_max(s_next, mx_next, kbuf, BIAS_NEXT);
-#pragma unroll
-      for (int i = 0; i < 4 * DT; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, QT, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, 4 * QT, 0);
+        for (int qt = 0; qt < QT; ++qt)
+          o[qt][dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[i], pf[kt][qt][kk], o[qt][dt], 0, 0, 0);
+        if (MORE && i < 2 * QT) hm[i / QT][i % QT] = half_max(s_nxt, i / QT, i % QT);
+        __builtin_amdgcn_sched_barrier(0);
       }
+      if (MORE) {
 #pragma unroll
-      for (int qt = 0; qt < QT; ++qt) {
-        mx_cur[qt] = mx_next[qt];
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt) s_cur[kt][qt] = s_next[kt][qt];
+        for (int qt = 0; qt < QT; ++qt) {
+          const float m = fmaxf(hm[0][qt], hm[1][qt]);
+          mx_nxt[qt] = fmaxf(m, __shfl_xor(m, 32, 64));
+        }
       }
     }
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_setprio(0);
   };
   using T_ = std::integral_constant<bool, true>;
   using F_ = std::integral_constant<bool, false>;
-  // the scores of tile t+1 need the bias when t+1 >= bias_block0
-  const int tb = a.bias_block0 - 1 < ntiles - 1 ? (a.bias_block0 - 1 > 0 ? a.bias_block0 - 1 : 0) : ntiles - 1;
-  for (int t = 0; t < tb; ++t) step(t, T_{}, F_{});
-  for (int t = tb; t < ntiles - 1; ++t) step(t, T_{}, T_{});
-  step(ntiles - 1, F_{}, F_{});
+  // Steps before tb feed tiles without a key bias; tb is rounded down to even (adding the zero
+  // bias of image keys is harmless) so the first loop ends on the A buffer.
+  int tb = a.bias_block0 - 1;
+  tb = tb < 0 ? 0 : (tb > ntiles - 1 ? ntiles - 1 : tb);
+  tb &= ~1;
+  int t = 0;
+  for (; t < tb; t += 2) {
+    step(t, sA, sB, mA, mB, T_{}, F_{});
+    step(t + 1, sB, sA, mB, mA, T_{}, F_{});
+  }
+  for (; t + 2 < ntiles; t += 2) {
+    step(t, sA, sB, mA, mB, T_{}, T_{});
+    step(t + 1, sB, sA, mB, mA, T_{}, T_{});
+  }
+  if (t + 1 < ntiles) {
+    step(t, sA, sB, mA, mB, T_{}, T_{});
+    step(t + 1, sB, sA, mB, mA, F_{}, F_{});
+  } else {
+    step(t, sA, sB, mA, mB, F_{}, F_{});
+  }
 
   // ---- normalise and store: o[qt][dt][r] = O[query lq][dim dt*32 + 8(r/4) + 4hi + r%4]
 #pragma unroll
