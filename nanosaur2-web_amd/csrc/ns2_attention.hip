@@ -192,13 +192,14 @@ struct FlashArgs {
 // rescale. Any reference gives the same softmax, and p <= 2^kRebase stays in fp16 range.
 constexpr float kRebase = 8.0f;
 
-template <int D, int QT, int NW, int STAGES>
+template <int D, int QT, int NW, int STAGES, bool PP>
 __global__ __launch_bounds__(NW * 64) void flash_kernel(FlashArgs a) {
   constexpr int DC = D / 16;             // k-steps of S
   constexpr int DT = D / 32;             // dim tiles of O
   constexpr int TILE = KB * D;           // halfs per K (or V) tile image
   constexpr int BLOCKS = 2 * TILE / 512; // 1 KB direct-load blocks per stage (K then V)
   static_assert(STAGES == 3 || STAGES == 4, "three or four LDS stages");
+  static_assert(!PP || (STAGES == 4 && NW % 8 == 0), "ping-pong needs four stages and two wave groups");
 
   // K of tile t+1 and V of tile t are read while tiles t+2 .. t+STAGES-1 land
   __shared__ __attribute__((aligned(16))) half_t ks[STAGES][TILE];
@@ -226,6 +227,9 @@ __global__ __launch_bounds__(NW * 64) void flash_kernel(FlashArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int q0 = qb * (NW * QT * 32) + wave * QT * 32;
   const int lq = lane & 31, hi = lane >> 5;
+  // ping-pong wave group: odd and even waves (measured faster than halves of the block, so the
+  // two waves that share a SIMD are taken to be neighbours)
+  const int grp = wave & 1;
   const int ntiles = a.Lk_pad / KB;
 
   const half_t* Kt = a.Kc + (long long)bh * ntiles * TILE;
@@ -317,18 +321,20 @@ __global__ __launch_bounds__(NW * 64) void flash_kernel(FlashArgs a) {
     const int kt = i / (2 * DT), kk = (i / DT) % 2, dt = i % DT;
     return *reinterpret_cast<const half8_t*>(&vts[buf][((4 * kt + 2 * kk + hi) * D + dt * 32 + lq) * 8]);
   };
-  auto init_scores = [&](float16_t (&s)[2][QT]) {
+  // -m_ref in all 16 accumulator slots: the C operand of the first score MFMA of each chain
+  // (rewritten only when the reference moves)
+  float16_t minit[QT];
+  auto set_minit = [&]() {
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
+    for (int qt = 0; qt < QT; ++qt)
 #pragma unroll
-      for (int qt = 0; qt < QT; ++qt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) s[kt][qt][r] = -m_ref[qt];
+      for (int r = 0; r < 16; ++r) minit[qt][r] = -m_ref[qt];
   };
   auto qk_mfma = [&](float16_t (&s)[2][QT], int i, const half8_t& kf) {
     const int c = i / 2, kt = i % 2;
 #pragma unroll
-    for (int qt = 0; qt < QT; ++qt) s[kt][qt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[qt][c], s[kt][qt], 0, 0, 0);
+    for (int qt = 0; qt < QT; ++qt)
+      s[kt][qt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[qt][c], c == 0 ? minit[qt] : s[kt][qt], 0, 0, 0);
   };
   // per-key bias of a tile (text and padding keys)
   auto add_bias = [&](float16_t (&s)[2][QT], int buf) {
@@ -367,7 +373,9 @@ __global__ __launch_bounds__(NW * 64) void flash_kernel(FlashArgs a) {
   float16_t sA[2][QT], sB[2][QT];
   float mA[QT], mB[QT];
   for (int i = 0; i < STAGES - 1 && i < ntiles; ++i) dma(i, i);
-  {
+  if (PP) {
+    wait_newer(W0_{});
+  } else {
     // tile 0 has landed once at most the tiles issued after it remain in flight
     const int newer = (STAGES - 2 < ntiles - 1 ? STAGES - 2 : ntiles - 1);
     if (newer >= 2) wait_newer(W2_{});
@@ -375,7 +383,7 @@ __global__ __launch_bounds__(NW * 64) void flash_kernel(FlashArgs a) {
     else wait_newer(W0_{});
   }
   __syncthreads();
-  init_scores(sA);
+  set_minit();
 #pragma unroll
   for (int i = 0; i < NK; ++i) qk_mfma(sA, i, read_k(i, 0));
   if (0 >= a.bias_block0) add_bias(sA, 0);
@@ -390,10 +398,24 @@ __global__ __launch_bounds__(NW * 64) void flash_kernel(FlashArgs a) {
     constexpr bool MORE = decltype(more_c)::value;
     constexpr bool BIAS = decltype(bias_c)::value;  // tile t+1 carries a key bias
     const int vbuf = t % STAGES, kbuf = (t + 1) % STAGES;
-    if (MORE && STAGES == 4 && t + 2 < ntiles) wait_newer(W1_{});
-    else wait_newer(W0_{});
-    __syncthreads();
-    if (MORE && t + STAGES - 1 < ntiles) dma(t + STAGES - 1, (t + STAGES - 1) % STAGES);
+    // Barrier t. Without ping-pong every wave takes it at the start of the step. With
+    // ping-pong, wave group 1 (the odd waves) takes it between its phases A and B, so a group-0
+    // and a group-1 wave on one SIMD run opposite phases (one mostly VALU, one mostly MFMA). Then each wave drains its loads before the barrier (tiles up to
+    // t+2 have landed) and tile t+3 goes into the stage of tile t-1, whose last readers (phase B
+    // of step t-1 in either group) are behind the barrier.
+    auto sync = [&]() {
+      if (PP) {
+        wait_newer(W0_{});
+        __syncthreads();
+        if (t + 3 < ntiles) dma(t + 3, (t + 3) % STAGES);
+      } else {
+        if (MORE && STAGES == 4 && t + 2 < ntiles) wait_newer(W1_{});
+        else wait_newer(W0_{});
+        __syncthreads();
+        if (MORE && t + STAGES - 1 < ntiles) dma(t + STAGES - 1, (t + STAGES - 1) % STAGES);
+      }
+    };
+    if (!PP || grp == 0) sync();
 
     // ---- move the reference when a score exceeds it by more than 2^kRebase, or when nothing
     // has been accumulated yet (l = 0: the tile maximum becomes the reference, so the largest
@@ -419,6 +441,7 @@ __global__ __launch_bounds__(NW * 64) void flash_kernel(FlashArgs a) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) s_cur[kt][qt][r] -= shift;
         }
+        set_minit();
       }
     }
 
@@ -448,7 +471,6 @@ __global__ __launch_bounds__(NW * 64) void flash_kernel(FlashArgs a) {
       // K fragment i+2 is read before the MFMAs of fragment i; each slot also does its share
       // of the exp work. Scheduling barriers pin this order (the default scheduler would put
       // every read right before its MFMA to save registers).
-      init_scores(s_nxt);
       half8_t kf[NK];
       kf[0] = read_k(0, kbuf);
       kf[1] = read_k(1, kbuf);
@@ -469,6 +491,7 @@ __global__ __launch_bounds__(NW * 64) void flash_kernel(FlashArgs a) {
     for (int qt = 0; qt < QT; ++qt) l_run[qt] += ls[0][qt] + ls[1][qt];
 
     __builtin_amdgcn_sched_barrier(0);
+    if (PP && grp == 1) sync();
     // ---- phase B: O^T += V^T P^T, the DT accumulators interleaved
     if (BIAS) add_bias(s_nxt, kbuf);
     {
@@ -542,13 +565,13 @@ __global__ __launch_bounds__(NW * 64) void flash_kernel(FlashArgs a) {
   }
 }
 
-template <int D, int QT, int NW, int STAGES = 4>
+template <int D, int QT, int NW, int STAGES = 4, bool PP = true>
 void launch_flash(FlashArgs fa, hipStream_t s) {
   constexpr int BQ = NW * QT * 32;
   fa.qblocks = (fa.Lq + BQ - 1) / BQ;
   const int blocks = fa.qblocks * fa.pairs;
   fa.xcd_order = (fa.pairs % 8 == 0) ? 1 : 0;
-  flash_kernel<D, QT, NW, STAGES><<<blocks, NW * 64, 0, s>>>(fa);
+  flash_kernel<D, QT, NW, STAGES, PP><<<blocks, NW * 64, 0, s>>>(fa);
 }
 
 template <int D>
