@@ -86,10 +86,24 @@ export class Nanosaur2DiT {
   constructor(gpu, fused = true) {
     this.gpu = gpu;
     this.fused = fused;
+    this.ropeCache = new Map();  // "HxW" -> 2-D RoPE table Tensor (depends on the grid only)
+  }
+
+  // 2-D RoPE table of an h x w latent grid, built and uploaded once per grid size.
+  rope(h, w) {
+    const key = `${h}x${w}`;
+    let cs = this.ropeCache.get(key);
+    if (!cs) {
+      cs = rope2dTable(this.gpu, h, w, HD);
+      this.ropeCache.set(key, cs);
+    }
+    return cs;
   }
 
   // Release every persistent weight buffer.
   unload() {
+    for (const cs of this.ropeCache.values()) cs.release();
+    this.ropeCache.clear();
     const seen = new Set();
     const walk = (o) => {
       if (!o || typeof o !== "object" || seen.has(o)) return;
@@ -274,7 +288,7 @@ export class Nanosaur2DiT {
     const gpu = this.gpu;
     const L = h * w;
     const x = ops.linear(gpu, tokens, this.sEmbed, { name: "dit.s_embed" });
-    const cs = rope2dTable(gpu, h, w, HD);
+    const cs = this.rope(h, w);
     const c = this.condition(text, sigma);
     const total = pathDrop ? SPRINT_F + SPRINT_H : BLOCKS;
     let done = 0;
@@ -292,7 +306,6 @@ export class Nanosaur2DiT {
       d.release();
     }
     for (let i = BLOCKS - SPRINT_H; i < BLOCKS; i++) await run(i, x);
-    cs.release();
     const n = ops.normMod(gpu, x, c.final, 0, D, D);
     x.release();
     c.release();
