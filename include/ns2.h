@@ -132,7 +132,7 @@ int ns2_linear_i8_tiled(const uint16_t* At, const int8_t* Wt, const float* scale
                         const float* bias, float* C, int M, int N, int K, int ldc,
                         long long cOff, float alpha, int act, int resid, const float* gate,
                         long long gOff);
-/* Re-tile an int8 weight [N, K] row-major into Wt [N/64][K/64][4][64][16 bytes] for
+/* Re-tile an int8 weight [N, K] row-major into Wt [N/64][K/64][8][64][8 bytes] for
  * ns2_linear_i8_tiled, each byte stored biased as w + 128 (N % 64 == 0, K % 64 == 0).
  * Done once when the weight is loaded. */
 int ns2_tile_i8_weight(const int8_t* W, int8_t* Wt, int N, int K);

@@ -6,10 +6,10 @@
 //     At[ceil(M/64)][K/64][8 k-chunks][64 rows][8 halfs]       (8 KB per 64x64 tile)
 //   W (int8 ConvRot weights), re-tiled once after upload (ns2_tile_i8_weight), each byte
 //   stored biased as u = w + 128:
-//     Wt[N/64][K/64][4 k-chunks][64 rows][16 bytes]           (4 KB per 64x64 tile)
+//     Wt[N/64][K/64][8 k-chunks][64 rows][8 bytes]            (4 KB per 64x64 tile)
 // Tiles move into LDS as 1 KB blocks with direct global->LDS copies (no registers, no LDS
-// stores) into a three-stage ring, and the MFMA fragment reads are conflict-free: the 32
-// lanes of a half-wave read 32 consecutive 16-byte (A) or 8-of-16-byte (W) rows. The int8
+// stores) into a ring of LDS stages, and the MFMA fragment reads are conflict-free: the 32
+// lanes of a half-wave read 32 consecutive 16-byte (A) or 8-byte (W) rows. The int8
 // weights are decoded to fp16 as they are read from LDS into the MFMA B operand (exact:
 // half(0x6400 | u) - 1152 = w for |w| <= 128), and the per-output-row scale is applied in
 // the epilogue, in the reference's order (app/gpu/gemm.js:159-164).
@@ -54,22 +54,23 @@ __device__ __forceinline__ half8_t u8x8_to_h8(uint2 w) {
   return r;
 }
 
-__device__ __forceinline__ void epilogue(const TGemmArgs& p, int m, int n, float acc, float rs, float bi, float gt) {
+// One output: (acc * alpha) * rs + bi, activation, then store or add into the residual `old`
+// (gated by gt) in the reference's order (app/gpu/gemm.js:159-164).
+__device__ __forceinline__ void epilogue(const TGemmArgs& p, float* c, float acc, float rs, float bi, float gt, float old) {
   float r = acc * p.alpha;
   r *= rs;
   r += bi;
   r = apply_act(r, p.act);
-  float* c = p.C + p.cOff + (long long)m * p.ldc + n;
   if (!p.resid) *c = r;
-  else if (!p.gate) *c = *c + r;
-  else *c = *c + gt * r;
+  else if (!p.gate) *c = old + r;
+  else *c = old + gt * r;
 }
 
 // Block tile BM x BN (multiples of 64), BK = 64; WAVES_M x WAVES_N waves, each computing
-// (BM/WAVES_M) x (BN/WAVES_N) with v_mfma_f32_32x32x16_f16 tiles. Three LDS stages, one
-// barrier per k-tile: tile kt+2 is copied in while tile kt is multiplied, and the wait before
-// the barrier leaves tile kt+1's copies in flight.
-template <int BM, int BN, int WAVES_M, int WAVES_N, bool PIPE, int STAGES>
+// (BM/WAVES_M) x (BN/WAVES_N) with v_mfma_f32_32x32x16_f16 tiles. STAGES LDS stages, one
+// barrier per k-tile: tile kt+STAGES-1 is copied in while tile kt is multiplied (with three
+// stages the wait before the barrier leaves tile kt+1's copies in flight).
+template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, bool RESID_PRE>
 __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void gemm_tiled_kernel(TGemmArgs p) {
   constexpr int NW = WAVES_M * WAVES_N;
   constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
@@ -109,31 +110,41 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void gemm_tiled_kernel(TGem
   const int m0 = tm * BM, n0 = tn * BN;
 
   const int kblocks = p.K / 64;
-  const uint32_t as_base = lds_addr(as), ws_base = lds_addr(ws);
-  // Stage image: A blocks (8 k-chunks of 1 KB per 64-row block), then W blocks (4 per block).
-  // Block ids past the last real 64-row block re-read the last one (their rows are dropped).
-  auto dma = [&](int kt, int st) {
+  // Stage image: A blocks (8 k-chunks of 1 KB per 64-row block), then W blocks (4 per 64-row
+  // block). Block ids past the last real 64-row block re-read the last one (their rows are
+  // dropped). The per-wave sources and destinations are fixed up front; a k-tile adds its offset.
+  const char* g_src[PER_WAVE];
+  uint32_t l_dst[PER_WAVE];
+  int g_step[PER_WAVE], l_step[PER_WAVE];
+  {
+    const uint32_t as_base = lds_addr(as), ws_base = lds_addr(ws);
 #pragma unroll
     for (int i = 0; i < PER_WAVE; ++i) {
       const int j = wave + i * NW;
-      const char* src;
-      uint32_t dst;
       if (j < A_BLOCKS) {
         const int mbi = j / 8, c = j % 8;
         int mb = m0 / 64 + mbi;
         mb = mb < p.mblocks ? mb : p.mblocks - 1;
-        src = reinterpret_cast<const char*>(p.At) + (((long long)mb * kblocks + kt) * 8 + c) * 1024;
-        dst = as_base + st * (BM * 64 * 2) + j * 1024;
+        g_src[i] = reinterpret_cast<const char*>(p.At) + ((long long)mb * kblocks * 8 + c) * 1024;
+        l_dst[i] = as_base + j * 1024;
+        g_step[i] = 8 * 1024;
+        l_step[i] = BM * 64 * 2;
       } else {
         const int jw = j - A_BLOCKS;
         const int nbi = jw / 4, c = jw % 4;
         int nb = n0 / 64 + nbi;
         nb = nb < p.nblocks ? nb : p.nblocks - 1;
-        src = reinterpret_cast<const char*>(p.Wt) + (((long long)nb * kblocks + kt) * 4 + c) * 1024;
-        dst = ws_base + st * (BN * 64) + jw * 1024;
+        g_src[i] = reinterpret_cast<const char*>(p.Wt) + ((long long)nb * kblocks * 4 + c) * 1024;
+        l_dst[i] = ws_base + jw * 1024;
+        g_step[i] = 4 * 1024;
+        l_step[i] = BN * 64;
       }
-      dma16(src + lane * 16, __builtin_amdgcn_readfirstlane(dst));
     }
+  }
+  auto dma = [&](int kt, int st) {
+#pragma unroll
+    for (int i = 0; i < PER_WAVE; ++i)
+      dma16(g_src[i] + (long long)kt * g_step[i] + lane * 16, __builtin_amdgcn_readfirstlane(l_dst[i] + st * l_step[i]));
   };
 
   float16_t acc[TM][TN];
@@ -144,8 +155,41 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void gemm_tiled_kernel(TGem
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
+  // RESID_PRE (residual launches of small wave tiles): the residual outputs are loaded before
+  // the k loop, where their latency hides behind it, instead of in the epilogue. Only those
+  // launches pay for the extra registers.
+  constexpr bool PRE_C = RESID_PRE && TM * TN * 16 <= 32;
+  float cold[PRE_C ? TM : 1][PRE_C ? TN : 1][16];
+  if (PRE_C && p.resid) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int n = n0 + wn * WTN + 32 * j + lq;
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int m = m0 + wm * WTM + 32 * i + 8 * (r >> 2) + 4 * hi + (r & 3);
+          cold[PRE_C ? i : 0][PRE_C ? j : 0][r] =
+              (m < p.M && n < p.N) ? p.C[p.cOff + (long long)m * p.ldc + n] : 0.0f;
+        }
+    }
+  }
+
   dma(0, 0);
   if (STAGES == 3 && kblocks > 1) dma(1, 1);
+
+  // fragments of k-step s (16 k) of a stage: A rows wm*WTM + 32i + lq, k 16s + 8hi .. +7 (chunk
+  // 2s + hi); W columns wn*WTN + 32j + lq, the same k (8-byte chunk 2s + hi)
+  auto read_a = [&](int st, int s, int i) {
+    const int row = wm * WTM + 32 * i;
+    const int mbi = row / 64, r0 = row % 64;
+    return *reinterpret_cast<const half8_t*>(&as[st][((mbi * 8 + 2 * s + hi) * 64 + r0 + lq) * 8]);
+  };
+  auto read_w = [&](int st, int s, int j) {
+    const int col = wn * WTN + 32 * j;
+    const int nbi = col / 64, c0 = col % 64;
+    return *reinterpret_cast<const uint2*>(&ws[st][((nbi * 8 + 2 * s + hi) * 64 + c0 + lq) * 8]);
+  };
 
   for (int kt = 0; kt < kblocks; ++kt) {
     const int st = kt % STAGES;
@@ -157,74 +201,39 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void gemm_tiled_kernel(TGem
     __syncthreads();
     if (kt + STAGES - 1 < kblocks) dma(kt + STAGES - 1, (kt + STAGES - 1) % STAGES);
     __builtin_amdgcn_s_setprio(1);
-    if constexpr (PIPE) {
-      // k-steps of 16, software-pipelined inside the k-tile: fragments are read from LDS two
-      // steps ahead and the weights decoded one step ahead, interleaved with the MFMAs.
-      half8_t a[3][TM];
-      uint2 w[3][TN];
-      half8_t b[2][TN];
-      auto read = [&](int s, int slot) {
+    // k-steps of 16, software-pipelined: fragments read two steps ahead, the weights decoded
+    // one step ahead, behind the MFMAs; scheduling barriers pin the order (the default
+    // scheduler would put every read right before its use to save registers)
+    half8_t a[3][TM], b[2][TN];
+    uint2 w[3][TN];
 #pragma unroll
-        for (int i = 0; i < TM; ++i) {
-          const int row = wm * WTM + 32 * i;
-          const int mbi = row / 64, r0 = row % 64;
-          a[slot][i] = *reinterpret_cast<const half8_t*>(&as[st][((mbi * 8 + 2 * s + hi) * 64 + r0 + lq) * 8]);
-        }
+    for (int s = 0; s < 2; ++s) {
 #pragma unroll
-        for (int j = 0; j < TN; ++j) {
-          const int col = wn * WTN + 32 * j;
-          const int nbi = col / 64, c0 = col % 64;
-          w[slot][j] = *reinterpret_cast<const uint2*>(&ws[st][((nbi * 4 + s) * 64 + c0 + lq) * 16 + 8 * hi]);
-        }
-      };
-      read(0, 0);
-      read(1, 1);
+      for (int i = 0; i < TM; ++i) a[s][i] = read_a(st, s, i);
 #pragma unroll
-      for (int j = 0; j < TN; ++j) b[0][j] = u8x8_to_h8(w[0][j]);
+      for (int j = 0; j < TN; ++j) w[s][j] = read_w(st, s, j);
+    }
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        if (s + 2 < 4) read(s + 2, (s + 2) % 3);
-        if (s + 1 < 4) {
+    for (int j = 0; j < TN; ++j) b[0][j] = u8x8_to_h8(w[0][j]);
 #pragma unroll
-          for (int j = 0; j < TN; ++j) b[(s + 1) & 1][j] = u8x8_to_h8(w[(s + 1) % 3][j]);
-        }
+    for (int s = 0; s < 4; ++s) {
+      if (s + 2 < 4) {
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
+        for (int i = 0; i < TM; ++i) a[(s + 2) % 3][i] = read_a(st, s + 2, i);
 #pragma unroll
-          for (int j = 0; j < TN; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[s % 3][i], b[s & 1][j], acc[i][j], 0, 0, 0);
-        // per MFMA: one LDS read and a share of the decode VALU work
-        constexpr int NMF = TM * TN, NRD = TM + TN, NVALU = TN * 8;
-#pragma unroll
-        for (int q = 0; q < NMF; ++q) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                       // MFMA
-          if (q < NRD && s + 2 < 4) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
-          if (s + 1 < 4) __builtin_amdgcn_sched_group_barrier(0x002, (NVALU + NMF - 1) / NMF, 0);  // VALU
-        }
+        for (int j = 0; j < TN; ++j) w[(s + 2) % 3][j] = read_w(st, s + 2, j);
       }
-    } else {
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {  // k-steps of 16
-      half8_t a[TM], b[TN];
-#pragma unroll
-      for (int i = 0; i < TM; ++i) {
-        const int row = wm * WTM + 32 * i;  // within the block tile
-        const int mbi = row / 64, r0 = row % 64;
-        a[i] = *reinterpret_cast<const half8_t*>(&as[st][((mbi * 8 + 2 * s + hi) * 64 + r0 + lq) * 8]);
-      }
-#pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        const int col = wn * WTN + 32 * j;
-        const int nbi = col / 64, c0 = col % 64;
-        const uint2 w8 = *reinterpret_cast<const uint2*>(&ws[st][((nbi * 4 + s) * 64 + c0 + lq) * 16 + 8 * hi]);
-        b[j] = u8x8_to_h8(w8);
-      }
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc[i][j], 0, 0, 0);
-    }
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[s % 3][i], b[s & 1][j], acc[i][j], 0, 0, 0);
+      if (s + 1 < 4) {
+#pragma unroll
+        for (int j = 0; j < TN; ++j) b[(s + 1) & 1][j] = u8x8_to_h8(w[(s + 1) % 3][j]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
     __builtin_amdgcn_s_setprio(0);
   }
@@ -242,58 +251,64 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void gemm_tiled_kernel(TGem
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int m = m0 + wm * WTM + 32 * i + 8 * (r >> 2) + 4 * hi + (r & 3);
-        if (m < p.M) epilogue(p, m, n, acc[i][j][r], rs, bi, gt);
+        if (m >= p.M) continue;
+        float* c = p.C + p.cOff + (long long)m * p.ldc + n;
+        const float old = !p.resid ? 0.0f : (PRE_C ? cold[PRE_C ? i : 0][PRE_C ? j : 0][r] : *c);
+        epilogue(p, c, acc[i][j][r], rs, bi, gt, old);
       }
   }
 }
 
-// W [N, K] row-major int8 -> Wt tiles of biased bytes (w + 128); one thread per 16-byte chunk.
+// W [N, K] row-major int8 -> Wt tiles [N/64][K/64][8 k-chunks of 8][64 rows][8 bytes] of biased
+// bytes (w + 128); one thread per 8-byte chunk.
 __global__ __launch_bounds__(256) void tile_w_kernel(const int8_t* __restrict__ W, uint8_t* __restrict__ Wt,
                                                       int N, int K) {
   const long long i = (long long)blockIdx.x * 256 + threadIdx.x;  // output chunk index
-  const long long chunks = (long long)N * K / 16;
+  const long long chunks = (long long)N * K / 8;
   if (i >= chunks) return;
-  // chunk order: [nb][kb][c 0..3][row 0..63]
+  // chunk order: [nb][kb][c 0..7][row 0..63]
   const int row = (int)(i % 64);
-  const int c = (int)((i / 64) % 4);
-  const long long rest = i / 256;  // nb * (K/64) + kb
+  const int c = (int)((i / 64) % 8);
+  const long long rest = i / 512;  // nb * (K/64) + kb
   const int kb = (int)(rest % (K / 64));
   const int nb = (int)(rest / (K / 64));
-  const int n = nb * 64 + row, kc = kb * 4 + c;
-  uint4 v = *reinterpret_cast<const uint4*>(W + (long long)n * K + kc * 16);
+  const int n = nb * 64 + row;
+  uint2 v = *reinterpret_cast<const uint2*>(W + (long long)n * K + kb * 64 + c * 8);
   v.x ^= 0x80808080u;
   v.y ^= 0x80808080u;
-  v.z ^= 0x80808080u;
-  v.w ^= 0x80808080u;
-  *reinterpret_cast<uint4*>(Wt + i * 16) = v;
+  *reinterpret_cast<uint2*>(Wt + i * 8) = v;
 }
 
-template <int BM, int BN, int WM, int WN, bool PIPE = false, int STAGES = 3>
+template <int BM, int BN, int WM, int WN, int STAGES = 2>
 int launch_tiled(TGemmArgs p) {
   p.tiles_m = (p.M + BM - 1) / BM;
   p.tiles_n = (p.N + BN - 1) / BN;
-  gemm_tiled_kernel<BM, BN, WM, WN, PIPE, STAGES><<<p.tiles_m * p.tiles_n, WM * WN * 64, 0, ns2::stream()>>>(p);
+  constexpr bool can_pre = (BM / WM / 32) * (BN / WN / 32) * 16 <= 32;
+  if (can_pre && p.resid)
+    gemm_tiled_kernel<BM, BN, WM, WN, STAGES, can_pre><<<p.tiles_m * p.tiles_n, WM * WN * 64, 0, ns2::stream()>>>(p);
+  else
+    gemm_tiled_kernel<BM, BN, WM, WN, STAGES, false><<<p.tiles_m * p.tiles_n, WM * WN * 64, 0, ns2::stream()>>>(p);
   NS2_LAUNCHED("gemm_tiled");
   return NS2_OK;
 }
 
-// Block-tile configurations (two LDS stages each): BM x BN, the waves' layout, and a per-CU
-// throughput factor fitted to measurements at the DiT shapes (3952 x {4608, 1536, 8192} x
-// {1536, 4096}, 256 x 3072 x 1536). Layouts with one wave row decode each weight fragment once.
+// Block-tile configurations (two LDS stages each): BM x BN, the waves' layout, and two
+// throughput figures fitted to measurements at the DiT shapes (3952 x {4608, 1536, 8192} x
+// {1536, 4096}, 256 x 3072 x 1536), in tile-area units per microsecond at K = 1536: `rate`
+// with the CUs full, `alone` for a CU that runs a single tile of this shape.
 struct TileCfg {
   int bm, bn;
-  float rate;
+  float rate, alone;
 };
 constexpr TileCfg kCfgs[] = {
-    {128, 256, 1.00f},  // 16 waves (2 x 8) of 64x32, 64 KB LDS
-    {64, 256, 0.95f},   // 8 waves (1 x 8) of 64x32, 48 KB
-    {64, 128, 0.70f},   // 4 waves (1 x 4) of 64x32, 32 KB
-    {64, 64, 0.40f},    // 4 waves (2 x 2) of 32x32, 24 KB: few rows (text tokens)
+    {256, 256, 1154.f, 1587.f},  // 16 waves (4 x 4) of 64x64, 96 KB LDS
+    {64, 128, 950.f, 532.f},     // 4 waves (1 x 4) of 64x32, 32 KB: each weight fragment decoded once
+    {64, 64, 350.f, 347.f},      // 4 waves (2 x 2) of 32x32, 24 KB: few rows (text tokens)
 };
 constexpr int kCUs = 256;
 
-// Estimated time: the tiles the busiest CU runs, times the work of a tile over its rate.
-// The configuration with the least estimate is used.
+// Estimated time: the tiles the busiest CU runs times the tile area over the full-CU rate, but
+// never less than one tile running alone. The configuration with the least estimate is used.
 int pick_config(int M, int N) {
   int best = -1;
   double best_t = 0;
@@ -301,7 +316,9 @@ int pick_config(int M, int N) {
     const TileCfg& c = kCfgs[i];
     const long long tiles = (long long)((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn);
     const long long per_cu = (tiles + kCUs - 1) / kCUs;
-    const double t = (double)per_cu * c.bm * c.bn / c.rate;
+    const double area = (double)c.bm * c.bn;
+    double t = per_cu * area / c.rate;
+    if (t < area / c.alone) t = area / c.alone;
     if (best < 0 || t < best_t) {
       best = i;
       best_t = t;
@@ -321,7 +338,7 @@ int ns2_tile_i8_weight(const int8_t* W, int8_t* Wt, int N, int K) {
   NS2_REQUIRE(W && Wt && aligned16(W) && aligned16(Wt), "ns2_tile_i8_weight: null or unaligned buffer");
   NS2_REQUIRE(N > 0 && K > 0 && N % 64 == 0 && K % 64 == 0,
               "ns2_tile_i8_weight: N=%d and K=%d must be multiples of 64", N, K);
-  const long long chunks = (long long)N * K / 16;
+  const long long chunks = (long long)N * K / 8;
   ns2::ProfScope prof_("tile_i8_weight");
   tile_w_kernel<<<(unsigned)((chunks + 255) / 256), 256, 0, ns2::stream()>>>(W, reinterpret_cast<uint8_t*>(Wt), N, K);
   NS2_LAUNCHED("tile_i8_weight");
@@ -343,10 +360,9 @@ int ns2_linear_i8_tiled(const uint16_t* At, const int8_t* Wt, const float* scale
               cOff, gOff, M, N, K, ldc, (M + 63) / 64, N / 64, 0, 0, alpha, act, resid};
   ns2::ProfScope prof_("gemm_i8_tiled");
   switch (pick_config(M, N)) {
-    case 0: return launch_tiled<128, 256, 2, 8, true, 2>(p);
-    case 1: return launch_tiled<64, 256, 1, 8, true, 2>(p);
-    case 2: return launch_tiled<64, 128, 1, 4, true, 2>(p);
-    default: return launch_tiled<64, 64, 2, 2, true, 2>(p);
+    case 0: return launch_tiled<256, 256, 4, 4>(p);
+    case 1: return launch_tiled<64, 128, 1, 4>(p);
+    default: return launch_tiled<64, 64, 2, 2>(p);
   }
 }
 

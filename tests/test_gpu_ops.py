@@ -40,8 +40,8 @@ def untile_a(t, M, K):
 
 
 def untile_w(t, N, K):
-    """Tiled weight [N/64][K/64][4][64][16] of biased bytes (w + 128) -> row-major int8 [N, K]."""
-    u = t.view(torch.uint8).reshape(N // 64, K // 64, 4, 64, 16).permute(0, 3, 1, 2, 4).reshape(N, K)
+    """Tiled weight [N/64][K/64][8][64][8] of biased bytes (w + 128) -> row-major int8 [N, K]."""
+    u = t.view(torch.uint8).reshape(N // 64, K // 64, 8, 64, 8).permute(0, 3, 1, 2, 4).reshape(N, K)
     return (u.to(torch.int16) - 128).to(torch.int8)
 
 
