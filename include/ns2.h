@@ -136,6 +136,18 @@ int ns2_linear_i8_tiled(const uint16_t* At, const int8_t* Wt, const float* scale
  * ns2_linear_i8_tiled, each byte stored biased as w + 128 (N % 64 == 0, K % 64 == 0).
  * Done once when the weight is loaded. */
 int ns2_tile_i8_weight(const int8_t* W, int8_t* Wt, int N, int K);
+/* The GLU MLP's first linear fused with the GLU and the rotation of its output (fused DiT
+ * path): with h = (At Wt^T) * alpha * scale + bias (N = 2I columns), writes
+ * Y = rotate(act(h[:, :I]) * h[:, I:]) as the tiled fp16 operand of the next int8 linear
+ * (ceil(M/64)*64 rows of I columns). Replaces ops.linear (app/gpu/ops.js:46-66) + ops.glu
+ * (ops.js:140-148) + ops.rotate (ops.js:37-44) on the MLP path (app/models/nanosaur2.js:142-152).
+ * Wt must come from ns2_tile_i8_weight_glu. N % 512 == 0, K % 256 == 0. */
+int ns2_linear_i8_glu_rot_tiled(const uint16_t* At, const int8_t* Wt, const float* scale,
+                                const float* bias, uint16_t* Y, int M, int N, int K, float alpha,
+                                int act);
+/* ns2_tile_i8_weight for ns2_linear_i8_glu_rot_tiled: tiled row 64q + t holds weight row
+ * 32q + t (t < 32) or N/2 + 32q + t - 32 (t >= 32), pairing the two GLU halves. */
+int ns2_tile_i8_weight_glu(const int8_t* W, int8_t* Wt, int N, int K);
 /* bf16 weights (gemm.js:98-118), fp32 activations [M, lda]. Requires K % 16 == 0. */
 int ns2_linear_bf16(const float* A, int lda, const uint16_t* W, const float* bias,
                     const float* add, float* C, int M, int N, int K, int ldc, long long cOff,

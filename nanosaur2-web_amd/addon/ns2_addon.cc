@@ -352,6 +352,30 @@ napi_value TileI8Weight(napi_env env, napi_callback_info info) {
   return check(env, c, c.failed ? 0 : ns2_tile_i8_weight(W, Wt, N, K));
 }
 
+// tileI8WeightGlu(W, Wt, N, K)
+napi_value TileI8WeightGlu(napi_env env, napi_callback_info info) {
+  ARGS(4);
+  auto W = (const int8_t*)c.ptr(0);
+  auto Wt = (int8_t*)c.ptr(1);
+  int N = c.i32(2), K = c.i32(3);
+  return check(env, c, c.failed ? 0 : ns2_tile_i8_weight_glu(W, Wt, N, K));
+}
+
+// linearI8GluRotTiled(At, Wt, scale, bias, Y, M, N, K, alpha, act)
+napi_value LinearI8GluRotTiled(napi_env env, napi_callback_info info) {
+  ARGS(10);
+  auto At = (const uint16_t*)c.ptr(0);
+  auto Wt = (const int8_t*)c.ptr(1);
+  auto scale = (const float*)c.ptr(2);
+  auto bias = (const float*)c.ptr(3);
+  auto Y = (uint16_t*)c.ptr(4);
+  int M = c.i32(5), N = c.i32(6), K = c.i32(7);
+  float alpha = c.f32(8);
+  int act = c.i32(9);
+  if (c.failed) return nullptr;
+  return check(env, c, ns2_linear_i8_glu_rot_tiled(At, Wt, scale, bias, Y, M, N, K, alpha, act));
+}
+
 // linearI8Tiled(At, Wt, scale, bias, C, M, N, K, ldc, cOff, alpha, act, resid, gate, gOff)
 napi_value LinearI8Tiled(napi_env env, napi_callback_info info) {
   ARGS(15);
@@ -540,6 +564,7 @@ napi_value Module(napi_env env, napi_value exports) {
       {"eventDestroy", EventDestroy}, {"profileEnable", ProfileEnable}, {"profileReset", ProfileReset},
       {"profileReport", ProfileReport}, {"hadamard256", Hadamard256}, {"rotateF16", RotateF16},
       {"tileI8Weight", TileI8Weight}, {"linearI8Tiled", LinearI8Tiled},
+      {"tileI8WeightGlu", TileI8WeightGlu}, {"linearI8GluRotTiled", LinearI8GluRotTiled},
       {"linearI8", LinearI8}, {"linearBf16", LinearBf16}, {"attention", Attention},
       {"headNorm", HeadNorm}, {"normMod", NormModT<false>}, {"normModRotateF16", NormModT<true>},
       {"glu", GluT<false>}, {"gluRotateF16", GluT<true>}, {"elementwise", Elementwise},

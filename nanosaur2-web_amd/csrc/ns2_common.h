@@ -131,6 +131,12 @@ __device__ __forceinline__ uint32_t pack_half2(float a, float b) {
   return __builtin_bit_cast(uint32_t, h);
 }
 
+// Offset (in halfs) of element (m, k) of an fp16 GEMM operand with K columns in the tiled
+// layout of the int8 GEMM: [M/64][K/64][8 k-chunks][64 rows][8 halfs] (ns2_linear_i8_tiled).
+__device__ __forceinline__ long long tiled_off(long long m, int k, int K) {
+  return (((m >> 6) * (K >> 6) + (k >> 6)) * 8 + ((k & 63) >> 3)) * 512 + (m & 63) * 8 + (k & 7);
+}
+
 // LDS byte address of a pointer into a __shared__ array, as a wave-uniform value.
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return __builtin_amdgcn_readfirstlane(

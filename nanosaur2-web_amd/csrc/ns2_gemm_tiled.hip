@@ -25,6 +25,7 @@ struct TGemmArgs {
   const float* scale;
   const float* bias;
   float* C;
+  uint16_t* Y;  // GLU epilogue: rotated fp16 output in the tiled layout, N/2 columns
   const float* gate;
   long long cOff, gOff;
   int M, N, K, ldc;
@@ -70,7 +71,11 @@ __device__ __forceinline__ void epilogue(const TGemmArgs& p, float* c, float acc
 // (BM/WAVES_M) x (BN/WAVES_N) with v_mfma_f32_32x32x16_f16 tiles. STAGES LDS stages, one
 // barrier per k-tile: tile kt+STAGES-1 is copied in while tile kt is multiplied (with three
 // stages the wait before the barrier leaves tile kt+1's copies in flight).
-template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, bool RESID_PRE>
+// EPI 0: C = epilogue(A W^T). EPI 1 (GLU): W's rows are interleaved in 32-row blocks
+// (ns2_tile_i8_weight_glu), so the 64 columns of a wave hold 32 columns of each GLU half; the
+// block's 512 columns give 256 consecutive outputs act(h1) * h2, one rotation group, which is
+// rotated and written to Y as the tiled fp16 operand of the next int8 linear.
+template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, bool RESID_PRE, int EPI>
 __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void gemm_tiled_kernel(TGemmArgs p) {
   constexpr int NW = WAVES_M * WAVES_N;
   constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
@@ -238,6 +243,53 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void gemm_tiled_kernel(TGem
     __builtin_amdgcn_s_setprio(0);
   }
 
+  if constexpr (EPI == 1) {
+    // ---- GLU + rotation epilogue (BM = 64, BN = 512, one wave row, 64 columns per wave)
+    static_assert(BM == 64 && BN == 512 && WAVES_M == 1 && TM == 2 && TN == 2, "GLU epilogue tile");
+    const int I = p.N / 2;
+    const int gb = n0 / 2;            // first output (GLU) column of the block
+    const int gc = 32 * wn + lq;      // this lane's output column within the block
+    const int G = gb + gc;
+    const float s1 = p.scale[G], s2 = p.scale[I + G];
+    const float b1 = p.bias ? p.bias[G] : 0.0f, b2 = p.bias ? p.bias[I + G] : 0.0f;
+    __syncthreads();  // every wave is done with the LDS stages
+    float* T = reinterpret_cast<float*>(&ws[0][0]);  // [64 rows][256 columns] fp32 = the W stages
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = 32 * i + 8 * (r >> 2) + 4 * hi + (r & 3);
+        // the linear's epilogue order (no activation there), then the GLU
+        float h1 = acc[i][0][r] * p.alpha;
+        h1 *= s1;
+        h1 += b1;
+        float h2 = acc[i][1][r] * p.alpha;
+        h2 *= s2;
+        h2 += b2;
+        T[row * 256 + gc] = apply_act(h1, p.act) * h2;
+      }
+    __syncthreads();
+    // rotation: wave w rotates rows 8w .. 8w+7, the fp16 result in place at the row's start
+#pragma unroll
+    for (int rr = 0; rr < 64 / NW; ++rr) {
+      const int row = (64 / NW) * wave + rr;
+      const float4 in = *reinterpret_cast<const float4*>(T + row * 256 + lane * 4);
+      float v[4] = {in.x, in.y, in.z, in.w};
+      fwht256_wave(v);
+      uint2 o;
+      o.x = pack_half2(v[0], v[1]);
+      o.y = pack_half2(v[2], v[3]);
+      *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(T + row * 256) + lane * 4) = o;
+    }
+    __syncthreads();
+    // 32 chunks of 8 columns x 64 rows: 1 KB contiguous each in the tiled layout
+    for (int q = tid; q < 32 * 64; q += NW * 64) {
+      const int row = q % 64, c = q / 64;
+      const uint4 v = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(T + row * 256) + c * 8);
+      *reinterpret_cast<uint4*>(p.Y + tiled_off(m0 + row, gb + c * 8, I)) = v;
+    }
+    return;
+  }
   // epilogue: acc[i][j][r] = C[m0 + wm*WTM + 32i + 8(r/4) + 4hi + r%4][n0 + wn*WTN + 32j + lq]
 #pragma unroll
   for (int j = 0; j < TN; ++j) {
@@ -262,7 +314,7 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void gemm_tiled_kernel(TGem
 // W [N, K] row-major int8 -> Wt tiles [N/64][K/64][8 k-chunks of 8][64 rows][8 bytes] of biased
 // bytes (w + 128); one thread per 8-byte chunk.
 __global__ __launch_bounds__(256) void tile_w_kernel(const int8_t* __restrict__ W, uint8_t* __restrict__ Wt,
-                                                      int N, int K) {
+                                                      int N, int K, int glu) {
   const long long i = (long long)blockIdx.x * 256 + threadIdx.x;  // output chunk index
   const long long chunks = (long long)N * K / 8;
   if (i >= chunks) return;
@@ -272,22 +324,25 @@ __global__ __launch_bounds__(256) void tile_w_kernel(const int8_t* __restrict__ 
   const long long rest = i / 512;  // nb * (K/64) + kb
   const int kb = (int)(rest % (K / 64));
   const int nb = (int)(rest / (K / 64));
-  const int n = nb * 64 + row;
+  int n = nb * 64 + row;
+  // GLU interleave: tiled row 64q + t holds row 32q + t of the first half (t < 32) or row
+  // N/2 + 32q + t - 32 of the second half
+  if (glu) n = row < 32 ? 32 * nb + row : N / 2 + 32 * nb + row - 32;
   uint2 v = *reinterpret_cast<const uint2*>(W + (long long)n * K + kb * 64 + c * 8);
   v.x ^= 0x80808080u;
   v.y ^= 0x80808080u;
   *reinterpret_cast<uint2*>(Wt + i * 8) = v;
 }
 
-template <int BM, int BN, int WM, int WN, int STAGES = 2>
+template <int BM, int BN, int WM, int WN, int STAGES = 2, int EPI = 0>
 int launch_tiled(TGemmArgs p) {
   p.tiles_m = (p.M + BM - 1) / BM;
   p.tiles_n = (p.N + BN - 1) / BN;
-  constexpr bool can_pre = (BM / WM / 32) * (BN / WN / 32) * 16 <= 32;
+  constexpr bool can_pre = EPI == 0 && (BM / WM / 32) * (BN / WN / 32) * 16 <= 32;
   if (can_pre && p.resid)
-    gemm_tiled_kernel<BM, BN, WM, WN, STAGES, can_pre><<<p.tiles_m * p.tiles_n, WM * WN * 64, 0, ns2::stream()>>>(p);
+    gemm_tiled_kernel<BM, BN, WM, WN, STAGES, can_pre, EPI><<<p.tiles_m * p.tiles_n, WM * WN * 64, 0, ns2::stream()>>>(p);
   else
-    gemm_tiled_kernel<BM, BN, WM, WN, STAGES, false><<<p.tiles_m * p.tiles_n, WM * WN * 64, 0, ns2::stream()>>>(p);
+    gemm_tiled_kernel<BM, BN, WM, WN, STAGES, false, EPI><<<p.tiles_m * p.tiles_n, WM * WN * 64, 0, ns2::stream()>>>(p);
   NS2_LAUNCHED("gemm_tiled");
   return NS2_OK;
 }
@@ -340,9 +395,36 @@ int ns2_tile_i8_weight(const int8_t* W, int8_t* Wt, int N, int K) {
               "ns2_tile_i8_weight: N=%d and K=%d must be multiples of 64", N, K);
   const long long chunks = (long long)N * K / 8;
   ns2::ProfScope prof_("tile_i8_weight");
-  tile_w_kernel<<<(unsigned)((chunks + 255) / 256), 256, 0, ns2::stream()>>>(W, reinterpret_cast<uint8_t*>(Wt), N, K);
+  tile_w_kernel<<<(unsigned)((chunks + 255) / 256), 256, 0, ns2::stream()>>>(W, reinterpret_cast<uint8_t*>(Wt), N, K, 0);
   NS2_LAUNCHED("tile_i8_weight");
   return NS2_OK;
+}
+
+int ns2_tile_i8_weight_glu(const int8_t* W, int8_t* Wt, int N, int K) {
+  NS2_READY();
+  NS2_REQUIRE(W && Wt && aligned16(W) && aligned16(Wt), "ns2_tile_i8_weight_glu: null or unaligned buffer");
+  NS2_REQUIRE(N > 0 && K > 0 && N % 64 == 0 && K % 64 == 0,
+              "ns2_tile_i8_weight_glu: N=%d and K=%d must be multiples of 64", N, K);
+  const long long chunks = (long long)N * K / 8;
+  ns2::ProfScope prof_("tile_i8_weight");
+  tile_w_kernel<<<(unsigned)((chunks + 255) / 256), 256, 0, ns2::stream()>>>(W, reinterpret_cast<uint8_t*>(Wt), N, K, 1);
+  NS2_LAUNCHED("tile_i8_weight_glu");
+  return NS2_OK;
+}
+
+int ns2_linear_i8_glu_rot_tiled(const uint16_t* At, const int8_t* Wt, const float* scale, const float* bias,
+                                uint16_t* Y, int M, int N, int K, float alpha, int act) {
+  NS2_READY();
+  if (M == 0) return NS2_OK;
+  NS2_REQUIRE(At && Wt && scale && Y, "ns2_linear_i8_glu_rot_tiled: null At, Wt, scale or Y");
+  NS2_REQUIRE(M > 0 && N > 0 && N % 512 == 0 && K > 0 && K % 256 == 0,
+              "ns2_linear_i8_glu_rot_tiled: M=%d N=%d K=%d (N %% 512 == 0, K %% 256 == 0 required)", M, N, K);
+  NS2_REQUIRE(aligned16(At) && aligned16(Wt) && aligned16(Y), "ns2_linear_i8_glu_rot_tiled: operands must be 16-byte aligned");
+  NS2_REQUIRE(act >= NS2_ACT_NONE && act <= NS2_ACT_GELU_TANH, "ns2_linear_i8_glu_rot_tiled: unknown act %d", act);
+  TGemmArgs p{reinterpret_cast<const half_t*>(At), reinterpret_cast<const uint8_t*>(Wt), scale, bias, nullptr, Y,
+              nullptr, 0, 0, M, N, K, N, (M + 63) / 64, N / 64, 0, 0, alpha, act, 0};
+  ns2::ProfScope prof_("gemm_i8_glu_rot");
+  return launch_tiled<64, 512, 1, 8, 2, 1>(p);
 }
 
 int ns2_linear_i8_tiled(const uint16_t* At, const int8_t* Wt, const float* scale, const float* bias,
@@ -356,7 +438,7 @@ int ns2_linear_i8_tiled(const uint16_t* At, const int8_t* Wt, const float* scale
   NS2_REQUIRE(ldc >= N && cOff >= 0 && gOff >= 0, "ns2_linear_i8_tiled: bad ldc/offsets");
   NS2_REQUIRE(aligned16(At) && aligned16(Wt), "ns2_linear_i8_tiled: operands must be 16-byte aligned");
   NS2_REQUIRE(act >= NS2_ACT_NONE && act <= NS2_ACT_GELU_TANH, "ns2_linear_i8_tiled: unknown act %d", act);
-  TGemmArgs p{reinterpret_cast<const half_t*>(At), reinterpret_cast<const uint8_t*>(Wt), scale, bias, C, gate,
+  TGemmArgs p{reinterpret_cast<const half_t*>(At), reinterpret_cast<const uint8_t*>(Wt), scale, bias, C, nullptr, gate,
               cOff, gOff, M, N, K, ldc, (M + 63) / 64, N / 64, 0, 0, alpha, act, resid};
   ns2::ProfScope prof_("gemm_i8_tiled");
   switch (pick_config(M, N)) {

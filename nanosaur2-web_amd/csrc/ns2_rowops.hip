@@ -20,12 +20,6 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
   return t;
 }
 
-// Offset (in halfs) of element (m, k) of an fp16 GEMM operand with K columns in the tiled
-// layout of the int8 GEMM: [M/64][K/64][8 k-chunks][64 rows][8 halfs] (ns2_linear_i8_tiled).
-__device__ __forceinline__ long long tiled_off(long long m, int k, int K) {
-  return (((m >> 6) * (K >> 6) + (k >> 6)) * 8 + ((k & 63) >> 3)) * 512 + (m & 63) * 8 + (k & 7);
-}
-
 // Store 4 consecutive rotated values (k..k+3, k % 4 == 0) as fp16, row-major or tiled.
 __device__ __forceinline__ void store4_f16(uint16_t* __restrict__ y, long long m, int k, int ldy, int K,
                                            int tiled, const float v[4]) {

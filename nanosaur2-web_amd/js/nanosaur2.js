@@ -77,7 +77,10 @@ export class Nanosaur2DiT {
     if (fused) {
       // the fused producers feed the block linears tiled operands: re-tile their weights once
       for (const b of m.text.concat(m.blocks)) {
-        for (const W of [b.qkv, b.kvY, b.proj, b.w12, b.w3]) if (W && ops.tileable(W)) ops.tileWeight(gpu, W);
+        for (const W of [b.qkv, b.kvY, b.proj, b.w3]) if (W && ops.tileable(W)) ops.tileWeight(gpu, W);
+        // the MLP's first linear runs fused with its GLU and the rotation for w3
+        if (b.w12.kind === "i8" && b.w12.N % 512 === 0 && b.w12.K % 256 === 0) ops.tileWeightGlu(gpu, b.w12);
+        else if (ops.tileable(b.w12)) ops.tileWeight(gpu, b.w12);
       }
     }
     return m;
@@ -159,6 +162,14 @@ export class Nanosaur2DiT {
   // x += gate_mlp * w3(silu(x1) * x2), [x1 x2] = w12(modulate(norm2(x))) (app/models/nanosaur2.js:142-152)
   mlp(x, b, mod) {
     const gpu = this.gpu;
+    if (this.fused && b.w12.tglu && b.w3.tbuf) {
+      const nr = ops.normModRotated(gpu, x, mod, 3 * D, 4 * D, D, b.n2, 1e-6, true);
+      const gr = ops.linearGluRotated(gpu, nr, b.w12, "silu", "dit.mlp.w12");
+      nr.release();
+      ops.linear(gpu, null, b.w3, { xr: gr, out: x, resid: true, gate: mod, gOff: 5 * D, name: "dit.mlp.w3" });
+      gr.release();
+      return;
+    }
     if (this.fused) {
       const nr = ops.normModRotated(gpu, x, mod, 3 * D, 4 * D, D, b.n2, 1e-6, !!b.w12.tbuf);
       const h = ops.linear(gpu, null, b.w12, { xr: nr, name: "dit.mlp.w12" });

@@ -54,6 +54,29 @@ export function tileWeight(gpu, W) {
   return W;
 }
 
+// Re-tile the GLU MLP's first int8 weight [2I, K] with its two halves interleaved (W.tglu),
+// for linearGluRotated.
+export function tileWeightGlu(gpu, W) {
+  if (W.kind !== "i8" || W.N % 512 !== 0 || W.K % 256 !== 0) throw new Error(`${W.name}: [${W.N}, ${W.K}] cannot take the fused GLU path`);
+  if (W.tglu) return W;
+  const ptr = native.malloc(W.N * W.K);
+  W.tglu = new DeviceBuffer(ptr, W.N * W.K, false);
+  gpu.run("tile_i8_weight", 0, () => native.tileI8WeightGlu(addr(W.buf), addr(W.tglu), W.N, W.K));
+  return W;
+}
+
+// glu(linear(x, W), act) rotated, as the tiled fp16 operand of the next int8 linear: one
+// kernel for ops.linear + ops.glu + ops.rotate of the MLP (app/gpu/ops.js:46-66, 140-148,
+// 37-44). xr is a tiled operand (normModRotated(..., tiled = true)).
+export function linearGluRotated(gpu, xr, W, act, name = "gemm.i8.glu") {
+  if (!xr.tiled || !W.tglu) throw new Error(`${W.name}: linearGluRotated needs a tiled operand and tileWeightGlu`);
+  const M = xr.rows, I = W.N / 2;
+  const y = rotatedOperand(gpu, M, I, true);
+  gpu.run(name, 2 * M * W.N * W.K, () =>
+    native.linearI8GluRotTiled(addr(xr), addr(W.tglu), addr(W.scale), addr(W.bias || null), addr(y), M, W.N, W.K, 1, ACT[act]));
+  return y;
+}
+
 // y = x @ W^T (+ bias) (act) (app/gpu/ops.js:46-66). opts: out, resid, gate, gOff, ldc, cOff,
 // bias, act, xr (pre-rotated input of an int8 weight: fp32 from rotate() or fp16 from a fused
 // producer), name. x may be null when xr is given.

@@ -50,6 +50,8 @@ SIGNATURES = {
     "ns2_linear_i8_tiled": [c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_ll, c_float,
                             c_int, c_int, c_vp, c_ll],
     "ns2_tile_i8_weight": [c_vp, c_vp, c_int, c_int],
+    "ns2_tile_i8_weight_glu": [c_vp, c_vp, c_int, c_int],
+    "ns2_linear_i8_glu_rot_tiled": [c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_float, c_int],
     "ns2_linear_i8": [c_vp, c_int, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int,
                       c_ll, c_float, c_int, c_int, c_vp, c_ll],
     "ns2_linear_bf16": [c_vp, c_int, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_ll,
@@ -160,6 +162,13 @@ class Lib:
 
     def tile_i8_weight(self, W, Wt, N, K):
         self.call("ns2_tile_i8_weight", _ptr(W), _ptr(Wt), N, K)
+
+    def tile_i8_weight_glu(self, W, Wt, N, K):
+        self.call("ns2_tile_i8_weight_glu", _ptr(W), _ptr(Wt), N, K)
+
+    def linear_i8_glu_rot_tiled(self, At, Wt, scale, Y, M, N, K, *, bias=None, alpha=1.0, act="silu"):
+        self.call("ns2_linear_i8_glu_rot_tiled", _ptr(At), _ptr(Wt), _ptr(scale), _ptr(bias), _ptr(Y), M, N, K,
+                  alpha, ACT[act])
 
     def linear_i8_tiled(self, At, Wt, scale, C, M, N, K, *, bias=None, ldc=None, cOff=0, alpha=1.0,
                         act="none", resid=False, gate=None, gOff=0):

@@ -179,15 +179,22 @@ def test_tile_i8_weight(ns2lib):
     assert torch.equal(untile_w(wt.cpu(), N, K), q)
 
 
-@pytest.mark.parametrize("rows", [1, 100, 517])
+@pytest.mark.parametrize("rows", [1, 7, 100, 517])
 def test_tiled_producers(ns2lib, rows):
-    """The tiled forms of the three producers hold exactly the row-major results."""
+    """The tiled forms of the three producers: the oracle's values in the tiled layout, and
+    exactly the row-major results."""
     g = gen(14 + rows)
     cols, I = 1536, 4096
-    x = torch.randn(rows, cols, generator=g).to(dev)
-    mod = (torch.randn(6 * cols, generator=g) * 0.1).to(dev)
-    w = (torch.randn(cols, generator=g) * 0.02).to(dev)
-    h = (torch.randn(rows, 2 * I, generator=g) * 2).to(dev)
+    xh = torch.randn(rows, cols, generator=g)
+    modh = torch.randn(6 * cols, generator=g) * 0.1
+    wh = torch.randn(cols, generator=g) * 0.02
+    hh = torch.randn(rows, 2 * I, generator=g) * 2
+    x, mod, w, h = xh.to(dev), modh.to(dev), wh.to(dev), hh.to(dev)
+    refs = {
+        "rotate_f16": O.rotate(xh.double()),
+        "norm_mod_rotate_f16": O.rotate(O.norm_mod(xh.double(), modh.double(), 0, cols, wh.double())),
+        "glu_rotate_f16": O.rotate(O.glu(hh.double(), "silu")),
+    }
     for name, call, K in [
         ("rotate_f16", lambda y, t: ns2lib.rotate_f16(x, cols, y, cols, rows, cols, tiled=t), cols),
         ("norm_mod_rotate_f16",
@@ -199,7 +206,9 @@ def test_tiled_producers(ns2lib, rows):
         til = tiled_operand(rows, K)
         call(til, True)
         torch.cuda.synchronize()
-        assert torch.equal(untile_a(til.cpu(), rows, K), flat.cpu()), name
+        got = untile_a(til.cpu(), rows, K)
+        assert_close(f16_as_float(got), refs[name], TOL_F16_OUT, f"{name} tiled rows={rows}")
+        assert torch.equal(got, flat.cpu()), name
 
 
 def _tiled_linear_inputs(M, N, K, seed):
@@ -265,6 +274,58 @@ def test_linear_i8_tiled_epilogues(ns2lib):
     assert torch.equal(got[:L], qkv[:L]) and torch.equal(got[L:, :N], qkv[L:, :N])
     assert torch.equal(got[L:, 2 * N:], qkv[L:, 2 * N:])
     assert_close(got, ref, TOL, "tiled column window")
+
+
+def test_tile_i8_weight_glu(ns2lib):
+    N, K = 1024, 256
+    q, _ = int8_weight(N, K, gen(16))
+    wt = torch.empty(N * K, dtype=torch.int8, device=dev)
+    ns2lib.tile_i8_weight_glu(q.to(dev), wt, N, K)
+    torch.cuda.synchronize()
+    got = untile_w(wt.cpu(), N, K)
+    c = torch.arange(N)
+    src = torch.where(c % 64 < 32, 32 * (c // 64) + c % 64, N // 2 + 32 * (c // 64) + c % 64 - 32)
+    assert torch.equal(got, q[src])
+    assert sorted(src.tolist()) == list(range(N))
+
+
+@pytest.mark.parametrize("M,N,K,act", [
+    (3952, 8192, 1536, "silu"),   # the DiT MLP
+    (256, 8192, 1536, "silu"),    # text refine blocks
+    (97, 1024, 512, "gelu_tanh"),
+    (1, 512, 256, "silu"),
+])
+def test_linear_i8_glu_rot_tiled(ns2lib, M, N, K, act):
+    """w12 GEMM + GLU + rotation in one kernel: against the three separate ops (rounding-level
+    differences in a few elements: the kernels may contract the scale-and-bias multiply-adds
+    differently, and the rotation spreads a group's rounding over its outputs), and against
+    the oracle."""
+    g = gen(M + N + K)
+    x = torch.randn(M, K, generator=g)
+    q, s = int8_weight(N, K, g)
+    bias = torch.randn(N, generator=g) * 0.1
+    I = N // 2
+    xd, qd, sd, bd = x.to(dev), q.to(dev), s.reshape(-1).to(dev), bias.to(dev)
+    at = tiled_operand(M, K)
+    ns2lib.rotate_f16(xd, K, at, K, M, K, tiled=True)
+    wglu = torch.empty(N * K, dtype=torch.int8, device=dev)
+    ns2lib.tile_i8_weight_glu(qd, wglu, N, K)
+    y = tiled_operand(M, I)
+    ns2lib.linear_i8_glu_rot_tiled(at, wglu, sd, y, M, N, K, bias=bd, alpha=0.75, act=act)
+    # the unfused sequence
+    wt = torch.empty(N * K, dtype=torch.int8, device=dev)
+    ns2lib.tile_i8_weight(qd, wt, N, K)
+    h = torch.empty(M, N, device=dev)
+    ns2lib.linear_i8_tiled(at, wt, sd, h, M, N, K, bias=bd, alpha=0.75)
+    y2 = tiled_operand(M, I)
+    ns2lib.glu_rotate_f16(h, y2, M, I, act, tiled=True)
+    torch.cuda.synchronize()
+    got = untile_a(y.cpu(), M, I)
+    a, b = f16_as_float(got), f16_as_float(untile_a(y2.cpu(), M, I))
+    assert (a - b).abs().max() <= 2.0 ** -10 * b.abs().max()
+    assert (a != b).float().mean() < 0.01
+    ref = O.rotate(O.glu(O.linear_i8(x.double(), q, s.double(), alpha=0.75, bias=bias.double()), act))
+    assert_close(a, ref, TOL, f"glu_rot {M}x{N}x{K} {act}")
 
 
 def test_linear_i8_tiled_errors(ns2lib):
