@@ -192,14 +192,13 @@ struct FlashArgs {
 // rescale. Any reference gives the same softmax, and p <= 2^kRebase stays in fp16 range.
 constexpr float kRebase = 8.0f;
 
-template <int D, int QT, int NW, int STAGES, bool PP>
+template <int D, int QT, int NW, int STAGES>
 __global__ __launch_bounds__(NW * 64) void flash_kernel(FlashArgs a) {
   constexpr int DC = D / 16;             // k-steps of S
   constexpr int DT = D / 32;             // dim tiles of O
   constexpr int TILE = KB * D;           // halfs per K (or V) tile image
   constexpr int BLOCKS = 2 * TILE / 512; // 1 KB direct-load blocks per stage (K then V)
   static_assert(STAGES == 3 || STAGES == 4, "three or four LDS stages");
-  static_assert(!PP || (STAGES == 4 && NW % 8 == 0), "ping-pong needs four stages and two wave groups");
 
   // K of tile t+1 and V of tile t are read while tiles t+2 .. t+STAGES-1 land
   __shared__ __attribute__((aligned(16))) half_t ks[STAGES][TILE];
@@ -227,9 +226,6 @@ __global__ __launch_bounds__(NW * 64) void flash_kernel(FlashArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int q0 = qb * (NW * QT * 32) + wave * QT * 32;
   const int lq = lane & 31, hi = lane >> 5;
-  // ping-pong wave group: odd and even waves (measured faster than halves of the block, so the
-  // two waves that share a SIMD are taken to be neighbours)
-  const int grp = wave & 1;
   const int ntiles = a.Lk_pad / KB;
 
   const half_t* Kt = a.Kc + (long long)bh * ntiles * TILE;
@@ -373,9 +369,7 @@ __global__ __launch_bounds__(NW * 64) void flash_kernel(FlashArgs a) {
   float16_t sA[2][QT], sB[2][QT];
   float mA[QT], mB[QT];
   for (int i = 0; i < STAGES - 1 && i < ntiles; ++i) dma(i, i);
-  if (PP) {
-    wait_newer(W0_{});
-  } else {
+  {
     // tile 0 has landed once at most the tiles issued after it remain in flight
     const int newer = (STAGES - 2 < ntiles - 1 ? STAGES - 2 : ntiles - 1);
     if (newer >= 2) wait_newer(W2_{});
@@ -398,24 +392,13 @@ __global__ __launch_bounds__(NW * 64) void flash_kernel(FlashArgs a) {
     constexpr bool MORE = decltype(more_c)::value;
     constexpr bool BIAS = decltype(bias_c)::value;  // tile t+1 carries a key bias
     const int vbuf = t % STAGES, kbuf = (t + 1) % STAGES;
-    // Barrier t. Without ping-pong every wave takes it at the start of the step. With
-    // ping-pong, wave group 1 (the odd waves) takes it between its phases A and B, so a group-0
-    // and a group-1 wave on one SIMD run opposite phases (one mostly VALU, one mostly MFMA). Then each wave drains its loads before the barrier (tiles up to
-    // t+2 have landed) and tile t+3 goes into the stage of tile t-1, whose last readers (phase B
-    // of step t-1 in either group) are behind the barrier.
-    auto sync = [&]() {
-      if (PP) {
-        wait_newer(W0_{});
-        __syncthreads();
-        if (t + 3 < ntiles) dma(t + 3, (t + 3) % STAGES);
-      } else {
-        if (MORE && STAGES == 4 && t + 2 < ntiles) wait_newer(W1_{});
-        else wait_newer(W0_{});
-        __syncthreads();
-        if (MORE && t + STAGES - 1 < ntiles) dma(t + STAGES - 1, (t + STAGES - 1) % STAGES);
-      }
-    };
-    if (!PP || grp == 0) sync();
+    // tile t+1 has landed once at most the tiles issued after it remain in flight; the barrier
+    // then covers every wave's loads, and every wave's reads of tile t-1, whose stage the next
+    // loads overwrite
+    if (MORE && STAGES == 4 && t + 2 < ntiles) wait_newer(W1_{});
+    else wait_newer(W0_{});
+    __syncthreads();
+    if (MORE && t + STAGES - 1 < ntiles) dma(t + STAGES - 1, (t + STAGES - 1) % STAGES);
 
     // ---- move the reference when a score exceeds it by more than 2^kRebase, or when nothing
     // has been accumulated yet (l = 0: the tile maximum becomes the reference, so the largest
@@ -445,10 +428,9 @@ __global__ __launch_bounds__(NW * 64) void flash_kernel(FlashArgs a) {
       }
     }
 
-    // ---- phase A (raised wave priority while this wave feeds the MFMA pipe); the scheduling
-    // barriers keep each phase's reads and VALU work inside the phase
+    // ---- phase A; the scheduling barriers keep each phase's reads and VALU work inside the
+    // phase
     __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_setprio(1);
     // P of tile t in fp16, pair by pair: pair p = ((kt*QT + qt)*2 + kk)*4 + e/2
     constexpr int NP = 2 * QT * 2 * 4;
     half8_t pf[2][QT][2];
@@ -478,9 +460,9 @@ __global__ __launch_bounds__(NW * 64) void flash_kernel(FlashArgs a) {
       for (int i = 0; i < NK; ++i) {
         if (i + 2 < NK) kf[i + 2] = read_k(i + 2, kbuf);
         __builtin_amdgcn_sched_barrier(0);
-        qk_mfma(s_nxt, i, kf[i]);
 #pragma unroll
         for (int p = i * NP / NK; p < (i + 1) * NP / NK; ++p) exp_pair(p);
+        qk_mfma(s_nxt, i, kf[i]);
         __builtin_amdgcn_sched_barrier(0);
       }
     } else {
@@ -491,7 +473,6 @@ __global__ __launch_bounds__(NW * 64) void flash_kernel(FlashArgs a) {
     for (int qt = 0; qt < QT; ++qt) l_run[qt] += ls[0][qt] + ls[1][qt];
 
     __builtin_amdgcn_sched_barrier(0);
-    if (PP && grp == 1) sync();
     // ---- phase B: O^T += V^T P^T, the DT accumulators interleaved
     if (BIAS) add_bias(s_nxt, kbuf);
     {
@@ -521,7 +502,6 @@ __global__ __launch_bounds__(NW * 64) void flash_kernel(FlashArgs a) {
       }
     }
     __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_setprio(0);
   };
   using T_ = std::integral_constant<bool, true>;
   using F_ = std::integral_constant<bool, false>;
@@ -565,13 +545,13 @@ __global__ __launch_bounds__(NW * 64) void flash_kernel(FlashArgs a) {
   }
 }
 
-template <int D, int QT, int NW, int STAGES = 4, bool PP = true>
+template <int D, int QT, int NW, int STAGES = 3>
 void launch_flash(FlashArgs fa, hipStream_t s) {
   constexpr int BQ = NW * QT * 32;
   fa.qblocks = (fa.Lq + BQ - 1) / BQ;
   const int blocks = fa.qblocks * fa.pairs;
   fa.xcd_order = (fa.pairs % 8 == 0) ? 1 : 0;
-  flash_kernel<D, QT, NW, STAGES, PP><<<blocks, NW * 64, 0, s>>>(fa);
+  flash_kernel<D, QT, NW, STAGES><<<blocks, NW * 64, 0, s>>>(fa);
 }
 
 template <int D>
