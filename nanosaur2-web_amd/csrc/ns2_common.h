@@ -92,36 +92,84 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-// One radix-4 stage of the regular Hadamard H4 = [[1,1,1,-1],[1,1,-1,1],[1,-1,1,1],[-1,1,1,1]]
-// across 4 lanes whose lane bits (lo, lo<<1) index the 4 inputs: output position i is
-// (a+b+c+e) - 2 * input[3 - i], and position 3 - i is lane ^ (3 * lo).
-__device__ __forceinline__ float h4_lanes(float v, int lo) {
-  float s = v + __shfl_xor(v, lo, 64);
-  s += __shfl_xor(s, 2 * lo, 64);
-  float partner = __shfl_xor(v, 3 * lo, 64);
-  return s - 2.0f * partner;
+// ---- in-wave fast Walsh-Hadamard transform (no LDS traffic) ----------------------------------
+//
+// The regular Hadamard H4 = [[1,1,1,-1],[1,1,-1,1],[1,-1,1,1],[-1,1,1,1]] (tools/quant.py:25)
+// maps x to y_i = (x_i + x_{i^1}) + (x_{i^2} - x_{i^3}): with T_i = x_i + x_{i^1} and
+// E_j = x_j - x_{j^1}, y_i = T_i + E_{i^2}. Each radix-4 stage below evaluates that over the
+// 4 values that differ in two index bits, held in registers or in lanes.
+
+// DPP controls: quad_perm [1,0,3,2] (lane ^ 1), [2,3,0,1] (lane ^ 2), [3,2,1,0] (lane ^ 3);
+// row_mirror (lane ^ 15 inside a row of 16); row_half_mirror (lane ^ 7 inside 8 lanes).
+constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppXor3 = 0x1B, kDppRowMirror = 0x140,
+              kDppHalfMirror = 0x141;
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
 }
 
-// In-wave fast Walsh-Hadamard transform of one 256-group: lane t holds elements 4t..4t+3
-// in v[0..3]. Computes y = x H with H = kron(H4, H4, H4, H4) / 16 (tools/quant.py:21-29):
-// radix-4 stages at strides 1 (in registers), 4, 16 and 64 (across lanes).
+// Stage over lane bits 0-1 (element stride 4): quad permutations.
+__device__ __forceinline__ float h4_bits01(float v) {
+  const float o = dpp<kDppXor1>(v);
+  const float t = v + o, e = v - o;
+  return t + dpp<kDppXor2>(e);
+}
+
+// Stage over lane bits 2-3 (stride 16): lane ^ 4 = half-row mirror then quad ^ 3, lane ^ 8 =
+// row mirror then half-row mirror.
+__device__ __forceinline__ float h4_bits23(float v) {
+  const float o = dpp<kDppXor3>(dpp<kDppHalfMirror>(v));
+  const float t = v + o, e = v - o;
+  return t + dpp<kDppHalfMirror>(dpp<kDppRowMirror>(e));
+}
+
+// v_permlane16_swap / v_permlane32_swap (gfx950) as inline assembly: both registers are
+// outputs, and the compiler's builtin returns the first operand's new value for both. The
+// s_nop gives the two wait states these instructions need after a VALU write of an operand.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void permlane16_swap(float& a, float& b) {
+  asm("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ void permlane32_swap(float& a, float& b) {
+  asm("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+#pragma clang diagnostic pop
+
+// Stage over lane bits 4-5 (stride 64), with the row swaps. permlane16_swap exchanges the odd
+// 16-lane rows of its first operand with the even rows of its second: on two copies of v (rows
+// r0..r3) it leaves {r0, r0, r2, r2} and {r1, r1, r3, r3}, so every row holds its pair sum T
+// and the difference (even - odd) of its pair. permlane32_swap does the same with 32-lane
+// halves and leaves {lower half twice} and {upper half twice}: row i then takes the other
+// half's difference, with the sign of x_{i^2} - x_{i^3} (negative on odd rows).
+__device__ __forceinline__ float h4_bits45(float v) {
+  float ev = v, od = v;
+  permlane16_swap(ev, od);
+  const float t = ev + od;
+  float lo = ev - od, hi = lo;
+  permlane32_swap(lo, hi);
+  const float other = (threadIdx.x & 32) ? lo : hi;
+  return __builtin_fmaf((threadIdx.x & 16) ? -1.0f : 1.0f, other, t);
+}
+
+// y = x H over one 256-group with H = kron(H4, H4, H4, H4) / 16 (tools/quant.py:21-29): lane t
+// holds elements 4t..4t+3 in v[0..3]; stride 1 in registers, strides 4, 16 and 64 across
+// lane bits 0-1, 2-3 and 4-5.
 __device__ __forceinline__ void fwht256_wave(float v[4]) {
   {
-    float a = v[0], b = v[1], c = v[2], e = v[3];
-    float s = a + b + c + e;
-    v[0] = s - 2.0f * e;
-    v[1] = s - 2.0f * c;
-    v[2] = s - 2.0f * b;
-    v[3] = s - 2.0f * a;
+    const float t01 = v[0] + v[1], e01 = v[0] - v[1], t23 = v[2] + v[3], e23 = v[2] - v[3];
+    v[0] = t01 + e23;
+    v[1] = t01 - e23;
+    v[2] = t23 + e01;
+    v[3] = t23 - e01;
   }
 #pragma unroll
-  for (int j = 0; j < 4; ++j) v[j] = h4_lanes(v[j], 1);   // stride 4: lane bits 0-1
+  for (int j = 0; j < 4; ++j) v[j] = h4_bits01(v[j]);
 #pragma unroll
-  for (int j = 0; j < 4; ++j) v[j] = h4_lanes(v[j], 4);   // stride 16: lane bits 2-3
+  for (int j = 0; j < 4; ++j) v[j] = h4_bits23(v[j]);
 #pragma unroll
-  for (int j = 0; j < 4; ++j) v[j] = h4_lanes(v[j], 16);  // stride 64: lane bits 4-5
-#pragma unroll
-  for (int j = 0; j < 4; ++j) v[j] *= 0.0625f;
+  for (int j = 0; j < 4; ++j) v[j] = h4_bits45(v[j]) * 0.0625f;
 }
 
 __device__ __forceinline__ uint32_t pack_half2(float a, float b) {

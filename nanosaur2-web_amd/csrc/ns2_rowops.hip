@@ -88,38 +88,87 @@ __global__ __launch_bounds__(256) void norm_mod_kernel(const float* __restrict__
   }
 }
 
-// normMod + rotation + fp16: one wave per 256-group of the row, the row in registers.
-__global__ __launch_bounds__(1024) void norm_mod_rot_kernel(const float* __restrict__ x,
-                                                             const float* __restrict__ mod,
-                                                             long long shiftOff,
-                                                             long long scaleOff, int cols,
-                                                             const float* __restrict__ w,
-                                                             float eps,
-                                                             uint16_t* __restrict__ y, int tiled) {
-  __shared__ float red[16];
-  const long long base = (long long)blockIdx.x * cols;
-  const int c = threadIdx.x * 4;  // blockDim.x * 4 == cols
-  const float4 in = *reinterpret_cast<const float4*>(x + base + c);
-  float v[4] = {in.x, in.y, in.z, in.w};
-  float mean = 0.f;
-  if (!w) mean = block_sum(v[0] + v[1] + v[2] + v[3], red) / (float)cols;
-  float ss = 0.f;
+// ---- rotated fp16 producers, one wave per row ------------------------------------------------
+
+struct RotRowsArgs {
+  const float* x;
+  int ldx;
+  const float* mod;  // normMod only: shift at mod + shiftOff, scale at mod + scaleOff
+  long long shiftOff, scaleOff;
+  const float* w;    // normMod only: RMSNorm weight, or null for LayerNorm without affine
+  float eps;
+  uint16_t* y;
+  int ldy, rows, tiled;
+};
+
+// [rows, 256 G] fp32 -> (normMod ->) rotated fp16, one wave per row and 8 rows per block.
+// Each lane loads its 4 values of every group before any arithmetic (the whole row is in
+// flight at once), the row statistics are wave reductions, and the 8 rows of a block fill
+// whole 128-byte lines of the tiled layout (rows 8q..8q+7 of a k-chunk are adjacent 16-byte
+// slots), so no line is assembled from partial writes of different L2s.
+template <int G, bool NORM>
+__global__ __launch_bounds__(512) void rot_rows_kernel(RotRowsArgs a) {
+  const int row = blockIdx.x * 8 + (threadIdx.x >> 6);
+  if (row >= a.rows) return;
+  const int lane = threadIdx.x & 63;
+  constexpr int cols = 256 * G;
+  const float* src = a.x + (long long)row * a.ldx + lane * 4;
+  float v[G][4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    v[j] -= mean;
-    ss += v[j] * v[j];
+  for (int g = 0; g < G; ++g) {
+    const float4 in = *reinterpret_cast<const float4*>(src + g * 256);
+    v[g][0] = in.x, v[g][1] = in.y, v[g][2] = in.z, v[g][3] = in.w;
   }
-  const float r = rsqrtf(block_sum(ss, red) / (float)cols + eps);
-  const float4 sc = *reinterpret_cast<const float4*>(mod + scaleOff + c);
-  const float4 sh = *reinterpret_cast<const float4*>(mod + shiftOff + c);
-  float4 ww = make_float4(1.f, 1.f, 1.f, 1.f);
-  if (w) ww = *reinterpret_cast<const float4*>(w + c);
-  v[0] = v[0] * r * ww.x * (1.0f + sc.x) + sh.x;
-  v[1] = v[1] * r * ww.y * (1.0f + sc.y) + sh.y;
-  v[2] = v[2] * r * ww.z * (1.0f + sc.z) + sh.z;
-  v[3] = v[3] * r * ww.w * (1.0f + sc.w) + sh.w;
-  fwht256_wave(v);
-  store4_f16(y, blockIdx.x, c, cols, cols, tiled, v);
+  float r = 1.f;
+  if (NORM) {
+    float mean = 0.f;
+    if (!a.w) {
+      float s = 0.f;
+#pragma unroll
+      for (int g = 0; g < G; ++g) s += (v[g][0] + v[g][1]) + (v[g][2] + v[g][3]);
+      mean = wave_sum(s) / (float)cols;
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        v[g][j] -= mean;
+        ss += v[g][j] * v[g][j];
+      }
+    r = rsqrtf(wave_sum(ss) / (float)cols + a.eps);
+  }
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    if (NORM) {
+      const int c = g * 256 + lane * 4;
+      const float4 sc = *reinterpret_cast<const float4*>(a.mod + a.scaleOff + c);
+      const float4 sh = *reinterpret_cast<const float4*>(a.mod + a.shiftOff + c);
+      float4 ww = make_float4(1.f, 1.f, 1.f, 1.f);
+      if (a.w) ww = *reinterpret_cast<const float4*>(a.w + c);
+      v[g][0] = v[g][0] * r * ww.x * (1.0f + sc.x) + sh.x;
+      v[g][1] = v[g][1] * r * ww.y * (1.0f + sc.y) + sh.y;
+      v[g][2] = v[g][2] * r * ww.z * (1.0f + sc.z) + sh.z;
+      v[g][3] = v[g][3] * r * ww.w * (1.0f + sc.w) + sh.w;
+    }
+    fwht256_wave(v[g]);
+    store4_f16(a.y, row, g * 256 + lane * 4, a.ldy, cols, a.tiled, v[g]);
+  }
+}
+
+template <bool NORM>
+void launch_rot_rows(const RotRowsArgs& a, int groups) {
+  const dim3 grid((a.rows + 7) / 8), block(512);
+  hipStream_t s = ns2::stream();
+  switch (groups) {
+#define NS2_ROT_CASE(G) \
+    case G: rot_rows_kernel<G, NORM><<<grid, block, 0, s>>>(a); break;
+    NS2_ROT_CASE(1) NS2_ROT_CASE(2) NS2_ROT_CASE(3) NS2_ROT_CASE(4) NS2_ROT_CASE(5) NS2_ROT_CASE(6)
+    NS2_ROT_CASE(7) NS2_ROT_CASE(8) NS2_ROT_CASE(9) NS2_ROT_CASE(10) NS2_ROT_CASE(11) NS2_ROT_CASE(12)
+    NS2_ROT_CASE(13) NS2_ROT_CASE(14) NS2_ROT_CASE(15) NS2_ROT_CASE(16)
+#undef NS2_ROT_CASE
+    default: break;
+  }
 }
 
 // ---- headNorm -------------------------------------------------------------------------------
@@ -257,7 +306,12 @@ int ns2_rotate_f16(const float* x, int ldx, uint16_t* y, int ldy, int rows, int 
   NS2_REQUIRE(x && y && aligned16(x) && aligned8(y), "ns2_rotate_f16: null or unaligned buffer");
   const int gpr = cols / 256;
   ns2::ProfScope prof_("rotate_f16");
-  rotate_f16_kernel<<<blocks_for((long long)rows * gpr, 4), 256, 0, ns2::stream()>>>(x, ldx, y, ldy, rows, gpr, tiled);
+  if (gpr <= 16) {
+    RotRowsArgs a{x, ldx, nullptr, 0, 0, nullptr, 0.f, y, ldy, rows, tiled};
+    launch_rot_rows<false>(a, gpr);
+  } else {
+    rotate_f16_kernel<<<blocks_for((long long)rows * gpr, 4), 256, 0, ns2::stream()>>>(x, ldx, y, ldy, rows, gpr, tiled);
+  }
   NS2_LAUNCHED("rotate_f16");
   return NS2_OK;
 }
@@ -284,7 +338,8 @@ int ns2_norm_mod_rotate_f16(const float* x, const float* mod, long long shiftOff
                   aligned16(mod) && (!weight || aligned16(weight)),
               "ns2_norm_mod_rotate_f16: null or unaligned buffer/offset");
   ns2::ProfScope prof_("norm_mod_rotate_f16");
-  norm_mod_rot_kernel<<<rows, cols / 4, 0, ns2::stream()>>>(x, mod, shiftOff, scaleOff, cols, weight, eps, y, tiled);
+  RotRowsArgs a{x, cols, mod, shiftOff, scaleOff, weight, eps, y, cols, rows, tiled};
+  launch_rot_rows<true>(a, cols / 256);
   NS2_LAUNCHED("norm_mod_rotate_f16");
   return NS2_OK;
 }
