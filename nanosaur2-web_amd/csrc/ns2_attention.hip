@@ -173,6 +173,151 @@ __global__ __launch_bounds__(256) void attn_pack_kernel(PackArgs a) {
   }
 }
 
+// Vectorized pack for 16-byte aligned views (every view of the DiT path): no LDS, no
+// barrier, every global access 16 bytes per lane except the V gathers (D/32 floats). One
+// block per (64-row tile, head, batch):
+//   waves 0-1: Q rows, two lanes per row (lane half hh owns rope pairs [hh D/4, (hh+1) D/4));
+//   waves 2-3: K rows, the same split, stored straight into the chunk-major tile;
+//   all waves: V, lane (kc, dg) gathers the 8 keys of stored key-chunk kc for dims
+//   [dg D/32, (dg+1) D/32) and writes them as the 16-byte rows of the transposed tile.
+template <int D>
+__device__ __forceinline__ void prep_half_row(const float* __restrict__ src, const float* __restrict__ nw,
+                                              const float* __restrict__ cs, long long sinOff, int row,
+                                              bool rope, float mul, float eps, int hh, float* x1, float* x2) {
+  constexpr int HALF = D / 2, PER = D / 4;
+  const int i0 = hh * PER;
+#pragma unroll
+  for (int j = 0; j < PER; j += 4) {
+    const float4 a = *reinterpret_cast<const float4*>(src + i0 + j);
+    const float4 b = *reinterpret_cast<const float4*>(src + HALF + i0 + j);
+    x1[j] = a.x, x1[j + 1] = a.y, x1[j + 2] = a.z, x1[j + 3] = a.w;
+    x2[j] = b.x, x2[j + 1] = b.y, x2[j + 2] = b.z, x2[j + 3] = b.w;
+  }
+  if (nw) {
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) ss += x1[j] * x1[j] + x2[j] * x2[j];
+    ss += dpp<kDppXor1>(ss);  // the row's other lane
+    const float r = rsqrtf(ss / (float)D + eps);
+#pragma unroll
+    for (int j = 0; j < PER; j += 4) {
+      const float4 w1 = *reinterpret_cast<const float4*>(nw + i0 + j);
+      const float4 w2 = *reinterpret_cast<const float4*>(nw + HALF + i0 + j);
+      x1[j] = x1[j] * r * w1.x, x1[j + 1] = x1[j + 1] * r * w1.y;
+      x1[j + 2] = x1[j + 2] * r * w1.z, x1[j + 3] = x1[j + 3] * r * w1.w;
+      x2[j] = x2[j] * r * w2.x, x2[j + 1] = x2[j + 1] * r * w2.y;
+      x2[j + 2] = x2[j + 2] * r * w2.z, x2[j + 3] = x2[j + 3] * r * w2.w;
+    }
+  }
+  if (rope) {
+    const float* cp = cs + (long long)row * HALF + i0;
+    const float* sp = cs + sinOff + (long long)row * HALF + i0;
+#pragma unroll
+    for (int j = 0; j < PER; j += 4) {
+      const float4 c4 = *reinterpret_cast<const float4*>(cp + j);
+      const float4 s4 = *reinterpret_cast<const float4*>(sp + j);
+      const float c[4] = {c4.x, c4.y, c4.z, c4.w}, sn[4] = {s4.x, s4.y, s4.z, s4.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float y1 = x1[j + e] * c[e] - x2[j + e] * sn[e];
+        const float y2 = x2[j + e] * c[e] + x1[j + e] * sn[e];
+        x1[j + e] = y1;
+        x2[j + e] = y2;
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    x1[j] *= mul;
+    x2[j] *= mul;
+  }
+}
+
+__device__ __forceinline__ uint4 pack8_f16(const float* x) {
+  return make_uint4(pack_half2(x[0], x[1]), pack_half2(x[2], x[3]), pack_half2(x[4], x[5]), pack_half2(x[6], x[7]));
+}
+
+template <int D>
+__global__ __launch_bounds__(256) void attn_pack_vec_kernel(PackArgs a) {
+  constexpr int HALF = D / 2, PER = D / 4, DPL = D / 32;
+  const int h = blockIdx.y, b = blockIdx.z;
+  const int bh = b * a.H + h;
+  const int tile = blockIdx.x, row0 = tile * KB;
+  const int tid = threadIdx.x;
+  const long long tiles = a.Lk_pad / KB;
+  const bool kv = row0 < a.Lk_pad;  // uniform per block
+
+  // V gathers first: they do not depend on the Q/K work
+  const int kc = tid >> 5, dg = tid & 31;
+  float vv[8][DPL];
+  if (kv) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int key = row0 + vkey_pos(kc * 8 + e);
+      const float* src = a.v + a.vOff + b * a.vBatch + (long long)key * a.ldv + (long long)h * D + dg * DPL;
+#pragma unroll
+      for (int j = 0; j < DPL; ++j) vv[e][j] = key < a.Lk ? src[j] : 0.f;
+    }
+  }
+
+  const int rl = (tid & 127) >> 1, hh = tid & 1;
+  const int row = row0 + rl;
+  float x1[PER], x2[PER];
+  if (tid < 128) {
+    if (row0 < a.Lq_pad) {
+      if (row < a.Lq) {
+        const float* src = a.q + a.qOff + b * a.qBatch + (long long)row * a.ldq + (long long)h * D;
+        prep_half_row<D>(src, a.q_norm, a.cs, a.sinOff, row, a.cs && row < a.rope_rows, a.qscale, a.eps, hh, x1, x2);
+      } else {
+#pragma unroll
+        for (int j = 0; j < PER; ++j) x1[j] = x2[j] = 0.f;
+      }
+      half_t* dst = a.Qp + ((long long)bh * a.Lq_pad + row) * D + hh * PER;
+#pragma unroll
+      for (int j = 0; j < PER; j += 8) {
+        *reinterpret_cast<uint4*>(dst + j) = pack8_f16(x1 + j);
+        *reinterpret_cast<uint4*>(dst + HALF + j) = pack8_f16(x2 + j);
+      }
+    }
+  } else if (kv) {
+    if (row < a.Lk) {
+      const float* src = a.k + a.kOff + b * a.kBatch + (long long)row * a.ldk + (long long)h * D;
+      prep_half_row<D>(src, a.k_norm, a.cs, a.sinOff, row, a.cs && row < a.rope_rows, 1.0f, a.eps, hh, x1, x2);
+    } else {
+#pragma unroll
+      for (int j = 0; j < PER; ++j) x1[j] = x2[j] = 0.f;
+    }
+    // chunk c (dims 8c..8c+7) of key rl sits at (c * 64 + rl) * 8 in the tile
+    half_t* kdst = a.Kc + ((long long)bh * tiles + tile) * (KB * D) + rl * 8;
+#pragma unroll
+    for (int j = 0; j < PER; j += 8) {
+      *reinterpret_cast<uint4*>(kdst + ((hh * PER + j) / 8) * (KB * 8)) = pack8_f16(x1 + j);
+      *reinterpret_cast<uint4*>(kdst + ((HALF + hh * PER + j) / 8) * (KB * 8)) = pack8_f16(x2 + j);
+    }
+  }
+
+  if (kv) {
+    half_t* vdst = a.Vc + ((long long)bh * tiles + tile) * (KB * D) + ((long long)kc * D + dg * DPL) * 8;
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) {
+      float col[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) col[e] = vv[e][j];
+      *reinterpret_cast<uint4*>(vdst + j * 8) = pack8_f16(col);
+    }
+    // per-key bias in log2 units (one head does it)
+    if (h == 0 && tid < KB) {
+      const int key = row0 + tid;
+      float bv = kMaskBias;
+      if (key < a.Lk) {
+        bv = 0.f;
+        if (a.key_bias && key >= a.biasStart) bv = a.key_bias[b * a.biasBatch + key - a.biasStart] * kLog2e;
+      }
+      a.bias2[(long long)b * a.Lk_pad + key] = bv;
+    }
+  }
+}
+
 struct FlashArgs {
   const half_t* Qp;
   const half_t* Kc;
@@ -555,12 +700,13 @@ void launch_flash(FlashArgs fa, hipStream_t s) {
 }
 
 template <int D>
-int run_attention(PackArgs pa, FlashArgs fa, int batch) {
+int run_attention(PackArgs pa, FlashArgs fa, int batch, bool vec) {
   hipStream_t s = ns2::stream();
   const int rows = pa.Lq_pad > pa.Lk_pad ? pa.Lq_pad : pa.Lk_pad;
   {
     ns2::ProfScope prof_("attn_pack");
-    attn_pack_kernel<D><<<dim3(rows / KB, pa.H, batch), 256, 0, s>>>(pa);
+    if (vec) attn_pack_vec_kernel<D><<<dim3(rows / KB, pa.H, batch), 256, 0, s>>>(pa);
+    else attn_pack_kernel<D><<<dim3(rows / KB, pa.H, batch), 256, 0, s>>>(pa);
     NS2_LAUNCHED("attn_pack");
   }
   ns2::ProfScope prof_("attn_flash");
@@ -608,13 +754,19 @@ extern "C" int ns2_attention(const float* q, const float* k, const float* v, flo
               qOff, kOff, vOff, qBatch, kBatch, vBatch, biasBatch, sin_off,
               Lq, Lk, Lq_pad, Lk_pad, H, ldq, ldk, ldv, biasStart, rope_rows,
               scale * kLog2e, eps};
+  // the vectorized pack needs 16-byte aligned rows in every view it reads
+  auto al4 = [](long long x) { return x % 4 == 0; };
+  const bool vec = aligned16(q) && aligned16(k) && aligned16(v) && al4(ldq) && al4(ldk) && al4(ldv) &&
+                   al4(qOff) && al4(kOff) && al4(vOff) && al4(qBatch) && al4(kBatch) && al4(vBatch) &&
+                   (!q_norm || aligned16(q_norm)) && (!k_norm || aligned16(k_norm)) &&
+                   (!rope_cs || (aligned16(rope_cs) && al4(sin_off)));
   int first_biased = Lk;  // padding keys need the mask bias too
   if (key_bias && biasStart < Lk) first_biased = biasStart;
   FlashArgs fa{Qp, Kc, Vc, B2, o, oOff, oBatch, Lq, Lk, Lq_pad, Lk_pad, H, ldo, first_biased / KB, 0, 0, 0};
   switch (D) {
-    case 32: return run_attention<32>(pa, fa, batch);
-    case 64: return run_attention<64>(pa, fa, batch);
-    case 96: return run_attention<96>(pa, fa, batch);
-    default: return run_attention<128>(pa, fa, batch);
+    case 32: return run_attention<32>(pa, fa, batch, vec);
+    case 64: return run_attention<64>(pa, fa, batch, vec);
+    case 96: return run_attention<96>(pa, fa, batch, vec);
+    default: return run_attention<128>(pa, fa, batch, vec);
   }
 }
