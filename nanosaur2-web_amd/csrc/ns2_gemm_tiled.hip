@@ -57,25 +57,24 @@ __device__ __forceinline__ half8_t u8x8_to_h8(uint2 w) {
 
 // One output: (acc * alpha) * rs + bi, activation, then store or add into the residual `old`
 // (gated by gt) in the reference's order (app/gpu/gemm.js:159-164).
-__device__ __forceinline__ void epilogue(const TGemmArgs& p, float* c, float acc, float rs, float bi, float gt, float old) {
-  float r = acc * p.alpha;
-  r *= rs;
-  r += bi;
-  r = apply_act(r, p.act);
-  if (!p.resid) *c = r;
-  else if (!p.gate) *c = old + r;
-  else *c = old + gt * r;
+// Activation chosen at compile time (the launch dispatches on the argument).
+template <int ACT>
+__device__ __forceinline__ float act_t(float x) {
+  if (ACT == NS2_ACT_SILU) return silu(x);
+  if (ACT == NS2_ACT_GELU_TANH) return gelu_tanh(x);
+  return x;
 }
 
 // Block tile BM x BN (multiples of 64), BK = 64; WAVES_M x WAVES_N waves, each computing
 // (BM/WAVES_M) x (BN/WAVES_N) with v_mfma_f32_32x32x16_f16 tiles. STAGES LDS stages, one
 // barrier per k-tile: tile kt+STAGES-1 is copied in while tile kt is multiplied (with three
 // stages the wait before the barrier leaves tile kt+1's copies in flight).
-// EPI 0: C = epilogue(A W^T). EPI 1 (GLU): W's rows are interleaved in 32-row blocks
+// EPI 0: C = act(A W^T * alpha * scale + bias) (RM 0), C += that (RM 1) or C += gate * that
+// (RM 2), the order of gemm.js:159-164. EPI 1 (GLU): W's rows are interleaved in 32-row blocks
 // (ns2_tile_i8_weight_glu), so the 64 columns of a wave hold 32 columns of each GLU half; the
 // block's 512 columns give 256 consecutive outputs act(h1) * h2, one rotation group, which is
 // rotated and written to Y as the tiled fp16 operand of the next int8 linear.
-template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, bool RESID_PRE, int EPI>
+template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int EPI, int ACT, int RM>
 __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void gemm_tiled_kernel(TGemmArgs p) {
   constexpr int NW = WAVES_M * WAVES_N;
   constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
@@ -160,12 +159,11 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void gemm_tiled_kernel(TGem
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  // RESID_PRE (residual launches of small wave tiles): the residual outputs are loaded before
-  // the k loop, where their latency hides behind it, instead of in the epilogue. Only those
-  // launches pay for the extra registers.
-  constexpr bool PRE_C = RESID_PRE && TM * TN * 16 <= 32;
+  // Residual launches of small wave tiles load their old outputs before the k loop, where the
+  // latency hides behind it, instead of in the epilogue.
+  constexpr bool PRE_C = EPI == 0 && RM != 0 && TM * TN * 16 <= 32;
   float cold[PRE_C ? TM : 1][PRE_C ? TN : 1][16];
-  if (PRE_C && p.resid) {
+  if (PRE_C) {
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
       const int n = n0 + wn * WTN + 32 * j + lq;
@@ -266,7 +264,7 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void gemm_tiled_kernel(TGem
         float h2 = acc[i][1][r] * p.alpha;
         h2 *= s2;
         h2 += b2;
-        T[row * 256 + gc] = apply_act(h1, p.act) * h2;
+        T[row * 256 + gc] = act_t<ACT>(h1) * h2;
       }
     __syncthreads();
     // rotation: wave w rotates rows 8w .. 8w+7, the fp16 result in place at the row's start
@@ -290,24 +288,44 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void gemm_tiled_kernel(TGem
     }
     return;
   }
-  // epilogue: acc[i][j][r] = C[m0 + wm*WTM + 32i + 8(r/4) + 4hi + r%4][n0 + wn*WTN + 32j + lq]
+  // epilogue: acc[i][j][r] = C[mb + 32i + 8(r/4) + r%4][n0 + wn*WTN + 32j + lq], mb = the
+  // wave's first row + 4hi. Per column: scale, bias, gate and the row-mb pointer; per element
+  // one multiply-add of its row offset and the arithmetic, with the row check only in tiles
+  // that cross M.
+  const int mb = m0 + wm * WTM + 4 * hi;
+  const bool full = m0 + BM <= p.M;
 #pragma unroll
   for (int j = 0; j < TN; ++j) {
     const int n = n0 + wn * WTN + 32 * j + lq;
     if (n >= p.N) continue;
     const float rs = p.scale[n];
     const float bi = p.bias ? p.bias[n] : 0.0f;
-    const float gt = p.gate ? p.gate[p.gOff + n] : 1.0f;
+    const float gt = RM == 2 ? p.gate[p.gOff + n] : 1.0f;
+    float* cj = p.C + p.cOff + (long long)mb * p.ldc + n;
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+    for (int i = 0; i < TM; ++i) {
+      float old[16];
+      if (RM != 0) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int dm = 32 * i + 8 * (r >> 2) + (r & 3);
+          old[r] = PRE_C ? cold[PRE_C ? i : 0][PRE_C ? j : 0][r]
+                         : ((full || mb + dm < p.M) ? cj[(long long)dm * p.ldc] : 0.0f);
+        }
+      }
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int m = m0 + wm * WTM + 32 * i + 8 * (r >> 2) + 4 * hi + (r & 3);
-        if (m >= p.M) continue;
-        float* c = p.C + p.cOff + (long long)m * p.ldc + n;
-        const float old = !p.resid ? 0.0f : (PRE_C ? cold[PRE_C ? i : 0][PRE_C ? j : 0][r] : *c);
-        epilogue(p, c, acc[i][j][r], rs, bi, gt, old);
+        const int dm = 32 * i + 8 * (r >> 2) + (r & 3);
+        if (!full && mb + dm >= p.M) continue;
+        float v = acc[i][j][r] * p.alpha;
+        v *= rs;
+        v += bi;
+        v = act_t<ACT>(v);
+        if (RM == 1) v = old[r] + v;
+        if (RM == 2) v = old[r] + gt * v;
+        cj[(long long)dm * p.ldc] = v;
       }
+    }
   }
 }
 
@@ -338,11 +356,28 @@ template <int BM, int BN, int WM, int WN, int STAGES = 2, int EPI = 0>
 int launch_tiled(TGemmArgs p) {
   p.tiles_m = (p.M + BM - 1) / BM;
   p.tiles_n = (p.N + BN - 1) / BN;
-  constexpr bool can_pre = EPI == 0 && (BM / WM / 32) * (BN / WN / 32) * 16 <= 32;
-  if (can_pre && p.resid)
-    gemm_tiled_kernel<BM, BN, WM, WN, STAGES, can_pre, EPI><<<p.tiles_m * p.tiles_n, WM * WN * 64, 0, ns2::stream()>>>(p);
-  else
-    gemm_tiled_kernel<BM, BN, WM, WN, STAGES, false, EPI><<<p.tiles_m * p.tiles_n, WM * WN * 64, 0, ns2::stream()>>>(p);
+  const dim3 grid(p.tiles_m * p.tiles_n), block(WM * WN * 64);
+  hipStream_t s = ns2::stream();
+  const int rm = !p.resid ? 0 : (p.gate ? 2 : 1);
+#define NS2_TILED(A, R) gemm_tiled_kernel<BM, BN, WM, WN, STAGES, EPI, A, R><<<grid, block, 0, s>>>(p)
+  if constexpr (EPI == 1) {
+    if (p.act == NS2_ACT_SILU) NS2_TILED(NS2_ACT_SILU, 0);
+    else if (p.act == NS2_ACT_GELU_TANH) NS2_TILED(NS2_ACT_GELU_TANH, 0);
+    else NS2_TILED(NS2_ACT_NONE, 0);
+  } else {
+    switch (p.act * 3 + rm) {
+      case 0: NS2_TILED(NS2_ACT_NONE, 0); break;
+      case 1: NS2_TILED(NS2_ACT_NONE, 1); break;
+      case 2: NS2_TILED(NS2_ACT_NONE, 2); break;
+      case 3: NS2_TILED(NS2_ACT_SILU, 0); break;
+      case 4: NS2_TILED(NS2_ACT_SILU, 1); break;
+      case 5: NS2_TILED(NS2_ACT_SILU, 2); break;
+      case 6: NS2_TILED(NS2_ACT_GELU_TANH, 0); break;
+      case 7: NS2_TILED(NS2_ACT_GELU_TANH, 1); break;
+      default: NS2_TILED(NS2_ACT_GELU_TANH, 2); break;
+    }
+  }
+#undef NS2_TILED
   NS2_LAUNCHED("gemm_tiled");
   return NS2_OK;
 }
