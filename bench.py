@@ -40,10 +40,14 @@ METRIC = "ms per 832x1216 DiT pass (int8) + joint-attention TFLOP/s, 1 MI355X"
 PUBLISHED_PASS_MS = 1730.0   # README.md:86-88 of the reference (WebGPU, laptop GPU)
 FP16_PEAK_TFLOPS = 2516.6    # MI355X dense fp16 MFMA
 H_IMG, W_IMG, T_TXT, D, HEADS, HD, I_MLP, BLOCKS = 76, 52, 256, 1536, 16, 96, 4096, 18
-# HBM bytes per launch from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE (scaled by the copy-kernel
-# calibration; see profiles/), or None where not collected for the current kernels
-GEMM_TRAFFIC_BYTES_PER_LAUNCH = None
-ATTN_TRAFFIC_BYTES_PER_LAUNCH = None
+# HBM bytes per launch from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE, each scaled by what the
+# counter reads for a copy kernel of known size (FETCH_SIZE x 2.0, WRITE_SIZE x 1.0), measured on
+# the current kernels (profiles/): the mean over the pass's 89 tiled-GEMM launches, and one flash
+# launch at the joint shape. Beside each, the algorithmic bytes of the same launches.
+GEMM_TRAFFIC_BYTES_PER_LAUNCH = 147.0e6
+GEMM_ALGORITHMIC_BYTES_PER_LAUNCH = 67.5e6   # N*K int8 W + 2*M*K fp16 A + output (+ old output for +=)
+ATTN_TRAFFIC_BYTES_PER_LAUNCH = 126.2e6
+ATTN_ALGORITHMIC_BYTES_PER_LAUNCH = 125.7e6  # fp16 Q, K, V^T + fp32 O
 
 
 def log(msg):
@@ -341,6 +345,7 @@ def main():
             "unit": "TFLOP/s",
             "frac": gemm["tflops"] / FP16_PEAK_TFLOPS if gemm and gemm["tflops"] else None,
             "traffic": GEMM_TRAFFIC_BYTES_PER_LAUNCH,
+            "traffic_algorithmic": GEMM_ALGORITHMIC_BYTES_PER_LAUNCH,
         },
         "roofline_attention": {
             "kernel": "flash_kernel (joint attention, 3952x4208, batch 2)",
@@ -350,6 +355,7 @@ def main():
             "unit": "TFLOP/s",
             "frac": attn["flash_tflops"] / FP16_PEAK_TFLOPS if attn["flash_tflops"] else None,
             "traffic": ATTN_TRAFFIC_BYTES_PER_LAUNCH,
+            "traffic_algorithmic": ATTN_ALGORITHMIC_BYTES_PER_LAUNCH,
         },
         "cpu_baseline": cpu,
         "kernels": kernels,

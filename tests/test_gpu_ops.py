@@ -428,29 +428,34 @@ def test_attention_batch2_config2(ns2lib):
             assert_close(o[b, :, sl].cpu(), ref, TOL, f"config2 batch {b} head {h}")
 
 
-def test_attention_strided_qkv_views(ns2lib):
+@pytest.mark.parametrize("pad", [0, 1])
+def test_attention_strided_qkv_views(ns2lib, pad):
     """q/k/v as column windows of one packed [Lk, 3D] buffer, like the DiT's qkv
-    (app/models/nanosaur2.js:205-208), with fused per-head norms (the headNorm calls)."""
+    (app/models/nanosaur2.js:205-208), with fused per-head norms (the headNorm calls).
+    pad=1 shifts every window by one float and makes the row stride odd, so the views are
+    not 16-byte aligned and the per-element pack path runs instead of the vectorized one."""
     L, T, Dm = 130, 20, 1536
+    ld = 3 * Dm + pad
     g = gen(31)
-    qkv = torch.randn(L + T, 3 * Dm, generator=g)
+    qkv = torch.randn(L + T, ld, generator=g)
     qn = torch.randn(96, generator=g) * 0.5 + 1
     kn = torch.randn(96, generator=g) * 0.5 + 1
     cs, sin_off = O.rope2d_table(10, 13)
     lb = torch.log(torch.rand(T, generator=g) + 0.5)
     o = torch.empty(L, Dm, device=dev)
-    ns2lib.attention(qkv.to(dev), qkv.to(dev), qkv.to(dev), o, Lq=L, Lk=L + T, H=16, D=96, ldq=3 * Dm,
-                     ldk=3 * Dm, ldv=3 * Dm, ldo=Dm, qOff=0, kOff=Dm, vOff=2 * Dm, key_bias=lb.to(dev),
+    qkv_d = qkv.to(dev)
+    ns2lib.attention(qkv_d, qkv_d, qkv_d, o, Lq=L, Lk=L + T, H=16, D=96, ldq=ld,
+                     ldk=ld, ldv=ld, ldo=Dm, qOff=pad, kOff=Dm + pad, vOff=2 * Dm + pad, key_bias=lb.to(dev),
                      biasStart=L, q_norm=qn.to(dev), k_norm=kn.to(dev), rope_cs=cs.to(dev),
                      sin_off=sin_off, rope_rows=L)
     torch.cuda.synchronize()
-    ref_buf = qkv.double().clone()
+    ref_buf = qkv.double()[:, pad:pad + 3 * Dm].clone()
     O.head_norm_rope(ref_buf, qn.double(), L, 16, 96, 3 * Dm, colOff=0, cs=cs, sinOff=sin_off)
     O.head_norm_rope(ref_buf, kn.double(), L, 16, 96, 3 * Dm, colOff=Dm, cs=cs, sinOff=sin_off)
     O.head_norm_rope(ref_buf, kn.double(), T, 16, 96, 3 * Dm, colOff=Dm, rowOff=L)
     bias = torch.cat([torch.zeros(L, dtype=torch.float64), lb.double()])
     ref = O.attention_heads(ref_buf[:L, :Dm], ref_buf[:, Dm:2 * Dm], ref_buf[:, 2 * Dm:], 16, 96, bias)
-    assert_close(o.cpu(), ref, TOL, "strided qkv + fused head norms")
+    assert_close(o.cpu(), ref, TOL, f"strided qkv + fused head norms (pad {pad})")
 
 
 @pytest.mark.parametrize("Lk", [64, 100, 150, 200, 257])
