@@ -594,6 +594,12 @@ __global__ __launch_bounds__(NW * 64) void flash_kernel(FlashArgs a) {
       const half2_t one = {(half_t)1.0f, (half_t)1.0f};
       ls[kt][qt] = __builtin_amdgcn_fdot2(pp, one, ls[kt][qt], false);
     };
+    // The exp work is spread over both phases so that every MFMA slot carries a similar share
+    // of VALU work (a wave issues its VALU work while its own MFMA runs, but only a short run of
+    // it per MFMA hides): phase A takes the pairs of score half 0 and some of half 1, phase B's
+    // first half (the MFMAs that consume P half 0) the rest of half 1.
+    constexpr int PA_BAL = NP * NK / (NK + NV / 2);
+    constexpr int PA = PA_BAL > NP / 2 ? PA_BAL : NP / 2;
     if (MORE) {
       // K fragment i+2 is read before the MFMAs of fragment i; each slot also does its share
       // of the exp work. Scheduling barriers pin this order (the default scheduler would put
@@ -606,23 +612,20 @@ __global__ __launch_bounds__(NW * 64) void flash_kernel(FlashArgs a) {
         if (i + 2 < NK) kf[i + 2] = read_k(i + 2, kbuf);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int p = i * NP / NK; p < (i + 1) * NP / NK; ++p) exp_pair(p);
+        for (int p = i * PA / NK; p < (i + 1) * PA / NK; ++p) exp_pair(p);
         qk_mfma(s_nxt, i, kf[i]);
         __builtin_amdgcn_sched_barrier(0);
       }
     } else {
 #pragma unroll
-      for (int p = 0; p < NP; ++p) exp_pair(p);
+      for (int p = 0; p < PA; ++p) exp_pair(p);
     }
-#pragma unroll
-    for (int qt = 0; qt < QT; ++qt) l_run[qt] += ls[0][qt] + ls[1][qt];
 
     __builtin_amdgcn_sched_barrier(0);
-    // ---- phase B: O^T += V^T P^T, the DT accumulators interleaved
-    if (BIAS) add_bias(s_nxt, kbuf);
+    // ---- phase B: O^T += V^T P^T, the DT accumulators interleaved. Slots 0 .. NV/2-1 use P of
+    // score half 0 and finish the exp pairs of half 1; slots NV/2 .. NV-1 use half 1 and take
+    // the key bias (for the tiles that have one) and the half-row maxima of tile t+1.
     {
-      // V fragment i+2 is read before the MFMAs of fragment i; the first 2*QT slots also take
-      // a half-row maximum of tile t+1
       half8_t vf[NV];
       float hm[2][QT];
       vf[0] = read_v(0, vbuf);
@@ -635,7 +638,14 @@ __global__ __launch_bounds__(NW * 64) void flash_kernel(FlashArgs a) {
 #pragma unroll
         for (int qt = 0; qt < QT; ++qt)
           o[qt][dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[i], pf[kt][qt][kk], o[qt][dt], 0, 0, 0);
-        if (MORE && i < 2 * QT) hm[i / QT][i % QT] = half_max(s_nxt, i / QT, i % QT);
+        if (i < NV / 2) {
+#pragma unroll
+          for (int p = PA + i * (NP - PA) / (NV / 2); p < PA + (i + 1) * (NP - PA) / (NV / 2); ++p) exp_pair(p);
+        } else if (MORE) {
+          const int j = i - NV / 2;
+          if (BIAS && j == 0) add_bias(s_nxt, kbuf);
+          if (j < 2 * QT) hm[j / QT][j % QT] = half_max(s_nxt, j / QT, j % QT);
+        }
         __builtin_amdgcn_sched_barrier(0);
       }
       if (MORE) {
@@ -646,6 +656,8 @@ __global__ __launch_bounds__(NW * 64) void flash_kernel(FlashArgs a) {
         }
       }
     }
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) l_run[qt] += ls[0][qt] + ls[1][qt];
     __builtin_amdgcn_sched_barrier(0);
   };
   using T_ = std::integral_constant<bool, true>;
