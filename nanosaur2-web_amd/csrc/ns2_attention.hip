@@ -54,6 +54,7 @@ struct PackArgs {
   long long qOff, kOff, vOff, qBatch, kBatch, vBatch, biasBatch, sinOff;
   int Lq, Lk, Lq_pad, Lk_pad, H, ldq, ldk, ldv, biasStart, rope_rows;
   float qscale, eps;
+  int skip_q;  // the flash kernel prepares Q itself (vectorized pack only)
 };
 
 // Per-row prologue for one head row of D values, 4 threads per row: thread part p owns
@@ -264,7 +265,7 @@ __global__ __launch_bounds__(256) void attn_pack_vec_kernel(PackArgs a) {
   const int row = row0 + rl;
   float x1[PER], x2[PER];
   if (tid < 128) {
-    if (row0 < a.Lq_pad) {
+    if (!a.skip_q && row0 < a.Lq_pad) {
       if (row < a.Lq) {
         const float* src = a.q + a.qOff + b * a.qBatch + (long long)row * a.ldq + (long long)h * D;
         prep_half_row<D>(src, a.q_norm, a.cs, a.sinOff, row, a.cs && row < a.rope_rows, a.qscale, a.eps, hh, x1, x2);
@@ -330,6 +331,15 @@ struct FlashArgs {
   int qblocks;      // query blocks per (batch, head)
   int pairs;        // batch * heads
   int xcd_order;    // 1: block id -> (pair, query block) keeps a pair on one XCD
+  // qraw: Q comes straight from the fp32 view (16-byte aligned) and the kernel applies the
+  // optional per-head RMSNorm, RoPE and scale*log2(e) itself; otherwise it reads Qp
+  int qraw;
+  const float* q;
+  const float* q_norm;
+  const float* cs;
+  long long qOff, qBatch, sinOff;
+  int ldq, rope_rows;
+  float qscale, eps;
 };
 
 // Scores are kept relative to a per-query reference m_ref (log2 units) that only moves when a
@@ -377,13 +387,75 @@ __global__ __launch_bounds__(NW * 64) void flash_kernel(FlashArgs a) {
   const half_t* Vt = a.Vc + (long long)bh * ntiles * TILE;
   const float* Bg = a.bias2 + (long long)b * a.Lk_pad;
 
-  // Q^T operands: lane holds query q0 + qt*32 + lq, dims c*16 + 8*hi .. +7
+  // Q^T operands: lane holds query q0 + qt*32 + lq, dims c*16 + 8*hi .. +7. With qraw the
+  // lane reads those 8*DC fp32 values and prepares them as the pack does (kernels.js:307-342):
+  // RMSNorm over the head row (its other half is in lane ^ 32), then split-half RoPE, whose
+  // partner of dim 16c + 8hi + e is dim 16(c + DC/2) + 8hi + e of the same lane, then the
+  // scale; rows past Lq are zero.
   half8_t qf[QT][DC];
+  static_assert(DC % 2 == 0, "RoPE halves must be whole k-steps");
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
-    const half_t* qrow = a.Qp + ((long long)bh * a.Lq_pad + q0 + qt * 32 + lq) * D + 8 * hi;
+    const int q = q0 + qt * 32 + lq;
+    if (a.qraw) {
+      float x[DC][8];
+      if (q < a.Lq) {
+        const float* src = a.q + a.qOff + (long long)b * a.qBatch + (long long)q * a.ldq + (long long)h * D + 8 * hi;
 #pragma unroll
-    for (int c = 0; c < DC; ++c) qf[qt][c] = *reinterpret_cast<const half8_t*>(qrow + c * 16);
+        for (int c = 0; c < DC; ++c) {
+          const float4 u = *reinterpret_cast<const float4*>(src + 16 * c);
+          const float4 w = *reinterpret_cast<const float4*>(src + 16 * c + 4);
+          x[c][0] = u.x, x[c][1] = u.y, x[c][2] = u.z, x[c][3] = u.w;
+          x[c][4] = w.x, x[c][5] = w.y, x[c][6] = w.z, x[c][7] = w.w;
+        }
+      } else {
+#pragma unroll
+        for (int c = 0; c < DC; ++c)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) x[c][e] = 0.f;
+      }
+      if (a.q_norm) {
+        float ss = 0.f;
+#pragma unroll
+        for (int c = 0; c < DC; ++c)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) ss += x[c][e] * x[c][e];
+        ss += __shfl_xor(ss, 32, 64);
+        const float r = rsqrtf(ss / (float)D + a.eps);
+#pragma unroll
+        for (int c = 0; c < DC; ++c) {
+          const float4 w1 = *reinterpret_cast<const float4*>(a.q_norm + 16 * c + 8 * hi);
+          const float4 w2 = *reinterpret_cast<const float4*>(a.q_norm + 16 * c + 8 * hi + 4);
+          const float wv[8] = {w1.x, w1.y, w1.z, w1.w, w2.x, w2.y, w2.z, w2.w};
+#pragma unroll
+          for (int e = 0; e < 8; ++e) x[c][e] = x[c][e] * r * wv[e];
+        }
+      }
+      if (a.cs && q < a.rope_rows) {
+        constexpr int HALF = D / 2;
+#pragma unroll
+        for (int c = 0; c < DC / 2; ++c) {
+          const float* cp = a.cs + (long long)q * HALF + 16 * c + 8 * hi;
+          const float* sp = a.cs + a.sinOff + (long long)q * HALF + 16 * c + 8 * hi;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float cv = cp[e], sv = sp[e];
+            const float y1 = x[c][e] * cv - x[c + DC / 2][e] * sv;
+            const float y2 = x[c + DC / 2][e] * cv + x[c][e] * sv;
+            x[c][e] = y1;
+            x[c + DC / 2][e] = y2;
+          }
+        }
+      }
+#pragma unroll
+      for (int c = 0; c < DC; ++c)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qf[qt][c][e] = (half_t)(x[c][e] * a.qscale);
+    } else {
+      const half_t* qrow = a.Qp + ((long long)bh * a.Lq_pad + q) * D + 8 * hi;
+#pragma unroll
+      for (int c = 0; c < DC; ++c) qf[qt][c] = *reinterpret_cast<const half8_t*>(qrow + c * 16);
+    }
   }
 
   float16_t o[QT][DT];
@@ -714,7 +786,7 @@ void launch_flash(FlashArgs fa, hipStream_t s) {
 template <int D>
 int run_attention(PackArgs pa, FlashArgs fa, int batch, bool vec) {
   hipStream_t s = ns2::stream();
-  const int rows = pa.Lq_pad > pa.Lk_pad ? pa.Lq_pad : pa.Lk_pad;
+  const int rows = (pa.skip_q || pa.Lk_pad > pa.Lq_pad) ? pa.Lk_pad : pa.Lq_pad;
   {
     ns2::ProfScope prof_("attn_pack");
     if (vec) attn_pack_vec_kernel<D><<<dim3(rows / KB, pa.H, batch), 256, 0, s>>>(pa);
@@ -774,7 +846,9 @@ extern "C" int ns2_attention(const float* q, const float* k, const float* v, flo
                    (!rope_cs || (aligned16(rope_cs) && al4(sin_off)));
   int first_biased = Lk;  // padding keys need the mask bias too
   if (key_bias && biasStart < Lk) first_biased = biasStart;
-  FlashArgs fa{Qp, Kc, Vc, B2, o, oOff, oBatch, Lq, Lk, Lq_pad, Lk_pad, H, ldo, first_biased / KB, 0, 0, 0};
+  FlashArgs fa{Qp, Kc, Vc, B2, o, oOff, oBatch, Lq, Lk, Lq_pad, Lk_pad, H, ldo, first_biased / KB, 0, 0, 0,
+               vec ? 1 : 0, q, q_norm, rope_cs, qOff, qBatch, sin_off, ldq, rope_rows, scale * kLog2e, eps};
+  pa.skip_q = vec ? 1 : 0;
   switch (D) {
     case 32: return run_attention<32>(pa, fa, batch, vec);
     case 64: return run_attention<64>(pa, fa, batch, vec);
