@@ -201,6 +201,10 @@ int ns2_glu_rotate_f16(const float* x, uint16_t* y, int rows, int I, int act, in
 int ns2_elementwise(int op, const float* a, const float* b, float* y, long long n);
 /* ops.accumulate (app/gpu/ops.js:188-192): y += a. */
 int ns2_accumulate(float* y, const float* a, long long n);
+/* The per-block modulation add of the DiT (app/models/nanosaur2.js:190, `elementwise(add,
+ * mod, offset)` once per block) batched over blocks: y[r, i] = a[i] + b[r, i] for r < rows,
+ * i < n. Additive to the reference interface (one launch instead of one per block). */
+int ns2_add_rows(const float* a, const float* b, float* y, int rows, int n);
 /* ops.rowSum (app/gpu/ops.js:151-156, kernels.js:362-376): y[n] = scale*sum_r w[r] x[r, n]. */
 int ns2_row_sum(const float* x, const float* w, float* y, int rows, int N, float scale);
 /* ops.rmsnorm (app/gpu/ops.js:111-117, kernels.js:60-80): y = x * rsqrt(mean x^2 + eps) * w. */

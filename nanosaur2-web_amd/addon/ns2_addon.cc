@@ -528,6 +528,17 @@ napi_value Accumulate(napi_env env, napi_callback_info info) {
   return check(env, c, ns2_accumulate(y, a, n));
 }
 
+// addRows(a, b, y, rows, n)
+napi_value AddRows(napi_env env, napi_callback_info info) {
+  ARGS(5);
+  auto a = (const float*)c.ptr(0);
+  auto b = (const float*)c.ptr(1);
+  auto y = (float*)c.ptr(2);
+  int rows = c.i32(3), n = c.i32(4);
+  if (c.failed) return nullptr;
+  return check(env, c, ns2_add_rows(a, b, y, rows, n));
+}
+
 // rowSum(x, w, y, rows, N, scale)
 napi_value RowSum(napi_env env, napi_callback_info info) {
   ARGS(6);
@@ -568,7 +579,7 @@ napi_value Module(napi_env env, napi_value exports) {
       {"linearI8", LinearI8}, {"linearBf16", LinearBf16}, {"attention", Attention},
       {"headNorm", HeadNorm}, {"normMod", NormModT<false>}, {"normModRotateF16", NormModT<true>},
       {"glu", GluT<false>}, {"gluRotateF16", GluT<true>}, {"elementwise", Elementwise},
-      {"accumulate", Accumulate}, {"rowSum", RowSum}, {"rmsnorm", Rmsnorm},
+      {"accumulate", Accumulate}, {"addRows", AddRows}, {"rowSum", RowSum}, {"rmsnorm", Rmsnorm},
   };
   for (const Fn& f : fns) {
     napi_value fn;

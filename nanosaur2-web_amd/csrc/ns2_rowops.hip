@@ -255,15 +255,33 @@ __global__ __launch_bounds__(256) void accumulate_kernel(float* __restrict__ y,
 }
 
 // Y[n] = scale * sum_r w[r] X[r][n]: one thread per column, rows in order (kernels.js:362-376).
-__global__ __launch_bounds__(64) void row_sum_kernel(const float* __restrict__ x,
-                                                      const float* __restrict__ w,
-                                                      float* __restrict__ y, int rows, int N,
-                                                      float scale) {
-  int n = blockIdx.x * 64 + threadIdx.x;
-  if (n >= N) return;
+// y[n] = scale * sum_r w[r] x[r, n]: one block of 16 waves per 64 columns; wave i sums rows i,
+// i + 16, ... of its column, and the 16 partial sums are added in a fixed order.
+__global__ __launch_bounds__(1024) void row_sum_kernel(const float* __restrict__ x,
+                                                        const float* __restrict__ w,
+                                                        float* __restrict__ y, int rows, int N,
+                                                        float scale) {
+  __shared__ float part[16][64];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int n = blockIdx.x * 64 + lane;
   float s = 0.f;
-  for (int r = 0; r < rows; ++r) s += w[r] * x[(long long)r * N + n];
-  y[n] = s * scale;
+  if (n < N)
+    for (int r = wv; r < rows; r += 16) s += w[r] * x[(long long)r * N + n];
+  part[wv][lane] = s;
+  __syncthreads();
+  if (wv == 0 && n < N) {
+    float t = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) t += part[i][lane];
+    y[n] = t * scale;
+  }
+}
+
+// y[r, i] = a[i] + b[r, i]
+__global__ __launch_bounds__(256) void add_rows_kernel(const float* __restrict__ a, const float* __restrict__ b,
+                                                        float* __restrict__ y, long long total, int n) {
+  const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (i < total) y[i] = a[i % n] + b[i];
 }
 
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ x,
@@ -399,12 +417,23 @@ int ns2_accumulate(float* y, const float* a, long long n) {
   return NS2_OK;
 }
 
+int ns2_add_rows(const float* a, const float* b, float* y, int rows, int n) {
+  NS2_READY();
+  if (rows <= 0 || n <= 0) return NS2_OK;
+  NS2_REQUIRE(a && b && y, "ns2_add_rows: null buffer");
+  const long long total = (long long)rows * n;
+  ns2::ProfScope prof_("add_rows");
+  add_rows_kernel<<<blocks_for(total, 256), 256, 0, ns2::stream()>>>(a, b, y, total, n);
+  NS2_LAUNCHED("add_rows");
+  return NS2_OK;
+}
+
 int ns2_row_sum(const float* x, const float* w, float* y, int rows, int N, float scale) {
   NS2_READY();
   if (N <= 0) return NS2_OK;
   NS2_REQUIRE(x && w && y && rows >= 0, "ns2_row_sum: bad arguments");
   ns2::ProfScope prof_("row_sum");
-  row_sum_kernel<<<blocks_for(N, 64), 64, 0, ns2::stream()>>>(x, w, y, rows, N, scale);
+  row_sum_kernel<<<blocks_for(N, 64), 1024, 0, ns2::stream()>>>(x, w, y, rows, N, scale);
   NS2_LAUNCHED("row_sum");
   return NS2_OK;
 }

@@ -75,6 +75,10 @@ export class Nanosaur2DiT {
     m.finalAda = await lin("final_layer.adaLN_modulation.");
     m.finalLinear = await lin("final_layer.linear.");
     if (fused) {
+      // the blocks' adaLN offsets in one [BLOCKS, 6D] tensor, so that every pass forms all the
+      // block modulations with one launch
+      m.offsets = gpu.empty([BLOCKS, 6 * D]);
+      m.blocks.forEach((b, i) => ops.elementwise(gpu, "copy", b.offset, null, ops.rowView(m.offsets, i)));
       // the fused producers feed the block linears tiled operands: re-tile their weights once
       for (const b of m.text.concat(m.blocks)) {
         for (const W of [b.qkv, b.kvY, b.proj, b.w3]) if (W && ops.tileable(W)) ops.tileWeight(gpu, W);
@@ -105,6 +109,8 @@ export class Nanosaur2DiT {
 
   // Release every persistent weight buffer.
   unload() {
+    if (this.offsets) this.offsets.release();
+    this.offsets = null;
     for (const cs of this.ropeCache.values()) cs.release();
     this.ropeCache.clear();
     const seen = new Set();
@@ -265,9 +271,17 @@ export class Nanosaur2DiT {
     const mod = ops.linear(gpu, cond, this.sharedAda, { name: "dit.shared_ada" });
     const final = ops.linear(gpu, cond, this.finalAda, { name: "dit.final_ada" });
     cond.release();
+    // every block's modulation mod + offset_i (app/models/nanosaur2.js:190) at once
+    const modAll = this.offsets ? ops.addRows(gpu, mod, this.offsets) : null;
     return {
-      txt, txtR, mod, final,
-      release() { if (txt) txt.release(); if (txtR) txtR.release(); mod.release(); final.release(); },
+      txt, txtR, mod, final, modAll,
+      release() {
+        if (txt) txt.release();
+        if (txtR) txtR.release();
+        mod.release();
+        final.release();
+        if (modAll) modAll.release();
+      },
     };
   }
 
@@ -277,7 +291,7 @@ export class Nanosaur2DiT {
   block(i, x, L, text, c, cs) {
     const gpu = this.gpu;
     const b = this.blocks[i];
-    const mod = ops.elementwise(gpu, "add", c.mod, b.offset); // [1, 6D]
+    const mod = c.modAll ? ops.rowView(c.modAll, i) : ops.elementwise(gpu, "add", c.mod, b.offset); // [1, 6D]
     const cross = !!(b.kvY && text.L);
     // rows [0, L): image q|k|v; rows [L, L + text): text k|v (q columns unused)
     const Lk = L + (cross ? text.L : 0);

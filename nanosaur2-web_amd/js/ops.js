@@ -169,6 +169,22 @@ export function gluRotated(gpu, x, act, tiled = false) {
 }
 
 // [1, N] = scale * sum_r w[r] * x[r] (app/gpu/ops.js:150-156)
+// y[r, :] = a + b[r, :] for every row of b: the DiT's per-block modulation add
+// (app/models/nanosaur2.js:190) for all blocks in one launch (addition to the reference ops).
+export function addRows(gpu, a, b) {
+  const [rows, n] = b.shape;
+  if (a.size !== n) throw new Error(`addRows: a has ${a.size} values, rows have ${n}`);
+  const y = gpu.empty([rows, n]);
+  gpu.run("add_rows", 0, () => native.addRows(addr(a), addr(b), addr(y), rows, n));
+  return y;
+}
+
+// Row r of a [rows, n] tensor as a [1, n] view (no copy; valid while t is).
+export function rowView(t, r) {
+  const n = t.shape[t.shape.length - 1];
+  return { buf: { ptr: addr(t) + BigInt(r * n * 4) }, shape: [1, n], size: n, release() {} };
+}
+
 export function rowSum(gpu, x, w, scale = 1) {
   const [rows, N] = x.shape;
   const y = gpu.empty([1, N]);

@@ -66,6 +66,7 @@ SIGNATURES = {
     "ns2_glu_rotate_f16": [c_vp, c_vp, c_int, c_int, c_int, c_int],
     "ns2_elementwise": [c_int, c_vp, c_vp, c_vp, c_ll],
     "ns2_accumulate": [c_vp, c_vp, c_ll],
+    "ns2_add_rows": [c_vp, c_vp, c_vp, c_int, c_int],
     "ns2_row_sum": [c_vp, c_vp, c_vp, c_int, c_int, c_float],
     "ns2_rmsnorm": [c_vp, c_vp, c_vp, c_int, c_int, c_float],
 }
@@ -218,6 +219,9 @@ class Lib:
 
     def accumulate(self, y, a, n):
         self.call("ns2_accumulate", _ptr(y), _ptr(a), n)
+
+    def add_rows(self, a, b, y, rows, n):
+        self.call("ns2_add_rows", _ptr(a), _ptr(b), _ptr(y), rows, n)
 
     def row_sum(self, x, w, y, rows, N, scale=1.0):
         self.call("ns2_row_sum", _ptr(x), _ptr(w), _ptr(y), rows, N, scale)

@@ -564,6 +564,20 @@ def test_elementwise_accumulate_rowsum_rmsnorm(ns2lib):
     ns2lib.row_sum(x.to(dev), w.to(dev), out, 256, 1536, 1 / w.sum().item())
     torch.cuda.synchronize()
     assert_close(out.cpu(), O.row_sum(x.double(), w.double(), 1 / w.sum().item()), TOL_F32, "row_sum")
+    # rows not a multiple of the 16 row-splitting waves, columns not a multiple of 64
+    x2 = torch.randn(37, 100, generator=g)
+    w2 = torch.rand(37, generator=g)
+    out2 = torch.empty(100, device=dev)
+    ns2lib.row_sum(x2.to(dev), w2.to(dev), out2, 37, 100, 0.5)
+    torch.cuda.synchronize()
+    assert_close(out2.cpu(), O.row_sum(x2.double(), w2.double(), 0.5), TOL_F32, "row_sum 37x100")
+    # the DiT's block modulations mod + offset_i, all blocks in one launch (exact: one add each)
+    mod = torch.randn(9216, generator=g)
+    offs = torch.randn(18, 9216, generator=g)
+    yrows = torch.empty(18, 9216, device=dev)
+    ns2lib.add_rows(mod.to(dev), offs.to(dev), yrows, 18, 9216)
+    torch.cuda.synchronize()
+    assert torch.equal(yrows.cpu(), mod[None, :] + offs), "add_rows"
     nw = torch.randn(1536, generator=g) * 0.02
     out = torch.empty(256, 1536, device=dev)
     ns2lib.rmsnorm(x.to(dev), nw.to(dev), out, 256, 1536)
