@@ -85,12 +85,6 @@ __device__ __forceinline__ float apply_act(float x, int act) {
   return x;
 }
 
-// Sum over the 64 lanes of a wave.
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
-  return v;
-}
 
 // ---- in-wave fast Walsh-Hadamard transform (no LDS traffic) ----------------------------------
 //
@@ -137,6 +131,28 @@ __device__ __forceinline__ void permlane32_swap(float& a, float& b) {
 }
 #pragma clang diagnostic pop
 
+// Sum over the 64 lanes of a wave, every lane gets it, without LDS traffic: quad sums by DPP
+// (lane ^ 1, ^ 2), then the other quad of the 8-lane half row (half-row mirror), the other
+// half of the 16-lane row (row mirror), the other row of the pair and the other 32-lane half
+// (row swaps).
+__device__ __forceinline__ float wave_sum(float v) {
+  v += dpp<kDppXor1>(v);
+  v += dpp<kDppXor2>(v);
+  v += dpp<kDppHalfMirror>(v);
+  v += dpp<kDppRowMirror>(v);
+  {
+    float a = v, b = v;
+    permlane16_swap(a, b);  // {r0, r0, r2, r2}, {r1, r1, r3, r3}
+    v = a + b;
+  }
+  {
+    float a = v, b = v;
+    permlane32_swap(a, b);  // {h0, h0}, {h1, h1}
+    v = a + b;
+  }
+  return v;
+}
+
 // Stage over lane bits 4-5 (stride 64), with the row swaps. permlane16_swap exchanges the odd
 // 16-lane rows of its first operand with the even rows of its second: on two copies of v (rows
 // r0..r3) it leaves {r0, r0, r2, r2} and {r1, r1, r3, r3}, so every row holds its pair sum T
@@ -170,6 +186,63 @@ __device__ __forceinline__ void fwht256_wave(float v[4]) {
   for (int j = 0; j < 4; ++j) v[j] = h4_bits23(v[j]);
 #pragma unroll
   for (int j = 0; j < 4; ++j) v[j] = h4_bits45(v[j]) * 0.0625f;
+}
+
+// ---- FWHT of a 256-group on the matrix cores -----------------------------------------------
+//
+// With i = 16a + b, H256 = kron(H16, H16) / 16 for H16 = kron(H4, H4) (tools/quant.py:21-29), so
+// y = x H256 is Y = H X H with X[a][b] = x[16a + b], Y[c][d] = y[16c + d] and H = H16 / 4.
+// Two v_mfma_f32_16x16x16_f16 per factor: Z = X H, then Y^T = Z^T H. The lane layout of a
+// 16x16x16 product (A[l%16][4(l/16)+j], B[4(l/16)+j][l%16], D[4(l/16)+j][l%16]) makes Z's
+// accumulators exactly the A operand Z^T of the second product, and leaves Y^T's
+// accumulators in the input layout: lane l holds elements 16(l%16) + 4(l/16) + j, j < 4.
+// Each fp32 operand goes in as an fp16 pair hi + lo (two products accumulated in fp32; H's
+// entries are +-1/4, exact), so the result keeps fp32 accuracy (~2^-21 relative).
+typedef _Float16 half4v_t __attribute__((ext_vector_type(4)));
+
+// H's B-operand fragment of this lane: H[4(l/16)+j][l%16] (H is symmetric, so it also serves
+// as the A fragment H[l%16][4(l/16)+j] up to the transposition the layout already applies).
+__device__ __forceinline__ half4v_t fwht_h16_fragment() {
+  const int l = threadIdx.x & 63, n = l & 15;
+  half4v_t h;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int k = 4 * (l >> 4) + j;
+    // H4[p][q] = -1 where p + q = 3, else 1; H16[k][n] = H4[k/4][n/4] * H4[k%4][n%4]
+    const int neg = ((k >> 2) + (n >> 2) == 3) ^ ((k & 3) + (n & 3) == 3);
+    h[j] = (half_t)(neg ? -0.25f : 0.25f);
+  }
+  return h;
+}
+
+__device__ __forceinline__ void split_f16(const float v[4], half4v_t& hi, half4v_t& lo) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    hi[j] = (half_t)v[j];
+    lo[j] = (half_t)(v[j] - (float)hi[j]);
+  }
+}
+
+// In place on v[4] in the layout above (lane l: elements 16(l%16) + 4(l/16) + j).
+__device__ __forceinline__ void fwht256_mfma(float v[4], const half4v_t& h) {
+  half4v_t hi, lo;
+  split_f16(v, hi, lo);
+  float4_t z = {0.f, 0.f, 0.f, 0.f};
+  z = __builtin_amdgcn_mfma_f32_16x16x16f16(hi, h, z, 0, 0, 0);
+  z = __builtin_amdgcn_mfma_f32_16x16x16f16(lo, h, z, 0, 0, 0);
+  const float zv[4] = {z[0], z[1], z[2], z[3]};
+  split_f16(zv, hi, lo);
+  float4_t y = {0.f, 0.f, 0.f, 0.f};
+  y = __builtin_amdgcn_mfma_f32_16x16x16f16(hi, h, y, 0, 0, 0);
+  y = __builtin_amdgcn_mfma_f32_16x16x16f16(lo, h, y, 0, 0, 0);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) v[j] = y[j];
+}
+
+// First element of this lane's 4 in the matrix-core FWHT layout.
+__device__ __forceinline__ int fwht_mfma_offset() {
+  const int l = threadIdx.x & 63;
+  return 16 * (l & 15) + 4 * (l >> 4);
 }
 
 __device__ __forceinline__ uint32_t pack_half2(float a, float b) {

@@ -13,8 +13,6 @@
 // weights are decoded to fp16 as they are read from LDS into the MFMA B operand (exact:
 // half(0x6400 | u) - 1152 = w for |w| <= 128), and the per-output-row scale is applied in
 // the epilogue, in the reference's order (app/gpu/gemm.js:159-164).
-#include <type_traits>
-
 #include "ns2_common.h"
 
 using namespace ns2dev;
@@ -343,148 +341,6 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void gemm_tiled_kernel(TGem
   store_plain<TM, TN, ACT, RM, PRE_C>(p, acc, cold, m0 + wm * WTM + 4 * hi, n0 + wn * WTN, m0 + BM <= p.M, lq);
 }
 
-// Weights straight to registers (EPI 0): a BM x BN block of NW waves side by side, each
-// BM x BN/NW. The waves' W columns are private, so W never passes through LDS: each lane loads
-// its 8-byte B fragments (column n, k chunk 2s + hi of k-step s) from the tiled weight with
-// ordinary loads two k-tiles ahead. Only A is staged, in three LDS stages of BM x 64 fp16 (the
-// copy of tile kt+2 is issued while tile kt is multiplied), so a block needs 24 KB of LDS at
-// BM = 64 and the deeper pipeline costs no resident blocks. The k loop is unrolled by three so
-// stage and register-set indices are compile-time constants.
-template <int BM, int BN, int NW, int ACT, int RM>
-__global__ __launch_bounds__(NW * 64) void gemm_wreg_kernel(TGemmArgs p) {
-  constexpr int ASTAGES = 3;
-  constexpr int WTN = BN / NW, TM = BM / 32, TN = WTN / 32;
-  constexpr int A_BLOCKS = BM / 64 * 8;  // 1 KB copies per stage
-  constexpr int PER_WAVE = A_BLOCKS / NW;
-  constexpr int W_LOADS = 4 * TN;        // 8-byte fragment loads per lane and k-tile
-  static_assert(BM % 64 == 0 && WTN % 32 == 0 && A_BLOCKS % NW == 0, "tile shape");
-  static_assert(2 * (PER_WAVE + W_LOADS) < 64, "loads in flight must fit the counter");
-  __shared__ __attribute__((aligned(16))) half_t as[ASTAGES][BM * 64];
-
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wn = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int lq = lane & 31, hi = lane >> 5;
-  int tm, tn;
-  block_tile(p, tm, tn);
-  const int m0 = tm * BM, n0 = tn * BN;
-  const int kblocks = p.K / 64;
-
-  // A copies: block j of a stage is k-chunk j % 8 of 64-row block j / 8 (rows past the last
-  // 64-row block re-read it; they are dropped)
-  const char* g_src[PER_WAVE];
-  uint32_t l_dst[PER_WAVE];
-  {
-    const uint32_t as_base = lds_addr(as);
-#pragma unroll
-    for (int i = 0; i < PER_WAVE; ++i) {
-      const int j = wn + i * NW;
-      int mb = m0 / 64 + j / 8;
-      mb = mb < p.mblocks ? mb : p.mblocks - 1;
-      g_src[i] = reinterpret_cast<const char*>(p.At) + ((long long)mb * kblocks * 8 + j % 8) * 1024;
-      l_dst[i] = as_base + j * 1024;
-    }
-  }
-  auto dma = [&](int kt, int st) {
-#pragma unroll
-    for (int i = 0; i < PER_WAVE; ++i)
-      dma16(g_src[i] + (long long)kt * 8 * 1024 + lane * 16,
-            __builtin_amdgcn_readfirstlane(l_dst[i] + st * (BM * 64 * 2)));
-  };
-  // W fragments: column n = n0 + wn*WTN + 32j + lq sits in 64-row block n / 64 (clamped; columns
-  // past N are dropped), row n % 64; k-step s of k-tile kt is chunk 2s + hi of tile (nb, kt)
-  const uint8_t* w_src[TN];
-#pragma unroll
-  for (int j = 0; j < TN; ++j) {
-    const int n = n0 + wn * WTN + 32 * j + lq;
-    int nb = n / 64;
-    nb = nb < p.nblocks ? nb : p.nblocks - 1;
-    w_src[j] = p.Wt + ((long long)nb * kblocks * 8 + hi) * 512 + (n % 64) * 8;
-  }
-  auto load_w = [&](int kt, uint2 (&w)[TN][4]) {
-#pragma unroll
-    for (int j = 0; j < TN; ++j)
-#pragma unroll
-      for (int s = 0; s < 4; ++s) w[j][s] = *reinterpret_cast<const uint2*>(w_src[j] + (long long)kt * 4096 + s * 1024);
-  };
-
-  float16_t acc[TM][TN];
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
-  constexpr bool PRE_C = RM != 0 && TM * TN * 16 <= 32;
-  float cold[PRE_C ? TM : 1][PRE_C ? TN : 1][16];
-  if constexpr (PRE_C) load_old<TM, TN>(p, cold, m0 + 4 * hi, n0 + wn * WTN, lq);
-
-  // Issue order per k-tile: A copies, then W loads; tiles 0 and 1 before the loop. Every step
-  // issues tile kt+2 unconditionally (clamped to the last tile; a copy past the end lands in a
-  // stage nothing reads again), so the loads in flight always follow the same pattern: the
-  // compiler's own waits for W registers then see two younger k-tiles of loads and stay
-  // partial, and the A wait below is one constant.
-  const int klast = kblocks - 1;
-  uint2 wr[3][TN][4];
-  dma(0, 0);
-  load_w(0, wr[0]);
-  dma(klast < 1 ? klast : 1, 1);
-  load_w(klast < 1 ? klast : 1, wr[1]);
-
-  auto read_a = [&](int st, int s, int i) {
-    return *reinterpret_cast<const half8_t*>(&as[st][((i / 2 * 8 + 2 * s + hi) * 64 + (i % 2) * 32 + lq) * 8]);
-  };
-  auto step = [&](auto U_, int kt) {
-    constexpr int U = decltype(U_)::value;
-    // in flight, oldest first: A(kt), W(kt), A(kt+1), W(kt+1): wait for A(kt) only (the
-    // compiler waits for W(kt) at its first use)
-    vm_wait<W_LOADS + PER_WAVE + W_LOADS>();
-    __syncthreads();
-    {
-      const int kn = kt + 2 < kblocks ? kt + 2 : klast;
-      dma(kn, (U + 2) % 3);
-      load_w(kn, wr[(U + 2) % 3]);
-    }
-    __builtin_amdgcn_s_setprio(1);
-    half8_t a[3][TM], b[2][TN];
-#pragma unroll
-    for (int s = 0; s < 2; ++s)
-#pragma unroll
-      for (int i = 0; i < TM; ++i) a[s][i] = read_a(U, s, i);
-#pragma unroll
-    for (int j = 0; j < TN; ++j) b[0][j] = u8x8_to_h8(wr[U][j][0]);
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      if (s + 2 < 4) {
-#pragma unroll
-        for (int i = 0; i < TM; ++i) a[(s + 2) % 3][i] = read_a(U, s + 2, i);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[s % 3][i], b[s & 1][j], acc[i][j], 0, 0, 0);
-      if (s + 1 < 4) {
-#pragma unroll
-        for (int j = 0; j < TN; ++j) b[(s + 1) & 1][j] = u8x8_to_h8(wr[U][j][s + 1]);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    __builtin_amdgcn_s_setprio(0);
-  };
-  int kt = 0;
-  for (; kt + 3 <= kblocks; kt += 3) {
-    step(std::integral_constant<int, 0>{}, kt);
-    step(std::integral_constant<int, 1>{}, kt + 1);
-    step(std::integral_constant<int, 2>{}, kt + 2);
-  }
-  if (kt < kblocks) step(std::integral_constant<int, 0>{}, kt);
-  if (kt + 1 < kblocks) step(std::integral_constant<int, 1>{}, kt + 1);
-  vm_wait<0>();  // the clamped tail copies land before the wave ends
-
-  store_plain<TM, TN, ACT, RM, PRE_C>(p, acc, cold, m0 + 4 * hi, n0 + wn * WTN, m0 + BM <= p.M, lq);
-}
-
 // W [N, K] row-major int8 -> Wt tiles [N/64][K/64][8 k-chunks of 8][64 rows][8 bytes] of biased
 // bytes (w + 128); one thread per 8-byte chunk.
 __global__ __launch_bounds__(256) void tile_w_kernel(const int8_t* __restrict__ W, uint8_t* __restrict__ Wt,
@@ -535,30 +391,6 @@ int launch_tiled(TGemmArgs p) {
   }
 #undef NS2_TILED
   NS2_LAUNCHED("gemm_tiled");
-  return NS2_OK;
-}
-
-template <int BM, int BN, int NW>
-int launch_wreg(TGemmArgs p) {
-  p.tiles_m = (p.M + BM - 1) / BM;
-  p.tiles_n = (p.N + BN - 1) / BN;
-  const dim3 grid(p.tiles_m * p.tiles_n), block(NW * 64);
-  hipStream_t s = ns2::stream();
-  const int rm = !p.resid ? 0 : (p.gate ? 2 : 1);
-#define NS2_WREG(A, R) gemm_wreg_kernel<BM, BN, NW, A, R><<<grid, block, 0, s>>>(p)
-  switch (p.act * 3 + rm) {
-    case 0: NS2_WREG(NS2_ACT_NONE, 0); break;
-    case 1: NS2_WREG(NS2_ACT_NONE, 1); break;
-    case 2: NS2_WREG(NS2_ACT_NONE, 2); break;
-    case 3: NS2_WREG(NS2_ACT_SILU, 0); break;
-    case 4: NS2_WREG(NS2_ACT_SILU, 1); break;
-    case 5: NS2_WREG(NS2_ACT_SILU, 2); break;
-    case 6: NS2_WREG(NS2_ACT_GELU_TANH, 0); break;
-    case 7: NS2_WREG(NS2_ACT_GELU_TANH, 1); break;
-    default: NS2_WREG(NS2_ACT_GELU_TANH, 2); break;
-  }
-#undef NS2_WREG
-  NS2_LAUNCHED("gemm_wreg");
   return NS2_OK;
 }
 

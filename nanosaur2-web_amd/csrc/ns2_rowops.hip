@@ -110,9 +110,11 @@ template <int G, bool NORM>
 __global__ __launch_bounds__(512) void rot_rows_kernel(RotRowsArgs a) {
   const int row = blockIdx.x * 8 + (threadIdx.x >> 6);
   if (row >= a.rows) return;
-  const int lane = threadIdx.x & 63;
   constexpr int cols = 256 * G;
-  const float* src = a.x + (long long)row * a.ldx + lane * 4;
+  // lane l holds elements 16(l%16) + 4(l/16) .. +3 of every group: the layout of the
+  // matrix-core FWHT (its float4 loads still cover each group's 1 KB once per wave)
+  const int lo = fwht_mfma_offset();
+  const float* src = a.x + (long long)row * a.ldx + lo;
   float v[G][4];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
@@ -138,10 +140,11 @@ __global__ __launch_bounds__(512) void rot_rows_kernel(RotRowsArgs a) {
       }
     r = rsqrtf(wave_sum(ss) / (float)cols + a.eps);
   }
+  const half4v_t h = fwht_h16_fragment();
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     if (NORM) {
-      const int c = g * 256 + lane * 4;
+      const int c = g * 256 + lo;
       const float4 sc = *reinterpret_cast<const float4*>(a.mod + a.scaleOff + c);
       const float4 sh = *reinterpret_cast<const float4*>(a.mod + a.shiftOff + c);
       float4 ww = make_float4(1.f, 1.f, 1.f, 1.f);
@@ -151,8 +154,8 @@ __global__ __launch_bounds__(512) void rot_rows_kernel(RotRowsArgs a) {
       v[g][2] = v[g][2] * r * ww.z * (1.0f + sc.z) + sh.z;
       v[g][3] = v[g][3] * r * ww.w * (1.0f + sc.w) + sh.w;
     }
-    fwht256_wave(v[g]);
-    store4_f16(a.y, row, g * 256 + lane * 4, a.ldy, cols, a.tiled, v[g]);
+    fwht256_mfma(v[g], h);
+    store4_f16(a.y, row, g * 256 + lo, a.ldy, cols, a.tiled, v[g]);
   }
 }
 
