@@ -566,11 +566,22 @@ __global__ __launch_bounds__(NW * 64) void flash_kernel(FlashArgs a) {
       }
   };
   // partial row maximum over one 32-key half (kt) of the tile, 16 values per lane
+  // (a tree of three-input maxima: dependency depth 3 instead of 15)
   auto half_max = [&](float16_t (&s)[2][QT], int kt, int qt) {
-    float m = s[kt][qt][0];
-#pragma unroll
-    for (int r = 1; r < 16; ++r) m = fmaxf(m, s[kt][qt][r]);
-    return m;
+    const float16_t& v = s[kt][qt];
+    const float a = __builtin_fmaxf(__builtin_fmaxf(v[0], v[1]), v[2]);
+    const float b = __builtin_fmaxf(__builtin_fmaxf(v[3], v[4]), v[5]);
+    const float c = __builtin_fmaxf(__builtin_fmaxf(v[6], v[7]), v[8]);
+    const float d = __builtin_fmaxf(__builtin_fmaxf(v[9], v[10]), v[11]);
+    const float e = __builtin_fmaxf(__builtin_fmaxf(v[12], v[13]), v[14]);
+    return __builtin_fmaxf(__builtin_fmaxf(__builtin_fmaxf(a, b), c),
+                           __builtin_fmaxf(__builtin_fmaxf(d, e), v[15]));
+  };
+  // maximum of a lane's value and the one 32 lanes away (the other half of the query column)
+  auto col_max = [&](float m) {
+    float lo = m, hi2 = m;
+    permlane32_swap(lo, hi2);
+    return __builtin_fmaxf(lo, hi2);
   };
 
   // Software pipeline, one barrier per tile. Step t:
@@ -601,7 +612,7 @@ __global__ __launch_bounds__(NW * 64) void flash_kernel(FlashArgs a) {
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
     const float m = fmaxf(half_max(sA, 0, qt), half_max(sA, 1, qt));
-    mA[qt] = fmaxf(m, __shfl_xor(m, 32, 64));
+    mA[qt] = col_max(m);
   }
 
   auto step = [&](int t, float16_t (&s_cur)[2][QT], float16_t (&s_nxt)[2][QT], float (&mx_cur)[QT],
@@ -716,15 +727,18 @@ __global__ __launch_bounds__(NW * 64) void flash_kernel(FlashArgs a) {
         } else if (MORE) {
           const int j = i - NV / 2;
           if (BIAS && j == 0) add_bias(s_nxt, kbuf);
-          if (j < 2 * QT) hm[j / QT][j % QT] = half_max(s_nxt, j / QT, j % QT);
+          if (j < 2 * QT) {
+            hm[j / QT][j % QT] = half_max(s_nxt, j / QT, j % QT);
+            // keep the maximum in this slot (it would otherwise sink to its use after the loop)
+            asm volatile("" : "+v"(hm[j / QT][j % QT]));
+          }
         }
         __builtin_amdgcn_sched_barrier(0);
       }
       if (MORE) {
 #pragma unroll
         for (int qt = 0; qt < QT; ++qt) {
-          const float m = fmaxf(hm[0][qt], hm[1][qt]);
-          mx_nxt[qt] = fmaxf(m, __shfl_xor(m, 32, 64));
+          mx_nxt[qt] = col_max(fmaxf(hm[0][qt], hm[1][qt]));
         }
       }
     }
