@@ -153,6 +153,18 @@ int ns2_linear_bf16(const float* A, int lda, const uint16_t* W, const float* bia
                     const float* add, float* C, int M, int N, int K, int ldc, long long cOff,
                     float alpha, int act, int resid, const float* gate, long long gOff);
 
+/* ---- attention without the fused kernel (ops.attention's materialized path, app/gpu/ops.js:
+ *      211-241, softmaxShader) -----------------------------------------------------------
+ * For heads h < H with K/V head g = h / group:
+ *   s_ij = <q_i, k_j> / sqrt(D), masked to j <= i when causal;
+ *   O[i*ldo + h*D ..] = sum_j softmax_j(s_ij) v_j,
+ * q_i = Q[qOff + i*ldq + h*D ..], k_j = K[kOff + j*ldk + g*D ..], v_j = V[vOff + j*ldv + g*D ..].
+ * fp32 throughout. D <= 256, H % group == 0; no key bias (the reference rejects a bias on this
+ * path). Used for causal / grouped-head attention (the Gemma3 text encoder). */
+int ns2_attention_rows(const float* q, const float* k, const float* v, float* o, int Lq, int Lk,
+                       int H, int D, int ldq, int ldk, int ldv, int ldo, long long qOff,
+                       long long kOff, long long vOff, int group, int causal);
+
 /* ---- attention (ops.attention, app/gpu/ops.js:199-209; flashAttentionShader,
  *      app/gpu/kernels.js:119-305) ----------------------------------------------------------
  * For every batch element b and head h < H, with q_i = Q[qOff + b*qBatch + i*ldq + h*D ..],

@@ -461,6 +461,21 @@ napi_value Attention(napi_env env, napi_callback_info info) {
                                      qB, kB, vB, oB, scale, kb, biasStart, biasBatch, qn, kn, eps, cs, sinOff, ropeRows));
 }
 
+// attentionRows(q, k, v, o, Lq, Lk, H, D, ldq, ldk, ldv, ldo, qOff, kOff, vOff, group, causal)
+napi_value AttentionRows(napi_env env, napi_callback_info info) {
+  ARGS(17);
+  auto q = (const float*)c.ptr(0);
+  auto k = (const float*)c.ptr(1);
+  auto v = (const float*)c.ptr(2);
+  auto o = (float*)c.ptr(3);
+  int Lq = c.i32(4), Lk = c.i32(5), H = c.i32(6), D = c.i32(7);
+  int ldq = c.i32(8), ldk = c.i32(9), ldv = c.i32(10), ldo = c.i32(11);
+  long long qOff = c.i64(12), kOff = c.i64(13), vOff = c.i64(14);
+  int group = c.i32(15), causal = c.i32(16);
+  if (c.failed) return nullptr;
+  return check(env, c, ns2_attention_rows(q, k, v, o, Lq, Lk, H, D, ldq, ldk, ldv, ldo, qOff, kOff, vOff, group, causal));
+}
+
 // headNorm(X, w, L, H, D, ld, colOff, rowOff, cs, sinOff, eps)
 napi_value HeadNorm(napi_env env, napi_callback_info info) {
   ARGS(11);
@@ -577,6 +592,7 @@ napi_value Module(napi_env env, napi_value exports) {
       {"tileI8Weight", TileI8Weight}, {"linearI8Tiled", LinearI8Tiled},
       {"tileI8WeightGlu", TileI8WeightGlu}, {"linearI8GluRotTiled", LinearI8GluRotTiled},
       {"linearI8", LinearI8}, {"linearBf16", LinearBf16}, {"attention", Attention},
+      {"attentionRows", AttentionRows},
       {"headNorm", HeadNorm}, {"normMod", NormModT<false>}, {"normModRotateF16", NormModT<true>},
       {"glu", GluT<false>}, {"gluRotateF16", GluT<true>}, {"elementwise", Elementwise},
       {"accumulate", Accumulate}, {"addRows", AddRows}, {"rowSum", RowSum}, {"rmsnorm", Rmsnorm},

@@ -818,7 +818,106 @@ int run_attention(PackArgs pa, FlashArgs fa, int batch, bool vec) {
 
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
+// ---- attention without the fused kernel's restrictions ---------------------------------------
+//
+// The semantics of ops.attention's materialized path (app/gpu/ops.js:211-241): causal masking,
+// grouped K/V heads, any D <= 256, fp32 arithmetic. One wave per (query, head): lane l holds
+// dims [DV l, DV l + DV) of q (pre-scaled by 1/sqrt(D)) and of the output row. Keys are taken
+// four at a time (four independent dot products and wave sums in flight), with an online
+// softmax. The waves of a block are the heads of one K/V group at one query, so they read the
+// same K/V rows together and share them through L1.
+struct RowsArgs {
+  const float* q;
+  const float* k;
+  const float* v;
+  float* o;
+  long long qOff, kOff, vOff;
+  int Lq, Lk, H, D, ldq, ldk, ldv, ldo, group, causal, hpb;
+  float scale;
+};
+
+template <int DV>
+__global__ __launch_bounds__(1024) void attn_rows_kernel(RowsArgs a) {
+  const int i = blockIdx.x;
+  const int h = blockIdx.y * a.hpb + (threadIdx.x >> 6);
+  if (h >= a.H) return;
+  const int lane = threadIdx.x & 63;
+  const int g = h / a.group;
+  const int d0 = lane * DV;
+  const float* qr = a.q + a.qOff + (long long)i * a.ldq + (long long)h * a.D;
+  const float* kb = a.k + a.kOff + (long long)g * a.D;
+  const float* vb = a.v + a.vOff + (long long)g * a.D;
+  float qv[DV], ov[DV];
+#pragma unroll
+  for (int j = 0; j < DV; ++j) {
+    qv[j] = d0 + j < a.D ? qr[d0 + j] * a.scale : 0.f;
+    ov[j] = 0.f;
+  }
+  float m = -INFINITY, l = 0.f;
+  const int kend = a.causal ? (i + 1 < a.Lk ? i + 1 : a.Lk) : a.Lk;
+  auto dot = [&](int j) {
+    const float* kr = kb + (long long)j * a.ldk;
+    float s = 0.f;
+#pragma unroll
+    for (int e = 0; e < DV; ++e) s += d0 + e < a.D ? qv[e] * kr[d0 + e] : 0.f;
+    return s;
+  };
+  auto accumulate = [&](int j, float s) {
+    const float mn = fmaxf(m, s);
+    const float corr = __expf(m - mn), p = __expf(s - mn);
+    l = l * corr + p;
+    const float* vr = vb + (long long)j * a.ldv;
+#pragma unroll
+    for (int e = 0; e < DV; ++e) ov[e] = ov[e] * corr + (d0 + e < a.D ? p * vr[d0 + e] : 0.f);
+    m = mn;
+  };
+  int j = 0;
+  for (; j + 4 <= kend; j += 4) {
+    float s0 = dot(j), s1 = dot(j + 1), s2 = dot(j + 2), s3 = dot(j + 3);
+    s0 = wave_sum(s0);
+    s1 = wave_sum(s1);
+    s2 = wave_sum(s2);
+    s3 = wave_sum(s3);
+    accumulate(j, s0);
+    accumulate(j + 1, s1);
+    accumulate(j + 2, s2);
+    accumulate(j + 3, s3);
+  }
+  for (; j < kend; ++j) accumulate(j, wave_sum(dot(j)));
+  const float inv = l > 0.f ? 1.0f / l : 0.f;
+  float* orow = a.o + (long long)i * a.ldo + (long long)h * a.D;
+#pragma unroll
+  for (int e = 0; e < DV; ++e)
+    if (d0 + e < a.D) orow[d0 + e] = ov[e] * inv;
+}
+
 }  // namespace
+
+extern "C" int ns2_attention_rows(const float* q, const float* k, const float* v, float* o, int Lq, int Lk,
+                                  int H, int D, int ldq, int ldk, int ldv, int ldo, long long qOff,
+                                  long long kOff, long long vOff, int group, int causal) {
+  NS2_READY();
+  if (Lq <= 0 || H <= 0) return NS2_OK;
+  NS2_REQUIRE(q && k && v && o, "ns2_attention_rows: null q, k, v or o");
+  NS2_REQUIRE(D > 0 && D <= 256, "ns2_attention_rows: unsupported head dim %d", D);
+  NS2_REQUIRE(group > 0 && H % group == 0, "ns2_attention_rows: H=%d is not a multiple of group=%d", H, group);
+  NS2_REQUIRE(Lk > 0 && ldq >= D && ldk >= D && ldv >= D && ldo >= H * D && qOff >= 0 && kOff >= 0 && vOff >= 0,
+              "ns2_attention_rows: bad sizes or strides");
+  // the waves of a block: the heads of one K/V group (at most 16)
+  const int hpb = group < 16 ? group : 16;
+  RowsArgs a{q, k, v, o, qOff, kOff, vOff, Lq, Lk, H, D, ldq, ldk, ldv, ldo, group, causal ? 1 : 0, hpb,
+             1.0f / sqrtf((float)D)};
+  const dim3 grid(Lq, (H + hpb - 1) / hpb), block(64 * hpb);
+  ns2::ProfScope prof_("attn_rows");
+  hipStream_t s = ns2::stream();
+  const int dv = (D + 63) / 64;
+  if (dv == 1) attn_rows_kernel<1><<<grid, block, 0, s>>>(a);
+  else if (dv == 2) attn_rows_kernel<2><<<grid, block, 0, s>>>(a);
+  else if (dv == 3) attn_rows_kernel<3><<<grid, block, 0, s>>>(a);
+  else attn_rows_kernel<4><<<grid, block, 0, s>>>(a);
+  NS2_LAUNCHED("attn_rows");
+  return NS2_OK;
+}
 
 extern "C" int ns2_attention(const float* q, const float* k, const float* v, float* o, int batch,
                              int Lq, int Lk, int H, int D, int ldq, int ldk, int ldv, int ldo,

@@ -1,0 +1,121 @@
+// Gemma3-270M text encoder as Nanosaur2 uses it (app/models/gemma3.js): the hidden state after
+// the 17th of 18 layers with the final norm applied (ComfyUI layer="hidden", layer_idx=-2).
+//
+// Embeddings scaled by sqrt(640); RMSNorm weights stored as w - 1 (+1 at load); norms before and
+// after both attention and MLP; q/k norms with split-half RoPE; one K/V head for the four query
+// heads (causal, through ops.attention's materialized-path kernel); GELU(tanh)-gated MLP. Every
+// 6th layer is global (RoPE theta 1e6), the others local (theta 1e4; their 512-token window
+// never applies at <= 256 tokens).
+
+import * as ops from "./ops.js";
+import { concatLinears } from "./weights.js";
+import { ropeTable } from "./common.js";
+
+export const GEMMA = { layers: 18, hidden: 640, heads: 4, kvHeads: 1, headDim: 256, globalEvery: 6 };
+const RUN = GEMMA.layers - 1; // layers needed for the penultimate hidden state
+
+export class Gemma3 {
+  // st: { linear, vector, rows, has } (weights.js SafeTensors or the synthetic source)
+  static async load(gpu, st, onProgress) {
+    const m = new Gemma3(gpu, st);
+    const L = [];
+    for (let i = 0; i < RUN; i++) {
+      const p = `model.layers.${i}.`;
+      const norm = (n) => st.vector(gpu, p + n + ".weight", 1);
+      L.push({
+        global: (i + 1) % GEMMA.globalEvery === 0,
+        inNorm: await norm("input_layernorm"),
+        postAttnNorm: await norm("post_attention_layernorm"),
+        preMlpNorm: await norm("pre_feedforward_layernorm"),
+        postMlpNorm: await norm("post_feedforward_layernorm"),
+        qn: await norm("self_attn.q_norm"),
+        kn: await norm("self_attn.k_norm"),
+        qkv: concatLinears(gpu, [await st.linear(gpu, p + "self_attn.q_proj."), await st.linear(gpu, p + "self_attn.k_proj."),
+          await st.linear(gpu, p + "self_attn.v_proj.")]),
+        o: await st.linear(gpu, p + "self_attn.o_proj."),
+        gateUp: concatLinears(gpu, [await st.linear(gpu, p + "mlp.gate_proj."), await st.linear(gpu, p + "mlp.up_proj.")]),
+        down: await st.linear(gpu, p + "mlp.down_proj."),
+      });
+      if (onProgress) onProgress((i + 1) / RUN);
+    }
+    m.layers = L;
+    m.norm = await st.vector(gpu, "model.norm.weight", 1);
+    return m;
+  }
+
+  constructor(gpu, st) {
+    this.gpu = gpu;
+    this.st = st; // embedding rows are gathered from the source on demand
+  }
+
+  // Token ids -> Tensor [L, 640] on the device.
+  async encode(ids) {
+    const x = this.embed(await this.st.rows("model.embed_tokens.weight", ids), ids.length);
+    return this.encodeEmbedded(x);
+  }
+
+  // Host embedding rows [L, 640] -> scaled device tensor.
+  embed(rows, L) {
+    const scale = Math.sqrt(GEMMA.hidden);
+    const e = new Float32Array(rows.length);
+    for (let i = 0; i < rows.length; i++) e[i] = rows[i] * scale;
+    return this.gpu.fromArray(e, [L, GEMMA.hidden]);
+  }
+
+  // The layer stack on a device tensor x [L, 640] (released here); returns the normed output.
+  encodeEmbedded(x) {
+    const gpu = this.gpu;
+    const { hidden: D, heads: H, kvHeads: KH, headDim: HD } = GEMMA;
+    const Lt = x.shape[0];
+    const qkvW = (H + 2 * KH) * HD;
+    const csLocal = ropeTable(gpu, Lt, HD, 1e4);
+    const csGlobal = ropeTable(gpu, Lt, HD, 1e6);
+    for (const l of this.layers) {
+      const cs = l.global ? csGlobal : csLocal;
+      const h = ops.rmsnorm(gpu, x, l.inNorm, D);
+      const qkv = ops.linear(gpu, h, l.qkv, { name: "te.qkv" }); // [Lt, q 1024 | k 256 | v 256]
+      h.release();
+      ops.headNorm(gpu, qkv, l.qn, { L: Lt, H, D: HD, ld: qkvW, colOff: 0, cs });
+      ops.headNorm(gpu, qkv, l.kn, { L: Lt, H: KH, D: HD, ld: qkvW, colOff: H * HD, cs });
+      const a = ops.attention(gpu, {
+        q: qkv, k: qkv, v: qkv, Lq: Lt, Lk: Lt, H, D: HD, ldq: qkvW, ldk: qkvW, ldv: qkvW,
+        qOff: 0, kOff: H * HD, vOff: (H + KH) * HD, group: H / KH, causal: true,
+      });
+      qkv.release();
+      const o = ops.linear(gpu, a, l.o, { name: "te.o" });
+      a.release();
+      const on = ops.rmsnorm(gpu, o, l.postAttnNorm, D);
+      o.release();
+      ops.accumulate(gpu, x, on);
+      on.release();
+      const h2 = ops.rmsnorm(gpu, x, l.preMlpNorm, D);
+      const gu = ops.linear(gpu, h2, l.gateUp, { name: "te.mlp" });
+      h2.release();
+      const g = ops.glu(gpu, gu, "gelu_tanh");
+      gu.release();
+      const d = ops.linear(gpu, g, l.down, { name: "te.mlp" });
+      g.release();
+      const dn = ops.rmsnorm(gpu, d, l.postMlpNorm, D);
+      d.release();
+      ops.accumulate(gpu, x, dn);
+      dn.release();
+    }
+    csLocal.release();
+    csGlobal.release();
+    const out = ops.rmsnorm(gpu, x, this.norm, D);
+    x.release();
+    return out;
+  }
+
+  unload() {
+    const seen = new Set();
+    const walk = (o) => {
+      if (!o || typeof o !== "object" || seen.has(o)) return;
+      seen.add(o);
+      if (typeof o.destroy === "function" && o.ptr !== undefined) { o.destroy(); return; }
+      for (const k of Object.keys(o)) if (k !== "gpu" && k !== "st") walk(o[k]);
+    };
+    walk(this.layers);
+    walk(this.norm);
+  }
+}

@@ -204,18 +204,29 @@ export function accumulate(gpu, y, a) {
   gpu.run("accumulate", 0, () => native.accumulate(addr(y), addr(a), y.size));
 }
 
-// Multi-head attention (app/gpu/ops.js:194-209), fused kernel only.
-//  q: [Lq, ldq] with head h at column qOff + h*D; k, v: [Lk, ldk]/[Lk, ldv]. Output [Lq, H*D].
+// Multi-head attention (app/gpu/ops.js:194-242): the fused flash kernel when non-causal, group
+// 1, D % 32 = 0, D <= 128 and 4-aligned; otherwise the materialized path's semantics (causal
+// masking, K/V head h / group) on the row kernel.
+//  q: [Lq, ldq] with head h at column qOff + h*D; k, v: [Lk, ldk]/[Lk, ldv] with K/V head
+//  h / group at kOff / vOff + (h / group)*D. Output [Lq, H*D].
 //  bias: optional Tensor of additive score biases for keys biasStart...
 // Fused prologue options of this build: qNorm/kNorm (per-head RMSNorm weights, the DiT's
 // headNorm), cs (RoPE table with .sinOff) applied to q/k rows < ropeRows, eps.
 export function attention(gpu, { q, k, v, Lq, Lk, H, D, ldq, ldk, ldv, qOff = 0, kOff = 0, vOff = 0, group = 1,
   causal = false, bias = null, biasStart = 0, out, qNorm = null, kNorm = null, cs = null, ropeRows = 0, eps = 1e-6 }) {
-  if (causal || group !== 1) {
-    throw new Error("attention: causal / grouped-query attention (the reference's unfused text-encoder path) is not part of this build");
-  }
-  if (D % 32 || D > 128) throw new Error(`flash attention: unsupported head dim ${D}`);
   const o = out || gpu.empty([Lq, H * D]);
+  // the fused kernel's conditions (app/gpu/ops.js:202-203); otherwise the materialized path's
+  // semantics (:211-241), which rejects a key bias
+  const aligned = [ldq, ldk, ldv, qOff, kOff, vOff].every((x) => x % 4 === 0);
+  if (causal || group !== 1 || D % 32 || D > 128 || !aligned) {
+    if (bias) throw new Error("attention: key bias needs the fused kernel");
+    if (qNorm || kNorm || cs) throw new Error("attention: fused head norms need the fused kernel");
+    if (D > 256) throw new Error(`attention: unsupported head dim ${D}`);
+    gpu.run("attn.rows", 4 * Lq * Lk * D * H, () =>
+      native.attentionRows(addr(q), addr(k), addr(v), addr(o), Lq, Lk, H, D, ldq, ldk, ldv, H * D, qOff, kOff, vOff,
+        group, causal ? 1 : 0));
+    return o;
+  }
   gpu.run("attn.flash", 4 * Lq * Lk * D * H, () =>
     native.attention(addr(q), addr(k), addr(v), addr(o), 1, Lq, Lk, H, D, ldq, ldk, ldv, H * D, qOff, kOff, vOff, 0,
       0, 0, 0, 0, 1 / Math.sqrt(D), addr(bias), biasStart, 0, addr(qNorm), addr(kNorm), eps,

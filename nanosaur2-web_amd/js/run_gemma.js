@@ -1,0 +1,109 @@
+// Command-line driver for the Gemma3 text encoder on the MI355X through the Node host.
+//
+//   node run_gemma.js (--weights FILE.safetensors | --synthetic SEED)
+//                     (--ids FILE.json | --tokens N[,SEED])
+//                     [--out FILE.f32] [--warmup N] [--reps N] [--profile]
+//
+// --ids holds a JSON array of token ids; --tokens draws N seeded ids. --out writes the hidden
+// states [L, 640] as raw fp32. With --reps the encoder is timed on device-resident embeddings
+// (stream events and wall clock); one JSON line with the timings (and the per-op profile with
+// --profile) is printed.
+
+import fs from "fs";
+import { GPU } from "./device.js";
+import { native } from "./native.js";
+import * as ops from "./ops.js";
+import { Gemma3 } from "./gemma3.js";
+import { SafeTensors } from "./weights.js";
+import { SyntheticWeights } from "./synthetic.js";
+
+function parseArgs(argv) {
+  const a = { warmup: 0, reps: 0 };
+  for (let i = 0; i < argv.length; i++) {
+    const k = argv[i];
+    const next = () => argv[++i];
+    if (k === "--weights") a.weights = next();
+    else if (k === "--synthetic") a.synthetic = Number(next());
+    else if (k === "--ids") a.ids = JSON.parse(fs.readFileSync(next(), "utf8"));
+    else if (k === "--tokens") a.tokens = next().split(",").map(Number);
+    else if (k === "--out") a.out = next();
+    else if (k === "--warmup") a.warmup = Number(next());
+    else if (k === "--reps") a.reps = Number(next());
+    else if (k === "--profile") a.profile = true;
+    else throw new Error(`unknown argument ${k}`);
+  }
+  return a;
+}
+
+function seededIds([n, seed = 1], vocab) {
+  let s = (seed * 2654435761) >>> 0 || 1;
+  const ids = [];
+  for (let i = 0; i < n; i++) {
+    s ^= s << 13; s >>>= 0; s ^= s >>> 17; s ^= s << 5; s >>>= 0;
+    ids.push(s % vocab);
+  }
+  return ids;
+}
+
+const median = (xs) => {
+  const s = [...xs].sort((p, q) => p - q);
+  return s.length ? s[Math.floor(s.length / 2)] : null;
+};
+
+async function main() {
+  const a = parseArgs(process.argv.slice(2));
+  const t0 = Date.now();
+  const gpu = await GPU.create({ profile: !!a.profile });
+  const st = a.weights ? await SafeTensors.open(a.weights) : new SyntheticWeights(a.synthetic || 3, { gemma: true });
+  const te = await Gemma3.load(gpu, st);
+  const vocab = (st.info ? st.info("model.embed_tokens.weight") : st.spec.get("model.embed_tokens.weight")).shape[0];
+  const ids = a.ids || seededIds(a.tokens || [256, 1], vocab);
+  const rows = await st.rows("model.embed_tokens.weight", ids);
+  const report = { tokens: ids.length, load_ms: Date.now() - t0, device: gpu.info };
+
+  if (a.out) {
+    const h = te.encodeEmbedded(te.embed(rows, ids.length));
+    const out = await gpu.read(h);
+    h.release();
+    fs.writeFileSync(a.out, Buffer.from(out.buffer));
+    report.out = a.out;
+  }
+  if (a.reps > 0) {
+    const emb = te.embed(rows, ids.length);
+    // each pass starts from a copy of the embeddings (the stack updates its input in place)
+    const pass = () => te.encodeEmbedded(ops.elementwise(gpu, "copy", emb)).release();
+    for (let i = 0; i < a.warmup; i++) pass();
+    await gpu.sync();
+    if (gpu.profiler) gpu.profiler.reset();
+    const evA = native.eventCreate();
+    const evB = native.eventCreate();
+    const dev = [];
+    const wall = [];
+    for (let i = 0; i < a.reps; i++) {
+      const w0 = process.hrtime.bigint();
+      native.eventRecord(evA);
+      pass();
+      native.eventRecord(evB);
+      await gpu.sync();
+      wall.push(Number(process.hrtime.bigint() - w0) / 1e6);
+      dev.push(native.eventElapsed(evA, evB));
+    }
+    if (gpu.profiler) {
+      const prof = await gpu.profiler.report();
+      report.profile = prof.map((r) => ({ name: r.name, count: r.count / a.reps, ms: r.ms / a.reps, tflops: r.flops ? r.flops / (r.ms / 1e3) / 1e12 : null }));
+    }
+    emb.release();
+    native.eventDestroy(evA);
+    native.eventDestroy(evB);
+    Object.assign(report, { reps: a.reps, warmup: a.warmup, ms_device: dev, ms_wall: wall,
+      ms_device_median: median(dev), ms_wall_median: median(wall) });
+  }
+  if (st.close) st.close();
+  te.unload();
+  process.stdout.write(JSON.stringify(report) + "\n");
+}
+
+main().catch((e) => {
+  process.stderr.write(`[run_gemma] error: ${e && e.stack ? e.stack : e}\n`);
+  process.exit(1);
+});

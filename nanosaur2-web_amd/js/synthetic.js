@@ -50,6 +50,30 @@ export function ditSpec({ I = 4096, blocks = 18, textBlocks = 2, ctx = 640 } = {
   return s;
 }
 
+// name -> spec for the Gemma3-270M text encoder (app/models/gemma3.js:13-45): bf16 linears and
+// norms, the [262144, 640] embedding table (its rows are generated on demand).
+export function gemmaSpec({ layers = 17, vocab = 262144 } = {}) {
+  const s = new Map();
+  const bf = (n, shape) => s.set(n, { shape, kind: "bf16" });
+  const vec = (n, len) => s.set(n, { shape: [len], kind: "vec" });
+  s.set("model.embed_tokens.weight", { shape: [vocab, 640], kind: "table" });
+  for (let i = 0; i < layers; i++) {
+    const p = `model.layers.${i}.`;
+    for (const n of ["input_layernorm", "post_attention_layernorm", "pre_feedforward_layernorm", "post_feedforward_layernorm"]) vec(p + n + ".weight", 640);
+    vec(p + "self_attn.q_norm.weight", 256);
+    vec(p + "self_attn.k_norm.weight", 256);
+    bf(p + "self_attn.q_proj.weight", [1024, 640]);
+    bf(p + "self_attn.k_proj.weight", [256, 640]);
+    bf(p + "self_attn.v_proj.weight", [256, 640]);
+    bf(p + "self_attn.o_proj.weight", [640, 1024]);
+    bf(p + "mlp.gate_proj.weight", [2048, 640]);
+    bf(p + "mlp.up_proj.weight", [2048, 640]);
+    bf(p + "mlp.down_proj.weight", [640, 2048]);
+  }
+  vec("model.norm.weight", 640);
+  return s;
+}
+
 // xorshift128+-style generator on 32-bit halves (seeded per tensor name)
 function rng(seed, name) {
   let h = (seed ^ 0x9e3779b9) >>> 0;
@@ -70,7 +94,7 @@ function rng(seed, name) {
 export class SyntheticWeights {
   constructor(seed = 3, opts = {}) {
     this.seed = seed;
-    this.spec = ditSpec(opts);
+    this.spec = opts.gemma ? gemmaSpec(opts) : ditSpec(opts);
   }
   has(name) {
     if (name.endsWith("weight_scale")) return this.spec.has(name.replace(/_scale$/, ""));
@@ -86,10 +110,20 @@ export class SyntheticWeights {
     }
     return out;
   }
-  async vector(gpu, name) {
+  async vector(gpu, name, add = 0) {
     const e = this.spec.get(name);
     if (!e) throw new Error(`missing tensor ${name}`);
-    return gpu.upload(this.normal(name, e.shape[0], 0.02));
+    const v = this.normal(name, e.shape[0], 0.02);
+    return gpu.upload(add ? v.map((x) => x + add) : v);
+  }
+  // rows of a table (embeddings), each generated from its own seed
+  async rows(name, ids) {
+    const e = this.spec.get(name);
+    if (!e) throw new Error(`missing tensor ${name}`);
+    const dim = e.shape[1];
+    const out = new Float32Array(ids.length * dim);
+    ids.forEach((id, i) => out.set(this.normal(`${name}#${id}`, dim, 1.0), i * dim));
+    return out;
   }
   async linear(gpu, base) {
     const e = this.spec.get(base + "weight");

@@ -8,6 +8,8 @@
 // (app/weights.js:127-131). bf16 weights are uploaded as raw bf16 and decoded in the GEMM.
 
 import fs from "fs";
+import { addr } from "./device.js";
+import { native, EW } from "./native.js";
 
 const BYTES = { F32: 4, F16: 2, BF16: 2, I8: 1, U8: 1, I32: 4, I64: 8 };
 
@@ -113,6 +115,23 @@ export class SafeTensors {
     return JSON.parse(Buffer.from(u8).toString("utf8"));
   }
 
+  // Rows `ids` of a 2-D table (embeddings) as fp32, read row by row from the file
+  // (app/weights.js:97-108).
+  async rows(name, ids) {
+    const t = this.info(name);
+    const dim = t.shape[1];
+    const rowBytes = dim * BYTES[t.dtype];
+    const out = new Float32Array(ids.length * dim);
+    const u8 = new Uint8Array(rowBytes);
+    ids.forEach((id, i) => {
+      if (id < 0 || id >= t.shape[0]) throw new Error(`${name}: row ${id} out of range`);
+      fs.readSync(this.fd, u8, 0, rowBytes, this.dataStart + t.data_offsets[0] + id * rowBytes);
+      const row = t.dtype === "BF16" ? bf16ToF32(u8) : t.dtype === "F16" ? f16ToF32(u8) : new Float32Array(u8.slice().buffer);
+      out.set(row, i * dim);
+    });
+    return out;
+  }
+
   // f32 vector on the GPU; add: a constant added to every element (app/weights.js:111-115)
   async vector(gpu, name, add = 0) {
     const v = await this.f32(name);
@@ -138,4 +157,42 @@ export class SafeTensors {
     }
     return { kind: "bf16", N, K, buf: gpu.upload(await this.bf16(base + "weight")), bias, name };
   }
+}
+
+// Stack bf16 linears that share an input into one [sum N, K] weight (q, k, v -> qkv), with
+// `parts` naming each slice; biases are stacked too, zero for parts without one
+// (app/weights.js:148-172). The copies run on the device; the parts' buffers are freed.
+export function concatLinears(gpu, Ws) {
+  const { K } = Ws[0];
+  if (!Ws.every((w) => w.kind === "bf16" && w.K === K)) throw new Error("concatLinears: mismatched weights");
+  if (K % 2) throw new Error("concatLinears: K must be even");
+  const N = Ws.reduce((a, w) => a + w.N, 0);
+  const out = { kind: "bf16", K, N, parts: [], bias: null };
+  let off = 0;
+  for (const w of Ws) {
+    out.parts.push({ name: w.name, off, n: w.N });
+    off += w.N;
+  }
+  // bf16 rows as 32-bit words (K even), copied with the elementwise copy op
+  out.buf = gpu.upload(new Uint32Array((N * K) / 2));
+  off = 0;
+  for (const w of Ws) {
+    const words = (w.N * K) / 2;
+    native.elementwise(EW.copy, addr(w.buf), null, addr(out.buf) + BigInt(off * K * 2), words);
+    off += w.N;
+  }
+  if (Ws.some((w) => w.bias)) {
+    out.bias = gpu.upload(new Float32Array(N));
+    off = 0;
+    for (const w of Ws) {
+      if (w.bias) native.elementwise(EW.copy, addr(w.bias), null, addr(out.bias) + BigInt(off * 4), w.N);
+      off += w.N;
+    }
+  }
+  native.sync();
+  for (const w of Ws) {
+    w.buf.destroy();
+    if (w.bias) w.bias.destroy();
+  }
+  return out;
 }

@@ -59,6 +59,8 @@ SIGNATURES = {
     "ns2_attention": [c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
                       c_int, c_ll, c_ll, c_ll, c_ll, c_ll, c_ll, c_ll, c_ll, c_float, c_vp, c_int,
                       c_ll, c_vp, c_vp, c_float, c_vp, c_ll, c_int],
+    "ns2_attention_rows": [c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
+                           c_ll, c_ll, c_ll, c_int, c_int],
     "ns2_head_norm": [c_vp, c_vp, c_int, c_int, c_int, c_int, c_ll, c_ll, c_vp, c_ll, c_float],
     "ns2_norm_mod": [c_vp, c_vp, c_ll, c_ll, c_int, c_int, c_vp, c_float, c_vp],
     "ns2_norm_mod_rotate_f16": [c_vp, c_vp, c_ll, c_ll, c_int, c_int, c_vp, c_float, c_vp, c_int],
@@ -197,6 +199,11 @@ class Lib:
                   ldv, ldo, qOff, kOff, vOff, oOff, qBatch, kBatch, vBatch, oBatch, scale,
                   _ptr(key_bias), biasStart, biasBatch, _ptr(q_norm), _ptr(k_norm), eps,
                   _ptr(rope_cs), sin_off, rope_rows)
+
+    def attention_rows(self, q, k, v, o, *, Lq, Lk, H, D, ldq, ldk, ldv, ldo, qOff=0, kOff=0, vOff=0,
+                       group=1, causal=False):
+        self.call("ns2_attention_rows", _ptr(q), _ptr(k), _ptr(v), _ptr(o), Lq, Lk, H, D, ldq, ldk, ldv,
+                  ldo, qOff, kOff, vOff, group, int(causal))
 
     def head_norm(self, X, w, L, H, D, ld, colOff=0, rowOff=0, cs=None, sinOff=0, eps=1e-6):
         self.call("ns2_head_norm", _ptr(X), _ptr(w), L, H, D, ld, colOff, rowOff, _ptr(cs), sinOff, eps)

@@ -282,6 +282,82 @@ def joint_attention_op(q, k, v, L, cos, sin, key_bias=None, bias_start=None, hea
     return attention_heads(qr, kr, v, heads, hd, bias)
 
 
+def attention_rows(q, k, v, heads, hd, group=1, causal=False):
+    """The materialized attention path of ops.attention (app/gpu/ops.js:211-241 with
+    softmaxShader): per head h with K/V head h // group, softmax(q k^T / sqrt(hd)) v over the
+    keys, masked to key <= query when causal. q [Lq, heads*hd], k/v [Lk, (heads//group)*hd]."""
+    Lq, Lk = q.shape[0], k.shape[0]
+    kvh = heads // group
+    qh = q.reshape(Lq, heads, hd).transpose(0, 1)
+    kh = k.reshape(Lk, kvh, hd).transpose(0, 1).repeat_interleave(group, 0)
+    vh = v.reshape(Lk, kvh, hd).transpose(0, 1).repeat_interleave(group, 0)
+    mask = None
+    if causal:
+        mask = torch.full((Lq, Lk), float("-inf"), dtype=q.dtype).triu(1)[None]
+    o = F.scaled_dot_product_attention(qh[None], kh[None], vh[None], attn_mask=mask)[0]
+    return o.transpose(0, 1).reshape(Lq, heads * hd)
+
+
+def attention_rows_bruteforce(q, k, v, heads, hd, group=1, causal=False):
+    """attention_rows written out query by query with explicit max/exp/sum; pins it."""
+    Lq = q.shape[0]
+    out = torch.empty(Lq, heads * hd, dtype=q.dtype)
+    for h in range(heads):
+        g = h // group
+        for i in range(Lq):
+            n = i + 1 if causal else k.shape[0]
+            qi = q[i, h * hd:(h + 1) * hd]
+            kk = k[:n, g * hd:(g + 1) * hd]
+            vv = v[:n, g * hd:(g + 1) * hd]
+            s = (kk @ qi) / math.sqrt(hd)
+            p = torch.exp(s - s.max())
+            out[i, h * hd:(h + 1) * hd] = (p @ vv) / p.sum()
+    return out
+
+
+# --------------------------------------------------------------------------- Gemma3 text encoder
+
+GEMMA = {"hidden": 640, "heads": 4, "kv_heads": 1, "head_dim": 256, "layers": 17, "global_every": 6}
+
+
+def gemma_rope(L, theta, D=256, dtype=torch.float32):
+    """tools/reference.py:170-173: angles l / theta^(2i/D), i < D/2 (cos, sin)."""
+    inv = 1.0 / (theta ** (torch.arange(0, D, 2).to(dtype) / D))
+    a = torch.arange(L).to(dtype)[:, None] * inv[None]
+    return a.cos(), a.sin()
+
+
+def gemma_encode(W, ids, dtype=torch.float32):
+    """Hidden state after the 17th of 18 layers with the final norm applied
+    (tools/reference.py:176-200; app/models/gemma3.js:49-95): scaled embeddings, pre/post norms
+    around attention and MLP with RMSNorm weights stored as w - 1, q/k norms, split-half RoPE
+    (theta 1e6 on every 6th layer, 1e4 otherwise), causal attention with one K/V head for the
+    four query heads, GELU(tanh)-gated MLP."""
+    G = GEMMA
+    H, KH, HD = G["heads"], G["kv_heads"], G["head_dim"]
+    x = W("model.embed_tokens.weight")[torch.tensor(ids)].to(dtype) * math.sqrt(G["hidden"])
+    L = x.shape[0]
+    ropes = {t: gemma_rope(L, t, HD, dtype) for t in (1e4, 1e6)}
+    for i in range(G["layers"]):
+        p = f"model.layers.{i}."
+        n = lambda k: W(p + k + ".weight").to(dtype) + 1.0  # noqa: E731
+        cos, sin = ropes[1e6 if (i + 1) % G["global_every"] == 0 else 1e4]
+        h = rms_norm(x, n("input_layernorm"))
+        q = (h @ W(p + "self_attn.q_proj.weight").to(dtype).T).view(L, H, HD).transpose(0, 1)
+        k = (h @ W(p + "self_attn.k_proj.weight").to(dtype).T).view(L, KH, HD).transpose(0, 1)
+        v = h @ W(p + "self_attn.v_proj.weight").to(dtype).T
+        q = rope_split_half(rms_norm(q, n("self_attn.q_norm")), cos, sin).transpose(0, 1).reshape(L, H * HD)
+        k = rope_split_half(rms_norm(k, n("self_attn.k_norm")), cos, sin).transpose(0, 1).reshape(L, KH * HD)
+        a = attention_rows(q, k, v, H, HD, group=H // KH, causal=True)
+        a = a @ W(p + "self_attn.o_proj.weight").to(dtype).T
+        x = x + rms_norm(a, n("post_attention_layernorm"))
+        h = rms_norm(x, n("pre_feedforward_layernorm"))
+        g = F.gelu(h @ W(p + "mlp.gate_proj.weight").to(dtype).T, approximate="tanh")
+        g = g * (h @ W(p + "mlp.up_proj.weight").to(dtype).T)
+        x = x + rms_norm(g @ W(p + "mlp.down_proj.weight").to(dtype).T, n("post_feedforward_layernorm"))
+    return rms_norm(x, W("model.norm.weight").to(dtype) + 1.0)
+
+
 # --------------------------------------------------------------------------- DiT pass
 
 def lin(W, name, x):

@@ -17,6 +17,7 @@ dev = "cuda"
 TOL = 2e-3        # parity tolerance for attention / GEMM outputs (max-abs / max|ref|, rel-L2)
 TOL_F32 = 1e-5    # kernels that compute in fp32 end to end
 TOL_F16_OUT = 2e-3  # fp32 math, fp16-rounded output
+TOL_ROWS = 1e-4  # fp32 attention with the hardware exp (v_exp_f32)
 
 
 def gen(seed):
@@ -596,3 +597,45 @@ def test_fill_and_errors(ns2lib):
         ns2lib.linear_i8(buf, 0, 100, buf, buf, buf, 4, 4, 100)
     with pytest.raises(ns2.NS2Error, match="head dim"):
         ns2lib.attention(buf, buf, buf, buf, Lq=4, Lk=4, H=1, D=80, ldq=80, ldk=80, ldv=80, ldo=80)
+
+
+# ------------------------------------------------------------------ materialized-path attention
+
+@pytest.mark.parametrize("D,H,group,causal,Lq,Lk", [
+    (256, 4, 4, True, 37, 37),    # the Gemma3 text encoder: 4 query heads over 1 K/V head
+    (256, 4, 4, True, 256, 256),  # its longest prompt
+    (64, 8, 1, False, 50, 70),
+    (96, 6, 2, True, 33, 33),
+    (40, 3, 3, False, 9, 130),    # head dim not a multiple of 32
+    (200, 2, 1, True, 1, 1),
+])
+def test_attention_rows(ns2lib, D, H, group, causal, Lq, Lk):
+    """ns2_attention_rows (ops.attention's materialized path, app/gpu/ops.js:211-241) against the
+    oracle's softmax(q k^T / sqrt(D)) v with grouped K/V heads and the causal mask."""
+    g = gen(D * 7 + H + Lq)
+    KH = H // group
+    q = torch.randn(Lq, H * D, generator=g)
+    k = torch.randn(Lk, KH * D, generator=g)
+    v = torch.randn(Lk, KH * D, generator=g)
+    o = torch.empty(Lq, H * D, device=dev)
+    ns2lib.attention_rows(q.to(dev), k.to(dev), v.to(dev), o, Lq=Lq, Lk=Lk, H=H, D=D, ldq=H * D,
+                          ldk=KH * D, ldv=KH * D, ldo=H * D, group=group, causal=causal)
+    torch.cuda.synchronize()
+    ref = O.attention_rows(q.double(), k.double(), v.double(), H, D, group=group, causal=causal)
+    assert_close(o.cpu(), ref, TOL_ROWS, f"attention_rows D={D} H={H} group={group} causal={causal}")
+
+
+def test_attention_rows_packed_qkv_view(ns2lib):
+    """q, k and v as column windows of one [L, 1536] buffer (the Gemma3 layer's fused qkv)."""
+    L, H, D = 29, 4, 256
+    W = (H + 2) * D
+    g = gen(77)
+    qkv = torch.randn(L, W, generator=g)
+    o = torch.empty(L, H * D, device=dev)
+    d = qkv.to(dev)
+    ns2lib.attention_rows(d, d, d, o, Lq=L, Lk=L, H=H, D=D, ldq=W, ldk=W, ldv=W, ldo=H * D,
+                          qOff=0, kOff=H * D, vOff=(H + 1) * D, group=H, causal=True)
+    torch.cuda.synchronize()
+    x = qkv.double()
+    ref = O.attention_rows(x[:, :H * D], x[:, H * D:(H + 1) * D], x[:, (H + 1) * D:], H, D, group=H, causal=True)
+    assert_close(o.cpu(), ref, TOL_ROWS, "attention_rows packed qkv")

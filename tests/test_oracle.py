@@ -215,3 +215,49 @@ def test_timestep_embedding_and_glu_rowsum():
     assert torch.allclose(O.glu(x), torch.tensor([[0.0, 2.0 / (1 + math.exp(-2.0)) * 5.0]], dtype=f64))
     xs = torch.tensor([[1.0, 2.0], [3.0, 4.0]], dtype=f64)
     assert torch.allclose(O.row_sum(xs, torch.tensor([2.0, -1.0], dtype=f64), 0.5), torch.tensor([[-0.5, 0.0]], dtype=f64))
+
+
+# ----------------------------------------------------------------------------- Gemma3 pieces
+
+@pytest.mark.parametrize("group,causal", [(1, False), (1, True), (4, True), (2, False)])
+def test_attention_rows_matches_bruteforce(group, causal):
+    g = torch.Generator().manual_seed(group * 10 + causal)
+    H, hd, L = 4, 16, 9
+    q = torch.randn(L, H * hd, generator=g, dtype=torch.float64)
+    k = torch.randn(L, H // group * hd, generator=g, dtype=torch.float64)
+    v = torch.randn(L, H // group * hd, generator=g, dtype=torch.float64)
+    got = O.attention_rows(q, k, v, H, hd, group=group, causal=causal)
+    ref = O.attention_rows_bruteforce(q, k, v, H, hd, group=group, causal=causal)
+    assert torch.allclose(got, ref, atol=1e-12)
+
+
+def test_attention_rows_causal_invariants():
+    g = torch.Generator().manual_seed(5)
+    H, hd, L = 2, 8, 7
+    q = torch.randn(L, H * hd, generator=g, dtype=torch.float64)
+    k = torch.randn(L, H * hd, generator=g, dtype=torch.float64)
+    v = torch.randn(L, H * hd, generator=g, dtype=torch.float64)
+    o = O.attention_rows(q, k, v, H, hd, causal=True)
+    # the first query sees only the first key: its output is v_0
+    assert torch.allclose(o[0], v[0], atol=1e-12)
+    # changing future keys leaves earlier outputs unchanged
+    k2, v2 = k.clone(), v.clone()
+    k2[4:] += 3.0
+    v2[4:] -= 1.0
+    o2 = O.attention_rows(q, k2, v2, H, hd, causal=True)
+    assert torch.allclose(o[:4], o2[:4], atol=1e-12) and not torch.allclose(o[4:], o2[4:])
+    # one K/V head repeated equals grouped attention with group = H
+    kk = k[:, :hd].repeat(1, H)
+    vv = v[:, :hd].repeat(1, H)
+    assert torch.allclose(O.attention_rows(q, k[:, :hd], v[:, :hd], H, hd, group=H, causal=True),
+                          O.attention_rows(q, kk, vv, H, hd, causal=True), atol=1e-12)
+
+
+def test_gemma_rope_closed_form():
+    cos, sin = O.gemma_rope(5, 1e4, D=8, dtype=torch.float64)
+    for l in range(5):
+        for i in range(4):
+            a = l / 1e4 ** (2 * i / 8)
+            assert abs(cos[l, i] - math.cos(a)) < 1e-12 and abs(sin[l, i] - math.sin(a)) < 1e-12
+    # position 0 is the identity
+    assert torch.all(cos[0] == 1) and torch.all(sin[0] == 0)
