@@ -221,6 +221,13 @@ int ns2_add_rows(const float* a, const float* b, float* y, int rows, int n);
 int ns2_row_sum(const float* x, const float* w, float* y, int rows, int N, float scale);
 /* ops.rmsnorm (app/gpu/ops.js:111-117, kernels.js:60-80): y = x * rsqrt(mean x^2 + eps) * w. */
 int ns2_rmsnorm(const float* x, const float* w, float* y, int rows, int cols, float eps);
+/* The Gemma3 sandwich norms in one launch: x += rmsnorm(a) * w_add (the post-attention /
+ * post-MLP norm and the residual add, app/models/gemma3.js:76-77, 87-88 = ops.rmsnorm +
+ * ops.accumulate), then, when y is not null, y = rmsnorm(x) * w_out (the next norm: the MLP's
+ * pre-norm, the next layer's input norm or the final norm, gemma3.js:80, 62, 92). Rows of
+ * `cols` floats; x, a and y must not alias. Additive to the reference interface. */
+int ns2_add_rmsnorm(float* x, const float* a, const float* w_add, const float* w_out, float* y, int rows,
+                    int cols, float eps);
 
 #ifdef __cplusplus
 }

@@ -578,6 +578,20 @@ napi_value Rmsnorm(napi_env env, napi_callback_info info) {
   return check(env, c, ns2_rmsnorm(x, w, y, rows, cols, eps));
 }
 
+// addRmsnorm(x, a, wAdd, wOut, y, rows, cols, eps)
+napi_value AddRmsnorm(napi_env env, napi_callback_info info) {
+  ARGS(8);
+  auto x = (float*)c.ptr(0);
+  auto a = (const float*)c.ptr(1);
+  auto wa = (const float*)c.ptr(2);
+  auto wo = (const float*)c.ptr(3);
+  auto y = (float*)c.ptr(4);
+  int rows = c.i32(5), cols = c.i32(6);
+  float eps = c.f32(7);
+  if (c.failed) return nullptr;
+  return check(env, c, ns2_add_rmsnorm(x, a, wa, wo, y, rows, cols, eps));
+}
+
 napi_value Module(napi_env env, napi_value exports) {
   struct Fn {
     const char* name;
@@ -596,6 +610,7 @@ napi_value Module(napi_env env, napi_value exports) {
       {"headNorm", HeadNorm}, {"normMod", NormModT<false>}, {"normModRotateF16", NormModT<true>},
       {"glu", GluT<false>}, {"gluRotateF16", GluT<true>}, {"elementwise", Elementwise},
       {"accumulate", Accumulate}, {"addRows", AddRows}, {"rowSum", RowSum}, {"rmsnorm", Rmsnorm},
+      {"addRmsnorm", AddRmsnorm},
   };
   for (const Fn& f : fns) {
     napi_value fn;

@@ -891,6 +891,166 @@ __global__ __launch_bounds__(1024) void attn_rows_kernel(RowsArgs a) {
     if (d0 + e < a.D) orow[d0 + e] = ov[e] * inv;
 }
 
+// The same attention on the matrix cores, for head dims D = 16 * DB with 16-byte aligned q, k
+// and o views. A block of NW waves takes 16 queries of one head; wave w takes key blocks
+// w, w + NW, ... (16 keys each), and the NW partial softmax states are merged through LDS at the
+// end (flash-decoding style). The path is latency-bound at these sizes (a few hundred queries):
+// splitting the keys over waves shortens each wave's chain of dependent loads, and each key
+// block's K and V loads are issued together.
+// Per key block the wave forms S^T = K Q^T (v_mfma_f32_16x16x16_f16, D/16 steps), whose
+// accumulator layout is the B operand of O^T += V^T P^T, so probabilities never leave registers.
+// Lane l holds query q0 + (l % 16): its scores for keys 4(l/16)..4(l/16)+3 of the block, and in
+// product t (t < DB) the O^T rows r = 4(l/16) + j standing for d = DB r + t, which makes the
+// online-softmax rescale a per-lane scalar, gives every lane DB consecutive d of a V row
+// (vector loads) and makes its outputs one run of 4 DB consecutive d. Scores are in the log2
+// domain (Q pre-scaled by log2(e)/sqrt(D)); fp16 operands, fp32 accumulation.
+constexpr int kRowsWaves = 8;  // waves per block of attn_rows_mfma_kernel (LDS: 8 * D * 64 B)
+
+template <int DB, int NW>
+__global__ __launch_bounds__(64 * NW) void attn_rows_mfma_kernel(RowsArgs a) {
+  constexpr int D = 16 * DB;
+  __shared__ float4 o_part[NW][DB][64];
+  __shared__ float m_part[NW][16], l_part[NW][16];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int h = blockIdx.y;
+  // heaviest causal tiles first
+  const int q0 = (gridDim.x - 1 - blockIdx.x) * 16;
+  const int col = lane & 15, grp = lane >> 4;
+  const int g = h / a.group;
+  const int qi = q0 + col;
+  const bool qvalid = qi < a.Lq;
+
+  // Q^T fragments (the B operand of every S^T product), shared by the block's waves through
+  // LDS; wave w converts fragments t = w, w + NW, ... Rows past the end are read from the last
+  // row (loads stay unconditional, so they issue back to back); their scores are masked and
+  // their probabilities are zero.
+  __shared__ half4_t q_lds[DB][64];
+  {
+    const float* qr = a.q + a.qOff + (long long)(qvalid ? qi : a.Lq - 1) * a.ldq + (long long)h * D + 4 * grp;
+    for (int t = wave; t < DB; t += NW) {
+      const float4 x = *reinterpret_cast<const float4*>(qr + 16 * t);
+      q_lds[t][lane] = half4_t{(half_t)(x.x * a.scale), (half_t)(x.y * a.scale), (half_t)(x.z * a.scale),
+                               (half_t)(x.w * a.scale)};
+    }
+  }
+  __syncthreads();
+  const float* kb0 = a.k + a.kOff + (long long)g * D;
+  const float* vb0 = a.v + a.vOff + (long long)g * D;
+
+  float4_t o[DB];
+#pragma unroll
+  for (int t = 0; t < DB; ++t) o[t] = float4_t{0.f, 0.f, 0.f, 0.f};
+  float m = -INFINITY, lsum = 0.f;
+
+  const int qlast = (q0 + 15 < a.Lq ? q0 + 15 : a.Lq - 1);
+  int nkb = (a.Lk + 15) / 16;
+  if (a.causal && qlast / 16 + 1 < nkb) nkb = qlast / 16 + 1;
+  for (int kb = wave; kb < nkb; kb += NW) {
+    // keeps the Q^T fragments in LDS instead of 2 * DB registers hoisted out of the loop
+    asm volatile("" ::: "memory");
+    // K rows (key kb*16 + col) for S^T's A operand, and V^T (d = 16t + col, keys key0..key0+3)
+    // for the PV product's A operand: all loads of the block issued before any use
+    const int kr = kb * 16 + col;
+    const int key0 = kb * 16 + 4 * grp;
+    const float* krow = kb0 + (long long)(kr < a.Lk ? kr : a.Lk - 1) * a.ldk + 4 * grp;
+    float4 kx[DB];
+#pragma unroll
+    for (int t = 0; t < DB; ++t) kx[t] = *reinterpret_cast<const float4*>(krow + 16 * t);
+    // V^T's A operand in product t: row col = d DB col + t, keys key0 + j
+    float vx[DB][4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float* vr = vb0 + DB * col + (long long)(key0 + j < a.Lk ? key0 + j : a.Lk - 1) * a.ldv;
+      if constexpr (DB % 4 == 0) {
+#pragma unroll
+        for (int t4 = 0; t4 < DB; t4 += 4) {
+          const float4 x = *reinterpret_cast<const float4*>(vr + t4);
+          vx[t4][j] = x.x;
+          vx[t4 + 1][j] = x.y;
+          vx[t4 + 2][j] = x.z;
+          vx[t4 + 3][j] = x.w;
+        }
+      } else {
+#pragma unroll
+        for (int t = 0; t < DB; ++t) vx[t][j] = vr[t];
+      }
+    }
+    // keep every load of the block in flight before the first use (left alone, the scheduler
+    // converts each group of V values as it arrives and waits on each group in turn)
+    __builtin_amdgcn_sched_barrier(0);
+    float4_t s = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < DB; ++t) {
+      const half4_t kf = half4_t{(half_t)kx[t].x, (half_t)kx[t].y, (half_t)kx[t].z, (half_t)kx[t].w};
+      s = __builtin_amdgcn_mfma_f32_16x16x16f16(kf, q_lds[t][lane], s, 0, 0, 0);
+    }
+    // s[j]: key kb*16 + 4 grp + j of query qi
+    float bm = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int key = key0 + j;
+      if (key >= a.Lk || (a.causal && key > qi)) s[j] = -INFINITY;
+      bm = fmaxf(bm, s[j]);
+    }
+    bm = fmaxf(bm, __shfl_xor(bm, 16));
+    bm = fmaxf(bm, __shfl_xor(bm, 32));
+    // a block of a later wave may have no visible key for this query yet: keep the state
+    // unchanged then (bm = -inf), instead of exp2(-inf - -inf)
+    const float mn = fmaxf(m, bm);
+    const float corr = mn == -INFINITY ? 1.f : exp2f(m - mn);
+    float p[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) p[j] = mn == -INFINITY ? 0.f : exp2f(s[j] - mn);
+    lsum = lsum * corr + ((p[0] + p[1]) + (p[2] + p[3]));
+    m = mn;
+    const half4_t pf = half4_t{(half_t)p[0], (half_t)p[1], (half_t)p[2], (half_t)p[3]};
+    // O^T += V^T P^T
+#pragma unroll
+    for (int t = 0; t < DB; ++t) {
+      const half4_t vf = half4_t{(half_t)vx[t][0], (half_t)vx[t][1], (half_t)vx[t][2], (half_t)vx[t][3]};
+      o[t] *= corr;
+      o[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(vf, pf, o[t], 0, 0, 0);
+    }
+  }
+  lsum += __shfl_xor(lsum, 16);
+  lsum += __shfl_xor(lsum, 32);
+
+  // merge the waves' states: O = sum_w 2^(m_w - M) O_w, L = sum_w 2^(m_w - M) l_w
+#pragma unroll
+  for (int t = 0; t < DB; ++t) o_part[wave][t][lane] = make_float4(o[t][0], o[t][1], o[t][2], o[t][3]);
+  if (grp == 0) {
+    m_part[wave][col] = m;
+    l_part[wave][col] = lsum;
+  }
+  __syncthreads();
+  if (!qvalid) return;
+  float M = m_part[0][col];
+#pragma unroll
+  for (int w = 1; w < NW; ++w) M = fmaxf(M, m_part[w][col]);  // finite: wave 0 sees key 0
+  float sc[NW], L = 0.f;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    sc[w] = exp2f(m_part[w][col] - M);
+    L += sc[w] * l_part[w][col];
+  }
+  const float inv = 1.0f / L;
+  // the lane's outputs are d = 4 DB grp + f, f = DB j + t < 4 DB; wave w writes f in
+  // [w FW, (w + 1) FW)
+  constexpr int F = 4 * DB, FW = (F + NW - 1) / NW;
+  float* orow = a.o + (long long)qi * a.ldo + (long long)h * D + F * grp;
+#pragma unroll
+  for (int u = 0; u < FW; ++u) {
+    const int f = wave * FW + u;
+    if (f < F) {
+      const int j = f / DB, t = f % DB;
+      float r = 0.f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) r += sc[w] * reinterpret_cast<const float*>(&o_part[w][t][lane])[j];
+      orow[f] = r * inv;
+    }
+  }
+}
+
 }  // namespace
 
 extern "C" int ns2_attention_rows(const float* q, const float* k, const float* v, float* o, int Lq, int Lk,
@@ -901,15 +1061,35 @@ extern "C" int ns2_attention_rows(const float* q, const float* k, const float* v
   NS2_REQUIRE(q && k && v && o, "ns2_attention_rows: null q, k, v or o");
   NS2_REQUIRE(D > 0 && D <= 256, "ns2_attention_rows: unsupported head dim %d", D);
   NS2_REQUIRE(group > 0 && H % group == 0, "ns2_attention_rows: H=%d is not a multiple of group=%d", H, group);
-  NS2_REQUIRE(Lk > 0 && ldq >= D && ldk >= D && ldv >= D && ldo >= H * D && qOff >= 0 && kOff >= 0 && vOff >= 0,
+  NS2_REQUIRE(Lk > 0 && ldq >= H * D && ldk >= H / group * D && ldv >= H / group * D && ldo >= H * D && qOff >= 0 &&
+                  kOff >= 0 && vOff >= 0,
               "ns2_attention_rows: bad sizes or strides");
   // the waves of a block: the heads of one K/V group (at most 16)
   const int hpb = group < 16 ? group : 16;
   RowsArgs a{q, k, v, o, qOff, kOff, vOff, Lq, Lk, H, D, ldq, ldk, ldv, ldo, group, causal ? 1 : 0, hpb,
              1.0f / sqrtf((float)D)};
-  const dim3 grid(Lq, (H + hpb - 1) / hpb), block(64 * hpb);
   ns2::ProfScope prof_("attn_rows");
   hipStream_t s = ns2::stream();
+  // matrix-core path: D a multiple of 16 and every row read or written 16-byte aligned
+  auto al4 = [](long long x) { return x % 4 == 0; };
+  const bool al = aligned16(q) && aligned16(k) && aligned16(v) && al4(ldq) && al4(ldk) && al4(ldv) &&
+                  al4(qOff) && al4(kOff) && al4(vOff) && D % 16 == 0;
+  if (al) {
+    a.scale *= kLog2e;
+    const dim3 mgrid((Lq + 15) / 16, H);
+    switch (D / 16) {
+#define NS2_ROWS_CASE(N) \
+  case N: attn_rows_mfma_kernel<N, kRowsWaves><<<mgrid, 64 * kRowsWaves, 0, s>>>(a); break;
+      NS2_ROWS_CASE(1) NS2_ROWS_CASE(2) NS2_ROWS_CASE(3) NS2_ROWS_CASE(4) NS2_ROWS_CASE(5) NS2_ROWS_CASE(6)
+      NS2_ROWS_CASE(7) NS2_ROWS_CASE(8) NS2_ROWS_CASE(9) NS2_ROWS_CASE(10) NS2_ROWS_CASE(11)
+      NS2_ROWS_CASE(12) NS2_ROWS_CASE(13) NS2_ROWS_CASE(14) NS2_ROWS_CASE(15) NS2_ROWS_CASE(16)
+#undef NS2_ROWS_CASE
+      default: break;
+    }
+    NS2_LAUNCHED("attn_rows_mfma");
+    return NS2_OK;
+  }
+  const dim3 grid(Lq, (H + hpb - 1) / hpb), block(64 * hpb);
   const int dv = (D + 63) / 64;
   if (dv == 1) attn_rows_kernel<1><<<grid, block, 0, s>>>(a);
   else if (dv == 2) attn_rows_kernel<2><<<grid, block, 0, s>>>(a);

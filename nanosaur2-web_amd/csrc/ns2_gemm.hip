@@ -28,6 +28,10 @@ struct GemmArgs {
   int M, N, K;
   float alpha;
   int act, resid;
+  // split-K: block z sums k tiles [z * ksteps, (z + 1) * ksteps) into part[z] ([M, N], no
+  // epilogue); splitk_reduce_kernel adds the splits in z order and applies the epilogue
+  float* part;
+  int ksteps;
 };
 
 constexpr int BK = 64;        // k per LDS tile
@@ -184,9 +188,13 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_kernel(G
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  const int nk = (p.K + BK - 1) / BK;
-  la.load(p, m0, 0, tid);
-  lw.load(p, n0, 0, tid);
+  int kt0 = 0, nk = (p.K + BK - 1) / BK;
+  if (p.part) {
+    kt0 = blockIdx.z * p.ksteps;
+    nk = nk - kt0 < p.ksteps ? nk - kt0 : p.ksteps;
+  }
+  la.load(p, m0, kt0 * BK, tid);
+  lw.load(p, n0, kt0 * BK, tid);
   la.store(lds_a[0], tid);
   lw.store(lds_b[0], tid);
   __syncthreads();
@@ -195,8 +203,8 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_kernel(G
   for (int kt = 0; kt < nk; ++kt) {
     const int cur = kt & 1;
     if (kt + 1 < nk) {
-      la.load(p, m0, (kt + 1) * BK, tid);
-      lw.load(p, n0, (kt + 1) * BK, tid);
+      la.load(p, m0, (kt0 + kt + 1) * BK, tid);
+      lw.load(p, n0, (kt0 + kt + 1) * BK, tid);
     }
     const half_t* A = lds_a[cur] + (wm * WM + lrow) * LROW + lk;
     const half_t* B = lds_b[cur] + (wn * WN + lrow) * LROW + lk;
@@ -220,6 +228,24 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_kernel(G
     __syncthreads();
   }
 
+  // (the launcher splits K only on grids of 64x64 tiles)
+  if constexpr (BM * BN <= 64 * 64) if (p.part) {
+    float* part = p.part + (long long)blockIdx.z * p.M * p.N;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int n = n0 + wn * WN + j * 32 + lrow;
+      if (n >= p.N) continue;
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int m = m0 + wm * WM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+          if (m < p.M) part[(long long)m * p.N + n] = acc[i][j][r];
+        }
+    }
+    return;
+  }
+
   // epilogue
 #pragma unroll
   for (int j = 0; j < TN; ++j) {
@@ -237,6 +263,18 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_kernel(G
       }
     }
   }
+}
+
+// Split-K reduction: the splits summed in z order (deterministic), then the GEMM epilogue.
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs p, int splits) {
+  const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+  const long long mn = (long long)p.M * p.N;
+  if (i >= mn) return;
+  float acc = 0.f;
+  for (int z = 0; z < splits; ++z) acc += p.part[z * mn + i];
+  const int m = (int)(i / p.N), n = (int)(i % p.N);
+  epilogue_store(p, m, n, acc, p.scale ? p.scale[n] : 1.0f, p.bias ? p.bias[n] : 0.0f,
+                 p.gate ? p.gate[p.gOff + n] : 1.0f);
 }
 
 // Small-M path: one wave per output column n, all M (<= 8) rows, fp32 FMA.
@@ -312,17 +350,41 @@ __global__ __launch_bounds__(256) void cast_f16_kernel(const float* __restrict__
 }
 
 constexpr int kGemvMaxM = 8;
-
+constexpr long long kSmallGridBlocks = 256;  // one block per CU
+constexpr int kMaxSplits = 16;
 template <bool A_F32, bool W_BF16>
 int launch_gemm(const GemmArgs& p, const char* name) {
   hipStream_t s = ns2::stream();
   ns2::ProfScope prof_(p.M <= kGemvMaxM ? (W_BF16 ? "gemv_bf16" : "gemv_i8") : (W_BF16 ? "gemm_bf16" : "gemm_i8"));
+  const long long big_tiles = (long long)((p.N + 127) / 128) * ((p.M + 127) / 128);
   if (p.M <= kGemvMaxM) {
     gemv_kernel<W_BF16><<<(p.N + 3) / 4, 256, 0, s>>>(p);
-  } else {
+  } else if (big_tiles >= kSmallGridBlocks) {
     constexpr int BM = 128, BN = 128, WM = 64, WN = 64;
     dim3 grid((p.N + BN - 1) / BN, (p.M + BM - 1) / BM);
     gemm_mfma_kernel<BM, BN, WM, WN, A_F32, W_BF16><<<grid, (BM / WM) * (BN / WN) * 64, 0, s>>>(p);
+  } else {
+    // Too few 128x128 tiles to fill 256 CUs (a short sequence): 64x64 tiles, and when even
+    // those leave the chip idle, split K over blockIdx.z (at least 4 k tiles per split).
+    constexpr int BM = 64, BN = 64, WM = 32, WN = 32;
+    const long long tiles = (long long)((p.N + BN - 1) / BN) * ((p.M + BM - 1) / BM);
+    const int nk = (p.K + BK - 1) / BK;
+    int splits = (int)(2 * kSmallGridBlocks / tiles);
+    if (splits > nk / 4) splits = nk / 4;
+    if (splits > kMaxSplits) splits = kMaxSplits;
+    GemmArgs q = p;
+    if (splits > 1) {
+      q.ksteps = (nk + splits - 1) / splits;
+      splits = (nk + q.ksteps - 1) / q.ksteps;
+      q.part = static_cast<float*>(ns2::workspace(5, (size_t)splits * p.M * p.N * sizeof(float)));
+      if (!q.part) return ns2::set_error(NS2_ERR_OOM, "%s: split-K workspace allocation failed", name);
+    }
+    dim3 grid((p.N + BN - 1) / BN, (p.M + BM - 1) / BM, splits > 1 ? splits : 1);
+    gemm_mfma_kernel<BM, BN, WM, WN, A_F32, W_BF16><<<grid, (BM / WM) * (BN / WN) * 64, 0, s>>>(q);
+    if (splits > 1) {
+      const long long mn = (long long)p.M * p.N;
+      splitk_reduce_kernel<<<(unsigned)((mn + 255) / 256), 256, 0, s>>>(q, splits);
+    }
   }
   NS2_LAUNCHED(name);
   return NS2_OK;

@@ -299,6 +299,29 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
   for (int c = threadIdx.x; c < cols; c += 256) y[base + c] = x[base + c] * r * w[c];
 }
 
+// x += rmsnorm(a) * w_add, then y = rmsnorm(x) * w_out (when y is given): the sandwich norms
+// around each Gemma3 sublayer (app/models/gemma3.js:76-77, 87-88 and the next layer's input norm).
+__global__ __launch_bounds__(256) void add_rmsnorm_kernel(float* __restrict__ x,
+                                                          const float* __restrict__ a,
+                                                          const float* __restrict__ w_add,
+                                                          const float* __restrict__ w_out,
+                                                          float* __restrict__ y, int cols, float eps) {
+  __shared__ float red[16];
+  const long long base = (long long)blockIdx.x * cols;
+  float ss = 0.f;
+  for (int c = threadIdx.x; c < cols; c += 256) ss += a[base + c] * a[base + c];
+  const float r = rsqrtf(block_sum(ss, red) / (float)cols + eps);
+  float sx = 0.f;
+  for (int c = threadIdx.x; c < cols; c += 256) {
+    const float v = x[base + c] + a[base + c] * r * w_add[c];
+    x[base + c] = v;
+    sx += v * v;
+  }
+  if (!y) return;
+  const float rx = rsqrtf(block_sum(sx, red) / (float)cols + eps);
+  for (int c = threadIdx.x; c < cols; c += 256) y[base + c] = x[base + c] * rx * w_out[c];
+}
+
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 inline bool aligned8(const void* p) { return ((uintptr_t)p & 7) == 0; }
 
@@ -448,6 +471,18 @@ int ns2_rmsnorm(const float* x, const float* w, float* y, int rows, int cols, fl
   ns2::ProfScope prof_("rmsnorm");
   rmsnorm_kernel<<<rows, 256, 0, ns2::stream()>>>(x, w, y, cols, eps);
   NS2_LAUNCHED("rmsnorm");
+  return NS2_OK;
+}
+
+int ns2_add_rmsnorm(float* x, const float* a, const float* w_add, const float* w_out, float* y, int rows,
+                    int cols, float eps) {
+  NS2_READY();
+  if (rows <= 0) return NS2_OK;
+  NS2_REQUIRE(x && a && w_add && cols > 0 && (!y || w_out), "ns2_add_rmsnorm: bad arguments");
+  NS2_REQUIRE(y != x && y != a && a != x, "ns2_add_rmsnorm: x, a and y must not alias");
+  ns2::ProfScope prof_("add_rmsnorm");
+  add_rmsnorm_kernel<<<rows, 256, 0, ns2::stream()>>>(x, a, w_add, w_out, y, cols, eps);
+  NS2_LAUNCHED("add_rmsnorm");
   return NS2_OK;
 }
 

@@ -63,6 +63,7 @@ export class Gemma3 {
   }
 
   // The layer stack on a device tensor x [L, 640] (released here); returns the normed output.
+  // Each sublayer's post-norm, residual add and the norm after it run as one addRmsnorm.
   encodeEmbedded(x) {
     const gpu = this.gpu;
     const { hidden: D, heads: H, kvHeads: KH, headDim: HD } = GEMMA;
@@ -70,9 +71,9 @@ export class Gemma3 {
     const qkvW = (H + 2 * KH) * HD;
     const csLocal = ropeTable(gpu, Lt, HD, 1e4);
     const csGlobal = ropeTable(gpu, Lt, HD, 1e6);
-    for (const l of this.layers) {
+    let h = ops.rmsnorm(gpu, x, this.layers[0].inNorm, D);
+    this.layers.forEach((l, i) => {
       const cs = l.global ? csGlobal : csLocal;
-      const h = ops.rmsnorm(gpu, x, l.inNorm, D);
       const qkv = ops.linear(gpu, h, l.qkv, { name: "te.qkv" }); // [Lt, q 1024 | k 256 | v 256]
       h.release();
       ops.headNorm(gpu, qkv, l.qn, { L: Lt, H, D: HD, ld: qkvW, colOff: 0, cs });
@@ -84,27 +85,22 @@ export class Gemma3 {
       qkv.release();
       const o = ops.linear(gpu, a, l.o, { name: "te.o" });
       a.release();
-      const on = ops.rmsnorm(gpu, o, l.postAttnNorm, D);
+      const h2 = ops.addRmsnorm(gpu, x, o, l.postAttnNorm, l.preMlpNorm, D);
       o.release();
-      ops.accumulate(gpu, x, on);
-      on.release();
-      const h2 = ops.rmsnorm(gpu, x, l.preMlpNorm, D);
       const gu = ops.linear(gpu, h2, l.gateUp, { name: "te.mlp" });
       h2.release();
       const g = ops.glu(gpu, gu, "gelu_tanh");
       gu.release();
       const d = ops.linear(gpu, g, l.down, { name: "te.mlp" });
       g.release();
-      const dn = ops.rmsnorm(gpu, d, l.postMlpNorm, D);
+      const next = i + 1 < this.layers.length ? this.layers[i + 1].inNorm : this.norm;
+      h = ops.addRmsnorm(gpu, x, d, l.postMlpNorm, next, D);
       d.release();
-      ops.accumulate(gpu, x, dn);
-      dn.release();
-    }
+    });
     csLocal.release();
     csGlobal.release();
-    const out = ops.rmsnorm(gpu, x, this.norm, D);
     x.release();
-    return out;
+    return h; // the final norm of the last layer's output
   }
 
   unload() {

@@ -125,6 +125,16 @@ export function rmsnorm(gpu, x, weight, cols, eps = 1e-6, out) {
   return y;
 }
 
+// x += rmsnorm(a) * wAdd; returns rmsnorm(x) * wOut (or null without wOut): a sandwich norm,
+// its residual add and the following norm in one launch (app/models/gemma3.js:76-80, 87-88;
+// addition to the reference ops).
+export function addRmsnorm(gpu, x, a, wAdd, wOut, cols, eps = 1e-6) {
+  const rows = x.size / cols;
+  const y = wOut ? gpu.empty(x.shape) : null;
+  gpu.run("add_rmsnorm", 0, () => native.addRmsnorm(addr(x), addr(a), addr(wAdd), addr(wOut), addr(y), rows, cols, eps));
+  return y;
+}
+
 // norm(x) * (1 + mod[scaleOff..]) + mod[shiftOff..]; RMSNorm*weight, or LayerNorm without
 // affine when weight is null (app/gpu/ops.js:119-129).
 export function normMod(gpu, x, mod, shiftOff, scaleOff, cols, weight = null, eps = 1e-6) {

@@ -71,6 +71,7 @@ SIGNATURES = {
     "ns2_add_rows": [c_vp, c_vp, c_vp, c_int, c_int],
     "ns2_row_sum": [c_vp, c_vp, c_vp, c_int, c_int, c_float],
     "ns2_rmsnorm": [c_vp, c_vp, c_vp, c_int, c_int, c_float],
+    "ns2_add_rmsnorm": [c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_float],
 }
 _RESTYPES = {"ns2_last_error": ctypes.c_char_p, "ns2_get_stream": c_vp, "ns2_pool_round": c_size}
 
@@ -235,6 +236,9 @@ class Lib:
 
     def rmsnorm(self, x, w, y, rows, cols, eps=1e-6):
         self.call("ns2_rmsnorm", _ptr(x), _ptr(w), _ptr(y), rows, cols, eps)
+
+    def add_rmsnorm(self, x, a, w_add, w_out, y, rows, cols, eps=1e-6):
+        self.call("ns2_add_rmsnorm", _ptr(x), _ptr(a), _ptr(w_add), _ptr(w_out), _ptr(y), rows, cols, eps)
 
 
 _LIB = None

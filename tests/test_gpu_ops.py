@@ -343,7 +343,8 @@ def test_linear_i8_tiled_errors(ns2lib):
 # ----------------------------------------------------------------------------- bf16 linear
 
 @pytest.mark.parametrize("M,N,K", [(3952, 1536, 64), (3952, 1536, 1536), (3952, 64, 1536),
-                                   (256, 1536, 640), (1, 9216, 1536), (1, 1536, 256), (3, 3072, 1536)])
+                                   (256, 1536, 640), (256, 640, 2048), (256, 4096, 640), (37, 200, 1024),
+                                   (1, 9216, 1536), (1, 1536, 256), (3, 3072, 1536)])
 def test_linear_bf16(ns2lib, M, N, K):
     g = gen(M + N + K)
     x = torch.randn(M, K, generator=g)
@@ -354,6 +355,34 @@ def test_linear_bf16(ns2lib, M, N, K):
     ns2lib.linear_bf16(x.to(dev), K, w.view(torch.int16).to(dev), out, M, N, K, bias=bias.to(dev))
     torch.cuda.synchronize()
     assert_close(out.cpu(), ref, TOL, f"linear_bf16 {M}x{N}x{K}")
+
+
+@pytest.mark.parametrize("M,N,K", [(256, 640, 2048), (40, 96, 512)])
+def test_linear_bf16_split_k_epilogue(ns2lib, M, N, K):
+    """Short sequences take 64x64 tiles with K split over blocks and a reduce kernel that applies
+    the epilogue once: alpha, bias, an added tensor and GELU(tanh), then a gated += into a column
+    window of a wider output."""
+    g = gen(M * 5 + N)
+    x = torch.randn(M, K, generator=g)
+    w = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
+    bias = torch.randn(N, generator=g) * 0.1
+    add = torch.randn(M, N, generator=g) * 0.1
+    out = torch.empty(M, N, device=dev)
+    ns2lib.linear_bf16(x.to(dev), K, w.view(torch.int16).to(dev), out, M, N, K, bias=bias.to(dev),
+                       add=add.to(dev), alpha=0.5, act="gelu_tanh")
+    torch.cuda.synchronize()
+    ref = O.linear_bf16(x.double(), w, alpha=0.5, bias=bias.double(), add=add.double(), act="gelu_tanh")
+    assert_close(out.cpu(), ref, TOL, f"split-K epilogue {M}x{N}x{K}")
+    ldc, cOff = N + 32, 16
+    base = torch.randn(M * ldc, generator=g)
+    gate = torch.randn(N + 8, generator=g)
+    outd = base.to(dev)
+    ns2lib.linear_bf16(x.to(dev), K, w.view(torch.int16).to(dev), outd, M, N, K, ldc=ldc, cOff=cOff,
+                       resid=True, gate=gate.to(dev), gOff=8)
+    torch.cuda.synchronize()
+    ref = O.linear_bf16(x.double(), w, out=base.double().clone(), resid=True, gate=gate.double(), gOff=8,
+                        ldc=ldc, cOff=cOff)
+    assert_close(outd.cpu(), ref, TOL, f"split-K gated += {M}x{N}x{K}")
 
 
 def test_linear_bf16_gemv_silu_resid(ns2lib):
@@ -586,6 +615,25 @@ def test_elementwise_accumulate_rowsum_rmsnorm(ns2lib):
     assert_close(out.cpu(), O.rms_norm(x.double(), nw.double()), TOL_F32, "rmsnorm")
 
 
+@pytest.mark.parametrize("with_out", [True, False])
+def test_add_rmsnorm(ns2lib, with_out):
+    """The Gemma3 sandwich norm: x += rmsnorm(a) * w_add, then y = rmsnorm(x) * w_out
+    (app/models/gemma3.js:76-80: ops.rmsnorm, ops.accumulate, ops.rmsnorm), at L = 37 x 640."""
+    g = gen(640 + with_out)
+    x = torch.randn(37, 640, generator=g) * 20
+    a = torch.randn(37, 640, generator=g) * 3
+    wa = torch.randn(640, generator=g) * 0.3 + 1
+    wo = torch.randn(640, generator=g) * 0.3 + 1
+    xd = x.to(dev)
+    y = torch.empty(37, 640, device=dev) if with_out else None
+    ns2lib.add_rmsnorm(xd, a.to(dev), wa.to(dev), wo.to(dev) if with_out else None, y, 37, 640)
+    torch.cuda.synchronize()
+    xr = x.double() + O.rms_norm(a.double(), wa.double())
+    assert_close(xd.cpu(), xr, TOL_F32, "add_rmsnorm x")
+    if with_out:
+        assert_close(y.cpu(), O.rms_norm(xr, wo.double()), TOL_F32, "add_rmsnorm y")
+
+
 def test_fill_and_errors(ns2lib):
     import ns2
 
@@ -611,7 +659,9 @@ def test_fill_and_errors(ns2lib):
 ])
 def test_attention_rows(ns2lib, D, H, group, causal, Lq, Lk):
     """ns2_attention_rows (ops.attention's materialized path, app/gpu/ops.js:211-241) against the
-    oracle's softmax(q k^T / sqrt(D)) v with grouped K/V heads and the causal mask."""
+    oracle's softmax(q k^T / sqrt(D)) v with grouped K/V heads and the causal mask. Head dims that
+    are multiples of 16 run the matrix-core kernel (fp16 operands, tolerance 2e-3), the others
+    the fp32 kernel (1e-4)."""
     g = gen(D * 7 + H + Lq)
     KH = H // group
     q = torch.randn(Lq, H * D, generator=g)
@@ -622,20 +672,41 @@ def test_attention_rows(ns2lib, D, H, group, causal, Lq, Lk):
                           ldk=KH * D, ldv=KH * D, ldo=H * D, group=group, causal=causal)
     torch.cuda.synchronize()
     ref = O.attention_rows(q.double(), k.double(), v.double(), H, D, group=group, causal=causal)
-    assert_close(o.cpu(), ref, TOL_ROWS, f"attention_rows D={D} H={H} group={group} causal={causal}")
+    tol = TOL if D % 16 == 0 else TOL_ROWS
+    assert_close(o.cpu(), ref, tol, f"attention_rows D={D} H={H} group={group} causal={causal}")
 
 
-def test_attention_rows_packed_qkv_view(ns2lib):
-    """q, k and v as column windows of one [L, 1536] buffer (the Gemma3 layer's fused qkv)."""
+@pytest.mark.parametrize("pad", [0, 1])
+def test_attention_rows_packed_qkv_view(ns2lib, pad):
+    """q, k and v as column windows of one [L, 1536] buffer (the Gemma3 layer's fused qkv).
+    pad=1 shifts the windows by one float and makes the stride odd: the views are not 16-byte
+    aligned and the fp32 kernel runs instead of the matrix-core one."""
     L, H, D = 29, 4, 256
-    W = (H + 2) * D
+    W = (H + 2) * D + pad
     g = gen(77)
     qkv = torch.randn(L, W, generator=g)
     o = torch.empty(L, H * D, device=dev)
     d = qkv.to(dev)
     ns2lib.attention_rows(d, d, d, o, Lq=L, Lk=L, H=H, D=D, ldq=W, ldk=W, ldv=W, ldo=H * D,
-                          qOff=0, kOff=H * D, vOff=(H + 1) * D, group=H, causal=True)
+                          qOff=pad, kOff=H * D + pad, vOff=(H + 1) * D + pad, group=H, causal=True)
     torch.cuda.synchronize()
-    x = qkv.double()
+    x = qkv.double()[:, pad:]
     ref = O.attention_rows(x[:, :H * D], x[:, H * D:(H + 1) * D], x[:, (H + 1) * D:], H, D, group=H, causal=True)
-    assert_close(o.cpu(), ref, TOL_ROWS, "attention_rows packed qkv")
+    assert_close(o.cpu(), ref, TOL_ROWS if pad else TOL, f"attention_rows packed qkv (pad {pad})")
+
+
+@pytest.mark.parametrize("Lq,Lk,causal", [(100, 37, True), (5, 300, False), (300, 300, True)])
+def test_attention_rows_ragged_tiles(ns2lib, Lq, Lk, causal):
+    """Query and key counts that are not multiples of the 16-row tiles, Lq != Lk under the causal
+    mask, more keys than queries, and a full causal square of 300."""
+    H, D, group = 8, 128, 2
+    g = gen(Lq * 3 + Lk)
+    q = torch.randn(Lq, H * D, generator=g)
+    k = torch.randn(Lk, H // group * D, generator=g)
+    v = torch.randn(Lk, H // group * D, generator=g)
+    o = torch.empty(Lq, H * D, device=dev)
+    ns2lib.attention_rows(q.to(dev), k.to(dev), v.to(dev), o, Lq=Lq, Lk=Lk, H=H, D=D, ldq=H * D,
+                          ldk=H // group * D, ldv=H // group * D, ldo=H * D, group=group, causal=causal)
+    torch.cuda.synchronize()
+    ref = O.attention_rows(q.double(), k.double(), v.double(), H, D, group=group, causal=causal)
+    assert_close(o.cpu(), ref, TOL, f"attention_rows ragged Lq={Lq} Lk={Lk} causal={causal}")
