@@ -18,7 +18,10 @@
    the library's kernel profiler times each launch of the flash kernel with stream events,
    which gives `roofline_attention` (algorithmic 4*Lq*Lk*D*H*B flops per launch / mean launch
    time).
-3. CPU baseline: the oracle (a PyTorch-CPU restatement of tools/reference.py) on a bounded
+3. Gemma3-270M text encoder (17 of 18 layers + final norm, 256 token ids, random-init bf16
+   weights of the real architecture) through the Node host (run_gemma.js): median device time
+   per encode, with the algorithmic flops of its linears (2*M*N*K) and attention (4*L*L*256*4).
+4. CPU baseline: the oracle (a PyTorch-CPU restatement of tools/reference.py) on a bounded
    sample -- one joint block and one image-only block at the full 3952-token shape -- scaled
    to 18 blocks, on this host's cores.
 """
@@ -36,6 +39,8 @@ import time
 ROOT = os.path.dirname(os.path.abspath(__file__))
 PKG = os.path.join(ROOT, "nanosaur2-web_amd")
 RUN_DIT = os.path.join(PKG, "js", "run_dit.js")
+RUN_GEMMA = os.path.join(PKG, "js", "run_gemma.js")
+GEMMA_TOKENS, GEMMA_LAYERS = 256, 17
 METRIC = "ms per 832x1216 DiT pass (int8) + joint-attention TFLOP/s, 1 MI355X"
 PUBLISHED_PASS_MS = 1730.0   # README.md:86-88 of the reference (WebGPU, laptop GPU)
 FP16_PEAK_TFLOPS = 2516.6    # MI355X dense fp16 MFMA
@@ -89,6 +94,31 @@ def run_dit_profile():
         sys.stderr.write(p.stderr[-3000:])
         raise SystemExit(f"run_dit.js --profile failed with {p.returncode}")
     return json.loads(p.stdout.strip().splitlines()[-1]).get("profile", [])
+
+
+def gemma_flops(L=GEMMA_TOKENS):
+    """Algorithmic FLOPs of the 17-layer Gemma3-270M stack (app/models/gemma3.js:62-92):
+    per layer q/k/v (1536 x 640), o (640 x 1024), gate/up (4096 x 640), down (640 x 2048), and
+    4*L*L*256*4 for the attention (the causal mask not subtracted)."""
+    per_layer = 2 * L * 640 * (1536 + 1024 + 4096 + 2048) + 4 * L * L * 256 * 4
+    return GEMMA_LAYERS * per_layer
+
+
+def run_gemma(steps, warmup):
+    cmd = ["node", RUN_GEMMA, "--synthetic", "3", "--tokens", f"{GEMMA_TOKENS},1",
+           "--warmup", str(warmup), "--reps", str(steps)]
+    log(" ".join(cmd))
+    p = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
+    if p.returncode != 0:
+        sys.stderr.write(p.stderr[-3000:])
+        raise SystemExit(f"run_gemma.js failed with {p.returncode}")
+    r = json.loads(p.stdout.strip().splitlines()[-1])
+    ms = r["ms_device_median"]
+    fl = gemma_flops()
+    return {"workload": f"Gemma3-270M text encoder, {GEMMA_LAYERS} layers + final norm, {GEMMA_TOKENS} tokens, "
+                        "bf16 weights (fp16 matrix-core products, fp32 accumulation)",
+            "ms": ms, "ms_wall": r["ms_wall_median"], "gflop": fl / 1e9,
+            "tflops": fl / (ms / 1e3) / 1e12, "ms_device": r["ms_device"]}
 
 
 # int8 ConvRot linears of the pass (tiled GEMM launches), by the op names the DiT driver uses
@@ -289,6 +319,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-dit", action="store_true", help="only the joint-attention measurement")
+    ap.add_argument("--no-gemma", action="store_true", help="skip the text-encoder measurement")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a 256 MiB -> 256 MiB copy kernel (reference point for HBM counters)")
     args = ap.parse_args()
@@ -305,6 +336,10 @@ def main():
         kernels = run_dit_profile()
         gemm = gemm_roofline(kernels)
         log(f"int8 GEMMs: {gemm['ms_per_pass']:.3f} ms/pass, {gemm['tflops']:.1f} TFLOP/s")
+    gemma = None
+    if not args.no_gemma:
+        gemma = run_gemma(max(10, args.steps), max(3, args.warmup))
+        log(f"text encoder: {gemma['ms']:.3f} ms per {GEMMA_TOKENS}-token encode, {gemma['tflops']:.1f} TFLOP/s")
     attn = bench_attention(reps=max(10, args.steps), warmup=max(2, args.warmup))
     if args.copy_calibration:
         attn["copy_calibration"] = copy_calibration()
@@ -336,6 +371,7 @@ def main():
         "pass_ms_wall": dit["ms_wall_median"] if dit else None,
         "pass_ms_host_to_host": dit["ms_host_to_host_median"] if dit else None,
         "joint_attention": attn,
+        "text_encoder": gemma,
         "gemm_i8": gemm,
         "roofline": {
             "kernel": "gemm_tiled_kernel (int8 ConvRot block linears of one pass: qkv, proj, w12, w3, kv_y)",
