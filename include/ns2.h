@@ -153,6 +153,37 @@ int ns2_linear_bf16(const float* A, int lda, const uint16_t* W, const float* bia
                     const float* add, float* C, int M, int N, int K, int ldc, long long cOff,
                     float alpha, int act, int resid, const float* gate, long long gOff);
 
+/* ---- LoRA side path (ops.linear with W.lora, app/gpu/ops.js:50-87 loraDelta; app/lora.js) ---
+ * The _lora variants compute the same linear plus the low-rank term
+ *   r += sum_k t[m,k] lora_b[n,k],  t = x lora_a^T,
+ * added after the bias, where the reference adds its `delta` (ADD, gemm.js:162), so it is not
+ * scaled by alpha or the int8 row scale. x is the linear's GEMM input: the rotated operand for
+ * int8 weights (so lora_a holds the down-projections rotated per 256-group, app/lora.js:61-78),
+ * the fp32 activations for bf16 weights.
+ *   lora_a: fp16 [lora_r, K], the down-projections A_i of every LoRA on the weight, stacked;
+ *   lora_b: fp16 [N, lora_r], column block i = strength_i * alpha_i / r_i * B_i in the rows of
+ *           its output window [off_i, off_i + n_i) and zero elsewhere (app/lora.js:144-152);
+ *   lora_r: the stacked rank, a multiple of 32 (pad with zero rows/columns), at most 256.
+ * Both 16-byte aligned; lora_b in the weight's original row order (also for the GLU-interleaved
+ * tiles of ns2_linear_i8_glu_rot_tiled). lora_r = 0 is the plain entry point. t lives in
+ * library scratch. Additive to the reference interface (its loraDelta materializes the
+ * [M, N] delta; here the term starts the GEMM accumulators). */
+int ns2_linear_i8_lora(const void* A, int a_fmt, int lda, const int8_t* W, const float* scale,
+                       const float* bias, const float* add, float* C, int M, int N, int K, int ldc,
+                       long long cOff, float alpha, int act, int resid, const float* gate,
+                       long long gOff, const uint16_t* lora_a, const uint16_t* lora_b, int lora_r);
+int ns2_linear_i8_tiled_lora(const uint16_t* At, const int8_t* Wt, const float* scale,
+                             const float* bias, float* C, int M, int N, int K, int ldc,
+                             long long cOff, float alpha, int act, int resid, const float* gate,
+                             long long gOff, const uint16_t* lora_a, const uint16_t* lora_b, int lora_r);
+int ns2_linear_i8_glu_rot_tiled_lora(const uint16_t* At, const int8_t* Wt, const float* scale,
+                                     const float* bias, uint16_t* Y, int M, int N, int K, float alpha,
+                                     int act, const uint16_t* lora_a, const uint16_t* lora_b, int lora_r);
+int ns2_linear_bf16_lora(const float* A, int lda, const uint16_t* W, const float* bias,
+                         const float* add, float* C, int M, int N, int K, int ldc, long long cOff,
+                         float alpha, int act, int resid, const float* gate, long long gOff,
+                         const uint16_t* lora_a, const uint16_t* lora_b, int lora_r);
+
 /* ---- attention without the fused kernel (ops.attention's materialized path, app/gpu/ops.js:
  *      211-241, softmaxShader) -----------------------------------------------------------
  * For heads h < H with K/V head g = h / group:

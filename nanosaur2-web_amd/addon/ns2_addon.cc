@@ -361,9 +361,9 @@ napi_value TileI8WeightGlu(napi_env env, napi_callback_info info) {
   return check(env, c, c.failed ? 0 : ns2_tile_i8_weight_glu(W, Wt, N, K));
 }
 
-// linearI8GluRotTiled(At, Wt, scale, bias, Y, M, N, K, alpha, act)
+// linearI8GluRotTiled(At, Wt, scale, bias, Y, M, N, K, alpha, act[, loraA, loraB, loraR])
 napi_value LinearI8GluRotTiled(napi_env env, napi_callback_info info) {
-  ARGS(10);
+  ARGS(13);
   auto At = (const uint16_t*)c.ptr(0);
   auto Wt = (const int8_t*)c.ptr(1);
   auto scale = (const float*)c.ptr(2);
@@ -372,13 +372,17 @@ napi_value LinearI8GluRotTiled(napi_env env, napi_callback_info info) {
   int M = c.i32(5), N = c.i32(6), K = c.i32(7);
   float alpha = c.f32(8);
   int act = c.i32(9);
+  // optional LoRA side path: loraA, loraB (device addresses), loraR (0: none)
+  auto la = (const uint16_t*)c.ptr(10);
+  auto lb = (const uint16_t*)c.ptr(11);
+  int lr = c.type(12) == napi_number ? c.i32(12) : 0;
   if (c.failed) return nullptr;
-  return check(env, c, ns2_linear_i8_glu_rot_tiled(At, Wt, scale, bias, Y, M, N, K, alpha, act));
+  return check(env, c, ns2_linear_i8_glu_rot_tiled_lora(At, Wt, scale, bias, Y, M, N, K, alpha, act, la, lb, lr));
 }
 
-// linearI8Tiled(At, Wt, scale, bias, C, M, N, K, ldc, cOff, alpha, act, resid, gate, gOff)
+// linearI8Tiled(At, Wt, scale, bias, C, M, N, K, ldc, cOff, alpha, act, resid, gate, gOff[, loraA, loraB, loraR])
 napi_value LinearI8Tiled(napi_env env, napi_callback_info info) {
-  ARGS(15);
+  ARGS(18);
   auto At = (const uint16_t*)c.ptr(0);
   auto Wt = (const int8_t*)c.ptr(1);
   auto scale = (const float*)c.ptr(2);
@@ -390,13 +394,17 @@ napi_value LinearI8Tiled(napi_env env, napi_callback_info info) {
   int act = c.i32(11), resid = c.i32(12);
   auto gate = (const float*)c.ptr(13);
   long long gOff = c.i64(14);
+  // optional LoRA side path: loraA, loraB (device addresses), loraR (0: none)
+  auto la = (const uint16_t*)c.ptr(15);
+  auto lb = (const uint16_t*)c.ptr(16);
+  int lr = c.type(17) == napi_number ? c.i32(17) : 0;
   if (c.failed) return nullptr;
-  return check(env, c, ns2_linear_i8_tiled(At, Wt, scale, bias, C, M, N, K, ldc, cOff, alpha, act, resid, gate, gOff));
+  return check(env, c, ns2_linear_i8_tiled_lora(At, Wt, scale, bias, C, M, N, K, ldc, cOff, alpha, act, resid, gate, gOff, la, lb, lr));
 }
 
-// linearI8(A, aFmt, lda, W, scale, bias, add, C, M, N, K, ldc, cOff, alpha, act, resid, gate, gOff)
+// linearI8(A, aFmt, lda, W, scale, bias, add, C, M, N, K, ldc, cOff, alpha, act, resid, gate, gOff[, loraA, loraB, loraR])
 napi_value LinearI8(napi_env env, napi_callback_info info) {
-  ARGS(18);
+  ARGS(21);
   const void* A = c.ptr(0);
   int aFmt = c.i32(1), lda = c.i32(2);
   auto W = (const int8_t*)c.ptr(3);
@@ -410,13 +418,17 @@ napi_value LinearI8(napi_env env, napi_callback_info info) {
   int act = c.i32(14), resid = c.i32(15);
   auto gate = (const float*)c.ptr(16);
   long long gOff = c.i64(17);
+  // optional LoRA side path: loraA, loraB (device addresses), loraR (0: none)
+  auto la = (const uint16_t*)c.ptr(18);
+  auto lb = (const uint16_t*)c.ptr(19);
+  int lr = c.type(20) == napi_number ? c.i32(20) : 0;
   if (c.failed) return nullptr;
-  return check(env, c, ns2_linear_i8(A, aFmt, lda, W, scale, bias, add, C, M, N, K, ldc, cOff, alpha, act, resid, gate, gOff));
+  return check(env, c, ns2_linear_i8_lora(A, aFmt, lda, W, scale, bias, add, C, M, N, K, ldc, cOff, alpha, act, resid, gate, gOff, la, lb, lr));
 }
 
-// linearBf16(A, lda, W, bias, add, C, M, N, K, ldc, cOff, alpha, act, resid, gate, gOff)
+// linearBf16(A, lda, W, bias, add, C, M, N, K, ldc, cOff, alpha, act, resid, gate, gOff[, loraA, loraB, loraR])
 napi_value LinearBf16(napi_env env, napi_callback_info info) {
-  ARGS(16);
+  ARGS(19);
   auto A = (const float*)c.ptr(0);
   int lda = c.i32(1);
   auto W = (const uint16_t*)c.ptr(2);
@@ -429,8 +441,12 @@ napi_value LinearBf16(napi_env env, napi_callback_info info) {
   int act = c.i32(12), resid = c.i32(13);
   auto gate = (const float*)c.ptr(14);
   long long gOff = c.i64(15);
+  // optional LoRA side path: loraA, loraB (device addresses), loraR (0: none)
+  auto la = (const uint16_t*)c.ptr(16);
+  auto lb = (const uint16_t*)c.ptr(17);
+  int lr = c.type(18) == napi_number ? c.i32(18) : 0;
   if (c.failed) return nullptr;
-  return check(env, c, ns2_linear_bf16(A, lda, W, bias, add, C, M, N, K, ldc, cOff, alpha, act, resid, gate, gOff));
+  return check(env, c, ns2_linear_bf16_lora(A, lda, W, bias, add, C, M, N, K, ldc, cOff, alpha, act, resid, gate, gOff, la, lb, lr));
 }
 
 // attention(q, k, v, o, batch, Lq, Lk, H, D, ldq, ldk, ldv, ldo, qOff, kOff, vOff, oOff,

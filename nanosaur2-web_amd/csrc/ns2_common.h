@@ -19,7 +19,13 @@ bool initialised();
 // Stream-ordered scratch owned by the library, grown on demand and reused by later calls
 // (one slot per concurrent use inside a single entry point).
 void* workspace(int slot, size_t bytes);
-constexpr int kWorkspaceSlots = 6;
+constexpr int kWorkspaceSlots = 7;
+// LoRA side path of a linear: checks the stacked down/up projections (lora_a fp16 [R][K],
+// lora_b fp16 [N][R], R % 32 == 0, R <= 256) and computes *t = x lora_a^T (fp32 [M][R], library
+// scratch) from the linear's input x: x_fmt 0 fp32 [M][ldx], 1 fp16 [M][ldx], 2 fp16 in the
+// tiled operand layout of the int8 GEMM (K columns). Returns a status code.
+int lora_prepare(const float** t, const uint16_t* lora_a, const uint16_t* lora_b, int R, const void* x, int x_fmt,
+                 int ldx, int M, int K, const char* name);
 
 // Kernel profiler (ns2_profile_*): when enabled, stream events bracket every launch and are
 // aggregated by kernel name on ns2_profile_report.
@@ -285,6 +291,39 @@ template <int N>
 __device__ __forceinline__ void vm_wait() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// ---- LoRA side path (app/gpu/ops.js:70-87: y = W x + sum_i s_i B_i (A_i x)) ----------------
+// The low-rank term of one 32x32 output tile, D[m][n] = sum_k t[m][k] lb[n][k] over k < R
+// (R % 16 == 0), as v_mfma_f32_32x32x16_f16 products: lane l supplies row `mrow` of t (fp32
+// [M][R], the down-projected input, rounded to fp16) and row `nrow` of lb (fp16 [N][R], the
+// up-projections with their strengths, stacked along R), k = 16s + 8(l/32) .. +7. The caller
+// passes the rows of its lane (l % 32 of the tile), clamped into the matrices.
+__device__ __forceinline__ float16_t lora_tile(const float* __restrict__ t, const half_t* __restrict__ lb, int R,
+                                               int mrow, int nrow, int hi) {
+  float16_t d;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) d[r] = 0.f;
+  const float* tp = t + (long long)mrow * R + 8 * hi;
+  const half_t* bp = lb + (long long)nrow * R + 8 * hi;
+  for (int k = 0; k < R; k += 16) {
+    const float4 x0 = *reinterpret_cast<const float4*>(tp + k);
+    const float4 x1 = *reinterpret_cast<const float4*>(tp + k + 4);
+    const half8_t a = {(half_t)x0.x, (half_t)x0.y, (half_t)x0.z, (half_t)x0.w,
+                       (half_t)x1.x, (half_t)x1.y, (half_t)x1.z, (half_t)x1.w};
+    const half8_t b = *reinterpret_cast<const half8_t*>(bp + k);
+    d = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, d, 0, 0, 0);
+  }
+  return d;
+}
+
+// Start value of a GEMM accumulator tile that folds the LoRA term into the products: the
+// epilogue computes acc * alpha * rs + bias + ..., so acc starts at D / (alpha * rs) and the
+// result carries D unscaled after bias, where the reference adds it (gemm.js:159-162).
+__device__ __forceinline__ void lora_init(float16_t& acc, const float16_t& d, float alpha_rs) {
+  const float inv = alpha_rs != 0.f ? 1.0f / alpha_rs : 0.f;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) acc[r] = d[r] * inv;
 }
 
 }  // namespace ns2dev

@@ -32,6 +32,10 @@ struct GemmArgs {
   // epilogue); splitk_reduce_kernel adds the splits in z order and applies the epilogue
   float* part;
   int ksteps;
+  // LoRA side path (lora_tile / lora_init): lt fp32 [M][lr], lb fp16 [N][lr]; lr = 0 without
+  const float* lt;
+  const half_t* lb;
+  int lr;
 };
 
 constexpr int BK = 64;        // k per LDS tile
@@ -164,7 +168,7 @@ struct WLoader {
 // MFMA 32x32x16 operand layout: lane l supplies row (l % 32) of A and column (l % 32) of B,
 // each with 8 consecutive k of the 16 (k = 8 * (l / 32) + e); accumulator element r of lane
 // l is C[8 * (r / 4) + 4 * (l / 32) + r % 4][l % 32].
-template <int BM, int BN, int WM, int WN, bool A_F32, bool W_BF16>
+template <int BM, int BN, int WM, int WN, bool A_F32, bool W_BF16, bool LORA>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_kernel(GemmArgs p) {
   constexpr int WAVES_N = BN / WN;
   constexpr int NT = (BM / WM) * WAVES_N * 64;
@@ -195,11 +199,26 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_kernel(G
   }
   la.load(p, m0, kt0 * BK, tid);
   lw.load(p, n0, kt0 * BK, tid);
+  const int lrow = lane & 31, lk = (lane >> 5) * 8;
+  // LoRA: the accumulators start at the low-rank term over alpha * scale (the first split only)
+  if (LORA && blockIdx.z == 0) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      int n = n0 + wn * WN + j * 32 + lrow;
+      n = n < p.N ? n : p.N - 1;
+      const float ars = p.alpha * (p.scale ? p.scale[n] : 1.0f);
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        int m = m0 + wm * WM + i * 32 + lrow;
+        m = m < p.M ? m : p.M - 1;
+        lora_init(acc[i][j], lora_tile(p.lt, p.lb, p.lr, m, n, lane >> 5), ars);
+      }
+    }
+  }
   la.store(lds_a[0], tid);
   lw.store(lds_b[0], tid);
   __syncthreads();
 
-  const int lrow = lane & 31, lk = (lane >> 5) * 8;
   for (int kt = 0; kt < nk; ++kt) {
     const int cur = kt & 1;
     if (kt + 1 < nk) {
@@ -326,6 +345,19 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemmArgs p) {
   const float rs = p.scale ? p.scale[n] : 1.0f;
   const float bi = p.bias ? p.bias[n] : 0.0f;
   const float gt = p.gate ? p.gate[p.gOff + n] : 1.0f;
+  if (p.lr) {
+    // LoRA term over alpha * scale, summed across the lanes with the products
+    const float ars = p.alpha * rs;
+    const float inv = ars != 0.f ? 1.0f / ars : 0.f;
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      if (m < p.M) {
+        float d = 0.f;
+        for (int k = lane; k < p.lr; k += 64) d += p.lt[(long long)m * p.lr + k] * (float)p.lb[(long long)n * p.lr + k];
+        acc[m] += d * inv;
+      }
+    }
+  }
 #pragma unroll
   for (int m = 0; m < 8; ++m) {
     if (m < p.M) {
@@ -349,6 +381,66 @@ __global__ __launch_bounds__(256) void cast_f16_kernel(const float* __restrict__
   *reinterpret_cast<uint2*>(y + i) = o;
 }
 
+// ---- LoRA down-projection -------------------------------------------------------------------
+// t[M][R] = x A^T for the LoRA side path (A fp16 [R][K], the stacked down-projections). A block
+// of NWV waves takes 32 rows; wave w takes the k-steps w, w + NWV, ... of 16, and the partial
+// 32 x R accumulators are summed through LDS. RT = R / 32 output tiles of 32 columns.
+template <int RT>
+constexpr int lora_waves() { return RT <= 4 ? 8 : 4; }
+
+template <int XFMT, int RT>
+__global__ __launch_bounds__(64 * lora_waves<RT>()) void lora_down_kernel(const void* __restrict__ x, int ldx,
+                                                                          const half_t* __restrict__ A,
+                                                                          float* __restrict__ t, int M, int K) {
+  constexpr int R = 32 * RT;
+  constexpr int kLoraWaves = lora_waves<RT>();
+  __shared__ float red[kLoraWaves - 1][RT][16][64];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, lq = lane & 31, hi = lane >> 5;
+  const int m0 = blockIdx.x * 32;
+  const int m = m0 + lq < M ? m0 + lq : M - 1;  // rows past M read the last row (not stored)
+  float16_t acc[RT];
+#pragma unroll
+  for (int j = 0; j < RT; ++j)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[j][r] = 0.f;
+  for (int k = 16 * wave + 8 * hi; k < K; k += 16 * kLoraWaves) {
+    half8_t a;
+    if constexpr (XFMT == 0) {
+      const float* xp = static_cast<const float*>(x) + (long long)m * ldx + k;
+      const float4 u = *reinterpret_cast<const float4*>(xp);
+      const float4 v = *reinterpret_cast<const float4*>(xp + 4);
+      a = half8_t{(half_t)u.x, (half_t)u.y, (half_t)u.z, (half_t)u.w, (half_t)v.x, (half_t)v.y, (half_t)v.z, (half_t)v.w};
+    } else if constexpr (XFMT == 1) {
+      a = *reinterpret_cast<const half8_t*>(static_cast<const half_t*>(x) + (long long)m * ldx + k);
+    } else {
+      a = *reinterpret_cast<const half8_t*>(static_cast<const half_t*>(x) + tiled_off(m, k, K));
+    }
+#pragma unroll
+    for (int j = 0; j < RT; ++j) {
+      const half8_t b = *reinterpret_cast<const half8_t*>(A + (long long)(32 * j + lq) * K + k);
+      acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc[j], 0, 0, 0);
+    }
+  }
+  if (wave > 0) {
+#pragma unroll
+    for (int j = 0; j < RT; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) red[wave - 1][j][r][lane] = acc[j][r];
+  }
+  __syncthreads();
+  if (wave > 0) return;
+#pragma unroll
+  for (int j = 0; j < RT; ++j)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      float v = acc[j][r];
+#pragma unroll
+      for (int w = 0; w < kLoraWaves - 1; ++w) v += red[w][j][r][lane];
+      const int row = m0 + 8 * (r >> 2) + 4 * hi + (r & 3);
+      if (row < M) t[(long long)row * R + 32 * j + lq] = v;
+    }
+}
+
 constexpr int kGemvMaxM = 8;
 constexpr long long kSmallGridBlocks = 256;  // one block per CU
 constexpr int kMaxSplits = 16;
@@ -362,7 +454,8 @@ int launch_gemm(const GemmArgs& p, const char* name) {
   } else if (big_tiles >= kSmallGridBlocks) {
     constexpr int BM = 128, BN = 128, WM = 64, WN = 64;
     dim3 grid((p.N + BN - 1) / BN, (p.M + BM - 1) / BM);
-    gemm_mfma_kernel<BM, BN, WM, WN, A_F32, W_BF16><<<grid, (BM / WM) * (BN / WN) * 64, 0, s>>>(p);
+    if (p.lr) gemm_mfma_kernel<BM, BN, WM, WN, A_F32, W_BF16, true><<<grid, (BM / WM) * (BN / WN) * 64, 0, s>>>(p);
+    else gemm_mfma_kernel<BM, BN, WM, WN, A_F32, W_BF16, false><<<grid, (BM / WM) * (BN / WN) * 64, 0, s>>>(p);
   } else {
     // Too few 128x128 tiles to fill 256 CUs (a short sequence): 64x64 tiles, and when even
     // those leave the chip idle, split K over blockIdx.z (at least 4 k tiles per split).
@@ -380,7 +473,8 @@ int launch_gemm(const GemmArgs& p, const char* name) {
       if (!q.part) return ns2::set_error(NS2_ERR_OOM, "%s: split-K workspace allocation failed", name);
     }
     dim3 grid((p.N + BN - 1) / BN, (p.M + BM - 1) / BM, splits > 1 ? splits : 1);
-    gemm_mfma_kernel<BM, BN, WM, WN, A_F32, W_BF16><<<grid, (BM / WM) * (BN / WN) * 64, 0, s>>>(q);
+    if (q.lr) gemm_mfma_kernel<BM, BN, WM, WN, A_F32, W_BF16, true><<<grid, (BM / WM) * (BN / WN) * 64, 0, s>>>(q);
+    else gemm_mfma_kernel<BM, BN, WM, WN, A_F32, W_BF16, false><<<grid, (BM / WM) * (BN / WN) * 64, 0, s>>>(q);
     if (splits > 1) {
       const long long mn = (long long)p.M * p.N;
       splitk_reduce_kernel<<<(unsigned)((mn + 255) / 256), 256, 0, s>>>(q, splits);
@@ -404,7 +498,43 @@ int check_common(const GemmArgs& p, const char* name) {
   return NS2_OK;
 }
 
+template <int XFMT>
+void launch_lora_down(const void* x, int ldx, const half_t* A, float* t, int M, int K, int R, hipStream_t s) {
+  const dim3 grid((M + 31) / 32);
+  switch (R / 32) {
+#define NS2_LORA_CASE(RT) \
+  case RT: lora_down_kernel<XFMT, RT><<<grid, 64 * lora_waves<RT>(), 0, s>>>(x, ldx, A, t, M, K); break;
+    NS2_LORA_CASE(1) NS2_LORA_CASE(2) NS2_LORA_CASE(3) NS2_LORA_CASE(4)
+    NS2_LORA_CASE(5) NS2_LORA_CASE(6) NS2_LORA_CASE(7) NS2_LORA_CASE(8)
+#undef NS2_LORA_CASE
+    default: break;
+  }
+}
+
 }  // namespace
+
+namespace ns2 {
+
+int lora_prepare(const float** t, const uint16_t* lora_a, const uint16_t* lora_b, int R, const void* x, int x_fmt,
+                 int ldx, int M, int K, const char* name) {
+  NS2_REQUIRE(lora_a && lora_b && aligned16(lora_a) && aligned16(lora_b), "%s: null or unaligned LoRA projections", name);
+  NS2_REQUIRE(R > 0 && R % 32 == 0 && R <= 256,
+              "%s: LoRA rank %d must be a positive multiple of 32, at most 256 (pad with zero rows)", name, R);
+  NS2_REQUIRE(K % 16 == 0 && x && aligned16(x), "%s: LoRA input must be 16-byte aligned with K %% 16 == 0", name);
+  NS2_REQUIRE(x_fmt == 2 || ldx % (x_fmt == 0 ? 4 : 8) == 0, "%s: LoRA input stride %d not 16-byte aligned", name, ldx);
+  float* tb = static_cast<float*>(workspace(6, (size_t)M * R * sizeof(float)));
+  if (!tb) return set_error(NS2_ERR_OOM, "%s: LoRA workspace allocation failed", name);
+  ProfScope prof_("lora_down");
+  const half_t* A = reinterpret_cast<const half_t*>(lora_a);
+  if (x_fmt == 0) launch_lora_down<0>(x, ldx, A, tb, M, K, R, stream());
+  else if (x_fmt == 1) launch_lora_down<1>(x, ldx, A, tb, M, K, R, stream());
+  else launch_lora_down<2>(x, ldx, A, tb, M, K, R, stream());
+  NS2_LAUNCHED("lora_down");
+  *t = tb;
+  return NS2_OK;
+}
+
+}  // namespace ns2
 
 extern "C" {
 
@@ -412,6 +542,14 @@ int ns2_linear_i8(const void* A, int a_fmt, int lda, const int8_t* W, const floa
                   const float* bias, const float* add, float* C, int M, int N, int K, int ldc,
                   long long cOff, float alpha, int act, int resid, const float* gate,
                   long long gOff) {
+  return ns2_linear_i8_lora(A, a_fmt, lda, W, scale, bias, add, C, M, N, K, ldc, cOff, alpha, act, resid, gate,
+                            gOff, nullptr, nullptr, 0);
+}
+
+int ns2_linear_i8_lora(const void* A, int a_fmt, int lda, const int8_t* W, const float* scale,
+                       const float* bias, const float* add, float* C, int M, int N, int K, int ldc,
+                       long long cOff, float alpha, int act, int resid, const float* gate,
+                       long long gOff, const uint16_t* lora_a, const uint16_t* lora_b, int lora_r) {
   NS2_READY();
   if (M == 0) return NS2_OK;
   GemmArgs p{A, W, scale, bias, add, C, gate, cOff, gOff, lda, ldc, M, N, K, alpha, act, resid};
@@ -439,17 +577,38 @@ int ns2_linear_i8(const void* A, int a_fmt, int lda, const int8_t* W, const floa
   }
   int rc = check_common(p, "ns2_linear_i8");
   if (rc) return rc;
+  if (lora_r) {
+    // the LoRA down-projections take the rotated input (rotated A for int8 weights)
+    rc = ns2::lora_prepare(&p.lt, lora_a, lora_b, lora_r, p.A, 1, p.lda, M, K, "ns2_linear_i8_lora");
+    if (rc) return rc;
+    p.lb = reinterpret_cast<const half_t*>(lora_b);
+    p.lr = lora_r;
+  }
   return launch_gemm<false, false>(p, "linear_i8");
 }
 
 int ns2_linear_bf16(const float* A, int lda, const uint16_t* W, const float* bias,
                     const float* add, float* C, int M, int N, int K, int ldc, long long cOff,
                     float alpha, int act, int resid, const float* gate, long long gOff) {
+  return ns2_linear_bf16_lora(A, lda, W, bias, add, C, M, N, K, ldc, cOff, alpha, act, resid, gate, gOff,
+                              nullptr, nullptr, 0);
+}
+
+int ns2_linear_bf16_lora(const float* A, int lda, const uint16_t* W, const float* bias,
+                         const float* add, float* C, int M, int N, int K, int ldc, long long cOff,
+                         float alpha, int act, int resid, const float* gate, long long gOff,
+                         const uint16_t* lora_a, const uint16_t* lora_b, int lora_r) {
   NS2_READY();
   if (M == 0) return NS2_OK;
   GemmArgs p{A, W, nullptr, bias, add, C, gate, cOff, gOff, lda, ldc, M, N, K, alpha, act, resid};
   int rc = check_common(p, "ns2_linear_bf16");
   if (rc) return rc;
+  if (lora_r) {
+    rc = ns2::lora_prepare(&p.lt, lora_a, lora_b, lora_r, A, 0, lda, M, K, "ns2_linear_bf16_lora");
+    if (rc) return rc;
+    p.lb = reinterpret_cast<const half_t*>(lora_b);
+    p.lr = lora_r;
+  }
   return launch_gemm<true, true>(p, "linear_bf16");
 }
 

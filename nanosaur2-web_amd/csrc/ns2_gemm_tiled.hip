@@ -33,6 +33,11 @@ struct TGemmArgs {
   int tiles_m, tiles_n;  // block tiles
   float alpha;
   int act, resid;
+  // LoRA side path: lt fp32 [M][lr] (the down-projected input), lb fp16 [N][lr] (up-projections,
+  // original row order, strengths folded), lr % 32 == 0; lr = 0 without LoRA
+  const float* lt;
+  const half_t* lb;
+  int lr;
 };
 
 // 8 biased bytes (two dwords) -> 8 halfs: byte u -> half(0x6400 | u) - 1152 = u - 128 = w.
@@ -152,7 +157,7 @@ __device__ __forceinline__ void store_plain(const TGemmArgs& p, const float16_t 
 // (ns2_tile_i8_weight_glu), so the 64 columns of a wave hold 32 columns of each GLU half; the
 // block's 512 columns give 256 consecutive outputs act(h1) * h2, one rotation group, which is
 // rotated and written to Y as the tiled fp16 operand of the next int8 linear.
-template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int EPI, int ACT, int RM>
+template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int EPI, int ACT, int RM, bool LORA>
 __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void gemm_tiled_kernel(TGemmArgs p) {
   constexpr int NW = WAVES_M * WAVES_N;
   constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
@@ -230,6 +235,26 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void gemm_tiled_kernel(TGem
 
   dma(0, 0);
   if (STAGES == 3 && kblocks > 1) dma(1, 1);
+
+  // LoRA: the accumulators start at the low-rank term over alpha * scale (its loads overlap the
+  // first copies). GLU launches: column j = 0 of a wave is output G of the first half, j = 1
+  // output I + G of the second (the interleave of ns2_tile_i8_weight_glu).
+  if constexpr (LORA) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      int n;
+      if constexpr (EPI == 1) n = (j == 0 ? 0 : p.N / 2) + n0 / 2 + 32 * wn + lq;
+      else n = n0 + wn * WTN + 32 * j + lq;
+      n = n < p.N ? n : p.N - 1;
+      const float ars = p.alpha * p.scale[n];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        int m = m0 + wm * WTM + 32 * i + lq;
+        m = m < p.M ? m : p.M - 1;
+        lora_init(acc[i][j], lora_tile(p.lt, p.lb, p.lr, m, n, hi), ars);
+      }
+    }
+  }
 
   // fragments of k-step s (16 k) of a stage: A rows wm*WTM + 32i + lq, k 16s + 8hi .. +7 (chunk
   // 2s + hi); W columns wn*WTN + 32j + lq, the same k (8-byte chunk 2s + hi)
@@ -371,7 +396,11 @@ int launch_tiled(TGemmArgs p) {
   const dim3 grid(p.tiles_m * p.tiles_n), block(WM * WN * 64);
   hipStream_t s = ns2::stream();
   const int rm = !p.resid ? 0 : (p.gate ? 2 : 1);
-#define NS2_TILED(A, R) gemm_tiled_kernel<BM, BN, WM, WN, STAGES, EPI, A, R><<<grid, block, 0, s>>>(p)
+#define NS2_TILED(A, R)                                                              \
+  do {                                                                               \
+    if (p.lr) gemm_tiled_kernel<BM, BN, WM, WN, STAGES, EPI, A, R, true><<<grid, block, 0, s>>>(p);  \
+    else gemm_tiled_kernel<BM, BN, WM, WN, STAGES, EPI, A, R, false><<<grid, block, 0, s>>>(p);      \
+  } while (0)
   if constexpr (EPI == 1) {
     if (p.act == NS2_ACT_SILU) NS2_TILED(NS2_ACT_SILU, 0);
     else if (p.act == NS2_ACT_GELU_TANH) NS2_TILED(NS2_ACT_GELU_TANH, 0);
@@ -461,6 +490,12 @@ int ns2_tile_i8_weight_glu(const int8_t* W, int8_t* Wt, int N, int K) {
 
 int ns2_linear_i8_glu_rot_tiled(const uint16_t* At, const int8_t* Wt, const float* scale, const float* bias,
                                 uint16_t* Y, int M, int N, int K, float alpha, int act) {
+  return ns2_linear_i8_glu_rot_tiled_lora(At, Wt, scale, bias, Y, M, N, K, alpha, act, nullptr, nullptr, 0);
+}
+
+int ns2_linear_i8_glu_rot_tiled_lora(const uint16_t* At, const int8_t* Wt, const float* scale, const float* bias,
+                                     uint16_t* Y, int M, int N, int K, float alpha, int act, const uint16_t* lora_a,
+                                     const uint16_t* lora_b, int lora_r) {
   NS2_READY();
   if (M == 0) return NS2_OK;
   NS2_REQUIRE(At && Wt && scale && Y, "ns2_linear_i8_glu_rot_tiled: null At, Wt, scale or Y");
@@ -470,6 +505,12 @@ int ns2_linear_i8_glu_rot_tiled(const uint16_t* At, const int8_t* Wt, const floa
   NS2_REQUIRE(act >= NS2_ACT_NONE && act <= NS2_ACT_GELU_TANH, "ns2_linear_i8_glu_rot_tiled: unknown act %d", act);
   TGemmArgs p{reinterpret_cast<const half_t*>(At), reinterpret_cast<const uint8_t*>(Wt), scale, bias, nullptr, Y,
               nullptr, 0, 0, M, N, K, N, (M + 63) / 64, N / 64, 0, 0, alpha, act, 0};
+  if (lora_r) {
+    int rc = ns2::lora_prepare(&p.lt, lora_a, lora_b, lora_r, At, 2, K, M, K, "ns2_linear_i8_glu_rot_tiled_lora");
+    if (rc) return rc;
+    p.lb = reinterpret_cast<const half_t*>(lora_b);
+    p.lr = lora_r;
+  }
   ns2::ProfScope prof_("gemm_i8_glu_rot");
   return launch_tiled<64, 512, 1, 8, 2, 1>(p);
 }
@@ -477,6 +518,14 @@ int ns2_linear_i8_glu_rot_tiled(const uint16_t* At, const int8_t* Wt, const floa
 int ns2_linear_i8_tiled(const uint16_t* At, const int8_t* Wt, const float* scale, const float* bias,
                         float* C, int M, int N, int K, int ldc, long long cOff, float alpha, int act,
                         int resid, const float* gate, long long gOff) {
+  return ns2_linear_i8_tiled_lora(At, Wt, scale, bias, C, M, N, K, ldc, cOff, alpha, act, resid, gate, gOff,
+                                  nullptr, nullptr, 0);
+}
+
+int ns2_linear_i8_tiled_lora(const uint16_t* At, const int8_t* Wt, const float* scale, const float* bias,
+                             float* C, int M, int N, int K, int ldc, long long cOff, float alpha, int act,
+                             int resid, const float* gate, long long gOff, const uint16_t* lora_a,
+                             const uint16_t* lora_b, int lora_r) {
   NS2_READY();
   if (M == 0) return NS2_OK;
   NS2_REQUIRE(At && Wt && scale && C, "ns2_linear_i8_tiled: null At, Wt, scale or C");
@@ -487,6 +536,12 @@ int ns2_linear_i8_tiled(const uint16_t* At, const int8_t* Wt, const float* scale
   NS2_REQUIRE(act >= NS2_ACT_NONE && act <= NS2_ACT_GELU_TANH, "ns2_linear_i8_tiled: unknown act %d", act);
   TGemmArgs p{reinterpret_cast<const half_t*>(At), reinterpret_cast<const uint8_t*>(Wt), scale, bias, C, nullptr, gate,
               cOff, gOff, M, N, K, ldc, (M + 63) / 64, N / 64, 0, 0, alpha, act, resid};
+  if (lora_r) {
+    int rc = ns2::lora_prepare(&p.lt, lora_a, lora_b, lora_r, At, 2, K, M, K, "ns2_linear_i8_tiled_lora");
+    if (rc) return rc;
+    p.lb = reinterpret_cast<const half_t*>(lora_b);
+    p.lr = lora_r;
+  }
   ns2::ProfScope prof_("gemm_i8_tiled");
   switch (pick_config(M, N)) {
     case 0: return launch_tiled<256, 256, 4, 4>(p);

@@ -8,6 +8,7 @@
 
 import { addr, DeviceBuffer } from "./device.js";
 import { native, ACT, EW } from "./native.js";
+import { loraArgs } from "./lora.js";
 
 const opt = (v, d) => (v === undefined || v === null ? d : v);
 
@@ -72,8 +73,10 @@ export function linearGluRotated(gpu, xr, W, act, name = "gemm.i8.glu") {
   if (!xr.tiled || !W.tglu) throw new Error(`${W.name}: linearGluRotated needs a tiled operand and tileWeightGlu`);
   const M = xr.rows, I = W.N / 2;
   const y = rotatedOperand(gpu, M, I, true);
+  const lora = loraArgs(gpu, W);
   gpu.run(name, 2 * M * W.N * W.K, () =>
-    native.linearI8GluRotTiled(addr(xr), addr(W.tglu), addr(W.scale), addr(W.bias || null), addr(y), M, W.N, W.K, 1, ACT[act]));
+    native.linearI8GluRotTiled(addr(xr), addr(W.tglu), addr(W.scale), addr(W.bias || null), addr(y), M, W.N, W.K, 1,
+      ACT[act], ...lora));
   return y;
 }
 
@@ -83,7 +86,9 @@ export function linearGluRotated(gpu, xr, W, act, name = "gemm.i8.glu") {
 export function linear(gpu, x, W, opts = {}) {
   const src = opts.xr || x;
   const M = src.tiled ? src.rows : src.size / W.K;
-  if (W.lora && W.lora.length) throw new Error(`${W.name}: LoRA side paths are not part of this build`);
+  // LoRA side paths (W.lora, attached by lora.js): the stacked low-rank term starts the GEMM's
+  // accumulators; the down-projection takes the same (rotated) input (app/gpu/ops.js:54-58)
+  const lora = loraArgs(gpu, W);
   const out = opts.out || gpu.empty([M, W.N]);
   const ldc = opt(opts.ldc, W.N);
   const cOff = opt(opts.cOff, 0);
@@ -97,16 +102,16 @@ export function linear(gpu, x, W, opts = {}) {
     if (!W.tbuf) throw new Error(`${W.name}: a tiled operand needs the tiled weight (tileWeight)`);
     gpu.run(opts.name || "gemm.i8", flops, () =>
       native.linearI8Tiled(addr(src), addr(W.tbuf), addr(W.scale), addr(bias), addr(out), M, W.N, W.K, ldc,
-        cOff, 1, act, resid, addr(opts.gate), gOff));
+        cOff, 1, act, resid, addr(opts.gate), gOff, ...lora));
   } else if (W.kind === "i8") {
     const aFmt = opts.xr ? (opts.xr.dtype === "f16" ? 1 : 2) : 0;
     gpu.run(opts.name || "gemm.i8", flops, () =>
       native.linearI8(addr(src), aFmt, W.K, addr(W.buf), addr(W.scale), addr(bias), null, addr(out),
-        M, W.N, W.K, ldc, cOff, 1, act, resid, addr(opts.gate), gOff));
+        M, W.N, W.K, ldc, cOff, 1, act, resid, addr(opts.gate), gOff, ...lora));
   } else if (W.kind === "bf16") {
     gpu.run(opts.name || "gemm.bf16", flops, () =>
       native.linearBf16(addr(x), W.K, addr(W.buf), addr(bias), null, addr(out), M, W.N, W.K, ldc, cOff,
-        1, act, resid, addr(opts.gate), gOff));
+        1, act, resid, addr(opts.gate), gOff, ...lora));
   } else {
     throw new Error(`linear: weight kind ${W.kind} is not part of this build`);
   }

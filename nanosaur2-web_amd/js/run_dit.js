@@ -2,14 +2,15 @@
 //
 //   node run_dit.js (--weights FILE.safetensors | --synthetic SEED)
 //                   (--inputs DIR | --shape H,W,T[,SEED])
-//                   [--out FILE.f32] [--reference-ops] [--path-drop]
+//                   [--out FILE.f32] [--reference-ops] [--path-drop] [--lora FILE[:STRENGTH]]...
 //                   [--warmup N] [--reps N] [--profile]
 //
 // --inputs DIR holds inputs.json {h, w, sigma, T} and latent.f32 [64*h*w], context.f32
 // [T*640], weights.f32 [T]. --out writes the x0 prediction [64, h, w] as raw fp32.
 // With --reps, the pass is timed with the latent resident in device memory (stream events
 // and wall clock), and once more host-to-host (upload, pass, readback); one JSON line with
-// the timings (and the per-op profile with --profile) is printed.
+// the timings (and the per-op profile with --profile) is printed. --lora attaches a LoRA file
+// (strength 1 by default; repeatable) to the model's linears (lora.js), as the pipeline does.
 
 import fs from "fs";
 import path from "path";
@@ -18,9 +19,10 @@ import { native } from "./native.js";
 import { Nanosaur2DiT } from "./nanosaur2.js";
 import { SafeTensors } from "./weights.js";
 import { SyntheticWeights } from "./synthetic.js";
+import { linearRegistry, loadLora, attachLoras } from "./lora.js";
 
 function parseArgs(argv) {
-  const a = { warmup: 0, reps: 0 };
+  const a = { warmup: 0, reps: 0, loras: [] };
   for (let i = 0; i < argv.length; i++) {
     const k = argv[i];
     const next = () => argv[++i];
@@ -34,9 +36,16 @@ function parseArgs(argv) {
     else if (k === "--warmup") a.warmup = Number(next());
     else if (k === "--reps") a.reps = Number(next());
     else if (k === "--profile") a.profile = true;
+    else if (k === "--lora") a.loras.push(parseLora(next()));
     else throw new Error(`unknown argument ${k}`);
   }
   return a;
+}
+
+// "FILE[:STRENGTH]" -> { file, strength }
+export function parseLora(arg) {
+  const m = /^(.*):(-?[\d.]+)$/.exec(arg);
+  return m ? { file: m[1], strength: Number(m[2]) } : { file: arg, strength: 1 };
 }
 
 function readF32(file) {
@@ -83,11 +92,23 @@ async function main() {
   const st = a.weights ? await SafeTensors.open(a.weights) : new SyntheticWeights(a.synthetic || 3);
   const dit = await Nanosaur2DiT.load(gpu, st, null, { fused: !a.referenceOps });
   if (st.close) st.close();
+  const loraReports = [];
+  if (a.loras.length) {
+    const regs = { dit: linearRegistry(dit) };
+    const active = [];
+    for (const { file, strength } of a.loras) {
+      const L = await loadLora(file, regs);
+      loraReports.push({ file, strength, matched: L.matched, total: L.total, unsupported: L.unsupported, skipped: L.skipped });
+      active.push({ lora: L, strength });
+    }
+    attachLoras(regs, active);
+  }
   const inp = a.inputs ? loadInputs(a.inputs) : syntheticInputs(a.shape || [76, 52, 256]);
   const { h, w, sigma } = inp;
   const text = dit.prepareText(inp.context, Array.from(inp.weights));
   const loadMs = Date.now() - t0;
-  const report = { h, w, T: inp.T, tokens: h * w, fused: !a.referenceOps, pathDrop: !!a.pathDrop, load_ms: loadMs, device: gpu.info };
+  const report = { h, w, T: inp.T, tokens: h * w, fused: !a.referenceOps, pathDrop: !!a.pathDrop, load_ms: loadMs, device: gpu.info,
+    loras: loraReports };
 
   if (a.out) {
     const x0 = await dit.forward(inp.latent, h, w, text, sigma, { pathDrop: !!a.pathDrop });

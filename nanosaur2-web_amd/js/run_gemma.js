@@ -2,7 +2,7 @@
 //
 //   node run_gemma.js (--weights FILE.safetensors | --synthetic SEED)
 //                     (--ids FILE.json | --tokens N[,SEED])
-//                     [--out FILE.f32] [--warmup N] [--reps N] [--profile]
+//                     [--out FILE.f32] [--warmup N] [--reps N] [--profile] [--lora FILE[:STRENGTH]]...
 //
 // --ids holds a JSON array of token ids; --tokens draws N seeded ids. --out writes the hidden
 // states [L, 640] as raw fp32. With --reps the encoder is timed on device-resident embeddings
@@ -16,9 +16,10 @@ import * as ops from "./ops.js";
 import { Gemma3 } from "./gemma3.js";
 import { SafeTensors } from "./weights.js";
 import { SyntheticWeights } from "./synthetic.js";
+import { linearRegistry, loadLora, attachLoras } from "./lora.js";
 
 function parseArgs(argv) {
-  const a = { warmup: 0, reps: 0 };
+  const a = { warmup: 0, reps: 0, loras: [] };
   for (let i = 0; i < argv.length; i++) {
     const k = argv[i];
     const next = () => argv[++i];
@@ -30,7 +31,10 @@ function parseArgs(argv) {
     else if (k === "--warmup") a.warmup = Number(next());
     else if (k === "--reps") a.reps = Number(next());
     else if (k === "--profile") a.profile = true;
-    else throw new Error(`unknown argument ${k}`);
+    else if (k === "--lora") {
+      const m = /^(.*):(-?[\d.]+)$/.exec(next() || "");
+      a.loras.push(m ? { file: m[1], strength: Number(m[2]) } : { file: argv[i], strength: 1 });
+    } else throw new Error(`unknown argument ${k}`);
   }
   return a;
 }
@@ -56,10 +60,21 @@ async function main() {
   const gpu = await GPU.create({ profile: !!a.profile });
   const st = a.weights ? await SafeTensors.open(a.weights) : new SyntheticWeights(a.synthetic || 3, { gemma: true });
   const te = await Gemma3.load(gpu, st);
+  const loraReports = [];
+  if (a.loras.length) {
+    const regs = { te: linearRegistry(te) };
+    const active = [];
+    for (const { file, strength } of a.loras) {
+      const L = await loadLora(file, regs);
+      loraReports.push({ file, strength, matched: L.matched, total: L.total, unsupported: L.unsupported, skipped: L.skipped });
+      active.push({ lora: L, strength });
+    }
+    attachLoras(regs, active);
+  }
   const vocab = (st.info ? st.info("model.embed_tokens.weight") : st.spec.get("model.embed_tokens.weight")).shape[0];
   const ids = a.ids || seededIds(a.tokens || [256, 1], vocab);
   const rows = await st.rows("model.embed_tokens.weight", ids);
-  const report = { tokens: ids.length, load_ms: Date.now() - t0, device: gpu.info };
+  const report = { tokens: ids.length, load_ms: Date.now() - t0, device: gpu.info, loras: loraReports };
 
   if (a.out) {
     const h = te.encodeEmbedded(te.embed(rows, ids.length));

@@ -49,13 +49,20 @@ SIGNATURES = {
     "ns2_rotate_f16": [c_vp, c_int, c_vp, c_int, c_int, c_int, c_int],
     "ns2_linear_i8_tiled": [c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_ll, c_float,
                             c_int, c_int, c_vp, c_ll],
+    "ns2_linear_i8_tiled_lora": [c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_ll, c_float,
+                            c_int, c_int, c_vp, c_ll, c_vp, c_vp, c_int],
     "ns2_tile_i8_weight": [c_vp, c_vp, c_int, c_int],
     "ns2_tile_i8_weight_glu": [c_vp, c_vp, c_int, c_int],
     "ns2_linear_i8_glu_rot_tiled": [c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_float, c_int],
+    "ns2_linear_i8_glu_rot_tiled_lora": [c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_float, c_int, c_vp, c_vp, c_int],
     "ns2_linear_i8": [c_vp, c_int, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int,
                       c_ll, c_float, c_int, c_int, c_vp, c_ll],
+    "ns2_linear_i8_lora": [c_vp, c_int, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int,
+                      c_ll, c_float, c_int, c_int, c_vp, c_ll, c_vp, c_vp, c_int],
     "ns2_linear_bf16": [c_vp, c_int, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_ll,
                         c_float, c_int, c_int, c_vp, c_ll],
+    "ns2_linear_bf16_lora": [c_vp, c_int, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_ll,
+                        c_float, c_int, c_int, c_vp, c_ll, c_vp, c_vp, c_int],
     "ns2_attention": [c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
                       c_int, c_ll, c_ll, c_ll, c_ll, c_ll, c_ll, c_ll, c_ll, c_float, c_vp, c_int,
                       c_ll, c_vp, c_vp, c_float, c_vp, c_ll, c_int],
@@ -170,25 +177,36 @@ class Lib:
     def tile_i8_weight_glu(self, W, Wt, N, K):
         self.call("ns2_tile_i8_weight_glu", _ptr(W), _ptr(Wt), N, K)
 
-    def linear_i8_glu_rot_tiled(self, At, Wt, scale, Y, M, N, K, *, bias=None, alpha=1.0, act="silu"):
-        self.call("ns2_linear_i8_glu_rot_tiled", _ptr(At), _ptr(Wt), _ptr(scale), _ptr(bias), _ptr(Y), M, N, K,
-                  alpha, ACT[act])
+    # lora = (lora_a fp16 [R, K], lora_b fp16 [N, R], R) selects the *_lora entry point
+    def linear_i8_glu_rot_tiled(self, At, Wt, scale, Y, M, N, K, *, bias=None, alpha=1.0, act="silu", lora=None):
+        args = [_ptr(At), _ptr(Wt), _ptr(scale), _ptr(bias), _ptr(Y), M, N, K, alpha, ACT[act]]
+        self._linear("ns2_linear_i8_glu_rot_tiled", args, lora)
 
     def linear_i8_tiled(self, At, Wt, scale, C, M, N, K, *, bias=None, ldc=None, cOff=0, alpha=1.0,
-                        act="none", resid=False, gate=None, gOff=0):
-        self.call("ns2_linear_i8_tiled", _ptr(At), _ptr(Wt), _ptr(scale), _ptr(bias), _ptr(C), M, N, K,
-                  N if ldc is None else ldc, cOff, alpha, ACT[act], int(resid), _ptr(gate), gOff)
+                        act="none", resid=False, gate=None, gOff=0, lora=None):
+        args = [_ptr(At), _ptr(Wt), _ptr(scale), _ptr(bias), _ptr(C), M, N, K,
+                N if ldc is None else ldc, cOff, alpha, ACT[act], int(resid), _ptr(gate), gOff]
+        self._linear("ns2_linear_i8_tiled", args, lora)
 
     def linear_i8(self, A, a_fmt, lda, W, scale, C, M, N, K, *, bias=None, add=None, ldc=None,
-                  cOff=0, alpha=1.0, act="none", resid=False, gate=None, gOff=0):
-        self.call("ns2_linear_i8", _ptr(A), a_fmt, lda, _ptr(W), _ptr(scale), _ptr(bias), _ptr(add),
-                  _ptr(C), M, N, K, N if ldc is None else ldc, cOff, alpha, ACT[act], int(resid),
-                  _ptr(gate), gOff)
+                  cOff=0, alpha=1.0, act="none", resid=False, gate=None, gOff=0, lora=None):
+        args = [_ptr(A), a_fmt, lda, _ptr(W), _ptr(scale), _ptr(bias), _ptr(add),
+                _ptr(C), M, N, K, N if ldc is None else ldc, cOff, alpha, ACT[act], int(resid),
+                _ptr(gate), gOff]
+        self._linear("ns2_linear_i8", args, lora)
 
     def linear_bf16(self, A, lda, W, C, M, N, K, *, bias=None, add=None, ldc=None, cOff=0,
-                    alpha=1.0, act="none", resid=False, gate=None, gOff=0):
-        self.call("ns2_linear_bf16", _ptr(A), lda, _ptr(W), _ptr(bias), _ptr(add), _ptr(C), M, N, K,
-                  N if ldc is None else ldc, cOff, alpha, ACT[act], int(resid), _ptr(gate), gOff)
+                    alpha=1.0, act="none", resid=False, gate=None, gOff=0, lora=None):
+        args = [_ptr(A), lda, _ptr(W), _ptr(bias), _ptr(add), _ptr(C), M, N, K,
+                N if ldc is None else ldc, cOff, alpha, ACT[act], int(resid), _ptr(gate), gOff]
+        self._linear("ns2_linear_bf16", args, lora)
+
+    def _linear(self, name, args, lora):
+        if lora is None:
+            self.call(name, *args)
+        else:
+            a, b, r = lora
+            self.call(name + "_lora", *args, _ptr(a), _ptr(b), r)
 
     def attention(self, q, k, v, o, *, Lq, Lk, H, D, ldq, ldk, ldv, ldo, qOff=0, kOff=0, vOff=0,
                   oOff=0, batch=1, qBatch=0, kBatch=0, vBatch=0, oBatch=0, scale=None,

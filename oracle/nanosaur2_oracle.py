@@ -119,6 +119,35 @@ def linear_i8(x, q, scale, **epi):
     return linear_epilogue(acc, N=q.shape[0], row_scale=scale.reshape(-1).to(x.dtype), **epi)
 
 
+def lora_delta(x, entries, N):
+    """app/gpu/ops.js:70-87 (loraDelta): D [M, N] = sum_i scale_i * (x A_i^T) B_i^T in output
+    columns [off_i, off_i + n_i); entries are (A [r, K], B [n, r], scale, off, n) over the
+    linear's un-rotated input x (for int8 weights the app feeds the rotated input and rotated A,
+    app/lora.js:61-78, which gives the same product since H is orthogonal)."""
+    D = torch.zeros(x.shape[0], N, dtype=x.dtype)
+    for A, B, scale, off, n in entries:
+        D[:, off:off + n] += scale * ((x @ A.to(x.dtype).T) @ B.to(x.dtype).T)
+    return D
+
+
+def pack_lora(entries, N, K, rotate_a=False):
+    """The stacked side path the *_lora entry points take: lora_a [R, K] (rotated per 256-group
+    for int8 weights) and lora_b [N, R] with each entry's scale folded in and zeros outside its
+    column window; R = the summed ranks rounded up to a multiple of 32. fp64 tensors; the
+    callers round them to fp16."""
+    rs = sum(A.shape[0] for A, *_ in entries)
+    R = (rs + 31) // 32 * 32
+    la = torch.zeros(R, K, dtype=torch.float64)
+    lb = torch.zeros(N, R, dtype=torch.float64)
+    r0 = 0
+    for A, B, scale, off, n in entries:
+        r = A.shape[0]
+        la[r0:r0 + r] = rotate(A.double()) if rotate_a else A.double()
+        lb[off:off + n, r0:r0 + r] = scale * B.double()
+        r0 += r
+    return la, lb, R
+
+
 def bf16_to_float(w_bits: torch.Tensor) -> torch.Tensor:
     """bf16 bit patterns (int16 storage) -> fp32: the pattern is the high half of the fp32
     word (app/gpu/gemm.js:99-100)."""
@@ -465,16 +494,47 @@ class DiT:
         return lin(W, "final_layer.linear", x).T.reshape(CH, h, w)
 
 
+LORA_SUFFIXES = [(".lora_A.weight", "A"), (".lora_B.weight", "B"), (".lora_down.weight", "A"),
+                 (".lora_up.weight", "B"), (".alpha", "alpha")]
+LORA_PREFIXES = ["lora_unet_", "model.diffusion_model.", "diffusion_model.", "lora_te_", "text_encoder."]
+
+
+def lora_deltas(loras, dtype=torch.float32):
+    """tools/reference.py:70-95: module name (dots as underscores) -> [(scale, B, A)] with
+    scale = strength * alpha / r (alpha absent: strength), from PEFT (lora_A/B) or kohya
+    (lora_down/up) keys; `loras` holds (name -> tensor dict, strength) pairs."""
+    out = {}
+    for tensors, strength in loras:
+        groups = {}
+        for k in tensors:
+            for suf, role in LORA_SUFFIXES:
+                if k.endswith(suf):
+                    groups.setdefault(k[: -len(suf)], {})[role] = k
+        for module, ks in groups.items():
+            name = module
+            for p in LORA_PREFIXES:
+                if name.startswith(p):
+                    name = name[len(p):]
+                    break
+            A = tensors[ks["A"]].float().to(dtype)
+            B = tensors[ks["B"]].float().to(dtype)
+            scale = strength * (float(tensors[ks["alpha"]].float().item()) / A.shape[0] if "alpha" in ks else 1.0)
+            out.setdefault(name.replace(".", "_"), []).append((scale, B, A))
+    return out
+
+
 class TensorWeights:
     """Weights from a name -> tensor dict in the reference's on-disk layout: int8 ConvRot
     linears as `<base>.weight` int8 [N,K] + `<base>.weight_scale` fp32 [N,1] (dequantized on
     access like tools/reference.py:54-64), everything else (bf16 bit patterns as int16, or
-    float) converted to `dtype`."""
+    float) converted to `dtype`. LoRAs ((tensor dict, strength) pairs) are merged into the
+    weights they name on access, w + scale * B A, as tools/reference.py:62-64 does."""
 
-    def __init__(self, tensors: dict, dtype=torch.float32):
+    def __init__(self, tensors: dict, dtype=torch.float32, loras=()):
         self.t = tensors
         self.dtype = dtype
         self.cache = {}
+        self.deltas = lora_deltas(loras, dtype)
 
     def has(self, name: str) -> bool:
         return name in self.t
@@ -488,5 +548,8 @@ class TensorWeights:
         else:
             v = self.t[name]
             w = v.float().to(self.dtype)  # bf16 -> fp32 is exact
+        if name.endswith(".weight"):
+            for scale, B, A in self.deltas.get(name[: -len(".weight")].replace(".", "_"), []):
+                w = w + scale * (B @ A)
         self.cache[name] = w
         return w

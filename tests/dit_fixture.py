@@ -106,6 +106,40 @@ def write_inputs(inp, d):
     inp["weights"].astype(np.float32).tofile(os.path.join(d, "weights.f32"))
 
 
+def lora_targets(I=4096):
+    """LoRA test targets: (module, out features, in features, rank, naming). They cover every
+    kind of linear launch of the pass: int8 tiled (qkv_x, kv_y, proj, w3), the fused w12 + GLU +
+    rotation launch, an int8 text-refine linear, and bf16 GEMV / GEMM linears; one module uses
+    kohya naming, the others PEFT naming."""
+    return [
+        ("blocks.0.attn.qkv_x", 3 * D, D, 8, "peft"),
+        ("blocks.0.attn.kv_y", 2 * D, D, 4, "peft"),
+        ("blocks.1.mlp.w12", 2 * I, D, 16, "peft"),
+        ("blocks.2.attn.proj", D, D, 4, "peft"),
+        ("blocks.3.mlp.w3", D, I, 8, "kohya"),
+        ("text_refine_blocks.0.attn.qkv", 3 * D, D, 8, "peft"),
+        ("t_embedder.mlp.0", D, 256, 4, "peft"),
+        ("final_layer.linear", 64, D, 4, "peft"),
+    ]
+
+
+def make_lora(seed=9, I=4096, a_std=0.05, b_std=0.05):
+    """A LoRA file's tensors (bf16 A/B, fp32 alpha = rank / 2) for lora_targets(I), seeded."""
+    rng = np.random.default_rng(seed)
+    out = {}
+    for module, n_out, n_in, r, naming in lora_targets(I):
+        A = torch.from_numpy(rng.standard_normal((r, n_in), dtype=np.float32) * np.float32(a_std)).to(torch.bfloat16)
+        B = torch.from_numpy(rng.standard_normal((n_out, r), dtype=np.float32) * np.float32(b_std)).to(torch.bfloat16)
+        alpha = torch.tensor(r / 2.0, dtype=torch.float32)
+        if naming == "peft":
+            base = "diffusion_model." + module
+            out[base + ".lora_A.weight"], out[base + ".lora_B.weight"], out[base + ".alpha"] = A, B, alpha
+        else:
+            base = "lora_unet_" + module.replace(".", "_")
+            out[base + ".lora_down.weight"], out[base + ".lora_up.weight"], out[base + ".alpha"] = A, B, alpha
+    return out
+
+
 def run_node(args, timeout=600):
     """Run the Node host's run_dit.js; returns its JSON report. Fails loudly on error."""
     cmd = ["node", RUN_DIT, *args]
@@ -116,11 +150,12 @@ def run_node(args, timeout=600):
     return json.loads(p.stdout.strip().splitlines()[-1])
 
 
-def oracle_forward(tensors, inp, path_drop=False, dtype=torch.float32):
-    """x0 [64, h, w] from the oracle's restatement of tools/reference.py DiT.forward."""
+def oracle_forward(tensors, inp, path_drop=False, dtype=torch.float32, loras=()):
+    """x0 [64, h, w] from the oracle's restatement of tools/reference.py DiT.forward; loras:
+    (LoRA tensor dict, strength) pairs merged into the weights."""
     import oracle.nanosaur2_oracle as O
 
-    W = O.TensorWeights(tensors, dtype)
+    W = O.TensorWeights(tensors, dtype, loras)
     dit = O.DiT(W)
     with torch.no_grad():
         return dit.forward(torch.from_numpy(inp["latent"]).to(dtype), inp["sigma"],

@@ -56,6 +56,29 @@ def save_weights(tensors, path):
     save_file(tensors, path)
 
 
+def te_lora_targets():
+    """(module, out, in, rank): a LoRA on a slice of the stacked q/k/v weight (k_proj), on a
+    slice of the stacked gate/up weight (up_proj) and on a whole weight (o_proj)."""
+    return [("layers.1.self_attn.k_proj", 256, 640, 8), ("layers.6.mlp.up_proj", 2048, 640, 16),
+            ("layers.16.self_attn.o_proj", 640, 1024, 4)]
+
+
+def make_te_lora(seed=12, a_std=0.05, b_std=0.05):
+    """A text-encoder LoRA file's tensors with PEFT names under "text_encoder.model." (the
+    prefix both loaders strip, tools/reference.py:74, app/lora.js:18), bf16 A/B and fp32
+    alpha = rank."""
+    rng = np.random.default_rng(seed)
+    out = {}
+    for module, n_out, n_in, r in te_lora_targets():
+        base = "text_encoder.model." + module
+        out[base + ".lora_A.weight"] = torch.from_numpy(
+            rng.standard_normal((r, n_in), dtype=np.float32) * np.float32(a_std)).to(torch.bfloat16)
+        out[base + ".lora_B.weight"] = torch.from_numpy(
+            rng.standard_normal((n_out, r), dtype=np.float32) * np.float32(b_std)).to(torch.bfloat16)
+        out[base + ".alpha"] = torch.tensor(float(r), dtype=torch.float32)
+    return out
+
+
 def make_ids(n, vocab=64, seed=11):
     return [int(x) for x in np.random.default_rng(seed).integers(0, vocab, size=n)]
 

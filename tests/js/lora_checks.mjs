@@ -1,0 +1,43 @@
+// CPU-only checks of the Node host's LoRA module (lora.js): the rotation of the down-projections,
+// fp16 rounding, the stacked side path, key inspection and the loader's name matching against
+// fake registries. Reads a JSON job file, prints one JSON object for tests/test_lora_host.py.
+import fs from "fs";
+import path from "path";
+import { fileURLToPath, pathToFileURL } from "url";
+
+const here = path.dirname(fileURLToPath(import.meta.url));
+const js = path.resolve(here, "..", "..", "nanosaur2-web_amd", "js");
+const mod = (f) => import(pathToFileURL(path.join(js, f)).href);
+
+async function main() {
+  const job = JSON.parse(fs.readFileSync(process.argv[2], "utf8"));
+  const L = await mod("lora.js");
+  const out = {};
+  const h = Float32Array.from(job.hadamard.data);
+  L.hadamardRows(h, job.hadamard.rows, job.hadamard.K);
+  out.hadamard = Array.from(h);
+  out.f16 = Array.from(L.f32ToF16Bits(Float32Array.from(job.f16)));
+  const W = { name: "w", N: job.N, K: job.K, lora: job.entries.map((e) => ({ ...e, A: Float32Array.from(e.A), B: Float32Array.from(e.B) })) };
+  const s = L.stackLora(W);
+  out.stack = { R: s.R, a: Array.from(s.a), b: Array.from(s.b) };
+  out.inspect = job.keys.map((ks) => L.inspectLoraKeys(ks));
+  // loaders against fake registries built from { name, kind, N, K } linears (and stacked parts)
+  out.loads = [];
+  for (const ld of job.loads) {
+    const model = { layers: ld.linears.map((l) => (l.parts ? { ...l, buf: {} } : { ...l, buf: {} })) };
+    const reg = L.linearRegistry(model);
+    const regs = ld.te ? { te: reg } : { dit: reg };
+    const res = await L.loadLora(ld.file, regs);
+    out.loads.push({
+      matched: res.matched, total: res.total, skipped: res.skipped, unsupported: res.unsupported,
+      modules: res.modules.map((m) => ({ W: m.target.W.name || m.target.W.parts.map((p) => p.name).join("+"),
+        off: m.target.off, n: m.target.n, r: m.r, alphaScale: m.alphaScale, A: Array.from(m.A.slice(0, 512)) })),
+    });
+  }
+  process.stdout.write(JSON.stringify(out) + "\n");
+}
+
+main().catch((e) => {
+  process.stderr.write(String(e && e.stack ? e.stack : e) + "\n");
+  process.exit(1);
+});
