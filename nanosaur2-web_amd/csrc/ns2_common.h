@@ -294,36 +294,45 @@ __device__ __forceinline__ void vm_wait() {
 }
 
 // ---- LoRA side path (app/gpu/ops.js:70-87: y = W x + sum_i s_i B_i (A_i x)) ----------------
-// The low-rank term of one 32x32 output tile, D[m][n] = sum_k t[m][k] lb[n][k] over k < R
-// (R % 16 == 0), as v_mfma_f32_32x32x16_f16 products: lane l supplies row `mrow` of t (fp32
-// [M][R], the down-projected input, rounded to fp16) and row `nrow` of lb (fp16 [N][R], the
-// up-projections with their strengths, stacked along R), k = 16s + 8(l/32) .. +7. The caller
-// passes the rows of its lane (l % 32 of the tile), clamped into the matrices.
+// The LoRA term of one 32x32 output tile in the v_mfma_f32_32x32x16_f16 accumulator layout:
+// D[m][n] = sum_k t[m][k] lb[n][k] over k < R (R % 32 == 0), with t fp32 [M][R] (the
+// down-projected input, rounded to fp16 here) and lb fp16 [N][R] (the stacked up-projections).
+// Lane l supplies row `mrow` of t and row `nrow` of lb (rows l % 32 of the tile, clamped into
+// the matrices), k = 16s + 8(l/32) .. +7. The GEMM epilogues add D after the bias, where the
+// reference adds its delta (gemm.js:159-162), one tile at a time so that it costs 16 registers
+// beyond the accumulators. Each 32-wide chunk of R issues its loads before its two products.
 __device__ __forceinline__ float16_t lora_tile(const float* __restrict__ t, const half_t* __restrict__ lb, int R,
                                                int mrow, int nrow, int hi) {
+  const float* tp = t + (long long)mrow * R + 8 * hi;
+  const half_t* bp = lb + (long long)nrow * R + 8 * hi;
   float16_t d;
 #pragma unroll
   for (int r = 0; r < 16; ++r) d[r] = 0.f;
-  const float* tp = t + (long long)mrow * R + 8 * hi;
-  const half_t* bp = lb + (long long)nrow * R + 8 * hi;
-  for (int k = 0; k < R; k += 16) {
-    const float4 x0 = *reinterpret_cast<const float4*>(tp + k);
-    const float4 x1 = *reinterpret_cast<const float4*>(tp + k + 4);
-    const half8_t a = {(half_t)x0.x, (half_t)x0.y, (half_t)x0.z, (half_t)x0.w,
-                       (half_t)x1.x, (half_t)x1.y, (half_t)x1.z, (half_t)x1.w};
-    const half8_t b = *reinterpret_cast<const half8_t*>(bp + k);
-    d = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, d, 0, 0, 0);
+  for (int k0 = 0; k0 < R; k0 += 32) {
+    const float4 x0 = *reinterpret_cast<const float4*>(tp + k0);
+    const float4 x1 = *reinterpret_cast<const float4*>(tp + k0 + 4);
+    const float4 y0 = *reinterpret_cast<const float4*>(tp + k0 + 16);
+    const float4 y1 = *reinterpret_cast<const float4*>(tp + k0 + 20);
+    const half8_t b0 = *reinterpret_cast<const half8_t*>(bp + k0);
+    const half8_t b1 = *reinterpret_cast<const half8_t*>(bp + k0 + 16);
+    const half8_t a0 = {(half_t)x0.x, (half_t)x0.y, (half_t)x0.z, (half_t)x0.w,
+                        (half_t)x1.x, (half_t)x1.y, (half_t)x1.z, (half_t)x1.w};
+    const half8_t a1 = {(half_t)y0.x, (half_t)y0.y, (half_t)y0.z, (half_t)y0.w,
+                        (half_t)y1.x, (half_t)y1.y, (half_t)y1.z, (half_t)y1.w};
+    d = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, b0, d, 0, 0, 0);
+    d = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, b1, d, 0, 0, 0);
   }
   return d;
 }
 
-// Start value of a GEMM accumulator tile that folds the LoRA term into the products: the
-// epilogue computes acc * alpha * rs + bias + ..., so acc starts at D / (alpha * rs) and the
-// result carries D unscaled after bias, where the reference adds it (gemm.js:159-162).
-__device__ __forceinline__ void lora_init(float16_t& acc, const float16_t& d, float alpha_rs) {
-  const float inv = alpha_rs != 0.f ? 1.0f / alpha_rs : 0.f;
-#pragma unroll
-  for (int r = 0; r < 16; ++r) acc[r] = d[r] * inv;
+// The LoRA term of one output element by scalar products (GEMV and split-K reduce paths).
+__device__ __forceinline__ float lora_dot(const float* __restrict__ t, const half_t* __restrict__ lb, int R,
+                                          int m, int n) {
+  const float* tp = t + (long long)m * R;
+  const half_t* bp = lb + (long long)n * R;
+  float d = 0.f;
+  for (int k = 0; k < R; ++k) d += tp[k] * (float)bp[k];
+  return d;
 }
 
 }  // namespace ns2dev

@@ -32,7 +32,7 @@ struct GemmArgs {
   // epilogue); splitk_reduce_kernel adds the splits in z order and applies the epilogue
   float* part;
   int ksteps;
-  // LoRA side path (lora_tile / lora_init): lt fp32 [M][lr], lb fp16 [N][lr]; lr = 0 without
+  // LoRA side path (lora_tile / lora_dot, added after the bias): lt fp32 [M][lr], lb fp16 [N][lr]; lr = 0 without
   const float* lt;
   const half_t* lb;
   int lr;
@@ -44,10 +44,11 @@ constexpr int LROW = BK + LDS_PAD;
 
 // Epilogue of one output element (gemm.js:159-164).
 __device__ __forceinline__ void epilogue_store(const GemmArgs& p, int m, int n, float acc,
-                                               float rs, float bi, float gt) {
+                                               float rs, float bi, float gt, float lora = 0.f) {
   float r = acc * p.alpha;
   r *= rs;
   r += bi;
+  r += lora;  // the LoRA term, where the reference adds its delta (gemm.js:162)
   if (p.add) r += p.add[(long long)m * p.N + n];
   r = apply_act(r, p.act);
   float* c = p.C + p.cOff + (long long)m * p.ldc + n;
@@ -200,21 +201,6 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_kernel(G
   la.load(p, m0, kt0 * BK, tid);
   lw.load(p, n0, kt0 * BK, tid);
   const int lrow = lane & 31, lk = (lane >> 5) * 8;
-  // LoRA: the accumulators start at the low-rank term over alpha * scale (the first split only)
-  if (LORA && blockIdx.z == 0) {
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      int n = n0 + wn * WN + j * 32 + lrow;
-      n = n < p.N ? n : p.N - 1;
-      const float ars = p.alpha * (p.scale ? p.scale[n] : 1.0f);
-#pragma unroll
-      for (int i = 0; i < TM; ++i) {
-        int m = m0 + wm * WM + i * 32 + lrow;
-        m = m < p.M ? m : p.M - 1;
-        lora_init(acc[i][j], lora_tile(p.lt, p.lb, p.lr, m, n, lane >> 5), ars);
-      }
-    }
-  }
   la.store(lds_a[0], tid);
   lw.store(lds_b[0], tid);
   __syncthreads();
@@ -275,10 +261,15 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_kernel(G
     const float gt = p.gate ? p.gate[p.gOff + n] : 1.0f;
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
+      float16_t d;
+      if constexpr (LORA) {
+        const int ml = m0 + wm * WM + i * 32 + lrow;
+        d = lora_tile(p.lt, p.lb, p.lr, ml < p.M ? ml : p.M - 1, n, lane >> 5);
+      }
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int m = m0 + wm * WM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        if (m < p.M) epilogue_store(p, m, n, acc[i][j][r], rs, bi, gt);
+        if (m < p.M) epilogue_store(p, m, n, acc[i][j][r], rs, bi, gt, LORA ? d[r] : 0.f);
       }
     }
   }
@@ -293,7 +284,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs p, int spli
   for (int z = 0; z < splits; ++z) acc += p.part[z * mn + i];
   const int m = (int)(i / p.N), n = (int)(i % p.N);
   epilogue_store(p, m, n, acc, p.scale ? p.scale[n] : 1.0f, p.bias ? p.bias[n] : 0.0f,
-                 p.gate ? p.gate[p.gOff + n] : 1.0f);
+                 p.gate ? p.gate[p.gOff + n] : 1.0f, p.lr ? lora_dot(p.lt, p.lb, p.lr, m, n) : 0.f);
 }
 
 // Small-M path: one wave per output column n, all M (<= 8) rows, fp32 FMA.
@@ -345,24 +336,17 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemmArgs p) {
   const float rs = p.scale ? p.scale[n] : 1.0f;
   const float bi = p.bias ? p.bias[n] : 0.0f;
   const float gt = p.gate ? p.gate[p.gOff + n] : 1.0f;
-  if (p.lr) {
-    // LoRA term over alpha * scale, summed across the lanes with the products
-    const float ars = p.alpha * rs;
-    const float inv = ars != 0.f ? 1.0f / ars : 0.f;
-#pragma unroll
-    for (int m = 0; m < 8; ++m) {
-      if (m < p.M) {
-        float d = 0.f;
-        for (int k = lane; k < p.lr; k += 64) d += p.lt[(long long)m * p.lr + k] * (float)p.lb[(long long)n * p.lr + k];
-        acc[m] += d * inv;
-      }
-    }
-  }
 #pragma unroll
   for (int m = 0; m < 8; ++m) {
     if (m < p.M) {
       const float s = wave_sum(acc[m]);
-      if (lane == 0) epilogue_store(p, m, n, s, rs, bi, gt);
+      // LoRA term: the lanes split the rank
+      float d = 0.f;
+      if (p.lr) {
+        for (int k = lane; k < p.lr; k += 64) d += p.lt[(long long)m * p.lr + k] * (float)p.lb[(long long)n * p.lr + k];
+        d = wave_sum(d);
+      }
+      if (lane == 0) epilogue_store(p, m, n, s, rs, bi, gt, d);
     }
   }
 }
@@ -403,22 +387,36 @@ __global__ __launch_bounds__(64 * lora_waves<RT>()) void lora_down_kernel(const 
   for (int j = 0; j < RT; ++j)
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[j][r] = 0.f;
-  for (int k = 16 * wave + 8 * hi; k < K; k += 16 * kLoraWaves) {
-    half8_t a;
-    if constexpr (XFMT == 0) {
-      const float* xp = static_cast<const float*>(x) + (long long)m * ldx + k;
-      const float4 u = *reinterpret_cast<const float4*>(xp);
-      const float4 v = *reinterpret_cast<const float4*>(xp + 4);
-      a = half8_t{(half_t)u.x, (half_t)u.y, (half_t)u.z, (half_t)u.w, (half_t)v.x, (half_t)v.y, (half_t)v.z, (half_t)v.w};
-    } else if constexpr (XFMT == 1) {
-      a = *reinterpret_cast<const half8_t*>(static_cast<const half_t*>(x) + (long long)m * ldx + k);
-    } else {
-      a = *reinterpret_cast<const half8_t*>(static_cast<const half_t*>(x) + tiled_off(m, k, K));
+  // k-steps of 16 (k = 16 s + 8 hi), s = wave + kLoraWaves * j; batches of NB steps issue all
+  // their loads (from clamped addresses; steps past K are zeroed) before their products
+  constexpr int NB = RT <= 2 ? 6 : (RT <= 4 ? 3 : 2);
+  const int steps = K / 16;
+  const int mine = steps > wave ? (steps - wave + kLoraWaves - 1) / kLoraWaves : 0;
+  for (int j0 = 0; j0 < mine; j0 += NB) {
+    half8_t a[NB], b[NB][RT];
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+      const int sidx = wave + kLoraWaves * (j0 + u);
+      const int k = (sidx < steps ? sidx : steps - 1) * 16 + 8 * hi;
+      if constexpr (XFMT == 0) {
+        const float* xp = static_cast<const float*>(x) + (long long)m * ldx + k;
+        const float4 u0 = *reinterpret_cast<const float4*>(xp);
+        const float4 u1 = *reinterpret_cast<const float4*>(xp + 4);
+        a[u] = half8_t{(half_t)u0.x, (half_t)u0.y, (half_t)u0.z, (half_t)u0.w,
+                       (half_t)u1.x, (half_t)u1.y, (half_t)u1.z, (half_t)u1.w};
+      } else if constexpr (XFMT == 1) {
+        a[u] = *reinterpret_cast<const half8_t*>(static_cast<const half_t*>(x) + (long long)m * ldx + k);
+      } else {
+        a[u] = *reinterpret_cast<const half8_t*>(static_cast<const half_t*>(x) + tiled_off(m, k, K));
+      }
+#pragma unroll
+      for (int j = 0; j < RT; ++j) b[u][j] = *reinterpret_cast<const half8_t*>(A + (long long)(32 * j + lq) * K + k);
     }
 #pragma unroll
-    for (int j = 0; j < RT; ++j) {
-      const half8_t b = *reinterpret_cast<const half8_t*>(A + (long long)(32 * j + lq) * K + k);
-      acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc[j], 0, 0, 0);
+    for (int u = 0; u < NB; ++u) {
+      if (j0 + u >= mine) a[u] = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+      for (int j = 0; j < RT; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[u], b[u][j], acc[j], 0, 0, 0);
     }
   }
   if (wave > 0) {

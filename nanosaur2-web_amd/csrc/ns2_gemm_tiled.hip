@@ -110,7 +110,8 @@ __device__ __forceinline__ void load_old(const TGemmArgs& p, float (&cold)[TM][T
 // element one multiply-add of its row offset and the arithmetic, with the row check only in
 // tiles that cross M. RM 0 stores, RM 1 adds, RM 2 adds gate times the result
 // (gemm.js:159-164); old outputs come from cold when PRE_C, else they are loaded here in a batch.
-template <int TM, int TN, int ACT, int RM, bool PRE_C, int CI, int CJ>
+// LORA: the low-rank term of each tile (lora_tile) is added after the bias.
+template <int TM, int TN, int ACT, int RM, bool PRE_C, bool LORA, int CI, int CJ>
 __device__ __forceinline__ void store_plain(const TGemmArgs& p, const float16_t (&acc)[TM][TN],
                                             const float (&cold)[CI][CJ][16], int mb, int nb, bool full, int lq) {
 #pragma unroll
@@ -123,6 +124,12 @@ __device__ __forceinline__ void store_plain(const TGemmArgs& p, const float16_t 
     float* cj = p.C + p.cOff + (long long)mb * p.ldc + n;
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
+      float16_t d;
+      if constexpr (LORA) {
+        const int hi = (mb & 4) ? 1 : 0;  // mb = the wave's first row + 4 hi (rows are 32-aligned)
+        const int m = mb - 4 * hi + 32 * i + lq;
+        d = lora_tile(p.lt, p.lb, p.lr, m < p.M ? m : p.M - 1, n, hi);
+      }
       float old[16];
       if (RM != 0) {
 #pragma unroll
@@ -139,6 +146,7 @@ __device__ __forceinline__ void store_plain(const TGemmArgs& p, const float16_t 
         float v = acc[i][j][r] * p.alpha;
         v *= rs;
         v += bi;
+        if constexpr (LORA) v += d[r];
         v = act_t<ACT>(v);
         if (RM == 1) v = old[r] + v;
         if (RM == 2) v = old[r] + gt * v;
@@ -157,8 +165,20 @@ __device__ __forceinline__ void store_plain(const TGemmArgs& p, const float16_t 
 // (ns2_tile_i8_weight_glu), so the 64 columns of a wave hold 32 columns of each GLU half; the
 // block's 512 columns give 256 consecutive outputs act(h1) * h2, one rotation group, which is
 // rotated and written to Y as the tiled fp16 operand of the next int8 linear.
+// Waves per SIMD that a launch with the LoRA term keeps: the occupancy of the plain kernel of
+// the same shape (left free, the compiler spends a few more registers on the LoRA variants and
+// they lose a resident block: 128 -> 140 for the GLU launch).
+template <int BM, int BN, int RM, bool LORA>
+constexpr int lora_waves_per_eu() {
+  if (!LORA) return 1;
+  if (BM == 64 && BN == 512) return 4;
+  if (BM == 64 && BN == 128) return RM ? 4 : 5;
+  return 1;
+}
+
 template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int EPI, int ACT, int RM, bool LORA>
-__global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void gemm_tiled_kernel(TGemmArgs p) {
+__global__ __launch_bounds__(WAVES_M * WAVES_N * 64) __attribute__((amdgpu_waves_per_eu(lora_waves_per_eu<BM, BN, RM, LORA>())))
+void gemm_tiled_kernel(TGemmArgs p) {
   constexpr int NW = WAVES_M * WAVES_N;
   constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
   constexpr int TM = WTM / 32, TN = WTN / 32;
@@ -236,26 +256,6 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void gemm_tiled_kernel(TGem
   dma(0, 0);
   if (STAGES == 3 && kblocks > 1) dma(1, 1);
 
-  // LoRA: the accumulators start at the low-rank term over alpha * scale (its loads overlap the
-  // first copies). GLU launches: column j = 0 of a wave is output G of the first half, j = 1
-  // output I + G of the second (the interleave of ns2_tile_i8_weight_glu).
-  if constexpr (LORA) {
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      int n;
-      if constexpr (EPI == 1) n = (j == 0 ? 0 : p.N / 2) + n0 / 2 + 32 * wn + lq;
-      else n = n0 + wn * WTN + 32 * j + lq;
-      n = n < p.N ? n : p.N - 1;
-      const float ars = p.alpha * p.scale[n];
-#pragma unroll
-      for (int i = 0; i < TM; ++i) {
-        int m = m0 + wm * WTM + 32 * i + lq;
-        m = m < p.M ? m : p.M - 1;
-        lora_init(acc[i][j], lora_tile(p.lt, p.lb, p.lr, m, n, hi), ars);
-      }
-    }
-  }
-
   // fragments of k-step s (16 k) of a stage: A rows wm*WTM + 32i + lq, k 16s + 8hi .. +7 (chunk
   // 2s + hi); W columns wn*WTN + 32j + lq, the same k (8-byte chunk 2s + hi)
   auto read_a = [&](int st, int s, int i) {
@@ -328,19 +328,45 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void gemm_tiled_kernel(TGem
     __syncthreads();  // every wave is done with the LDS stages
     float* T = reinterpret_cast<float*>(&ws[0][0]);  // [64 rows][256 columns] fp32 = the W stages
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+    for (int i = 0; i < TM; ++i) {
+      if constexpr (LORA) {
+        // the low-rank terms of the two halves' tiles (weight rows G and I + G), one tile at a
+        // time: act(h1) goes through T, then h2 multiplies it in place
+        int m = m0 + 32 * i + lq;
+        m = m < p.M ? m : p.M - 1;
+        const float16_t d1 = lora_tile(p.lt, p.lb, p.lr, m, G, hi);
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = 32 * i + 8 * (r >> 2) + 4 * hi + (r & 3);
-        // the linear's epilogue order (no activation there), then the GLU
-        float h1 = acc[i][0][r] * p.alpha;
-        h1 *= s1;
-        h1 += b1;
-        float h2 = acc[i][1][r] * p.alpha;
-        h2 *= s2;
-        h2 += b2;
-        T[row * 256 + gc] = act_t<ACT>(h1) * h2;
+        for (int r = 0; r < 16; ++r) {
+          const int row = 32 * i + 8 * (r >> 2) + 4 * hi + (r & 3);
+          float h1 = acc[i][0][r] * p.alpha;
+          h1 *= s1;
+          h1 += b1;
+          T[row * 256 + gc] = act_t<ACT>(h1 + d1[r]);
+        }
+        const float16_t d2 = lora_tile(p.lt, p.lb, p.lr, m, I + G, hi);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = 32 * i + 8 * (r >> 2) + 4 * hi + (r & 3);
+          float h2 = acc[i][1][r] * p.alpha;
+          h2 *= s2;
+          h2 += b2;
+          T[row * 256 + gc] *= h2 + d2[r];
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = 32 * i + 8 * (r >> 2) + 4 * hi + (r & 3);
+          // the linear's epilogue order (no activation there), then the GLU
+          float h1 = acc[i][0][r] * p.alpha;
+          h1 *= s1;
+          h1 += b1;
+          float h2 = acc[i][1][r] * p.alpha;
+          h2 *= s2;
+          h2 += b2;
+          T[row * 256 + gc] = act_t<ACT>(h1) * h2;
+        }
       }
+    }
     __syncthreads();
     // rotation: wave w rotates rows 8w .. 8w+7, the fp16 result in place at the row's start
 #pragma unroll
@@ -363,7 +389,7 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void gemm_tiled_kernel(TGem
     }
     return;
   }
-  store_plain<TM, TN, ACT, RM, PRE_C>(p, acc, cold, m0 + wm * WTM + 4 * hi, n0 + wn * WTN, m0 + BM <= p.M, lq);
+  store_plain<TM, TN, ACT, RM, PRE_C, LORA>(p, acc, cold, m0 + wm * WTM + 4 * hi, n0 + wn * WTN, m0 + BM <= p.M, lq);
 }
 
 // W [N, K] row-major int8 -> Wt tiles [N/64][K/64][8 k-chunks of 8][64 rows][8 bytes] of biased
@@ -396,10 +422,15 @@ int launch_tiled(TGemmArgs p) {
   const dim3 grid(p.tiles_m * p.tiles_n), block(WM * WN * 64);
   hipStream_t s = ns2::stream();
   const int rm = !p.resid ? 0 : (p.gate ? 2 : 1);
-#define NS2_TILED(A, R)                                                              \
-  do {                                                                               \
-    if (p.lr) gemm_tiled_kernel<BM, BN, WM, WN, STAGES, EPI, A, R, true><<<grid, block, 0, s>>>(p);  \
-    else gemm_tiled_kernel<BM, BN, WM, WN, STAGES, EPI, A, R, false><<<grid, block, 0, s>>>(p);      \
+#define NS2_TILED(A, R)                                                                               \
+  do {                                                                                                \
+    if constexpr (BM * BN < 256 * 256) {                                                              \
+      if (p.lr) {                                                                                     \
+        gemm_tiled_kernel<BM, BN, WM, WN, STAGES, EPI, A, R, true><<<grid, block, 0, s>>>(p);         \
+        break;                                                                                        \
+      }                                                                                               \
+    }                                                                                                 \
+    gemm_tiled_kernel<BM, BN, WM, WN, STAGES, EPI, A, R, false><<<grid, block, 0, s>>>(p);            \
   } while (0)
   if constexpr (EPI == 1) {
     if (p.act == NS2_ACT_SILU) NS2_TILED(NS2_ACT_SILU, 0);
@@ -543,7 +574,10 @@ int ns2_linear_i8_tiled_lora(const uint16_t* At, const int8_t* Wt, const float* 
     p.lr = lora_r;
   }
   ns2::ProfScope prof_("gemm_i8_tiled");
-  switch (pick_config(M, N)) {
+  // the 256x256 tiles (16 waves, 128 registers each) have no room for the LoRA term's registers
+  int cfg = pick_config(M, N);
+  if (lora_r && cfg == 0) cfg = 1;
+  switch (cfg) {
     case 0: return launch_tiled<256, 256, 4, 4>(p);
     case 1: return launch_tiled<64, 128, 1, 4>(p);
     default: return launch_tiled<64, 64, 2, 2>(p);
