@@ -38,6 +38,11 @@ struct TGemmArgs {
   const float* lt;
   const half_t* lb;
   int lr;
+  // split-K (plain epilogue only): block (tile, z) sums k-tiles [z * ksplit, (z + 1) * ksplit)
+  // into part[z] ([M, N] fp32, no epilogue); tiled_splitk_reduce_kernel adds the splits in z
+  // order and applies the epilogue. part = nullptr: no split.
+  float* part;
+  int ksplit;
 };
 
 // 8 biased bytes (two dwords) -> 8 halfs: byte u -> half(0x6400 | u) - 1152 = u - 128 = w.
@@ -201,7 +206,10 @@ void gemm_tiled_kernel(TGemmArgs p) {
   block_tile(p, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
 
-  const int kblocks = p.K / 64;
+  // k-tiles of this block: all of K, or split z = blockIdx.y's range
+  const int kt0 = p.part ? (int)blockIdx.y * p.ksplit : 0;
+  const int kblocks = p.part ? (p.K / 64 - kt0 < p.ksplit ? p.K / 64 - kt0 : p.ksplit) : p.K / 64;
+  const int kall = p.K / 64;
   // Stage image: A blocks (8 k-chunks of 1 KB per 64-row block), then W blocks (4 per 64-row
   // block). Block ids past the last real 64-row block re-read the last one (their rows are
   // dropped). The per-wave sources and destinations are fixed up front; a k-tile adds its offset.
@@ -217,7 +225,7 @@ void gemm_tiled_kernel(TGemmArgs p) {
         const int mbi = j / 8, c = j % 8;
         int mb = m0 / 64 + mbi;
         mb = mb < p.mblocks ? mb : p.mblocks - 1;
-        g_src[i] = reinterpret_cast<const char*>(p.At) + ((long long)mb * kblocks * 8 + c) * 1024;
+        g_src[i] = reinterpret_cast<const char*>(p.At) + ((long long)mb * kall * 8 + (long long)kt0 * 8 + c) * 1024;
         l_dst[i] = as_base + j * 1024;
         g_step[i] = 8 * 1024;
         l_step[i] = BM * 64 * 2;
@@ -226,7 +234,7 @@ void gemm_tiled_kernel(TGemmArgs p) {
         const int nbi = jw / 4, c = jw % 4;
         int nb = n0 / 64 + nbi;
         nb = nb < p.nblocks ? nb : p.nblocks - 1;
-        g_src[i] = reinterpret_cast<const char*>(p.Wt) + ((long long)nb * kblocks * 4 + c) * 1024;
+        g_src[i] = reinterpret_cast<const char*>(p.Wt) + ((long long)nb * kall * 4 + (long long)kt0 * 4 + c) * 1024;
         l_dst[i] = ws_base + jw * 1024;
         g_step[i] = 4 * 1024;
         l_step[i] = BN * 64;
@@ -251,7 +259,9 @@ void gemm_tiled_kernel(TGemmArgs p) {
   // latency hides behind it, instead of in the epilogue.
   constexpr bool PRE_C = EPI == 0 && RM != 0 && TM * TN * 16 <= 32;
   float cold[PRE_C ? TM : 1][PRE_C ? TN : 1][16];
-  if constexpr (PRE_C) load_old<TM, TN>(p, cold, m0 + wm * WTM + 4 * hi, n0 + wn * WTN, lq);
+  if constexpr (PRE_C) {
+    if (!p.part) load_old<TM, TN>(p, cold, m0 + wm * WTM + 4 * hi, n0 + wn * WTN, lq);
+  }
 
   dma(0, 0);
   if (STAGES == 3 && kblocks > 1) dma(1, 1);
@@ -389,7 +399,46 @@ void gemm_tiled_kernel(TGemmArgs p) {
     }
     return;
   }
+  if (p.part) {
+    // split-K: the raw partial products of split blockIdx.y
+    float* part = p.part + (long long)blockIdx.y * p.M * p.N;
+    const int mb = m0 + wm * WTM + 4 * hi, nb = n0 + wn * WTN;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int n = nb + 32 * j + lq;
+      if (n >= p.N) continue;
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int m = mb + 32 * i + 8 * (r >> 2) + (r & 3);
+          if (m < p.M) part[(long long)m * p.N + n] = acc[i][j][r];
+        }
+    }
+    return;
+  }
   store_plain<TM, TN, ACT, RM, PRE_C, LORA>(p, acc, cold, m0 + wm * WTM + 4 * hi, n0 + wn * WTN, m0 + BM <= p.M, lq);
+}
+
+// The splits of a split-K launch summed in z order (deterministic), then the plain epilogue of
+// store_plain (scale, bias, the LoRA term, activation, store / += / += gate times).
+__global__ __launch_bounds__(256) void tiled_splitk_reduce_kernel(TGemmArgs p, int splits) {
+  const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
+  const long long mn = (long long)p.M * p.N;
+  if (idx >= mn) return;
+  float acc = 0.f;
+  for (int z = 0; z < splits; ++z) acc += p.part[z * mn + idx];
+  const int m = (int)(idx / p.N), n = (int)(idx % p.N);
+  float v = acc * p.alpha;
+  v *= p.scale[n];
+  v += p.bias ? p.bias[n] : 0.0f;
+  if (p.lr) v += lora_dot(p.lt, p.lb, p.lr, m, n);
+  if (p.act == NS2_ACT_SILU) v = silu(v);
+  else if (p.act == NS2_ACT_GELU_TANH) v = gelu_tanh(v);
+  float* c = p.C + p.cOff + (long long)m * p.ldc + n;
+  if (!p.resid) *c = v;
+  else if (!p.gate) *c = *c + v;
+  else *c = *c + p.gate[p.gOff + n] * v;
 }
 
 // W [N, K] row-major int8 -> Wt tiles [N/64][K/64][8 k-chunks of 8][64 rows][8 bytes] of biased
@@ -416,10 +465,10 @@ __global__ __launch_bounds__(256) void tile_w_kernel(const int8_t* __restrict__ 
 }
 
 template <int BM, int BN, int WM, int WN, int STAGES = 2, int EPI = 0>
-int launch_tiled(TGemmArgs p) {
+int launch_tiled(TGemmArgs p, int splits = 1) {
   p.tiles_m = (p.M + BM - 1) / BM;
   p.tiles_n = (p.N + BN - 1) / BN;
-  const dim3 grid(p.tiles_m * p.tiles_n), block(WM * WN * 64);
+  const dim3 grid(p.tiles_m * p.tiles_n, splits), block(WM * WN * 64);
   hipStream_t s = ns2::stream();
   const int rm = !p.resid ? 0 : (p.gate ? 2 : 1);
 #define NS2_TILED(A, R)                                                                               \
@@ -451,6 +500,11 @@ int launch_tiled(TGemmArgs p) {
   }
 #undef NS2_TILED
   NS2_LAUNCHED("gemm_tiled");
+  if (p.part) {
+    const long long mn = (long long)p.M * p.N;
+    tiled_splitk_reduce_kernel<<<(unsigned)((mn + 255) / 256), 256, 0, s>>>(p, splits);
+    NS2_LAUNCHED("gemm_tiled_splitk_reduce");
+  }
   return NS2_OK;
 }
 
@@ -577,10 +631,29 @@ int ns2_linear_i8_tiled_lora(const uint16_t* At, const int8_t* Wt, const float* 
   // the 256x256 tiles (16 waves, 128 registers each) have no room for the LoRA term's registers
   int cfg = pick_config(M, N);
   if (lora_r && cfg == 0) cfg = 1;
+  // Few rows (the 256 text tokens): when the tiles leave CUs idle, split K over blockIdx.y (at
+  // least 4 k-tiles per split, at most 8 splits) and reduce in a second launch.
+  int splits = 1;
+  if (cfg != 0) {
+    const int bm = 64, bn = cfg == 1 ? 128 : 64;
+    const long long tiles = (long long)((M + bm - 1) / bm) * ((N + bn - 1) / bn);
+    const int kt = K / 64;
+    if (tiles < kCUs && kt >= 8) {
+      splits = (int)((2 * kCUs + tiles - 1) / tiles);
+      if (splits > kt / 4) splits = kt / 4;
+      if (splits > 8) splits = 8;
+    }
+    if (splits > 1) {
+      p.ksplit = (kt + splits - 1) / splits;
+      splits = (kt + p.ksplit - 1) / p.ksplit;
+      p.part = static_cast<float*>(ns2::workspace(5, (size_t)splits * M * N * sizeof(float)));
+      if (!p.part) return ns2::set_error(NS2_ERR_OOM, "ns2_linear_i8_tiled: split-K workspace allocation failed");
+    }
+  }
   switch (cfg) {
     case 0: return launch_tiled<256, 256, 4, 4>(p);
-    case 1: return launch_tiled<64, 128, 1, 4>(p);
-    default: return launch_tiled<64, 64, 2, 2>(p);
+    case 1: return launch_tiled<64, 128, 1, 4>(p, splits);
+    default: return launch_tiled<64, 64, 2, 2>(p, splits);
   }
 }
 
