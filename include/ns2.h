@@ -248,6 +248,10 @@ int ns2_accumulate(float* y, const float* a, long long n);
  * mod, offset)` once per block) batched over blocks: y[r, i] = a[i] + b[r, i] for r < rows,
  * i < n. Additive to the reference interface (one launch instead of one per block). */
 int ns2_add_rows(const float* a, const float* b, float* y, int rows, int n);
+/* y[c, r] = x[r, c], fp32 [rows, cols] -> [cols, rows]: the latent <-> token layout change
+ * around a pass that the reference's forward does on the host (app/models/nanosaur2.js:220-221,
+ * 254-255). Additive to the reference interface. */
+int ns2_transpose(const float* x, float* y, int rows, int cols);
 /* ops.rowSum (app/gpu/ops.js:151-156, kernels.js:362-376): y[n] = scale*sum_r w[r] x[r, n]. */
 int ns2_row_sum(const float* x, const float* w, float* y, int rows, int N, float scale);
 /* ops.rmsnorm (app/gpu/ops.js:111-117, kernels.js:60-80): y = x * rsqrt(mean x^2 + eps) * w. */

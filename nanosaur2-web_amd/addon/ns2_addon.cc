@@ -594,6 +594,16 @@ napi_value Rmsnorm(napi_env env, napi_callback_info info) {
   return check(env, c, ns2_rmsnorm(x, w, y, rows, cols, eps));
 }
 
+// transpose(x, y, rows, cols)
+napi_value Transpose(napi_env env, napi_callback_info info) {
+  ARGS(4);
+  auto x = (const float*)c.ptr(0);
+  auto y = (float*)c.ptr(1);
+  int rows = c.i32(2), cols = c.i32(3);
+  if (c.failed) return nullptr;
+  return check(env, c, ns2_transpose(x, y, rows, cols));
+}
+
 // addRmsnorm(x, a, wAdd, wOut, y, rows, cols, eps)
 napi_value AddRmsnorm(napi_env env, napi_callback_info info) {
   ARGS(8);
@@ -626,7 +636,7 @@ napi_value Module(napi_env env, napi_value exports) {
       {"headNorm", HeadNorm}, {"normMod", NormModT<false>}, {"normModRotateF16", NormModT<true>},
       {"glu", GluT<false>}, {"gluRotateF16", GluT<true>}, {"elementwise", Elementwise},
       {"accumulate", Accumulate}, {"addRows", AddRows}, {"rowSum", RowSum}, {"rmsnorm", Rmsnorm},
-      {"addRmsnorm", AddRmsnorm},
+      {"addRmsnorm", AddRmsnorm}, {"transpose", Transpose},
   };
   for (const Fn& f : fns) {
     napi_value fn;

@@ -287,6 +287,26 @@ __global__ __launch_bounds__(256) void add_rows_kernel(const float* __restrict__
   if (i < total) y[i] = a[i % n] + b[i];
 }
 
+// y[c][r] = x[r][c] for an fp32 [rows, cols] matrix: 64x64 tiles through LDS (one padding
+// column against bank conflicts), 256 threads, coalesced reads and writes.
+__global__ __launch_bounds__(256) void transpose_kernel(const float* __restrict__ x, float* __restrict__ y,
+                                                        int rows, int cols) {
+  __shared__ float tile[64][65];
+  const int r0 = blockIdx.y * 64, c0 = blockIdx.x * 64;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const int r = r0 + ty + 4 * k, c = c0 + tx;
+    if (r < rows && c < cols) tile[ty + 4 * k][tx] = x[(long long)r * cols + c];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const int c = c0 + ty + 4 * k, r = r0 + tx;
+    if (c < cols && r < rows) y[(long long)c * rows + r] = tile[tx][ty + 4 * k];
+  }
+}
+
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ x,
                                                        const float* __restrict__ w,
                                                        float* __restrict__ y, int cols,
@@ -451,6 +471,16 @@ int ns2_add_rows(const float* a, const float* b, float* y, int rows, int n) {
   ns2::ProfScope prof_("add_rows");
   add_rows_kernel<<<blocks_for(total, 256), 256, 0, ns2::stream()>>>(a, b, y, total, n);
   NS2_LAUNCHED("add_rows");
+  return NS2_OK;
+}
+
+int ns2_transpose(const float* x, float* y, int rows, int cols) {
+  NS2_READY();
+  if (rows <= 0 || cols <= 0) return NS2_OK;
+  NS2_REQUIRE(x && y && x != y, "ns2_transpose: null or aliased buffers");
+  ns2::ProfScope prof_("transpose");
+  transpose_kernel<<<dim3((cols + 63) / 64, (rows + 63) / 64), 256, 0, ns2::stream()>>>(x, y, rows, cols);
+  NS2_LAUNCHED("transpose");
   return NS2_OK;
 }
 

@@ -130,6 +130,15 @@ export function rmsnorm(gpu, x, weight, cols, eps = 1e-6, out) {
   return y;
 }
 
+// [rows, cols] -> [cols, rows] (the latent <-> token layout change of the reference's forward,
+// app/models/nanosaur2.js:220-221, 254-255, on the device; addition to the reference ops).
+export function transpose(gpu, x) {
+  const [rows, cols] = x.shape;
+  const y = gpu.empty([cols, rows]);
+  gpu.run("transpose", 0, () => native.transpose(addr(x), addr(y), rows, cols));
+  return y;
+}
+
 // x += rmsnorm(a) * wAdd; returns rmsnorm(x) * wOut (or null without wOut): a sandwich norm,
 // its residual add and the following norm in one launch (app/models/gemma3.js:76-80, 87-88;
 // addition to the reference ops).

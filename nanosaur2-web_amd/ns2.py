@@ -79,6 +79,7 @@ SIGNATURES = {
     "ns2_row_sum": [c_vp, c_vp, c_vp, c_int, c_int, c_float],
     "ns2_rmsnorm": [c_vp, c_vp, c_vp, c_int, c_int, c_float],
     "ns2_add_rmsnorm": [c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_float],
+    "ns2_transpose": [c_vp, c_vp, c_int, c_int],
 }
 _RESTYPES = {"ns2_last_error": ctypes.c_char_p, "ns2_get_stream": c_vp, "ns2_pool_round": c_size}
 
@@ -254,6 +255,9 @@ class Lib:
 
     def rmsnorm(self, x, w, y, rows, cols, eps=1e-6):
         self.call("ns2_rmsnorm", _ptr(x), _ptr(w), _ptr(y), rows, cols, eps)
+
+    def transpose(self, x, y, rows, cols):
+        self.call("ns2_transpose", _ptr(x), _ptr(y), rows, cols)
 
     def add_rmsnorm(self, x, a, w_add, w_out, y, rows, cols, eps=1e-6):
         self.call("ns2_add_rmsnorm", _ptr(x), _ptr(a), _ptr(w_add), _ptr(w_out), _ptr(y), rows, cols, eps)

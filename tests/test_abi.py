@@ -86,7 +86,7 @@ def test_addon_exports_and_errors(host):
     want = {"init", "malloc", "free", "h2d", "d2h", "sync", "poolGet", "poolPut", "poolTrim", "poolRound",
             "linearI8", "linearBf16", "attention", "headNorm", "normMod", "normModRotateF16", "glu",
             "gluRotateF16", "hadamard256", "rotateF16", "elementwise", "accumulate", "rowSum", "rmsnorm",
-            "addRows", "attentionRows", "addRmsnorm",
+            "addRows", "attentionRows", "addRmsnorm", "transpose",
             "eventCreate", "eventRecord", "eventElapsed", "profileEnable", "profileReport"}
     assert want <= set(out["addonExports"])
     assert out["initError"] and "device" in out["initError"]

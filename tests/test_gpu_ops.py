@@ -634,6 +634,16 @@ def test_add_rmsnorm(ns2lib, with_out):
         assert_close(y.cpu(), O.rms_norm(xr, wo.double()), TOL_F32, "add_rmsnorm y")
 
 
+@pytest.mark.parametrize("rows,cols", [(64, 3952), (3952, 64), (37, 100), (1, 5)])
+def test_transpose(ns2lib, rows, cols):
+    """The latent <-> token layout change of forward() (exact)."""
+    x = torch.randn(rows, cols, generator=gen(rows * cols))
+    y = torch.empty(cols, rows, device=dev)
+    ns2lib.transpose(x.to(dev), y, rows, cols)
+    torch.cuda.synchronize()
+    assert torch.equal(y.cpu(), x.t().contiguous())
+
+
 def test_fill_and_errors(ns2lib):
     import ns2
 
