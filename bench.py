@@ -49,10 +49,10 @@ H_IMG, W_IMG, T_TXT, D, HEADS, HD, I_MLP, BLOCKS = 76, 52, 256, 1536, 16, 96, 40
 # counter reads for a copy kernel of known size (FETCH_SIZE x 2.0, WRITE_SIZE x 1.0), measured on
 # the current kernels (profiles/): the mean over the pass's 89 tiled-GEMM launches, and one flash
 # launch at the joint shape. Beside each, the algorithmic bytes of the same launches.
-GEMM_TRAFFIC_BYTES_PER_LAUNCH = 147.0e6
+GEMM_TRAFFIC_BYTES_PER_LAUNCH = 148.2e6
 GEMM_ALGORITHMIC_BYTES_PER_LAUNCH = 67.5e6   # N*K int8 W + 2*M*K fp16 A + output (+ old output for +=)
-ATTN_TRAFFIC_BYTES_PER_LAUNCH = 126.2e6
-ATTN_ALGORITHMIC_BYTES_PER_LAUNCH = 125.7e6  # fp16 Q, K, V^T + fp32 O
+ATTN_TRAFFIC_BYTES_PER_LAUNCH = 173.9e6
+ATTN_ALGORITHMIC_BYTES_PER_LAUNCH = 149.1e6  # fp32 Q (read in the kernel's prologue), fp16 K, V^T, fp32 O
 
 
 def log(msg):
