@@ -248,16 +248,24 @@ __global__ __launch_bounds__(256) void attn_pack_vec_kernel(PackArgs a) {
   const long long tiles = a.Lk_pad / KB;
   const bool kv = row0 < a.Lk_pad;  // uniform per block
 
-  // V gathers first: they do not depend on the Q/K work
+  // V gathers first: they do not depend on the Q/K work. Keys past Lk read the last key (the
+  // loads stay unconditional and issue back to back) and are zeroed afterwards.
   const int kc = tid >> 5, dg = tid & 31;
   float vv[8][DPL];
   if (kv) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const int key = row0 + vkey_pos(kc * 8 + e);
-      const float* src = a.v + a.vOff + b * a.vBatch + (long long)key * a.ldv + (long long)h * D + dg * DPL;
+      const int kr = key < a.Lk ? key : a.Lk - 1;
+      const float* src = a.v + a.vOff + b * a.vBatch + (long long)kr * a.ldv + (long long)h * D + dg * DPL;
 #pragma unroll
-      for (int j = 0; j < DPL; ++j) vv[e][j] = key < a.Lk ? src[j] : 0.f;
+      for (int j = 0; j < DPL; ++j) vv[e][j] = src[j];
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int key = row0 + vkey_pos(kc * 8 + e);
+#pragma unroll
+      for (int j = 0; j < DPL; ++j) vv[e][j] = key < a.Lk ? vv[e][j] : 0.f;
     }
   }
 
@@ -847,10 +855,13 @@ __global__ __launch_bounds__(1024) void attn_rows_kernel(RowsArgs a) {
   const float* qr = a.q + a.qOff + (long long)i * a.ldq + (long long)h * a.D;
   const float* kb = a.k + a.kOff + (long long)g * a.D;
   const float* vb = a.v + a.vOff + (long long)g * a.D;
+  // lanes past D read element D - 1 (unconditional loads) with q = 0; their outputs are not stored
   float qv[DV], ov[DV];
+  int dc[DV];
 #pragma unroll
   for (int j = 0; j < DV; ++j) {
-    qv[j] = d0 + j < a.D ? qr[d0 + j] * a.scale : 0.f;
+    dc[j] = d0 + j < a.D ? d0 + j : a.D - 1;
+    qv[j] = d0 + j < a.D ? qr[dc[j]] * a.scale : 0.f;
     ov[j] = 0.f;
   }
   float m = -INFINITY, l = 0.f;
@@ -859,7 +870,7 @@ __global__ __launch_bounds__(1024) void attn_rows_kernel(RowsArgs a) {
     const float* kr = kb + (long long)j * a.ldk;
     float s = 0.f;
 #pragma unroll
-    for (int e = 0; e < DV; ++e) s += d0 + e < a.D ? qv[e] * kr[d0 + e] : 0.f;
+    for (int e = 0; e < DV; ++e) s += qv[e] * kr[dc[e]];
     return s;
   };
   auto accumulate = [&](int j, float s) {
@@ -868,7 +879,7 @@ __global__ __launch_bounds__(1024) void attn_rows_kernel(RowsArgs a) {
     l = l * corr + p;
     const float* vr = vb + (long long)j * a.ldv;
 #pragma unroll
-    for (int e = 0; e < DV; ++e) ov[e] = ov[e] * corr + (d0 + e < a.D ? p * vr[d0 + e] : 0.f);
+    for (int e = 0; e < DV; ++e) ov[e] = ov[e] * corr + p * vr[dc[e]];
     m = mn;
   };
   int j = 0;

@@ -89,14 +89,16 @@ struct ALoader {
       const int c = tid + i * NT;
       const int row = c / CPR, kc = (c % CPR) * KPC;
       const int m = row0 + row, k = k0 + kc;
-      if (m < p.M && k < p.K) {
-        if (A_F32)
-          r[i] = *reinterpret_cast<const uint4*>(static_cast<const float*>(p.A) + (long long)m * p.lda + k);
-        else
-          r[i] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.A) + (long long)m * p.lda + k);
-      } else {
-        r[i] = make_uint4(0, 0, 0, 0);
-      }
+      // unconditional loads from clamped addresses (a load behind a branch costs a wait each),
+      // chunks outside the matrix zeroed afterwards
+      const bool in = m < p.M && k < p.K;
+      const long long off = (long long)(m < p.M ? m : p.M - 1) * p.lda + (k < p.K ? k : 0);
+      if (A_F32)
+        r[i] = *reinterpret_cast<const uint4*>(static_cast<const float*>(p.A) + off);
+      else
+        r[i] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.A) + off);
+      const uint32_t keep = 0u - (uint32_t)in;  // mask, not a branch: a branch would wait for the load
+      r[i].x &= keep; r[i].y &= keep; r[i].z &= keep; r[i].w &= keep;
     }
   }
   __device__ __forceinline__ void store(half_t* lds, int tid) const {
@@ -131,14 +133,14 @@ struct WLoader {
       const int c = tid + i * NT;
       const int row = c / CPR, kc = (c % CPR) * KPC;
       const int n = row0 + row, k = k0 + kc;
-      if (n < p.N && k < p.K) {
-        if (W_BF16)
-          r[i] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.W) + (long long)n * p.K + k);
-        else
-          r[i] = *reinterpret_cast<const uint4*>(static_cast<const int8_t*>(p.W) + (long long)n * p.K + k);
-      } else {
-        r[i] = make_uint4(0, 0, 0, 0);
-      }
+      const bool in = n < p.N && k < p.K;
+      const long long off = (long long)(n < p.N ? n : p.N - 1) * p.K + (k < p.K ? k : 0);
+      if (W_BF16)
+        r[i] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.W) + off);
+      else
+        r[i] = *reinterpret_cast<const uint4*>(static_cast<const int8_t*>(p.W) + off);
+      const uint32_t keep = 0u - (uint32_t)in;  // mask, not a branch: a branch would wait for the load
+      r[i].x &= keep; r[i].y &= keep; r[i].z &= keep; r[i].w &= keep;
     }
   }
   __device__ __forceinline__ void store(half_t* lds, int tid) const {
@@ -298,39 +300,56 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemmArgs p) {
 #pragma unroll
   for (int m = 0; m < 8; ++m) acc[m] = 0.f;
   for (int k = lane * 8; k < p.K; k += 512) {
+    // every load of the step is issued before the first use: W's 8 values and the 8 rows of A
+    // (rows past M repeat the last row, so the loads are unconditional; their sums are not stored)
+    uint4 wq;
+    uint4 ar[8][2];
+    if (W_BF16) {
+      wq = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.W) + (long long)n * p.K + k);
+    } else {
+      const uint2 q = *reinterpret_cast<const uint2*>(static_cast<const int8_t*>(p.W) + (long long)n * p.K + k);
+      wq = make_uint4(q.x, q.y, 0u, 0u);
+    }
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      const int mr = m < p.M ? m : p.M - 1;
+      if (W_BF16) {
+        const float* ap = static_cast<const float*>(p.A) + (long long)mr * p.lda + k;
+        ar[m][0] = *reinterpret_cast<const uint4*>(ap);
+        ar[m][1] = *reinterpret_cast<const uint4*>(ap + 4);
+      } else {
+        ar[m][0] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.A) + (long long)mr * p.lda + k);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
     float w[8];
     if (W_BF16) {
-      const uint4 q = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.W) + (long long)n * p.K + k);
-      const uint32_t qq[4] = {q.x, q.y, q.z, q.w};
+      const uint32_t qq[4] = {wq.x, wq.y, wq.z, wq.w};
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         w[2 * j] = __builtin_bit_cast(float, qq[j] << 16);
         w[2 * j + 1] = __builtin_bit_cast(float, qq[j] & 0xffff0000u);
       }
     } else {
-      const uint2 q = *reinterpret_cast<const uint2*>(static_cast<const int8_t*>(p.W) + (long long)n * p.K + k);
-      const uint32_t qq[2] = {q.x, q.y};
+      const uint32_t qq[2] = {wq.x, wq.y};
 #pragma unroll
       for (int j = 0; j < 8; ++j) w[j] = (float)(int8_t)((qq[j >> 2] >> (8 * (j & 3))) & 0xff);
     }
 #pragma unroll
     for (int m = 0; m < 8; ++m) {
-      if (m < p.M) {
-        float a[8];
-        if (W_BF16) {
-          const float* ap = static_cast<const float*>(p.A) + (long long)m * p.lda + k;
-          const float4 x0 = *reinterpret_cast<const float4*>(ap);
-          const float4 x1 = *reinterpret_cast<const float4*>(ap + 4);
-          a[0] = x0.x; a[1] = x0.y; a[2] = x0.z; a[3] = x0.w;
-          a[4] = x1.x; a[5] = x1.y; a[6] = x1.z; a[7] = x1.w;
-        } else {
-          const half8_t h = *reinterpret_cast<const half8_t*>(static_cast<const uint16_t*>(p.A) + (long long)m * p.lda + k);
+      float a[8];
+      if (W_BF16) {
+        const float4 x0 = __builtin_bit_cast(float4, ar[m][0]);
+        const float4 x1 = __builtin_bit_cast(float4, ar[m][1]);
+        a[0] = x0.x; a[1] = x0.y; a[2] = x0.z; a[3] = x0.w;
+        a[4] = x1.x; a[5] = x1.y; a[6] = x1.z; a[7] = x1.w;
+      } else {
+        const half8_t h = __builtin_bit_cast(half8_t, ar[m][0]);
 #pragma unroll
-          for (int j = 0; j < 8; ++j) a[j] = (float)h[j];
-        }
-#pragma unroll
-        for (int j = 0; j < 8; ++j) acc[m] = fmaf(a[j], w[j], acc[m]);
+        for (int j = 0; j < 8; ++j) a[j] = (float)h[j];
       }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[m] = fmaf(a[j], w[j], acc[m]);
     }
   }
   const float rs = p.scale ? p.scale[n] : 1.0f;

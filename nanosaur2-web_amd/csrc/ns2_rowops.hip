@@ -296,8 +296,9 @@ __global__ __launch_bounds__(256) void transpose_kernel(const float* __restrict_
   const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
 #pragma unroll
   for (int k = 0; k < 16; ++k) {
+    // clamped, unconditional loads; the clamped copies land in tile cells that are not stored
     const int r = r0 + ty + 4 * k, c = c0 + tx;
-    if (r < rows && c < cols) tile[ty + 4 * k][tx] = x[(long long)r * cols + c];
+    tile[ty + 4 * k][tx] = x[(long long)(r < rows ? r : rows - 1) * cols + (c < cols ? c : cols - 1)];
   }
   __syncthreads();
 #pragma unroll
