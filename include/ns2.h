@@ -85,6 +85,19 @@ int ns2_sync(void);
  * ops.zero (app/gpu/ops.js:89-93) is value = 0. */
 int ns2_fill_u32(void* dst, uint32_t value, size_t count);
 
+/* Recorded launch sequences (HIP graphs), the analogue of the reference's command-buffer
+ * batching (app/gpu/device.js:196-215: dispatches recorded into one encoder, submitted on
+ * flush). Launches issued between ns2_graph_begin and ns2_graph_end are recorded, not run;
+ * ns2_graph_launch replays them on the stream with the same buffer addresses. No call inside
+ * a capture may wait for the stream (ns2_h2d, ns2_d2h, ns2_sync fail and void the capture), and
+ * the recorded launches should have run eagerly once with the same shapes, so that no
+ * workspace grows during the capture. While a graph is alive, ns2_pool_trim frees nothing and
+ * replaced workspace buffers are kept until the last ns2_graph_destroy. */
+int ns2_graph_begin(void);
+int ns2_graph_end(void** graph);
+int ns2_graph_launch(void* graph);
+int ns2_graph_destroy(void* graph);
+
 /* Profiler (app/gpu/device.js:234-288): stream-ordered timing events. */
 int ns2_event_create(void** ev);
 int ns2_event_record(void* ev);

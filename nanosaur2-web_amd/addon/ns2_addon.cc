@@ -270,6 +270,33 @@ napi_value Fill(napi_env env, napi_callback_info info) {
   return check(env, c, c.failed ? 0 : ns2_fill_u32(p, v, n));
 }
 
+// graphBegin() / graphEnd() -> BigInt handle / graphLaunch(h) / graphDestroy(h)
+napi_value GraphBegin(napi_env env, napi_callback_info info) {
+  Ctx c{env, nullptr, 0};
+  return check(env, c, ns2_graph_begin());
+}
+
+napi_value GraphEnd(napi_env env, napi_callback_info info) {
+  void* g = nullptr;
+  if (ns2_graph_end(&g) != NS2_OK) {
+    napi_throw_error(env, nullptr, ns2_last_error());
+    return nullptr;
+  }
+  return bigint(env, g);
+}
+
+napi_value GraphLaunch(napi_env env, napi_callback_info info) {
+  ARGS(1);
+  void* g = c.ptr(0);
+  return check(env, c, c.failed ? 0 : ns2_graph_launch(g));
+}
+
+napi_value GraphDestroy(napi_env env, napi_callback_info info) {
+  ARGS(1);
+  void* g = c.ptr(0);
+  return check(env, c, c.failed ? 0 : ns2_graph_destroy(g));
+}
+
 napi_value EventCreate(napi_env env, napi_callback_info info) {
   void* ev = nullptr;
   if (ns2_event_create(&ev) != NS2_OK) {
@@ -627,7 +654,8 @@ napi_value Module(napi_env env, napi_value exports) {
       {"poolRound", PoolRound}, {"poolGet", PoolGet}, {"poolPut", PoolPut}, {"poolTrim", PoolTrim},
       {"poolStats", PoolStats}, {"h2d", H2D}, {"d2h", D2H}, {"sync", Sync}, {"fill", Fill},
       {"eventCreate", EventCreate}, {"eventRecord", EventRecord}, {"eventElapsed", EventElapsed},
-      {"eventDestroy", EventDestroy}, {"profileEnable", ProfileEnable}, {"profileReset", ProfileReset},
+      {"eventDestroy", EventDestroy}, {"graphBegin", GraphBegin}, {"graphEnd", GraphEnd},
+      {"graphLaunch", GraphLaunch}, {"graphDestroy", GraphDestroy}, {"profileEnable", ProfileEnable}, {"profileReset", ProfileReset},
       {"profileReport", ProfileReport}, {"hadamard256", Hadamard256}, {"rotateF16", RotateF16},
       {"tileI8Weight", TileI8Weight}, {"linearI8Tiled", LinearI8Tiled},
       {"tileI8WeightGlu", TileI8WeightGlu}, {"linearI8GluRotTiled", LinearI8GluRotTiled},

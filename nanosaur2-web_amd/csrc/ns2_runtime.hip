@@ -17,6 +17,15 @@ static thread_local char g_error[1024] = "";
 static bool g_init = false;
 static int g_device = 0;
 static hipStream_t g_stream = nullptr;
+static hipStream_t g_own_stream = nullptr;  // the library's stream when the caller sets none
+
+// ---- graph capture state ------------------------------------------------------------------
+// While a capture is open or a recorded graph is alive, device memory that a graph may address
+// is never freed: workspace buffers that grow are retired (freed when the last graph goes) and
+// the pool keeps its cached buffers.
+static bool g_capturing = false;
+static int g_graphs = 0;
+static std::vector<void*> g_retired;
 
 int set_error(int code, const char* fmt, ...) {
   va_list ap;
@@ -50,10 +59,15 @@ void* workspace(int slot, size_t bytes) {
   if (slot < 0 || slot >= kWorkspaceSlots) return nullptr;
   Workspace& w = g_ws[slot];
   if (w.bytes >= bytes && w.ptr) return w.ptr;
-  // the old buffer may still be read by queued kernels: wait before freeing it
   if (w.ptr) {
-    if (hipStreamSynchronize(g_stream) != hipSuccess) return nullptr;
-    if (hipFree(w.ptr) != hipSuccess) return nullptr;
+    if (g_capturing || g_graphs > 0) {
+      // a graph (recorded or being recorded) may address the old buffer
+      g_retired.push_back(w.ptr);
+    } else {
+      // the old buffer may still be read by queued kernels: wait before freeing it
+      if (hipStreamSynchronize(g_stream) != hipSuccess) return nullptr;
+      if (hipFree(w.ptr) != hipSuccess) return nullptr;
+    }
     w.ptr = nullptr;
     w.bytes = 0;
   }
@@ -145,6 +159,10 @@ int ns2_init(int device) {
   NS2_REQUIRE(device >= 0 && device < n, "ns2_init: device %d out of range (%d devices)", device, n);
   NS2_HIP(hipSetDevice(device));
   g_device = device;
+  // launches go to a stream of the library's own (default priority) unless the caller sets
+  // one: the legacy null stream cannot be captured into a graph
+  if (!g_own_stream) NS2_HIP(hipStreamCreate(&g_own_stream));
+  if (!g_stream) g_stream = g_own_stream;
   g_init = true;
   return NS2_OK;
 }
@@ -233,6 +251,7 @@ int ns2_pool_put(void* ptr, size_t rounded) {
 
 int ns2_pool_trim(void) {
   NS2_READY();
+  if (g_capturing || g_graphs > 0) return NS2_OK;  // recorded graphs may address cached buffers
   NS2_HIP(hipStreamSynchronize(g_stream));
   std::lock_guard<std::mutex> lk(g_pool.mu);
   for (auto& kv : g_pool.free_lists) {
@@ -321,6 +340,7 @@ int ns2_event_destroy(void* ev) {
 
 int ns2_profile_enable(int on) {
   NS2_READY();
+  NS2_REQUIRE(!(on && g_capturing), "ns2_profile_enable: a graph capture is open");
   if (!on) {
     int rc = prof_collect();
     if (rc) return rc;
@@ -354,6 +374,71 @@ int ns2_profile_report(char* buf, size_t cap) {
   s += "}";
   NS2_REQUIRE(s.size() < cap, "ns2_profile_report: buffer of %zu bytes too small (%zu needed)", cap, s.size() + 1);
   memcpy(buf, s.c_str(), s.size() + 1);
+  return NS2_OK;
+}
+
+
+// ---- HIP graphs ------------------------------------------------------------------------------
+// The recorded analogue of the reference's command-buffer batching (app/gpu/device.js:196-215):
+// every launch issued between ns2_graph_begin and ns2_graph_end is recorded (not run) and
+// ns2_graph_launch replays the whole sequence with one call.
+
+int ns2_graph_begin(void) {
+  NS2_READY();
+  NS2_REQUIRE(!g_capturing, "ns2_graph_begin: a capture is already open");
+  NS2_REQUIRE(!g_prof_on, "ns2_graph_begin: disable the kernel profiler before capturing");
+  NS2_REQUIRE(g_stream != nullptr, "ns2_graph_begin: the null stream cannot be captured (ns2_set_stream)");
+  NS2_HIP(hipStreamBeginCapture(g_stream, hipStreamCaptureModeRelaxed));
+  g_capturing = true;
+  return NS2_OK;
+}
+
+int ns2_graph_end(void** graph) {
+  NS2_READY();
+  NS2_REQUIRE(g_capturing, "ns2_graph_end: no capture is open");
+  g_capturing = false;
+  hipGraph_t g = nullptr;
+  const hipError_t e = hipStreamEndCapture(g_stream, &g);
+  if (e != hipSuccess || !g) {
+    (void)hipGetLastError();
+    if (g) (void)hipGraphDestroy(g);
+    return set_error(NS2_ERR_HIP, "ns2_graph_end: the capture failed (%s); calls that wait for the stream "
+                     "(reads, writes, sync) cannot be recorded", hipGetErrorString(e));
+  }
+  hipGraphExec_t x = nullptr;
+  const hipError_t e2 = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(g);
+  if (e2 != hipSuccess) {
+    (void)hipGetLastError();
+    return set_error(NS2_ERR_HIP, "ns2_graph_end: hipGraphInstantiate: %s", hipGetErrorString(e2));
+  }
+  if (!graph) {
+    (void)hipGraphExecDestroy(x);
+    return set_error(NS2_ERR_INVALID, "ns2_graph_end: null out-pointer (the graph was discarded)");
+  }
+  g_graphs++;
+  *graph = (void*)x;
+  return NS2_OK;
+}
+
+int ns2_graph_launch(void* graph) {
+  NS2_READY();
+  NS2_REQUIRE(graph != nullptr, "ns2_graph_launch: null graph");
+  NS2_REQUIRE(!g_capturing, "ns2_graph_launch: a capture is open");
+  NS2_HIP(hipGraphLaunch((hipGraphExec_t)graph, g_stream));
+  return NS2_OK;
+}
+
+int ns2_graph_destroy(void* graph) {
+  NS2_READY();
+  if (!graph) return NS2_OK;
+  NS2_REQUIRE(g_graphs > 0, "ns2_graph_destroy: no live graph");
+  NS2_HIP(hipStreamSynchronize(g_stream));
+  NS2_HIP(hipGraphExecDestroy((hipGraphExec_t)graph));
+  if (--g_graphs == 0 && !g_capturing) {
+    for (void* p : g_retired) NS2_HIP(hipFree(p));
+    g_retired.clear();
+  }
   return NS2_OK;
 }
 

@@ -49,6 +49,9 @@ export function addr(x) {
 
 // app/gpu/device.js:26-57, backed by ns2_pool_* (same bucket rounding).
 class BufferPool {
+  constructor() {
+    this.held = null;
+  }
   static round(bytes) {
     return native.poolRound(bytes);
   }
@@ -57,7 +60,22 @@ class BufferPool {
     return { buf: new DeviceBuffer(ptr, size, true), size };
   }
   put(buf, size) {
-    native.poolPut(buf.ptr, size);
+    if (this.held) this.held.push([buf, size]);
+    else native.poolPut(buf.ptr, size);
+  }
+  // Between holdBegin and holdEnd released buffers are kept out of circulation; holdEnd returns
+  // them ([buf, size] pairs) for putAll.
+  holdBegin() {
+    if (this.held) throw new Error("BufferPool: nested hold");
+    this.held = [];
+  }
+  holdEnd() {
+    const h = this.held || [];
+    this.held = null;
+    return h;
+  }
+  putAll(list) {
+    for (const [buf, size] of list) native.poolPut(buf.ptr, size);
   }
   trim() {
     native.poolTrim();
@@ -120,6 +138,57 @@ export class GPU {
   }
 
   flush() {}
+
+  // Records the launches that fn issues as one HIP graph instead of running them (the
+  // replayable analogue of the reference's command-buffer batching, app/gpu/device.js:196-215).
+  // fn runs twice: eagerly first, with every release held back, so that the pool afterwards has
+  // a free buffer for each tensor fn allocates (and the workspaces their sizes); then under
+  // capture, where it allocates nothing new. fn may not read, write or sync. The tensors fn
+  // releases during the capture are the graph's own scratch: they stay out of the pool until
+  // destroy(), so no live tensor can alias them when the graph is replayed. Returns { result:
+  // fn's recorded return value, launch(), destroy() }; a replay reuses the addresses fn saw,
+  // so the caller keeps fn's inputs and result alive and refills the inputs in place.
+  capture(fn) {
+    if (this.profiler) throw new Error("GPU.capture: turn the per-op profiler off first");
+    this.pool.holdBegin();
+    try {
+      const r = fn();
+      if (r && typeof r.release === "function") r.release();
+    } finally {
+      this.pool.putAll(this.pool.holdEnd());
+    }
+    this.pool.holdBegin();
+    native.graphBegin();
+    let result;
+    try {
+      result = fn();
+    } catch (e) {
+      try { native.graphDestroy(native.graphEnd()); } catch (_) { /* the capture is void anyway */ }
+      this.pool.putAll(this.pool.holdEnd());
+      throw e;
+    }
+    let handle;
+    try {
+      handle = native.graphEnd();
+    } catch (e) {
+      this.pool.putAll(this.pool.holdEnd());
+      throw e;
+    }
+    const scratch = this.pool.holdEnd();
+    return {
+      result,
+      launch: () => {
+        if (handle === null) throw new Error("GPU.capture: launch of a destroyed graph");
+        native.graphLaunch(handle);
+      },
+      destroy: () => {
+        if (handle === null) return;
+        native.graphDestroy(handle);
+        handle = null;
+        this.pool.putAll(scratch);
+      },
+    };
+  }
 
   async sync() {
     native.sync();

@@ -69,8 +69,7 @@ export class Gemma3 {
     const { hidden: D, heads: H, kvHeads: KH, headDim: HD } = GEMMA;
     const Lt = x.shape[0];
     const qkvW = (H + 2 * KH) * HD;
-    const csLocal = ropeTable(gpu, Lt, HD, 1e4);
-    const csGlobal = ropeTable(gpu, Lt, HD, 1e6);
+    const [csLocal, csGlobal] = this.ropeTables(Lt);
     let h = ops.rmsnorm(gpu, x, this.layers[0].inNorm, D);
     this.layers.forEach((l, i) => {
       const cs = l.global ? csGlobal : csLocal;
@@ -97,13 +96,45 @@ export class Gemma3 {
       h = ops.addRmsnorm(gpu, x, d, l.postMlpNorm, next, D);
       d.release();
     });
-    csLocal.release();
-    csGlobal.release();
     x.release();
     return h; // the final norm of the last layer's output
   }
 
+  // The local (theta 1e4) and global (1e6) RoPE tables for L tokens, built once per L (they
+  // depend on L only; keeping them also keeps host uploads out of a captured encode).
+  ropeTables(L) {
+    if (!this.rope) this.rope = new Map();
+    if (!this.rope.has(L)) {
+      const { headDim: HD } = GEMMA;
+      this.rope.set(L, [ropeTable(this.gpu, L, HD, 1e4), ropeTable(this.gpu, L, HD, 1e6)]);
+    }
+    return this.rope.get(L);
+  }
+
+  // One encode of L tokens recorded as a HIP graph. Returns { input [L, 640], output [L, 640],
+  // launch(), destroy() }: write the scaled embeddings into input, launch, then read output.
+  // The graph copies input before the stack (which updates its input in place), so input
+  // survives a replay.
+  captureEncode(L) {
+    const gpu = this.gpu;
+    const input = gpu.empty([L, GEMMA.hidden]);
+    gpu.write(input.buf, new Float32Array(L * GEMMA.hidden));
+    const g = gpu.capture(() => this.encodeEmbedded(ops.elementwise(gpu, "copy", input)));
+    return {
+      input,
+      output: g.result,
+      launch: g.launch,
+      destroy: () => {
+        g.destroy();
+        g.result.release();
+        input.release();
+      },
+    };
+  }
+
   unload() {
+    if (this.rope) for (const ts of this.rope.values()) for (const t of ts) t.release();
+    this.rope = null;
     const seen = new Set();
     const walk = (o) => {
       if (!o || typeof o !== "object" || seen.has(o)) return;

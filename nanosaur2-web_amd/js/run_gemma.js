@@ -3,11 +3,15 @@
 //   node run_gemma.js (--weights FILE.safetensors | --synthetic SEED)
 //                     (--ids FILE.json | --tokens N[,SEED])
 //                     [--out FILE.f32] [--warmup N] [--reps N] [--profile] [--lora FILE[:STRENGTH]]...
+//                     [--graph] [--graph-check N]
 //
 // --ids holds a JSON array of token ids; --tokens draws N seeded ids. --out writes the hidden
 // states [L, 640] as raw fp32. With --reps the encoder is timed on device-resident embeddings
 // (stream events and wall clock); one JSON line with the timings (and the per-op profile with
-// --profile) is printed.
+// --profile) is printed. --graph records one encode as a HIP graph and times (and writes --out
+// from) its replays instead. --graph-check N replays the graph N times, alternating the
+// embeddings of the ids and of a second seeded id set, with an eager encode between replays,
+// and reports each replay's largest difference from the eager encode of the same ids.
 
 import fs from "fs";
 import { GPU } from "./device.js";
@@ -31,6 +35,8 @@ function parseArgs(argv) {
     else if (k === "--warmup") a.warmup = Number(next());
     else if (k === "--reps") a.reps = Number(next());
     else if (k === "--profile") a.profile = true;
+    else if (k === "--graph") a.graph = true;
+    else if (k === "--graph-check") a.graphCheck = Number(next());
     else if (k === "--lora") {
       const m = /^(.*):(-?[\d.]+)$/.exec(next() || "");
       a.loras.push(m ? { file: m[1], strength: Number(m[2]) } : { file: argv[i], strength: 1 });
@@ -75,18 +81,58 @@ async function main() {
   const ids = a.ids || seededIds(a.tokens || [256, 1], vocab);
   const rows = await st.rows("model.embed_tokens.weight", ids);
   const report = { tokens: ids.length, load_ms: Date.now() - t0, device: gpu.info, loras: loraReports };
+  const L = ids.length;
+  const graph = a.graph || a.graphCheck ? te.captureEncode(L) : null;
+  if (graph) report.graph = true;
+  // one graph replay on the embeddings emb (device tensor [L, 640])
+  const replay = (emb) => {
+    ops.elementwise(gpu, "copy", emb, null, graph.input);
+    graph.launch();
+  };
 
   if (a.out) {
-    const h = te.encodeEmbedded(te.embed(rows, ids.length));
-    const out = await gpu.read(h);
-    h.release();
+    let out;
+    if (graph) {
+      const emb = te.embed(rows, L);
+      replay(emb);
+      emb.release();
+      out = await gpu.read(graph.output);
+    } else {
+      const h = te.encodeEmbedded(te.embed(rows, L));
+      out = await gpu.read(h);
+      h.release();
+    }
     fs.writeFileSync(a.out, Buffer.from(out.buffer));
     report.out = a.out;
   }
+  if (a.graphCheck) {
+    const ids2 = seededIds([L, 7], vocab);
+    const embs = [te.embed(rows, L), te.embed(await st.rows("model.embed_tokens.weight", ids2), L)];
+    const eager = async (emb) => {
+      const h = te.encodeEmbedded(ops.elementwise(gpu, "copy", emb));
+      const r = await gpu.read(h);
+      h.release();
+      return r;
+    };
+    const refs = [await eager(embs[0]), await eager(embs[1])];
+    report.graph_check = [];
+    for (let r = 0; r < a.graphCheck; r++) {
+      const which = r % 2;
+      replay(embs[which]);
+      const got = await gpu.read(graph.output);
+      await eager(embs[1 - which]); // eager work between replays, on the same pooled buffers
+      let d = 0;
+      for (let i = 0; i < got.length; i++) d = Math.max(d, Math.abs(got[i] - refs[which][i]));
+      report.graph_check.push({ ids: which, max_abs_diff: d });
+    }
+    for (const e of embs) e.release();
+  }
   if (a.reps > 0) {
-    const emb = te.embed(rows, ids.length);
+    const emb = te.embed(rows, L);
     // each pass starts from a copy of the embeddings (the stack updates its input in place)
-    const pass = () => te.encodeEmbedded(ops.elementwise(gpu, "copy", emb)).release();
+    // (a graph replay leaves its input intact, so the embeddings are copied in once)
+    if (graph) ops.elementwise(gpu, "copy", emb, null, graph.input);
+    const pass = graph ? () => graph.launch() : () => te.encodeEmbedded(ops.elementwise(gpu, "copy", emb)).release();
     for (let i = 0; i < a.warmup; i++) pass();
     await gpu.sync();
     if (gpu.profiler) gpu.profiler.reset();
@@ -113,6 +159,7 @@ async function main() {
     Object.assign(report, { reps: a.reps, warmup: a.warmup, ms_device: dev, ms_wall: wall,
       ms_device_median: median(dev), ms_wall_median: median(wall) });
   }
+  if (graph) graph.destroy();
   if (st.close) st.close();
   te.unload();
   process.stdout.write(JSON.stringify(report) + "\n");

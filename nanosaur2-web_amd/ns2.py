@@ -38,6 +38,10 @@ SIGNATURES = {
     "ns2_d2h": [c_vp, c_vp, c_size],
     "ns2_sync": [],
     "ns2_fill_u32": [c_vp, ctypes.c_uint32, c_size],
+    "ns2_graph_begin": [],
+    "ns2_graph_end": [ctypes.POINTER(c_vp)],
+    "ns2_graph_launch": [c_vp],
+    "ns2_graph_destroy": [c_vp],
     "ns2_event_create": [ctypes.POINTER(c_vp)],
     "ns2_event_record": [c_vp],
     "ns2_event_elapsed": [c_vp, c_vp, ctypes.POINTER(c_float)],
@@ -137,6 +141,21 @@ class Lib:
         cus, hbm = c_int(), c_size()
         self.call("ns2_device_info", name, 256, ctypes.byref(cus), ctypes.byref(hbm))
         return {"name": name.value.decode(), "compute_units": cus.value, "hbm_bytes": hbm.value}
+
+    # recorded launch sequences (HIP graphs) on the library's stream
+    def graph_begin(self):
+        self.call("ns2_graph_begin")
+
+    def graph_end(self) -> int:
+        g = c_vp()
+        self.call("ns2_graph_end", ctypes.byref(g))
+        return g.value
+
+    def graph_launch(self, g):
+        self.call("ns2_graph_launch", g)
+
+    def graph_destroy(self, g):
+        self.call("ns2_graph_destroy", g)
 
     def event(self):
         ev = c_vp()

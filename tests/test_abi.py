@@ -87,7 +87,8 @@ def test_addon_exports_and_errors(host):
             "linearI8", "linearBf16", "attention", "headNorm", "normMod", "normModRotateF16", "glu",
             "gluRotateF16", "hadamard256", "rotateF16", "elementwise", "accumulate", "rowSum", "rmsnorm",
             "addRows", "attentionRows", "addRmsnorm", "transpose",
-            "eventCreate", "eventRecord", "eventElapsed", "profileEnable", "profileReport"}
+            "eventCreate", "eventRecord", "eventElapsed", "profileEnable", "profileReport",
+            "graphBegin", "graphEnd", "graphLaunch", "graphDestroy"}
     assert want <= set(out["addonExports"])
     assert out["initError"] and "device" in out["initError"]
     assert "ns2_init" in out["callError"]

@@ -58,3 +58,33 @@ def test_gemma_encode_full_prompt_matches_oracle(weights_file):
     got = _encode(weights_file, "full", ids)
     ref = G.oracle_encode(tensors, ids, torch.float32)
     assert_close(got, ref, TOL_ENCODE, "gemma encode 256 tokens vs oracle")
+
+
+def test_gemma_graph_replays_match_eager(weights_file):
+    """A recorded encode (HIP graph, GPU.capture) replayed 4 times, alternating two id sets,
+    with an eager encode on the same pooled buffers between replays: every replay equals the
+    eager encode of the same ids bit for bit (same kernels, same inputs, deterministic
+    reductions)."""
+    _, path, d, _ = weights_file
+    ids = G.make_ids(37, seed=45)
+    idf = str(d / "ids_graph.json")
+    with open(idf, "w") as f:
+        json.dump(ids, f)
+    rep = G.run_node(["--weights", path, "--ids", idf, "--graph-check", "4"])
+    checks = rep["graph_check"]
+    assert [c["ids"] for c in checks] == [0, 1, 0, 1]
+    assert all(c["max_abs_diff"] == 0.0 for c in checks), checks
+
+
+def test_gemma_graph_output_matches_golden(weights_file):
+    """--out from a graph replay (GPU.capture) against the reference's own outputs."""
+    _, path, d, z = weights_file
+    ids = [int(i) for i in z["short.ids"]]
+    idf = str(d / "ids_graph_short.json")
+    with open(idf, "w") as f:
+        json.dump(ids, f)
+    out = str(d / "h_graph_short.f32")
+    rep = G.run_node(["--weights", path, "--ids", idf, "--graph", "--out", out])
+    assert rep["graph"] is True
+    got = torch.from_numpy(np.fromfile(out, dtype=np.float32).reshape(len(ids), 640))
+    assert_close(got, torch.from_numpy(z["short.out"]), TOL_ENCODE, "gemma graph replay (short) vs golden")
