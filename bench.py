@@ -20,7 +20,8 @@
    time).
 3. Gemma3-270M text encoder (17 of 18 layers + final norm, 256 token ids, random-init bf16
    weights of the real architecture) through the Node host (run_gemma.js): median device time
-   per encode, with the algorithmic flops of its linears (2*M*N*K) and attention (4*L*L*256*4).
+   per encode, with the algorithmic flops of its linears (2*M*N*K) and attention (4*L*L*256*4);
+   `ms_graph` is the same encode recorded once as a HIP graph and replayed.
 4. CPU baseline: the oracle (a PyTorch-CPU restatement of tools/reference.py) on a bounded
    sample -- one joint block and one image-only block at the full 3952-token shape -- scaled
    to 18 blocks, on this host's cores.
@@ -104,9 +105,9 @@ def gemma_flops(L=GEMMA_TOKENS):
     return GEMMA_LAYERS * per_layer
 
 
-def run_gemma(steps, warmup):
+def run_gemma(steps, warmup, graph=False):
     cmd = ["node", RUN_GEMMA, "--synthetic", "3", "--tokens", f"{GEMMA_TOKENS},1",
-           "--warmup", str(warmup), "--reps", str(steps)]
+           "--warmup", str(warmup), "--reps", str(steps)] + (["--graph"] if graph else [])
     log(" ".join(cmd))
     p = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
     if p.returncode != 0:
@@ -339,7 +340,11 @@ def main():
     gemma = None
     if not args.no_gemma:
         gemma = run_gemma(max(10, args.steps), max(3, args.warmup))
-        log(f"text encoder: {gemma['ms']:.3f} ms per {GEMMA_TOKENS}-token encode, {gemma['tflops']:.1f} TFLOP/s")
+        # the same encode recorded once as a HIP graph and replayed (GPU.capture)
+        replay = run_gemma(max(10, args.steps), max(3, args.warmup), graph=True)
+        gemma["ms_graph"], gemma["ms_graph_wall"] = replay["ms"], replay["ms_wall"]
+        log(f"text encoder: {gemma['ms']:.3f} ms per {GEMMA_TOKENS}-token encode, {gemma['tflops']:.1f} TFLOP/s "
+            f"(graph replay {gemma['ms_graph']:.3f} ms)")
     attn = bench_attention(reps=max(10, args.steps), warmup=max(2, args.warmup))
     if args.copy_calibration:
         attn["copy_calibration"] = copy_calibration()
