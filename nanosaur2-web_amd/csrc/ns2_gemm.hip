@@ -289,21 +289,21 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs p, int spli
                  p.gate ? p.gate[p.gOff + n] : 1.0f, p.lr ? lora_dot(p.lt, p.lb, p.lr, m, n) : 0.f);
 }
 
-// Small-M path: one wave per output column n, all M (<= 8) rows, fp32 FMA.
+// Small-M path: one wave per output column n, all M (<= MR <= 8) rows, fp32 FMA.
 // A: fp32 [M, lda] (bf16 layers) or rotated fp16 [M, lda] (int8 layers).
-template <bool W_BF16>
+template <bool W_BF16, int MR>
 __global__ __launch_bounds__(256) void gemv_kernel(GemmArgs p) {
   const int lane = threadIdx.x & 63;
   const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (n >= p.N) return;
-  float acc[8];
+  float acc[MR];
 #pragma unroll
-  for (int m = 0; m < 8; ++m) acc[m] = 0.f;
+  for (int m = 0; m < MR; ++m) acc[m] = 0.f;
   for (int k = lane * 8; k < p.K; k += 512) {
-    // every load of the step is issued before the first use: W's 8 values and the 8 rows of A
+    // every load of the step is issued before the first use: W's 8 values and the MR rows of A
     // (rows past M repeat the last row, so the loads are unconditional; their sums are not stored)
     uint4 wq;
-    uint4 ar[8][2];
+    uint4 ar[MR][2];
     if (W_BF16) {
       wq = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.W) + (long long)n * p.K + k);
     } else {
@@ -311,7 +311,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemmArgs p) {
       wq = make_uint4(q.x, q.y, 0u, 0u);
     }
 #pragma unroll
-    for (int m = 0; m < 8; ++m) {
+    for (int m = 0; m < MR; ++m) {
       const int mr = m < p.M ? m : p.M - 1;
       if (W_BF16) {
         const float* ap = static_cast<const float*>(p.A) + (long long)mr * p.lda + k;
@@ -336,7 +336,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemmArgs p) {
       for (int j = 0; j < 8; ++j) w[j] = (float)(int8_t)((qq[j >> 2] >> (8 * (j & 3))) & 0xff);
     }
 #pragma unroll
-    for (int m = 0; m < 8; ++m) {
+    for (int m = 0; m < MR; ++m) {
       float a[8];
       if (W_BF16) {
         const float4 x0 = __builtin_bit_cast(float4, ar[m][0]);
@@ -356,7 +356,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemmArgs p) {
   const float bi = p.bias ? p.bias[n] : 0.0f;
   const float gt = p.gate ? p.gate[p.gOff + n] : 1.0f;
 #pragma unroll
-  for (int m = 0; m < 8; ++m) {
+  for (int m = 0; m < MR; ++m) {
     if (m < p.M) {
       const float s = wave_sum(acc[m]);
       // LoRA term: the lanes split the rank
@@ -467,7 +467,12 @@ int launch_gemm(const GemmArgs& p, const char* name) {
   ns2::ProfScope prof_(p.M <= kGemvMaxM ? (W_BF16 ? "gemv_bf16" : "gemv_i8") : (W_BF16 ? "gemm_bf16" : "gemm_i8"));
   const long long big_tiles = (long long)((p.N + 127) / 128) * ((p.M + 127) / 128);
   if (p.M <= kGemvMaxM) {
-    gemv_kernel<W_BF16><<<(p.N + 3) / 4, 256, 0, s>>>(p);
+    // row count rounded up to 1, 2, 4 or 8: no duplicate A loads for the common M = 1
+    const dim3 grid((p.N + 3) / 4);
+    if (p.M == 1) gemv_kernel<W_BF16, 1><<<grid, 256, 0, s>>>(p);
+    else if (p.M == 2) gemv_kernel<W_BF16, 2><<<grid, 256, 0, s>>>(p);
+    else if (p.M <= 4) gemv_kernel<W_BF16, 4><<<grid, 256, 0, s>>>(p);
+    else gemv_kernel<W_BF16, 8><<<grid, 256, 0, s>>>(p);
   } else if (big_tiles >= kSmallGridBlocks) {
     constexpr int BM = 128, BN = 128, WM = 64, WN = 64;
     dim3 grid((p.N + BN - 1) / BN, (p.M + BM - 1) / BM);
