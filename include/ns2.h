@@ -276,6 +276,14 @@ int ns2_rmsnorm(const float* x, const float* w, float* y, int rows, int cols, fl
  * `cols` floats; x, a and y must not alias. Additive to the reference interface. */
 int ns2_add_rmsnorm(float* x, const float* a, const float* w_add, const float* w_out, float* y, int rows,
                     int cols, float eps);
+/* A Gemma3 output projection and the sublayer norms after it, without the [M, N] product in
+ * HBM: t = A W^T (+ bias) (ns2_linear_bf16, gemm.js:98-118), then x += rmsnorm(t) * w_add and,
+ * when y is not null, y = rmsnorm(x) * w_out (ns2_add_rmsnorm; app/models/gemma3.js:72-80 for
+ * the o projection, 83-92 for the down projection). A fp32 [M, lda]; W bf16 [N, K]; x, y fp32
+ * [M, N] contiguous, N <= 1024; x must not alias A or y. Additive to the reference interface. */
+int ns2_linear_bf16_add_rmsnorm(const float* A, int lda, const uint16_t* W, const float* bias, float* x,
+                                const float* w_add, const float* w_out, float* y, int M, int N, int K,
+                                float eps);
 
 #ifdef __cplusplus
 }

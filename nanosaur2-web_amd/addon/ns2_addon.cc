@@ -645,6 +645,23 @@ napi_value AddRmsnorm(napi_env env, napi_callback_info info) {
   return check(env, c, ns2_add_rmsnorm(x, a, wa, wo, y, rows, cols, eps));
 }
 
+// linearBf16AddRmsnorm(A, lda, W, bias, x, wAdd, wOut, y, M, N, K, eps)
+napi_value LinearBf16AddRmsnorm(napi_env env, napi_callback_info info) {
+  ARGS(12);
+  auto A = (const float*)c.ptr(0);
+  int lda = c.i32(1);
+  auto W = (const uint16_t*)c.ptr(2);
+  auto bias = (const float*)c.ptr(3);
+  auto x = (float*)c.ptr(4);
+  auto wa = (const float*)c.ptr(5);
+  auto wo = (const float*)c.ptr(6);
+  auto y = (float*)c.ptr(7);
+  int M = c.i32(8), N = c.i32(9), K = c.i32(10);
+  float eps = c.f32(11);
+  if (c.failed) return nullptr;
+  return check(env, c, ns2_linear_bf16_add_rmsnorm(A, lda, W, bias, x, wa, wo, y, M, N, K, eps));
+}
+
 napi_value Module(napi_env env, napi_value exports) {
   struct Fn {
     const char* name;
@@ -664,7 +681,7 @@ napi_value Module(napi_env env, napi_value exports) {
       {"headNorm", HeadNorm}, {"normMod", NormModT<false>}, {"normModRotateF16", NormModT<true>},
       {"glu", GluT<false>}, {"gluRotateF16", GluT<true>}, {"elementwise", Elementwise},
       {"accumulate", Accumulate}, {"addRows", AddRows}, {"rowSum", RowSum}, {"rmsnorm", Rmsnorm},
-      {"addRmsnorm", AddRmsnorm}, {"transpose", Transpose},
+      {"addRmsnorm", AddRmsnorm}, {"linearBf16AddRmsnorm", LinearBf16AddRmsnorm}, {"transpose", Transpose},
   };
   for (const Fn& f : fns) {
     napi_value fn;

@@ -159,6 +159,18 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// Block-wide sum for blockDim.x == 64 * nwaves (<= 1024); every thread gets the total.
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  v = wave_sum(v);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  __syncthreads();  // red may still be read by a previous call
+  if (lane == 0) red[w] = v;
+  __syncthreads();
+  float t = 0.f;
+  for (int i = 0; i < nw; ++i) t += red[i];
+  return t;
+}
+
 // Stage over lane bits 4-5 (stride 64), with the row swaps. permlane16_swap exchanges the odd
 // 16-lane rows of its first operand with the even rows of its second: on two copies of v (rows
 // r0..r3) it leaves {r0, r0, r2, r2} and {r1, r1, r3, r3}, so every row holds its pair sum T

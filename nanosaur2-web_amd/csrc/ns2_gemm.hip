@@ -289,6 +289,76 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs p, int spli
                  p.gate ? p.gate[p.gOff + n] : 1.0f, p.lr ? lora_dot(p.lt, p.lb, p.lr, m, n) : 0.f);
 }
 
+// Split-K sum of one output row followed by the Gemma3 sublayer norms of that row (one block
+// per row): t = epilogue(sum of the splits), x += rmsnorm(t) * w_add, y = rmsnorm(x) * w_out
+// (y optional). Thread i owns columns i + 256 j (j < kRowNormCols); the splits are read four
+// at a time (16 loads in flight per thread) from clamped addresses and added in split order, as
+// splitk_reduce_kernel adds them.
+constexpr int kRowNormCols = 4;
+constexpr int kRowNormMaxN = 256 * kRowNormCols;
+struct RowNorm {
+  float* x;
+  const float* w_add;
+  const float* w_out;
+  float* y;
+  float eps;
+};
+__global__ __launch_bounds__(256) void splitk_add_rmsnorm_kernel(GemmArgs p, int splits, RowNorm rn) {
+  constexpr int C = kRowNormCols;
+  __shared__ float red[4];
+  const int N = p.N, tid = threadIdx.x;
+  const long long mn = (long long)p.M * N, row = (long long)blockIdx.x * N;
+  int col[C];
+  float acc[C], xv[C];
+#pragma unroll
+  for (int j = 0; j < C; ++j) {
+    const int n = tid + 256 * j;
+    col[j] = n < N ? n : N - 1;
+    acc[j] = 0.f;
+    xv[j] = rn.x[row + col[j]];
+  }
+  for (int z0 = 0; z0 < splits; z0 += 4) {
+    float v[4][C];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const long long zo = (long long)(z0 + k < splits ? z0 + k : splits - 1) * mn + row;
+#pragma unroll
+      for (int j = 0; j < C; ++j) v[k][j] = p.part[zo + col[j]];
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+#pragma unroll
+      for (int j = 0; j < C; ++j)
+        if (z0 + k < splits) acc[j] += v[k][j];
+  }
+  float t[C], ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < C; ++j) {
+    const int n = col[j];
+    float r = acc[j] * p.alpha;
+    if (p.scale) r *= p.scale[n];
+    if (p.bias) r += p.bias[n];
+    t[j] = r;
+    if (tid + 256 * j < N) ss += r * r;
+  }
+  const float r1 = rsqrtf(block_sum(ss, red) / (float)N + rn.eps);
+  float sx = 0.f;
+#pragma unroll
+  for (int j = 0; j < C; ++j) {
+    const float v = xv[j] + t[j] * r1 * rn.w_add[col[j]];
+    t[j] = v;
+    if (tid + 256 * j < N) {
+      rn.x[row + col[j]] = v;
+      sx += v * v;
+    }
+  }
+  if (!rn.y) return;
+  const float r2 = rsqrtf(block_sum(sx, red) / (float)N + rn.eps);
+#pragma unroll
+  for (int j = 0; j < C; ++j)
+    if (tid + 256 * j < N) rn.y[row + col[j]] = t[j] * r2 * rn.w_out[col[j]];
+}
+
 // Small-M path: one wave per output column n, all M (<= MR <= 8) rows, fp32 FMA.
 // A: fp32 [M, lda] (bf16 layers) or rotated fp16 [M, lda] (int8 layers).
 template <bool W_BF16, int MR>
@@ -461,19 +531,22 @@ __global__ __launch_bounds__(64 * lora_waves<RT>()) void lora_down_kernel(const 
 constexpr int kGemvMaxM = 8;
 constexpr long long kSmallGridBlocks = 256;  // one block per CU
 constexpr int kMaxSplits = 16;
+// rn: a row post-op (Gemma3's sublayer norms). It takes the 64x64 split-K path at any M, with
+// the row kernel in place of the split-K reduce (a single split when K is short).
 template <bool A_F32, bool W_BF16>
-int launch_gemm(const GemmArgs& p, const char* name) {
+int launch_gemm(const GemmArgs& p, const char* name, const RowNorm* rn = nullptr) {
   hipStream_t s = ns2::stream();
-  ns2::ProfScope prof_(p.M <= kGemvMaxM ? (W_BF16 ? "gemv_bf16" : "gemv_i8") : (W_BF16 ? "gemm_bf16" : "gemm_i8"));
+  ns2::ProfScope prof_(rn ? "gemm_bf16_add_rmsnorm"
+                          : p.M <= kGemvMaxM ? (W_BF16 ? "gemv_bf16" : "gemv_i8") : (W_BF16 ? "gemm_bf16" : "gemm_i8"));
   const long long big_tiles = (long long)((p.N + 127) / 128) * ((p.M + 127) / 128);
-  if (p.M <= kGemvMaxM) {
+  if (!rn && p.M <= kGemvMaxM) {
     // row count rounded up to 1, 2, 4 or 8: no duplicate A loads for the common M = 1
     const dim3 grid((p.N + 3) / 4);
     if (p.M == 1) gemv_kernel<W_BF16, 1><<<grid, 256, 0, s>>>(p);
     else if (p.M == 2) gemv_kernel<W_BF16, 2><<<grid, 256, 0, s>>>(p);
     else if (p.M <= 4) gemv_kernel<W_BF16, 4><<<grid, 256, 0, s>>>(p);
     else gemv_kernel<W_BF16, 8><<<grid, 256, 0, s>>>(p);
-  } else if (big_tiles >= kSmallGridBlocks) {
+  } else if (!rn && big_tiles >= kSmallGridBlocks) {
     constexpr int BM = 128, BN = 128, WM = 64, WN = 64;
     dim3 grid((p.N + BN - 1) / BN, (p.M + BM - 1) / BM);
     if (p.lr) gemm_mfma_kernel<BM, BN, WM, WN, A_F32, W_BF16, true><<<grid, (BM / WM) * (BN / WN) * 64, 0, s>>>(p);
@@ -487,17 +560,20 @@ int launch_gemm(const GemmArgs& p, const char* name) {
     int splits = (int)(2 * kSmallGridBlocks / tiles);
     if (splits > nk / 4) splits = nk / 4;
     if (splits > kMaxSplits) splits = kMaxSplits;
+    if (splits < 1) splits = 1;
     GemmArgs q = p;
-    if (splits > 1) {
+    if (splits > 1 || rn) {
       q.ksteps = (nk + splits - 1) / splits;
       splits = (nk + q.ksteps - 1) / q.ksteps;
       q.part = static_cast<float*>(ns2::workspace(5, (size_t)splits * p.M * p.N * sizeof(float)));
       if (!q.part) return ns2::set_error(NS2_ERR_OOM, "%s: split-K workspace allocation failed", name);
     }
-    dim3 grid((p.N + BN - 1) / BN, (p.M + BM - 1) / BM, splits > 1 ? splits : 1);
+    dim3 grid((p.N + BN - 1) / BN, (p.M + BM - 1) / BM, splits);
     if (q.lr) gemm_mfma_kernel<BM, BN, WM, WN, A_F32, W_BF16, true><<<grid, (BM / WM) * (BN / WN) * 64, 0, s>>>(q);
     else gemm_mfma_kernel<BM, BN, WM, WN, A_F32, W_BF16, false><<<grid, (BM / WM) * (BN / WN) * 64, 0, s>>>(q);
-    if (splits > 1) {
+    if (rn) {
+      splitk_add_rmsnorm_kernel<<<p.M, 256, 0, s>>>(q, splits, *rn);
+    } else if (splits > 1) {
       const long long mn = (long long)p.M * p.N;
       splitk_reduce_kernel<<<(unsigned)((mn + 255) / 256), 256, 0, s>>>(q, splits);
     }
@@ -614,6 +690,21 @@ int ns2_linear_bf16(const float* A, int lda, const uint16_t* W, const float* bia
                     float alpha, int act, int resid, const float* gate, long long gOff) {
   return ns2_linear_bf16_lora(A, lda, W, bias, add, C, M, N, K, ldc, cOff, alpha, act, resid, gate, gOff,
                               nullptr, nullptr, 0);
+}
+
+int ns2_linear_bf16_add_rmsnorm(const float* A, int lda, const uint16_t* W, const float* bias, float* x,
+                                const float* w_add, const float* w_out, float* y, int M, int N, int K, float eps) {
+  NS2_READY();
+  if (M == 0) return NS2_OK;
+  NS2_REQUIRE(x && w_add && (!y || w_out), "ns2_linear_bf16_add_rmsnorm: null x, w_add or w_out");
+  NS2_REQUIRE(N <= kRowNormMaxN, "ns2_linear_bf16_add_rmsnorm: N=%d exceeds %d", N, kRowNormMaxN);
+  NS2_REQUIRE(y != x && A != x, "ns2_linear_bf16_add_rmsnorm: x must not alias A or y");
+  // C is not written on this path (the row kernel writes x and y); x stands in for the check
+  GemmArgs p{A, W, nullptr, bias, nullptr, x, nullptr, 0, 0, lda, N, M, N, K, 1.0f, NS2_ACT_NONE, 0};
+  int rc = check_common(p, "ns2_linear_bf16_add_rmsnorm");
+  if (rc) return rc;
+  const RowNorm rn{x, w_add, w_out, y, eps};
+  return launch_gemm<true, true>(p, "linear_bf16_add_rmsnorm", &rn);
 }
 
 int ns2_linear_bf16_lora(const float* A, int lda, const uint16_t* W, const float* bias,

@@ -8,18 +8,6 @@ using namespace ns2dev;
 
 namespace {
 
-// Block-wide sum for blockDim.x == 64 * nwaves (<= 1024); every thread gets the total.
-__device__ __forceinline__ float block_sum(float v, float* red) {
-  v = wave_sum(v);
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
-  __syncthreads();  // red may still be read by a previous call
-  if (lane == 0) red[w] = v;
-  __syncthreads();
-  float t = 0.f;
-  for (int i = 0; i < nw; ++i) t += red[i];
-  return t;
-}
-
 // Store 4 consecutive rotated values (k..k+3, k % 4 == 0) as fp16, row-major or tiled.
 __device__ __forceinline__ void store4_f16(uint16_t* __restrict__ y, long long m, int k, int ldy, int K,
                                            int tiled, const float v[4]) {

@@ -63,7 +63,8 @@ export class Gemma3 {
   }
 
   // The layer stack on a device tensor x [L, 640] (released here); returns the normed output.
-  // Each sublayer's post-norm, residual add and the norm after it run as one addRmsnorm.
+  // Each sublayer's output projection, post-norm, residual add and the norm after it run as one
+  // linearAddRmsnorm (a GEMM and a row kernel).
   encodeEmbedded(x) {
     const gpu = this.gpu;
     const { hidden: D, heads: H, kvHeads: KH, headDim: HD } = GEMMA;
@@ -82,19 +83,15 @@ export class Gemma3 {
         qOff: 0, kOff: H * HD, vOff: (H + KH) * HD, group: H / KH, causal: true,
       });
       qkv.release();
-      const o = ops.linear(gpu, a, l.o, { name: "te.o" });
+      const h2 = ops.linearAddRmsnorm(gpu, a, l.o, x, l.postAttnNorm, l.preMlpNorm);
       a.release();
-      const h2 = ops.addRmsnorm(gpu, x, o, l.postAttnNorm, l.preMlpNorm, D);
-      o.release();
       const gu = ops.linear(gpu, h2, l.gateUp, { name: "te.mlp" });
       h2.release();
       const g = ops.glu(gpu, gu, "gelu_tanh");
       gu.release();
-      const d = ops.linear(gpu, g, l.down, { name: "te.mlp" });
-      g.release();
       const next = i + 1 < this.layers.length ? this.layers[i + 1].inNorm : this.norm;
-      h = ops.addRmsnorm(gpu, x, d, l.postMlpNorm, next, D);
-      d.release();
+      h = ops.linearAddRmsnorm(gpu, g, l.down, x, l.postMlpNorm, next);
+      g.release();
     });
     x.release();
     return h; // the final norm of the last layer's output

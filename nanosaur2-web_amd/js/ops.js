@@ -149,6 +149,25 @@ export function addRmsnorm(gpu, x, a, wAdd, wOut, cols, eps = 1e-6) {
   return y;
 }
 
+// linear(a, W) followed by addRmsnorm(x, ., wAdd, wOut) for a bf16 weight without LoRA: the
+// projection's rows are summed and normed in one row kernel, so the [M, N] product never
+// reaches HBM (app/models/gemma3.js:72-80, 83-92; addition to the reference ops). Other weights
+// take the two ops.
+export function linearAddRmsnorm(gpu, a, W, x, wAdd, wOut, eps = 1e-6) {
+  if (W.kind !== "bf16" || (W.lora && W.lora.length) || W.N > 1024) {
+    const t = linear(gpu, a, W, { name: "te.proj" });
+    const y = addRmsnorm(gpu, x, t, wAdd, wOut, W.N, eps);
+    t.release();
+    return y;
+  }
+  const M = a.size / W.K;
+  const y = wOut ? gpu.empty(x.shape) : null;
+  gpu.run("te.proj+norm", 2 * M * W.N * W.K, () =>
+    native.linearBf16AddRmsnorm(addr(a), W.K, addr(W.buf), addr(W.bias || null), addr(x), addr(wAdd), addr(wOut),
+                                addr(y), M, W.N, W.K, eps));
+  return y;
+}
+
 // norm(x) * (1 + mod[scaleOff..]) + mod[shiftOff..]; RMSNorm*weight, or LayerNorm without
 // affine when weight is null (app/gpu/ops.js:119-129).
 export function normMod(gpu, x, mod, shiftOff, scaleOff, cols, weight = null, eps = 1e-6) {

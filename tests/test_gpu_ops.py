@@ -634,6 +634,43 @@ def test_add_rmsnorm(ns2lib, with_out):
         assert_close(y.cpu(), O.rms_norm(xr, wo.double()), TOL_F32, "add_rmsnorm y")
 
 
+@pytest.mark.parametrize("M,K,with_out,bias", [(256, 1024, True, False), (256, 2048, True, True),
+                                               (37, 2048, False, False), (5, 1024, True, True)])
+def test_linear_bf16_add_rmsnorm(ns2lib, M, K, with_out, bias):
+    """Gemma3's output projection and the norms after it in one GEMM + row kernel
+    (app/models/gemma3.js:72-80, 83-92): against the two-launch ns2_linear_bf16 + ns2_add_rmsnorm
+    (bit-exact where both sum K in the same splits, M > 8) and against the oracle (fp16 products,
+    TOL). N = 640; K = 1024 (o) and 2048 (down) give 4 and 8 K splits at 256 rows."""
+    N = 640
+    g = gen(M * K + with_out)
+    a = torch.randn(M, K, generator=g)
+    w = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
+    b = torch.randn(N, generator=g) * 0.1 if bias else None
+    x = torch.randn(M, N, generator=g) * 20
+    wa = torch.randn(N, generator=g) * 0.3 + 1
+    wo = torch.randn(N, generator=g) * 0.3 + 1
+    ad, wd, xd = a.to(dev), w.view(torch.int16).to(dev), x.to(dev)
+    bd, wad, wod = (b.to(dev) if bias else None), wa.to(dev), wo.to(dev)
+    y = torch.empty(M, N, device=dev) if with_out else None
+    ns2lib.linear_bf16_add_rmsnorm(ad, K, wd, bd, xd, wad, wod if with_out else None, y, M, N, K)
+    # two launches: the projection into t, then the sandwich norm
+    t = torch.empty(M, N, device=dev)
+    ns2lib.linear_bf16(ad, K, wd, t, M, N, K, bias=bd)
+    x2 = x.to(dev)
+    y2 = torch.empty(M, N, device=dev) if with_out else None
+    ns2lib.add_rmsnorm(x2, t, wad, wod if with_out else None, y2, M, N)
+    torch.cuda.synchronize()
+    if M > 8:
+        assert torch.equal(xd, x2), "fused x vs two launches"
+        if with_out:
+            assert torch.equal(y, y2), "fused y vs two launches"
+    tr = O.linear_bf16(a.double(), w, bias=b.double() if bias else None)
+    xr = x.double() + O.rms_norm(tr, wa.double())
+    assert_close(xd.cpu(), xr, TOL, "linear_bf16_add_rmsnorm x")
+    if with_out:
+        assert_close(y.cpu(), O.rms_norm(xr, wo.double()), TOL, "linear_bf16_add_rmsnorm y")
+
+
 @pytest.mark.parametrize("rows,cols", [(64, 3952), (3952, 64), (37, 100), (1, 5)])
 def test_transpose(ns2lib, rows, cols):
     """The latent <-> token layout change of forward() (exact)."""
