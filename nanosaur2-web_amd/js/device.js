@@ -157,8 +157,8 @@ export class GPU {
     } finally {
       this.pool.putAll(this.pool.holdEnd());
     }
-    this.pool.holdBegin();
     native.graphBegin();
+    this.pool.holdBegin();
     let result;
     try {
       result = fn();
