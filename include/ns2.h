@@ -235,6 +235,11 @@ int ns2_attention(const float* q, const float* k, const float* v, float* o, int 
  * in place on X[(rowOff + l)*ld + colOff + h*D ..] for l < L, h < H; cs may be NULL. */
 int ns2_head_norm(float* X, const float* w, int L, int H, int D, int ld, long long colOff,
                   long long rowOff, const float* cs, long long sinOff, float eps);
+/* Two ops.headNorm calls on adjacent head ranges of the same rows in one launch: heads
+ * [0, H1) with w1, then heads [H1, H1 + H2) with w2, from colOff on (Gemma3's q and k norms of
+ * the packed q/k/v rows, app/models/gemma3.js:64-67). Additive to the reference interface. */
+int ns2_head_norm2(float* X, const float* w1, int H1, const float* w2, int H2, int L, int D, int ld,
+                   long long colOff, long long rowOff, const float* cs, long long sinOff, float eps);
 /* ops.normMod + normModShader (app/gpu/ops.js:121-129, app/gpu/kernels.js:82-117):
  * y = norm(x) * (1 + mod[scaleOff + c]) + mod[shiftOff + c]; weight != NULL: RMSNorm * w,
  * weight == NULL: LayerNorm without affine. */

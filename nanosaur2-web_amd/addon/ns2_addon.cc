@@ -533,6 +533,22 @@ napi_value HeadNorm(napi_env env, napi_callback_info info) {
   return check(env, c, ns2_head_norm(X, w, L, H, D, ld, colOff, rowOff, cs, sinOff, eps));
 }
 
+// headNorm2(X, w1, H1, w2, H2, L, D, ld, colOff, rowOff, cs, sinOff, eps)
+napi_value HeadNorm2(napi_env env, napi_callback_info info) {
+  ARGS(13);
+  auto X = (float*)c.ptr(0);
+  auto w1 = (const float*)c.ptr(1);
+  int H1 = c.i32(2);
+  auto w2 = (const float*)c.ptr(3);
+  int H2 = c.i32(4), L = c.i32(5), D = c.i32(6), ld = c.i32(7);
+  long long colOff = c.i64(8), rowOff = c.i64(9);
+  auto cs = (const float*)c.ptr(10);
+  long long sinOff = c.i64(11);
+  float eps = c.f32(12);
+  if (c.failed) return nullptr;
+  return check(env, c, ns2_head_norm2(X, w1, H1, w2, H2, L, D, ld, colOff, rowOff, cs, sinOff, eps));
+}
+
 // normMod(x, mod, shiftOff, scaleOff, rows, cols, weight, eps, y) /
 // normModRotateF16(x, mod, shiftOff, scaleOff, rows, cols, weight, eps, y, tiled)
 template <bool ROT>
@@ -678,7 +694,7 @@ napi_value Module(napi_env env, napi_value exports) {
       {"tileI8WeightGlu", TileI8WeightGlu}, {"linearI8GluRotTiled", LinearI8GluRotTiled},
       {"linearI8", LinearI8}, {"linearBf16", LinearBf16}, {"attention", Attention},
       {"attentionRows", AttentionRows},
-      {"headNorm", HeadNorm}, {"normMod", NormModT<false>}, {"normModRotateF16", NormModT<true>},
+      {"headNorm", HeadNorm}, {"headNorm2", HeadNorm2}, {"normMod", NormModT<false>}, {"normModRotateF16", NormModT<true>},
       {"glu", GluT<false>}, {"gluRotateF16", GluT<true>}, {"elementwise", Elementwise},
       {"accumulate", Accumulate}, {"addRows", AddRows}, {"rowSum", RowSum}, {"rmsnorm", Rmsnorm},
       {"addRmsnorm", AddRmsnorm}, {"linearBf16AddRmsnorm", LinearBf16AddRmsnorm}, {"transpose", Transpose},

@@ -165,8 +165,10 @@ void launch_rot_rows(const RotRowsArgs& a, int groups) {
 // ---- headNorm -------------------------------------------------------------------------------
 
 // In-place per-head RMSNorm (+ split-half RoPE), kernels.js:307-342. One wave per (row, head).
+// Heads h < H1 use w, heads h >= H1 use w2 (two adjacent head ranges with their own weights).
 __global__ __launch_bounds__(256) void head_norm_kernel(float* __restrict__ X,
-                                                         const float* __restrict__ w, int L,
+                                                         const float* __restrict__ w1, int H1,
+                                                         const float* __restrict__ w2, int L,
                                                          int H, int D, int ld, long long colOff,
                                                          long long rowOff,
                                                          const float* __restrict__ cs,
@@ -175,6 +177,7 @@ __global__ __launch_bounds__(256) void head_norm_kernel(float* __restrict__ X,
   if (id >= (long long)L * H) return;
   const int lane = threadIdx.x & 63;
   const int l = (int)(id / H), h = (int)(id % H);
+  const float* __restrict__ w = h < H1 ? w1 : w2;
   float* row = X + (rowOff + l) * (long long)ld + colOff + (long long)h * D;
   float ss = 0.f;
   for (int i = lane; i < D; i += 64) ss += row[i] * row[i];
@@ -403,8 +406,21 @@ int ns2_head_norm(float* X, const float* w, int L, int H, int D, int ld, long lo
   if (L <= 0 || H <= 0) return NS2_OK;
   NS2_REQUIRE(X && w && D > 0 && D % 2 == 0, "ns2_head_norm: bad arguments");
   ns2::ProfScope prof_("head_norm");
-  head_norm_kernel<<<blocks_for((long long)L * H, 4), 256, 0, ns2::stream()>>>(X, w, L, H, D, ld, colOff, rowOff, cs, sinOff, eps);
+  head_norm_kernel<<<blocks_for((long long)L * H, 4), 256, 0, ns2::stream()>>>(X, w, H, w, L, H, D, ld, colOff, rowOff, cs, sinOff, eps);
   NS2_LAUNCHED("head_norm");
+  return NS2_OK;
+}
+
+int ns2_head_norm2(float* X, const float* w1, int H1, const float* w2, int H2, int L, int D, int ld,
+                   long long colOff, long long rowOff, const float* cs, long long sinOff, float eps) {
+  NS2_READY();
+  if (L <= 0 || H1 + H2 <= 0) return NS2_OK;
+  NS2_REQUIRE(X && (H1 <= 0 || w1) && (H2 <= 0 || w2) && H1 >= 0 && H2 >= 0 && D > 0 && D % 2 == 0,
+              "ns2_head_norm2: bad arguments");
+  const int H = H1 + H2;
+  ns2::ProfScope prof_("head_norm");
+  head_norm_kernel<<<blocks_for((long long)L * H, 4), 256, 0, ns2::stream()>>>(X, w1, H1, w2, L, H, D, ld, colOff, rowOff, cs, sinOff, eps);
+  NS2_LAUNCHED("head_norm2");
   return NS2_OK;
 }
 

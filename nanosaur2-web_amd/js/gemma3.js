@@ -76,8 +76,8 @@ export class Gemma3 {
       const cs = l.global ? csGlobal : csLocal;
       const qkv = ops.linear(gpu, h, l.qkv, { name: "te.qkv" }); // [Lt, q 1024 | k 256 | v 256]
       h.release();
-      ops.headNorm(gpu, qkv, l.qn, { L: Lt, H, D: HD, ld: qkvW, colOff: 0, cs });
-      ops.headNorm(gpu, qkv, l.kn, { L: Lt, H: KH, D: HD, ld: qkvW, colOff: H * HD, cs });
+      // q heads then the k head: adjacent columns, one launch
+      ops.headNorm2(gpu, qkv, l.qn, H, l.kn, KH, { L: Lt, D: HD, ld: qkvW, colOff: 0, cs });
       const a = ops.attention(gpu, {
         q: qkv, k: qkv, v: qkv, Lq: Lt, Lk: Lt, H, D: HD, ldq: qkvW, ldk: qkvW, ldv: qkvW,
         qOff: 0, kOff: H * HD, vOff: (H + KH) * HD, group: H / KH, causal: true,

@@ -195,6 +195,14 @@ export function headNorm(gpu, X, weight, { L, H, D, ld, colOff = 0, rowOff = 0, 
     native.headNorm(addr(X), addr(weight), L, H, D, ld, colOff, rowOff, cs ? addr(cs) : null, cs ? cs.sinOff : 0, eps));
 }
 
+// headNorm on two adjacent head ranges in one launch: H1 heads with w1 from colOff on, then H2
+// heads with w2 (Gemma3's q and k norms; addition to the reference ops).
+export function headNorm2(gpu, X, w1, H1, w2, H2, { L, D, ld, colOff = 0, rowOff = 0, cs = null, eps = 1e-6 }) {
+  gpu.run(cs ? "head_norm_rope" : "head_norm", 0, () =>
+    native.headNorm2(addr(X), addr(w1), H1, addr(w2), H2, L, D, ld, colOff, rowOff, cs ? addr(cs) : null,
+                     cs ? cs.sinOff : 0, eps));
+}
+
 // [rows, 2I] -> [rows, I]: act(first half) * second half (app/gpu/ops.js:140-148)
 export function glu(gpu, x, act) {
   const I = x.shape[1] / 2;

@@ -73,6 +73,7 @@ SIGNATURES = {
     "ns2_attention_rows": [c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
                            c_ll, c_ll, c_ll, c_int, c_int],
     "ns2_head_norm": [c_vp, c_vp, c_int, c_int, c_int, c_int, c_ll, c_ll, c_vp, c_ll, c_float],
+    "ns2_head_norm2": [c_vp, c_vp, c_int, c_vp, c_int, c_int, c_int, c_int, c_ll, c_ll, c_vp, c_ll, c_float],
     "ns2_norm_mod": [c_vp, c_vp, c_ll, c_ll, c_int, c_int, c_vp, c_float, c_vp],
     "ns2_norm_mod_rotate_f16": [c_vp, c_vp, c_ll, c_ll, c_int, c_int, c_vp, c_float, c_vp, c_int],
     "ns2_glu": [c_vp, c_vp, c_int, c_int, c_int],
@@ -247,6 +248,10 @@ class Lib:
 
     def head_norm(self, X, w, L, H, D, ld, colOff=0, rowOff=0, cs=None, sinOff=0, eps=1e-6):
         self.call("ns2_head_norm", _ptr(X), _ptr(w), L, H, D, ld, colOff, rowOff, _ptr(cs), sinOff, eps)
+
+    def head_norm2(self, X, w1, H1, w2, H2, L, D, ld, colOff=0, rowOff=0, cs=None, sinOff=0, eps=1e-6):
+        self.call("ns2_head_norm2", _ptr(X), _ptr(w1), H1, _ptr(w2), H2, L, D, ld, colOff, rowOff, _ptr(cs),
+                  sinOff, eps)
 
     def norm_mod(self, x, mod, shiftOff, scaleOff, rows, cols, weight, y, eps=1e-6):
         self.call("ns2_norm_mod", _ptr(x), _ptr(mod), shiftOff, scaleOff, rows, cols, _ptr(weight), eps, _ptr(y))

@@ -558,6 +558,29 @@ def test_head_norm(ns2lib):
     assert_close(Xd.cpu(), ref, TOL_F32, "head_norm")
 
 
+def test_head_norm2(ns2lib):
+    """Gemma3's q norms (4 heads of 256) and k norm (1 head) with RoPE in one launch, against
+    two ns2_head_norm calls (bit-exact) and the oracle, on packed q/k/v rows (ld 1536)."""
+    g = gen(52)
+    L, D, ld = 37, 256, 1536
+    X = torch.randn(L, ld, generator=g)
+    wq = torch.randn(D, generator=g)
+    wk = torch.randn(D, generator=g)
+    ang = torch.arange(L, dtype=torch.float64)[:, None] * torch.rand(D // 2, generator=g, dtype=torch.float64)[None]
+    cs = torch.cat([ang.cos().flatten(), ang.sin().flatten()]).float()
+    sin_off = L * D // 2
+    Xd, X2 = X.to(dev), X.to(dev)
+    ns2lib.head_norm2(Xd, wq.to(dev), 4, wk.to(dev), 1, L, D, ld, cs=cs.to(dev), sinOff=sin_off)
+    ns2lib.head_norm(X2, wq.to(dev), L, 4, D, ld, colOff=0, cs=cs.to(dev), sinOff=sin_off)
+    ns2lib.head_norm(X2, wk.to(dev), L, 1, D, ld, colOff=4 * D, cs=cs.to(dev), sinOff=sin_off)
+    torch.cuda.synchronize()
+    assert torch.equal(Xd, X2), "head_norm2 vs two head_norm launches"
+    ref = X.double().clone()
+    O.head_norm_rope(ref, wq.double(), L, 4, D, ld, colOff=0, cs=cs, sinOff=sin_off)
+    O.head_norm_rope(ref, wk.double(), L, 1, D, ld, colOff=4 * D, cs=cs, sinOff=sin_off)
+    assert_close(Xd.cpu(), ref, TOL_F32, "head_norm2")
+
+
 @pytest.mark.parametrize("act", ["silu", "gelu_tanh"])
 def test_glu(ns2lib, act):
     g = gen(61)
