@@ -286,6 +286,12 @@ int ns2_add_rmsnorm(float* x, const float* a, const float* w_add, const float* w
  * when y is not null, y = rmsnorm(x) * w_out (ns2_add_rmsnorm; app/models/gemma3.js:72-80 for
  * the o projection, 83-92 for the down projection). A fp32 [M, lda]; W bf16 [N, K]; x, y fp32
  * [M, N] contiguous, N <= 1024; x must not alias A or y. Additive to the reference interface. */
+/* A gate/up projection and its GLU without the [M, N] product in HBM: t = A W^T (+ bias), then
+ * Y[m][i] = act(t[m][i]) * t[m][N/2 + i] (ns2_linear_bf16 + ns2_glu; the Gemma3 MLP's fused
+ * gate/up weight, app/models/gemma3.js:79-82). W bf16 [N, K] with the gate rows first; Y fp32
+ * [M, N/2]. Additive to the reference interface. */
+int ns2_linear_bf16_glu(const float* A, int lda, const uint16_t* W, const float* bias, float* Y, int M, int N,
+                        int K, int act);
 int ns2_linear_bf16_add_rmsnorm(const float* A, int lda, const uint16_t* W, const float* bias, float* x,
                                 const float* w_add, const float* w_out, float* y, int M, int N, int K,
                                 float eps);

@@ -661,6 +661,19 @@ napi_value AddRmsnorm(napi_env env, napi_callback_info info) {
   return check(env, c, ns2_add_rmsnorm(x, a, wa, wo, y, rows, cols, eps));
 }
 
+// linearBf16Glu(A, lda, W, bias, Y, M, N, K, act)
+napi_value LinearBf16Glu(napi_env env, napi_callback_info info) {
+  ARGS(9);
+  auto A = (const float*)c.ptr(0);
+  int lda = c.i32(1);
+  auto W = (const uint16_t*)c.ptr(2);
+  auto bias = (const float*)c.ptr(3);
+  auto Y = (float*)c.ptr(4);
+  int M = c.i32(5), N = c.i32(6), K = c.i32(7), act = c.i32(8);
+  if (c.failed) return nullptr;
+  return check(env, c, ns2_linear_bf16_glu(A, lda, W, bias, Y, M, N, K, act));
+}
+
 // linearBf16AddRmsnorm(A, lda, W, bias, x, wAdd, wOut, y, M, N, K, eps)
 napi_value LinearBf16AddRmsnorm(napi_env env, napi_callback_info info) {
   ARGS(12);
@@ -697,7 +710,8 @@ napi_value Module(napi_env env, napi_value exports) {
       {"headNorm", HeadNorm}, {"headNorm2", HeadNorm2}, {"normMod", NormModT<false>}, {"normModRotateF16", NormModT<true>},
       {"glu", GluT<false>}, {"gluRotateF16", GluT<true>}, {"elementwise", Elementwise},
       {"accumulate", Accumulate}, {"addRows", AddRows}, {"rowSum", RowSum}, {"rmsnorm", Rmsnorm},
-      {"addRmsnorm", AddRmsnorm}, {"linearBf16AddRmsnorm", LinearBf16AddRmsnorm}, {"transpose", Transpose},
+      {"addRmsnorm", AddRmsnorm}, {"linearBf16AddRmsnorm", LinearBf16AddRmsnorm},
+      {"linearBf16Glu", LinearBf16Glu}, {"transpose", Transpose},
   };
   for (const Fn& f : fns) {
     napi_value fn;

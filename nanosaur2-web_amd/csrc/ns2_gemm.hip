@@ -359,6 +359,33 @@ __global__ __launch_bounds__(256) void splitk_add_rmsnorm_kernel(GemmArgs p, int
     if (tid + 256 * j < N) rn.y[row + col[j]] = t[j] * r2 * rn.w_out[col[j]];
 }
 
+// Split-K sum of a gate/up product followed by the GLU: y[m][i] = act(t[m][i]) * t[m][I + i]
+// with t = epilogue(sum of the splits), N = 2I (gate rows first, as concatLinears stacks them).
+// The splits are added in split order, as splitk_reduce_kernel adds them.
+__global__ __launch_bounds__(256) void splitk_glu_kernel(GemmArgs p, int splits, float* __restrict__ y, int glu_act) {
+  const int I = p.N / 2;
+  const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (long long)p.M * I) return;
+  const long long m = i / I, j = i % I;
+  const long long mn = (long long)p.M * p.N, g0 = m * p.N + j;
+  float g = 0.f, u = 0.f;
+  for (int z = 0; z < splits; ++z) {
+    g += p.part[z * mn + g0];
+    u += p.part[z * mn + g0 + I];
+  }
+  g *= p.alpha;
+  u *= p.alpha;
+  if (p.scale) {
+    g *= p.scale[j];
+    u *= p.scale[j + I];
+  }
+  if (p.bias) {
+    g += p.bias[j];
+    u += p.bias[j + I];
+  }
+  y[i] = apply_act(g, glu_act) * u;
+}
+
 // Small-M path: one wave per output column n, all M (<= MR <= 8) rows, fp32 FMA.
 // A: fp32 [M, lda] (bf16 layers) or rotated fp16 [M, lda] (int8 layers).
 template <bool W_BF16, int MR>
@@ -533,20 +560,23 @@ constexpr long long kSmallGridBlocks = 256;  // one block per CU
 constexpr int kMaxSplits = 16;
 // rn: a row post-op (Gemma3's sublayer norms). It takes the 64x64 split-K path at any M, with
 // the row kernel in place of the split-K reduce (a single split when K is short).
+// glu_y: a GLU post-op (y [M, N/2] = act(gate) * up, act glu_act), on the same split-K path.
 template <bool A_F32, bool W_BF16>
-int launch_gemm(const GemmArgs& p, const char* name, const RowNorm* rn = nullptr) {
+int launch_gemm(const GemmArgs& p, const char* name, const RowNorm* rn = nullptr, float* glu_y = nullptr,
+                int glu_act = 0) {
   hipStream_t s = ns2::stream();
-  ns2::ProfScope prof_(rn ? "gemm_bf16_add_rmsnorm"
+  const bool post = rn || glu_y;
+  ns2::ProfScope prof_(rn ? "gemm_bf16_add_rmsnorm" : glu_y ? "gemm_bf16_glu"
                           : p.M <= kGemvMaxM ? (W_BF16 ? "gemv_bf16" : "gemv_i8") : (W_BF16 ? "gemm_bf16" : "gemm_i8"));
   const long long big_tiles = (long long)((p.N + 127) / 128) * ((p.M + 127) / 128);
-  if (!rn && p.M <= kGemvMaxM) {
+  if (!post && p.M <= kGemvMaxM) {
     // row count rounded up to 1, 2, 4 or 8: no duplicate A loads for the common M = 1
     const dim3 grid((p.N + 3) / 4);
     if (p.M == 1) gemv_kernel<W_BF16, 1><<<grid, 256, 0, s>>>(p);
     else if (p.M == 2) gemv_kernel<W_BF16, 2><<<grid, 256, 0, s>>>(p);
     else if (p.M <= 4) gemv_kernel<W_BF16, 4><<<grid, 256, 0, s>>>(p);
     else gemv_kernel<W_BF16, 8><<<grid, 256, 0, s>>>(p);
-  } else if (!rn && big_tiles >= kSmallGridBlocks) {
+  } else if (!post && big_tiles >= kSmallGridBlocks) {
     constexpr int BM = 128, BN = 128, WM = 64, WN = 64;
     dim3 grid((p.N + BN - 1) / BN, (p.M + BM - 1) / BM);
     if (p.lr) gemm_mfma_kernel<BM, BN, WM, WN, A_F32, W_BF16, true><<<grid, (BM / WM) * (BN / WN) * 64, 0, s>>>(p);
@@ -562,7 +592,7 @@ int launch_gemm(const GemmArgs& p, const char* name, const RowNorm* rn = nullptr
     if (splits > kMaxSplits) splits = kMaxSplits;
     if (splits < 1) splits = 1;
     GemmArgs q = p;
-    if (splits > 1 || rn) {
+    if (splits > 1 || post) {
       q.ksteps = (nk + splits - 1) / splits;
       splits = (nk + q.ksteps - 1) / q.ksteps;
       q.part = static_cast<float*>(ns2::workspace(5, (size_t)splits * p.M * p.N * sizeof(float)));
@@ -573,6 +603,9 @@ int launch_gemm(const GemmArgs& p, const char* name, const RowNorm* rn = nullptr
     else gemm_mfma_kernel<BM, BN, WM, WN, A_F32, W_BF16, false><<<grid, (BM / WM) * (BN / WN) * 64, 0, s>>>(q);
     if (rn) {
       splitk_add_rmsnorm_kernel<<<p.M, 256, 0, s>>>(q, splits, *rn);
+    } else if (glu_y) {
+      const long long n = (long long)p.M * (p.N / 2);
+      splitk_glu_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(q, splits, glu_y, glu_act);
     } else if (splits > 1) {
       const long long mn = (long long)p.M * p.N;
       splitk_reduce_kernel<<<(unsigned)((mn + 255) / 256), 256, 0, s>>>(q, splits);
@@ -705,6 +738,20 @@ int ns2_linear_bf16_add_rmsnorm(const float* A, int lda, const uint16_t* W, cons
   if (rc) return rc;
   const RowNorm rn{x, w_add, w_out, y, eps};
   return launch_gemm<true, true>(p, "linear_bf16_add_rmsnorm", &rn);
+}
+
+int ns2_linear_bf16_glu(const float* A, int lda, const uint16_t* W, const float* bias, float* Y, int M, int N,
+                        int K, int act) {
+  NS2_READY();
+  if (M == 0) return NS2_OK;
+  NS2_REQUIRE(Y && N % 2 == 0, "ns2_linear_bf16_glu: null Y or odd N=%d", N);
+  NS2_REQUIRE(act >= NS2_ACT_NONE && act <= NS2_ACT_GELU_TANH, "ns2_linear_bf16_glu: unknown act %d", act);
+  NS2_REQUIRE(Y != A, "ns2_linear_bf16_glu: Y must not alias A");
+  // C is not written on this path (the GLU kernel writes Y); Y stands in for the check
+  GemmArgs p{A, W, nullptr, bias, nullptr, Y, nullptr, 0, 0, lda, N, M, N, K, 1.0f, NS2_ACT_NONE, 0};
+  int rc = check_common(p, "ns2_linear_bf16_glu");
+  if (rc) return rc;
+  return launch_gemm<true, true>(p, "linear_bf16_glu", nullptr, Y, act);
 }
 
 int ns2_linear_bf16_lora(const float* A, int lda, const uint16_t* W, const float* bias,

@@ -85,10 +85,8 @@ export class Gemma3 {
       qkv.release();
       const h2 = ops.linearAddRmsnorm(gpu, a, l.o, x, l.postAttnNorm, l.preMlpNorm);
       a.release();
-      const gu = ops.linear(gpu, h2, l.gateUp, { name: "te.mlp" });
+      const g = ops.linearGlu(gpu, h2, l.gateUp, "gelu_tanh");
       h2.release();
-      const g = ops.glu(gpu, gu, "gelu_tanh");
-      gu.release();
       const next = i + 1 < this.layers.length ? this.layers[i + 1].inNorm : this.norm;
       h = ops.linearAddRmsnorm(gpu, g, l.down, x, l.postMlpNorm, next);
       g.release();

@@ -149,6 +149,24 @@ export function addRmsnorm(gpu, x, a, wAdd, wOut, cols, eps = 1e-6) {
   return y;
 }
 
+// linear(a, W) followed by glu(., act) for a bf16 gate/up weight without LoRA: the split-K sums
+// feed the GLU directly, so the [M, 2I] product never reaches HBM (app/models/gemma3.js:79-82;
+// addition to the reference ops). Other weights take the two ops.
+export function linearGlu(gpu, a, W, act) {
+  if (W.kind !== "bf16" || (W.lora && W.lora.length)) {
+    const t = linear(gpu, a, W, { name: "te.mlp" });
+    const y = glu(gpu, t, act);
+    t.release();
+    return y;
+  }
+  if (ACT[act] === undefined) throw new Error(`linearGlu: unknown activation ${act}`);
+  const M = a.size / W.K;
+  const y = gpu.empty([M, W.N / 2]);
+  gpu.run("te.mlp+glu", 2 * M * W.N * W.K, () =>
+    native.linearBf16Glu(addr(a), W.K, addr(W.buf), addr(W.bias || null), addr(y), M, W.N, W.K, ACT[act]));
+  return y;
+}
+
 // linear(a, W) followed by addRmsnorm(x, ., wAdd, wOut) for a bf16 weight without LoRA: the
 // projection's rows are summed and normed in one row kernel, so the [M, N] product never
 // reaches HBM (app/models/gemma3.js:72-80, 83-92; addition to the reference ops). Other weights

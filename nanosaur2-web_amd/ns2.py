@@ -85,6 +85,7 @@ SIGNATURES = {
     "ns2_rmsnorm": [c_vp, c_vp, c_vp, c_int, c_int, c_float],
     "ns2_add_rmsnorm": [c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_float],
     "ns2_transpose": [c_vp, c_vp, c_int, c_int],
+    "ns2_linear_bf16_glu": [c_vp, c_int, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int],
     "ns2_linear_bf16_add_rmsnorm": [c_vp, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_float],
 }
 _RESTYPES = {"ns2_last_error": ctypes.c_char_p, "ns2_get_stream": c_vp, "ns2_pool_round": c_size}
@@ -286,6 +287,9 @@ class Lib:
 
     def add_rmsnorm(self, x, a, w_add, w_out, y, rows, cols, eps=1e-6):
         self.call("ns2_add_rmsnorm", _ptr(x), _ptr(a), _ptr(w_add), _ptr(w_out), _ptr(y), rows, cols, eps)
+
+    def linear_bf16_glu(self, A, lda, W, bias, Y, M, N, K, act="gelu_tanh"):
+        self.call("ns2_linear_bf16_glu", _ptr(A), lda, _ptr(W), _ptr(bias), _ptr(Y), M, N, K, ACT[act])
 
     def linear_bf16_add_rmsnorm(self, A, lda, W, bias, x, w_add, w_out, y, M, N, K, eps=1e-6):
         self.call("ns2_linear_bf16_add_rmsnorm", _ptr(A), lda, _ptr(W), _ptr(bias), _ptr(x), _ptr(w_add),

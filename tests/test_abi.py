@@ -88,7 +88,7 @@ def test_addon_exports_and_errors(host):
             "gluRotateF16", "hadamard256", "rotateF16", "elementwise", "accumulate", "rowSum", "rmsnorm",
             "addRows", "attentionRows", "addRmsnorm", "transpose",
             "eventCreate", "eventRecord", "eventElapsed", "profileEnable", "profileReport",
-            "graphBegin", "graphEnd", "graphLaunch", "graphDestroy", "linearBf16AddRmsnorm", "headNorm2"}
+            "graphBegin", "graphEnd", "graphLaunch", "graphDestroy", "linearBf16AddRmsnorm", "headNorm2", "linearBf16Glu"}
     assert want <= set(out["addonExports"])
     assert out["initError"] and "device" in out["initError"]
     assert "ns2_init" in out["callError"]

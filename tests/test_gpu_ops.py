@@ -694,6 +694,31 @@ def test_linear_bf16_add_rmsnorm(ns2lib, M, K, with_out, bias):
         assert_close(y.cpu(), O.rms_norm(xr, wo.double()), TOL, "linear_bf16_add_rmsnorm y")
 
 
+@pytest.mark.parametrize("M,bias", [(256, False), (37, True), (5, False)])
+def test_linear_bf16_glu(ns2lib, M, bias):
+    """Gemma3's gate/up projection and its GELU-tanh gate in one GEMM + GLU launch
+    (app/models/gemma3.js:79-82): against ns2_linear_bf16 + ns2_glu (bit-exact at 256 rows,
+    where both take the same K splits) and against the oracle (TOL). N = 2 x 2048, K = 640."""
+    N, K, I = 4096, 640, 2048
+    g = gen(M + 7 * bias)
+    a = torch.randn(M, K, generator=g)
+    w = (torch.randn(N, K, generator=g) * 0.05).to(torch.bfloat16)
+    b = torch.randn(N, generator=g) * 0.1 if bias else None
+    ad, wd, bd = a.to(dev), w.view(torch.int16).to(dev), (b.to(dev) if bias else None)
+    y = torch.empty(M, I, device=dev)
+    ns2lib.linear_bf16_glu(ad, K, wd, bd, y, M, N, K, "gelu_tanh")
+    t = torch.empty(M, N, device=dev)
+    ns2lib.linear_bf16(ad, K, wd, t, M, N, K, bias=bd)
+    y2 = torch.empty(M, I, device=dev)
+    ns2lib.glu(t, y2, M, I, "gelu_tanh")
+    torch.cuda.synchronize()
+    if M == 256:
+        assert torch.equal(y, y2), "fused GLU vs two launches"
+    tr = O.linear_bf16(a.double(), w, bias=b.double() if bias else None)
+    ref = torch.nn.functional.gelu(tr[:, :I], approximate="tanh") * tr[:, I:]
+    assert_close(y.cpu(), ref, TOL, "linear_bf16_glu")
+
+
 @pytest.mark.parametrize("rows,cols", [(64, 3952), (3952, 64), (37, 100), (1, 5)])
 def test_transpose(ns2lib, rows, cols):
     """The latent <-> token layout change of forward() (exact)."""
