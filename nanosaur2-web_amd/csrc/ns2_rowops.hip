@@ -109,6 +109,23 @@ __global__ __launch_bounds__(512) void rot_rows_kernel(RotRowsArgs a) {
     const float4 in = *reinterpret_cast<const float4*>(src + g * 256);
     v[g][0] = in.x, v[g][1] = in.y, v[g][2] = in.z, v[g][3] = in.w;
   }
+  // modulation of each element, loaded together with the row (unconditional loads; without a
+  // norm weight the scale row stands in for w and is replaced by 1): y = v * r * mul + add
+  float mul[NORM ? G : 1][4], add[NORM ? G : 1][4];
+  if (NORM) {
+    const float* wp = a.w ? a.w : a.mod + a.scaleOff;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const int c = g * 256 + lo;
+      const float4 sc = *reinterpret_cast<const float4*>(a.mod + a.scaleOff + c);
+      const float4 sh = *reinterpret_cast<const float4*>(a.mod + a.shiftOff + c);
+      float4 ww = *reinterpret_cast<const float4*>(wp + c);
+      if (!a.w) ww = make_float4(1.f, 1.f, 1.f, 1.f);
+      mul[g][0] = ww.x * (1.0f + sc.x), mul[g][1] = ww.y * (1.0f + sc.y);
+      mul[g][2] = ww.z * (1.0f + sc.z), mul[g][3] = ww.w * (1.0f + sc.w);
+      add[g][0] = sh.x, add[g][1] = sh.y, add[g][2] = sh.z, add[g][3] = sh.w;
+    }
+  }
   float r = 1.f;
   if (NORM) {
     float mean = 0.f;
@@ -132,15 +149,8 @@ __global__ __launch_bounds__(512) void rot_rows_kernel(RotRowsArgs a) {
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     if (NORM) {
-      const int c = g * 256 + lo;
-      const float4 sc = *reinterpret_cast<const float4*>(a.mod + a.scaleOff + c);
-      const float4 sh = *reinterpret_cast<const float4*>(a.mod + a.shiftOff + c);
-      float4 ww = make_float4(1.f, 1.f, 1.f, 1.f);
-      if (a.w) ww = *reinterpret_cast<const float4*>(a.w + c);
-      v[g][0] = v[g][0] * r * ww.x * (1.0f + sc.x) + sh.x;
-      v[g][1] = v[g][1] * r * ww.y * (1.0f + sc.y) + sh.y;
-      v[g][2] = v[g][2] * r * ww.z * (1.0f + sc.z) + sh.z;
-      v[g][3] = v[g][3] * r * ww.w * (1.0f + sc.w) + sh.w;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[g][j] = v[g][j] * r * mul[g][j] + add[g][j];
     }
     fwht256_mfma(v[g], h);
     store4_f16(a.y, row, g * 256 + lo, a.ldy, cols, a.tiled, v[g]);
