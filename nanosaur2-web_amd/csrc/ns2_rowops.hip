@@ -109,21 +109,23 @@ __global__ __launch_bounds__(512) void rot_rows_kernel(RotRowsArgs a) {
     const float4 in = *reinterpret_cast<const float4*>(src + g * 256);
     v[g][0] = in.x, v[g][1] = in.y, v[g][2] = in.z, v[g][3] = in.w;
   }
-  // modulation of each element, loaded together with the row (unconditional loads; without a
-  // norm weight the scale row stands in for w and is replaced by 1): y = v * r * mul + add
-  float mul[NORM ? G : 1][4], add[NORM ? G : 1][4];
-  if (NORM) {
-    const float* wp = a.w ? a.w : a.mod + a.scaleOff;
+  // modulation of each element: y = ((v * r) * w) * (1 + scale) + shift, the reference's
+  // order (kernels.js:82-117). Up to 8 groups the three vectors are loaded together with the
+  // row (unconditional loads; without a norm weight the scale row stands in for w and is
+  // replaced by 1); above that they are loaded per group in the store loop, which keeps the
+  // wide rows (up to 4096 columns) out of scratch.
+  constexpr bool HOIST = NORM && G <= 8;
+  constexpr int GH = HOIST ? G : 1;
+  float4 wv[GH], sc1[GH], shv[GH];
+  const float* wp = a.w ? a.w : a.mod + a.scaleOff;
+  if (HOIST) {
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
+    for (int g = 0; g < GH; ++g) {
       const int c = g * 256 + lo;
       const float4 sc = *reinterpret_cast<const float4*>(a.mod + a.scaleOff + c);
-      const float4 sh = *reinterpret_cast<const float4*>(a.mod + a.shiftOff + c);
-      float4 ww = *reinterpret_cast<const float4*>(wp + c);
-      if (!a.w) ww = make_float4(1.f, 1.f, 1.f, 1.f);
-      mul[g][0] = ww.x * (1.0f + sc.x), mul[g][1] = ww.y * (1.0f + sc.y);
-      mul[g][2] = ww.z * (1.0f + sc.z), mul[g][3] = ww.w * (1.0f + sc.w);
-      add[g][0] = sh.x, add[g][1] = sh.y, add[g][2] = sh.z, add[g][3] = sh.w;
+      shv[g] = *reinterpret_cast<const float4*>(a.mod + a.shiftOff + c);
+      wv[g] = *reinterpret_cast<const float4*>(wp + c);
+      sc1[g] = make_float4(1.0f + sc.x, 1.0f + sc.y, 1.0f + sc.z, 1.0f + sc.w);
     }
   }
   float r = 1.f;
@@ -149,8 +151,23 @@ __global__ __launch_bounds__(512) void rot_rows_kernel(RotRowsArgs a) {
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     if (NORM) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) v[g][j] = v[g][j] * r * mul[g][j] + add[g][j];
+      float4 ww, s1, sh;
+      if (HOIST) {
+        ww = wv[g], s1 = sc1[g], sh = shv[g];
+      } else {
+        const int c = g * 256 + lo;
+        const float4 sc = *reinterpret_cast<const float4*>(a.mod + a.scaleOff + c);
+        sh = *reinterpret_cast<const float4*>(a.mod + a.shiftOff + c);
+        ww = *reinterpret_cast<const float4*>(wp + c);
+        s1 = make_float4(1.0f + sc.x, 1.0f + sc.y, 1.0f + sc.z, 1.0f + sc.w);
+      }
+      if (a.w) {
+        v[g][0] = v[g][0] * r * ww.x * s1.x + sh.x, v[g][1] = v[g][1] * r * ww.y * s1.y + sh.y;
+        v[g][2] = v[g][2] * r * ww.z * s1.z + sh.z, v[g][3] = v[g][3] * r * ww.w * s1.w + sh.w;
+      } else {
+        v[g][0] = v[g][0] * r * s1.x + sh.x, v[g][1] = v[g][1] * r * s1.y + sh.y;
+        v[g][2] = v[g][2] * r * s1.z + sh.z, v[g][3] = v[g][3] * r * s1.w + sh.w;
+      }
     }
     fwht256_mfma(v[g], h);
     store4_f16(a.y, row, g * 256 + lo, a.ldy, cols, a.tiled, v[g]);

@@ -526,10 +526,13 @@ def test_attention_head_dims(ns2lib, Dh):
 
 # ----------------------------------------------------------------------------- row kernels
 
-@pytest.mark.parametrize("rms", [True, False])
-def test_norm_mod(ns2lib, rms):
-    g = gen(41)
-    rows, cols = 517, 1536
+@pytest.mark.parametrize("rms,cols", [(True, 1536), (False, 1536), (True, 4096), (False, 3840), (True, 512)])
+def test_norm_mod(ns2lib, rms, cols):
+    """normMod and the fused normMod + rotation. 1536 columns is the DiT's width; 512 and 4096
+    are the smallest and widest groups per row of the modulation hoisted with the row (2) and
+    loaded per group (16), 3840 one more width above the hoisting limit."""
+    g = gen(41 + cols)
+    rows = 517
     x = torch.randn(rows, cols, generator=g) * 3 + 0.5
     mod = torch.randn(6 * cols, generator=g) * 0.1
     w = torch.randn(cols, generator=g) * 0.02 if rms else None
@@ -537,11 +540,11 @@ def test_norm_mod(ns2lib, rms):
     ns2lib.norm_mod(x.to(dev), mod.to(dev), 3 * cols, 4 * cols, rows, cols, w.to(dev) if rms else None, y)
     torch.cuda.synchronize()
     ref = O.norm_mod(x.double(), mod.double(), 3 * cols, 4 * cols, w.double() if rms else None)
-    assert_close(y.cpu(), ref, TOL_F32, f"norm_mod rms={rms}")
+    assert_close(y.cpu(), ref, TOL_F32, f"norm_mod rms={rms} cols={cols}")
     yr = torch.empty(rows, cols, dtype=torch.int16, device=dev)
     ns2lib.norm_mod_rotate_f16(x.to(dev), mod.to(dev), 3 * cols, 4 * cols, rows, cols, w.to(dev) if rms else None, yr)
     torch.cuda.synchronize()
-    assert_close(f16_as_float(yr.cpu()), O.rotate(ref), TOL_F16_OUT, f"norm_mod_rotate rms={rms}")
+    assert_close(f16_as_float(yr.cpu()), O.rotate(ref), TOL_F16_OUT, f"norm_mod_rotate rms={rms} cols={cols}")
 
 
 def test_head_norm(ns2lib):
