@@ -114,12 +114,22 @@ export class GPU {
   }
 
   fromArray(arr, shape) {
+    const n = shape.reduce((a, b) => a * b, 1);
+    if (arr.byteLength > n * 4) {
+      throw new Error(`GPU.fromArray: ${arr.byteLength} bytes do not fit shape [${shape}] (${n * 4} bytes)`);
+    }
     const t = this.empty(shape);
     this.write(t.buf, arr);
     return t;
   }
 
+  // Copy a typed array into a device buffer at a byte offset; the copy must stay inside the
+  // buffer (WebGPU's writeBuffer raises the same validation error).
   write(buf, arr, offset = 0) {
+    if (!buf || buf.ptr === null) throw new Error("GPU.write: destination buffer was released");
+    if (!(offset >= 0) || offset + arr.byteLength > buf.size) {
+      throw new Error(`GPU.write: ${arr.byteLength} bytes at offset ${offset} overrun a ${buf.size}-byte buffer`);
+    }
     native.h2d(buf.ptr, arr, offset);
   }
 
@@ -132,6 +142,9 @@ export class GPU {
   }
 
   async read(t, count = t.size) {
+    if (!(count >= 0) || count > t.size) {
+      throw new Error(`GPU.read: ${count} values requested from a tensor of ${t.size}`);
+    }
     const out = new Float32Array(count);
     native.d2h(addr(t), out);
     return out;

@@ -43,6 +43,19 @@ async function main() {
   out.rope2d = { sinOff: t.sinOff, values: Array.from(t.arr) };
   const r1 = ropeTable(fake, 4, 8, 10000);
   out.rope1d = { sinOff: r1.sinOff, values: Array.from(r1.arr) };
+  // bounds of host <-> device copies: every error is raised before the addon is called, so a
+  // GPU object without a device (and fake buffers) exercises them
+  const { GPU, DeviceBuffer, Tensor } = await mod("device.js");
+  const g = new GPU({});
+  const bounds = {};
+  const tryMsg = (f) => { try { f(); return null; } catch (e) { return String(e.message); } };
+  bounds.writeOverrun = tryMsg(() => g.write(new DeviceBuffer(1n, 16), new Float32Array(5)));
+  bounds.writeOffset = tryMsg(() => g.write(new DeviceBuffer(1n, 16), new Float32Array(4), 4));
+  bounds.writeReleased = tryMsg(() => g.write(new DeviceBuffer(null, 16), new Float32Array(1)));
+  bounds.fromArrayShape = tryMsg(() => g.fromArray(new Float32Array(7), [2, 3]));
+  bounds.readCount = await g.read(new Tensor(g, new DeviceBuffer(1n, 256, true), [2, 3], 256), 7)
+    .then(() => null, (e) => String(e.message));
+  out.bounds = bounds;
   const { timestepEmbedding } = await mod("nanosaur2.js");
   out.temb = Array.from(timestepEmbedding(0.37));
 

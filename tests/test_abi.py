@@ -127,3 +127,12 @@ def test_js_safetensors_reader(host):
     assert st["bf16"] == {"kind": "bf16", "N": 4, "K": 64}
     assert np.allclose(st["vec"], t["norm.weight"].float().numpy())
     assert st["badError"] and "unsupported quantization" in st["badError"]
+
+
+def test_js_copy_bounds(host):
+    """GPU.write / fromArray / read refuse copies that leave the device buffer or tensor."""
+    b = host[0]["bounds"]
+    assert "overrun" in b["writeOverrun"] and "overrun" in b["writeOffset"]
+    assert "released" in b["writeReleased"]
+    assert "do not fit shape" in b["fromArrayShape"]
+    assert "requested from a tensor of 6" in b["readCount"]
