@@ -85,9 +85,39 @@ export class Nanosaur2DiT {
         // the MLP's first linear runs fused with its GLU and the rotation for w3
         if (b.w12.kind === "i8" && b.w12.N % 512 === 0 && b.w12.K % 256 === 0) ops.tileWeightGlu(gpu, b.w12);
         else if (ops.tileable(b.w12)) ops.tileWeight(gpu, b.w12);
+        // the fused path feeds every re-tiled weight tiled operands only: keep one copy (w12's
+        // GLU tiles serve only while w3 takes the tiled operand the GLU launch writes)
+        for (const W of [b.qkv, b.kvY, b.proj, b.w3]) if (W && W.tbuf) ops.dropRowMajor(W);
+        if (b.w12.tbuf || (b.w12.tglu && b.w3.tbuf)) ops.dropRowMajor(b.w12);
       }
     }
     return m;
+  }
+
+  // Every linear weight of the model (LoRA targets, lora.js linearRegistry).
+  linears() {
+    const top = [this.sEmbed, this.t1, this.t2, this.yEmbed, this.yPool, this.sharedAda, this.sprintOut,
+      this.finalAda, this.finalLinear];
+    const text = this.text.flatMap((b) => [b.ada, b.qkv, b.proj, b.w12, b.w3]);
+    const blocks = this.blocks.flatMap((b) => [b.qkv, b.kvY, b.proj, b.w12, b.w3]);
+    return top.concat(text, blocks).filter((W) => W);
+  }
+
+  // Bytes of device memory the loaded weights hold (every persistent buffer, once).
+  weightBytes() {
+    const seen = new Set();
+    let bytes = 0;
+    const walk = (o) => {
+      if (!o || typeof o !== "object" || seen.has(o)) return;
+      seen.add(o);
+      if (typeof o.destroy === "function" && o.ptr !== undefined) {
+        if (o.ptr !== null) bytes += o.size;
+        return;
+      }
+      for (const k of Object.keys(o)) if (k !== "gpu" && k !== "ropeCache") walk(o[k]);
+    };
+    walk(this);
+    return bytes;
   }
 
   constructor(gpu, fused = true) {

@@ -55,6 +55,16 @@ export function tileWeight(gpu, W) {
   return W;
 }
 
+// Free the row-major int8 copy of a re-tiled weight when the caller only ever feeds it tiled
+// operands (the fused DiT path): the tiled copy alone then holds the weight, so the int8
+// model stays resident once instead of twice. linear() refuses a row-major launch afterwards.
+export function dropRowMajor(W) {
+  if (!W.tbuf && !W.tglu) throw new Error(`${W.name}: only a re-tiled int8 weight can drop its row-major copy`);
+  if (W.buf) W.buf.destroy();
+  W.buf = null;
+  return W;
+}
+
 // Re-tile the GLU MLP's first int8 weight [2I, K] with its two halves interleaved (W.tglu),
 // for linearGluRotated.
 export function tileWeightGlu(gpu, W) {
@@ -104,6 +114,7 @@ export function linear(gpu, x, W, opts = {}) {
       native.linearI8Tiled(addr(src), addr(W.tbuf), addr(W.scale), addr(bias), addr(out), M, W.N, W.K, ldc,
         cOff, 1, act, resid, addr(opts.gate), gOff, ...lora));
   } else if (W.kind === "i8") {
+    if (!W.buf) throw new Error(`${W.name}: the row-major int8 weight was freed after tiling; pass a tiled operand`);
     const aFmt = opts.xr ? (opts.xr.dtype === "f16" ? 1 : 2) : 0;
     gpu.run(opts.name || "gemm.i8", flops, () =>
       native.linearI8(addr(src), aFmt, W.K, addr(W.buf), addr(W.scale), addr(bias), null, addr(out),

@@ -108,7 +108,7 @@ async function main() {
   const text = dit.prepareText(inp.context, Array.from(inp.weights));
   const loadMs = Date.now() - t0;
   const report = { h, w, T: inp.T, tokens: h * w, fused: !a.referenceOps, pathDrop: !!a.pathDrop, load_ms: loadMs, device: gpu.info,
-    loras: loraReports };
+    loras: loraReports, weight_bytes: dit.weightBytes() };
 
   if (a.out) {
     const x0 = await dit.forward(inp.latent, h, w, text, sigma, { pathDrop: !!a.pathDrop });
