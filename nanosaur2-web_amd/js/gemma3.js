@@ -48,6 +48,12 @@ export class Gemma3 {
     this.st = st; // embedding rows are gathered from the source on demand
   }
 
+  // Every linear weight of the stack (LoRA targets; q|k|v and gate|up are stacked weights
+  // whose parts keep their module names).
+  linears() {
+    return this.layers.flatMap((l) => [l.qkv, l.o, l.gateUp, l.down]);
+  }
+
   // Token ids -> Tensor [L, 640] on the device.
   async encode(ids) {
     const x = this.embed(await this.st.rows("model.embed_tokens.weight", ids), ids.length);

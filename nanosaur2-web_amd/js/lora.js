@@ -1,32 +1,38 @@
-// LoRA support for the Node host (app/lora.js): each targeted linear gets a low-rank side path,
-// y = W x + sum_i s_i B_i (A_i x), without touching the base weights. Strength changes are
-// host-side: the stacked side path of a weight is rebuilt and re-uploaded (a few hundred KB).
+// LoRA side paths for the Node host: every linear a LoRA file names gets
+// y = W x + sum_i s_i B_i (A_i x), and the base weights stay as they are (the behaviour of
+// app/lora.js). Files use PEFT names ("<module>.lora_A/B.weight" + ".alpha") or kohya names
+// ("lora_unet_<module_with_underscores>.lora_down/up.weight" + ".alpha"), for the DiT and the
+// Gemma3 text encoder; LoKr / LoHa / DoRA tensors are counted as unsupported.
 //
-// File formats and name matching as the reference: PEFT naming ("<module>.lora_A/B.weight" +
-// ".alpha") or kohya ("lora_unet_<module_with_underscores>.lora_down/up.weight" + ".alpha"), for
-// the DiT and the Gemma3 text encoder; LoKr/LoHa/DoRA are reported as unsupported.
-//
-// Where the reference (app/gpu/ops.js:70-87) runs two matmuls per LoRA and adds the [M, N] delta
-// in the GEMM epilogue, this build stacks every LoRA of a weight into one fp16 pair
-//   lora_a [R, K]  (the down-projections; rotated per 256-group for int8 ConvRot weights),
-//   lora_b [N, R]  (strength * alpha / r * B_i in its output window, zero elsewhere),
-// R = the summed ranks rounded up to 32, and the GEMM kernels start their accumulators at the
-// low-rank term (the *_lora entry points of the C ABI).
+// How it is organised here:
+//  * each model lists its linears (linears()), and linearRegistry maps the canonical module key
+//    (dots as underscores) to a weight slice { W, off, n } -- a stacked weight such as Gemma3's
+//    q|k|v has one slice per part;
+//  * loadLora reads a file into host arrays and resolves each module to a slice; attachLoras
+//    hands them to their weights with a strength;
+//  * the first launch of a weight after that builds its side path on the device (loraArgs):
+//    every LoRA of the weight stacked into one fp16 pair, lora_a [R, K] and lora_b [N, R]
+//    (strength * alpha / r * B_i in its output window, zero elsewhere), R the summed ranks
+//    rounded up to 32. The GEMM kernels start their accumulators at the low-rank term (the
+//    *_lora entry points of the C ABI) where the reference runs two more matmuls per LoRA and
+//    adds an [M, N] delta (app/gpu/ops.js:70-87).
+//  * int8 ConvRot weights take rotated inputs x H, and x A^T = (x H)(A H)^T, so their lora_a
+//    rows are rotated on the device by the kernel that rotates the activations
+//    (app/lora.js:72-91 rotates them on the host).
 
 import { SafeTensors } from "./weights.js";
+import { addr, DeviceBuffer } from "./device.js";
+import { native } from "./native.js";
 
-const norm = (name) => name.replace(/\./g, "_");
+// ---- names (format data: the tensor roles, trainer prefixes and unsupported markers) ---------
 
-const SUFFIXES = [
-  [".lora_A.weight", "A"], [".lora_B.weight", "B"],
-  [".lora_down.weight", "A"], [".lora_up.weight", "B"],
-  [".alpha", "alpha"],
-];
+// "<module>.<role>": role A (down-projection), B (up-projection) or the alpha scalar
+const ROLE = /^(.+)\.(?:(lora_A|lora_down)\.weight|(lora_B|lora_up)\.weight|(alpha))$/;
 const TE_PREFIXES = ["lora_te_", "lora_te1_", "text_encoders.gemma3_270m.transformer.", "text_encoder.", "te."];
 const DIT_PREFIXES = ["lora_unet_", "model.diffusion_model.", "diffusion_model.", "base_model.model.", "transformer.", "unet."];
 const UNSUPPORTED = /(lokr_|hada_|\.dora_scale|\.diff$|\.diff_b$|\.w_norm|\.b_norm)/;
 
-// Module names of Nanosaur2's linears (DiT and Gemma3), dots as underscores.
+// Module keys of Nanosaur2's linears (DiT and Gemma3).
 const NANOSAUR_MODULE = new RegExp("^(" + [
   "blocks_\\d+_(attn_(qkv_x|kv_y|proj)|mlp_w(12|3))",
   "text_refine_blocks_\\d+_(attn_(qkv|proj)|mlp_w(12|3)|adaLN_modulation_0)",
@@ -35,124 +41,108 @@ const NANOSAUR_MODULE = new RegExp("^(" + [
   "(model_)?layers_\\d+_(self_attn_[qkvo]_proj|mlp_(gate|up|down)_proj)",
 ].join("|") + ")$");
 
-function suffixOf(key) {
-  for (const s of SUFFIXES) if (key.endsWith(s[0])) return s;
-  return null;
+const keyOf = (dotted) => dotted.split(".").join("_");
+
+// { module, role } of a LoRA tensor name, or null for a tensor that is not part of a LoRA pair.
+function parseName(name) {
+  const m = ROLE.exec(name);
+  if (!m) return null;
+  return { module: m[1], role: m[2] ? "A" : m[3] ? "B" : "alpha" };
 }
 
-function stripPrefix(name, prefixes) {
-  for (const p of prefixes) if (name.startsWith(p)) return [name.slice(p.length), true];
-  return [name, false];
+// A module name without its trainer prefix: { key, textEncoder } -- a text-encoder prefix
+// confines the lookup to the text encoder.
+function canonical(module) {
+  const te = TE_PREFIXES.find((p) => module.startsWith(p));
+  const other = te ? "" : DIT_PREFIXES.find((p) => module.startsWith(p)) || "";
+  return { key: keyOf(module.slice((te || other).length)), textEncoder: !!te };
 }
 
-// A LoRA file's tensor names -> { lora, modules, fits, unsupported } (app/lora.js:32-48).
-export function inspectLoraKeys(keys) {
-  const modules = new Set();
+// The tensors of a LoRA file grouped by module: { groups: Map(module -> {A, B, alpha}), unsupported }.
+function groupTensors(names) {
+  const groups = new Map();
   let unsupported = 0;
-  for (const key of keys) {
-    if (UNSUPPORTED.test(key)) { unsupported++; continue; }
-    const suf = suffixOf(key);
-    if (suf && suf[1] !== "alpha") modules.add(key.slice(0, -suf[0].length));
+  for (const name of names) {
+    if (UNSUPPORTED.test(name)) {
+      unsupported++;
+      continue;
+    }
+    const p = parseName(name);
+    if (!p) continue;
+    const g = groups.get(p.module) || {};
+    g[p.role] = name;
+    groups.set(p.module, g);
   }
-  let fits = 0;
-  for (const m of modules) {
-    const [name] = stripPrefix(m, TE_PREFIXES.concat(DIT_PREFIXES));
-    if (NANOSAUR_MODULE.test(norm(name))) fits++;
-  }
-  return { lora: modules.size > 0, modules: modules.size, fits, unsupported };
+  return { groups, unsupported };
 }
 
-// name (dots as underscores) -> { W, off, n } for every linear reachable from a model object;
-// stacked weights register each part (app/lora.js:52-68).
-export function linearRegistry(root) {
+// A LoRA file's tensor names -> { lora, modules, fits, unsupported }: is it a LoRA this build
+// applies, and how many of its modules have Nanosaur2's names (app/lora.js:32-48).
+export function inspectLoraKeys(names) {
+  const { groups, unsupported } = groupTensors(names);
+  const modules = [...groups].filter(([, g]) => g.A || g.B).map(([m]) => m);
+  const fits = modules.filter((m) => NANOSAUR_MODULE.test(canonical(m).key)).length;
+  return { lora: modules.length > 0, modules: modules.length, fits, unsupported };
+}
+
+// ---- registry ------------------------------------------------------------------------------
+
+// The named slices of a weight: one per part of a stacked weight, else the whole weight.
+export function weightSlices(W) {
+  if (W.parts) return W.parts.map((p) => ({ name: p.name, W, off: p.off, n: p.n }));
+  return [{ name: W.name, W, off: 0, n: W.N }];
+}
+
+// module key -> { W, off, n } over the linears a model lists (model.linears()).
+export function linearRegistry(model) {
   const reg = new Map();
-  const seen = new Set();
-  const walk = (o) => {
-    if (!o || typeof o !== "object" || seen.has(o) || ArrayBuffer.isView(o)) return;
-    if (o instanceof SafeTensors) return;
-    seen.add(o);
-    if (o.kind && (o.buf || o.tbuf || o.tglu) && o.N && o.K) {
-      if (o.parts) for (const p of o.parts) reg.set(norm(p.name), { W: o, off: p.off, n: p.n });
-      else if (o.name) reg.set(norm(o.name), { W: o, off: 0, n: o.N });
-      return;
-    }
-    for (const k of Object.keys(o)) if (k !== "gpu" && k !== "st") walk(o[k]);
-  };
-  walk(root);
+  for (const W of model.linears()) for (const s of weightSlices(W)) reg.set(keyOf(s.name), s);
   return reg;
 }
 
-// In place: each row's 256-groups times the regular Hadamard H256 (x 1/16), the transform of the
-// int8 layers' inputs, so x_r (A H)^T = x A^T (app/lora.js:72-91): four radix-4 stages at strides
-// 1, 4, 16, 64 with y = (a + b + c - e, a + b - c + e, a - b + c + e, -a + b + c + e).
-export function hadamardRows(data, rows, K) {
-  for (let r = 0; r < rows; r++) {
-    for (let g = 0; g < K; g += 256) {
-      const base = r * K + g;
-      for (let stride = 1; stride < 256; stride *= 4) {
-        for (let blk = 0; blk < 256; blk += 4 * stride) {
-          for (let t = 0; t < stride; t++) {
-            const i0 = base + blk + t;
-            const a = data[i0], b = data[i0 + stride], c = data[i0 + 2 * stride], e = data[i0 + 3 * stride];
-            data[i0] = a + b + c - e;
-            data[i0 + stride] = a + b - c + e;
-            data[i0 + 2 * stride] = a - b + c + e;
-            data[i0 + 3 * stride] = -a + b + c + e;
-          }
-        }
-      }
-      for (let i = 0; i < 256; i++) data[base + i] *= 0.0625;
-    }
-  }
-}
-
-function findTarget(module, regs) {
-  let [name, te] = stripPrefix(module, TE_PREFIXES);
-  if (!te) name = stripPrefix(name, DIT_PREFIXES)[0];
-  const key = norm(name);
-  const order = te ? [regs.te] : [regs.dit, regs.te];
-  for (const reg of order) {
+// The weight slice a LoRA module targets in regs ({ dit, te }), or null. A module without a
+// text-encoder prefix is looked up in the DiT first; kohya text-encoder names leave out the
+// model's "model." root, so "model_" + key is tried as well.
+function resolve(module, regs) {
+  const { key, textEncoder } = canonical(module);
+  const where = textEncoder ? [regs.te] : [regs.dit, regs.te];
+  for (const reg of where) {
     if (!reg) continue;
-    if (reg.has(key)) return reg.get(key);
-    if (reg.has("model_" + key)) return reg.get("model_" + key); // kohya TE names omit "model."
+    const hit = reg.get(key) || reg.get("model_" + key);
+    if (hit) return hit;
   }
   return null;
 }
 
-// Parses a LoRA file (a path or an open SafeTensors) for the given registries ({ dit, te }).
-// Returns { modules: [{ target, A, B, r, alphaScale }], matched, total, unsupported, skipped }
-// with A (rotated for int8 targets) and B as host Float32Arrays (app/lora.js:96-131).
+// ---- loading -------------------------------------------------------------------------------
+
+// Parses a LoRA file (a path or an open SafeTensors) for the registries { dit, te }. Returns
+// { modules: [{ target, A, B, r, alphaScale }], matched, total, unsupported, skipped }, A [r, K]
+// and B [n, r] as host Float32Arrays (app/lora.js:96-131). A module is skipped when it lacks
+// A or B, names no linear of the model, or its shapes do not fit the slice it names.
 export async function loadLora(source, regs) {
   const st = typeof source === "string" ? await SafeTensors.open(source) : source;
-  const groups = new Map();
-  let unsupported = 0;
-  for (const key of Object.keys(st.header)) {
-    if (UNSUPPORTED.test(key)) { unsupported++; continue; }
-    const suf = suffixOf(key);
-    if (!suf) continue;
-    const module = key.slice(0, -suf[0].length);
-    if (!groups.has(module)) groups.set(module, {});
-    groups.get(module)[suf[1]] = key;
+  try {
+    const { groups, unsupported } = groupTensors(st.names());
+    const modules = [];
+    for (const [module, g] of groups) {
+      const target = g.A && g.B ? resolve(module, regs) : null;
+      if (!target) continue;
+      const [r, k] = st.info(g.A).shape;
+      const [n, rb] = st.info(g.B).shape;
+      if (k !== target.W.K || n !== target.n || rb !== r) continue;
+      const A = Float32Array.from(await st.f32(g.A));
+      const B = Float32Array.from(await st.f32(g.B));
+      const alpha = g.alpha ? (await st.f32(g.alpha))[0] : null;
+      modules.push({ target, A, B, r, alphaScale: alpha ? alpha / r : 1 });
+    }
+    return { modules, matched: modules.length, total: groups.size, unsupported, skipped: groups.size - modules.length };
+  } finally {
+    if (typeof source === "string") st.close();
   }
-  const modules = [];
-  let skipped = 0;
-  for (const [module, keys] of groups) {
-    if (!keys.A || !keys.B) { skipped++; continue; }
-    const target = findTarget(module, regs);
-    const aInfo = st.info(keys.A), bInfo = st.info(keys.B);
-    const r = aInfo.shape[0];
-    if (!target || aInfo.shape[1] !== target.W.K || bInfo.shape[0] !== target.n || bInfo.shape[1] !== r) { skipped++; continue; }
-    const A = Float32Array.from(await st.f32(keys.A)); // own copy: rotated in place for int8 layers
-    if (target.W.kind === "i8") hadamardRows(A, r, target.W.K);
-    const B = Float32Array.from(await st.f32(keys.B));
-    const alpha = keys.alpha ? (await st.f32(keys.alpha))[0] : null;
-    modules.push({ target, A, B, r, alphaScale: alpha ? alpha / r : 1 });
-  }
-  if (typeof source === "string") st.close();
-  return { modules, matched: modules.length, total: groups.size, unsupported, skipped };
 }
 
-// Releases the stacked side paths built for a registry's weights.
+// Releases the device side paths built for a registry's weights.
 function dropPacks(regs) {
   for (const reg of [regs.dit, regs.te]) {
     if (!reg) continue;
@@ -181,6 +171,8 @@ export function attachLoras(regs, active) {
     }
   }
 }
+
+// ---- the stacked side path -----------------------------------------------------------------
 
 // fp32 -> fp16 bit patterns, round to nearest even (subnormals kept, overflow to infinity).
 export function f32ToF16Bits(f) {
@@ -217,7 +209,7 @@ export function f32ToF16Bits(f) {
   return out;
 }
 
-// Host arrays of a weight's stacked side path: { a: fp32 [R, K], b: fp32 [N, R], R }.
+// Host arrays of a weight's stacked side path: { a: fp32 [R, K] (not rotated), b: fp32 [N, R], R }.
 export function stackLora(W) {
   const rs = W.lora.reduce((s, e) => s + e.r, 0);
   const R = Math.ceil(rs / 32) * 32;
@@ -236,13 +228,28 @@ export function stackLora(W) {
   return { a, b, R };
 }
 
-// The device side path of W for the *_lora entry points ([loraA, loraB, loraR]), built on first
-// use after attachLoras; [null, null, 0] without LoRA.
+// The device side path of W: lora_b uploaded as fp16; lora_a as fp16 too, for an int8 weight
+// rotated per 256-group on the way by the activation rotation kernel (fp32 rows in a pooled
+// staging tensor, rotated and rounded to fp16 into the persistent buffer).
+function buildPack(gpu, W) {
+  const { a, b, R } = stackLora(W);
+  let aBuf;
+  if (W.kind === "i8") {
+    const bytes = R * W.K * 2;
+    aBuf = new DeviceBuffer(native.malloc(bytes), bytes, false);
+    const staged = gpu.fromArray(a, [R, W.K]);
+    native.rotateF16(addr(staged), W.K, aBuf.ptr, W.K, R, W.K, 0);
+    staged.release();
+  } else {
+    aBuf = gpu.upload(f32ToF16Bits(a));
+  }
+  return { a: aBuf, b: gpu.upload(f32ToF16Bits(b)), R };
+}
+
+// [loraA, loraB, loraR] of W for the *_lora entry points, the side path built on first use
+// after attachLoras; [null, null, 0] without LoRA.
 export function loraArgs(gpu, W) {
   if (!W.lora || !W.lora.length) return [null, null, 0];
-  if (!W.loraPack) {
-    const { a, b, R } = stackLora(W);
-    W.loraPack = { a: gpu.upload(f32ToF16Bits(a)), b: gpu.upload(f32ToF16Bits(b)), R };
-  }
+  if (!W.loraPack) W.loraPack = buildPack(gpu, W);
   return [W.loraPack.a.ptr, W.loraPack.b.ptr, W.loraPack.R];
 }

@@ -1,6 +1,6 @@
-// CPU-only checks of the Node host's LoRA module (lora.js): the rotation of the down-projections,
-// fp16 rounding, the stacked side path, key inspection and the loader's name matching against
-// fake registries. Reads a JSON job file, prints one JSON object for tests/test_lora_host.py.
+// CPU-only checks of the Node host's LoRA module (lora.js): fp16 rounding, the stacked side path,
+// key inspection and the loader's name matching against fake models that list their linears.
+// Reads a JSON job file, prints one JSON object for tests/test_lora_host.py.
 import fs from "fs";
 import path from "path";
 import { fileURLToPath, pathToFileURL } from "url";
@@ -13,9 +13,6 @@ async function main() {
   const job = JSON.parse(fs.readFileSync(process.argv[2], "utf8"));
   const L = await mod("lora.js");
   const out = {};
-  const h = Float32Array.from(job.hadamard.data);
-  L.hadamardRows(h, job.hadamard.rows, job.hadamard.K);
-  out.hadamard = Array.from(h);
   out.f16 = Array.from(L.f32ToF16Bits(Float32Array.from(job.f16)));
   const W = { name: "w", N: job.N, K: job.K, lora: job.entries.map((e) => ({ ...e, A: Float32Array.from(e.A), B: Float32Array.from(e.B) })) };
   const s = L.stackLora(W);
@@ -24,7 +21,7 @@ async function main() {
   // loaders against fake registries built from { name, kind, N, K } linears (and stacked parts)
   out.loads = [];
   for (const ld of job.loads) {
-    const model = { layers: ld.linears.map((l) => (l.parts ? { ...l, buf: {} } : { ...l, buf: {} })) };
+    const model = { linears: () => ld.linears.map((l) => ({ ...l, buf: {} })) };
     const reg = L.linearRegistry(model);
     const regs = ld.te ? { te: reg } : { dit: reg };
     const res = await L.loadLora(ld.file, regs);

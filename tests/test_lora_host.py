@@ -1,8 +1,9 @@
-"""CPU checks of the Node host's LoRA module (nanosaur2-web_amd/js/lora.js, the restatement of
-app/lora.js): the per-256-group rotation of the down-projections for int8 targets against the
-oracle's Hadamard, the fp16 rounding of the stacked operands against numpy, the stacked side
-path against the oracle's pack_lora, key inspection, and the loader's name matching (PEFT and
-kohya names, DiT and text-encoder prefixes, slices of stacked weights) with fake registries."""
+"""CPU checks of the Node host's LoRA module (nanosaur2-web_amd/js/lora.js, the behaviour of
+app/lora.js): the fp16 rounding of the stacked operands against numpy, the stacked side path
+against the oracle's pack_lora, key inspection, and the loader's name matching (PEFT and kohya
+names, DiT and text-encoder prefixes, slices of stacked weights) with fake models. The rotation
+of int8 targets' down-projections runs on the device (the activation rotation kernel); the GPU
+LoRA tests cover it against the reference's own LoRA outputs."""
 
 import json
 import os
@@ -25,7 +26,6 @@ CHECKS = os.path.join(ROOT, "tests", "js", "lora_checks.mjs")
 def host(tmp_path_factory):
     d = tmp_path_factory.mktemp("lora")
     g = torch.Generator().manual_seed(8)
-    had = torch.randn(3, 512, generator=g)
     f16 = [0.0, -0.0, 1.0, 65504.0, 65520.0, 1e6, -1e6, 6.1e-5, 5.96e-8, 2.98e-8, 1e-9, 0.1, 1 / 3,
            1.0 + 2 ** -11, 1.0 + 3 * 2 ** -11, -2.5e-6, float(np.float32(np.pi))]
     f16 += torch.randn(200, generator=g).mul(30).tolist()
@@ -56,7 +56,6 @@ def host(tmp_path_factory):
         {"name": "model.layers.6.mlp.up_proj", "off": 2048, "n": 2048}]}
     o = {"name": "model.layers.16.self_attn.o_proj", "kind": "bf16", "N": 640, "K": 1024}
     job = {
-        "hadamard": {"rows": 3, "K": 512, "data": had.reshape(-1).tolist()},
         "f16": f16, "N": N, "K": K,
         "entries": [{"A": A.reshape(-1).tolist(), "B": B.reshape(-1).tolist(), "r": A.shape[0], "scale": s, "off": off, "n": n}
                     for A, B, s, off, n in ents],
@@ -71,13 +70,7 @@ def host(tmp_path_factory):
         json.dump(job, f)
     p = subprocess.run(["node", CHECKS, jf], capture_output=True, text=True, timeout=120)
     assert p.returncode == 0, p.stderr
-    return json.loads(p.stdout), had, f16, ents, lora_dit, te_lora
-
-
-def test_hadamard_rows_is_the_convrot_rotation(host):
-    out, had, *_ = host
-    got = torch.tensor(out["hadamard"], dtype=torch.float64).reshape(3, 512)
-    assert torch.allclose(got, O.rotate(had.double()), atol=1e-5)
+    return json.loads(p.stdout), None, f16, ents, lora_dit, te_lora
 
 
 def test_f16_rounding_matches_numpy(host):
@@ -112,9 +105,8 @@ def test_loader_matches_modules(host):
         key = ("diffusion_model." + mname + ".lora_A.weight") if naming == "peft" else \
               ("lora_unet_" + mname.replace(".", "_") + ".lora_down.weight")
         A = lora_dit[key].float().double()
-        want = O.rotate(A) if mname.startswith(("blocks", "text_refine")) else A
         got = torch.tensor(m["A"], dtype=torch.float64)
-        assert torch.allclose(got, want.reshape(-1)[:got.numel()], atol=1e-5), mname
+        assert torch.allclose(got, A.reshape(-1)[:got.numel()], atol=1e-6), mname
     assert te["matched"] == 3
     windows = sorted((m["off"], m["n"], m["r"]) for m in te["modules"])
     assert windows == [(0, 640, 4), (1024, 256, 8), (2048, 2048, 16)]
