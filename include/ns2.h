@@ -14,7 +14,8 @@
  *  - Activations are fp32, row-major. Strides (ld*) and offsets (*Off) are in ELEMENTS,
  *    exactly as in the reference's dispatch parameters.
  *  - All launches are asynchronous and ordered on one HIP stream (ns2_set_stream; the
- *    default is the null stream). ns2_sync / ns2_d2h wait for completion.
+ *    default is a stream the library creates at ns2_init, default priority). ns2_sync /
+ *    ns2_d2h wait for completion.
  *  - int8 weights are "int8_tensorwise + convrot": W_q int8 [N, K] row-major with one fp32
  *    scale per output row; the layer computes (x H) W_q^T diag(scale), where H is the
  *    normalized 256-point regular Hadamard matrix applied per 256-feature group
@@ -228,6 +229,30 @@ int ns2_attention(const float* q, const float* k, const float* v, float* o, int 
                   float scale, const float* key_bias, int biasStart, long long biasBatch,
                   const float* q_norm, const float* k_norm, float eps, const float* rope_cs,
                   long long sin_off, int rope_rows);
+
+/* Bytes of the fixed device scratch array behind ns2_attention_noalloc (one per GPU, held
+ * until the process ends). */
+#define NS2_NOALLOC_SCRATCH_BYTES (64u << 20)
+
+/* ns2_attention without any device allocation. No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). Same arguments, semantics and results as
+ * ns2_attention; its packed K/V tiles, key biases and (for views that are not 16-byte aligned)
+ * packed queries live in a static device array of NS2_NOALLOC_SCRATCH_BYTES instead of
+ * library workspace, and it calls no hipMalloc / hipFree. It needs
+ *   2 * batch*H * ceil(Lk/64)*64 * D * 2  +  batch * ceil(Lk/64)*64 * 4
+ *   (+ batch*H * ceil(Lq/256)*256 * D * 2 for unaligned views) bytes, each part rounded up to
+ * 256, and fails with NS2_ERR_INVALID beyond the array: the 832x1216 joint attention
+ * (3952 + 256 keys, 16 heads of 96) fits at batch 2. The array is shared by every call on a
+ * GPU and keeps the last call's contents (every byte a call reads it writes first): calls that
+ * overlap on one GPU (several streams or threads) race. */
+int ns2_attention_noalloc(const float* q, const float* k, const float* v, float* o, int batch,
+                          int Lq, int Lk, int H, int D, int ldq, int ldk, int ldv, int ldo,
+                          long long qOff, long long kOff, long long vOff, long long oOff,
+                          long long qBatch, long long kBatch, long long vBatch, long long oBatch,
+                          float scale, const float* key_bias, int biasStart, long long biasBatch,
+                          const float* q_norm, const float* k_norm, float eps, const float* rope_cs,
+                          long long sin_off, int rope_rows);
 
 /* ---- row kernels ---------------------------------------------------------------------- */
 

@@ -806,17 +806,31 @@ void launch_flash(FlashArgs fa, hipStream_t s) {
 }
 
 template <int D>
-int run_attention(PackArgs pa, FlashArgs fa, int batch, bool vec) {
-  hipStream_t s = ns2::stream();
+void launch_pack(const PackArgs& pa, int batch, bool vec, hipStream_t s) {
   const int rows = (pa.skip_q || pa.Lk_pad > pa.Lq_pad) ? pa.Lk_pad : pa.Lq_pad;
+  if (vec) attn_pack_vec_kernel<D><<<dim3(rows / KB, pa.H, batch), 256, 0, s>>>(pa);
+  else attn_pack_kernel<D><<<dim3(rows / KB, pa.H, batch), 256, 0, s>>>(pa);
+}
+
+// profile: bracket the two launches with the kernel profiler's events (off for the
+// allocation-free entry point, whose callers may not create events)
+template <int D>
+int run_attention(PackArgs pa, FlashArgs fa, int batch, bool vec, bool profile) {
+  hipStream_t s = ns2::stream();
+  fa.pairs = pa.H * batch;
+  if (!profile) {
+    launch_pack<D>(pa, batch, vec, s);
+    NS2_LAUNCHED("attn_pack");
+    launch_flash<D, 1, 8>(fa, s);
+    NS2_LAUNCHED("attn_flash");
+    return NS2_OK;
+  }
   {
     ns2::ProfScope prof_("attn_pack");
-    if (vec) attn_pack_vec_kernel<D><<<dim3(rows / KB, pa.H, batch), 256, 0, s>>>(pa);
-    else attn_pack_kernel<D><<<dim3(rows / KB, pa.H, batch), 256, 0, s>>>(pa);
+    launch_pack<D>(pa, batch, vec, s);
     NS2_LAUNCHED("attn_pack");
   }
   ns2::ProfScope prof_("attn_flash");
-  fa.pairs = pa.H * batch;
   // 32 queries per wave, 8 waves (256 queries) per workgroup: two waves per SIMD, all
   // accumulators in architectural VGPRs
   launch_flash<D, 1, 8>(fa, s);
@@ -1110,6 +1124,81 @@ extern "C" int ns2_attention_rows(const float* q, const float* k, const float* v
   return NS2_OK;
 }
 
+namespace {
+
+// The body of ns2_attention and ns2_attention_noalloc: the packed operands live in library
+// workspace, or (noalloc) are carved from the fixed scratch array.
+int attention_call(const char* fn, bool noalloc, const float* q, const float* k, const float* v, float* o,
+                   int batch, int Lq, int Lk, int H, int D, int ldq, int ldk, int ldv, int ldo, long long qOff,
+                   long long kOff, long long vOff, long long oOff, long long qBatch, long long kBatch,
+                   long long vBatch, long long oBatch, float scale, const float* key_bias, int biasStart,
+                   long long biasBatch, const float* q_norm, const float* k_norm, float eps,
+                   const float* rope_cs, long long sin_off, int rope_rows) {
+  NS2_READY();
+  if (Lq <= 0 || batch <= 0) return NS2_OK;
+  NS2_REQUIRE(q && k && v && o, "%s: null q, k, v or o", fn);
+  NS2_REQUIRE(D == 32 || D == 64 || D == 96 || D == 128, "%s: unsupported head dim %d", fn, D);
+  NS2_REQUIRE(Lk > 0 && H > 0, "%s: Lk=%d H=%d", fn, Lk, H);
+  NS2_REQUIRE(ldo % 4 == 0 && oOff % 4 == 0 && oBatch % 4 == 0 && aligned16(o),
+              "%s: the output view must be 16-byte aligned (ldo, oOff, oBatch multiples of 4)", fn);
+  NS2_REQUIRE(ldq >= D && ldk >= D && ldv >= D, "%s: row strides must cover one head", fn);
+  if (key_bias) NS2_REQUIRE(biasStart >= 0, "%s: negative biasStart", fn);
+  const int Lq_pad = (Lq + QPAD - 1) / QPAD * QPAD;
+  const int Lk_pad = (Lk + KB - 1) / KB * KB;
+  const long long bh = (long long)batch * H;
+  const size_t qbytes = (size_t)bh * Lq_pad * D * sizeof(half_t);
+  const size_t kbytes = (size_t)bh * Lk_pad * D * sizeof(half_t);
+  const size_t bbytes = (size_t)batch * Lk_pad * sizeof(float);
+  // the vectorized pack needs 16-byte aligned rows in every view it reads; then the flash
+  // kernel reads Q itself and no packed Q is written
+  auto al4 = [](long long x) { return x % 4 == 0; };
+  const bool vec = aligned16(q) && aligned16(k) && aligned16(v) && al4(ldq) && al4(ldk) && al4(ldv) &&
+                   al4(qOff) && al4(kOff) && al4(vOff) && al4(qBatch) && al4(kBatch) && al4(vBatch) &&
+                   (!q_norm || aligned16(q_norm)) && (!k_norm || aligned16(k_norm)) &&
+                   (!rope_cs || (aligned16(rope_cs) && al4(sin_off)));
+  half_t *Qp, *Kc, *Vc;
+  float* B2;
+  if (noalloc) {
+    auto up = [](size_t b) { return (b + 255) / 256 * 256; };
+    const size_t need = up(kbytes) * 2 + up(bbytes) + (vec ? 0 : up(qbytes));
+    NS2_REQUIRE(need <= (size_t)NS2_NOALLOC_SCRATCH_BYTES,
+                "%s: batch %d x %d heads x %d keys (D=%d) needs %zu bytes of scratch, more than the %zu "
+                "of the fixed array",
+                fn, batch, H, Lk, D, need, (size_t)NS2_NOALLOC_SCRATCH_BYTES);
+    unsigned char* base = static_cast<unsigned char*>(ns2::noalloc_scratch());
+    if (!base) return ns2::set_error(NS2_ERR_STATE, "%s: the scratch array of this device is not resolved", fn);
+    Kc = reinterpret_cast<half_t*>(base);
+    Vc = reinterpret_cast<half_t*>(base + up(kbytes));
+    B2 = reinterpret_cast<float*>(base + 2 * up(kbytes));
+    Qp = vec ? nullptr : reinterpret_cast<half_t*>(base + 2 * up(kbytes) + up(bbytes));
+  } else {
+    Qp = static_cast<half_t*>(ns2::workspace(1, qbytes));
+    Kc = static_cast<half_t*>(ns2::workspace(2, kbytes));
+    Vc = static_cast<half_t*>(ns2::workspace(3, kbytes));
+    B2 = static_cast<float*>(ns2::workspace(4, bbytes));
+    if (!Qp || !Kc || !Vc || !B2) return ns2::set_error(NS2_ERR_OOM, "%s: workspace allocation failed", fn);
+  }
+
+  PackArgs pa{q, k, v, key_bias, q_norm, k_norm, rope_cs, Qp, Kc, Vc, B2,
+              qOff, kOff, vOff, qBatch, kBatch, vBatch, biasBatch, sin_off,
+              Lq, Lk, Lq_pad, Lk_pad, H, ldq, ldk, ldv, biasStart, rope_rows,
+              scale * kLog2e, eps};
+  int first_biased = Lk;  // padding keys need the mask bias too
+  if (key_bias && biasStart < Lk) first_biased = biasStart;
+  FlashArgs fa{Qp, Kc, Vc, B2, o, oOff, oBatch, Lq, Lk, Lq_pad, Lk_pad, H, ldo, first_biased / KB, 0, 0, 0,
+               vec ? 1 : 0, q, q_norm, rope_cs, qOff, qBatch, sin_off, ldq, rope_rows, scale * kLog2e, eps};
+  pa.skip_q = vec ? 1 : 0;
+  const bool profile = !noalloc;
+  switch (D) {
+    case 32: return run_attention<32>(pa, fa, batch, vec, profile);
+    case 64: return run_attention<64>(pa, fa, batch, vec, profile);
+    case 96: return run_attention<96>(pa, fa, batch, vec, profile);
+    default: return run_attention<128>(pa, fa, batch, vec, profile);
+  }
+}
+
+}  // namespace
+
 extern "C" int ns2_attention(const float* q, const float* k, const float* v, float* o, int batch,
                              int Lq, int Lk, int H, int D, int ldq, int ldk, int ldv, int ldo,
                              long long qOff, long long kOff, long long vOff, long long oOff,
@@ -1117,46 +1206,19 @@ extern "C" int ns2_attention(const float* q, const float* k, const float* v, flo
                              float scale, const float* key_bias, int biasStart, long long biasBatch,
                              const float* q_norm, const float* k_norm, float eps,
                              const float* rope_cs, long long sin_off, int rope_rows) {
-  NS2_READY();
-  if (Lq <= 0 || batch <= 0) return NS2_OK;
-  NS2_REQUIRE(q && k && v && o, "ns2_attention: null q, k, v or o");
-  NS2_REQUIRE(D == 32 || D == 64 || D == 96 || D == 128, "ns2_attention: unsupported head dim %d", D);
-  NS2_REQUIRE(Lk > 0 && H > 0, "ns2_attention: Lk=%d H=%d", Lk, H);
-  NS2_REQUIRE(ldo % 4 == 0 && oOff % 4 == 0 && oBatch % 4 == 0 && aligned16(o),
-              "ns2_attention: the output view must be 16-byte aligned (ldo, oOff, oBatch multiples of 4)");
-  NS2_REQUIRE(ldq >= D && ldk >= D && ldv >= D, "ns2_attention: row strides must cover one head");
-  if (key_bias) NS2_REQUIRE(biasStart >= 0, "ns2_attention: negative biasStart");
-  const int Lq_pad = (Lq + QPAD - 1) / QPAD * QPAD;
-  const int Lk_pad = (Lk + KB - 1) / KB * KB;
-  const long long bh = (long long)batch * H;
-  const size_t qbytes = (size_t)bh * Lq_pad * D * sizeof(half_t);
-  const size_t kbytes = (size_t)bh * Lk_pad * D * sizeof(half_t);
-  const size_t bbytes = (size_t)batch * Lk_pad * sizeof(float);
-  half_t* Qp = static_cast<half_t*>(ns2::workspace(1, qbytes));
-  half_t* Kc = static_cast<half_t*>(ns2::workspace(2, kbytes));
-  half_t* Vc = static_cast<half_t*>(ns2::workspace(3, kbytes));
-  float* B2 = static_cast<float*>(ns2::workspace(4, bbytes));
-  if (!Qp || !Kc || !Vc || !B2) return ns2::set_error(NS2_ERR_OOM, "ns2_attention: workspace allocation failed");
+  return attention_call("ns2_attention", false, q, k, v, o, batch, Lq, Lk, H, D, ldq, ldk, ldv, ldo, qOff, kOff,
+                        vOff, oOff, qBatch, kBatch, vBatch, oBatch, scale, key_bias, biasStart, biasBatch, q_norm,
+                        k_norm, eps, rope_cs, sin_off, rope_rows);
+}
 
-  PackArgs pa{q, k, v, key_bias, q_norm, k_norm, rope_cs, Qp, Kc, Vc, B2,
-              qOff, kOff, vOff, qBatch, kBatch, vBatch, biasBatch, sin_off,
-              Lq, Lk, Lq_pad, Lk_pad, H, ldq, ldk, ldv, biasStart, rope_rows,
-              scale * kLog2e, eps};
-  // the vectorized pack needs 16-byte aligned rows in every view it reads
-  auto al4 = [](long long x) { return x % 4 == 0; };
-  const bool vec = aligned16(q) && aligned16(k) && aligned16(v) && al4(ldq) && al4(ldk) && al4(ldv) &&
-                   al4(qOff) && al4(kOff) && al4(vOff) && al4(qBatch) && al4(kBatch) && al4(vBatch) &&
-                   (!q_norm || aligned16(q_norm)) && (!k_norm || aligned16(k_norm)) &&
-                   (!rope_cs || (aligned16(rope_cs) && al4(sin_off)));
-  int first_biased = Lk;  // padding keys need the mask bias too
-  if (key_bias && biasStart < Lk) first_biased = biasStart;
-  FlashArgs fa{Qp, Kc, Vc, B2, o, oOff, oBatch, Lq, Lk, Lq_pad, Lk_pad, H, ldo, first_biased / KB, 0, 0, 0,
-               vec ? 1 : 0, q, q_norm, rope_cs, qOff, qBatch, sin_off, ldq, rope_rows, scale * kLog2e, eps};
-  pa.skip_q = vec ? 1 : 0;
-  switch (D) {
-    case 32: return run_attention<32>(pa, fa, batch, vec);
-    case 64: return run_attention<64>(pa, fa, batch, vec);
-    case 96: return run_attention<96>(pa, fa, batch, vec);
-    default: return run_attention<128>(pa, fa, batch, vec);
-  }
+extern "C" int ns2_attention_noalloc(const float* q, const float* k, const float* v, float* o, int batch,
+                                     int Lq, int Lk, int H, int D, int ldq, int ldk, int ldv, int ldo,
+                                     long long qOff, long long kOff, long long vOff, long long oOff,
+                                     long long qBatch, long long kBatch, long long vBatch, long long oBatch,
+                                     float scale, const float* key_bias, int biasStart, long long biasBatch,
+                                     const float* q_norm, const float* k_norm, float eps,
+                                     const float* rope_cs, long long sin_off, int rope_rows) {
+  return attention_call("ns2_attention_noalloc", true, q, k, v, o, batch, Lq, Lk, H, D, ldq, ldk, ldv, ldo, qOff,
+                        kOff, vOff, oOff, qBatch, kBatch, vBatch, oBatch, scale, key_bias, biasStart, biasBatch,
+                        q_norm, k_norm, eps, rope_cs, sin_off, rope_rows);
 }

@@ -20,6 +20,10 @@ bool initialised();
 // (one slot per concurrent use inside a single entry point).
 void* workspace(int slot, size_t bytes);
 constexpr int kWorkspaceSlots = 7;
+// Device address of the current device's copy of the fixed scratch array that the
+// allocation-free entry points use (NS2_NOALLOC_SCRATCH_BYTES bytes, resolved by ns2_init), or
+// null before ns2_init has run on that device.
+void* noalloc_scratch();
 // LoRA side path of a linear: checks the stacked down/up projections (lora_a fp16 [R][K],
 // lora_b fp16 [N][R], R % 32 == 0, R <= 256) and computes *t = x lora_a^T (fp32 [M][R], library
 // scratch) from the linear's input x: x_fmt 0 fp32 [M][ldx], 1 fp16 [M][ldx], 2 fp16 in the

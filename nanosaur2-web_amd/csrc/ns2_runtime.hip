@@ -80,6 +80,17 @@ void* workspace(int slot, size_t bytes) {
   return w.ptr;
 }
 
+// ---- fixed scratch of the allocation-free entry points ------------------------------------
+// A file-scope device array: every GPU the library runs on holds its own copy, at its own
+// address, until the process ends. Its name is only a host-side stand-in for the symbol: host
+// code uses the address that ns2_init resolves per device with hipGetSymbolAddress, never the
+// name itself.
+static __device__ __align__(256) unsigned char scratch[NS2_NOALLOC_SCRATCH_BYTES];
+constexpr int kMaxDevices = 64;
+static void* g_scratch[kMaxDevices];
+
+void* noalloc_scratch() { return g_init && g_device < kMaxDevices ? g_scratch[g_device] : nullptr; }
+
 // ---- kernel profiler -----------------------------------------------------------------------
 struct ProfPending {
   const char* name;
@@ -157,8 +168,16 @@ int ns2_init(int device) {
   int n = 0;
   NS2_HIP(hipGetDeviceCount(&n));
   NS2_REQUIRE(device >= 0 && device < n, "ns2_init: device %d out of range (%d devices)", device, n);
+  NS2_REQUIRE(device < kMaxDevices, "ns2_init: device %d beyond the %d this library tracks", device, kMaxDevices);
   NS2_HIP(hipSetDevice(device));
   g_device = device;
+  // this device's copy of the allocation-free entry points' scratch array (once per device,
+  // with the device current)
+  if (!g_scratch[device]) {
+    void* ptr = nullptr;
+    NS2_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+    g_scratch[device] = ptr;
+  }
   // launches go to a stream of the library's own (default priority) unless the caller sets
   // one: the legacy null stream cannot be captured into a graph
   if (!g_own_stream) NS2_HIP(hipStreamCreate(&g_own_stream));

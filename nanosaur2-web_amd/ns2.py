@@ -70,6 +70,9 @@ SIGNATURES = {
     "ns2_attention": [c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
                       c_int, c_ll, c_ll, c_ll, c_ll, c_ll, c_ll, c_ll, c_ll, c_float, c_vp, c_int,
                       c_ll, c_vp, c_vp, c_float, c_vp, c_ll, c_int],
+    "ns2_attention_noalloc": [c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
+                              c_int, c_ll, c_ll, c_ll, c_ll, c_ll, c_ll, c_ll, c_ll, c_float, c_vp, c_int,
+                              c_ll, c_vp, c_vp, c_float, c_vp, c_ll, c_int],
     "ns2_attention_rows": [c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
                            c_ll, c_ll, c_ll, c_int, c_int],
     "ns2_head_norm": [c_vp, c_vp, c_int, c_int, c_int, c_int, c_ll, c_ll, c_vp, c_ll, c_float],
@@ -234,10 +237,13 @@ class Lib:
     def attention(self, q, k, v, o, *, Lq, Lk, H, D, ldq, ldk, ldv, ldo, qOff=0, kOff=0, vOff=0,
                   oOff=0, batch=1, qBatch=0, kBatch=0, vBatch=0, oBatch=0, scale=None,
                   key_bias=None, biasStart=0, biasBatch=0, q_norm=None, k_norm=None, eps=1e-6,
-                  rope_cs=None, sin_off=0, rope_rows=0):
+                  rope_cs=None, sin_off=0, rope_rows=0, noalloc=False):
+        """ns2_attention, or with noalloc=True ns2_attention_noalloc (same arguments; its
+        scratch is the library's fixed device array, no allocation)."""
         if scale is None:
             scale = 1.0 / D ** 0.5
-        self.call("ns2_attention", _ptr(q), _ptr(k), _ptr(v), _ptr(o), batch, Lq, Lk, H, D, ldq, ldk,
+        fn = "ns2_attention_noalloc" if noalloc else "ns2_attention"
+        self.call(fn, _ptr(q), _ptr(k), _ptr(v), _ptr(o), batch, Lq, Lk, H, D, ldq, ldk,
                   ldv, ldo, qOff, kOff, vOff, oOff, qBatch, kBatch, vBatch, oBatch, scale,
                   _ptr(key_bias), biasStart, biasBatch, _ptr(q_norm), _ptr(k_norm), eps,
                   _ptr(rope_cs), sin_off, rope_rows)

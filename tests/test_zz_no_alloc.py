@@ -1,0 +1,106 @@
+"""ns2_attention_noalloc (the allocation-free attention entry point) against ns2_attention, through
+the C ABI: identical results on two calls in a row -- the 832x1216 joint attention at batch 2,
+then a smaller DiT-style call on a packed qkv buffer with fused head norms -- plus a call on
+views that are not 16-byte aligned (its packed queries also come from the fixed array), the
+oracle on the small calls, and the size check that refuses a problem beyond the array."""
+
+import pytest
+import torch
+
+import oracle.nanosaur2_oracle as O
+from conftest import assert_close
+
+pytestmark = pytest.mark.gpu
+dev = "cuda"
+TOL = 2e-3
+
+
+def _joint_inputs(seed, L, T, batch):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(batch, L, 1536, generator=g)
+    k = torch.randn(batch, L + T, 1536, generator=g)
+    v = torch.randn(batch, L + T, 1536, generator=g)
+    lb = torch.log(torch.rand(batch, T, generator=g) + 0.5)
+    return q, k, v, lb
+
+
+def test_noalloc_matches_attention_two_calls(ns2lib):
+    # call 1: config 2 (76 x 52 latent = 3952 image tokens + 256 text tokens, batch 2)
+    L, T, B = 76 * 52, 256, 2
+    q, k, v, lb = _joint_inputs(5, L, T, B)
+    cs, sin_off = O.rope2d_table(76, 52)
+    qd, kd, vd, lbd, csd = q.to(dev), k.to(dev), v.to(dev), lb.to(dev), cs.to(dev)
+    outs = []
+    for noalloc in (False, True):
+        o = torch.full((B, L, 1536), float("nan"), device=dev)
+        ns2lib.attention(qd, kd, vd, o, Lq=L, Lk=L + T, H=16, D=96, ldq=1536, ldk=1536, ldv=1536, ldo=1536,
+                         batch=B, qBatch=L * 1536, kBatch=(L + T) * 1536, vBatch=(L + T) * 1536, oBatch=L * 1536,
+                         key_bias=lbd, biasStart=L, biasBatch=T, rope_cs=csd, sin_off=sin_off, rope_rows=L,
+                         noalloc=noalloc)
+        torch.cuda.synchronize()
+        outs.append(o.cpu())
+    assert torch.isfinite(outs[1]).all()
+    assert torch.equal(outs[0], outs[1]), "noalloc differs from ns2_attention at 3952x4208 batch 2"
+    print("[noalloc] call 1: 3952 x 4208 keys, batch 2: bit-identical to ns2_attention", flush=True)
+
+    # call 2, smaller: a packed [Lk, 3D] qkv buffer (the DiT's layout) with fused q/k norms and
+    # RoPE, 6 x 8 latent + 16 text tokens
+    h, w, T2 = 6, 8, 16
+    L2 = h * w
+    g = torch.Generator().manual_seed(6)
+    qkv = torch.randn(L2 + T2, 3 * 1536, generator=g)
+    qn = torch.randn(96, generator=g) * 0.5 + 1
+    kn = torch.randn(96, generator=g) * 0.5 + 1
+    lb2 = torch.log(torch.rand(T2, generator=g) + 0.5)
+    cs2, sin_off2 = O.rope2d_table(h, w)
+    qkv_d = qkv.to(dev)
+    outs = []
+    for noalloc in (False, True):
+        o = torch.full((L2, 1536), float("nan"), device=dev)
+        ns2lib.attention(qkv_d, qkv_d, qkv_d, o, Lq=L2, Lk=L2 + T2, H=16, D=96, ldq=4608, ldk=4608, ldv=4608,
+                         ldo=1536, qOff=0, kOff=1536, vOff=3072, key_bias=lb2.to(dev), biasStart=L2,
+                         q_norm=qn.to(dev), k_norm=kn.to(dev), rope_cs=cs2.to(dev), sin_off=sin_off2, rope_rows=L2,
+                         noalloc=noalloc)
+        torch.cuda.synchronize()
+        outs.append(o.cpu())
+    assert torch.equal(outs[0], outs[1]), "noalloc differs from ns2_attention on the packed qkv call"
+    ref_buf = qkv.double().clone()
+    O.head_norm_rope(ref_buf, qn.double(), L2, 16, 96, 4608, colOff=0, cs=cs2, sinOff=sin_off2)
+    O.head_norm_rope(ref_buf, kn.double(), L2, 16, 96, 4608, colOff=1536, cs=cs2, sinOff=sin_off2)
+    O.head_norm_rope(ref_buf, kn.double(), T2, 16, 96, 4608, colOff=1536, rowOff=L2)
+    bias = torch.cat([torch.zeros(L2, dtype=torch.float64), lb2.double()])
+    ref = O.attention_heads(ref_buf[:L2, :1536], ref_buf[:, 1536:3072], ref_buf[:, 3072:], 16, 96, bias)
+    assert_close(outs[1], ref, TOL, "noalloc call 2 (6x8 + 16 text, packed qkv, fused norms)")
+
+
+def test_noalloc_unaligned_views(ns2lib):
+    """Views shifted by one float: the packed queries are written to the fixed array too."""
+    L, T, Dm = 130, 20, 1536
+    ld = 3 * Dm + 1
+    g = torch.Generator().manual_seed(7)
+    qkv = torch.randn(L + T, ld, generator=g)
+    qkv_d = qkv.to(dev)
+    outs = []
+    for noalloc in (False, True):
+        o = torch.full((L, Dm), float("nan"), device=dev)
+        ns2lib.attention(qkv_d, qkv_d, qkv_d, o, Lq=L, Lk=L + T, H=16, D=96, ldq=ld, ldk=ld, ldv=ld, ldo=Dm,
+                         qOff=1, kOff=Dm + 1, vOff=2 * Dm + 1, noalloc=noalloc)
+        torch.cuda.synchronize()
+        outs.append(o.cpu())
+    assert torch.equal(outs[0], outs[1])
+    x = qkv.double()[:, 1:1 + 3 * Dm]
+    ref = O.attention_heads(x[:L, :Dm], x[:, Dm:2 * Dm], x[:, 2 * Dm:], 16, 96)
+    assert_close(outs[1], ref, TOL, "noalloc unaligned views")
+
+
+def test_noalloc_refuses_beyond_the_array(ns2lib):
+    """Batch 4 at 4208 keys needs ~104 MB of packed K/V: refused on the host, nothing launched."""
+    import ns2
+
+    L, Lk, B = 3952, 4208, 4
+    q = torch.empty(B, L, 1536, device=dev)
+    k = torch.empty(B, Lk, 1536, device=dev)
+    o = torch.empty(B, L, 1536, device=dev)
+    with pytest.raises(ns2.NS2Error, match="needs .* bytes of scratch"):
+        ns2lib.attention(q, k, k, o, Lq=L, Lk=Lk, H=16, D=96, ldq=1536, ldk=1536, ldv=1536, ldo=1536, batch=B,
+                         qBatch=L * 1536, kBatch=Lk * 1536, vBatch=Lk * 1536, oBatch=L * 1536, noalloc=True)
