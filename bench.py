@@ -1,30 +1,36 @@
 #!/usr/bin/env python3
 """Benchmark: ms per 832x1216 int8 DiT pass + joint-attention TFLOP/s on one MI355X.
 
-  python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-dit]
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-dit] [--no-gemma]
 
-1. DiT pass (the metric): the Node host (nanosaur2-web_amd/js/run_dit.js) runs one full pass
-   of the 18-block Nanosaur2 DiT at 832x1216 (latent 76 rows x 52 cols = 3952 image tokens,
-   256 text tokens, batch 1) on seeded random-init weights of the real architecture (int8
-   ConvRot block linears, bf16 elsewhere). W untimed passes, then K timed passes with the
-   latent tokens resident in device memory, bracketed by stream events and a device sync.
-   `value` is the median device time per pass in ms.
-   The dominant kernel of the pass is the tiled int8 ConvRot GEMM (qkv, proj, w12, w3, kv_y of
-   every block): a profiled run of the same pass times every launch with stream events on the
-   library's stream, and `roofline` is its algorithmic 2*M*N*K flops summed over the pass /
-   its summed launch time, against the 2516.6 TFLOP/s dense fp16 MFMA peak.
-2. Joint attention at the production shape (3952 queries x 4208 keys, 16 heads x 96, batch 2,
-   2-D RoPE on image rows, log-weight bias on the text keys) through the C ABI (ctypes);
-   the library's kernel profiler times each launch of the flash kernel with stream events,
-   which gives `roofline_attention` (algorithmic 4*Lq*Lk*D*H*B flops per launch / mean launch
-   time).
-3. Gemma3-270M text encoder (17 of 18 layers + final norm, 256 token ids, random-init bf16
-   weights of the real architecture) through the Node host (run_gemma.js): median device time
-   per encode, with the algorithmic flops of its linears (2*M*N*K) and attention (4*L*L*256*4);
-   `ms_graph` is the same encode recorded once as a HIP graph and replayed.
-4. CPU baseline: the oracle (a PyTorch-CPU restatement of tools/reference.py) on a bounded
-   sample -- one joint block and one image-only block at the full 3952-token shape -- scaled
-   to 18 blocks, on this host's cores.
+Prints one JSON line. Legs, in order:
+
+1. DiT pass (the metric, `value`): the Node host (nanosaur2-web_amd/js/run_dit.js) runs one full
+   pass of the 18-block Nanosaur2 DiT at 832x1216 (latent 76 rows x 52 cols = 3952 image tokens,
+   256 text tokens, batch 1) on seeded random-init weights of the real architecture (int8 ConvRot
+   block linears, bf16 elsewhere). W untimed passes, then K timed passes with the latent tokens
+   resident in device memory, bracketed by stream events and a device sync; `value` is the median
+   device time per pass. The region runs from the resident latent tokens to the resident x0
+   tokens and includes condition() and the text refine; `pass_ms_host_to_host` adds the latent
+   upload, the two device transposes and the x0 readback.
+   The dominant kernel is the tiled int8 ConvRot GEMM (qkv, proj, w12, w3, kv_y of every block):
+   a profiled run of the same pass times every launch with stream events on the library's
+   stream, and `roofline` is its algorithmic 2*M*N*K flops summed over the pass / its summed
+   launch time, against the 2516.6 TFLOP/s dense fp16 MFMA peak.
+2. Gemma3-270M text encoder (17 of 18 layers + final norm, 256 token ids, random-init bf16 weights
+   of the real architecture) through the Node host (run_gemma.js), eager and replayed as a graph.
+3. Through the C ABI (ctypes), each after 1 s of back-to-back warm-up calls, timed with stream
+   events and the library's per-kernel profiler:
+   - joint attention at 832x1216 (3952 queries x 4208 keys, 16 heads x 96, batch 2, 2-D RoPE on
+     image rows, log-weight bias on text keys): `roofline_attention` (flash kernel) and the
+     whole op (pack + flash);
+   - joint attention at 768x768 (2304 queries x 2432 keys, batch 1);
+   - the int8 ConvRot linear at M = 2432 on fp32 activations for N x K = 4608x1536, 1536x1536,
+     6144x1536 and 1536x6144: the rotation into the tiled fp16 operand plus the tiled GEMM.
+4. CPU baselines: the oracle (a PyTorch-CPU restatement of tools/reference.py, fp32) on this
+   host's cores for the same workloads -- the DiT pass on a bounded sample (one joint and one
+   image-only block at 3952 tokens, scaled to 18 blocks), the two attention shapes, the four
+   linears and the text encoder -- 1 warm-up and up to 3 timed repetitions each (median).
 """
 
 from __future__ import annotations
@@ -45,19 +51,48 @@ GEMMA_TOKENS, GEMMA_LAYERS = 256, 17
 METRIC = "ms per 832x1216 DiT pass (int8) + joint-attention TFLOP/s, 1 MI355X"
 PUBLISHED_PASS_MS = 1730.0   # README.md:86-88 of the reference (WebGPU, laptop GPU)
 FP16_PEAK_TFLOPS = 2516.6    # MI355X dense fp16 MFMA
+HBM_PEAK_GBS = 8000.0        # MI355X HBM3E
 H_IMG, W_IMG, T_TXT, D, HEADS, HD, I_MLP, BLOCKS = 76, 52, 256, 1536, 16, 96, 4096, 18
+CFG1_M = 2432
+CFG1_SHAPES = (("qkv", 4608, 1536), ("proj", 1536, 1536), ("up", 6144, 1536), ("down", 1536, 6144))
 # HBM bytes per launch from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE, each scaled by what the
-# counter reads for a copy kernel of known size (FETCH_SIZE x 2.0, WRITE_SIZE x 1.0), measured on
-# the current kernels (profiles/): the mean over the pass's 89 tiled-GEMM launches, and one flash
-# launch at the joint shape. Beside each, the algorithmic bytes of the same launches.
+# counter reads for a copy kernel of known size (FETCH_SIZE x 2.0, WRITE_SIZE x 1.0): the mean
+# over the pass's tiled-GEMM launches and one flash launch at 3952x4208 batch 2. Beside each, the
+# algorithmic bytes of the same launches. Source files name the commands.
 GEMM_TRAFFIC_BYTES_PER_LAUNCH = 148.2e6
 GEMM_ALGORITHMIC_BYTES_PER_LAUNCH = 67.5e6   # N*K int8 W + 2*M*K fp16 A + output (+ old output for +=)
+GEMM_TRAFFIC_SOURCE = "profiles/dit_pass_832x1216_int8.md"
 ATTN_TRAFFIC_BYTES_PER_LAUNCH = 173.9e6
 ATTN_ALGORITHMIC_BYTES_PER_LAUNCH = 149.1e6  # fp32 Q (read in the kernel's prologue), fp16 K, V^T, fp32 O
+ATTN_TRAFFIC_SOURCE = "profiles/attn_flash_joint_3952x4208_b2.md"
 
 
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def cpu_threads():
+    """Threads for the CPU baselines: this process's CPU share (affinity, OMP_NUM_THREADS)."""
+    n = os.cpu_count() or 1
+    try:
+        n = min(n, len(os.sched_getaffinity(0)))
+    except AttributeError:
+        pass
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    if omp.isdigit() and int(omp) > 0:
+        n = min(n, int(omp))
+    return n
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def pass_flops(L=H_IMG * W_IMG, T=T_TXT):
@@ -75,26 +110,27 @@ def pass_flops(L=H_IMG * W_IMG, T=T_TXT):
     return total
 
 
-def run_dit(steps, warmup):
-    cmd = ["node", RUN_DIT, "--synthetic", "3", "--shape", f"{H_IMG},{W_IMG},{T_TXT}",
-           "--warmup", str(warmup), "--reps", str(steps)]
+# ------------------------------------------------------------------------------ Node legs
+
+def run_node(script, args, what, timeout=900):
+    cmd = ["node", script] + args
     log(" ".join(cmd))
-    p = subprocess.run(cmd, capture_output=True, text=True, timeout=900)
-    sys.stderr.write(p.stderr[-3000:])
+    p = subprocess.run(cmd, capture_output=True, text=True, timeout=timeout)
     if p.returncode != 0:
-        raise SystemExit(f"run_dit.js failed with {p.returncode}")
+        sys.stderr.write(p.stderr[-3000:])
+        raise SystemExit(f"{what} failed with {p.returncode}")
     return json.loads(p.stdout.strip().splitlines()[-1])
 
 
+def run_dit(steps, warmup):
+    return run_node(RUN_DIT, ["--synthetic", "3", "--shape", f"{H_IMG},{W_IMG},{T_TXT}",
+                              "--warmup", str(warmup), "--reps", str(steps)], "run_dit.js")
+
+
 def run_dit_profile():
-    cmd = ["node", RUN_DIT, "--synthetic", "3", "--shape", f"{H_IMG},{W_IMG},{T_TXT}",
-           "--warmup", "1", "--reps", "2", "--profile"]
-    log(" ".join(cmd))
-    p = subprocess.run(cmd, capture_output=True, text=True, timeout=900)
-    if p.returncode != 0:
-        sys.stderr.write(p.stderr[-3000:])
-        raise SystemExit(f"run_dit.js --profile failed with {p.returncode}")
-    return json.loads(p.stdout.strip().splitlines()[-1]).get("profile", [])
+    r = run_node(RUN_DIT, ["--synthetic", "3", "--shape", f"{H_IMG},{W_IMG},{T_TXT}",
+                           "--warmup", "1", "--reps", "2", "--profile"], "run_dit.js --profile")
+    return r.get("profile", [])
 
 
 def gemma_flops(L=GEMMA_TOKENS):
@@ -106,20 +142,15 @@ def gemma_flops(L=GEMMA_TOKENS):
 
 
 def run_gemma(steps, warmup, graph=False):
-    cmd = ["node", RUN_GEMMA, "--synthetic", "3", "--tokens", f"{GEMMA_TOKENS},1",
-           "--warmup", str(warmup), "--reps", str(steps)] + (["--graph"] if graph else [])
-    log(" ".join(cmd))
-    p = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
-    if p.returncode != 0:
-        sys.stderr.write(p.stderr[-3000:])
-        raise SystemExit(f"run_gemma.js failed with {p.returncode}")
-    r = json.loads(p.stdout.strip().splitlines()[-1])
+    r = run_node(RUN_GEMMA, ["--synthetic", "3", "--tokens", f"{GEMMA_TOKENS},1", "--warmup", str(warmup),
+                             "--reps", str(steps)] + (["--graph"] if graph else []), "run_gemma.js", timeout=600)
     ms = r["ms_device_median"]
     fl = gemma_flops()
     return {"workload": f"Gemma3-270M text encoder, {GEMMA_LAYERS} layers + final norm, {GEMMA_TOKENS} tokens, "
                         "bf16 weights (fp16 matrix-core products, fp32 accumulation)",
             "ms": ms, "ms_wall": r["ms_wall_median"], "gflop": fl / 1e9,
-            "tflops": fl / (ms / 1e3) / 1e12, "ms_device": r["ms_device"]}
+            "tflops": fl / (ms / 1e3) / 1e12, "frac": fl / (ms / 1e3) / 1e12 / FP16_PEAK_TFLOPS,
+            "ms_device": r["ms_device"]}
 
 
 # int8 ConvRot linears of the pass (tiled GEMM launches), by the op names the DiT driver uses
@@ -140,34 +171,14 @@ def gemm_roofline(kernels):
     }
 
 
-def bench_attention(reps, warmup):
-    """Joint attention at the production shape, batch 2 (cond + uncond)."""
+# ------------------------------------------------------------------------------ C ABI legs
+
+def timed(lib, call, reps, warmup):
+    """Mean ms per call over `reps` back-to-back calls (stream events), and the library profiler's
+    mean ms per launch of each kernel, after at least `warmup` calls and one second of untimed
+    calls (the clocks a busy GPU settles at)."""
     import torch
 
-    sys.path.insert(0, PKG)
-    import ns2
-
-    lib = ns2.load(0, torch.cuda.current_stream().cuda_stream)
-    dev = "cuda"
-    L, B = H_IMG * W_IMG, 2
-    Lk = L + T_TXT
-    g = torch.Generator(device=dev).manual_seed(2)
-    q = torch.randn(B, L, D, device=dev, generator=g)
-    k = torch.randn(B, Lk, D, device=dev, generator=g)
-    v = torch.randn(B, Lk, D, device=dev, generator=g)
-    bias = torch.log(torch.rand(B, T_TXT, device=dev, generator=g) + 0.5)
-    o = torch.empty(B, L, D, device=dev)
-    cs = rope_table(H_IMG, W_IMG).to(dev)
-    sin_off = L * HD // 2
-
-    def call():
-        lib.attention(q, k, v, o, Lq=L, Lk=Lk, H=HEADS, D=HD, ldq=D, ldk=D, ldv=D, ldo=D, batch=B,
-                      qBatch=L * D, kBatch=Lk * D, vBatch=Lk * D, oBatch=L * D, key_bias=bias,
-                      biasStart=L, biasBatch=T_TXT, rope_cs=cs, sin_off=sin_off, rope_rows=L)
-
-    # untimed warmup: at least `warmup` calls and one second of back-to-back launches, so the
-    # timed calls run at the clocks a busy GPU settles at (this leg starts in a fresh process
-    # after the GPU has idled)
     t0 = time.perf_counter()
     n = 0
     while n < warmup or time.perf_counter() - t0 < 1.0:
@@ -185,41 +196,9 @@ def bench_attention(reps, warmup):
     lib.record(b)
     torch.cuda.synchronize()
     total_ms = lib.elapsed_ms(a, b) / reps
-    prof = lib.profile_report()
+    prof = {k: {"count": v["count"], "ms": v["ms"] / max(1, v["count"])} for k, v in lib.profile_report().items()}
     lib.profile(False)
-    flops = 4 * L * Lk * HD * HEADS * B
-    flash = prof.get("attn_flash", {"count": 0, "ms": 0})
-    pack = prof.get("attn_pack", {"count": 0, "ms": 0})
-    flash_ms = flash["ms"] / max(1, flash["count"])
-    pack_ms = pack["ms"] / max(1, pack["count"])
-    return {
-        "config": f"{L} queries x {Lk} keys ({L} image + {T_TXT} text), {HEADS} heads x {HD}, batch {B}, "
-                  "2-D RoPE on image rows, log-weight bias on text keys, fp32 in/out",
-        "gflop": flops / 1e9,
-        "ms": total_ms,
-        "tflops": flops / (total_ms / 1e3) / 1e12,
-        "flash_ms": flash_ms,
-        "flash_tflops": flops / (flash_ms / 1e3) / 1e12 if flash_ms else None,
-        "pack_ms": pack_ms,
-        "launches": flash["count"],
-        "flops_per_launch": flops,
-    }
-
-
-def copy_calibration(n=64 << 20, reps=3):
-    """ns2_elementwise copy of n fp32 values: 4n bytes read + 4n bytes written per launch,
-    the known-size kernel that HBM byte counters are scaled against."""
-    import torch
-
-    import ns2
-
-    lib = ns2.load(0)
-    a = torch.ones(n, device="cuda")
-    b = torch.empty(n, device="cuda")
-    for _ in range(reps):
-        lib.elementwise("copy", a, None, b, n)
-    torch.cuda.synchronize()
-    return {"kernel": "elementwise_kernel (copy)", "bytes_read": 4 * n, "bytes_written": 4 * n, "launches": reps}
+    return total_ms, prof
 
 
 def rope_table(h, w):
@@ -238,16 +217,191 @@ def rope_table(h, w):
     return torch.cat([ang.cos().reshape(-1), ang.sin().reshape(-1)]).float()
 
 
-def cpu_baseline():
+def attention_inputs(h, w, T, B, seed, device):
+    import torch
+
+    L = h * w
+    g = torch.Generator(device=device).manual_seed(seed)
+    q = torch.randn(B, L, D, device=device, generator=g)
+    k = torch.randn(B, L + T, D, device=device, generator=g)
+    v = torch.randn(B, L + T, D, device=device, generator=g)
+    bias = torch.log(torch.rand(B, T, device=device, generator=g) + 0.5)
+    return q, k, v, bias
+
+
+def bench_attention(lib, h, w, T, B, reps, warmup):
+    """Joint attention (image + text keys) through ns2_attention: flash kernel and whole op."""
+    import torch
+
+    L = h * w
+    Lk = L + T
+    q, k, v, bias = attention_inputs(h, w, T, B, 2, "cuda")
+    o = torch.empty(B, L, D, device="cuda")
+    cs = rope_table(h, w).to("cuda")
+
+    def call():
+        lib.attention(q, k, v, o, Lq=L, Lk=Lk, H=HEADS, D=HD, ldq=D, ldk=D, ldv=D, ldo=D, batch=B,
+                      qBatch=L * D, kBatch=Lk * D, vBatch=Lk * D, oBatch=L * D, key_bias=bias,
+                      biasStart=L, biasBatch=T, rope_cs=cs, sin_off=L * HD // 2, rope_rows=L)
+
+    total_ms, prof = timed(lib, call, reps, warmup)
+    flops = 4 * L * Lk * HD * HEADS * B
+    flash_ms = prof["attn_flash"]["ms"]
+    pack_ms = prof["attn_pack"]["ms"]
+    tf = lambda ms: flops / (ms / 1e3) / 1e12  # noqa: E731
+    return {
+        "config": f"{L} queries x {Lk} keys ({h}x{w} image + {T} text), {HEADS} heads x {HD}, batch {B}, "
+                  "2-D RoPE on image rows, log-weight bias on text keys, fp32 in/out",
+        "gflop": flops / 1e9,
+        "ms": total_ms, "tflops": tf(total_ms), "frac": tf(total_ms) / FP16_PEAK_TFLOPS,
+        "flash_ms": flash_ms, "flash_tflops": tf(flash_ms), "flash_frac": tf(flash_ms) / FP16_PEAK_TFLOPS,
+        "pack_ms": pack_ms, "flops_per_launch": flops,
+    }
+
+
+def bench_linear_cfg1(lib, reps, warmup):
+    """The int8 ConvRot linear at M = 2432 on fp32 activations: rotation into the tiled fp16
+    operand (ns2_rotate_f16) + the tiled GEMM (ns2_linear_i8_tiled) on a weight re-tiled once."""
+    import torch
+
+    M = CFG1_M
+    out = []
+    g = torch.Generator(device="cuda").manual_seed(1)
+    for name, N, K in CFG1_SHAPES:
+        x = torch.randn(M, K, device="cuda", generator=g)
+        q = torch.randint(-127, 128, (N, K), device="cuda", generator=g, dtype=torch.int32).to(torch.int8)
+        s = torch.rand(N, device="cuda", generator=g) * 9e-3 + 1e-3
+        wt = torch.empty(N * K, dtype=torch.int8, device="cuda")
+        lib.tile_i8_weight(q, wt, N, K)
+        at = torch.empty((M + 63) // 64 * 64, K, dtype=torch.int16, device="cuda")
+        y = torch.empty(M, N, device="cuda")
+
+        def call():
+            lib.rotate_f16(x, K, at, K, M, K, tiled=True)
+            lib.linear_i8_tiled(at, wt, s, y, M, N, K)
+
+        total_ms, prof = timed(lib, call, reps, warmup)
+        flops = 2 * M * N * K
+        nbytes = N * K + 4 * N + 4 * M * K + 4 * M * N   # int8 W, scales, fp32 x in, fp32 y out
+        gemm_ms, rot_ms = prof["gemm_i8_tiled"]["ms"], prof["rotate_f16"]["ms"]
+        tf = lambda ms: flops / (ms / 1e3) / 1e12  # noqa: E731
+        out.append({
+            "shape": f"{name}: M {M} x N {N} x K {K}", "gflop": flops / 1e9, "algorithmic_mb": nbytes / 1e6,
+            "ms": total_ms, "tflops": tf(total_ms), "frac": tf(total_ms) / FP16_PEAK_TFLOPS,
+            "gbs": nbytes / (total_ms / 1e3) / 1e9,
+            "gemm_ms": gemm_ms, "gemm_tflops": tf(gemm_ms), "gemm_frac": tf(gemm_ms) / FP16_PEAK_TFLOPS,
+            "rotate_ms": rot_ms, "rotate_gbs": M * K * 6 / (rot_ms / 1e3) / 1e9,
+        })
+        del x, q, s, wt, at, y
+    return out
+
+
+def copy_calibration(lib, n=64 << 20, reps=3):
+    """ns2_elementwise copy of n fp32 values: 4n bytes read + 4n bytes written per launch,
+    the known-size kernel that HBM byte counters are scaled against."""
+    import torch
+
+    a = torch.ones(n, device="cuda")
+    b = torch.empty(n, device="cuda")
+    for _ in range(reps):
+        lib.elementwise("copy", a, None, b, n)
+    torch.cuda.synchronize()
+    return {"kernel": "elementwise_kernel (copy)", "bytes_read": 4 * n, "bytes_written": 4 * n, "launches": reps}
+
+
+# ------------------------------------------------------------------------------ CPU legs
+
+def cpu_time(fn, max_reps=3, long_s=3.0):
+    """1 untimed warm-up call, then up to max_reps timed calls (1 when a call takes longer than
+    long_s); returns the median in ms and the repetitions."""
+    fn()
+    times = []
+    for _ in range(max_reps):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+        if times[0] > long_s:
+            break
+    return statistics.median(times) * 1e3, len(times)
+
+
+def cpu_attention(h, w, T, B):
+    import torch
+
+    import oracle.nanosaur2_oracle as O
+
+    L = h * w
+    q, k, v, bias = attention_inputs(h, w, T, B, 2, "cpu")
+    cos, sin = O.rope_2d(h, w)
+
+    def run():
+        with torch.no_grad():
+            for b in range(B):
+                O.joint_attention_op(q[b], k[b], v[b], L, cos, sin, key_bias=bias[b], bias_start=L)
+
+    ms, n = cpu_time(run)
+    flops = 4 * L * (L + T) * HD * HEADS * B
+    return {"value": ms, "unit": "ms per call", "tflops": flops / (ms / 1e3) / 1e12, "reps": n,
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"the whole op (RoPE, bias, softmax(QK^T/sqrt(96))V), fp32 PyTorch CPU, batch {B}"}
+
+
+def cpu_linear_cfg1():
+    import torch
+
+    import oracle.nanosaur2_oracle as O
+
+    g = torch.Generator().manual_seed(1)
+    rows = []
+    for name, N, K in CFG1_SHAPES:
+        x = torch.randn(CFG1_M, K, generator=g)
+        q = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int32).to(torch.int8)
+        s = torch.rand(N, 1, generator=g) * 9e-3 + 1e-3
+        with torch.no_grad():
+            ms, n = cpu_time(lambda: O.linear_i8(x, q, s))
+        rows.append({"shape": name, "ms": ms, "tflops": 2 * CFG1_M * N * K / (ms / 1e3) / 1e12, "reps": n})
+    return {"rows": rows, "unit": "ms per linear", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": "ops.linear on the int8 weight: rotation of x per 256-group, x_r q^T, row scale; fp32 PyTorch CPU"}
+
+
+def cpu_gemma():
+    """The oracle's Gemma3 encode of 256 tokens on seeded weights of the real architecture; the
+    embedding table holds 4096 rows (the gather is a negligible share of the work)."""
+    import torch
+
+    import oracle.nanosaur2_oracle as O
+
+    g = torch.Generator().manual_seed(4)
+    t = {"model.embed_tokens.weight": torch.randn(4096, 640, generator=g).to(torch.bfloat16)}
+    shapes = {"self_attn.q_proj.weight": (1024, 640), "self_attn.k_proj.weight": (256, 640),
+              "self_attn.v_proj.weight": (256, 640), "self_attn.o_proj.weight": (640, 1024),
+              "mlp.gate_proj.weight": (2048, 640), "mlp.up_proj.weight": (2048, 640),
+              "mlp.down_proj.weight": (640, 2048)}
+    for i in range(GEMMA_LAYERS):
+        p = f"model.layers.{i}."
+        for n, shp in shapes.items():
+            t[p + n] = (torch.randn(*shp, generator=g) * 0.02).to(torch.bfloat16)
+        for n in ("input_layernorm", "post_attention_layernorm", "pre_feedforward_layernorm",
+                  "post_feedforward_layernorm"):
+            t[p + n + ".weight"] = (torch.randn(640, generator=g) * 0.1).to(torch.bfloat16)
+        t[p + "self_attn.q_norm.weight"] = (torch.randn(256, generator=g) * 0.1).to(torch.bfloat16)
+        t[p + "self_attn.k_norm.weight"] = (torch.randn(256, generator=g) * 0.1).to(torch.bfloat16)
+    t["model.norm.weight"] = (torch.randn(640, generator=g) * 0.1).to(torch.bfloat16)
+    W = O.TensorWeights(t)
+    ids = torch.randint(0, 4096, (GEMMA_TOKENS,), generator=g).tolist()
+    with torch.no_grad():
+        ms, n = cpu_time(lambda: O.gemma_encode(W, ids))
+    return {"value": ms, "unit": "ms per encode", "tflops": gemma_flops() / (ms / 1e3) / 1e12, "reps": n,
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"{GEMMA_LAYERS} layers + final norm, {GEMMA_TOKENS} tokens, fp32 PyTorch CPU"}
+
+
+def cpu_dit_pass():
     """Oracle (PyTorch CPU, fp32) on one joint and one image-only block at full size."""
     import torch
 
-    sys.path.insert(0, ROOT)
     import oracle.nanosaur2_oracle as O
 
-    torch.manual_seed(0)
-    threads = os.cpu_count() or 1
-    torch.set_num_threads(threads)
     L, T = H_IMG * W_IMG, T_TXT
     gen = torch.Generator().manual_seed(5)
     t = {}
@@ -302,24 +456,15 @@ def cpu_baseline():
     }
 
 
-def cpu_model():
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
-    except OSError:
-        pass
-    return "unknown"
-
+# ------------------------------------------------------------------------------ main
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--no-dit", action="store_true", help="only the joint-attention measurement")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
+    ap.add_argument("--no-dit", action="store_true", help="skip the DiT pass (kernels and CPU legs only)")
     ap.add_argument("--no-gemma", action="store_true", help="skip the text-encoder measurement")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a 256 MiB -> 256 MiB copy kernel (reference point for HBM counters)")
@@ -336,7 +481,8 @@ def main():
         dit = run_dit(args.steps, args.warmup)
         kernels = run_dit_profile()
         gemm = gemm_roofline(kernels)
-        log(f"int8 GEMMs: {gemm['ms_per_pass']:.3f} ms/pass, {gemm['tflops']:.1f} TFLOP/s")
+        log(f"DiT pass {dit['ms_device_median']:.3f} ms; int8 GEMMs {gemm['ms_per_pass']:.3f} ms/pass, "
+            f"{gemm['tflops']:.1f} TFLOP/s")
     gemma = None
     if not args.no_gemma:
         gemma = run_gemma(max(10, args.steps), max(3, args.warmup))
@@ -345,11 +491,42 @@ def main():
         gemma["ms_graph"], gemma["ms_graph_wall"] = replay["ms"], replay["ms_wall"]
         log(f"text encoder: {gemma['ms']:.3f} ms per {GEMMA_TOKENS}-token encode, {gemma['tflops']:.1f} TFLOP/s "
             f"(graph replay {gemma['ms_graph']:.3f} ms)")
-    attn = bench_attention(reps=max(10, args.steps), warmup=max(2, args.warmup))
+
+    import torch
+
+    sys.path.insert(0, PKG)
+    import ns2
+
+    lib = ns2.load(0, torch.cuda.current_stream().cuda_stream)
+    reps = max(10, args.steps)
+    attn = bench_attention(lib, H_IMG, W_IMG, T_TXT, 2, reps, max(2, args.warmup))
+    log(f"attention 3952x4208 b2: {attn['ms']:.3f} ms/call, flash {attn['flash_ms']:.3f} ms "
+        f"({attn['flash_tflops']:.1f} TFLOP/s)")
+    attn0 = bench_attention(lib, 48, 48, 128, 1, reps, max(2, args.warmup))
+    log(f"attention 2304x2432: {attn0['ms']:.3f} ms/call, flash {attn0['flash_tflops']:.1f} TFLOP/s")
+    lin1 = bench_linear_cfg1(lib, reps, max(2, args.warmup))
+    for r in lin1:
+        log(f"linear {r['shape']}: {r['ms'] * 1e3:.1f} us ({r['tflops']:.0f} TFLOP/s with rotation, "
+            f"GEMM {r['gemm_tflops']:.0f})")
     if args.copy_calibration:
-        attn["copy_calibration"] = copy_calibration()
-    log(f"attention: {attn['ms']:.3f} ms/call, flash {attn['flash_ms']:.3f} ms ({attn['flash_tflops']:.1f} TFLOP/s)")
-    cpu = None if args.no_cpu else cpu_baseline()
+        attn["copy_calibration"] = copy_calibration(lib)
+
+    cpu = None
+    if not args.no_cpu:
+        sys.path.insert(0, ROOT)
+        torch.set_num_threads(cpu_threads())
+        log(f"CPU baselines on {torch.get_num_threads()} threads ({cpu_model()})")
+        cpu = cpu_dit_pass()
+        attn["cpu_baseline"] = cpu_attention(H_IMG, W_IMG, T_TXT, 2)
+        attn0["cpu_baseline"] = cpu_attention(48, 48, 128, 1)
+        lin1_cpu = cpu_linear_cfg1()
+        for r, c in zip(lin1, lin1_cpu["rows"]):
+            r["cpu_ms"], r["cpu_tflops"] = c["ms"], c["tflops"]
+        lin1_meta = {k: v for k, v in lin1_cpu.items() if k != "rows"}
+        if gemma:
+            gemma["cpu_baseline"] = cpu_gemma()
+    else:
+        lin1_meta = None
 
     ms = dit["ms_device_median"] if dit else None
     out = {
@@ -371,11 +548,17 @@ def main():
                         "block linears, batch 1",
             "tokens": H_IMG * W_IMG, "text_tokens": T_TXT, "blocks": BLOCKS, "parallelism": "none (1 GPU)",
         },
+        "value_region": "device time from the latent tokens resident in HBM to the x0 tokens in HBM, including "
+                        "condition() and the text refine; the reference's pass time also includes the latent "
+                        "upload and x0 readback, reported here as pass_ms_host_to_host",
         "pass_tflop": flops / 1e12,
         "pass_tflops": (flops / (ms / 1e3) / 1e12) if ms else None,
         "pass_ms_wall": dit["ms_wall_median"] if dit else None,
         "pass_ms_host_to_host": dit["ms_host_to_host_median"] if dit else None,
+        "weight_bytes": dit.get("weight_bytes") if dit else None,
         "joint_attention": attn,
+        "joint_attention_768": attn0,
+        "linear_int8_m2432": {"rows": lin1, "cpu_baseline": lin1_meta},
         "text_encoder": gemma,
         "gemm_i8": gemm,
         "roofline": {
@@ -387,6 +570,7 @@ def main():
             "frac": gemm["tflops"] / FP16_PEAK_TFLOPS if gemm and gemm["tflops"] else None,
             "traffic": GEMM_TRAFFIC_BYTES_PER_LAUNCH,
             "traffic_algorithmic": GEMM_ALGORITHMIC_BYTES_PER_LAUNCH,
+            "traffic_source": GEMM_TRAFFIC_SOURCE,
         },
         "roofline_attention": {
             "kernel": "flash_kernel (joint attention, 3952x4208, batch 2)",
@@ -394,9 +578,11 @@ def main():
             "achieved": attn["flash_tflops"],
             "peak": FP16_PEAK_TFLOPS,
             "unit": "TFLOP/s",
-            "frac": attn["flash_tflops"] / FP16_PEAK_TFLOPS if attn["flash_tflops"] else None,
+            "frac": attn["flash_frac"],
+            "whole_op_frac": attn["frac"],
             "traffic": ATTN_TRAFFIC_BYTES_PER_LAUNCH,
             "traffic_algorithmic": ATTN_ALGORITHMIC_BYTES_PER_LAUNCH,
+            "traffic_source": ATTN_TRAFFIC_SOURCE,
         },
         "cpu_baseline": cpu,
         "kernels": kernels,
