@@ -230,6 +230,19 @@ int ns2_attention(const float* q, const float* k, const float* v, float* o, int 
                   const float* q_norm, const float* k_norm, float eps, const float* rope_cs,
                   long long sin_off, int rope_rows);
 
+/* ns2_attention (batch 1) whose key and value rows from text_start on come from a second view:
+ * key row r >= text_start is k_text[(r - text_start) * ld_text + h*D ..], value row likewise in
+ * v_text; rows below text_start come from k / v as in ns2_attention. This is the DiT's joint
+ * attention with the text keys projected apart from the image rows (app/models/nanosaur2.js:
+ * 199-208: rows [L, L + T) of qkv hold the kv_y projection of the text; here the projections
+ * of all joint blocks run as one GEMM and each block's attention reads its columns). k_norm
+ * and the key bias apply to the text rows as to the others; RoPE only to rows < rope_rows. */
+int ns2_attention_text(const float* q, const float* k, const float* v, float* o, int Lq, int Lk, int H, int D,
+                       int ldq, int ldk, int ldv, int ldo, long long qOff, long long kOff, long long vOff,
+                       long long oOff, float scale, const float* key_bias, int biasStart, const float* q_norm,
+                       const float* k_norm, float eps, const float* rope_cs, long long sin_off, int rope_rows,
+                       const float* k_text, const float* v_text, int ld_text, int text_start);
+
 /* Bytes of the fixed device scratch array behind ns2_attention_noalloc (one per GPU, held
  * until the process ends). */
 #define NS2_NOALLOC_SCRATCH_BYTES (64u << 20)

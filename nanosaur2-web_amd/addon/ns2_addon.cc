@@ -504,6 +504,34 @@ napi_value Attention(napi_env env, napi_callback_info info) {
                                      qB, kB, vB, oB, scale, kb, biasStart, biasBatch, qn, kn, eps, cs, sinOff, ropeRows));
 }
 
+// attentionText(q, k, v, o, Lq, Lk, H, D, ldq, ldk, ldv, ldo, qOff, kOff, vOff, oOff, scale, keyBias,
+//               biasStart, qNorm, kNorm, eps, ropeCs, sinOff, ropeRows, kText, vText, ldText, textStart)
+napi_value AttentionText(napi_env env, napi_callback_info info) {
+  ARGS(29);
+  auto q = (const float*)c.ptr(0);
+  auto k = (const float*)c.ptr(1);
+  auto v = (const float*)c.ptr(2);
+  auto o = (float*)c.ptr(3);
+  int Lq = c.i32(4), Lk = c.i32(5), H = c.i32(6), D = c.i32(7);
+  int ldq = c.i32(8), ldk = c.i32(9), ldv = c.i32(10), ldo = c.i32(11);
+  long long qOff = c.i64(12), kOff = c.i64(13), vOff = c.i64(14), oOff = c.i64(15);
+  float scale = c.f32(16);
+  auto kb = (const float*)c.ptr(17);
+  int biasStart = c.i32(18);
+  auto qn = (const float*)c.ptr(19);
+  auto kn = (const float*)c.ptr(20);
+  float eps = c.f32(21);
+  auto cs = (const float*)c.ptr(22);
+  long long sinOff = c.i64(23);
+  int ropeRows = c.i32(24);
+  auto kt = (const float*)c.ptr(25);
+  auto vt = (const float*)c.ptr(26);
+  int ldText = c.i32(27), textStart = c.i32(28);
+  if (c.failed) return nullptr;
+  return check(env, c, ns2_attention_text(q, k, v, o, Lq, Lk, H, D, ldq, ldk, ldv, ldo, qOff, kOff, vOff, oOff, scale,
+                                          kb, biasStart, qn, kn, eps, cs, sinOff, ropeRows, kt, vt, ldText, textStart));
+}
+
 // attentionRows(q, k, v, o, Lq, Lk, H, D, ldq, ldk, ldv, ldo, qOff, kOff, vOff, group, causal)
 napi_value AttentionRows(napi_env env, napi_callback_info info) {
   ARGS(17);
@@ -706,7 +734,7 @@ napi_value Module(napi_env env, napi_value exports) {
       {"tileI8Weight", TileI8Weight}, {"linearI8Tiled", LinearI8Tiled},
       {"tileI8WeightGlu", TileI8WeightGlu}, {"linearI8GluRotTiled", LinearI8GluRotTiled},
       {"linearI8", LinearI8}, {"linearBf16", LinearBf16}, {"attention", Attention},
-      {"attentionRows", AttentionRows},
+      {"attentionRows", AttentionRows}, {"attentionText", AttentionText},
       {"headNorm", HeadNorm}, {"headNorm2", HeadNorm2}, {"normMod", NormModT<false>}, {"normModRotateF16", NormModT<true>},
       {"glu", GluT<false>}, {"gluRotateF16", GluT<true>}, {"elementwise", Elementwise},
       {"accumulate", Accumulate}, {"addRows", AddRows}, {"rowSum", RowSum}, {"rmsnorm", Rmsnorm},

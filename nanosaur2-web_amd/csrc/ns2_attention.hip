@@ -55,7 +55,22 @@ struct PackArgs {
   int Lq, Lk, Lq_pad, Lk_pad, H, ldq, ldk, ldv, biasStart, rope_rows;
   float qscale, eps;
   int skip_q;  // the flash kernel prepares Q itself (vectorized pack only)
+  // K and V rows from kv2_start on come from a second view (the DiT's text keys, projected
+  // apart from the image rows): row r at k2 / v2 + (r - kv2_start) * ld2; null: one view
+  const float* k2;
+  const float* v2;
+  int ld2, kv2_start;
 };
+
+// Row r of head 0 in the K and V views of batch element b.
+__device__ __forceinline__ const float* key_row(const PackArgs& a, int b, int r) {
+  return a.k2 && r >= a.kv2_start ? a.k2 + (long long)(r - a.kv2_start) * a.ld2
+                                  : a.k + a.kOff + b * a.kBatch + (long long)r * a.ldk;
+}
+__device__ __forceinline__ const float* value_row(const PackArgs& a, int b, int r) {
+  return a.v2 && r >= a.kv2_start ? a.v2 + (long long)(r - a.kv2_start) * a.ld2
+                                  : a.v + a.vOff + b * a.vBatch + (long long)r * a.ldv;
+}
 
 // Per-row prologue for one head row of D values, 4 threads per row: thread part p owns
 // the rope pairs i in [p*D/8, (p+1)*D/8), i.e. dims i and i + D/2.
@@ -131,14 +146,14 @@ __global__ __launch_bounds__(256) void attn_pack_kernel(PackArgs a) {
 
   // K rows -> LDS, V rows -> LDS transposed
   if (row < a.Lk) {
-    const float* src = a.k + a.kOff + b * a.kBatch + (long long)row * a.ldk + (long long)h * D;
+    const float* src = key_row(a, b, row) + (long long)h * D;
     prep_row<D>(src, a.k_norm, a.cs, a.sinOff, row, a.cs && row < a.rope_rows, 1.0f, a.eps, part, &ktile[rl][0]);
   } else {
 #pragma unroll
     for (int j = 0; j < D / 4; ++j) ktile[rl][part * (D / 4) + j] = (half_t)0.f;
   }
   {
-    const float* src = a.v + a.vOff + b * a.vBatch + (long long)row * a.ldv + (long long)h * D;
+    const float* src = value_row(a, b, row < a.Lk ? row : a.Lk - 1) + (long long)h * D;
 #pragma unroll
     for (int j = 0; j < D / 4; ++j) {
       const int d = part * (D / 4) + j;
@@ -257,7 +272,7 @@ __global__ __launch_bounds__(256) void attn_pack_vec_kernel(PackArgs a) {
     for (int e = 0; e < 8; ++e) {
       const int key = row0 + vkey_pos(kc * 8 + e);
       const int kr = key < a.Lk ? key : a.Lk - 1;
-      const float* src = a.v + a.vOff + b * a.vBatch + (long long)kr * a.ldv + (long long)h * D + dg * DPL;
+      const float* src = value_row(a, b, kr) + (long long)h * D + dg * DPL;
 #pragma unroll
       for (int j = 0; j < DPL; ++j) vv[e][j] = src[j];
     }
@@ -290,7 +305,7 @@ __global__ __launch_bounds__(256) void attn_pack_vec_kernel(PackArgs a) {
     }
   } else if (kv) {
     if (row < a.Lk) {
-      const float* src = a.k + a.kOff + b * a.kBatch + (long long)row * a.ldk + (long long)h * D;
+      const float* src = key_row(a, b, row) + (long long)h * D;
       prep_half_row<D>(src, a.k_norm, a.cs, a.sinOff, row, a.cs && row < a.rope_rows, 1.0f, a.eps, hh, x1, x2);
     } else {
 #pragma unroll
@@ -355,18 +370,23 @@ struct FlashArgs {
 // rescale. Any reference gives the same softmax, and p <= 2^kRebase stays in fp16 range.
 constexpr float kRebase = 8.0f;
 
-template <int D, int QT, int NW, int STAGES>
+// SUPER: 64-key tiles per LDS stage. The loads of a stage are issued together and waited for
+// with one barrier, so a barrier falls on every SUPER-th step and a stage's loads are issued
+// (STAGES - 2) * SUPER + 1 .. (STAGES - 1) * SUPER steps before its K fragments are read.
+template <int D, int QT, int NW, int STAGES, int SUPER>
 __global__ __launch_bounds__(NW * 64) void flash_kernel(FlashArgs a) {
   constexpr int DC = D / 16;             // k-steps of S
   constexpr int DT = D / 32;             // dim tiles of O
   constexpr int TILE = KB * D;           // halfs per K (or V) tile image
-  constexpr int BLOCKS = 2 * TILE / 512; // 1 KB direct-load blocks per stage (K then V)
-  static_assert(STAGES == 3 || STAGES == 4, "three or four LDS stages");
+  constexpr int BLOCKS = 2 * TILE / 512; // 1 KB direct-load blocks per tile (K then V)
+  constexpr int NSLOT = STAGES * SUPER;  // tile slots in LDS; tile t lives in slot t % NSLOT
+  static_assert(STAGES == 3 || (STAGES == 4 && SUPER == 1), "three stages, or four of one tile");
+  static_assert(SUPER == 1 || SUPER == 2, "one or two tiles per stage");
 
-  // K of tile t+1 and V of tile t are read while tiles t+2 .. t+STAGES-1 land
-  __shared__ __attribute__((aligned(16))) half_t ks[STAGES][TILE];
-  __shared__ __attribute__((aligned(16))) half_t vts[STAGES][TILE];
-  __shared__ __attribute__((aligned(16))) float kbias[STAGES][KB];
+  // K of tile t+1 and V of tile t are read while the later stages land
+  __shared__ __attribute__((aligned(16))) half_t ks[NSLOT][TILE];
+  __shared__ __attribute__((aligned(16))) half_t vts[NSLOT][TILE];
+  __shared__ __attribute__((aligned(16))) float kbias[NSLOT][KB];
 
   // Work unit: (pair = batch*H + head, query block). With xcd_order, consecutive block ids
   // land on different XCDs (round-robin dispatch), so block id i is mapped to pair
@@ -604,10 +624,12 @@ __global__ __launch_bounds__(NW * 64) void flash_kernel(FlashArgs a) {
   // Steps alternate the two score buffers (A holds tile t, B receives tile t+1).
   float16_t sA[2][QT], sB[2][QT];
   float mA[QT], mB[QT];
-  for (int i = 0; i < STAGES - 1 && i < ntiles; ++i) dma(i, i);
+  const int issued = (STAGES - 1) * SUPER < ntiles ? (STAGES - 1) * SUPER : ntiles;
+  for (int i = 0; i < issued; ++i) dma(i, i);
   {
-    // tile 0 has landed once at most the tiles issued after it remain in flight
-    const int newer = (STAGES - 2 < ntiles - 1 ? STAGES - 2 : ntiles - 1);
+    // the first stage (tiles 0 .. SUPER-1) has landed once at most the tiles issued after it
+    // remain in flight
+    const int newer = issued - (SUPER < ntiles ? SUPER : ntiles);
     if (newer >= 2) wait_newer(W2_{});
     else if (newer == 1) wait_newer(W1_{});
     else wait_newer(W0_{});
@@ -624,17 +646,24 @@ __global__ __launch_bounds__(NW * 64) void flash_kernel(FlashArgs a) {
   }
 
   auto step = [&](int t, float16_t (&s_cur)[2][QT], float16_t (&s_nxt)[2][QT], float (&mx_cur)[QT],
-                  float (&mx_nxt)[QT], auto more_c, auto bias_c) {
+                  float (&mx_nxt)[QT], auto more_c, auto bias_c, auto sync_c) {
     constexpr bool MORE = decltype(more_c)::value;
     constexpr bool BIAS = decltype(bias_c)::value;  // tile t+1 carries a key bias
-    const int vbuf = t % STAGES, kbuf = (t + 1) % STAGES;
-    // tile t+1 has landed once at most the tiles issued after it remain in flight; the barrier
-    // then covers every wave's loads, and every wave's reads of tile t-1, whose stage the next
-    // loads overwrite
-    if (MORE && STAGES == 4 && t + 2 < ntiles) wait_newer(W1_{});
-    else wait_newer(W0_{});
-    __syncthreads();
-    if (MORE && t + STAGES - 1 < ntiles) dma(t + STAGES - 1, (t + STAGES - 1) % STAGES);
+    constexpr bool SYNC = decltype(sync_c)::value;  // t is the first tile of its stage
+    const int vbuf = t % NSLOT, kbuf = (t + 1) % NSLOT;
+    // On the first step of stage u: the next stage (which holds tile t+1 for SUPER = 1, and the
+    // K of tile t+SUPER that step t+SUPER-1 reads) has landed once at most the tiles issued after
+    // it remain in flight; the barrier then covers every wave's loads, and every wave's reads of
+    // stage u-1, which the loads of stage u+STAGES-1 overwrite
+    if (SYNC) {
+      if (MORE && STAGES == 4 && t + 2 < ntiles) wait_newer(W1_{});
+      else wait_newer(W0_{});
+      __syncthreads();
+      const int first = (t / SUPER + STAGES - 1) * SUPER;
+#pragma unroll
+      for (int r = 0; r < SUPER; ++r)
+        if (MORE && first + r < ntiles) dma(first + r, (first + r) % NSLOT);
+    }
 
     // ---- move the reference when a score exceeds it by more than 2^kRebase, or when nothing
     // has been accumulated yet (l = 0: the tile maximum becomes the reference, so the largest
@@ -761,20 +790,22 @@ __global__ __launch_bounds__(NW * 64) void flash_kernel(FlashArgs a) {
   int tb = a.bias_block0 - 1;
   tb = tb < 0 ? 0 : (tb > ntiles - 1 ? ntiles - 1 : tb);
   tb &= ~1;
+  // steps go in pairs from an even t, so with SUPER = 2 the first step of a pair starts a stage
+  using S2_ = std::integral_constant<bool, SUPER == 1>;
   int t = 0;
   for (; t < tb; t += 2) {
-    step(t, sA, sB, mA, mB, T_{}, F_{});
-    step(t + 1, sB, sA, mB, mA, T_{}, F_{});
+    step(t, sA, sB, mA, mB, T_{}, F_{}, T_{});
+    step(t + 1, sB, sA, mB, mA, T_{}, F_{}, S2_{});
   }
   for (; t + 2 < ntiles; t += 2) {
-    step(t, sA, sB, mA, mB, T_{}, T_{});
-    step(t + 1, sB, sA, mB, mA, T_{}, T_{});
+    step(t, sA, sB, mA, mB, T_{}, T_{}, T_{});
+    step(t + 1, sB, sA, mB, mA, T_{}, T_{}, S2_{});
   }
   if (t + 1 < ntiles) {
-    step(t, sA, sB, mA, mB, T_{}, T_{});
-    step(t + 1, sB, sA, mB, mA, F_{}, F_{});
+    step(t, sA, sB, mA, mB, T_{}, T_{}, T_{});
+    step(t + 1, sB, sA, mB, mA, F_{}, F_{}, S2_{});
   } else {
-    step(t, sA, sB, mA, mB, F_{}, F_{});
+    step(t, sA, sB, mA, mB, F_{}, F_{}, T_{});
   }
 
   // ---- normalise and store: o[qt][dt][r] = O[query lq][dim dt*32 + 8(r/4) + 4hi + r%4]
@@ -796,13 +827,13 @@ __global__ __launch_bounds__(NW * 64) void flash_kernel(FlashArgs a) {
   }
 }
 
-template <int D, int QT, int NW, int STAGES = 3>
+template <int D, int QT, int NW, int STAGES = 3, int SUPER = 1>
 void launch_flash(FlashArgs fa, hipStream_t s) {
   constexpr int BQ = NW * QT * 32;
   fa.qblocks = (fa.Lq + BQ - 1) / BQ;
   const int blocks = fa.qblocks * fa.pairs;
   fa.xcd_order = (fa.pairs % 8 == 0) ? 1 : 0;
-  flash_kernel<D, QT, NW, STAGES><<<blocks, NW * 64, 0, s>>>(fa);
+  flash_kernel<D, QT, NW, STAGES, SUPER><<<blocks, NW * 64, 0, s>>>(fa);
 }
 
 template <int D>
@@ -1133,7 +1164,8 @@ int attention_call(const char* fn, bool noalloc, const float* q, const float* k,
                    long long kOff, long long vOff, long long oOff, long long qBatch, long long kBatch,
                    long long vBatch, long long oBatch, float scale, const float* key_bias, int biasStart,
                    long long biasBatch, const float* q_norm, const float* k_norm, float eps,
-                   const float* rope_cs, long long sin_off, int rope_rows) {
+                   const float* rope_cs, long long sin_off, int rope_rows, const float* k_text = nullptr,
+                   const float* v_text = nullptr, int ld_text = 0, int text_start = 0) {
   NS2_READY();
   if (Lq <= 0 || batch <= 0) return NS2_OK;
   NS2_REQUIRE(q && k && v && o, "%s: null q, k, v or o", fn);
@@ -1143,6 +1175,10 @@ int attention_call(const char* fn, bool noalloc, const float* q, const float* k,
               "%s: the output view must be 16-byte aligned (ldo, oOff, oBatch multiples of 4)", fn);
   NS2_REQUIRE(ldq >= D && ldk >= D && ldv >= D, "%s: row strides must cover one head", fn);
   if (key_bias) NS2_REQUIRE(biasStart >= 0, "%s: negative biasStart", fn);
+  if (k_text || v_text) {
+    NS2_REQUIRE(k_text && v_text && batch == 1 && text_start >= 0 && text_start <= Lk && ld_text >= H * D,
+                "%s: the text view needs k_text and v_text, batch 1, 0 <= text_start <= Lk and ld_text >= H*D", fn);
+  }
   const int Lq_pad = (Lq + QPAD - 1) / QPAD * QPAD;
   const int Lk_pad = (Lk + KB - 1) / KB * KB;
   const long long bh = (long long)batch * H;
@@ -1155,7 +1191,8 @@ int attention_call(const char* fn, bool noalloc, const float* q, const float* k,
   const bool vec = aligned16(q) && aligned16(k) && aligned16(v) && al4(ldq) && al4(ldk) && al4(ldv) &&
                    al4(qOff) && al4(kOff) && al4(vOff) && al4(qBatch) && al4(kBatch) && al4(vBatch) &&
                    (!q_norm || aligned16(q_norm)) && (!k_norm || aligned16(k_norm)) &&
-                   (!rope_cs || (aligned16(rope_cs) && al4(sin_off)));
+                   (!rope_cs || (aligned16(rope_cs) && al4(sin_off))) &&
+                   (!k_text || (aligned16(k_text) && aligned16(v_text) && al4(ld_text)));
   half_t *Qp, *Kc, *Vc;
   float* B2;
   if (noalloc) {
@@ -1188,6 +1225,10 @@ int attention_call(const char* fn, bool noalloc, const float* q, const float* k,
   FlashArgs fa{Qp, Kc, Vc, B2, o, oOff, oBatch, Lq, Lk, Lq_pad, Lk_pad, H, ldo, first_biased / KB, 0, 0, 0,
                vec ? 1 : 0, q, q_norm, rope_cs, qOff, qBatch, sin_off, ldq, rope_rows, scale * kLog2e, eps};
   pa.skip_q = vec ? 1 : 0;
+  pa.k2 = k_text;
+  pa.v2 = v_text;
+  pa.ld2 = ld_text;
+  pa.kv2_start = text_start;
   const bool profile = !noalloc;
   switch (D) {
     case 32: return run_attention<32>(pa, fa, batch, vec, profile);
@@ -1209,6 +1250,18 @@ extern "C" int ns2_attention(const float* q, const float* k, const float* v, flo
   return attention_call("ns2_attention", false, q, k, v, o, batch, Lq, Lk, H, D, ldq, ldk, ldv, ldo, qOff, kOff,
                         vOff, oOff, qBatch, kBatch, vBatch, oBatch, scale, key_bias, biasStart, biasBatch, q_norm,
                         k_norm, eps, rope_cs, sin_off, rope_rows);
+}
+
+extern "C" int ns2_attention_text(const float* q, const float* k, const float* v, float* o, int Lq, int Lk,
+                                  int H, int D, int ldq, int ldk, int ldv, int ldo, long long qOff, long long kOff,
+                                  long long vOff, long long oOff, float scale, const float* key_bias,
+                                  int biasStart, const float* q_norm, const float* k_norm, float eps,
+                                  const float* rope_cs, long long sin_off, int rope_rows, const float* k_text,
+                                  const float* v_text, int ld_text, int text_start) {
+  NS2_REQUIRE(k_text && v_text, "ns2_attention_text: null k_text or v_text");
+  return attention_call("ns2_attention_text", false, q, k, v, o, 1, Lq, Lk, H, D, ldq, ldk, ldv, ldo, qOff, kOff,
+                        vOff, oOff, 0, 0, 0, 0, scale, key_bias, biasStart, 0, q_norm, k_norm, eps, rope_cs,
+                        sin_off, rope_rows, k_text, v_text, ld_text, text_start);
 }
 
 extern "C" int ns2_attention_noalloc(const float* q, const float* k, const float* v, float* o, int batch,

@@ -13,6 +13,7 @@
 
 import * as ops from "./ops.js";
 import { rope2dTable } from "./common.js";
+import { concatLinears } from "./weights.js";
 
 const D = 1536;
 const HEADS = 16;
@@ -79,7 +80,22 @@ export class Nanosaur2DiT {
       // block modulations with one launch
       m.offsets = gpu.empty([BLOCKS, 6 * D]);
       m.blocks.forEach((b, i) => ops.elementwise(gpu, "copy", b.offset, null, ops.rowView(m.offsets, i)));
+      // the joint blocks' kv_y projections all take the same rotated text: one stacked weight
+      // [sum N, K] whose parts keep the blocks' module names, multiplied once per pass; block b
+      // reads its k|v columns at kvSlot * N_b (app/models/nanosaur2.js:168-169, 202)
+      const joint = m.blocks.filter((b) => b.kvY);
+      if (joint.length && joint.every((b) => b.kvY.kind === "i8" && b.kvY.N === joint[0].kvY.N && b.kvY.K === D)) {
+        m.kvAll = concatLinears(gpu, joint.map((b) => b.kvY));
+        joint.forEach((b, i) => {
+          b.kvSlot = i * b.kvY.N;
+          b.kvY = null;
+        });
+      }
       // the fused producers feed the block linears tiled operands: re-tile their weights once
+      if (m.kvAll && ops.tileable(m.kvAll)) {
+        ops.tileWeight(gpu, m.kvAll);
+        ops.dropRowMajor(m.kvAll);
+      }
       for (const b of m.text.concat(m.blocks)) {
         for (const W of [b.qkv, b.kvY, b.proj, b.w3]) if (W && ops.tileable(W)) ops.tileWeight(gpu, W);
         // the MLP's first linear runs fused with its GLU and the rotation for w3
@@ -100,7 +116,7 @@ export class Nanosaur2DiT {
       this.finalAda, this.finalLinear];
     const text = this.text.flatMap((b) => [b.ada, b.qkv, b.proj, b.w12, b.w3]);
     const blocks = this.blocks.flatMap((b) => [b.qkv, b.kvY, b.proj, b.w12, b.w3]);
-    return top.concat(text, blocks).filter((W) => W);
+    return top.concat(text, blocks, [this.kvAll]).filter((W) => W);
   }
 
   // Bytes of device memory the loaded weights hold (every persistent buffer, once).
@@ -184,11 +200,15 @@ export class Nanosaur2DiT {
 
   // Attention over a packed qkv [Lk, 3D] buffer; fused: per-head norms (and RoPE on the
   // first ropeRows rows) inside the attention call, else the reference's headNorm ops.
-  attend(qkv, L, Lk, b, { cs = null, textRows = 0, bias = null } = {}) {
+  // textKV: the text keys and values outside qkv ({ t, off, ld }, from the stacked kv_y product)
+  attend(qkv, L, Lk, b, { cs = null, textRows = 0, bias = null, textKV = null } = {}) {
     const gpu = this.gpu;
     const common = { q: qkv, k: qkv, v: qkv, Lq: L, Lk, H: HEADS, D: HD, ldq: 3 * D, ldk: 3 * D, ldv: 3 * D,
       qOff: 0, kOff: D, vOff: 2 * D, bias, biasStart: L };
-    if (this.fused) return ops.attention(gpu, { ...common, qNorm: b.qn, kNorm: b.kn, cs, ropeRows: L });
+    if (this.fused) {
+      return ops.attention(gpu, { ...common, qNorm: b.qn, kNorm: b.kn, cs, ropeRows: L,
+        textKV: textKV ? { ...textKV, start: L } : null });
+    }
     ops.headNorm(gpu, qkv, b.qn, { L, H: HEADS, D: HD, ld: 3 * D, colOff: 0, cs });
     ops.headNorm(gpu, qkv, b.kn, { L, H: HEADS, D: HD, ld: 3 * D, colOff: D, cs });
     if (textRows) ops.headNorm(gpu, qkv, b.kn, { L: textRows, H: HEADS, D: HD, ld: 3 * D, colOff: D, rowOff: L });
@@ -284,10 +304,17 @@ export class Nanosaur2DiT {
     const tc = ops.elementwise(gpu, "silu", t);
     let txt = null;
     let txtR = null;
+    let kvText = null;
     if (text.L) {
       txt = this.refineText(text, tc);
-      // the int8 kv_y projections take rotated inputs: rotate the text once for all blocks
-      if (this.blocks.some((b) => b.kvY && ops.needsRotation(b.kvY))) {
+      // the int8 kv_y projections take rotated inputs: rotate the text once for all blocks;
+      // with the stacked weight, project it for every joint block at once
+      if (this.kvAll) {
+        txtR = ops.rotateHalf(gpu, txt, D, !!this.kvAll.tbuf);
+        kvText = ops.linear(gpu, null, this.kvAll, { xr: txtR, name: "dit.kv_y" });
+        txtR.release();
+        txtR = null;
+      } else if (this.blocks.some((b) => b.kvY && ops.needsRotation(b.kvY))) {
         const tiled = this.blocks.every((b) => !b.kvY || b.kvY.tbuf);
         txtR = this.fused ? ops.rotateHalf(gpu, txt, D, tiled) : ops.rotate(gpu, txt);
       }
@@ -304,10 +331,11 @@ export class Nanosaur2DiT {
     // every block's modulation mod + offset_i (app/models/nanosaur2.js:190) at once
     const modAll = this.offsets ? ops.addRows(gpu, mod, this.offsets) : null;
     return {
-      txt, txtR, mod, final, modAll,
+      txt, txtR, kvText, mod, final, modAll,
       release() {
         if (txt) txt.release();
         if (txtR) txtR.release();
+        if (kvText) kvText.release();
         mod.release();
         final.release();
         if (modAll) modAll.release();
@@ -322,15 +350,18 @@ export class Nanosaur2DiT {
     const gpu = this.gpu;
     const b = this.blocks[i];
     const mod = c.modAll ? ops.rowView(c.modAll, i) : ops.elementwise(gpu, "add", c.mod, b.offset); // [1, 6D]
-    const cross = !!(b.kvY && text.L);
-    // rows [0, L): image q|k|v; rows [L, L + text): text k|v (q columns unused)
+    const stacked = b.kvSlot !== undefined && !!c.kvText;
+    const cross = !!((b.kvY || stacked) && text.L);
+    // rows [0, L): image q|k|v; rows [L, L + text): text k|v (q columns unused), unless the
+    // text k|v come from the stacked kv_y product
     const Lk = L + (cross ? text.L : 0);
-    const qkv = gpu.empty([Lk, 3 * D]);
+    const qkv = gpu.empty([stacked ? L : Lk, 3 * D]);
     this.qkvProj(x, mod, b, qkv, "dit.qkv");
-    if (cross) {
+    if (cross && !stacked) {
       ops.linear(gpu, c.txt, b.kvY, { xr: c.txtR, out: qkv, ldc: 3 * D, cOff: L * 3 * D + D, name: "dit.kv_y" });
     }
-    const a = this.attend(qkv, L, Lk, b, { cs, textRows: cross ? text.L : 0, bias: cross ? text.bias : null });
+    const textKV = cross && stacked ? { t: c.kvText, off: b.kvSlot, ld: this.kvAll.N } : null;
+    const a = this.attend(qkv, L, Lk, b, { cs, textRows: cross ? text.L : 0, bias: cross ? text.bias : null, textKV });
     qkv.release();
     this.projAdd(x, a, b.proj, mod, "dit.proj");
     a.release();

@@ -292,8 +292,12 @@ export function accumulate(gpu, y, a) {
 //  bias: optional Tensor of additive score biases for keys biasStart...
 // Fused prologue options of this build: qNorm/kNorm (per-head RMSNorm weights, the DiT's
 // headNorm), cs (RoPE table with .sinOff) applied to q/k rows < ropeRows, eps.
+// textKV (addition to the reference API): { t, off, ld, start } -- key and value rows from
+// `start` on come from Tensor t, keys at column off and values at off + H*D of rows with stride
+// ld (the DiT's text keys projected for all joint blocks at once); fused path only.
 export function attention(gpu, { q, k, v, Lq, Lk, H, D, ldq, ldk, ldv, qOff = 0, kOff = 0, vOff = 0, group = 1,
-  causal = false, bias = null, biasStart = 0, out, qNorm = null, kNorm = null, cs = null, ropeRows = 0, eps = 1e-6 }) {
+  causal = false, bias = null, biasStart = 0, out, qNorm = null, kNorm = null, cs = null, ropeRows = 0, eps = 1e-6,
+  textKV = null }) {
   const o = out || gpu.empty([Lq, H * D]);
   // the fused kernel's conditions (app/gpu/ops.js:202-203); otherwise the materialized path's
   // semantics (:211-241), which rejects a key bias
@@ -301,10 +305,20 @@ export function attention(gpu, { q, k, v, Lq, Lk, H, D, ldq, ldk, ldv, qOff = 0,
   if (causal || group !== 1 || D % 32 || D > 128 || !aligned) {
     if (bias) throw new Error("attention: key bias needs the fused kernel");
     if (qNorm || kNorm || cs) throw new Error("attention: fused head norms need the fused kernel");
+    if (textKV) throw new Error("attention: a separate text key/value view needs the fused kernel");
     if (D > 256) throw new Error(`attention: unsupported head dim ${D}`);
     gpu.run("attn.rows", 4 * Lq * Lk * D * H, () =>
       native.attentionRows(addr(q), addr(k), addr(v), addr(o), Lq, Lk, H, D, ldq, ldk, ldv, H * D, qOff, kOff, vOff,
         group, causal ? 1 : 0));
+    return o;
+  }
+  if (textKV) {
+    const base = addr(textKV.t);
+    const kt = base + BigInt(textKV.off * 4), vt = base + BigInt((textKV.off + H * D) * 4);
+    gpu.run("attn.flash", 4 * Lq * Lk * D * H, () =>
+      native.attentionText(addr(q), addr(k), addr(v), addr(o), Lq, Lk, H, D, ldq, ldk, ldv, H * D, qOff, kOff, vOff, 0,
+        1 / Math.sqrt(D), addr(bias), biasStart, addr(qNorm), addr(kNorm), eps, cs ? addr(cs) : null,
+        cs ? cs.sinOff : 0, cs ? ropeRows : 0, kt, vt, textKV.ld, textKV.start));
     return o;
   }
   gpu.run("attn.flash", 4 * Lq * Lk * D * H, () =>

@@ -239,39 +239,41 @@ export class SafeTensors {
   }
 }
 
-// Stack bf16 linears that share an input into one [sum N, K] weight (q, k, v -> qkv), with
-// `parts` naming each slice; biases are stacked too, zero for parts without one
-// (app/weights.js:148-172). The copies run on the device; the parts' buffers are freed.
+// Stack linears that share an input into one [sum N, K] weight (q, k, v -> qkv; the DiT's kv_y
+// projections of every joint block), with `parts` naming each slice; per-row scales (int8) and
+// biases are stacked too, zero bias for parts without one (app/weights.js:148-172). All parts
+// are bf16, or all int8 ConvRot. The copies run on the device; the parts' buffers are freed.
 export function concatLinears(gpu, Ws) {
-  const { K } = Ws[0];
-  if (!Ws.every((w) => w.kind === "bf16" && w.K === K)) throw new Error("concatLinears: mismatched weights");
-  if (K % 2) throw new Error("concatLinears: K must be even");
+  const { K, kind } = Ws[0];
+  if (!Ws.every((w) => w.kind === kind && w.K === K && (kind === "bf16" || kind === "i8"))) {
+    throw new Error("concatLinears: the weights must share K and be all bf16 or all int8");
+  }
+  const rowBytes = kind === "i8" ? K : 2 * K;
+  if (rowBytes % 4) throw new Error("concatLinears: rows must be whole 32-bit words");
   const N = Ws.reduce((a, w) => a + w.N, 0);
-  const out = { kind: "bf16", K, N, parts: [], bias: null };
+  const out = { kind, K, N, parts: [], bias: null };
   let off = 0;
   for (const w of Ws) {
     out.parts.push({ name: w.name, off, n: w.N });
     off += w.N;
   }
-  // bf16 rows as 32-bit words (K even), copied with the elementwise copy op
-  out.buf = gpu.upload(new Uint32Array((N * K) / 2));
-  off = 0;
-  for (const w of Ws) {
-    const words = (w.N * K) / 2;
-    native.elementwise(EW.copy, addr(w.buf), null, addr(out.buf) + BigInt(off * K * 2), words);
-    off += w.N;
-  }
-  if (Ws.some((w) => w.bias)) {
-    out.bias = gpu.upload(new Float32Array(N));
-    off = 0;
+  // rows as 32-bit words, copied with the elementwise copy op; f32 vectors likewise
+  const stack = (field, bytesPerRow) => {
+    const dst = gpu.upload(new Uint32Array((N * bytesPerRow) / 4));
+    let r = 0;
     for (const w of Ws) {
-      if (w.bias) native.elementwise(EW.copy, addr(w.bias), null, addr(out.bias) + BigInt(off * 4), w.N);
-      off += w.N;
+      if (w[field]) native.elementwise(EW.copy, addr(w[field]), null, addr(dst) + BigInt(r * bytesPerRow), (w.N * bytesPerRow) / 4);
+      r += w.N;
     }
-  }
+    return dst;
+  };
+  out.buf = stack("buf", rowBytes);
+  if (kind === "i8") out.scale = stack("scale", 4);
+  if (Ws.some((w) => w.bias)) out.bias = stack("bias", 4);
   native.sync();
   for (const w of Ws) {
     w.buf.destroy();
+    if (w.scale) w.scale.destroy();
     if (w.bias) w.bias.destroy();
   }
   return out;

@@ -73,6 +73,9 @@ SIGNATURES = {
     "ns2_attention_noalloc": [c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
                               c_int, c_ll, c_ll, c_ll, c_ll, c_ll, c_ll, c_ll, c_ll, c_float, c_vp, c_int,
                               c_ll, c_vp, c_vp, c_float, c_vp, c_ll, c_int],
+    "ns2_attention_text": [c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
+                           c_ll, c_ll, c_ll, c_ll, c_float, c_vp, c_int, c_vp, c_vp, c_float, c_vp, c_ll, c_int,
+                           c_vp, c_vp, c_int, c_int],
     "ns2_attention_rows": [c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
                            c_ll, c_ll, c_ll, c_int, c_int],
     "ns2_head_norm": [c_vp, c_vp, c_int, c_int, c_int, c_int, c_ll, c_ll, c_vp, c_ll, c_float],
@@ -247,6 +250,17 @@ class Lib:
                   ldv, ldo, qOff, kOff, vOff, oOff, qBatch, kBatch, vBatch, oBatch, scale,
                   _ptr(key_bias), biasStart, biasBatch, _ptr(q_norm), _ptr(k_norm), eps,
                   _ptr(rope_cs), sin_off, rope_rows)
+
+    def attention_text(self, q, k, v, o, *, Lq, Lk, H, D, ldq, ldk, ldv, ldo, k_text, v_text, ld_text, text_start,
+                       qOff=0, kOff=0, vOff=0, oOff=0, scale=None, key_bias=None, biasStart=0, q_norm=None,
+                       k_norm=None, eps=1e-6, rope_cs=None, sin_off=0, rope_rows=0):
+        """ns2_attention_text: key/value rows from text_start on come from k_text / v_text (row
+        stride ld_text)."""
+        if scale is None:
+            scale = 1.0 / D ** 0.5
+        self.call("ns2_attention_text", _ptr(q), _ptr(k), _ptr(v), _ptr(o), Lq, Lk, H, D, ldq, ldk, ldv, ldo, qOff,
+                  kOff, vOff, oOff, scale, _ptr(key_bias), biasStart, _ptr(q_norm), _ptr(k_norm), eps, _ptr(rope_cs),
+                  sin_off, rope_rows, _ptr(k_text), _ptr(v_text), ld_text, text_start)
 
     def attention_rows(self, q, k, v, o, *, Lq, Lk, H, D, ldq, ldk, ldv, ldo, qOff=0, kOff=0, vOff=0,
                        group=1, causal=False):

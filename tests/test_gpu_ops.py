@@ -225,6 +225,7 @@ def _tiled_linear_inputs(M, N, K, seed):
     (3952, 8192, 1536),   # MLP w12
     (3952, 1536, 4096),   # MLP w3
     (256, 3072, 1536),    # kv_y on the text rows
+    (256, 27648, 1536),   # the 9 joint blocks' kv_y stacked: one launch per pass
     (2432, 6144, 1536),
     (97, 320, 512),       # ragged rows, N not a multiple of 128
     (1, 64, 256),
@@ -458,6 +459,48 @@ def test_attention_batch2_config2(ns2lib):
             sl = slice(h * 96, (h + 1) * 96)
             assert_close(got[b, :, sl], ref[:, sl], TOL, f"config2 batch {b} head {h}")
         assert_close(got[b], ref, TOL, f"config2 batch {b} all heads")
+
+
+@pytest.mark.parametrize("pad", [0, 1])
+def test_attention_text_view(ns2lib, pad):
+    """ns2_attention_text: the DiT's joint attention with the text keys and values in a second
+    view (the stacked kv_y product, row stride 27648 at the block's column), against
+    ns2_attention on the same rows concatenated into one packed qkv buffer: identical results,
+    and the oracle. pad=1 makes the views unaligned (per-element pack path)."""
+    L, T, Dm = 6 * 8, 37, 1536
+    ld = 3 * Dm + pad
+    ldt = 9 * 2 * Dm + 4 * pad
+    slot = 4 * 2 * Dm + pad
+    g = gen(71 + pad)
+    img = torch.randn(L, ld, generator=g)
+    txt = torch.randn(T, ldt, generator=g)
+    qn = torch.randn(96, generator=g) * 0.5 + 1
+    kn = torch.randn(96, generator=g) * 0.5 + 1
+    lb = torch.log(torch.rand(T, generator=g) + 0.5)
+    cs, sin_off = O.rope2d_table(6, 8)
+    # the same keys in one buffer: text rows carry k|v at the columns of the image rows
+    joint = torch.zeros(L + T, ld)
+    joint[:L] = img
+    joint[L:, pad + Dm:pad + 3 * Dm] = txt[:, slot:slot + 2 * Dm]
+    o1 = torch.empty(L, Dm, device=dev)
+    o2 = torch.empty(L, Dm, device=dev)
+    kw = dict(Lq=L, Lk=L + T, H=16, D=96, ldq=ld, ldk=ld, ldv=ld, ldo=Dm, qOff=pad, kOff=Dm + pad,
+              vOff=2 * Dm + pad, key_bias=lb.to(dev), biasStart=L, q_norm=qn.to(dev), k_norm=kn.to(dev),
+              rope_cs=cs.to(dev), sin_off=sin_off, rope_rows=L)
+    jd = joint.to(dev)
+    ns2lib.attention(jd, jd, jd, o1, **kw)
+    imgd, txtd = img.to(dev), txt.to(dev)
+    ns2lib.attention_text(imgd, imgd, imgd, o2, k_text=txtd[:, slot:], v_text=txtd[:, slot + Dm:], ld_text=ldt,
+                          text_start=L, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(o1.cpu(), o2.cpu()), "text view differs from the packed buffer"
+    ref_buf = joint.double()[:, pad:pad + 3 * Dm].clone()
+    O.head_norm_rope(ref_buf, qn.double(), L, 16, 96, 3 * Dm, colOff=0, cs=cs, sinOff=sin_off)
+    O.head_norm_rope(ref_buf, kn.double(), L, 16, 96, 3 * Dm, colOff=Dm, cs=cs, sinOff=sin_off)
+    O.head_norm_rope(ref_buf, kn.double(), T, 16, 96, 3 * Dm, colOff=Dm, rowOff=L)
+    bias = torch.cat([torch.zeros(L, dtype=torch.float64), lb.double()])
+    ref = O.attention_heads(ref_buf[:L, :Dm], ref_buf[:, Dm:2 * Dm], ref_buf[:, 2 * Dm:], 16, 96, bias)
+    assert_close(o2.cpu(), ref, TOL, f"attention with a text view (pad {pad})")
 
 
 @pytest.mark.parametrize("pad", [0, 1])
