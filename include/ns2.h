@@ -324,6 +324,15 @@ int ns2_add_rmsnorm(float* x, const float* a, const float* w_add, const float* w
  * when y is not null, y = rmsnorm(x) * w_out (ns2_add_rmsnorm; app/models/gemma3.js:72-80 for
  * the o projection, 83-92 for the down projection). A fp32 [M, lda]; W bf16 [N, K]; x, y fp32
  * [M, N] contiguous, N <= 1024; x must not alias A or y. Additive to the reference interface. */
+/* linear (bf16 weight, no LoRA) of a stacked q|k|v projection followed by the per-head norms of
+ * two ops.headNorm calls on its rows (Gemma3, app/models/gemma3.js:62-67): C [M, N] = x W^T
+ * (+ bias), then heads [0, H1) RMS-normed with w1 and heads [H1, H1 + H2) with w2 (D each), with
+ * split-half RoPE on rows < rope_rows when cs is given (ns2_head_norm's table layout); heads past
+ * H1 + H2 (the values) as computed. D is 64, 128 or 256; N / D is at most 8 heads. Additive to the
+ * reference interface. */
+int ns2_linear_bf16_head_norm(const float* A, int lda, const uint16_t* W, const float* bias, float* C, int M, int N,
+                              int K, const float* w1, int H1, const float* w2, int H2, int D, const float* cs,
+                              long long sin_off, int rope_rows, float eps);
 /* A gate/up projection and its GLU without the [M, N] product in HBM: t = A W^T (+ bias), then
  * Y[m][i] = act(t[m][i]) * t[m][N/2 + i] (ns2_linear_bf16 + ns2_glu; the Gemma3 MLP's fused
  * gate/up weight, app/models/gemma3.js:79-82). W bf16 [N, K] with the gate rows first; Y fp32

@@ -702,6 +702,27 @@ napi_value LinearBf16Glu(napi_env env, napi_callback_info info) {
   return check(env, c, ns2_linear_bf16_glu(A, lda, W, bias, Y, M, N, K, act));
 }
 
+// linearBf16HeadNorm(A, lda, W, bias, C, M, N, K, w1, H1, w2, H2, D, cs, sinOff, ropeRows, eps)
+napi_value LinearBf16HeadNorm(napi_env env, napi_callback_info info) {
+  ARGS(17);
+  auto A = (const float*)c.ptr(0);
+  int lda = c.i32(1);
+  auto W = (const uint16_t*)c.ptr(2);
+  auto bias = (const float*)c.ptr(3);
+  auto C = (float*)c.ptr(4);
+  int M = c.i32(5), N = c.i32(6), K = c.i32(7);
+  auto w1 = (const float*)c.ptr(8);
+  int H1 = c.i32(9);
+  auto w2 = (const float*)c.ptr(10);
+  int H2 = c.i32(11), D = c.i32(12);
+  auto cs = (const float*)c.ptr(13);
+  long long sinOff = c.i64(14);
+  int ropeRows = c.i32(15);
+  float eps = c.f32(16);
+  if (c.failed) return nullptr;
+  return check(env, c, ns2_linear_bf16_head_norm(A, lda, W, bias, C, M, N, K, w1, H1, w2, H2, D, cs, sinOff, ropeRows, eps));
+}
+
 // linearBf16AddRmsnorm(A, lda, W, bias, x, wAdd, wOut, y, M, N, K, eps)
 napi_value LinearBf16AddRmsnorm(napi_env env, napi_callback_info info) {
   ARGS(12);
@@ -739,7 +760,7 @@ napi_value Module(napi_env env, napi_value exports) {
       {"glu", GluT<false>}, {"gluRotateF16", GluT<true>}, {"elementwise", Elementwise},
       {"accumulate", Accumulate}, {"addRows", AddRows}, {"rowSum", RowSum}, {"rmsnorm", Rmsnorm},
       {"addRmsnorm", AddRmsnorm}, {"linearBf16AddRmsnorm", LinearBf16AddRmsnorm},
-      {"linearBf16Glu", LinearBf16Glu}, {"transpose", Transpose},
+      {"linearBf16Glu", LinearBf16Glu}, {"linearBf16HeadNorm", LinearBf16HeadNorm}, {"transpose", Transpose},
   };
   for (const Fn& f : fns) {
     napi_value fn;

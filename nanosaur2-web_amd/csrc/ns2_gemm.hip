@@ -359,6 +359,66 @@ __global__ __launch_bounds__(256) void splitk_add_rmsnorm_kernel(GemmArgs p, int
     if (tid + 256 * j < N) rn.y[row + col[j]] = t[j] * r2 * rn.w_out[col[j]];
 }
 
+// Split-K sum of a stacked q|k|v product followed by the per-head norms of app/gpu/ops.js:
+// 133-138 on its q and k heads (Gemma3, app/models/gemma3.js:64-67): one block of D threads per
+// row, thread i owning dim i of every head. Heads h < H1 are RMS-normed with w1, heads
+// [H1, H1 + H2) with w2, then split-half RoPE on rows < rope_rows (pair i, i + D/2; cos at
+// cs[row*D/2 + i], sin at cs[sin_off + row*D/2 + i]); the remaining heads (the values) are stored
+// as summed. The splits are added in split order, as splitk_reduce_kernel adds them.
+struct HeadNorm {
+  const float* w1;
+  int H1;
+  const float* w2;
+  int H2, D;
+  const float* cs;
+  long long sin_off;
+  int rope_rows;
+  float eps;
+};
+constexpr int kHeadNormMaxHeads = 8;
+template <int D>
+__global__ __launch_bounds__(D) void splitk_head_norm_kernel(GemmArgs p, int splits, HeadNorm hn) {
+  constexpr int MH = kHeadNormMaxHeads;
+  __shared__ float red[D / 64];
+  __shared__ float row_buf[D];
+  const int tid = threadIdx.x, heads = p.N / D;
+  const long long mn = (long long)p.M * p.N, m = blockIdx.x;
+  // every load of the row first (unconditional, from clamped addresses): the split partials
+  // of all heads, the norm weights and the rotation's cos / sin
+  const float* part = p.part + m * p.N + tid;
+  float acc[MH];
+#pragma unroll
+  for (int h = 0; h < MH; ++h) acc[h] = 0.f;
+  for (int z = 0; z < splits; ++z) {
+#pragma unroll
+    for (int h = 0; h < MH; ++h) acc[h] += part[z * mn + (long long)(h < heads ? h : heads - 1) * D];
+  }
+  const float w1 = hn.H1 ? hn.w1[tid] : 0.f, w2 = hn.H2 ? hn.w2[tid] : 0.f;
+  const int half = D / 2, i = tid % half;
+  const bool rope = hn.cs && m < hn.rope_rows;  // uniform per block
+  const float c = rope ? hn.cs[m * half + i] : 1.f, sn = rope ? hn.cs[hn.sin_off + m * half + i] : 0.f;
+  float* out = p.C + p.cOff + m * p.ldc + tid;
+#pragma unroll
+  for (int h = 0; h < MH; ++h) {
+    if (h >= heads) break;
+    float r = acc[h] * p.alpha;
+    if (p.scale) r *= p.scale[h * D + tid];
+    if (p.bias) r += p.bias[h * D + tid];
+    if (h < hn.H1 + hn.H2) {  // uniform per block
+      const float rs = rsqrtf(block_sum(r * r, red) / (float)D + hn.eps);
+      r = r * rs * (h < hn.H1 ? w1 : w2);
+      if (rope) {
+        row_buf[tid] = r;
+        __syncthreads();
+        const float other = row_buf[tid < half ? tid + half : tid - half];
+        r = tid < half ? r * c - other * sn : r * c + other * sn;
+        __syncthreads();
+      }
+    }
+    out[(long long)h * D] = r;
+  }
+}
+
 // Split-K sum of a gate/up product followed by the GLU: y[m][i] = act(t[m][i]) * t[m][I + i]
 // with t = epilogue(sum of the splits), N = 2I (gate rows first, as concatLinears stacks them).
 // The splits are added in split order, as splitk_reduce_kernel adds them.
@@ -561,12 +621,13 @@ constexpr int kMaxSplits = 16;
 // rn: a row post-op (Gemma3's sublayer norms). It takes the 64x64 split-K path at any M, with
 // the row kernel in place of the split-K reduce (a single split when K is short).
 // glu_y: a GLU post-op (y [M, N/2] = act(gate) * up, act glu_act), on the same split-K path.
+// hn: the per-head norms of a stacked q|k|v product (Gemma3), on the same split-K path.
 template <bool A_F32, bool W_BF16>
 int launch_gemm(const GemmArgs& p, const char* name, const RowNorm* rn = nullptr, float* glu_y = nullptr,
-                int glu_act = 0) {
+                int glu_act = 0, const HeadNorm* hn = nullptr) {
   hipStream_t s = ns2::stream();
-  const bool post = rn || glu_y;
-  ns2::ProfScope prof_(rn ? "gemm_bf16_add_rmsnorm" : glu_y ? "gemm_bf16_glu"
+  const bool post = rn || glu_y || hn;
+  ns2::ProfScope prof_(rn ? "gemm_bf16_add_rmsnorm" : glu_y ? "gemm_bf16_glu" : hn ? "gemm_bf16_head_norm"
                           : p.M <= kGemvMaxM ? (W_BF16 ? "gemv_bf16" : "gemv_i8") : (W_BF16 ? "gemm_bf16" : "gemm_i8"));
   const long long big_tiles = (long long)((p.N + 127) / 128) * ((p.M + 127) / 128);
   if (!post && p.M <= kGemvMaxM) {
@@ -603,6 +664,10 @@ int launch_gemm(const GemmArgs& p, const char* name, const RowNorm* rn = nullptr
     else gemm_mfma_kernel<BM, BN, WM, WN, A_F32, W_BF16, false><<<grid, (BM / WM) * (BN / WN) * 64, 0, s>>>(q);
     if (rn) {
       splitk_add_rmsnorm_kernel<<<p.M, 256, 0, s>>>(q, splits, *rn);
+    } else if (hn) {
+      if (hn->D == 64) splitk_head_norm_kernel<64><<<p.M, 64, 0, s>>>(q, splits, *hn);
+      else if (hn->D == 128) splitk_head_norm_kernel<128><<<p.M, 128, 0, s>>>(q, splits, *hn);
+      else splitk_head_norm_kernel<256><<<p.M, 256, 0, s>>>(q, splits, *hn);
     } else if (glu_y) {
       const long long n = (long long)p.M * (p.N / 2);
       splitk_glu_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(q, splits, glu_y, glu_act);
@@ -738,6 +803,24 @@ int ns2_linear_bf16_add_rmsnorm(const float* A, int lda, const uint16_t* W, cons
   if (rc) return rc;
   const RowNorm rn{x, w_add, w_out, y, eps};
   return launch_gemm<true, true>(p, "linear_bf16_add_rmsnorm", &rn);
+}
+
+int ns2_linear_bf16_head_norm(const float* A, int lda, const uint16_t* W, const float* bias, float* C, int M, int N,
+                              int K, const float* w1, int H1, const float* w2, int H2, int D, const float* cs,
+                              long long sin_off, int rope_rows, float eps) {
+  NS2_READY();
+  if (M == 0) return NS2_OK;
+  NS2_REQUIRE(D == 64 || D == 128 || D == 256, "ns2_linear_bf16_head_norm: head dim %d is not 64, 128 or 256", D);
+  NS2_REQUIRE(N % D == 0 && N / D <= kHeadNormMaxHeads && H1 >= 0 && H2 >= 0 && (H1 + H2) * D <= N &&
+                  (!H1 || w1) && (!H2 || w2),
+              "ns2_linear_bf16_head_norm: N=%d (at most %d heads of %d), H1=%d, H2=%d or their weights", N,
+              kHeadNormMaxHeads, D, H1, H2);
+  NS2_REQUIRE(C != A, "ns2_linear_bf16_head_norm: C must not alias A");
+  GemmArgs p{A, W, nullptr, bias, nullptr, C, nullptr, 0, 0, lda, N, M, N, K, 1.0f, NS2_ACT_NONE, 0};
+  int rc = check_common(p, "ns2_linear_bf16_head_norm");
+  if (rc) return rc;
+  const HeadNorm hn{w1, H1, w2, H2, D, cs, sin_off, cs ? rope_rows : 0, eps};
+  return launch_gemm<true, true>(p, "linear_bf16_head_norm", nullptr, nullptr, 0, &hn);
 }
 
 int ns2_linear_bf16_glu(const float* A, int lda, const uint16_t* W, const float* bias, float* Y, int M, int N,

@@ -80,10 +80,10 @@ export class Gemma3 {
     let h = ops.rmsnorm(gpu, x, this.layers[0].inNorm, D);
     this.layers.forEach((l, i) => {
       const cs = l.global ? csGlobal : csLocal;
-      const qkv = ops.linear(gpu, h, l.qkv, { name: "te.qkv" }); // [Lt, q 1024 | k 256 | v 256]
+      // [Lt, q 1024 | k 256 | v 256], the q heads and then the k head normed and rotated in the
+      // projection's split-K sum
+      const qkv = ops.linearHeadNorm(gpu, h, l.qkv, l.qn, H, l.kn, KH, { D: HD, cs });
       h.release();
-      // q heads then the k head: adjacent columns, one launch
-      ops.headNorm2(gpu, qkv, l.qn, H, l.kn, KH, { L: Lt, D: HD, ld: qkvW, colOff: 0, cs });
       const a = ops.attention(gpu, {
         q: qkv, k: qkv, v: qkv, Lq: Lt, Lk: Lt, H, D: HD, ldq: qkvW, ldk: qkvW, ldv: qkvW,
         qOff: 0, kOff: H * HD, vOff: (H + KH) * HD, group: H / KH, causal: true,

@@ -178,6 +178,23 @@ export function linearGlu(gpu, a, W, act) {
   return y;
 }
 
+// linear(a, W) of a stacked q|k|v weight followed by headNorm2 on its q and k heads (Gemma3,
+// app/models/gemma3.js:62-67; addition to the reference ops): for a bf16 weight without LoRA the
+// split-K sums are normed (and rotated) in the same row kernel, else the two ops run.
+export function linearHeadNorm(gpu, a, W, w1, H1, w2, H2, { D, cs = null, eps = 1e-6 }) {
+  const M = a.size / W.K;
+  if (W.kind !== "bf16" || (W.lora && W.lora.length)) {
+    const t = linear(gpu, a, W, { name: "te.qkv" });
+    headNorm2(gpu, t, w1, H1, w2, H2, { L: M, D, ld: W.N, cs, eps });
+    return t;
+  }
+  const y = gpu.empty([M, W.N]);
+  gpu.run("te.qkv+head_norm", 2 * M * W.N * W.K, () =>
+    native.linearBf16HeadNorm(addr(a), W.K, addr(W.buf), addr(W.bias || null), addr(y), M, W.N, W.K, addr(w1), H1,
+      addr(w2), H2, D, cs ? addr(cs) : null, cs ? cs.sinOff : 0, cs ? M : 0, eps));
+  return y;
+}
+
 // linear(a, W) followed by addRmsnorm(x, ., wAdd, wOut) for a bf16 weight without LoRA: the
 // projection's rows are summed and normed in one row kernel, so the [M, N] product never
 // reaches HBM (app/models/gemma3.js:72-80, 83-92; addition to the reference ops). Other weights

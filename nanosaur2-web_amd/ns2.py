@@ -92,6 +92,8 @@ SIGNATURES = {
     "ns2_add_rmsnorm": [c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_float],
     "ns2_transpose": [c_vp, c_vp, c_int, c_int],
     "ns2_linear_bf16_glu": [c_vp, c_int, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int],
+    "ns2_linear_bf16_head_norm": [c_vp, c_int, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_vp, c_int, c_vp, c_int,
+                                  c_int, c_vp, c_ll, c_int, c_float],
     "ns2_linear_bf16_add_rmsnorm": [c_vp, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_float],
 }
 _RESTYPES = {"ns2_last_error": ctypes.c_char_p, "ns2_get_stream": c_vp, "ns2_pool_round": c_size}
@@ -307,6 +309,11 @@ class Lib:
 
     def add_rmsnorm(self, x, a, w_add, w_out, y, rows, cols, eps=1e-6):
         self.call("ns2_add_rmsnorm", _ptr(x), _ptr(a), _ptr(w_add), _ptr(w_out), _ptr(y), rows, cols, eps)
+
+    def linear_bf16_head_norm(self, A, lda, W, bias, C, M, N, K, w1, H1, w2, H2, D, cs=None, sin_off=0,
+                              rope_rows=0, eps=1e-6):
+        self.call("ns2_linear_bf16_head_norm", _ptr(A), lda, _ptr(W), _ptr(bias), _ptr(C), M, N, K, _ptr(w1), H1,
+                  _ptr(w2), H2, D, _ptr(cs), sin_off, rope_rows, eps)
 
     def linear_bf16_glu(self, A, lda, W, bias, Y, M, N, K, act="gelu_tanh"):
         self.call("ns2_linear_bf16_glu", _ptr(A), lda, _ptr(W), _ptr(bias), _ptr(Y), M, N, K, ACT[act])

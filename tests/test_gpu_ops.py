@@ -767,6 +767,42 @@ def test_linear_bf16_glu(ns2lib, M, bias):
     assert_close(y.cpu(), ref, TOL, "linear_bf16_glu")
 
 
+@pytest.mark.parametrize("M,bias,rope", [(256, False, True), (37, True, True), (5, False, False)])
+def test_linear_bf16_head_norm(ns2lib, M, bias, rope):
+    """Gemma3's q/k/v projection with the q and k head norms (and RoPE) in its split-K sum
+    (app/models/gemma3.js:62-67): against the oracle, and where ns2_linear_bf16 takes the same
+    matrix-core path (M > 8; at M <= 8 it runs the fp32 GEMV) against ns2_linear_bf16 +
+    ns2_head_norm2 (the same sums in a different order: fp32 rounding). N = 4 q heads + 1 k +
+    1 v of 256, K = 640; the v columns pass through unnormed."""
+    N, K, D = 1536, 640, 256
+    g = gen(M + 3 * bias + 11 * rope)
+    a = torch.randn(M, K, generator=g)
+    w = (torch.randn(N, K, generator=g) * 0.05).to(torch.bfloat16)
+    b = torch.randn(N, generator=g) * 0.1 if bias else None
+    wq = torch.randn(D, generator=g) * 0.3 + 1
+    wk = torch.randn(D, generator=g) * 0.3 + 1
+    cs, sin_off = None, 0
+    if rope:
+        ang = torch.arange(M, dtype=torch.float64)[:, None] * torch.rand(D // 2, generator=g, dtype=torch.float64)[None]
+        cs = torch.cat([ang.cos().flatten(), ang.sin().flatten()]).float()
+        sin_off = M * D // 2
+    ad, wd, bd = a.to(dev), w.view(torch.int16).to(dev), (b.to(dev) if bias else None)
+    csd = cs.to(dev) if rope else None
+    y = torch.empty(M, N, device=dev)
+    ns2lib.linear_bf16_head_norm(ad, K, wd, bd, y, M, N, K, wq.to(dev), 4, wk.to(dev), 1, D, cs=csd, sin_off=sin_off,
+                                 rope_rows=M)
+    t = torch.empty(M, N, device=dev)
+    ns2lib.linear_bf16(ad, K, wd, t, M, N, K, bias=bd)
+    ns2lib.head_norm2(t, wq.to(dev), 4, wk.to(dev), 1, M, D, N, cs=csd, sinOff=sin_off)
+    torch.cuda.synchronize()
+    if M > 8:
+        assert_close(y.cpu(), t.cpu().double(), TOL_F32, f"linear_bf16_head_norm vs two launches (M={M})")
+    ref = O.linear_bf16(a.double(), w, bias=b.double() if bias else None)
+    O.head_norm_rope(ref, wq.double(), M, 4, D, N, colOff=0, cs=cs, sinOff=sin_off)
+    O.head_norm_rope(ref, wk.double(), M, 1, D, N, colOff=4 * D, cs=cs, sinOff=sin_off)
+    assert_close(y.cpu(), ref, TOL, f"linear_bf16_head_norm (M={M}, bias={bias}, rope={rope})")
+
+
 @pytest.mark.parametrize("rows,cols", [(64, 3952), (3952, 64), (37, 100), (1, 5)])
 def test_transpose(ns2lib, rows, cols):
     """The latent <-> token layout change of forward() (exact)."""
