@@ -378,7 +378,10 @@ void gemm_tiled_kernel(TGemmArgs p) {
       }
     }
     __syncthreads();
-    // rotation: wave w rotates rows 8w .. 8w+7, the fp16 result in place at the row's start
+    // rotation: wave w rotates rows 8w .. 8w+7, the fp16 result in place in the first 512 bytes
+    // of the row, its 16-byte chunk c stored at chunk c ^ (row & 7): the copy-out below reads one
+    // chunk of 64 rows 1 KB apart per wave, and the swizzle puts 8 consecutive rows in 8
+    // different bank groups (unswizzled, all 64 lanes hit the same four banks)
 #pragma unroll
     for (int rr = 0; rr < 64 / NW; ++rr) {
       const int row = (64 / NW) * wave + rr;
@@ -388,13 +391,15 @@ void gemm_tiled_kernel(TGemmArgs p) {
       uint2 o;
       o.x = pack_half2(v[0], v[1]);
       o.y = pack_half2(v[2], v[3]);
-      *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(T + row * 256) + lane * 4) = o;
+      char* rb = reinterpret_cast<char*>(T + row * 256);
+      *reinterpret_cast<uint2*>(rb + ((lane >> 1) ^ (row & 7)) * 16 + (lane & 1) * 8) = o;
     }
     __syncthreads();
     // 32 chunks of 8 columns x 64 rows: 1 KB contiguous each in the tiled layout
     for (int q = tid; q < 32 * 64; q += NW * 64) {
       const int row = q % 64, c = q / 64;
-      const uint4 v = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(T + row * 256) + c * 8);
+      const char* rb = reinterpret_cast<const char*>(T + row * 256);
+      const uint4 v = *reinterpret_cast<const uint4*>(rb + (c ^ (row & 7)) * 16);
       *reinterpret_cast<uint4*>(p.Y + tiled_off(m0 + row, gb + c * 8, I)) = v;
     }
     return;
