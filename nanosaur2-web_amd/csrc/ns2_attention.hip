@@ -365,62 +365,15 @@ struct FlashArgs {
   float qscale, eps;
 };
 
-// Scores are kept relative to a per-query reference m_ref (log2 units) that only moves when a
-// score exceeds it by more than 2^kRebase; between moves the output accumulator needs no
-// rescale. Any reference gives the same softmax, and p <= 2^kRebase stays in fp16 range.
-constexpr float kRebase = 8.0f;
-
-// SUPER: 64-key tiles per LDS stage. The loads of a stage are issued together and waited for
-// with one barrier, so a barrier falls on every SUPER-th step and a stage's loads are issued
-// (STAGES - 2) * SUPER + 1 .. (STAGES - 1) * SUPER steps before its K fragments are read.
-template <int D, int QT, int NW, int STAGES, int SUPER>
-__global__ __launch_bounds__(NW * 64) void flash_kernel(FlashArgs a) {
-  constexpr int DC = D / 16;             // k-steps of S
-  constexpr int DT = D / 32;             // dim tiles of O
-  constexpr int TILE = KB * D;           // halfs per K (or V) tile image
-  constexpr int BLOCKS = 2 * TILE / 512; // 1 KB direct-load blocks per tile (K then V)
-  constexpr int NSLOT = STAGES * SUPER;  // tile slots in LDS; tile t lives in slot t % NSLOT
-  static_assert(STAGES == 3 || (STAGES == 4 && SUPER == 1), "three stages, or four of one tile");
-  static_assert(SUPER == 1 || SUPER == 2, "one or two tiles per stage");
-
-  // K of tile t+1 and V of tile t are read while the later stages land
-  __shared__ __attribute__((aligned(16))) half_t ks[NSLOT][TILE];
-  __shared__ __attribute__((aligned(16))) half_t vts[NSLOT][TILE];
-  __shared__ __attribute__((aligned(16))) float kbias[NSLOT][KB];
-
-  // Work unit: (pair = batch*H + head, query block). With xcd_order, consecutive block ids
-  // land on different XCDs (round-robin dispatch), so block id i is mapped to pair
-  // (i % 8) + 8 * ((i / 8) / qblocks): every query block of a pair runs on one XCD and its
-  // K/V tiles are fetched into that XCD's L2 once.
-  int pair, qb;
-  {
-    const int id = blockIdx.x;
-    if (a.xcd_order) {
-      const int local = id >> 3;
-      pair = (id & 7) + 8 * (local / a.qblocks);
-      qb = local % a.qblocks;
-    } else {
-      pair = id / a.qblocks;
-      qb = id % a.qblocks;
-    }
-  }
-  const int b = pair / a.H, h = pair % a.H, bh = pair;
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int q0 = qb * (NW * QT * 32) + wave * QT * 32;
-  const int lq = lane & 31, hi = lane >> 5;
-  const int ntiles = a.Lk_pad / KB;
-
-  const half_t* Kt = a.Kc + (long long)bh * ntiles * TILE;
-  const half_t* Vt = a.Vc + (long long)bh * ntiles * TILE;
-  const float* Bg = a.bias2 + (long long)b * a.Lk_pad;
-
-  // Q^T operands: lane holds query q0 + qt*32 + lq, dims c*16 + 8*hi .. +7. With qraw the
-  // lane reads those 8*DC fp32 values and prepares them as the pack does (kernels.js:307-342):
-  // RMSNorm over the head row (its other half is in lane ^ 32), then split-half RoPE, whose
-  // partner of dim 16c + 8hi + e is dim 16(c + DC/2) + 8hi + e of the same lane, then the
-  // scale; rows past Lq are zero.
-  half8_t qf[QT][DC];
+// Q^T operands of a wave: lane holds query q0 + qt*32 + lq, dims c*16 + 8*hi .. +7. With qraw
+// the lane reads those 8*DC fp32 values and prepares them as the pack does (kernels.js:307-342):
+// RMSNorm over the head row (its other half is in lane ^ 32), then split-half RoPE, whose
+// partner of dim 16c + 8hi + e is dim 16(c + DC/2) + 8hi + e of the same lane, then the
+// scale; rows past Lq are zero.
+template <int D, int QT>
+__device__ __forceinline__ void load_q(const FlashArgs& a, int b, int h, int bh, int q0, int lq, int hi,
+                                       half8_t (&qf)[QT][D / 16]) {
+  constexpr int DC = D / 16;
   static_assert(DC % 2 == 0, "RoPE halves must be whole k-steps");
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
@@ -486,30 +439,25 @@ __global__ __launch_bounds__(NW * 64) void flash_kernel(FlashArgs a) {
     }
   }
 
-  float16_t o[QT][DT];
-#pragma unroll
-  for (int qt = 0; qt < QT; ++qt)
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) o[qt][dt][r] = 0.f;
-  float m_ref[QT], l_run[QT];
-#pragma unroll
-  for (int qt = 0; qt < QT; ++qt) {
-    m_ref[qt] = 0.f;
-    l_run[qt] = 0.f;
-  }
+}
 
-  // Tile t -> LDS stage st with direct global->LDS loads: the stage image is BLOCKS blocks of
-  // 1 KB (K blocks, then V^T blocks) plus the 256-byte key bias; wave w moves blocks w, w+NW,
-  // ..., BLOCKS (the bias); lane l moves bytes [16l, 16l+16) of a block (16 lanes for the bias).
-  // The per-wave sources and destinations are fixed up front; a tile adds its offsets.
-  constexpr int NJ = (BLOCKS + NW) / NW;  // loads per wave per tile, at most
+// Tile t -> LDS stage st with direct global->LDS loads: the stage image is BLOCKS blocks of
+// 1 KB (K blocks, then V^T blocks) plus the 256-byte key bias; wave w of NW moves blocks w,
+// w+NW, ..., BLOCKS (the bias); lane l moves bytes [16l, 16l+16) of a block (16 lanes for the
+// bias). The per-wave sources and destinations are fixed up front; a tile adds its offsets.
+template <int D, int NW>
+struct TileLoader {
+  static constexpr int TILE = KB * D;            // halfs per K (or V) tile image
+  static constexpr int BLOCKS = 2 * TILE / 512;  // 1 KB blocks per tile (K then V)
+  static constexpr int NJ = (BLOCKS + NW) / NW;  // loads per wave per tile, at most
   const char* g_src[NJ];
   uint32_t l_dst[NJ];
   int g_step[NJ], l_step[NJ];
-  {
-    const uint32_t ks_base = lds_addr(ks), vts_base = lds_addr(vts), kb_base = lds_addr(kbias);
+  int wave, lane;
+
+  __device__ __forceinline__ TileLoader(const half_t* Kt, const half_t* Vt, const float* Bg, uint32_t ks_base,
+                                        uint32_t vts_base, uint32_t kb_base, int wave_, int lane_)
+      : wave(wave_), lane(lane_) {
 #pragma unroll
     for (int i = 0; i < NJ; ++i) {
       const int j = wave + i * NW;
@@ -527,22 +475,94 @@ __global__ __launch_bounds__(NW * 64) void flash_kernel(FlashArgs a) {
       l_step[i] = j < BLOCKS ? TILE * 2 : KB * 4;  // bytes per LDS stage
     }
   }
-  auto dma = [&](int t, int st) {
+  __device__ __forceinline__ void issue(int t, int st) const {
 #pragma unroll
     for (int i = 0; i < NJ; ++i) {
       const int j = wave + i * NW;
       if (j > BLOCKS) break;
       if (j < BLOCKS || lane < KB / 4)
-        dma16(g_src[i] + (long long)t * g_step[i] + lane * 16, __builtin_amdgcn_readfirstlane(l_dst[i] + st * l_step[i]));
+        dma16(g_src[i] + (long long)t * g_step[i] + lane * 16,
+              __builtin_amdgcn_readfirstlane(l_dst[i] + st * l_step[i]));
     }
-  };
+  }
   // Wait until at most the loads of the N most recent tiles are in flight for this wave
   // (wave w issues (BLOCKS - w) / NW + 1 loads per tile).
-  auto wait_newer = [&](auto n_c) {
-    constexpr int N = decltype(n_c)::value;
+  template <int N>
+  __device__ __forceinline__ void wait_newer() const {
     if (wave <= BLOCKS % NW) vm_wait<N * (BLOCKS / NW + 1)>();
     else vm_wait<N * (BLOCKS / NW)>();
-  };
+  }
+};
+
+// Scores are kept relative to a per-query reference m_ref (log2 units) that only moves when a
+// score exceeds it by more than 2^kRebase; between moves the output accumulator needs no
+// rescale. Any reference gives the same softmax, and p <= 2^kRebase stays in fp16 range.
+constexpr float kRebase = 8.0f;
+
+// SUPER: 64-key tiles per LDS stage. The loads of a stage are issued together and waited for
+// with one barrier, so a barrier falls on every SUPER-th step and a stage's loads are issued
+// (STAGES - 2) * SUPER + 1 .. (STAGES - 1) * SUPER steps before its K fragments are read.
+template <int D, int QT, int NW, int STAGES, int SUPER>
+__global__ __launch_bounds__(NW * 64) void flash_kernel(FlashArgs a) {
+  constexpr int DC = D / 16;             // k-steps of S
+  constexpr int DT = D / 32;             // dim tiles of O
+  constexpr int TILE = KB * D;           // halfs per K (or V) tile image
+  constexpr int NSLOT = STAGES * SUPER;  // tile slots in LDS; tile t lives in slot t % NSLOT
+  static_assert(STAGES == 3 || (STAGES == 4 && SUPER == 1), "three stages, or four of one tile");
+  static_assert(SUPER == 1 || SUPER == 2, "one or two tiles per stage");
+
+  // K of tile t+1 and V of tile t are read while the later stages land
+  __shared__ __attribute__((aligned(16))) half_t ks[NSLOT][TILE];
+  __shared__ __attribute__((aligned(16))) half_t vts[NSLOT][TILE];
+  __shared__ __attribute__((aligned(16))) float kbias[NSLOT][KB];
+
+  // Work unit: (pair = batch*H + head, query block). With xcd_order, consecutive block ids
+  // land on different XCDs (round-robin dispatch), so block id i is mapped to pair
+  // (i % 8) + 8 * ((i / 8) / qblocks): every query block of a pair runs on one XCD and its
+  // K/V tiles are fetched into that XCD's L2 once.
+  int pair, qb;
+  {
+    const int id = blockIdx.x;
+    if (a.xcd_order) {
+      const int local = id >> 3;
+      pair = (id & 7) + 8 * (local / a.qblocks);
+      qb = local % a.qblocks;
+    } else {
+      pair = id / a.qblocks;
+      qb = id % a.qblocks;
+    }
+  }
+  const int b = pair / a.H, h = pair % a.H, bh = pair;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int q0 = qb * (NW * QT * 32) + wave * QT * 32;
+  const int lq = lane & 31, hi = lane >> 5;
+  const int ntiles = a.Lk_pad / KB;
+
+  const half_t* Kt = a.Kc + (long long)bh * ntiles * TILE;
+  const half_t* Vt = a.Vc + (long long)bh * ntiles * TILE;
+  const float* Bg = a.bias2 + (long long)b * a.Lk_pad;
+
+  half8_t qf[QT][DC];
+  load_q<D, QT>(a, b, h, bh, q0, lq, hi, qf);
+
+  float16_t o[QT][DT];
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[qt][dt][r] = 0.f;
+  float m_ref[QT], l_run[QT];
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    m_ref[qt] = 0.f;
+    l_run[qt] = 0.f;
+  }
+
+  TileLoader<D, NW> loader(Kt, Vt, Bg, lds_addr(ks), lds_addr(vts), lds_addr(kbias), wave, lane);
+  auto dma = [&](int t, int st) { loader.issue(t, st); };
+  auto wait_newer = [&](auto n_c) { loader.template wait_newer<decltype(n_c)::value>(); };
   using W0_ = std::integral_constant<int, 0>;
   using W1_ = std::integral_constant<int, 1>;
   using W2_ = std::integral_constant<int, 2>;
@@ -639,6 +659,7 @@ __global__ __launch_bounds__(NW * 64) void flash_kernel(FlashArgs a) {
 #pragma unroll
   for (int i = 0; i < NK; ++i) qk_mfma(sA, i, read_k(i, 0));
   if (0 >= a.bias_block0) add_bias(sA, 0);
+
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
     const float m = fmaxf(half_max(sA, 0, qt), half_max(sA, 1, qt));
