@@ -94,13 +94,30 @@ struct RotRowsArgs {
 // flight at once), the row statistics are wave reductions, and the 8 rows of a block fill
 // whole 128-byte lines of the tiled layout (rows 8q..8q+7 of a k-chunk are adjacent 16-byte
 // slots), so no line is assembled from partial writes of different L2s.
+// normMod: the block stages the modulation vectors (1 + scale, shift and the norm weight, if
+// any) in LDS once, in lane order (slot 64g + l holds the 4 columns lane l uses in group g, so
+// the waves' 16-byte reads are conflict-free), instead of every row's wave loading them from
+// L1: at 8 rows per block that is 3x the row's own bytes through L1 otherwise.
 template <int G, bool NORM>
 __global__ __launch_bounds__(512) void rot_rows_kernel(RotRowsArgs a) {
   const int row = blockIdx.x * 8 + (threadIdx.x >> 6);
-  if (row >= a.rows) return;
   constexpr int cols = 256 * G;
+  constexpr int NV = NORM ? 3 : 1;
+  __shared__ __attribute__((aligned(16))) float4 mods[NV][G * 64];  // [1 + scale, shift, w]
+  if (NORM) {
+    for (int i = threadIdx.x; i < G * 64; i += 512) {
+      const int c = (i / 64) * 256 + 16 * (i % 16) + 4 * ((i % 64) / 16);
+      const float4 sc = *reinterpret_cast<const float4*>(a.mod + a.scaleOff + c);
+      mods[0][i] = make_float4(1.0f + sc.x, 1.0f + sc.y, 1.0f + sc.z, 1.0f + sc.w);
+      mods[1][i] = *reinterpret_cast<const float4*>(a.mod + a.shiftOff + c);
+      if (a.w) mods[NV - 1][i] = *reinterpret_cast<const float4*>(a.w + c);
+    }
+    __syncthreads();
+  }
+  if (row >= a.rows) return;
   // lane l holds elements 16(l%16) + 4(l/16) .. +3 of every group: the layout of the
   // matrix-core FWHT (its float4 loads still cover each group's 1 KB once per wave)
+  const int lane = threadIdx.x & 63;
   const int lo = fwht_mfma_offset();
   const float* src = a.x + (long long)row * a.ldx + lo;
   float v[G][4];
@@ -108,25 +125,6 @@ __global__ __launch_bounds__(512) void rot_rows_kernel(RotRowsArgs a) {
   for (int g = 0; g < G; ++g) {
     const float4 in = *reinterpret_cast<const float4*>(src + g * 256);
     v[g][0] = in.x, v[g][1] = in.y, v[g][2] = in.z, v[g][3] = in.w;
-  }
-  // modulation of each element: y = ((v * r) * w) * (1 + scale) + shift, the reference's
-  // order (kernels.js:82-117). Up to 8 groups the three vectors are loaded together with the
-  // row (unconditional loads; without a norm weight the scale row stands in for w and is
-  // replaced by 1); above that they are loaded per group in the store loop, which keeps the
-  // wide rows (up to 4096 columns) out of scratch.
-  constexpr bool HOIST = NORM && G <= 8;
-  constexpr int GH = HOIST ? G : 1;
-  float4 wv[GH], sc1[GH], shv[GH];
-  const float* wp = a.w ? a.w : a.mod + a.scaleOff;
-  if (HOIST) {
-#pragma unroll
-    for (int g = 0; g < GH; ++g) {
-      const int c = g * 256 + lo;
-      const float4 sc = *reinterpret_cast<const float4*>(a.mod + a.scaleOff + c);
-      shv[g] = *reinterpret_cast<const float4*>(a.mod + a.shiftOff + c);
-      wv[g] = *reinterpret_cast<const float4*>(wp + c);
-      sc1[g] = make_float4(1.0f + sc.x, 1.0f + sc.y, 1.0f + sc.z, 1.0f + sc.w);
-    }
   }
   float r = 1.f;
   if (NORM) {
@@ -151,17 +149,11 @@ __global__ __launch_bounds__(512) void rot_rows_kernel(RotRowsArgs a) {
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     if (NORM) {
-      float4 ww, s1, sh;
-      if (HOIST) {
-        ww = wv[g], s1 = sc1[g], sh = shv[g];
-      } else {
-        const int c = g * 256 + lo;
-        const float4 sc = *reinterpret_cast<const float4*>(a.mod + a.scaleOff + c);
-        sh = *reinterpret_cast<const float4*>(a.mod + a.shiftOff + c);
-        ww = *reinterpret_cast<const float4*>(wp + c);
-        s1 = make_float4(1.0f + sc.x, 1.0f + sc.y, 1.0f + sc.z, 1.0f + sc.w);
-      }
+      // modulation of each element: y = ((v * r) * w) * (1 + scale) + shift, the reference's
+      // order (kernels.js:82-117)
+      const float4 s1 = mods[0][g * 64 + lane], sh = mods[1][g * 64 + lane];
       if (a.w) {
+        const float4 ww = mods[NV - 1][g * 64 + lane];
         v[g][0] = v[g][0] * r * ww.x * s1.x + sh.x, v[g][1] = v[g][1] * r * ww.y * s1.y + sh.y;
         v[g][2] = v[g][2] * r * ww.z * s1.z + sh.z, v[g][3] = v[g][3] * r * ww.w * s1.w + sh.w;
       } else {
