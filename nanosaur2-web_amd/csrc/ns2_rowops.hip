@@ -114,12 +114,20 @@ __global__ __launch_bounds__(512) void rot_rows_kernel(RotRowsArgs a) {
     }
     __syncthreads();
   }
-  if (row >= a.rows) return;
+  // Tiled output goes through LDS (fp16, rows padded by 32 bytes: the 16 units of a quarter-wave
+  // write-out read, 2 chunks x 8 rows, fall in 16 different bank groups). A wave past the last
+  // row still takes part in the block's barrier: it works on the last row, and its result is
+  // not written.
+  constexpr bool TSTAGE = true;
+  constexpr int TROW = cols + 16;
+  __shared__ __attribute__((aligned(16))) uint16_t tout[TSTAGE ? 8 * TROW : 8];
+  const bool active = row < a.rows;
+  if (!active && !(TSTAGE && a.tiled)) return;
   // lane l holds elements 16(l%16) + 4(l/16) .. +3 of every group: the layout of the
   // matrix-core FWHT (its float4 loads still cover each group's 1 KB once per wave)
   const int lane = threadIdx.x & 63;
   const int lo = fwht_mfma_offset();
-  const float* src = a.x + (long long)row * a.ldx + lo;
+  const float* src = a.x + (long long)(active ? row : a.rows - 1) * a.ldx + lo;
   float v[G][4];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
@@ -162,7 +170,27 @@ __global__ __launch_bounds__(512) void rot_rows_kernel(RotRowsArgs a) {
       }
     }
     fwht256_mfma(v[g], h);
-    store4_f16(a.y, row, g * 256 + lo, a.ldy, cols, a.tiled, v[g]);
+    if (!a.tiled || !TSTAGE) {
+      if (active) store4_f16(a.y, row, g * 256 + lo, a.ldy, cols, a.tiled, v[g]);
+    }
+    else {
+      uint2 o;
+      o.x = pack_half2(v[g][0], v[g][1]);
+      o.y = pack_half2(v[g][2], v[g][3]);
+      *reinterpret_cast<uint2*>(&tout[(threadIdx.x >> 6) * TROW + g * 256 + lo]) = o;
+    }
+  }
+  if (TSTAGE && a.tiled) {
+    // write-out of the block's 8 rows: 16-byte unit u = (chunk u / 8, row u % 8), so the 8 units
+    // of a chunk are one 128-byte line of the tiled layout and a wave writes 8 whole lines
+    __syncthreads();
+    const int row0 = blockIdx.x * 8;
+    for (int u = threadIdx.x; u < G * 32 * 8; u += 512) {
+      const int c = u / 8, r = u % 8;
+      if (row0 + r >= a.rows) continue;
+      const uint4 q = *reinterpret_cast<const uint4*>(&tout[r * TROW + 8 * c]);
+      *reinterpret_cast<uint4*>(a.y + tiled_off(row0 + r, 8 * c, cols)) = q;
+    }
   }
 }
 
