@@ -43,6 +43,8 @@ struct TGemmArgs {
   // order and applies the epilogue. part = nullptr: no split.
   float* part;
   int ksplit;
+  // column bands of the tile order (block_tile): 1 keeps the row-group order
+  int bands;
 };
 
 // 8 biased bytes (two dwords) -> 8 halfs: byte u -> half(0x6400 | u) - 1152 = u - 128 = w.
@@ -77,14 +79,25 @@ __device__ __forceinline__ float act_t(float x) {
 
 // XCD-aware tile order: consecutive block ids go to different XCDs (round-robin dispatch);
 // block i is given tile start(x) + i/8 of XCD x = i % 8, where XCD x owns the contiguous range
-// of T/8 (+1 for the first T%8 XCDs) tiles, so neighbouring tiles (sharing A rows and W
-// columns) run on the same XCD and meet in its L2. Tiles are walked with N fastest inside
-// groups of 4 row-tiles (A reuse in L2).
+// of T/8 (+1 for the first T%8 XCDs) tiles of a linear tile order, so neighbouring tiles
+// (sharing A rows and W columns) run on the same XCD and meet in its L2. The linear order:
+//  * bands > 1: column bands of ceil(tiles_n / bands) tiles, band by band, rows within a band,
+//    N fastest. An XCD's range is then a 2-D block of one band, whose weight slice (sized on
+//    the host to about half an L2) stays resident while its rows stream through once;
+//  * bands = 1: N fastest inside groups of 4 row-tiles (A reuse in L2), for weights that fit.
 __device__ __forceinline__ void block_tile(const TGemmArgs& p, int& tm, int& tn) {
   const int tiles = p.tiles_m * p.tiles_n;
   const int x = blockIdx.x % 8, local = blockIdx.x / 8;
   const int q = tiles / 8, rmd = tiles % 8;
   const int tile = x * q + (x < rmd ? x : rmd) + local;
+  if (p.bands > 1) {
+    const int bw = (p.tiles_n + p.bands - 1) / p.bands;
+    const int band = tile / (bw * p.tiles_m), rem = tile % (bw * p.tiles_m);
+    const int w = p.tiles_n - band * bw < bw ? p.tiles_n - band * bw : bw;  // the last band may be narrower
+    tm = rem / w;
+    tn = band * bw + rem % w;
+    return;
+  }
   const int group = 4;
   const int gsize = group * p.tiles_n;
   const int g = tile / gsize, rem = tile % gsize;
@@ -469,10 +482,32 @@ __global__ __launch_bounds__(256) void tile_w_kernel(const int8_t* __restrict__ 
   *reinterpret_cast<uint2*>(Wt + i * 8) = v;
 }
 
+// Weight bytes per column band of the tile order: half of an XCD's 4 MB L2.
+constexpr long long kBandBytes = 2ll << 20;
+
 template <int BM, int BN, int WM, int WN, int STAGES = 2, int EPI = 0>
 int launch_tiled(TGemmArgs p, int splits = 1) {
   p.tiles_m = (p.M + BM - 1) / BM;
   p.tiles_n = (p.N + BN - 1) / BN;
+  // column bands (1, 2, 4 or 8) by an estimate of the bytes the XCDs' L2s miss: with b bands
+  // each of the 8 XCDs reads its rows of A (A b / 8 in all) and a 1/b slice of W, re-read about
+  // twice when the slice exceeds kBandBytes and three times when it exceeds an L2 (the factors
+  // fit FETCH_SIZE at the DiT shapes: 3952 rows x {4608, 1536, 8192} x {1536, 4096}). Launches
+  // with a few row tiles read each weight tile about once whatever the order.
+  p.bands = 1;
+  if (p.tiles_m >= 8) {
+    const double a_bytes = (double)p.tiles_m * BM * p.K * 2, w_bytes = (double)p.N * p.K;
+    double best = 0;
+    for (int b = 1; b <= 8 && b <= p.tiles_n; b *= 2) {
+      const double slice = w_bytes / b;
+      const double f = slice <= kBandBytes ? 1.0 : (slice <= 2 * kBandBytes ? 2.0 : 3.0);
+      const double est = a_bytes * b + w_bytes * (8.0 / b) * f;
+      if (b == 1 || est < best) {
+        best = est;
+        p.bands = b;
+      }
+    }
+  }
   const dim3 grid(p.tiles_m * p.tiles_n, splits), block(WM * WN * 64);
   hipStream_t s = ns2::stream();
   const int rm = !p.resid ? 0 : (p.gate ? 2 : 1);
