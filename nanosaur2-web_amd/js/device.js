@@ -51,15 +51,18 @@ export function addr(x) {
 class BufferPool {
   constructor() {
     this.held = null;
+    this.liveBytes = 0;  // bytes of pooled buffers handed out and not yet put back
   }
   static round(bytes) {
     return native.poolRound(bytes);
   }
   get(bytes) {
     const [ptr, size] = native.poolGet(bytes);
+    this.liveBytes += size;
     return { buf: new DeviceBuffer(ptr, size, true), size };
   }
   put(buf, size) {
+    this.liveBytes -= size;
     if (this.held) this.held.push([buf, size]);
     else native.poolPut(buf.ptr, size);
   }
@@ -82,6 +85,9 @@ class BufferPool {
   }
   get allocated() {
     return native.poolStats().allocated;
+  }
+  get live() {
+    return this.liveBytes;
   }
   get peak() {
     return native.poolStats().peak;

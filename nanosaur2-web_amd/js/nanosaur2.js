@@ -370,28 +370,42 @@ export class Nanosaur2DiT {
   }
 
   // Device-resident pass: tokens [L, 64] (Tensor) -> out [L, 64] (Tensor, caller releases).
+  // onBlock(fraction done) is awaited after every block; the pipeline cancels a generation by
+  // throwing from it (app/pipeline.js:233-247). An error from a block or from onBlock ends the
+  // pass: its tensors go back to the pool before the error propagates, so the model stays
+  // usable (work already queued on the stream finishes before the buffers are reused).
   async forwardTokens(tokens, h, w, text, sigma, { pathDrop = false, onBlock } = {}) {
     const gpu = this.gpu;
     const L = h * w;
     const x = ops.linear(gpu, tokens, this.sEmbed, { name: "dit.s_embed" });
     const cs = this.rope(h, w);
-    const c = this.condition(text, sigma);
-    const total = pathDrop ? SPRINT_F + SPRINT_H : BLOCKS;
-    let done = 0;
-    const run = async (i, s) => {
-      this.block(i, s, L, text, c, cs);
-      if (onBlock) await onBlock(++done / total);
-    };
-    for (let i = 0; i < SPRINT_F; i++) await run(i, x);
-    if (!pathDrop) {
-      const g = ops.elementwise(gpu, "copy", x);
-      for (let i = SPRINT_F; i < BLOCKS - SPRINT_H; i++) await run(i, g);
-      const d = ops.elementwise(gpu, "sub", g, x);
-      g.release();
-      ops.linear(gpu, d, this.sprintOut, { out: x, resid: true, name: "dit.sprint_out" });
-      d.release();
+    let c = null;
+    let g = null;
+    try {
+      c = this.condition(text, sigma);
+      const total = pathDrop ? SPRINT_F + SPRINT_H : BLOCKS;
+      let done = 0;
+      const run = async (i, s) => {
+        this.block(i, s, L, text, c, cs);
+        if (onBlock) await onBlock(++done / total);
+      };
+      for (let i = 0; i < SPRINT_F; i++) await run(i, x);
+      if (!pathDrop) {
+        g = ops.elementwise(gpu, "copy", x);
+        for (let i = SPRINT_F; i < BLOCKS - SPRINT_H; i++) await run(i, g);
+        const d = ops.elementwise(gpu, "sub", g, x);
+        g.release();
+        g = null;
+        ops.linear(gpu, d, this.sprintOut, { out: x, resid: true, name: "dit.sprint_out" });
+        d.release();
+      }
+      for (let i = BLOCKS - SPRINT_H; i < BLOCKS; i++) await run(i, x);
+    } catch (e) {
+      if (g) g.release();
+      if (c) c.release();
+      x.release();
+      throw e;
     }
-    for (let i = BLOCKS - SPRINT_H; i < BLOCKS; i++) await run(i, x);
     const n = ops.normMod(gpu, x, c.final, 0, D, D);
     x.release();
     c.release();
@@ -410,8 +424,12 @@ export class Nanosaur2DiT {
     const lat = gpu.fromArray(latent, [CH, L]);
     const xin = ops.transpose(gpu, lat); // [L, 64]
     lat.release();
-    const out = await this.forwardTokens(xin, h, w, text, sigma, opts);
-    xin.release();
+    let out;
+    try {
+      out = await this.forwardTokens(xin, h, w, text, sigma, opts);
+    } finally {
+      xin.release();
+    }
     const x0t = ops.transpose(gpu, out); // [64, L]
     out.release();
     const x0 = await gpu.read(x0t);

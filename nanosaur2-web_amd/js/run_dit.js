@@ -3,7 +3,7 @@
 //   node run_dit.js (--weights FILE.safetensors | --synthetic SEED)
 //                   (--inputs DIR | --shape H,W,T[,SEED])
 //                   [--out FILE.f32] [--reference-ops] [--path-drop] [--lora FILE[:STRENGTH]]...
-//                   [--warmup N] [--reps N] [--profile]
+//                   [--warmup N] [--reps N] [--profile] [--abort-at K]
 //
 // --inputs DIR holds inputs.json {h, w, sigma, T} and latent.f32 [64*h*w], context.f32
 // [T*640], weights.f32 [T]. --out writes the x0 prediction [64, h, w] as raw fp32.
@@ -11,6 +11,9 @@
 // and wall clock), and once more host-to-host (upload, pass, readback); one JSON line with
 // the timings (and the per-op profile with --profile) is printed. --lora attaches a LoRA file
 // (strength 1 by default; repeatable) to the model's linears (lora.js), as the pipeline does.
+// --abort-at K first runs a pass whose onBlock throws an AbortError after block K, as the
+// pipeline's cancel does, and reports the error, the blocks run and the pooled bytes in use
+// before and after it; the other passes follow on the same model.
 
 import fs from "fs";
 import path from "path";
@@ -37,6 +40,7 @@ function parseArgs(argv) {
     else if (k === "--reps") a.reps = Number(next());
     else if (k === "--profile") a.profile = true;
     else if (k === "--lora") a.loras.push(parseLora(next()));
+    else if (k === "--abort-at") a.abortAt = Number(next());
     else throw new Error(`unknown argument ${k}`);
   }
   return a;
@@ -109,6 +113,31 @@ async function main() {
   const loadMs = Date.now() - t0;
   const report = { h, w, T: inp.T, tokens: h * w, fused: !a.referenceOps, pathDrop: !!a.pathDrop, load_ms: loadMs, device: gpu.info,
     loras: loraReports, weight_bytes: dit.weightBytes() };
+
+  if (a.abortAt !== undefined) {
+    // a cancelled pass (app/pipeline.js:233-247 throws from onBlock)
+    dit.rope(h, w);  // the RoPE table is cached per shape on first use: not part of the pass
+    await gpu.sync();
+    const liveBefore = gpu.pool.live;
+    let blocks = 0;
+    const onBlock = async () => {
+      blocks++;
+      await gpu.sync();
+      if (blocks >= a.abortAt) {
+        const e = new Error("Generation cancelled");
+        e.name = "AbortError";
+        throw e;
+      }
+    };
+    let error = null;
+    try {
+      await dit.forward(inp.latent, h, w, text, sigma, { pathDrop: !!a.pathDrop, onBlock });
+    } catch (e) {
+      error = e.name;
+    }
+    await gpu.sync();
+    report.abort = { at: a.abortAt, blocks, error, live_before: liveBefore, live_after: gpu.pool.live };
+  }
 
   if (a.out) {
     const x0 = await dit.forward(inp.latent, h, w, text, sigma, { pathDrop: !!a.pathDrop });

@@ -27,7 +27,7 @@ def weights_file(tmp_path_factory):
     return tensors, path, d
 
 
-def _run_case(weights_file, name, h, w, T, *, zero=(), path_drop=False, reference_ops=False, seed=7):
+def _run_case(weights_file, name, h, w, T, *, zero=(), path_drop=False, reference_ops=False, seed=7, extra=()):
     tensors, path, d = weights_file
     inp = F.make_inputs(h, w, T, seed=seed, zero_weight_tokens=zero)
     idir = str(d / f"in_{name}")
@@ -38,6 +38,7 @@ def _run_case(weights_file, name, h, w, T, *, zero=(), path_drop=False, referenc
         args.append("--path-drop")
     if reference_ops:
         args.append("--reference-ops")
+    args += list(extra)
     rep = F.run_node(args)
     got = torch.from_numpy(np.fromfile(out, dtype=np.float32).reshape(64, h, w))
     ref = F.oracle_forward(tensors, inp, path_drop=path_drop)
@@ -59,6 +60,16 @@ def test_dit_pass_masked_token_and_path_drop(weights_file):
     path-drop pass that skips the SPRINT blocks."""
     _run_case(weights_file, "masked", 5, 7, 12, zero=(3,), seed=11)
     _run_case(weights_file, "pathdrop", 5, 7, 12, path_drop=True, seed=12)
+
+
+def test_dit_pass_cancelled_between_blocks(weights_file):
+    """A pass cancelled from onBlock after 5 blocks (the pipeline's cancel, app/pipeline.js:233-247):
+    the AbortError propagates after exactly those blocks, every pooled buffer of the pass is back
+    in the pool, and the next pass on the same model matches the oracle."""
+    rep = _run_case(weights_file, "cancel", 6, 8, 16, extra=["--abort-at", "5"])
+    ab = rep["abort"]
+    assert ab["error"] == "AbortError" and ab["blocks"] == 5, ab
+    assert ab["live_after"] == ab["live_before"], ab
 
 
 def test_dit_pass_against_reference_golden(tmp_path):
