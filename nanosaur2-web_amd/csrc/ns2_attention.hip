@@ -475,15 +475,16 @@ struct TileLoader {
       l_step[i] = j < BLOCKS ? TILE * 2 : KB * 4;  // bytes per LDS stage
     }
   }
+  // load i (< NJ) of this wave for tile t into stage st; loads past the wave's share are none
+  __device__ __forceinline__ void issue_one(int i, int t, int st) const {
+    const int j = wave + i * NW;
+    if (j > BLOCKS) return;
+    if (j < BLOCKS || lane < KB / 4)
+      dma16(g_src[i] + (long long)t * g_step[i] + lane * 16, __builtin_amdgcn_readfirstlane(l_dst[i] + st * l_step[i]));
+  }
   __device__ __forceinline__ void issue(int t, int st) const {
 #pragma unroll
-    for (int i = 0; i < NJ; ++i) {
-      const int j = wave + i * NW;
-      if (j > BLOCKS) break;
-      if (j < BLOCKS || lane < KB / 4)
-        dma16(g_src[i] + (long long)t * g_step[i] + lane * 16,
-              __builtin_amdgcn_readfirstlane(l_dst[i] + st * l_step[i]));
-    }
+    for (int i = 0; i < NJ; ++i) issue_one(i, t, st);
   }
   // Wait until at most the loads of the N most recent tiles are in flight for this wave
   // (wave w issues (BLOCKS - w) / NW + 1 loads per tile).
