@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark: ms per 832x1216 int8 DiT pass + joint-attention TFLOP/s on one MI355X.
 
-  python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-dit] [--no-gemma]
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-dit] [--no-gemma] [--no-vendor]
 
 Prints one JSON line. Legs, in order:
 
@@ -27,7 +27,9 @@ Prints one JSON line. Legs, in order:
    - joint attention at 768x768 (2304 queries x 2432 keys, batch 1);
    - the int8 ConvRot linear at M = 2432 on fp32 activations for N x K = 4608x1536, 1536x1536,
      6144x1536 and 1536x6144: the rotation into the tiled fp16 operand plus the tiled GEMM.
-4. CPU baselines: the oracle (a PyTorch-CPU restatement of tools/reference.py, fp32) on this
+4. Vendor libraries at the same shapes, for scale (`vendor_reference`): hipBLASLt fp16 GEMMs at the
+   four block-linear shapes (3952 rows) and torch SDPA at the joint-attention shape.
+5. CPU baselines: the oracle (a PyTorch-CPU restatement of tools/reference.py, fp32) on this
    host's cores for the same workloads -- the DiT pass on a bounded sample (one joint and one
    image-only block at 3952 tokens, scaled to 18 blocks), the two attention shapes, the four
    linears and the text encoder -- 1 warm-up and up to 3 timed repetitions each (median).
@@ -296,6 +298,55 @@ def bench_linear_cfg1(lib, reps, warmup):
     return out
 
 
+def bench_vendor(reps=20):
+    """The vendor libraries at the same shapes, for scale: torch.matmul in fp16 (hipBLASLt) on the
+    four block-linear shapes of the pass at 3952 rows (a plain GEMM on fp16 weights, without the
+    int8 decode, rotation or epilogue of the DiT's linears), and torch's scaled_dot_product_attention
+    (flash and memory-efficient backends) at the joint-attention shape in fp16 (no RoPE or key
+    bias). Best of 5 runs of `reps` calls, timed with torch events."""
+    import torch
+    import torch.nn.functional as F
+
+    def best_ms(fn):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        best = float("inf")
+        for _ in range(5):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            for _ in range(reps):
+                fn()
+            b.record()
+            torch.cuda.synchronize()
+            best = min(best, a.elapsed_time(b) / reps)
+        return best
+
+    M = H_IMG * W_IMG
+    gemms = []
+    for name, N, K in (("qkv", 3 * D, D), ("proj", D, D), ("w12", 2 * I_MLP, D), ("w3", D, I_MLP)):
+        a = torch.randn(M, K, device="cuda", dtype=torch.float16)
+        w = torch.randn(N, K, device="cuda", dtype=torch.float16)
+        ms = best_ms(lambda: a @ w.t())
+        gemms.append({"shape": f"{name}: M {M} x N {N} x K {K}", "ms": ms, "tflops": 2 * M * N * K / (ms / 1e3) / 1e12})
+    B, Lq, Lk = 2, M, M + T_TXT
+    q = torch.randn(B, HEADS, Lq, HD, device="cuda", dtype=torch.float16)
+    k = torch.randn(B, HEADS, Lk, HD, device="cuda", dtype=torch.float16)
+    v = torch.randn(B, HEADS, Lk, HD, device="cuda", dtype=torch.float16)
+    sdpa = {}
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    for be in (SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION):
+        try:
+            with sdpa_kernel([be]):
+                ms = best_ms(lambda: F.scaled_dot_product_attention(q, k, v))
+            sdpa[be.name.lower()] = {"ms": ms, "tflops": 4 * B * HEADS * Lq * Lk * HD / (ms / 1e3) / 1e12}
+        except RuntimeError as e:  # backend not built into this torch
+            sdpa[be.name.lower()] = {"unavailable": str(e)[:200]}
+    return {"hipblaslt_fp16_matmul": gemms,
+            "torch_sdpa_fp16": dict(sdpa, config=f"{Lq} queries x {Lk} keys, {HEADS} heads x {HD}, batch {B}")}
+
+
 def copy_calibration(lib, n=64 << 20, reps=3):
     """ns2_elementwise copy of n fp32 values: 4n bytes read + 4n bytes written per launch,
     the known-size kernel that HBM byte counters are scaled against."""
@@ -466,6 +517,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     ap.add_argument("--no-dit", action="store_true", help="skip the DiT pass (kernels and CPU legs only)")
     ap.add_argument("--no-gemma", action="store_true", help="skip the text-encoder measurement")
+    ap.add_argument("--no-vendor", action="store_true", help="skip the hipBLASLt / SDPA reference timings")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a 256 MiB -> 256 MiB copy kernel (reference point for HBM counters)")
     args = ap.parse_args()
@@ -510,6 +562,12 @@ def main():
             f"GEMM {r['gemm_tflops']:.0f})")
     if args.copy_calibration:
         attn["copy_calibration"] = copy_calibration(lib)
+    vendor = None
+    if not args.no_vendor:
+        vendor = bench_vendor()
+        log("vendor: hipBLASLt fp16 " + ", ".join(f"{g['shape'].split(':')[0]} {g['tflops']:.0f}"
+                                                   for g in vendor["hipblaslt_fp16_matmul"]) + " TFLOP/s; SDPA "
+            + ", ".join(f"{k} {v['ms'] * 1e3:.0f} us" for k, v in vendor["torch_sdpa_fp16"].items() if "ms" in v))
 
     cpu = None
     if not args.no_cpu:
@@ -585,6 +643,7 @@ def main():
             "traffic_source": ATTN_TRAFFIC_SOURCE,
         },
         "cpu_baseline": cpu,
+        "vendor_reference": vendor,
         "kernels": kernels,
     }
     print(json.dumps(out), flush=True)

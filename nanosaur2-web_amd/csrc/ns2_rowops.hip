@@ -103,7 +103,7 @@ __global__ __launch_bounds__(512) void rot_rows_kernel(RotRowsArgs a) {
   const int row = blockIdx.x * 8 + (threadIdx.x >> 6);
   constexpr int cols = 256 * G;
   constexpr int NV = NORM ? 3 : 1;
-  __shared__ __attribute__((aligned(16))) float4 mods[NV][G * 64];  // [1 + scale, shift, w]
+  __shared__ __attribute__((aligned(16))) float4 mods[NV][NORM ? G * 64 : 1];  // [1 + scale, shift, w]
   if (NORM) {
     for (int i = threadIdx.x; i < G * 64; i += 512) {
       const int c = (i / 64) * 256 + 16 * (i % 16) + 4 * ((i % 64) / 16);
@@ -115,10 +115,10 @@ __global__ __launch_bounds__(512) void rot_rows_kernel(RotRowsArgs a) {
     __syncthreads();
   }
   // Tiled output goes through LDS (fp16, rows padded by 32 bytes: the 16 units of a quarter-wave
-  // write-out read, 2 chunks x 8 rows, fall in 16 different bank groups). A wave past the last
-  // row still takes part in the block's barrier: it works on the last row, and its result is
-  // not written.
-  constexpr bool TSTAGE = true;
+  // write-out read, 2 chunks x 8 rows, fall in 16 different bank groups), up to 16 groups (66 KB;
+  // wider rows store directly and keep several blocks per CU). A wave past the last row still
+  // takes part in the block's barrier: it works on the last row, and its result is not written.
+  constexpr bool TSTAGE = G <= 16;
   constexpr int TROW = cols + 16;
   __shared__ __attribute__((aligned(16))) uint16_t tout[TSTAGE ? 8 * TROW : 8];
   const bool active = row < a.rows;
@@ -205,6 +205,9 @@ void launch_rot_rows(const RotRowsArgs& a, int groups) {
     NS2_ROT_CASE(7) NS2_ROT_CASE(8) NS2_ROT_CASE(9) NS2_ROT_CASE(10) NS2_ROT_CASE(11) NS2_ROT_CASE(12)
     NS2_ROT_CASE(13) NS2_ROT_CASE(14) NS2_ROT_CASE(15) NS2_ROT_CASE(16)
 #undef NS2_ROT_CASE
+    // rotation only, rows up to 6144 columns (the widest block-linear input)
+    case 20: if constexpr (!NORM) rot_rows_kernel<20, NORM><<<grid, block, 0, s>>>(a); break;
+    case 24: if constexpr (!NORM) rot_rows_kernel<24, NORM><<<grid, block, 0, s>>>(a); break;
     default: break;
   }
 }
@@ -409,7 +412,7 @@ int ns2_rotate_f16(const float* x, int ldx, uint16_t* y, int ldy, int rows, int 
   NS2_REQUIRE(x && y && aligned16(x) && aligned8(y), "ns2_rotate_f16: null or unaligned buffer");
   const int gpr = cols / 256;
   ns2::ProfScope prof_("rotate_f16");
-  if (gpr <= 16) {
+  if (gpr <= 16 || gpr == 20 || gpr == 24) {
     RotRowsArgs a{x, ldx, nullptr, 0, 0, nullptr, 0.f, y, ldy, rows, tiled};
     launch_rot_rows<false>(a, gpr);
   } else {

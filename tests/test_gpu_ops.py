@@ -212,6 +212,23 @@ def test_tiled_producers(ns2lib, rows):
         assert torch.equal(got, flat.cpu()), name
 
 
+@pytest.mark.parametrize("rows,cols", [(9, 5120), (100, 6144), (2432, 6144)])
+def test_rotate_f16_wide_rows(ns2lib, rows, cols):
+    """The rotation producer on rows of 20 and 24 groups (the widest block-linear input, 6144):
+    the oracle's values, tiled and row-major, and both forms equal."""
+    g = gen(rows + cols)
+    xh = torch.randn(rows, cols, generator=g)
+    x = xh.to(dev)
+    flat = torch.empty(rows, cols, dtype=torch.int16, device=dev)
+    ns2lib.rotate_f16(x, cols, flat, cols, rows, cols)
+    til = tiled_operand(rows, cols)
+    ns2lib.rotate_f16(x, cols, til, cols, rows, cols, tiled=True)
+    torch.cuda.synchronize()
+    got = untile_a(til.cpu(), rows, cols)
+    assert_close(f16_as_float(got), O.rotate(xh.double()), TOL_F16_OUT, f"rotate_f16 {rows}x{cols}")
+    assert torch.equal(got, flat.cpu())
+
+
 def _tiled_linear_inputs(M, N, K, seed):
     g = gen(seed)
     x = torch.randn(M, K, generator=g)
