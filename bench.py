@@ -57,14 +57,15 @@ HBM_PEAK_GBS = 8000.0        # MI355X HBM3E
 H_IMG, W_IMG, T_TXT, D, HEADS, HD, I_MLP, BLOCKS = 76, 52, 256, 1536, 16, 96, 4096, 18
 CFG1_M = 2432
 CFG1_SHAPES = (("qkv", 4608, 1536), ("proj", 1536, 1536), ("up", 6144, 1536), ("down", 1536, 6144))
-# HBM bytes per launch from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE, each scaled by what the
-# counter reads for a copy kernel of known size (FETCH_SIZE x 2.0, WRITE_SIZE x 1.0): the mean
-# over the pass's tiled-GEMM launches and one flash launch at 3952x4208 batch 2. Beside each, the
-# algorithmic bytes of the same launches. Source files name the commands.
-GEMM_TRAFFIC_BYTES_PER_LAUNCH = 148.2e6
-GEMM_ALGORITHMIC_BYTES_PER_LAUNCH = 67.5e6   # N*K int8 W + 2*M*K fp16 A + output (+ old output for +=)
+# Bytes per launch that leave the L2s (rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE, each scaled by
+# what the counter reads for a copy kernel of known size: FETCH_SIZE x 2.0, WRITE_SIZE x 1.0), beside
+# the algorithmic bytes of the same launches: the mean over one pass's 73 tiled-GEMM launches on the
+# 3952 image rows (18 each of qkv and w12+GLU, 36 of proj and w3, the stacked kv_y), and one flash
+# launch at 3952x4208 batch 2. The source files hold the per-kernel tables and the commands.
+GEMM_TRAFFIC_BYTES_PER_LAUNCH = 130.1e6
+GEMM_ALGORITHMIC_BYTES_PER_LAUNCH = 74.9e6   # N*K int8 W + 2*M*K fp16 A + output (+ old output for +=)
 GEMM_TRAFFIC_SOURCE = "profiles/dit_pass_832x1216_int8.md"
-ATTN_TRAFFIC_BYTES_PER_LAUNCH = 173.9e6
+ATTN_TRAFFIC_BYTES_PER_LAUNCH = 174.0e6
 ATTN_ALGORITHMIC_BYTES_PER_LAUNCH = 149.1e6  # fp32 Q (read in the kernel's prologue), fp16 K, V^T, fp32 O
 ATTN_TRAFFIC_SOURCE = "profiles/attn_flash_joint_3952x4208_b2.md"
 

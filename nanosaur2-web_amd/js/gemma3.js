@@ -14,31 +14,46 @@ import { ropeTable } from "./common.js";
 export const GEMMA = { layers: 18, hidden: 640, heads: 4, kvHeads: 1, headDim: 256, globalEvery: 6 };
 const RUN = GEMMA.layers - 1; // layers needed for the penultimate hidden state
 
+// One decoder layer's tensors under the checkpoint's names (app/models/gemma3.js:17-41 reads
+// the same set): its norm vectors, and its linears with q|k|v and gate|up stacked into one
+// weight each (concatLinears), so each pair of projections is one GEMM.
+const LAYER_NORMS = {
+  inNorm: "input_layernorm",
+  postAttnNorm: "post_attention_layernorm",
+  preMlpNorm: "pre_feedforward_layernorm",
+  postMlpNorm: "post_feedforward_layernorm",
+  qn: "self_attn.q_norm",
+  kn: "self_attn.k_norm",
+};
+const LAYER_LINEARS = {
+  qkv: ["self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj"],
+  o: ["self_attn.o_proj"],
+  gateUp: ["mlp.gate_proj", "mlp.up_proj"],
+  down: ["mlp.down_proj"],
+};
+
+async function loadLayer(gpu, st, i) {
+  const prefix = `model.layers.${i}.`;
+  // every GEMMA.globalEvery-th layer attends globally, the others through the sliding window
+  const layer = { global: (i + 1) % GEMMA.globalEvery === 0 };
+  for (const [key, name] of Object.entries(LAYER_NORMS)) layer[key] = await st.vector(gpu, `${prefix}${name}.weight`, 1);
+  for (const [key, parts] of Object.entries(LAYER_LINEARS)) {
+    const ws = [];
+    for (const part of parts) ws.push(await st.linear(gpu, `${prefix}${part}.`));
+    layer[key] = ws.length > 1 ? concatLinears(gpu, ws) : ws[0];
+  }
+  return layer;
+}
+
 export class Gemma3 {
   // st: { linear, vector, rows, has } (weights.js SafeTensors or the synthetic source)
   static async load(gpu, st, onProgress) {
     const m = new Gemma3(gpu, st);
-    const L = [];
+    m.layers = [];
     for (let i = 0; i < RUN; i++) {
-      const p = `model.layers.${i}.`;
-      const norm = (n) => st.vector(gpu, p + n + ".weight", 1);
-      L.push({
-        global: (i + 1) % GEMMA.globalEvery === 0,
-        inNorm: await norm("input_layernorm"),
-        postAttnNorm: await norm("post_attention_layernorm"),
-        preMlpNorm: await norm("pre_feedforward_layernorm"),
-        postMlpNorm: await norm("post_feedforward_layernorm"),
-        qn: await norm("self_attn.q_norm"),
-        kn: await norm("self_attn.k_norm"),
-        qkv: concatLinears(gpu, [await st.linear(gpu, p + "self_attn.q_proj."), await st.linear(gpu, p + "self_attn.k_proj."),
-          await st.linear(gpu, p + "self_attn.v_proj.")]),
-        o: await st.linear(gpu, p + "self_attn.o_proj."),
-        gateUp: concatLinears(gpu, [await st.linear(gpu, p + "mlp.gate_proj."), await st.linear(gpu, p + "mlp.up_proj.")]),
-        down: await st.linear(gpu, p + "mlp.down_proj."),
-      });
+      m.layers.push(await loadLayer(gpu, st, i));
       if (onProgress) onProgress((i + 1) / RUN);
     }
-    m.layers = L;
     m.norm = await st.vector(gpu, "model.norm.weight", 1);
     return m;
   }

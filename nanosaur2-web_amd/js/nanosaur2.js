@@ -25,18 +25,22 @@ const CH = 64;
 
 // Sinusoidal embedding of sigma * 1000, cos half then sin half, 256 dims, computed in fp32
 // steps (app/models/nanosaur2.js:24-36; tools/reference.py:213-217).
+// Sinusoidal embedding of t = 1000 sigma: 128 cosines, then 128 sines, of t times the frequencies
+// exp(-ln(1e4) i / 128). The frequency table, the product t f and t itself are rounded to fp32
+// where the reference rounds them (app/models/nanosaur2.js:25-36), which makes the embedding
+// bit-identical to the reference's.
+const T_FREQS = Float32Array.from({ length: 128 }, (_, i) => Math.exp(Math.fround((-Math.log(10000) * i) / 128)));
+
 export function timestepEmbedding(sigma) {
-  const dim = 256;
-  const half = dim / 2;
   const t = Math.fround(sigma * 1000);
-  const out = new Float32Array(dim);
-  for (let i = 0; i < half; i++) {
-    const f = Math.fround(Math.exp(Math.fround((-Math.log(10000) * i) / half)));
-    const a = Math.fround(t * f);
-    out[i] = Math.cos(a);
-    out[half + i] = Math.sin(a);
-  }
-  return out;
+  const n = T_FREQS.length;
+  const emb = new Float32Array(2 * n);
+  T_FREQS.forEach((f, i) => {
+    const angle = Math.fround(t * f);
+    emb[i] = Math.cos(angle);
+    emb[n + i] = Math.sin(angle);
+  });
+  return emb;
 }
 
 export class Nanosaur2DiT {
@@ -174,27 +178,40 @@ export class Nanosaur2DiT {
   // hidden: Float32Array [L, 640]; weights: per-token prompt weights. Tokens with weight <= 0
   // are masked in the reference (no key, zeroed text row, no pooling contribution), so they
   // are dropped; they still count in the pooling denominator (app/models/nanosaur2.js:94-118).
+  // The prompt as the blocks consume it (app/models/nanosaur2.js:97-118): tokens of weight > 0
+  // through y_embedder (linear, then RMSNorm) -> { L, y [L, D], pool [L] (their weights),
+  // poolScale = 1 / max(1, sum of all weights), bias [L] (log weights, floored at 1e-4) or null
+  // when every kept weight is 1 }. Zero-weight tokens are dropped where the reference's dense
+  // path masks them; the pooling denominator still counts every weight.
   prepareText(hidden, weights) {
     const gpu = this.gpu;
-    const keep = [];
-    weights.forEach((w, i) => { if (w > 0) keep.push(i); });
-    const L = keep.length;
-    const denom = Math.max(1, weights.reduce((a, b) => a + b, 0));
-    if (!L) return { L: 0, release() {} };
-    const ctx = new Float32Array(L * 640);
-    keep.forEach((src, i) => ctx.set(hidden.subarray(src * 640, (src + 1) * 640), i * 640));
-    const x = gpu.fromArray(ctx, [L, 640]);
-    const h = ops.linear(gpu, x, this.yEmbed, { name: "dit.y_embed" });
-    x.release();
-    const y = ops.rmsnorm(gpu, h, this.yNorm, D);
-    h.release();
-    const w = keep.map((i) => weights[i]);
-    const pool = gpu.fromArray(new Float32Array(w), [L]);
-    const bias = w.some((v) => v !== 1)
-      ? gpu.fromArray(new Float32Array(w.map((v) => Math.log(Math.max(v, 1e-4)))), [L]) : null;
+    let total = 0;
+    const rows = [];
+    for (let i = 0; i < weights.length; i++) {
+      total += weights[i];
+      if (weights[i] > 0) rows.push(i);
+    }
+    const L = rows.length;
+    if (L === 0) return { L: 0, release() {} };
+    const kept = Float32Array.from(rows, (i) => weights[i]);
+    const gathered = new Float32Array(L * 640);
+    rows.forEach((src, dst) => gathered.set(hidden.subarray(src * 640, src * 640 + 640), dst * 640));
+    const ctx = gpu.fromArray(gathered, [L, 640]);
+    const emb = ops.linear(gpu, ctx, this.yEmbed, { name: "dit.y_embed" });
+    ctx.release();
+    const y = ops.rmsnorm(gpu, emb, this.yNorm, D);
+    emb.release();
+    const pool = gpu.fromArray(kept, [L]);
+    // the log of each weight as given (before its fp32 rounding), then rounded once
+    const weighted = kept.some((w) => w !== 1);
+    const bias = weighted ? gpu.fromArray(Float32Array.from(rows, (i) => Math.log(Math.max(weights[i], 1e-4))), [L]) : null;
     return {
-      L, y, pool, poolScale: 1 / denom, bias,
-      release() { y.release(); pool.release(); if (bias) bias.release(); },
+      L, y, pool, poolScale: 1 / Math.max(1, total), bias,
+      release() {
+        y.release();
+        pool.release();
+        if (bias) bias.release();
+      },
     };
   }
 
