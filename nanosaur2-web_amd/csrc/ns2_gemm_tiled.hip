@@ -391,21 +391,25 @@ void gemm_tiled_kernel(TGemmArgs p) {
       }
     }
     __syncthreads();
-    // rotation: wave w rotates rows 8w .. 8w+7, the fp16 result in place in the first 512 bytes
-    // of the row, its 16-byte chunk c stored at chunk c ^ (row & 7): the copy-out below reads one
-    // chunk of 64 rows 1 KB apart per wave, and the swizzle puts 8 consecutive rows in 8
-    // different bank groups (unswizzled, all 64 lanes hit the same four banks)
+    // rotation: wave w rotates rows 8w .. 8w+7 on the matrix cores, the fp16 result in place in
+    // the first 512 bytes of the row, its 16-byte chunk c stored at chunk c ^ (row & 7): the
+    // copy-out below reads one chunk of 64 rows 1 KB apart per wave, and the swizzle puts 8
+    // consecutive rows in 8 different bank groups (unswizzled, all 64 lanes hit the same four
+    // banks)
 #pragma unroll
     for (int rr = 0; rr < 64 / NW; ++rr) {
+      // the matrix-core FWHT: lane l holds columns lo .. lo+3, lo = 16(l%16) + 4(l/16)
+      const half4v_t hf = fwht_h16_fragment();
+      const int lo = fwht_mfma_offset();
       const int row = (64 / NW) * wave + rr;
-      const float4 in = *reinterpret_cast<const float4*>(T + row * 256 + lane * 4);
+      const float4 in = *reinterpret_cast<const float4*>(T + row * 256 + lo);
       float v[4] = {in.x, in.y, in.z, in.w};
-      fwht256_wave(v);
+      fwht256_mfma(v, hf);
       uint2 o;
       o.x = pack_half2(v[0], v[1]);
       o.y = pack_half2(v[2], v[3]);
       char* rb = reinterpret_cast<char*>(T + row * 256);
-      *reinterpret_cast<uint2*>(rb + ((lane >> 1) ^ (row & 7)) * 16 + (lane & 1) * 8) = o;
+      *reinterpret_cast<uint2*>(rb + ((lo >> 3) ^ (row & 7)) * 16 + ((lo >> 2) & 1) * 8) = o;
     }
     __syncthreads();
     // 32 chunks of 8 columns x 64 rows: 1 KB contiguous each in the tiled layout
