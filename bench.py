@@ -632,7 +632,7 @@ def main():
             "traffic_source": GEMM_TRAFFIC_SOURCE,
         },
         "roofline_attention": {
-            "kernel": "flash_kernel (joint attention, 3952x4208, batch 2)",
+            "kernel": "flash_wide_kernel (joint attention, 3952x4208, batch 2: 512-query blocks)",
             "bound": "mfma",
             "achieved": attn["flash_tflops"],
             "peak": FP16_PEAK_TFLOPS,

@@ -849,6 +849,266 @@ __global__ __launch_bounds__(NW * 64) void flash_kernel(FlashArgs a) {
   }
 }
 
+// Wide variant for grids that fill the chip with 512-query blocks (the batch-2 CFG pair at
+// 3952 x 4208: 8 query blocks x 32 (batch, head) pairs = 256 work-groups): every wave owns 64
+// queries (two 32-query column tiles), so one 64-key K/V tile staged in LDS serves 512 queries
+// and the copies and barriers per product are halved. The Q^T fragments no longer fit in
+// registers beside the second tile's accumulators: the prologue writes each wave's prepared
+// queries into its own chunk-major LDS region (chunk 2c + hi of query 32 qt + lq at
+// (chunk * 64 + 32 qt + lq) * 8 halfs, conflict-free like K), and the score products read them
+// back. One score buffer per step, K/V in two LDS stages:
+//   barrier, copy tile t+1 -> QK of tile t (24 MFMAs) -> key bias, row maxima, lazy reference
+//   move -> P = exp2(S) -> PV of tile t (24 MFMAs)
+// Fragment reads are issued one k-step (QK) or two fragments (PV) ahead of their products; the
+// scheduling barriers keep that order (the default scheduler would place every read right
+// before its product). The softmax arithmetic, the lazy reference and the fp16 P with its row
+// sums are those of flash_kernel, so the two give the same results.
+template <int D>
+__global__ __launch_bounds__(512) void flash_wide_kernel(FlashArgs a) {
+  constexpr int NW = 8;          // waves per block
+  constexpr int QT = 2;          // 32-query column tiles per wave
+  constexpr int DC = D / 16;     // k-steps of S
+  constexpr int DT = D / 32;     // dim tiles of O
+  constexpr int TILE = KB * D;   // halfs per K (or V) tile image
+  constexpr int QCH = D / 8;     // 8-dim chunks of a Q row
+  __shared__ __attribute__((aligned(16))) half_t qs[NW][QCH * 64 * 8];
+  __shared__ __attribute__((aligned(16))) half_t ks[2][TILE];
+  __shared__ __attribute__((aligned(16))) half_t vts[2][TILE];
+  __shared__ __attribute__((aligned(16))) float kbias[2][KB];
+
+  int pair, qb;
+  {
+    const int id = blockIdx.x;
+    if (a.xcd_order) {
+      const int local = id >> 3;
+      pair = (id & 7) + 8 * (local / a.qblocks);
+      qb = local % a.qblocks;
+    } else {
+      pair = id / a.qblocks;
+      qb = id % a.qblocks;
+    }
+  }
+  const int b = pair / a.H, h = pair % a.H, bh = pair;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int q0 = qb * (NW * QT * 32) + wave * QT * 32;
+  const int lq = lane & 31, hi = lane >> 5;
+  const int ntiles = a.Lk_pad / KB;
+
+  const half_t* Kt = a.Kc + (long long)bh * ntiles * TILE;
+  const half_t* Vt = a.Vc + (long long)bh * ntiles * TILE;
+  const float* Bg = a.bias2 + (long long)b * a.Lk_pad;
+  TileLoader<D, NW> loader(Kt, Vt, Bg, lds_addr(ks), lds_addr(vts), lds_addr(kbias), wave, lane);
+  loader.issue(0, 0);
+  if (ntiles > 1) loader.issue(1, 1);
+
+  half_t* qw = &qs[wave][0];
+  {
+    half8_t qf[QT][DC];
+    load_q<D, QT>(a, b, h, bh, q0, lq, hi, qf);
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+      for (int c = 0; c < DC; ++c)
+        *reinterpret_cast<half8_t*>(qw + ((2 * c + hi) * 64 + 32 * qt + lq) * 8) = qf[qt][c];
+  }
+
+  float16_t o[QT][DT];
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[qt][dt][r] = 0.f;
+  float m_ref[QT], l_run[QT];
+  float16_t minit[QT];  // -m_ref in every accumulator slot: the C operand of each score chain
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    m_ref[qt] = 0.f;
+    l_run[qt] = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) minit[qt][r] = 0.f;
+  }
+
+  auto read_k = [&](int c, int kt, int buf) {
+    return *reinterpret_cast<const half8_t*>(&ks[buf][((2 * c + hi) * KB + kt * 32 + lq) * 8]);
+  };
+  auto read_q = [&](int c, int qt) {
+    return *reinterpret_cast<const half8_t*>(qw + ((2 * c + hi) * 64 + 32 * qt + lq) * 8);
+  };
+  // V fragment i = (2kt + kk) * DT + dt: stored key chunk 4kt + 2kk + hi of dim 32dt + lq
+  auto read_v = [&](int i, int buf) {
+    const int kt = i / (2 * DT), kk = (i / DT) % 2, dt = i % DT;
+    return *reinterpret_cast<const half8_t*>(&vts[buf][((4 * kt + 2 * kk + hi) * D + dt * 32 + lq) * 8]);
+  };
+  auto half_max = [&](const float16_t& v) {
+    const float a0 = __builtin_fmaxf(__builtin_fmaxf(v[0], v[1]), v[2]);
+    const float b0 = __builtin_fmaxf(__builtin_fmaxf(v[3], v[4]), v[5]);
+    const float c0 = __builtin_fmaxf(__builtin_fmaxf(v[6], v[7]), v[8]);
+    const float d0 = __builtin_fmaxf(__builtin_fmaxf(v[9], v[10]), v[11]);
+    const float e0 = __builtin_fmaxf(__builtin_fmaxf(v[12], v[13]), v[14]);
+    return __builtin_fmaxf(__builtin_fmaxf(__builtin_fmaxf(a0, b0), c0),
+                           __builtin_fmaxf(__builtin_fmaxf(d0, e0), v[15]));
+  };
+  auto col_max = [&](float m) {
+    float lo = m, hi2 = m;
+    permlane32_swap(lo, hi2);
+    return __builtin_fmaxf(lo, hi2);
+  };
+
+  vm_wait<0>();
+  __syncthreads();
+
+  auto step = [&](int t, auto bias_c) {
+    constexpr bool BIAS = decltype(bias_c)::value;
+    const int buf = t & 1;
+    // tile t landed (this wave's copies, then the barrier for every wave's); every wave is done
+    // with tile t-1, whose stage now receives tile t+1
+    if (t > 0) {
+      vm_wait<0>();
+      __syncthreads();
+      if (t + 1 < ntiles) loader.issue(t + 1, buf ^ 1);
+    }
+    // ---- S^T = K Q^T - m_ref
+    float16_t s[2][QT];
+    {
+      half8_t kf[2][2], qf[2][QT];
+      kf[0][0] = read_k(0, 0, buf);
+      kf[0][1] = read_k(0, 1, buf);
+      qf[0][0] = read_q(0, 0);
+      qf[0][1] = read_q(0, 1);
+#pragma unroll
+      for (int c = 0; c < DC; ++c) {
+        const int cur = c & 1, nx = cur ^ 1;
+        if (c + 1 < DC) {
+          kf[nx][0] = read_k(c + 1, 0, buf);
+          kf[nx][1] = read_k(c + 1, 1, buf);
+          qf[nx][0] = read_q(c + 1, 0);
+          qf[nx][1] = read_q(c + 1, 1);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+          for (int kt = 0; kt < 2; ++kt)
+            s[kt][qt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[cur][kt], qf[cur][qt], c == 0 ? minit[qt] : s[kt][qt],
+                                                               0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    if constexpr (BIAS) {
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const float4 bb = *reinterpret_cast<const float4*>(&kbias[buf][kt * 32 + 8 * g + 4 * hi]);
+#pragma unroll
+          for (int qt = 0; qt < QT; ++qt) {
+            s[kt][qt][4 * g + 0] += bb.x;
+            s[kt][qt][4 * g + 1] += bb.y;
+            s[kt][qt][4 * g + 2] += bb.z;
+            s[kt][qt][4 * g + 3] += bb.w;
+          }
+        }
+    }
+    // ---- the reference moves when a score exceeds it by more than 2^kRebase, or on the first
+    // tile (nothing accumulated yet: the reference becomes the tile maximum)
+    {
+      float mx[QT];
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) mx[qt] = col_max(__builtin_fmaxf(half_max(s[0][qt]), half_max(s[1][qt])));
+      bool need = false;
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) need |= (mx[qt] > kRebase) || (l_run[qt] == 0.f);
+      if (__builtin_amdgcn_ballot_w64(need)) {
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) {
+          const float shift = (l_run[qt] == 0.f) ? mx[qt] : fmaxf(mx[qt], 0.f);
+          const float alpha = __builtin_amdgcn_exp2f(-shift);
+          m_ref[qt] += shift;
+          l_run[qt] *= alpha;
+#pragma unroll
+          for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o[qt][dt][r] *= alpha;
+#pragma unroll
+          for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) s[kt][qt][r] -= shift;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) minit[qt][r] = -m_ref[qt];
+        }
+      }
+    }
+    // ---- P = exp2(S) in fp16; row sums of the rounded values the PV products use
+    half8_t pf[2][QT][2];
+    {
+      float ls[QT] = {0.f, 0.f};
+      const half2_t one = {(half_t)1.0f, (half_t)1.0f};
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+            for (int e = 0; e < 8; e += 2) {
+              half2_t pp;
+              pp[0] = (half_t)__builtin_amdgcn_exp2f(s[kt][qt][kk * 8 + e]);
+              pp[1] = (half_t)__builtin_amdgcn_exp2f(s[kt][qt][kk * 8 + e + 1]);
+              pf[kt][qt][kk][e] = pp[0];
+              pf[kt][qt][kk][e + 1] = pp[1];
+              ls[qt] = __builtin_amdgcn_fdot2(pp, one, ls[qt], false);
+            }
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) l_run[qt] += ls[qt];
+    }
+    // ---- O^T += V^T P^T
+    {
+      constexpr int NV = 4 * DT;
+      half8_t vf[NV];
+      vf[0] = read_v(0, buf);
+      vf[1] = read_v(1, buf);
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        if (i + 2 < NV) vf[i + 2] = read_v(i + 2, buf);
+        __builtin_amdgcn_sched_barrier(0);
+        const int kt = i / (2 * DT), kk = (i / DT) % 2, dt = i % DT;
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt)
+          o[qt][dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[i], pf[kt][qt][kk], o[qt][dt], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  };
+  using T_ = std::integral_constant<bool, true>;
+  using F_ = std::integral_constant<bool, false>;
+  // tiles before bias_block0 hold image keys only (no key bias)
+  int tb = a.bias_block0;
+  tb = tb < 0 ? 0 : (tb > ntiles ? ntiles : tb);
+  int t = 0;
+  for (; t < tb; ++t) step(t, F_{});
+  for (; t < ntiles; ++t) step(t, T_{});
+
+  // ---- normalise and store: o[qt][dt][r] = O[query 32 qt + lq][dim dt*32 + 8(r/4) + 4hi + r%4]
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    const float l_tot = l_run[qt] + __shfl_xor(l_run[qt], 32, 64);
+    const float inv = 1.0f / l_tot;
+    const int q = q0 + qt * 32 + lq;
+    if (q >= a.Lq) continue;
+    float* orow = a.O + a.oOff + (long long)b * a.oBatch + (long long)q * a.ldo + (long long)h * D + 4 * hi;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        float4 v = make_float4(o[qt][dt][4 * g] * inv, o[qt][dt][4 * g + 1] * inv, o[qt][dt][4 * g + 2] * inv,
+                               o[qt][dt][4 * g + 3] * inv);
+        *reinterpret_cast<float4*>(orow + dt * 32 + 8 * g) = v;
+      }
+  }
+}
+
 template <int D, int QT, int NW, int STAGES = 3, int SUPER = 1>
 void launch_flash(FlashArgs fa, hipStream_t s) {
   constexpr int BQ = NW * QT * 32;
@@ -856,6 +1116,26 @@ void launch_flash(FlashArgs fa, hipStream_t s) {
   const int blocks = fa.qblocks * fa.pairs;
   fa.xcd_order = (fa.pairs % 8 == 0) ? 1 : 0;
   flash_kernel<D, QT, NW, STAGES, SUPER><<<blocks, NW * 64, 0, s>>>(fa);
+}
+
+// The wide kernel where its grid of 512-query blocks covers every CU of the chip (D = 96: its
+// queries, K and V stages need 148 KB of LDS and its accumulators 250 VGPRs); the 256-query
+// kernel otherwise (the batch-1 DiT calls: 8 x 16 wide blocks would leave half the CUs idle).
+// The wide kernel reads Q from the fp32 view (qraw), which masks rows past Lq; the packed Qp is
+// padded to 256 rows only.
+constexpr int kWideQueries = 512;
+constexpr int kChipCUs = 256;
+
+template <int D>
+void launch_flash_auto(FlashArgs fa, hipStream_t s) {
+  const int wide_blocks = (fa.Lq + kWideQueries - 1) / kWideQueries * fa.pairs;
+  if (D == 96 && fa.qraw && wide_blocks >= kChipCUs) {
+    fa.qblocks = (fa.Lq + kWideQueries - 1) / kWideQueries;
+    fa.xcd_order = (fa.pairs % 8 == 0) ? 1 : 0;
+    flash_wide_kernel<96><<<wide_blocks, 512, 0, s>>>(fa);
+  } else {
+    launch_flash<D, 1, 8>(fa, s);
+  }
 }
 
 template <int D>
@@ -874,7 +1154,7 @@ int run_attention(PackArgs pa, FlashArgs fa, int batch, bool vec, bool profile) 
   if (!profile) {
     launch_pack<D>(pa, batch, vec, s);
     NS2_LAUNCHED("attn_pack");
-    launch_flash<D, 1, 8>(fa, s);
+    launch_flash_auto<D>(fa, s);
     NS2_LAUNCHED("attn_flash");
     return NS2_OK;
   }
@@ -884,9 +1164,7 @@ int run_attention(PackArgs pa, FlashArgs fa, int batch, bool vec, bool profile) 
     NS2_LAUNCHED("attn_pack");
   }
   ns2::ProfScope prof_("attn_flash");
-  // 32 queries per wave, 8 waves (256 queries) per workgroup: two waves per SIMD, all
-  // accumulators in architectural VGPRs
-  launch_flash<D, 1, 8>(fa, s);
+  launch_flash_auto<D>(fa, s);
   NS2_LAUNCHED("attn_flash");
   return NS2_OK;
 }

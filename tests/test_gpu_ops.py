@@ -478,6 +478,49 @@ def test_attention_batch2_config2(ns2lib):
         assert_close(got[b], ref, TOL, f"config2 batch {b} all heads")
 
 
+def test_attention_wide_blocks(ns2lib):
+    """Batch 8 x 16 heads at a ragged size (21x29 latent = 609 queries, 77 text keys, 686 keys in
+    11 tiles, the last one part padding), with the fused q/k head norms, RoPE and key bias: 2 query
+    blocks of 512 x 128 (batch, head) pairs fill the chip, so the call runs the 512-query-block
+    kernel. Checked against the oracle per batch element, and against the same attention run one
+    batch element per call (16 pairs: the 256-query-block kernel), which must agree to fp32
+    rounding (the kernels differ only in the order of the row sums)."""
+    hh, ww, T, B, Dm = 21, 29, 77, 8, 1536
+    L = hh * ww
+    Lk = L + T
+    g = gen(97)
+    q = torch.randn(B, L, Dm, generator=g)
+    k = torch.randn(B, Lk, Dm, generator=g)
+    v = torch.randn(B, Lk, Dm, generator=g)
+    lb = torch.log(torch.rand(B, T, generator=g) + 0.5)
+    qn = torch.randn(96, generator=g) * 0.5 + 1
+    kn = torch.randn(96, generator=g) * 0.5 + 1
+    cs, sin_off = O.rope2d_table(hh, ww)
+    qd, kd, vd, lbd = q.to(dev), k.to(dev), v.to(dev), lb.to(dev)
+    qnd, knd, csd = qn.to(dev), kn.to(dev), cs.to(dev)
+    common = dict(Lq=L, Lk=Lk, H=16, D=96, ldq=Dm, ldk=Dm, ldv=Dm, ldo=Dm, biasStart=L, q_norm=qnd,
+                  k_norm=knd, rope_cs=csd, sin_off=sin_off, rope_rows=L)
+    wide = torch.empty(B, L, Dm, device=dev)
+    ns2lib.attention(qd, kd, vd, wide, batch=B, qBatch=L * Dm, kBatch=Lk * Dm, vBatch=Lk * Dm, oBatch=L * Dm,
+                     key_bias=lbd, biasBatch=T, **common)
+    narrow = torch.empty(B, L, Dm, device=dev)
+    for b in range(B):
+        ns2lib.attention(qd[b], kd[b], vd[b], narrow[b], key_bias=lbd[b], **common)
+    torch.cuda.synchronize()
+    wide, narrow = wide.cpu(), narrow.cpu()
+    assert_close(wide, narrow, 1e-5, "512-query blocks vs 256-query blocks")
+    bias = torch.zeros(Lk, dtype=torch.float64)
+    for b in range(B):
+        qb = q[b].double().clone()
+        kb = k[b].double().clone()
+        O.head_norm_rope(qb, qn.double(), L, 16, 96, Dm, cs=cs, sinOff=sin_off)
+        O.head_norm_rope(kb, kn.double(), L, 16, 96, Dm, cs=cs, sinOff=sin_off)
+        O.head_norm_rope(kb, kn.double(), T, 16, 96, Dm, rowOff=L)
+        bias[L:] = lb[b].double()
+        ref = O.attention_heads(qb, kb, v[b].double(), 16, 96, bias)
+        assert_close(wide[b], ref, TOL, f"wide blocks, batch element {b}")
+
+
 @pytest.mark.parametrize("pad", [0, 1])
 def test_attention_text_view(ns2lib, pad):
     """ns2_attention_text: the DiT's joint attention with the text keys and values in a second
