@@ -65,7 +65,7 @@ CFG1_SHAPES = (("qkv", 4608, 1536), ("proj", 1536, 1536), ("up", 6144, 1536), ("
 GEMM_TRAFFIC_BYTES_PER_LAUNCH = 130.1e6
 GEMM_ALGORITHMIC_BYTES_PER_LAUNCH = 74.9e6   # N*K int8 W + 2*M*K fp16 A + output (+ old output for +=)
 GEMM_TRAFFIC_SOURCE = "profiles/dit_pass_832x1216_int8.md"
-ATTN_TRAFFIC_BYTES_PER_LAUNCH = 174.0e6
+ATTN_TRAFFIC_BYTES_PER_LAUNCH = 170.2e6
 ATTN_ALGORITHMIC_BYTES_PER_LAUNCH = 149.1e6  # fp32 Q (read in the kernel's prologue), fp16 K, V^T, fp32 O
 ATTN_TRAFFIC_SOURCE = "profiles/attn_flash_joint_3952x4208_b2.md"
 
