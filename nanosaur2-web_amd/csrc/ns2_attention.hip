@@ -1260,12 +1260,23 @@ __global__ __launch_bounds__(1024) void attn_rows_kernel(RowsArgs a) {
 // online-softmax rescale a per-lane scalar, gives every lane DB consecutive d of a V row
 // (vector loads) and makes its outputs one run of 4 DB consecutive d. Scores are in the log2
 // domain (Q pre-scaled by log2(e)/sqrt(D)); fp16 operands, fp32 accumulation.
+// At D = 256 a key row is 1 KB, one direct global->LDS copy: each wave copies its key block's
+// 16 K rows into its own LDS rows (padded by 16 bytes, so the fragment reads of 16 rows hit 16
+// different bank groups) and reads its K fragments from there. Every copy instruction moves
+// 1 KB of consecutive bytes; the fragment loads straight from memory touched 16 rows per
+// instruction and took 16.8 us against 13.2 us for the Gemma3 layer at 256 tokens.
 constexpr int kRowsWaves = 8;  // waves per block of attn_rows_mfma_kernel (LDS: 8 * D * 64 B)
 
 template <int DB, int NW>
 __global__ __launch_bounds__(64 * NW) void attn_rows_mfma_kernel(RowsArgs a) {
   constexpr int D = 16 * DB;
-  __shared__ float4 o_part[NW][DB][64];
+  constexpr bool KDMA = D == 256;
+  constexpr int RS = D * 4 + 16;                       // padded K row in LDS (bytes)
+  constexpr int KST = KDMA ? 16 * RS : 0;              // K rows of one wave
+  constexpr int OPB = NW * DB * 64 * 16;               // the partial outputs
+  constexpr int SM = NW * KST > OPB ? NW * KST : OPB;  // K rows in the loop, then o_part
+  __shared__ __attribute__((aligned(16))) char smem[SM];
+  float4(*o_part)[DB][64] = reinterpret_cast<float4(*)[DB][64]>(smem);
   __shared__ float m_part[NW][16], l_part[NW][16];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int h = blockIdx.y;
@@ -1308,10 +1319,20 @@ __global__ __launch_bounds__(64 * NW) void attn_rows_mfma_kernel(RowsArgs a) {
     // for the PV product's A operand: all loads of the block issued before any use
     const int kr = kb * 16 + col;
     const int key0 = kb * 16 + 4 * grp;
-    const float* krow = kb0 + (long long)(kr < a.Lk ? kr : a.Lk - 1) * a.ldk + 4 * grp;
     float4 kx[DB];
+    if constexpr (KDMA) {
+      const uint32_t kst = lds_addr(smem) + wave * KST;
 #pragma unroll
-    for (int t = 0; t < DB; ++t) kx[t] = *reinterpret_cast<const float4*>(krow + 16 * t);
+      for (int r = 0; r < 16; ++r) {
+        const int key = kb * 16 + r;
+        dma16(kb0 + (long long)(key < a.Lk ? key : a.Lk - 1) * a.ldk + 4 * lane,
+              __builtin_amdgcn_readfirstlane(kst + r * RS));
+      }
+    } else {
+      const float* krow = kb0 + (long long)(kr < a.Lk ? kr : a.Lk - 1) * a.ldk + 4 * grp;
+#pragma unroll
+      for (int t = 0; t < DB; ++t) kx[t] = *reinterpret_cast<const float4*>(krow + 16 * t);
+    }
     // V^T's A operand in product t: row col = d DB col + t, keys key0 + j
     float vx[DB][4];
 #pragma unroll
@@ -1334,6 +1355,14 @@ __global__ __launch_bounds__(64 * NW) void attn_rows_mfma_kernel(RowsArgs a) {
     // keep every load of the block in flight before the first use (left alone, the scheduler
     // converts each group of V values as it arrives and waits on each group in turn)
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (KDMA) {
+      // this wave's K rows have landed (it alone reads them): the fragments from LDS
+      vm_wait<0>();
+      asm volatile("" ::: "memory");
+      const char* kst_p = smem + wave * KST;
+#pragma unroll
+      for (int t = 0; t < DB; ++t) kx[t] = *reinterpret_cast<const float4*>(kst_p + col * RS + (16 * t + 4 * grp) * 4);
+    }
     float4_t s = float4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int t = 0; t < DB; ++t) {
@@ -1370,6 +1399,7 @@ __global__ __launch_bounds__(64 * NW) void attn_rows_mfma_kernel(RowsArgs a) {
   }
   lsum += __shfl_xor(lsum, 16);
   lsum += __shfl_xor(lsum, 32);
+  if constexpr (KDMA) __syncthreads();  // every wave is done with its K rows (o_part overlays them)
 
   // merge the waves' states: O = sum_w 2^(m_w - M) O_w, L = sum_w 2^(m_w - M) l_w
 #pragma unroll

@@ -891,6 +891,8 @@ def test_fill_and_errors(ns2lib):
 @pytest.mark.parametrize("D,H,group,causal,Lq,Lk", [
     (256, 4, 4, True, 37, 37),    # the Gemma3 text encoder: 4 query heads over 1 K/V head
     (256, 4, 4, True, 256, 256),  # its longest prompt
+    (256, 2, 1, False, 5, 300),   # K rows staged in LDS: a ragged last key block, 19 blocks
+    (256, 4, 2, True, 100, 37),   # more queries than keys under the causal mask
     (64, 8, 1, False, 50, 70),
     (96, 6, 2, True, 33, 33),
     (40, 3, 3, False, 9, 130),    # head dim not a multiple of 32
