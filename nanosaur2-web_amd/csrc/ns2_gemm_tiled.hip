@@ -202,10 +202,9 @@ void gemm_tiled_kernel(TGemmArgs p) {
   constexpr int TM = WTM / 32, TN = WTN / 32;
   constexpr int A_BLOCKS = BM / 64 * 8, W_BLOCKS = BN / 64 * 4;  // 1 KB blocks per stage
   constexpr int BLOCKS = A_BLOCKS + W_BLOCKS;
-  constexpr int PER_WAVE = (BLOCKS + NW - 1) / NW;  // the last copies go to the first waves
+  constexpr int PER_WAVE = BLOCKS / NW;
   static_assert(BM % 64 == 0 && BN % 64 == 0 && WTM % 32 == 0 && WTN % 32 == 0, "tile shape");
-  // three stages wait for all but one tile's copies by count: every wave must issue as many
-  static_assert(BLOCKS % NW == 0 || STAGES == 2, "uneven copies need two stages");
+  static_assert(BLOCKS % NW == 0, "copies must split evenly over the waves");
 
   static_assert(STAGES == 2 || STAGES == 3, "two or three LDS stages");
   __shared__ __attribute__((aligned(16))) half_t as[STAGES][BM * 64];
@@ -258,8 +257,7 @@ void gemm_tiled_kernel(TGemmArgs p) {
   auto dma = [&](int kt, int st) {
 #pragma unroll
     for (int i = 0; i < PER_WAVE; ++i)
-      if (BLOCKS % NW == 0 || wave + i * NW < BLOCKS)
-        dma16(g_src[i] + (long long)kt * g_step[i] + lane * 16, __builtin_amdgcn_readfirstlane(l_dst[i] + st * l_step[i]));
+      dma16(g_src[i] + (long long)kt * g_step[i] + lane * 16, __builtin_amdgcn_readfirstlane(l_dst[i] + st * l_step[i]));
   };
 
   float16_t acc[TM][TN];
@@ -568,16 +566,10 @@ constexpr TileCfg kCfgs[] = {
     {64, 64, 350.f, 347.f},      // 4 waves (2 x 2) of 32x32, 24 KB: few rows (text tokens)
 };
 constexpr int kCUs = 256;
-// 128x192 tiles, 12 waves (2 x 6) of 64x32, 56 KB: at N % 192 == 0 and 1024 rows or more they
-// beat every configuration above (3952 rows: qkv 66.5 against 71.9 us for 64x128, proj 29.7
-// against 31.2, w3 58.6 against 62.8, the same outputs bit for bit), with three waves of a
-// block on every SIMD; chosen ahead of the estimate below.
-constexpr int kCfgWide = 3;
 
 // Estimated time: the tiles the busiest CU runs times the tile area over the full-CU rate, but
 // never less than one tile running alone. The configuration with the least estimate is used.
 int pick_config(int M, int N) {
-  if (M >= 1024 && N % 192 == 0) return kCfgWide;
   int best = -1;
   double best_t = 0;
   for (int i = 0; i < (int)(sizeof(kCfgs) / sizeof(kCfgs[0])); ++i) {
@@ -686,7 +678,7 @@ int ns2_linear_i8_tiled_lora(const uint16_t* At, const int8_t* Wt, const float* 
   // Few rows (the 256 text tokens): when the tiles leave CUs idle, split K over blockIdx.y (at
   // least 4 k-tiles per split, at most 8 splits) and reduce in a second launch.
   int splits = 1;
-  if (cfg == 1 || cfg == 2) {
+  if (cfg != 0) {
     const int bm = 64, bn = cfg == 1 ? 128 : 64;
     const long long tiles = (long long)((M + bm - 1) / bm) * ((N + bn - 1) / bn);
     const int kt = K / 64;
@@ -704,7 +696,6 @@ int ns2_linear_i8_tiled_lora(const uint16_t* At, const int8_t* Wt, const float* 
   }
   switch (cfg) {
     case 0: return launch_tiled<256, 256, 4, 4>(p);
-    case kCfgWide: return launch_tiled<128, 192, 2, 6>(p);
     case 1: return launch_tiled<64, 128, 1, 4>(p, splits);
     default: return launch_tiled<64, 64, 2, 2>(p, splits);
   }

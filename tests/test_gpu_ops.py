@@ -244,7 +244,7 @@ def _tiled_linear_inputs(M, N, K, seed):
     (256, 3072, 1536),    # kv_y on the text rows
     (256, 27648, 1536),   # the 9 joint blocks' kv_y stacked: one launch per pass
     (2432, 6144, 1536),
-    (1100, 576, 768),     # 128x192 tiles (N % 192 == 0, >= 1024 rows) with a ragged last row tile
+    (1100, 576, 768),     # a ragged last row tile at more than 1024 rows
     (97, 320, 512),       # ragged rows, N not a multiple of 128
     (1, 64, 256),
 ])
