@@ -243,6 +243,38 @@ int ns2_attention_text(const float* q, const float* k, const float* v, float* o,
                        const float* k_norm, float eps, const float* rope_cs, long long sin_off, int rope_rows,
                        const float* k_text, const float* v_text, int ld_text, int text_start);
 
+/* The q|k|v projection and the attention of one DiT block with the values handed over in the
+ * attention's own fp16 layout instead of as fp32 rows (app/models/nanosaur2.js:193-208, the
+ * `qkv` linear followed by ops.attention; app/gpu/ops.js:46-66 and :199-242). The two calls
+ * give the same results as ns2_linear_i8_tiled + ns2_attention_text: the values are rounded
+ * to fp16 once, in the GEMM epilogue instead of in the attention's operand pack.
+ *
+ * ns2_attention_vpack_bytes: size of the packed-value buffer vpk for Lk keys of H heads of D
+ * (H * ceil(Lk/64)*64 * D halfs).
+ *
+ * ns2_linear_i8_tiled_vpack: ns2_linear_i8_tiled_lora (resid 0) whose output columns
+ * [vcol0, vcol0 + H*D) -- the last H*D columns, vcol0 % 64 == 0, D % 32 == 0 -- are written to
+ * vpk as the values of keys [0, M) of an attention over Lk >= M keys, instead of into C;
+ * M % 16 == 0. Columns below vcol0 go to C as usual (their part of C is all that is written).
+ *
+ * ns2_attention_vpacked: ns2_attention_text (k_text/v_text may be null for a single view)
+ * whose values of keys [0, v_rows) are taken from vpk as ns2_linear_i8_tiled_vpack wrote them;
+ * the values of keys from v_rows on (text and padding keys) are packed into vpk from v / v_text
+ * as usual. v_rows % 16 == 0, v_rows <= Lk; every view 16-byte aligned. */
+size_t ns2_attention_vpack_bytes(int Lk, int H, int D);
+int ns2_linear_i8_tiled_vpack(const uint16_t* At, const int8_t* Wt, const float* scale,
+                              const float* bias, float* C, int M, int N, int K, int ldc,
+                              long long cOff, float alpha, int act, const uint16_t* lora_a,
+                              const uint16_t* lora_b, int lora_r, uint16_t* vpk, int vcol0, int H,
+                              int D, int Lk);
+int ns2_attention_vpacked(const float* q, const float* k, const float* v, float* o, int Lq, int Lk,
+                          int H, int D, int ldq, int ldk, int ldv, int ldo, long long qOff,
+                          long long kOff, long long vOff, long long oOff, float scale,
+                          const float* key_bias, int biasStart, const float* q_norm,
+                          const float* k_norm, float eps, const float* rope_cs, long long sin_off,
+                          int rope_rows, const float* k_text, const float* v_text, int ld_text,
+                          int text_start, uint16_t* vpk, int v_rows);
+
 /* Bytes of the fixed device scratch array behind ns2_attention_noalloc (one per GPU, held
  * until the process ends). */
 #define NS2_NOALLOC_SCRATCH_BYTES (64u << 20)

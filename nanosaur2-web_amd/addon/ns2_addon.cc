@@ -504,6 +504,71 @@ napi_value Attention(napi_env env, napi_callback_info info) {
                                      qB, kB, vB, oB, scale, kb, biasStart, biasBatch, qn, kn, eps, cs, sinOff, ropeRows));
 }
 
+// linearI8TiledVpack(At, Wt, scale, bias, C, M, N, K, ldc, cOff, alpha, act, loraA, loraB, loraR, vpk, vcol0,
+//                    H, D, Lk)
+napi_value LinearI8TiledVpack(napi_env env, napi_callback_info info) {
+  ARGS(20);
+  auto At = (const uint16_t*)c.ptr(0);
+  auto Wt = (const int8_t*)c.ptr(1);
+  auto scale = (const float*)c.ptr(2);
+  auto bias = (const float*)c.ptr(3);
+  auto C = (float*)c.ptr(4);
+  int M = c.i32(5), N = c.i32(6), K = c.i32(7), ldc = c.i32(8);
+  long long cOff = c.i64(9);
+  float alpha = c.f32(10);
+  int act = c.i32(11);
+  auto la = (const uint16_t*)c.ptr(12);
+  auto lb = (const uint16_t*)c.ptr(13);
+  int lr = c.type(14) == napi_number ? c.i32(14) : 0;
+  auto vpk = (uint16_t*)c.ptr(15);
+  int vcol0 = c.i32(16), H = c.i32(17), D = c.i32(18), Lk = c.i32(19);
+  if (c.failed) return nullptr;
+  return check(env, c, ns2_linear_i8_tiled_vpack(At, Wt, scale, bias, C, M, N, K, ldc, cOff, alpha, act, la, lb, lr,
+                                                 vpk, vcol0, H, D, Lk));
+}
+
+// attentionVpackBytes(Lk, H, D) -> bytes of a packed-value buffer
+napi_value AttentionVpackBytes(napi_env env, napi_callback_info info) {
+  ARGS(3);
+  int Lk = c.i32(0), H = c.i32(1), D = c.i32(2);
+  if (c.failed) return nullptr;
+  napi_value r;
+  napi_create_double(env, (double)ns2_attention_vpack_bytes(Lk, H, D), &r);
+  return r;
+}
+
+// attentionVpacked(q, k, v, o, Lq, Lk, H, D, ldq, ldk, ldv, ldo, qOff, kOff, vOff, oOff, scale, keyBias,
+//                  biasStart, qNorm, kNorm, eps, ropeCs, sinOff, ropeRows, kText, vText, ldText, textStart,
+//                  vpk, vRows)
+napi_value AttentionVpacked(napi_env env, napi_callback_info info) {
+  ARGS(31);
+  auto q = (const float*)c.ptr(0);
+  auto k = (const float*)c.ptr(1);
+  auto v = (const float*)c.ptr(2);
+  auto o = (float*)c.ptr(3);
+  int Lq = c.i32(4), Lk = c.i32(5), H = c.i32(6), D = c.i32(7);
+  int ldq = c.i32(8), ldk = c.i32(9), ldv = c.i32(10), ldo = c.i32(11);
+  long long qOff = c.i64(12), kOff = c.i64(13), vOff = c.i64(14), oOff = c.i64(15);
+  float scale = c.f32(16);
+  auto kb = (const float*)c.ptr(17);
+  int biasStart = c.i32(18);
+  auto qn = (const float*)c.ptr(19);
+  auto kn = (const float*)c.ptr(20);
+  float eps = c.f32(21);
+  auto cs = (const float*)c.ptr(22);
+  long long sinOff = c.i64(23);
+  int ropeRows = c.i32(24);
+  auto kt = (const float*)c.ptr(25);
+  auto vt = (const float*)c.ptr(26);
+  int ldText = c.i32(27), textStart = c.i32(28);
+  auto vpk = (uint16_t*)c.ptr(29);
+  int vRows = c.i32(30);
+  if (c.failed) return nullptr;
+  return check(env, c, ns2_attention_vpacked(q, k, v, o, Lq, Lk, H, D, ldq, ldk, ldv, ldo, qOff, kOff, vOff, oOff,
+                                             scale, kb, biasStart, qn, kn, eps, cs, sinOff, ropeRows, kt, vt, ldText,
+                                             textStart, vpk, vRows));
+}
+
 // attentionText(q, k, v, o, Lq, Lk, H, D, ldq, ldk, ldv, ldo, qOff, kOff, vOff, oOff, scale, keyBias,
 //               biasStart, qNorm, kNorm, eps, ropeCs, sinOff, ropeRows, kText, vText, ldText, textStart)
 napi_value AttentionText(napi_env env, napi_callback_info info) {
@@ -756,6 +821,8 @@ napi_value Module(napi_env env, napi_value exports) {
       {"tileI8WeightGlu", TileI8WeightGlu}, {"linearI8GluRotTiled", LinearI8GluRotTiled},
       {"linearI8", LinearI8}, {"linearBf16", LinearBf16}, {"attention", Attention},
       {"attentionRows", AttentionRows}, {"attentionText", AttentionText},
+      {"linearI8TiledVpack", LinearI8TiledVpack}, {"attentionVpackBytes", AttentionVpackBytes},
+      {"attentionVpacked", AttentionVpacked},
       {"headNorm", HeadNorm}, {"headNorm2", HeadNorm2}, {"normMod", NormModT<false>}, {"normModRotateF16", NormModT<true>},
       {"glu", GluT<false>}, {"gluRotateF16", GluT<true>}, {"elementwise", Elementwise},
       {"accumulate", Accumulate}, {"addRows", AddRows}, {"rowSum", RowSum}, {"rmsnorm", Rmsnorm},

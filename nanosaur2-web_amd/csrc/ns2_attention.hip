@@ -60,6 +60,9 @@ struct PackArgs {
   const float* k2;
   const float* v2;
   int ld2, kv2_start;
+  // values of keys [0, v_pre) are already in Vc (written by the producing GEMM); v_pre % 16 == 0
+  // (vectorized pack only)
+  int v_pre;
 };
 
 // Row r of head 0 in the K and V views of batch element b.
@@ -266,8 +269,10 @@ __global__ __launch_bounds__(256) void attn_pack_vec_kernel(PackArgs a) {
   // V gathers first: they do not depend on the Q/K work. Keys past Lk read the last key (the
   // loads stay unconditional and issue back to back) and are zeroed afterwards.
   const int kc = tid >> 5, dg = tid & 31;
+  // chunk kc holds keys of the 16-key group row0 + 16 (kc / 2) only
+  const bool vput = kv && row0 + 16 * (kc >> 1) >= a.v_pre;
   float vv[8][DPL];
-  if (kv) {
+  if (vput) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const int key = row0 + vkey_pos(kc * 8 + e);
@@ -320,7 +325,7 @@ __global__ __launch_bounds__(256) void attn_pack_vec_kernel(PackArgs a) {
     }
   }
 
-  if (kv) {
+  if (vput) {
     half_t* vdst = a.Vc + ((long long)bh * tiles + tile) * (KB * D) + ((long long)kc * D + dg * DPL) * 8;
 #pragma unroll
     for (int j = 0; j < DPL; ++j) {
@@ -329,6 +334,8 @@ __global__ __launch_bounds__(256) void attn_pack_vec_kernel(PackArgs a) {
       for (int e = 0; e < 8; ++e) col[e] = vv[e][j];
       *reinterpret_cast<uint4*>(vdst + j * 8) = pack8_f16(col);
     }
+  }
+  if (kv) {
     // per-key bias in log2 units (one head does it)
     if (h == 0 && tid < KB) {
       const int key = row0 + tid;
@@ -1495,7 +1502,8 @@ int attention_call(const char* fn, bool noalloc, const float* q, const float* k,
                    long long vBatch, long long oBatch, float scale, const float* key_bias, int biasStart,
                    long long biasBatch, const float* q_norm, const float* k_norm, float eps,
                    const float* rope_cs, long long sin_off, int rope_rows, const float* k_text = nullptr,
-                   const float* v_text = nullptr, int ld_text = 0, int text_start = 0) {
+                   const float* v_text = nullptr, int ld_text = 0, int text_start = 0, uint16_t* vpk = nullptr,
+                   int v_rows = 0) {
   NS2_READY();
   if (Lq <= 0 || batch <= 0) return NS2_OK;
   NS2_REQUIRE(q && k && v && o, "%s: null q, k, v or o", fn);
@@ -1523,6 +1531,12 @@ int attention_call(const char* fn, bool noalloc, const float* q, const float* k,
                    (!q_norm || aligned16(q_norm)) && (!k_norm || aligned16(k_norm)) &&
                    (!rope_cs || (aligned16(rope_cs) && al4(sin_off))) &&
                    (!k_text || (aligned16(k_text) && aligned16(v_text) && al4(ld_text)));
+  if (vpk) {
+    NS2_REQUIRE(!noalloc && batch == 1 && aligned16(vpk) && v_rows >= 0 && v_rows % 16 == 0 && v_rows <= Lk,
+                "%s: packed values need batch 1, a 16-byte aligned buffer and 0 <= v_rows <= Lk, v_rows %% 16 == 0 "
+                "(v_rows=%d Lk=%d)", fn, v_rows, Lk);
+    NS2_REQUIRE(vec, "%s: packed values need 16-byte aligned views (the vectorized pack)", fn);
+  }
   half_t *Qp, *Kc, *Vc;
   float* B2;
   if (noalloc) {
@@ -1541,7 +1555,7 @@ int attention_call(const char* fn, bool noalloc, const float* q, const float* k,
   } else {
     Qp = static_cast<half_t*>(ns2::workspace(1, qbytes));
     Kc = static_cast<half_t*>(ns2::workspace(2, kbytes));
-    Vc = static_cast<half_t*>(ns2::workspace(3, kbytes));
+    Vc = vpk ? reinterpret_cast<half_t*>(vpk) : static_cast<half_t*>(ns2::workspace(3, kbytes));
     B2 = static_cast<float*>(ns2::workspace(4, bbytes));
     if (!Qp || !Kc || !Vc || !B2) return ns2::set_error(NS2_ERR_OOM, "%s: workspace allocation failed", fn);
   }
@@ -1559,6 +1573,7 @@ int attention_call(const char* fn, bool noalloc, const float* q, const float* k,
   pa.v2 = v_text;
   pa.ld2 = ld_text;
   pa.kv2_start = text_start;
+  pa.v_pre = vpk ? v_rows : 0;
   const bool profile = !noalloc;
   switch (D) {
     case 32: return run_attention<32>(pa, fa, batch, vec, profile);
@@ -1592,6 +1607,25 @@ extern "C" int ns2_attention_text(const float* q, const float* k, const float* v
   return attention_call("ns2_attention_text", false, q, k, v, o, 1, Lq, Lk, H, D, ldq, ldk, ldv, ldo, qOff, kOff,
                         vOff, oOff, 0, 0, 0, 0, scale, key_bias, biasStart, 0, q_norm, k_norm, eps, rope_cs,
                         sin_off, rope_rows, k_text, v_text, ld_text, text_start);
+}
+
+extern "C" int ns2_attention_vpacked(const float* q, const float* k, const float* v, float* o, int Lq, int Lk,
+                                     int H, int D, int ldq, int ldk, int ldv, int ldo, long long qOff,
+                                     long long kOff, long long vOff, long long oOff, float scale,
+                                     const float* key_bias, int biasStart, const float* q_norm,
+                                     const float* k_norm, float eps, const float* rope_cs, long long sin_off,
+                                     int rope_rows, const float* k_text, const float* v_text, int ld_text,
+                                     int text_start, uint16_t* vpk, int v_rows) {
+  NS2_REQUIRE(vpk, "ns2_attention_vpacked: null vpk");
+  NS2_REQUIRE(!k_text == !v_text, "ns2_attention_vpacked: k_text and v_text go together");
+  return attention_call("ns2_attention_vpacked", false, q, k, v, o, 1, Lq, Lk, H, D, ldq, ldk, ldv, ldo, qOff, kOff,
+                        vOff, oOff, 0, 0, 0, 0, scale, key_bias, biasStart, 0, q_norm, k_norm, eps, rope_cs,
+                        sin_off, rope_rows, k_text, v_text, ld_text, text_start, vpk, v_rows);
+}
+
+extern "C" size_t ns2_attention_vpack_bytes(int Lk, int H, int D) {
+  if (Lk <= 0 || H <= 0 || D <= 0) return 0;
+  return (size_t)H * ((Lk + KB - 1) / KB * KB) * D * sizeof(half_t);
 }
 
 extern "C" int ns2_attention_noalloc(const float* q, const float* k, const float* v, float* o, int batch,

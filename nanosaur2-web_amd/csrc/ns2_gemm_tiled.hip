@@ -45,6 +45,12 @@ struct TGemmArgs {
   int ksplit;
   // column bands of the tile order (block_tile): 1 keeps the row-group order
   int bands;
+  // Packed attention values (plain store only): output columns [vcol0, vcol0 + heads * vD) are
+  // written as fp16 into vpk in the flash kernel's value layout, [head][key tile][8 key chunks]
+  // [vD][8] with vtiles 64-key tiles per head (key r = output row r), instead of into C.
+  // vpk = nullptr: off. vcol0 and vD are multiples of 32 and M of 16.
+  half_t* vpk;
+  int vcol0, vD, vtiles;
 };
 
 // 8 biased bytes (two dwords) -> 8 halfs: byte u -> half(0x6400 | u) - 1152 = u - 128 = w.
@@ -169,6 +175,57 @@ __device__ __forceinline__ void store_plain(const TGemmArgs& p, const float16_t 
         if (RM == 1) v = old[r] + v;
         if (RM == 2) v = old[r] + gt * v;
         cj[(long long)dm * p.ldc] = v;
+      }
+    }
+  }
+}
+
+// Plain store of one wave whose 32-column tiles lie in the packed-value window (RM 0): the
+// values of the same epilogue, rounded to fp16 once, into the flash kernel's value layout. The
+// 16 accumulator rows of a lane are keys {4hi..4hi+3, 8+4hi..8+4hi+3} of two 16-key groups,
+// which the layout stores as one 16-byte chunk each (chunk 2g + hi of the group's 32 keys in
+// a 64-key tile holds keys 16g + 4hi + {0..3} then 16g + 8 + 4hi + {0..3}).
+template <int TM, int TN, int ACT, bool LORA>
+__device__ __forceinline__ void store_vpack(const TGemmArgs& p, const float16_t (&acc)[TM][TN], int mb, int nb, int lq) {
+  const int hi = (mb & 4) ? 1 : 0;  // mb = the wave's first row + 4 hi (rows are 32-aligned)
+  const int m0 = mb - 4 * hi;
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int n = nb + 32 * j + lq;
+    const float rs = p.scale[n];
+    const float bi = p.bias ? p.bias[n] : 0.0f;
+    const int c = n - p.vcol0, h = c / p.vD, dd = c % p.vD;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      float16_t d;
+      if constexpr (LORA) {
+        const int m = m0 + 32 * i + lq;
+        d = lora_tile(p.lt, p.lb, p.lr, m < p.M ? m : p.M - 1, n, hi);
+      }
+#pragma unroll
+      for (int g = 0; g < 2; ++g) {
+        const int key16 = m0 + 32 * i + 16 * g;
+        if (key16 >= p.M) continue;
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          float x = acc[i][j][8 * g + e] * p.alpha;
+          x *= rs;
+          x += bi;
+          if constexpr (LORA) x += d[8 * g + e];
+          v[e] = act_t<ACT>(x);
+          // the fp32 value first, as the plain store writes it: the conversion must not fuse
+          // with the multiply-add into one rounding to fp16 (v_fma_mix)
+          asm volatile("" : "+v"(v[e]));
+        }
+        const int kt = key16 >> 6, kc = 2 * ((key16 & 63) >> 4) + hi;
+        half_t* dst = p.vpk + ((long long)h * p.vtiles + kt) * 64 * p.vD + ((long long)kc * p.vD + dd) * 8;
+        uint4 q;
+        q.x = pack_half2(v[0], v[1]);
+        q.y = pack_half2(v[2], v[3]);
+        q.z = pack_half2(v[4], v[5]);
+        q.w = pack_half2(v[6], v[7]);
+        *reinterpret_cast<uint4*>(dst) = q;
       }
     }
   }
@@ -439,6 +496,10 @@ void gemm_tiled_kernel(TGemmArgs p) {
     }
     return;
   }
+  if (RM == 0 && p.vpk && n0 + wn * WTN >= p.vcol0 && n0 + wn * WTN < p.N) {
+    store_vpack<TM, TN, ACT, LORA>(p, acc, m0 + wm * WTM + 4 * hi, n0 + wn * WTN, lq);
+    return;
+  }
   store_plain<TM, TN, ACT, RM, PRE_C, LORA>(p, acc, cold, m0 + wm * WTM + 4 * hi, n0 + wn * WTN, m0 + BM <= p.M, lq);
 }
 
@@ -591,6 +652,64 @@ inline bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 }  // namespace
 
+namespace {
+
+int linear_i8_tiled(const char* fn, const uint16_t* At, const int8_t* Wt, const float* scale, const float* bias,
+                    float* C, int M, int N, int K, int ldc, long long cOff, float alpha, int act, int resid,
+                    const float* gate, long long gOff, const uint16_t* lora_a, const uint16_t* lora_b, int lora_r,
+                    uint16_t* vpk = nullptr, int vcol0 = 0, int vD = 0, int vtiles = 0) {
+  NS2_READY();
+  if (M == 0) return NS2_OK;
+  NS2_REQUIRE(At && Wt && scale && C, "%s: null At, Wt, scale or C", fn);
+  NS2_REQUIRE(M > 0 && N > 0 && N % 64 == 0 && K > 0 && K % 256 == 0,
+              "%s: M=%d N=%d K=%d (N %% 64 == 0, K %% 256 == 0 required)", fn, M, N, K);
+  NS2_REQUIRE(ldc >= N && cOff >= 0 && gOff >= 0, "%s: bad ldc/offsets", fn);
+  NS2_REQUIRE(aligned16(At) && aligned16(Wt), "%s: operands must be 16-byte aligned", fn);
+  NS2_REQUIRE(act >= NS2_ACT_NONE && act <= NS2_ACT_GELU_TANH, "%s: unknown act %d", fn, act);
+  TGemmArgs p{reinterpret_cast<const half_t*>(At), reinterpret_cast<const uint8_t*>(Wt), scale, bias, C, nullptr, gate,
+              cOff, gOff, M, N, K, ldc, (M + 63) / 64, N / 64, 0, 0, alpha, act, resid};
+  p.vpk = reinterpret_cast<half_t*>(vpk);
+  p.vcol0 = vcol0;
+  p.vD = vD;
+  p.vtiles = vtiles;
+  if (lora_r) {
+    int rc = ns2::lora_prepare(&p.lt, lora_a, lora_b, lora_r, At, 2, K, M, K, fn);
+    if (rc) return rc;
+    p.lb = reinterpret_cast<const half_t*>(lora_b);
+    p.lr = lora_r;
+  }
+  ns2::ProfScope prof_("gemm_i8_tiled");
+  // the 256x256 tiles (16 waves, 128 registers each) have no room for the LoRA term's registers
+  int cfg = pick_config(M, N);
+  if (lora_r && cfg == 0) cfg = 1;
+  // Few rows (the 256 text tokens): when the tiles leave CUs idle, split K over blockIdx.y (at
+  // least 4 k-tiles per split, at most 8 splits) and reduce in a second launch.
+  int splits = 1;
+  if (cfg != 0) {
+    const int bm = 64, bn = cfg == 1 ? 128 : 64;
+    const long long tiles = (long long)((M + bm - 1) / bm) * ((N + bn - 1) / bn);
+    const int kt = K / 64;
+    if (tiles < kCUs && kt >= 8 && !vpk) {
+      splits = (int)((2 * kCUs + tiles - 1) / tiles);
+      if (splits > kt / 4) splits = kt / 4;
+      if (splits > 8) splits = 8;
+    }
+    if (splits > 1) {
+      p.ksplit = (kt + splits - 1) / splits;
+      splits = (kt + p.ksplit - 1) / p.ksplit;
+      p.part = static_cast<float*>(ns2::workspace(5, (size_t)splits * M * N * sizeof(float)));
+      if (!p.part) return ns2::set_error(NS2_ERR_OOM, "%s: split-K workspace allocation failed", fn);
+    }
+  }
+  switch (cfg) {
+    case 0: return launch_tiled<256, 256, 4, 4>(p);
+    case 1: return launch_tiled<64, 128, 1, 4>(p, splits);
+    default: return launch_tiled<64, 64, 2, 2>(p, splits);
+  }
+}
+
+}  // namespace
+
 extern "C" {
 
 int ns2_tile_i8_weight(const int8_t* W, int8_t* Wt, int N, int K) {
@@ -647,58 +766,32 @@ int ns2_linear_i8_glu_rot_tiled_lora(const uint16_t* At, const int8_t* Wt, const
 int ns2_linear_i8_tiled(const uint16_t* At, const int8_t* Wt, const float* scale, const float* bias,
                         float* C, int M, int N, int K, int ldc, long long cOff, float alpha, int act,
                         int resid, const float* gate, long long gOff) {
-  return ns2_linear_i8_tiled_lora(At, Wt, scale, bias, C, M, N, K, ldc, cOff, alpha, act, resid, gate, gOff,
-                                  nullptr, nullptr, 0);
+  return linear_i8_tiled("ns2_linear_i8_tiled", At, Wt, scale, bias, C, M, N, K, ldc, cOff, alpha, act, resid, gate,
+                         gOff, nullptr, nullptr, 0);
 }
 
 int ns2_linear_i8_tiled_lora(const uint16_t* At, const int8_t* Wt, const float* scale, const float* bias,
                              float* C, int M, int N, int K, int ldc, long long cOff, float alpha, int act,
                              int resid, const float* gate, long long gOff, const uint16_t* lora_a,
                              const uint16_t* lora_b, int lora_r) {
+  return linear_i8_tiled("ns2_linear_i8_tiled_lora", At, Wt, scale, bias, C, M, N, K, ldc, cOff, alpha, act, resid,
+                         gate, gOff, lora_a, lora_b, lora_r);
+}
+
+int ns2_linear_i8_tiled_vpack(const uint16_t* At, const int8_t* Wt, const float* scale, const float* bias,
+                              float* C, int M, int N, int K, int ldc, long long cOff, float alpha, int act,
+                              const uint16_t* lora_a, const uint16_t* lora_b, int lora_r, uint16_t* vpk,
+                              int vcol0, int H, int D, int Lk) {
   NS2_READY();
   if (M == 0) return NS2_OK;
-  NS2_REQUIRE(At && Wt && scale && C, "ns2_linear_i8_tiled: null At, Wt, scale or C");
-  NS2_REQUIRE(M > 0 && N > 0 && N % 64 == 0 && K > 0 && K % 256 == 0,
-              "ns2_linear_i8_tiled: M=%d N=%d K=%d (N %% 64 == 0, K %% 256 == 0 required)", M, N, K);
-  NS2_REQUIRE(ldc >= N && cOff >= 0 && gOff >= 0, "ns2_linear_i8_tiled: bad ldc/offsets");
-  NS2_REQUIRE(aligned16(At) && aligned16(Wt), "ns2_linear_i8_tiled: operands must be 16-byte aligned");
-  NS2_REQUIRE(act >= NS2_ACT_NONE && act <= NS2_ACT_GELU_TANH, "ns2_linear_i8_tiled: unknown act %d", act);
-  TGemmArgs p{reinterpret_cast<const half_t*>(At), reinterpret_cast<const uint8_t*>(Wt), scale, bias, C, nullptr, gate,
-              cOff, gOff, M, N, K, ldc, (M + 63) / 64, N / 64, 0, 0, alpha, act, resid};
-  if (lora_r) {
-    int rc = ns2::lora_prepare(&p.lt, lora_a, lora_b, lora_r, At, 2, K, M, K, "ns2_linear_i8_tiled_lora");
-    if (rc) return rc;
-    p.lb = reinterpret_cast<const half_t*>(lora_b);
-    p.lr = lora_r;
-  }
-  ns2::ProfScope prof_("gemm_i8_tiled");
-  // the 256x256 tiles (16 waves, 128 registers each) have no room for the LoRA term's registers
-  int cfg = pick_config(M, N);
-  if (lora_r && cfg == 0) cfg = 1;
-  // Few rows (the 256 text tokens): when the tiles leave CUs idle, split K over blockIdx.y (at
-  // least 4 k-tiles per split, at most 8 splits) and reduce in a second launch.
-  int splits = 1;
-  if (cfg != 0) {
-    const int bm = 64, bn = cfg == 1 ? 128 : 64;
-    const long long tiles = (long long)((M + bm - 1) / bm) * ((N + bn - 1) / bn);
-    const int kt = K / 64;
-    if (tiles < kCUs && kt >= 8) {
-      splits = (int)((2 * kCUs + tiles - 1) / tiles);
-      if (splits > kt / 4) splits = kt / 4;
-      if (splits > 8) splits = 8;
-    }
-    if (splits > 1) {
-      p.ksplit = (kt + splits - 1) / splits;
-      splits = (kt + p.ksplit - 1) / p.ksplit;
-      p.part = static_cast<float*>(ns2::workspace(5, (size_t)splits * M * N * sizeof(float)));
-      if (!p.part) return ns2::set_error(NS2_ERR_OOM, "ns2_linear_i8_tiled: split-K workspace allocation failed");
-    }
-  }
-  switch (cfg) {
-    case 0: return launch_tiled<256, 256, 4, 4>(p);
-    case 1: return launch_tiled<64, 128, 1, 4>(p, splits);
-    default: return launch_tiled<64, 64, 2, 2>(p, splits);
-  }
+  NS2_REQUIRE(vpk && ((uintptr_t)vpk & 15) == 0, "ns2_linear_i8_tiled_vpack: null or unaligned vpk");
+  NS2_REQUIRE(H > 0 && D > 0 && D % 32 == 0 && vcol0 >= 0 && vcol0 % 64 == 0 && vcol0 + (long long)H * D == N,
+              "ns2_linear_i8_tiled_vpack: the value columns [vcol0, vcol0 + H*D) must end the output "
+              "(vcol0=%d H=%d D=%d N=%d; vcol0 %% 64 == 0, D %% 32 == 0)", vcol0, H, D, N);
+  NS2_REQUIRE(M % 16 == 0 && M <= Lk, "ns2_linear_i8_tiled_vpack: M=%d must be a multiple of 16 and at most Lk=%d",
+              M, Lk);
+  return linear_i8_tiled("ns2_linear_i8_tiled_vpack", At, Wt, scale, bias, C, M, N, K, ldc, cOff, alpha, act, 0,
+                         nullptr, 0, lora_a, lora_b, lora_r, vpk, vcol0, D, (Lk + 63) / 64);
 }
 
 }  // extern "C"

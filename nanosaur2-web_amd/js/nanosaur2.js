@@ -218,13 +218,14 @@ export class Nanosaur2DiT {
   // Attention over a packed qkv [Lk, 3D] buffer; fused: per-head norms (and RoPE on the
   // first ropeRows rows) inside the attention call, else the reference's headNorm ops.
   // textKV: the text keys and values outside qkv ({ t, off, ld }, from the stacked kv_y product)
-  attend(qkv, L, Lk, b, { cs = null, textRows = 0, bias = null, textKV = null } = {}) {
+  // vpack: the values of the L image keys, already packed by qkvProj
+  attend(qkv, L, Lk, b, { cs = null, textRows = 0, bias = null, textKV = null, vpack = null } = {}) {
     const gpu = this.gpu;
     const common = { q: qkv, k: qkv, v: qkv, Lq: L, Lk, H: HEADS, D: HD, ldq: 3 * D, ldk: 3 * D, ldv: 3 * D,
       qOff: 0, kOff: D, vOff: 2 * D, bias, biasStart: L };
     if (this.fused) {
       return ops.attention(gpu, { ...common, qNorm: b.qn, kNorm: b.kn, cs, ropeRows: L,
-        textKV: textKV ? { ...textKV, start: L } : null });
+        textKV: textKV ? { ...textKV, start: L } : null, vPacked: vpack ? { buf: vpack, rows: L } : null });
     }
     ops.headNorm(gpu, qkv, b.qn, { L, H: HEADS, D: HD, ld: 3 * D, colOff: 0, cs });
     ops.headNorm(gpu, qkv, b.kn, { L, H: HEADS, D: HD, ld: 3 * D, colOff: D, cs });
@@ -274,12 +275,13 @@ export class Nanosaur2DiT {
     ops.linear(gpu, a, W, { out: x, resid: true, gate: mod, gOff: 2 * D, name });
   }
 
-  // qkv projection of modulate(norm1(x)) into rows [0, L) of qkv
-  qkvProj(x, mod, b, qkv, name) {
+  // qkv projection of modulate(norm1(x)) into rows [0, L) of qkv; vpack: the values go into
+  // this packedValues() tensor instead of qkv's v columns (tiled weights only)
+  qkvProj(x, mod, b, qkv, name, vpack = null) {
     const gpu = this.gpu;
     if (this.fused) {
       const nr = ops.normModRotated(gpu, x, mod, 0, D, D, b.n1, 1e-6, !!b.qkv.tbuf);
-      ops.linear(gpu, null, b.qkv, { xr: nr, out: qkv, name });
+      ops.linear(gpu, null, b.qkv, { xr: nr, out: qkv, name, vpack: vpack ? { buf: vpack, col0: 2 * D } : null });
       nr.release();
       return;
     }
@@ -373,13 +375,18 @@ export class Nanosaur2DiT {
     // text k|v come from the stacked kv_y product
     const Lk = L + (cross ? text.L : 0);
     const qkv = gpu.empty([stacked ? L : Lk, 3 * D]);
-    this.qkvProj(x, mod, b, qkv, "dit.qkv");
+    // fused path: the qkv GEMM writes the image values straight into the attention's fp16 layout
+    // (the same rounding the attention's operand pack applies), 16-key groups at a time
+    const vpack = this.fused && b.qkv.tbuf && L % 16 === 0 ? ops.packedValues(gpu, Lk, HEADS, HD) : null;
+    this.qkvProj(x, mod, b, qkv, "dit.qkv", vpack);
     if (cross && !stacked) {
       ops.linear(gpu, c.txt, b.kvY, { xr: c.txtR, out: qkv, ldc: 3 * D, cOff: L * 3 * D + D, name: "dit.kv_y" });
     }
     const textKV = cross && stacked ? { t: c.kvText, off: b.kvSlot, ld: this.kvAll.N } : null;
-    const a = this.attend(qkv, L, Lk, b, { cs, textRows: cross ? text.L : 0, bias: cross ? text.bias : null, textKV });
+    const a = this.attend(qkv, L, Lk, b, { cs, textRows: cross ? text.L : 0, bias: cross ? text.bias : null, textKV,
+      vpack });
     qkv.release();
+    if (vpack) vpack.release();
     this.projAdd(x, a, b.proj, mod, "dit.proj");
     a.release();
     this.mlp(x, b, mod);

@@ -90,9 +90,20 @@ export function linearGluRotated(gpu, xr, W, act, name = "gemm.i8.glu") {
   return y;
 }
 
+// The attention's packed fp16 values for Lk keys of H heads of D (filled by linear() with
+// opts.vpack, read by attention() with opts.vPacked).
+export function packedValues(gpu, Lk, H, D) {
+  const halfs = native.attentionVpackBytes(Lk, H, D) / 2;
+  const t = gpu.empty([halfs], "f16");
+  t.vpack = { Lk, H, D };
+  return t;
+}
+
 // y = x @ W^T (+ bias) (act) (app/gpu/ops.js:46-66). opts: out, resid, gate, gOff, ldc, cOff,
 // bias, act, xr (pre-rotated input of an int8 weight: fp32 from rotate() or fp16 from a fused
-// producer), name. x may be null when xr is given.
+// producer), name. x may be null when xr is given. opts.vpack = { buf, col0 } (tiled int8 only,
+// no resid): the output columns from col0 on (the last H*D) are written into buf, a
+// packedValues() tensor, as the values of keys [0, M), instead of into out.
 export function linear(gpu, x, W, opts = {}) {
   const src = opts.xr || x;
   const M = src.tiled ? src.rows : src.size / W.K;
@@ -108,7 +119,15 @@ export function linear(gpu, x, W, opts = {}) {
   if (act === undefined) throw new Error(`linear: unknown activation ${opts.act}`);
   const resid = opts.resid ? 1 : 0;
   const flops = 2 * M * W.N * W.K;
-  if (W.kind === "i8" && src.tiled) {
+  if (W.kind === "i8" && src.tiled && opts.vpack) {
+    if (!W.tbuf) throw new Error(`${W.name}: a tiled operand needs the tiled weight (tileWeight)`);
+    if (resid) throw new Error("linear: packed values take a plain store (no resid)");
+    const { buf, col0 } = opts.vpack;
+    const { Lk, H, D } = buf.vpack;
+    gpu.run(opts.name || "gemm.i8", flops, () =>
+      native.linearI8TiledVpack(addr(src), addr(W.tbuf), addr(W.scale), addr(bias), addr(out), M, W.N, W.K, ldc,
+        cOff, 1, act, ...lora, addr(buf), col0, H, D, Lk));
+  } else if (W.kind === "i8" && src.tiled) {
     if (!W.tbuf) throw new Error(`${W.name}: a tiled operand needs the tiled weight (tileWeight)`);
     gpu.run(opts.name || "gemm.i8", flops, () =>
       native.linearI8Tiled(addr(src), addr(W.tbuf), addr(W.scale), addr(bias), addr(out), M, W.N, W.K, ldc,
@@ -314,7 +333,7 @@ export function accumulate(gpu, y, a) {
 // ld (the DiT's text keys projected for all joint blocks at once); fused path only.
 export function attention(gpu, { q, k, v, Lq, Lk, H, D, ldq, ldk, ldv, qOff = 0, kOff = 0, vOff = 0, group = 1,
   causal = false, bias = null, biasStart = 0, out, qNorm = null, kNorm = null, cs = null, ropeRows = 0, eps = 1e-6,
-  textKV = null }) {
+  textKV = null, vPacked = null }) {
   const o = out || gpu.empty([Lq, H * D]);
   // the fused kernel's conditions (app/gpu/ops.js:202-203); otherwise the materialized path's
   // semantics (:211-241), which rejects a key bias
@@ -323,10 +342,31 @@ export function attention(gpu, { q, k, v, Lq, Lk, H, D, ldq, ldk, ldv, qOff = 0,
     if (bias) throw new Error("attention: key bias needs the fused kernel");
     if (qNorm || kNorm || cs) throw new Error("attention: fused head norms need the fused kernel");
     if (textKV) throw new Error("attention: a separate text key/value view needs the fused kernel");
+    if (vPacked) throw new Error("attention: packed values need the fused kernel");
     if (D > 256) throw new Error(`attention: unsupported head dim ${D}`);
     gpu.run("attn.rows", 4 * Lq * Lk * D * H, () =>
       native.attentionRows(addr(q), addr(k), addr(v), addr(o), Lq, Lk, H, D, ldq, ldk, ldv, H * D, qOff, kOff, vOff,
         group, causal ? 1 : 0));
+    return o;
+  }
+  if (vPacked) {
+    // values of keys [0, vPacked.rows) already in vPacked.buf (linear() with opts.vpack)
+    const { buf, rows } = vPacked;
+    if (buf.vpack.Lk !== Lk || buf.vpack.H !== H || buf.vpack.D !== D) {
+      throw new Error("attention: the packed values were made for another shape");
+    }
+    let kt = null, vt = null, ldText = 0, textStart = 0;
+    if (textKV) {
+      const base = addr(textKV.t);
+      kt = base + BigInt(textKV.off * 4);
+      vt = base + BigInt((textKV.off + H * D) * 4);
+      ldText = textKV.ld;
+      textStart = textKV.start;
+    }
+    gpu.run("attn.flash", 4 * Lq * Lk * D * H, () =>
+      native.attentionVpacked(addr(q), addr(k), addr(v), addr(o), Lq, Lk, H, D, ldq, ldk, ldv, H * D, qOff, kOff,
+        vOff, 0, 1 / Math.sqrt(D), addr(bias), biasStart, addr(qNorm), addr(kNorm), eps, cs ? addr(cs) : null,
+        cs ? cs.sinOff : 0, cs ? ropeRows : 0, kt, vt, ldText, textStart, addr(buf), rows));
     return o;
   }
   if (textKV) {

@@ -76,6 +76,12 @@ SIGNATURES = {
     "ns2_attention_text": [c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
                            c_ll, c_ll, c_ll, c_ll, c_float, c_vp, c_int, c_vp, c_vp, c_float, c_vp, c_ll, c_int,
                            c_vp, c_vp, c_int, c_int],
+    "ns2_attention_vpacked": [c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
+                              c_ll, c_ll, c_ll, c_ll, c_float, c_vp, c_int, c_vp, c_vp, c_float, c_vp, c_ll, c_int,
+                              c_vp, c_vp, c_int, c_int, c_vp, c_int],
+    "ns2_attention_vpack_bytes": [c_int, c_int, c_int],
+    "ns2_linear_i8_tiled_vpack": [c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_ll, c_float, c_int,
+                                  c_vp, c_vp, c_int, c_vp, c_int, c_int, c_int, c_int],
     "ns2_attention_rows": [c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
                            c_ll, c_ll, c_ll, c_int, c_int],
     "ns2_head_norm": [c_vp, c_vp, c_int, c_int, c_int, c_int, c_ll, c_ll, c_vp, c_ll, c_float],
@@ -96,7 +102,8 @@ SIGNATURES = {
                                   c_int, c_vp, c_ll, c_int, c_float],
     "ns2_linear_bf16_add_rmsnorm": [c_vp, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_float],
 }
-_RESTYPES = {"ns2_last_error": ctypes.c_char_p, "ns2_get_stream": c_vp, "ns2_pool_round": c_size}
+_RESTYPES = {"ns2_last_error": ctypes.c_char_p, "ns2_get_stream": c_vp, "ns2_pool_round": c_size,
+             "ns2_attention_vpack_bytes": c_size}
 
 
 class NS2Error(RuntimeError):
@@ -219,6 +226,17 @@ class Lib:
                 N if ldc is None else ldc, cOff, alpha, ACT[act], int(resid), _ptr(gate), gOff]
         self._linear("ns2_linear_i8_tiled", args, lora)
 
+    def linear_i8_tiled_vpack(self, At, Wt, scale, C, M, N, K, vpk, *, vcol0, H, D, Lk, bias=None, ldc=None,
+                              cOff=0, alpha=1.0, act="none", lora=None):
+        """ns2_linear_i8_tiled_vpack: columns [vcol0, N) go to vpk as the attention's packed values
+        of keys [0, M)."""
+        a, b, r = lora if lora is not None else (None, None, 0)
+        self.call("ns2_linear_i8_tiled_vpack", _ptr(At), _ptr(Wt), _ptr(scale), _ptr(bias), _ptr(C), M, N, K,
+                  N if ldc is None else ldc, cOff, alpha, ACT[act], _ptr(a), _ptr(b), r, _ptr(vpk), vcol0, H, D, Lk)
+
+    def attention_vpack_bytes(self, Lk, H, D):
+        return int(self.dll.ns2_attention_vpack_bytes(Lk, H, D))
+
     def linear_i8(self, A, a_fmt, lda, W, scale, C, M, N, K, *, bias=None, add=None, ldc=None,
                   cOff=0, alpha=1.0, act="none", resid=False, gate=None, gOff=0, lora=None):
         args = [_ptr(A), a_fmt, lda, _ptr(W), _ptr(scale), _ptr(bias), _ptr(add),
@@ -263,6 +281,18 @@ class Lib:
         self.call("ns2_attention_text", _ptr(q), _ptr(k), _ptr(v), _ptr(o), Lq, Lk, H, D, ldq, ldk, ldv, ldo, qOff,
                   kOff, vOff, oOff, scale, _ptr(key_bias), biasStart, _ptr(q_norm), _ptr(k_norm), eps, _ptr(rope_cs),
                   sin_off, rope_rows, _ptr(k_text), _ptr(v_text), ld_text, text_start)
+
+    def attention_vpacked(self, q, k, v, o, vpk, v_rows, *, Lq, Lk, H, D, ldq, ldk, ldv, ldo, k_text=None,
+                          v_text=None, ld_text=0, text_start=0, qOff=0, kOff=0, vOff=0, oOff=0, scale=None,
+                          key_bias=None, biasStart=0, q_norm=None, k_norm=None, eps=1e-6, rope_cs=None, sin_off=0,
+                          rope_rows=0):
+        """ns2_attention_vpacked: the values of keys [0, v_rows) are already packed in vpk."""
+        if scale is None:
+            scale = 1.0 / D ** 0.5
+        self.call("ns2_attention_vpacked", _ptr(q), _ptr(k), _ptr(v), _ptr(o), Lq, Lk, H, D, ldq, ldk, ldv, ldo,
+                  qOff, kOff, vOff, oOff, scale, _ptr(key_bias), biasStart, _ptr(q_norm), _ptr(k_norm), eps,
+                  _ptr(rope_cs), sin_off, rope_rows, _ptr(k_text), _ptr(v_text), ld_text, text_start, _ptr(vpk),
+                  v_rows)
 
     def attention_rows(self, q, k, v, o, *, Lq, Lk, H, D, ldq, ldk, ldv, ldo, qOff=0, kOff=0, vOff=0,
                        group=1, causal=False):

@@ -564,6 +564,85 @@ def test_attention_text_view(ns2lib, pad):
     assert_close(o2.cpu(), ref, TOL, f"attention with a text view (pad {pad})")
 
 
+@pytest.mark.parametrize("L,T,text_view,lora", [
+    (3952, 256, True, False),   # the 832x1216 joint block: text keys from the stacked kv_y view
+    (496, 40, False, False),    # text rows inside the qkv buffer, a ragged last key tile
+    (512, 0, False, True),      # image-only keys, a LoRA term on the qkv weight
+])
+def test_qkv_vpack_attention(ns2lib, L, T, text_view, lora):
+    """ns2_linear_i8_tiled_vpack + ns2_attention_vpacked (the values go from the qkv GEMM's
+    epilogue straight into the attention's fp16 layout) against ns2_linear_i8_tiled +
+    ns2_attention / ns2_attention_text: the q|k columns and the attention output are
+    bit-identical, and the v columns of the qkv buffer are neither written nor read."""
+    Dm, H, HD, K = 1536, 16, 96, 1536
+    N, Lk = 3 * Dm, L + T
+    g = gen(L + T)
+    x = torch.randn(L, K, generator=g)
+    q8, s8 = int8_weight(N, K, g)
+    bias = (torch.randn(N, generator=g) * 0.1).to(dev)
+    sd = s8.reshape(-1).to(dev)
+    wt = torch.empty(N * K, dtype=torch.int8, device=dev)
+    ns2lib.tile_i8_weight(q8.to(dev), wt, N, K)
+    at = tiled_operand(L, K)
+    ns2lib.rotate_f16(x.to(dev), K, at, K, L, K, tiled=True)
+    lo = None
+    if lora:
+        R = 32
+        lo = ((torch.randn(R, K, generator=g) * 0.05).half().to(dev),
+              (torch.randn(N, R, generator=g) * 0.05).half().to(dev), R)
+    rows = L if text_view else Lk
+    txt = torch.randn(T, 2 * Dm, generator=g).to(dev)
+    qn = (torch.randn(HD, generator=g) * 0.5 + 1).to(dev)
+    kn = (torch.randn(HD, generator=g) * 0.5 + 1).to(dev)
+    lb = torch.log(torch.rand(T, generator=g) + 0.5).to(dev) if T else None
+    hgrid = 52 if L == 3952 else 16
+    cs, sin_off = O.rope2d_table(hgrid, L // hgrid)
+    kw = dict(Lq=L, Lk=Lk, H=H, D=HD, ldq=3 * Dm, ldk=3 * Dm, ldv=3 * Dm, ldo=Dm, qOff=0, kOff=Dm, vOff=2 * Dm,
+              key_bias=lb, biasStart=L, q_norm=qn, k_norm=kn, rope_cs=cs.to(dev), sin_off=sin_off, rope_rows=L)
+    tv = dict(k_text=txt[:, :Dm], v_text=txt[:, Dm:], ld_text=2 * Dm, text_start=L) if text_view else {}
+
+    qkv1 = torch.empty(rows, 3 * Dm, device=dev)
+    ns2lib.linear_i8_tiled(at, wt, sd, qkv1, L, N, K, bias=bias, ldc=3 * Dm, lora=lo)
+    if T and not text_view:
+        qkv1[L:, Dm:] = txt
+    o1 = torch.empty(L, Dm, device=dev)
+    if text_view:
+        ns2lib.attention_text(qkv1, qkv1, qkv1, o1, **tv, **kw)
+    else:
+        ns2lib.attention(qkv1, qkv1, qkv1, o1, **kw)
+
+    qkv2 = torch.full((rows, 3 * Dm), float("nan"), device=dev)
+    vpk = torch.empty(ns2lib.attention_vpack_bytes(Lk, H, HD) // 2, dtype=torch.int16, device=dev)
+    ns2lib.linear_i8_tiled_vpack(at, wt, sd, qkv2, L, N, K, vpk, vcol0=2 * Dm, H=H, D=HD, Lk=Lk, bias=bias,
+                                 ldc=3 * Dm, lora=lo)
+    if T and not text_view:
+        qkv2[L:, Dm:] = txt
+    o2 = torch.empty(L, Dm, device=dev)
+    ns2lib.attention_vpacked(qkv2, qkv2, qkv2, o2, vpk, L, **tv, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(qkv1[:L, :2 * Dm].cpu(), qkv2[:L, :2 * Dm].cpu()), "q|k columns differ"
+    assert torch.isnan(qkv2[:L, 2 * Dm:]).all().item(), "the v columns of qkv were written"
+    assert torch.equal(o1.cpu(), o2.cpu()), f"packed values change the attention (L {L}, T {T})"
+    assert torch.isfinite(o2).all().item()
+
+
+def test_qkv_vpack_errors(ns2lib):
+    vpk = torch.empty(1024, dtype=torch.int16, device=dev)
+    at = tiled_operand(64, 256)
+    wt = torch.empty(192 * 256, dtype=torch.int8, device=dev)
+    sc = torch.ones(192, device=dev)
+    out = torch.empty(64, 192, device=dev)
+    with pytest.raises(RuntimeError, match="multiple of 16"):
+        ns2lib.linear_i8_tiled_vpack(at, wt, sc, out, 40, 192, 256, vpk, vcol0=128, H=2, D=32, Lk=64)
+    with pytest.raises(RuntimeError, match="must end the output"):
+        ns2lib.linear_i8_tiled_vpack(at, wt, sc, out, 64, 192, 256, vpk, vcol0=64, H=2, D=32, Lk=64)
+    q = torch.zeros(64, 3 * 96, device=dev)
+    o = torch.empty(64, 96, device=dev)
+    with pytest.raises(RuntimeError, match="v_rows"):
+        ns2lib.attention_vpacked(q, q, q, o, vpk, 8, Lq=64, Lk=64, H=1, D=96, ldq=288, ldk=288, ldv=288, ldo=96,
+                                 kOff=96, vOff=192)
+
+
 @pytest.mark.parametrize("pad", [0, 1])
 def test_attention_strided_qkv_views(ns2lib, pad):
     """q/k/v as column windows of one packed [Lk, 3D] buffer, like the DiT's qkv
