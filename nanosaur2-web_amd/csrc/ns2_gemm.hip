@@ -637,7 +637,10 @@ int launch_gemm(const GemmArgs& p, const char* name, const RowNorm* rn = nullptr
     else if (p.M == 2) gemv_kernel<W_BF16, 2><<<grid, 256, 0, s>>>(p);
     else if (p.M <= 4) gemv_kernel<W_BF16, 4><<<grid, 256, 0, s>>>(p);
     else gemv_kernel<W_BF16, 8><<<grid, 256, 0, s>>>(p);
-  } else if (!post && big_tiles >= kSmallGridBlocks) {
+  } else if (!post && big_tiles >= 2 * kSmallGridBlocks && p.K > 256) {
+    // 128x128 tiles only where they make two full rounds over the CUs and K is not short: at
+    // 3952 x 1536 they make 1.45 rounds and the 64x64 grid is faster (x 1536 x 1536 with +=:
+    // 79.4 -> 70.3 us; x 1536 x 64: 17.7 -> 11.9 us; the same results)
     constexpr int BM = 128, BN = 128, WM = 64, WN = 64;
     dim3 grid((p.N + BN - 1) / BN, (p.M + BM - 1) / BM);
     if (p.lr) gemm_mfma_kernel<BM, BN, WM, WN, A_F32, W_BF16, true><<<grid, (BM / WM) * (BN / WN) * 64, 0, s>>>(p);
