@@ -192,19 +192,17 @@ __global__ __launch_bounds__(256) void attn_pack_kernel(PackArgs a) {
   }
 }
 
-// Vectorized pack for 16-byte aligned views (every view of the DiT path): no LDS, no
-// barrier, every global access 16 bytes per lane except the V gathers (D/32 floats). One
-// block per (64-row tile, head, batch):
-//   waves 0-1: Q rows, two lanes per row (lane half hh owns rope pairs [hh D/4, (hh+1) D/4));
-//   waves 2-3: K rows, the same split, stored straight into the chunk-major tile;
-//   all waves: V, lane (kc, dg) gathers the 8 keys of stored key-chunk kc for dims
-//   [dg D/32, (dg+1) D/32) and writes them as the 16-byte rows of the transposed tile.
+// One key row's share for four lanes (adjacent, within a quad): lane part q owns rope pairs
+// [q D/8, (q+1) D/8), i.e. dims q D/8 .. +D/8 of each half. Every load is issued first (the
+// row, the norm weights, the rope table): none depends on another, so their latencies overlap
+// instead of following the row's reduction.
 template <int D>
-__device__ __forceinline__ void prep_half_row(const float* __restrict__ src, const float* __restrict__ nw,
-                                              const float* __restrict__ cs, long long sinOff, int row,
-                                              bool rope, float mul, float eps, int hh, float* x1, float* x2) {
-  constexpr int HALF = D / 2, PER = D / 4;
-  const int i0 = hh * PER;
+__device__ __forceinline__ void prep_quarter_row(const float* __restrict__ src, const float* __restrict__ nw,
+                                                 const float* __restrict__ cs, long long sinOff, int row,
+                                                 bool rope, float eps, int q, float* x1, float* x2) {
+  constexpr int HALF = D / 2, PER = D / 8;
+  const int i0 = q * PER;
+  float w1[PER], w2[PER], c[PER], sn[PER];
 #pragma unroll
   for (int j = 0; j < PER; j += 4) {
     const float4 a = *reinterpret_cast<const float4*>(src + i0 + j);
@@ -213,19 +211,12 @@ __device__ __forceinline__ void prep_half_row(const float* __restrict__ src, con
     x2[j] = b.x, x2[j + 1] = b.y, x2[j + 2] = b.z, x2[j + 3] = b.w;
   }
   if (nw) {
-    float ss = 0.f;
-#pragma unroll
-    for (int j = 0; j < PER; ++j) ss += x1[j] * x1[j] + x2[j] * x2[j];
-    ss += dpp<kDppXor1>(ss);  // the row's other lane
-    const float r = rsqrtf(ss / (float)D + eps);
 #pragma unroll
     for (int j = 0; j < PER; j += 4) {
-      const float4 w1 = *reinterpret_cast<const float4*>(nw + i0 + j);
-      const float4 w2 = *reinterpret_cast<const float4*>(nw + HALF + i0 + j);
-      x1[j] = x1[j] * r * w1.x, x1[j + 1] = x1[j + 1] * r * w1.y;
-      x1[j + 2] = x1[j + 2] * r * w1.z, x1[j + 3] = x1[j + 3] * r * w1.w;
-      x2[j] = x2[j] * r * w2.x, x2[j + 1] = x2[j + 1] * r * w2.y;
-      x2[j + 2] = x2[j + 2] * r * w2.z, x2[j + 3] = x2[j + 3] * r * w2.w;
+      const float4 a = *reinterpret_cast<const float4*>(nw + i0 + j);
+      const float4 b = *reinterpret_cast<const float4*>(nw + HALF + i0 + j);
+      w1[j] = a.x, w1[j + 1] = a.y, w1[j + 2] = a.z, w1[j + 3] = a.w;
+      w2[j] = b.x, w2[j + 1] = b.y, w2[j + 2] = b.z, w2[j + 3] = b.w;
     }
   }
   if (rope) {
@@ -233,22 +224,33 @@ __device__ __forceinline__ void prep_half_row(const float* __restrict__ src, con
     const float* sp = cs + sinOff + (long long)row * HALF + i0;
 #pragma unroll
     for (int j = 0; j < PER; j += 4) {
-      const float4 c4 = *reinterpret_cast<const float4*>(cp + j);
-      const float4 s4 = *reinterpret_cast<const float4*>(sp + j);
-      const float c[4] = {c4.x, c4.y, c4.z, c4.w}, sn[4] = {s4.x, s4.y, s4.z, s4.w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float y1 = x1[j + e] * c[e] - x2[j + e] * sn[e];
-        const float y2 = x2[j + e] * c[e] + x1[j + e] * sn[e];
-        x1[j + e] = y1;
-        x2[j + e] = y2;
-      }
+      const float4 a = *reinterpret_cast<const float4*>(cp + j);
+      const float4 b = *reinterpret_cast<const float4*>(sp + j);
+      c[j] = a.x, c[j + 1] = a.y, c[j + 2] = a.z, c[j + 3] = a.w;
+      sn[j] = b.x, sn[j + 1] = b.y, sn[j + 2] = b.z, sn[j + 3] = b.w;
     }
   }
+  if (nw) {
+    float ss = 0.f;
 #pragma unroll
-  for (int j = 0; j < PER; ++j) {
-    x1[j] *= mul;
-    x2[j] *= mul;
+    for (int j = 0; j < PER; ++j) ss += x1[j] * x1[j] + x2[j] * x2[j];
+    ss += dpp<kDppXor1>(ss);  // the row's other three lanes
+    ss += dpp<kDppXor2>(ss);
+    const float r = rsqrtf(ss / (float)D + eps);
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      x1[j] = x1[j] * r * w1[j];
+      x2[j] = x2[j] * r * w2[j];
+    }
+  }
+  if (rope) {
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const float y1 = x1[j] * c[j] - x2[j] * sn[j];
+      const float y2 = x2[j] * c[j] + x1[j] * sn[j];
+      x1[j] = y1;
+      x2[j] = y2;
+    }
   }
 }
 
@@ -256,9 +258,16 @@ __device__ __forceinline__ uint4 pack8_f16(const float* x) {
   return make_uint4(pack_half2(x[0], x[1]), pack_half2(x[2], x[3]), pack_half2(x[4], x[5]), pack_half2(x[6], x[7]));
 }
 
+// Vectorized pack for 16-byte aligned views (every view of the DiT path): no LDS, no
+// barrier, every global access 16 bytes per lane except the V gathers (D/32 floats). One
+// block per (64-row tile, head, batch):
+//   all waves: K rows, four lanes per row (norm and RoPE applied), stored straight into the
+//   chunk-major tile (the flash kernel reads Q itself from these aligned views);
+//   all waves: V, lane (kc, dg) gathers the 8 keys of stored key-chunk kc for dims
+//   [dg D/32, (dg+1) D/32) and writes them as the 16-byte rows of the transposed tile.
 template <int D>
 __global__ __launch_bounds__(256) void attn_pack_vec_kernel(PackArgs a) {
-  constexpr int HALF = D / 2, PER = D / 4, DPL = D / 32;
+  constexpr int HALF = D / 2, DPL = D / 32;
   const int h = blockIdx.y, b = blockIdx.z;
   const int bh = b * a.H + h;
   const int tile = blockIdx.x, row0 = tile * KB;
@@ -289,39 +298,28 @@ __global__ __launch_bounds__(256) void attn_pack_vec_kernel(PackArgs a) {
     }
   }
 
-  const int rl = (tid & 127) >> 1, hh = tid & 1;
-  const int row = row0 + rl;
-  float x1[PER], x2[PER];
-  if (tid < 128) {
-    if (!a.skip_q && row0 < a.Lq_pad) {
-      if (row < a.Lq) {
-        const float* src = a.q + a.qOff + b * a.qBatch + (long long)row * a.ldq + (long long)h * D;
-        prep_half_row<D>(src, a.q_norm, a.cs, a.sinOff, row, a.cs && row < a.rope_rows, a.qscale, a.eps, hh, x1, x2);
-      } else {
-#pragma unroll
-        for (int j = 0; j < PER; ++j) x1[j] = x2[j] = 0.f;
-      }
-      half_t* dst = a.Qp + ((long long)bh * a.Lq_pad + row) * D + hh * PER;
-#pragma unroll
-      for (int j = 0; j < PER; j += 8) {
-        *reinterpret_cast<uint4*>(dst + j) = pack8_f16(x1 + j);
-        *reinterpret_cast<uint4*>(dst + HALF + j) = pack8_f16(x2 + j);
-      }
-    }
-  } else if (kv) {
+  // K rows, four lanes per row, stored as 4-half pieces of the 8-dim chunks: chunk c (dims
+  // 8c..8c+7) of key rl sits at (c * 64 + rl) * 8 in the tile
+  if (kv) {
+    constexpr int PER = D / 8;
+    const int rl = tid >> 2, q = tid & 3;
+    const int row = row0 + rl;
+    float x1[PER], x2[PER];
     if (row < a.Lk) {
       const float* src = key_row(a, b, row) + (long long)h * D;
-      prep_half_row<D>(src, a.k_norm, a.cs, a.sinOff, row, a.cs && row < a.rope_rows, 1.0f, a.eps, hh, x1, x2);
+      prep_quarter_row<D>(src, a.k_norm, a.cs, a.sinOff, row, a.cs && row < a.rope_rows, a.eps, q, x1, x2);
     } else {
 #pragma unroll
       for (int j = 0; j < PER; ++j) x1[j] = x2[j] = 0.f;
     }
-    // chunk c (dims 8c..8c+7) of key rl sits at (c * 64 + rl) * 8 in the tile
     half_t* kdst = a.Kc + ((long long)bh * tiles + tile) * (KB * D) + rl * 8;
 #pragma unroll
-    for (int j = 0; j < PER; j += 8) {
-      *reinterpret_cast<uint4*>(kdst + ((hh * PER + j) / 8) * (KB * 8)) = pack8_f16(x1 + j);
-      *reinterpret_cast<uint4*>(kdst + ((HALF + hh * PER + j) / 8) * (KB * 8)) = pack8_f16(x2 + j);
+    for (int j = 0; j < PER; j += 4) {
+      const int d1 = q * PER + j, d2 = HALF + d1;
+      *reinterpret_cast<uint2*>(kdst + (d1 / 8) * (KB * 8) + d1 % 8) =
+          make_uint2(pack_half2(x1[j], x1[j + 1]), pack_half2(x1[j + 2], x1[j + 3]));
+      *reinterpret_cast<uint2*>(kdst + (d2 / 8) * (KB * 8) + d2 % 8) =
+          make_uint2(pack_half2(x2[j], x2[j + 1]), pack_half2(x2[j + 2], x2[j + 3]));
     }
   }
 
