@@ -291,6 +291,23 @@ __global__ __launch_bounds__(256) void elementwise_kernel(int op, const float* _
   y[i] = v;
 }
 
+// The same per element, four elements per thread (16-byte aligned buffers, n % 4 == 0).
+__device__ __forceinline__ float ew_op(int op, float v, float w) {
+  if (op == NS2_EW_ADD) return v + w;
+  if (op == NS2_EW_SUB) return v - w;
+  if (op == NS2_EW_SILU) return silu(v);
+  return v;
+}
+__global__ __launch_bounds__(256) void elementwise4_kernel(int op, const float4* __restrict__ a,
+                                                            const float4* __restrict__ b,
+                                                            float4* __restrict__ y, long long n4) {
+  long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n4) return;
+  const float4 v = a[i];
+  const float4 w = (op == NS2_EW_ADD || op == NS2_EW_SUB) ? b[i] : v;
+  y[i] = make_float4(ew_op(op, v.x, w.x), ew_op(op, v.y, w.y), ew_op(op, v.z, w.z), ew_op(op, v.w, w.w));
+}
+
 __global__ __launch_bounds__(256) void accumulate_kernel(float* __restrict__ y,
                                                           const float* __restrict__ a,
                                                           long long n) {
@@ -503,7 +520,12 @@ int ns2_elementwise(int op, const float* a, const float* b, float* y, long long 
   NS2_REQUIRE(op >= NS2_EW_ADD && op <= NS2_EW_COPY, "ns2_elementwise: unknown op %d", op);
   NS2_REQUIRE(a && y && (b || op == NS2_EW_SILU || op == NS2_EW_COPY), "ns2_elementwise: null buffer");
   ns2::ProfScope prof_("elementwise");
-  elementwise_kernel<<<blocks_for(n, 256), 256, 0, ns2::stream()>>>(op, a, b, y, n);
+  if (n % 4 == 0 && aligned16(a) && aligned16(y) && (!b || aligned16(b))) {
+    elementwise4_kernel<<<blocks_for(n / 4, 256), 256, 0, ns2::stream()>>>(
+        op, reinterpret_cast<const float4*>(a), reinterpret_cast<const float4*>(b), reinterpret_cast<float4*>(y), n / 4);
+  } else {
+    elementwise_kernel<<<blocks_for(n, 256), 256, 0, ns2::stream()>>>(op, a, b, y, n);
+  }
   NS2_LAUNCHED("elementwise");
   return NS2_OK;
 }

@@ -795,6 +795,13 @@ def test_elementwise_accumulate_rowsum_rmsnorm(ns2lib):
         ns2lib.elementwise(op, ad, bd, y, a.numel())
         torch.cuda.synchronize()
         assert_close(y.cpu(), ref, TOL_F32, f"elementwise {op}")
+        # the per-element kernel: a length that is not a multiple of 4, and views 4 bytes off
+        # 16-byte alignment; both kernels give the same values
+        y1 = torch.zeros_like(ad)
+        ns2lib.elementwise(op, ad, bd, y1, a.numel() - 3)
+        ns2lib.elementwise(op, ad[1:], bd[1:], y1[1:], 8)
+        torch.cuda.synchronize()
+        assert torch.equal(y1.cpu()[:a.numel() - 3], y.cpu()[:a.numel() - 3]), f"elementwise {op} (scalar)"
     yd = a.to(dev)
     ns2lib.accumulate(yd, bd, a.numel())
     torch.cuda.synchronize()
