@@ -76,6 +76,54 @@ __global__ __launch_bounds__(256) void norm_mod_kernel(const float* __restrict__
   }
 }
 
+// The same for rows of 256 G columns on 16-byte aligned buffers: one wave per row, 8 rows per
+// block, every load of the row issued before any arithmetic (lane l holds columns 4l..4l+3 of
+// each 256-column group), the statistics as wave reductions, the same per-element order.
+template <int G>
+__global__ __launch_bounds__(512) void norm_mod_rows_kernel(const float* __restrict__ x,
+                                                             const float* __restrict__ mod,
+                                                             long long shiftOff, long long scaleOff, int rows,
+                                                             const float* __restrict__ w, float eps,
+                                                             float* __restrict__ y) {
+  const int row = blockIdx.x * 8 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  constexpr int cols = 256 * G;
+  const int lane = threadIdx.x & 63;
+  const float* src = x + (long long)row * cols + 4 * lane;
+  float4 v[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) v[g] = *reinterpret_cast<const float4*>(src + 256 * g);
+  float mean = 0.f;
+  if (!w) {
+    float s = 0.f;
+#pragma unroll
+    for (int g = 0; g < G; ++g) s += (v[g].x + v[g].y) + (v[g].z + v[g].w);
+    mean = wave_sum(s) / (float)cols;
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    v[g].x -= mean, v[g].y -= mean, v[g].z -= mean, v[g].w -= mean;
+    ss += v[g].x * v[g].x + v[g].y * v[g].y + v[g].z * v[g].z + v[g].w * v[g].w;
+  }
+  const float r = rsqrtf(wave_sum(ss) / (float)cols + eps);
+  float* dst = y + (long long)row * cols + 4 * lane;
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const int c = 256 * g + 4 * lane;
+    const float4 sc = *reinterpret_cast<const float4*>(mod + scaleOff + c);
+    const float4 sh = *reinterpret_cast<const float4*>(mod + shiftOff + c);
+    float4 n = make_float4(v[g].x * r, v[g].y * r, v[g].z * r, v[g].w * r);
+    if (w) {
+      const float4 ww = *reinterpret_cast<const float4*>(w + c);
+      n.x *= ww.x, n.y *= ww.y, n.z *= ww.z, n.w *= ww.w;
+    }
+    *reinterpret_cast<float4*>(dst + 256 * g) =
+        make_float4(n.x * (1.0f + sc.x) + sh.x, n.y * (1.0f + sc.y) + sh.y, n.z * (1.0f + sc.z) + sh.z,
+                    n.w * (1.0f + sc.w) + sh.w);
+  }
+}
+
 // ---- rotated fp16 producers, one wave per row ------------------------------------------------
 
 struct RotRowsArgs {
@@ -445,7 +493,18 @@ int ns2_norm_mod(const float* x, const float* mod, long long shiftOff, long long
   if (rows <= 0) return NS2_OK;
   NS2_REQUIRE(x && mod && y && cols > 0, "ns2_norm_mod: bad arguments");
   ns2::ProfScope prof_("norm_mod");
-  norm_mod_kernel<<<rows, 256, 0, ns2::stream()>>>(x, mod, shiftOff, scaleOff, cols, weight, eps, y);
+  const bool rows_ok = cols % 256 == 0 && cols <= 256 * 8 && aligned16(x) && aligned16(mod) && aligned16(y) &&
+                       shiftOff % 4 == 0 && scaleOff % 4 == 0 && (!weight || aligned16(weight));
+  const dim3 grid((rows + 7) / 8), block(512);
+  hipStream_t s = ns2::stream();
+  switch (rows_ok ? cols / 256 : 0) {
+#define NS2_NM_CASE(G) \
+    case G: norm_mod_rows_kernel<G><<<grid, block, 0, s>>>(x, mod, shiftOff, scaleOff, rows, weight, eps, y); break;
+    NS2_NM_CASE(1) NS2_NM_CASE(2) NS2_NM_CASE(3) NS2_NM_CASE(4) NS2_NM_CASE(5) NS2_NM_CASE(6) NS2_NM_CASE(7)
+    NS2_NM_CASE(8)
+#undef NS2_NM_CASE
+    default: norm_mod_kernel<<<rows, 256, 0, s>>>(x, mod, shiftOff, scaleOff, cols, weight, eps, y);
+  }
   NS2_LAUNCHED("norm_mod");
   return NS2_OK;
 }
