@@ -102,8 +102,11 @@ export class Nanosaur2DiT {
       }
       for (const b of m.text.concat(m.blocks)) {
         for (const W of [b.qkv, b.kvY, b.proj, b.w3]) if (W && ops.tileable(W)) ops.tileWeight(gpu, W);
-        // the MLP's first linear runs fused with its GLU and the rotation for w3
-        if (b.w12.kind === "i8" && b.w12.N % 512 === 0 && b.w12.K % 256 === 0) ops.tileWeightGlu(gpu, b.w12);
+        // the image blocks' MLP runs its first linear fused with the GLU and the rotation for w3;
+        // the text blocks' (a few hundred rows: 64 work-groups of the fused launch's 64 x 512
+        // tiles) run the plain tiled GEMM over 64 x 128 tiles, then the GLU and rotation
+        const text = m.text.includes(b);
+        if (!text && b.w12.kind === "i8" && b.w12.N % 512 === 0 && b.w12.K % 256 === 0) ops.tileWeightGlu(gpu, b.w12);
         else if (ops.tileable(b.w12)) ops.tileWeight(gpu, b.w12);
         // the fused path feeds every re-tiled weight tiled operands only: keep one copy (w12's
         // GLU tiles serve only while w3 takes the tiled operand the GLU launch writes)
