@@ -566,6 +566,7 @@ def test_attention_text_view(ns2lib, pad):
 
 @pytest.mark.parametrize("L,T,text_view,lora", [
     (3952, 256, True, False),   # the 832x1216 joint block: text keys from the stacked kv_y view
+    (4096, 256, True, False),   # 1024x1024: whole row tiles, 68 key tiles
     (496, 40, False, False),    # text rows inside the qkv buffer, a ragged last key tile
     (512, 0, False, True),      # image-only keys, a LoRA term on the qkv weight
 ])
@@ -595,7 +596,7 @@ def test_qkv_vpack_attention(ns2lib, L, T, text_view, lora):
     qn = (torch.randn(HD, generator=g) * 0.5 + 1).to(dev)
     kn = (torch.randn(HD, generator=g) * 0.5 + 1).to(dev)
     lb = torch.log(torch.rand(T, generator=g) + 0.5).to(dev) if T else None
-    hgrid = 52 if L == 3952 else 16
+    hgrid = {3952: 52, 4096: 64}.get(L, 16)
     cs, sin_off = O.rope2d_table(hgrid, L // hgrid)
     kw = dict(Lq=L, Lk=Lk, H=H, D=HD, ldq=3 * Dm, ldk=3 * Dm, ldv=3 * Dm, ldo=Dm, qOff=0, kOff=Dm, vOff=2 * Dm,
               key_bias=lb, biasStart=L, q_norm=qn, k_norm=kn, rope_cs=cs.to(dev), sin_off=sin_off, rope_rows=L)
