@@ -10,12 +10,15 @@
 //    q|k|v has one slice per part;
 //  * loadLora reads a file into host arrays and resolves each module to a slice; attachLoras
 //    hands them to their weights with a strength;
-//  * the first launch of a weight after that builds its side path on the device (loraArgs):
-//    every LoRA of the weight stacked into one fp16 pair, lora_a [R, K] and lora_b [N, R]
-//    (strength * alpha / r * B_i in its output window, zero elsewhere), R the summed ranks
-//    rounded up to 32. The GEMM kernels start their accumulators at the low-rank term (the
-//    *_lora entry points of the C ABI) where the reference runs two more matmuls per LoRA and
-//    adds an [M, N] delta (app/gpu/ops.js:70-87).
+//  * the first launch of a weight after that builds its side paths on the device
+//    (loraLaunches): the LoRAs of a row window of the weight stacked into one fp16 pair,
+//    lora_a [R, K] and lora_b [n, R] (strength * alpha / r * B_i in its output rows, zero
+//    elsewhere), R the summed ranks rounded up to 32 and at most MAX_RANK. A weight is one
+//    window; a stacked weight (Gemma3's q|k|v, the DiT's kv_y of all joint blocks) is cut into
+//    windows of whole parts when its parts' ranks do not fit one side path, and linear() then
+//    launches once per window. The GEMM kernels start their accumulators at the low-rank term
+//    (the *_lora entry points of the C ABI) where the reference runs two more matmuls per LoRA
+//    and adds an [M, N] delta (app/gpu/ops.js:70-87).
 //  * int8 ConvRot weights take rotated inputs x H, and x A^T = (x H)(A H)^T, so their lora_a
 //    rows are rotated on the device by the kernel that rotates the activations
 //    (app/lora.js:72-91 rotates them on the host).
@@ -147,11 +150,13 @@ function dropPacks(regs) {
   for (const reg of [regs.dit, regs.te]) {
     if (!reg) continue;
     for (const { W } of reg.values()) {
-      if (W.loraPack) {
-        W.loraPack.a.destroy();
-        W.loraPack.b.destroy();
-        W.loraPack = null;
+      if (!W.loraPacks) continue;
+      for (const p of W.loraPacks) {
+        if (!p.args) continue;
+        p.a.destroy();
+        p.b.destroy();
       }
+      W.loraPacks = null;
     }
   }
 }
@@ -209,18 +214,52 @@ export function f32ToF16Bits(f) {
   return out;
 }
 
-// Host arrays of a weight's stacked side path: { a: fp32 [R, K] (not rotated), b: fp32 [N, R], R }.
-export function stackLora(W) {
-  const rs = W.lora.reduce((s, e) => s + e.r, 0);
-  const R = Math.ceil(rs / 32) * 32;
-  if (R > 256) throw new Error(`${W.name}: stacked LoRA rank ${rs} exceeds 256`);
+// Largest stacked rank of one side path (the GEMM epilogues' low-rank term).
+export const MAX_RANK = 256;
+
+const roundRank = (r) => Math.ceil(r / 32) * 32;
+const weightLabel = (W) => W.name || (W.parts ? W.parts.map((p) => p.name).join("+") : "linear");
+
+// The row windows of W that share one side path: [{ off, n, entries }]. A weight without parts
+// is one window. The parts of a stacked weight stay together while their ranks fit MAX_RANK;
+// past that a new window starts at the next part, so each window is a run of whole parts
+// (the reference applies each LoRA on its own, with no rank limit: app/gpu/ops.js:70-87).
+export function loraWindows(W) {
+  const lora = W.lora || [];
+  const parts = W.parts || [{ name: W.name, off: 0, n: W.N }];
+  const wins = [];
+  let cur = null;
+  for (const p of parts) {
+    const entries = lora.filter((e) => e.off >= p.off && e.off < p.off + p.n);
+    const r = entries.reduce((s, e) => s + e.r, 0);
+    if (roundRank(r) > MAX_RANK) {
+      throw new Error(`${p.name || weightLabel(W)}: LoRA rank ${r} on one linear exceeds ${MAX_RANK}`);
+    }
+    if (cur && roundRank(cur.rank + r) <= MAX_RANK) {
+      cur.n += p.n;
+      cur.rank += r;
+      cur.entries.push(...entries);
+    } else {
+      cur = { off: p.off, n: p.n, rank: r, entries };
+      wins.push(cur);
+    }
+  }
+  return wins.map(({ off, n, entries }) => ({ off, n, entries }));
+}
+
+// Host arrays of one side path: { a: fp32 [R, K] (not rotated), b: fp32 [n, R], R } over the
+// row window win of W (the whole weight by default).
+export function stackLora(W, win = { off: 0, n: W.N, entries: W.lora }) {
+  const rs = win.entries.reduce((s, e) => s + e.r, 0);
+  const R = roundRank(rs);
+  if (R > MAX_RANK) throw new Error(`${weightLabel(W)}: stacked LoRA rank ${rs} exceeds ${MAX_RANK}`);
   const a = new Float32Array(R * W.K);
-  const b = new Float32Array(W.N * R);
+  const b = new Float32Array(win.n * R);
   let r0 = 0;
-  for (const e of W.lora) {
+  for (const e of win.entries) {
     a.set(e.A, r0 * W.K);
     for (let i = 0; i < e.n; i++) {
-      const row = (e.off + i) * R + r0;
+      const row = (e.off - win.off + i) * R + r0;
       for (let k = 0; k < e.r; k++) b[row + k] = e.scale * e.B[i * e.r + k];
     }
     r0 += e.r;
@@ -228,11 +267,11 @@ export function stackLora(W) {
   return { a, b, R };
 }
 
-// The device side path of W: lora_b uploaded as fp16; lora_a as fp16 too, for an int8 weight
-// rotated per 256-group on the way by the activation rotation kernel (fp32 rows in a pooled
-// staging tensor, rotated and rounded to fp16 into the persistent buffer).
-function buildPack(gpu, W) {
-  const { a, b, R } = stackLora(W);
+// The device side path of one window of W: lora_b uploaded as fp16; lora_a as fp16 too, for an
+// int8 weight rotated per 256-group on the way by the activation rotation kernel (fp32 rows in a
+// pooled staging tensor, rotated and rounded to fp16 into the persistent buffer).
+function buildPack(gpu, W, win) {
+  const { a, b, R } = stackLora(W, win);
   let aBuf;
   if (W.kind === "i8") {
     const bytes = R * W.K * 2;
@@ -246,10 +285,26 @@ function buildPack(gpu, W) {
   return { a: aBuf, b: gpu.upload(f32ToF16Bits(b)), R };
 }
 
-// [loraA, loraB, loraR] of W for the *_lora entry points, the side path built on first use
-// after attachLoras; [null, null, 0] without LoRA.
+// The launches a linear over W makes: [{ off, n, args }], args = [loraA, loraB, loraR] for the
+// *_lora entry points over output rows [off, off + n) of W. One launch over the whole weight
+// without LoRA ([null, null, 0]) or when its LoRAs fit one side path; the side paths are built
+// on first use after attachLoras.
+export function loraLaunches(gpu, W) {
+  if (!W.lora || !W.lora.length) return [{ off: 0, n: W.N, args: [null, null, 0] }];
+  if (!W.loraPacks) {
+    W.loraPacks = loraWindows(W).map((win) => {
+      if (!win.entries.length) return { off: win.off, n: win.n, args: [null, null, 0] };
+      const p = buildPack(gpu, W, win);
+      return { off: win.off, n: win.n, a: p.a, b: p.b, args: [p.a.ptr, p.b.ptr, p.R] };
+    });
+  }
+  return W.loraPacks;
+}
+
+// [loraA, loraB, loraR] of W for a launch that covers the whole weight (the fused GLU and
+// packed-value launches); [null, null, 0] without LoRA.
 export function loraArgs(gpu, W) {
-  if (!W.lora || !W.lora.length) return [null, null, 0];
-  if (!W.loraPack) W.loraPack = buildPack(gpu, W);
-  return [W.loraPack.a.ptr, W.loraPack.b.ptr, W.loraPack.R];
+  const ls = loraLaunches(gpu, W);
+  if (ls.length !== 1) throw new Error(`${weightLabel(W)}: its LoRAs need ${ls.length} side paths; this launch takes one`);
+  return ls[0].args;
 }

@@ -8,7 +8,7 @@
 
 import { addr, DeviceBuffer } from "./device.js";
 import { native, ACT, EW } from "./native.js";
-import { loraArgs } from "./lora.js";
+import { loraArgs, loraLaunches } from "./lora.js";
 
 const opt = (v, d) => (v === undefined || v === null ? d : v);
 
@@ -107,9 +107,6 @@ export function packedValues(gpu, Lk, H, D) {
 export function linear(gpu, x, W, opts = {}) {
   const src = opts.xr || x;
   const M = src.tiled ? src.rows : src.size / W.K;
-  // LoRA side paths (W.lora, attached by lora.js): the stacked low-rank term starts the GEMM's
-  // accumulators; the down-projection takes the same (rotated) input (app/gpu/ops.js:54-58)
-  const lora = loraArgs(gpu, W);
   const out = opts.out || gpu.empty([M, W.N]);
   const ldc = opt(opts.ldc, W.N);
   const cOff = opt(opts.cOff, 0);
@@ -118,32 +115,47 @@ export function linear(gpu, x, W, opts = {}) {
   const act = ACT[opts.act || "none"];
   if (act === undefined) throw new Error(`linear: unknown activation ${opts.act}`);
   const resid = opts.resid ? 1 : 0;
-  const flops = 2 * M * W.N * W.K;
   if (W.kind === "i8" && src.tiled && opts.vpack) {
     if (!W.tbuf) throw new Error(`${W.name}: a tiled operand needs the tiled weight (tileWeight)`);
     if (resid) throw new Error("linear: packed values take a plain store (no resid)");
+    const lora = loraArgs(gpu, W);
     const { buf, col0 } = opts.vpack;
     const { Lk, H, D } = buf.vpack;
-    gpu.run(opts.name || "gemm.i8", flops, () =>
+    gpu.run(opts.name || "gemm.i8", 2 * M * W.N * W.K, () =>
       native.linearI8TiledVpack(addr(src), addr(W.tbuf), addr(W.scale), addr(bias), addr(out), M, W.N, W.K, ldc,
         cOff, 1, act, ...lora, addr(buf), col0, H, D, Lk));
-  } else if (W.kind === "i8" && src.tiled) {
-    if (!W.tbuf) throw new Error(`${W.name}: a tiled operand needs the tiled weight (tileWeight)`);
-    gpu.run(opts.name || "gemm.i8", flops, () =>
-      native.linearI8Tiled(addr(src), addr(W.tbuf), addr(W.scale), addr(bias), addr(out), M, W.N, W.K, ldc,
-        cOff, 1, act, resid, addr(opts.gate), gOff, ...lora));
-  } else if (W.kind === "i8") {
-    if (!W.buf) throw new Error(`${W.name}: the row-major int8 weight was freed after tiling; pass a tiled operand`);
-    const aFmt = opts.xr ? (opts.xr.dtype === "f16" ? 1 : 2) : 0;
-    gpu.run(opts.name || "gemm.i8", flops, () =>
-      native.linearI8(addr(src), aFmt, W.K, addr(W.buf), addr(W.scale), addr(bias), null, addr(out),
-        M, W.N, W.K, ldc, cOff, 1, act, resid, addr(opts.gate), gOff, ...lora));
-  } else if (W.kind === "bf16") {
-    gpu.run(opts.name || "gemm.bf16", flops, () =>
-      native.linearBf16(addr(x), W.K, addr(W.buf), addr(bias), null, addr(out), M, W.N, W.K, ldc, cOff,
-        1, act, resid, addr(opts.gate), gOff, ...lora));
-  } else {
-    throw new Error(`linear: weight kind ${W.kind} is not part of this build`);
+    return out;
+  }
+  if (W.kind === "i8" && src.tiled && !W.tbuf) throw new Error(`${W.name}: a tiled operand needs the tiled weight (tileWeight)`);
+  if (W.kind === "i8" && !src.tiled && !W.buf) {
+    throw new Error(`${W.name}: the row-major int8 weight was freed after tiling; pass a tiled operand`);
+  }
+  if (W.kind !== "i8" && W.kind !== "bf16") throw new Error(`linear: weight kind ${W.kind} is not part of this build`);
+  // LoRA side paths (W.lora, attached by lora.js): the stacked low-rank term starts the GEMM's
+  // accumulators; the down-projection takes the same (rotated) input (app/gpu/ops.js:54-58). A
+  // stacked weight whose LoRAs need several side paths launches once per row window of W,
+  // each into its own output columns.
+  for (const { off, n, args: lora } of loraLaunches(gpu, W)) {
+    if (W.kind === "i8" && src.tiled && off % 64) throw new Error(`${W.name}: LoRA window at row ${off} is not tile aligned`);
+    const rowBytes = W.kind === "i8" ? W.K : 2 * W.K;
+    const wAt = (buf) => addr(buf) + BigInt(off * rowBytes);
+    const vAt = (t) => (t ? addr(t) + BigInt(4 * off) : null);
+    const flops = 2 * M * n * W.K;
+    const c0 = cOff + off, g0 = gOff + off;
+    if (W.kind === "i8" && src.tiled) {
+      gpu.run(opts.name || "gemm.i8", flops, () =>
+        native.linearI8Tiled(addr(src), wAt(W.tbuf), vAt(W.scale), vAt(bias), addr(out), M, n, W.K, ldc,
+          c0, 1, act, resid, addr(opts.gate), g0, ...lora));
+    } else if (W.kind === "i8") {
+      const aFmt = opts.xr ? (opts.xr.dtype === "f16" ? 1 : 2) : 0;
+      gpu.run(opts.name || "gemm.i8", flops, () =>
+        native.linearI8(addr(src), aFmt, W.K, wAt(W.buf), vAt(W.scale), vAt(bias), null, addr(out),
+          M, n, W.K, ldc, c0, 1, act, resid, addr(opts.gate), g0, ...lora));
+    } else {
+      gpu.run(opts.name || "gemm.bf16", flops, () =>
+        native.linearBf16(addr(x), W.K, wAt(W.buf), vAt(bias), null, addr(out), M, n, W.K, ldc, c0,
+          1, act, resid, addr(opts.gate), g0, ...lora));
+    }
   }
   return out;
 }

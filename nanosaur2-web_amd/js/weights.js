@@ -251,7 +251,8 @@ export function concatLinears(gpu, Ws) {
   const rowBytes = kind === "i8" ? K : 2 * K;
   if (rowBytes % 4) throw new Error("concatLinears: rows must be whole 32-bit words");
   const N = Ws.reduce((a, w) => a + w.N, 0);
-  const out = { kind, K, N, parts: [], bias: null };
+  const name = Ws.length > 2 ? `${Ws[0].name} + ... + ${Ws[Ws.length - 1].name}` : Ws.map((w) => w.name).join(" + ");
+  const out = { name, kind, K, N, parts: [], bias: null };
   let off = 0;
   for (const w of Ws) {
     out.parts.push({ name: w.name, off, n: w.N });

@@ -123,11 +123,17 @@ def lora_targets(I=4096):
     ]
 
 
-def make_lora(seed=9, I=4096, a_std=0.05, b_std=0.05):
-    """A LoRA file's tensors (bf16 A/B, fp32 alpha = rank / 2) for lora_targets(I), seeded."""
+def joint_kv_targets(r=32, blocks=18):
+    """A rank-r LoRA on the text k|v projection (kv_y) of every joint block (the even blocks)."""
+    return [(f"blocks.{i}.attn.kv_y", 2 * D, D, r, "peft") for i in range(0, blocks, 2)]
+
+
+def make_lora(seed=9, I=4096, a_std=0.05, b_std=0.05, targets=None):
+    """A LoRA file's tensors (bf16 A/B, fp32 alpha = rank / 2) for targets (lora_targets(I) by
+    default), seeded."""
     rng = np.random.default_rng(seed)
     out = {}
-    for module, n_out, n_in, r, naming in lora_targets(I):
+    for module, n_out, n_in, r, naming in (targets or lora_targets(I)):
         A = torch.from_numpy(rng.standard_normal((r, n_in), dtype=np.float32) * np.float32(a_std)).to(torch.bfloat16)
         B = torch.from_numpy(rng.standard_normal((n_out, r), dtype=np.float32) * np.float32(b_std)).to(torch.bfloat16)
         alpha = torch.tensor(r / 2.0, dtype=torch.float32)

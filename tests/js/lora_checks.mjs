@@ -17,6 +17,20 @@ async function main() {
   const W = { name: "w", N: job.N, K: job.K, lora: job.entries.map((e) => ({ ...e, A: Float32Array.from(e.A), B: Float32Array.from(e.B) })) };
   const s = L.stackLora(W);
   out.stack = { R: s.R, a: Array.from(s.a), b: Array.from(s.b) };
+  // a stacked weight whose parts' LoRAs do not fit one side path: cut into windows of whole parts
+  const toEntry = (e) => ({ ...e, A: Float32Array.from(e.A), B: Float32Array.from(e.B) });
+  const SW = { name: "stacked", N: job.stacked.N, K: job.stacked.K, parts: job.stacked.parts, lora: job.stacked.entries.map(toEntry) };
+  out.windows = L.loraWindows(SW).map((w) => {
+    const st = L.stackLora(SW, w);
+    return { off: w.off, n: w.n, R: st.R, a: Array.from(st.a), b: Array.from(st.b) };
+  });
+  const big = { ...SW, lora: [toEntry({ ...job.stacked.entries[0], r: 260 })] };
+  try {
+    L.loraWindows(big);
+    out.rankError = null;
+  } catch (e) {
+    out.rankError = String(e.message);
+  }
   out.inspect = job.keys.map((ks) => L.inspectLoraKeys(ks));
   // loaders against fake registries built from { name, kind, N, K } linears (and stacked parts)
   out.loads = [];

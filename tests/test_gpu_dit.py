@@ -1,7 +1,13 @@
 """Full DiT pass through the Node host (run_dit.js -> N-API addon -> C ABI -> HIP) against the
 oracle's restatement of tools/reference.py DiT.forward, on seeded real-architecture weights
-(D=1536, 18 blocks, I=4096, int8 ConvRot block linears). Tolerance 1e-2 (max|d|/max|ref| and
-rel-L2) for the full 18-block pass.
+(D=1536, 18 blocks, I=4096, int8 ConvRot block linears).
+
+Two bounds on x0 (max|d|/max|ref| and rel-L2): the 1e-2 required of a full 18-block pass, and a
+regression bound near the measured error of the fp16-operand path (rel-L2 4.5e-4 to 6.2e-4,
+max 6e-4 to 1.3e-3), so that a tenfold loss of precision fails even though it would stay inside
+1e-2. The reference's own check harness compares its WebGPU x0 against fp32 PyTorch at a
+rel-L2 of 1e-4 (tools/check.js:89-98); that bound is for an fp32 engine, and fp16 MFMA operands
+cannot meet it (each rounding is 2^-11 relative).
 """
 
 import os
@@ -11,10 +17,19 @@ import pytest
 import torch
 
 import dit_fixture as F
-from conftest import assert_close
+from conftest import assert_close, rel_errors
 
 pytestmark = pytest.mark.gpu
 TOL_PASS = 1e-2
+REG_REL_L2 = 2e-3   # regression bound, about 3x the measured rel-L2
+REG_MAX = 4e-3      # regression bound, about 3x the measured max|d|/max|ref|
+
+
+def assert_pass(got, ref, what):
+    assert_close(got, ref, TOL_PASS, what)
+    max_rel, rel_l2 = rel_errors(got, ref)
+    assert rel_l2 <= REG_REL_L2 and max_rel <= REG_MAX, \
+        f"{what}: precision regression: max_rel {max_rel:.3e} (bound {REG_MAX}), rel_l2 {rel_l2:.3e} (bound {REG_REL_L2})"
 
 
 @pytest.fixture(scope="module")
@@ -42,7 +57,7 @@ def _run_case(weights_file, name, h, w, T, *, zero=(), path_drop=False, referenc
     rep = F.run_node(args)
     got = torch.from_numpy(np.fromfile(out, dtype=np.float32).reshape(64, h, w))
     ref = F.oracle_forward(tensors, inp, path_drop=path_drop)
-    assert_close(got, ref, TOL_PASS, f"DiT pass {name} ({h}x{w}, T={T})")
+    assert_pass(got, ref, f"DiT pass {name} ({h}x{w}, T={T})")
     return rep
 
 
@@ -90,7 +105,7 @@ def test_dit_pass_against_reference_golden(tmp_path):
         args = ["--weights", path, "--inputs", idir, "--out", out] + (["--path-drop"] if c["path_drop"] else [])
         F.run_node(args)
         got = torch.from_numpy(np.fromfile(out, dtype=np.float32).reshape(64, c["h"], c["w"]))
-        assert_close(got, torch.from_numpy(z[f"{c['name']}.x0"]), TOL_PASS, f"HIP pass vs reference golden {c['name']}")
+        assert_pass(got, torch.from_numpy(z[f"{c['name']}.x0"]), f"HIP pass vs reference golden {c['name']}")
 
 
 # ------------------------------------------------------------------ the benchmarked size (832x1216)
@@ -114,9 +129,9 @@ def full_size(weights_file):
 
 @pytest.mark.parametrize("mode", ["fused", "reference_ops", "path_drop"])
 def test_dit_pass_full_size(weights_file, full_size, mode):
-    """x0 of the 832x1216 pass against the oracle's fp32 DiT.forward at 1e-2 (the reference's
-    own harness checks this pass, tools/check.js:80-101): the fused driver, the reference's op
-    sequence, and the path-drop pass (blocks 2-15 skipped)."""
+    """x0 of the 832x1216 pass against the oracle's fp32 DiT.forward, at 1e-2 and at the
+    regression bound: the fused driver, the reference's op sequence, and the path-drop pass
+    (blocks 2-15 skipped)."""
     tensors, path, d = weights_file
     path_drop = mode == "path_drop"
     out = str(d / f"x0_full_{mode}.f32")
@@ -129,5 +144,5 @@ def test_dit_pass_full_size(weights_file, full_size, mode):
     got = torch.from_numpy(np.fromfile(out, dtype=np.float32).reshape(64, FULL_H, FULL_W))
     if path_drop not in full_size["ref"]:
         full_size["ref"][path_drop] = F.oracle_forward(tensors, full_size["inp"], path_drop=path_drop)
-    assert_close(got, full_size["ref"][path_drop], TOL_PASS,
-                 f"DiT pass 832x1216 {mode} ({FULL_H}x{FULL_W}, T={FULL_T}, one zero-weight token)")
+    assert_pass(got, full_size["ref"][path_drop],
+                f"DiT pass 832x1216 {mode} ({FULL_H}x{FULL_W}, T={FULL_T}, one zero-weight token)")

@@ -16,7 +16,7 @@ import torch
 import dit_fixture as F
 import gemma_fixture as G
 import oracle.nanosaur2_oracle as O
-from conftest import assert_close
+from conftest import assert_close, rel_errors
 from test_gpu_ops import TOL, dev, f16_as_float, gen, int8_weight, tiled_operand, untile_a
 
 pytestmark = pytest.mark.gpu
@@ -222,3 +222,35 @@ def test_gemma_encode_with_lora(lora_golden):
     assert rep["loras"][0]["matched"] == 3
     got = torch.from_numpy(np.fromfile(out, dtype=np.float32).reshape(len(ids), 640))
     assert_close(got, torch.from_numpy(z["te.out"]), TOL_PASS, "Gemma3 encoding with LoRA")
+
+
+@pytest.mark.parametrize("reference_ops", [False, True])
+def test_dit_pass_lora_on_every_joint_kv(tmp_path, reference_ops):
+    """A rank-32 LoRA on the kv_y of all 9 joint blocks (288 summed ranks). The fused pass runs
+    the 9 kv_y projections as one stacked weight, whose side paths then split into two row
+    windows (8 parts at rank 256, 1 at rank 32) and two launches; the reference op sequence
+    runs each kv_y with its own side path. Both against the oracle with the LoRA merged into
+    the weights (tools/reference.py:48-95), and closer to it than to the pass without the LoRA."""
+    from safetensors.torch import save_file
+
+    I = 256
+    tensors = F.make_weights(seed=5, I=I)
+    lora = F.make_lora(seed=14, I=I, b_std=0.3, targets=F.joint_kv_targets(32))
+    wpath, lpath = str(tmp_path / "dit.safetensors"), str(tmp_path / "kv_lora.safetensors")
+    F.save_weights(tensors, wpath)
+    save_file(lora, lpath)
+    inp = F.make_inputs(5, 6, 24, seed=15)
+    idir = str(tmp_path / "in")
+    F.write_inputs(inp, idir)
+    out = str(tmp_path / "x0.f32")
+    args = ["--weights", wpath, "--inputs", idir, "--out", out, "--lora", f"{lpath}:0.8"]
+    if reference_ops:
+        args.append("--reference-ops")
+    rep = F.run_node(args)
+    assert rep["loras"][0]["matched"] == 9 and rep["loras"][0]["skipped"] == 0
+    got = torch.from_numpy(np.fromfile(out, dtype=np.float32).reshape(64, 5, 6))
+    ref = F.oracle_forward(tensors, inp, loras=[(lora, 0.8)])
+    assert_close(got, ref, TOL_PASS, f"DiT pass, rank-32 LoRA on all joint kv_y (reference ops {reference_ops})")
+    _, without = rel_errors(F.oracle_forward(tensors, inp), ref)
+    _, err = rel_errors(got, ref)
+    assert err < 0.1 * without, f"the LoRA's effect (rel-L2 {without:.3e}) is not resolved: error {err:.3e}"

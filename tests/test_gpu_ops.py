@@ -243,7 +243,10 @@ def _tiled_linear_inputs(M, N, K, seed):
     (3952, 1536, 4096),   # MLP w3
     (256, 3072, 1536),    # kv_y on the text rows
     (256, 27648, 1536),   # the 9 joint blocks' kv_y stacked: one launch per pass
-    (2432, 6144, 1536),
+    (2432, 4608, 1536),   # the 2432-row linears on fp32 activations: fused QKV,
+    (2432, 1536, 1536),   # out projection,
+    (2432, 6144, 1536),   # MLP up,
+    (2432, 1536, 6144),   # MLP down (24 k-tiles)
     (1100, 576, 768),     # a ragged last row tile at more than 1024 rows
     (97, 320, 512),       # ragged rows, N not a multiple of 128
     (1, 64, 256),

@@ -55,7 +55,16 @@ def host(tmp_path_factory):
         {"name": "model.layers.6.mlp.gate_proj", "off": 0, "n": 2048},
         {"name": "model.layers.6.mlp.up_proj", "off": 2048, "n": 2048}]}
     o = {"name": "model.layers.16.self_attn.o_proj", "kind": "bf16", "N": 640, "K": 1024}
+    # nine stacked parts with a rank-32 LoRA each (the DiT's kv_y of the 9 joint blocks, scaled
+    # down): 288 > 256, so the side paths split into windows of whole parts
+    SN, SK, SP = 16, 32, 9
+    stacked = [(torch.randn(32, SK, generator=g), torch.randn(SN, 32, generator=g), 0.25 * (i + 1), SN * i, SN)
+               for i in range(SP)]
     job = {
+        "stacked": {"N": SN * SP, "K": SK,
+                    "parts": [{"name": f"blocks.{2 * i}.attn.kv_y", "off": SN * i, "n": SN} for i in range(SP)],
+                    "entries": [{"A": A.reshape(-1).tolist(), "B": B.reshape(-1).tolist(), "r": 32, "scale": s,
+                                 "off": off, "n": n} for A, B, s, off, n in stacked]},
         "f16": f16, "N": N, "K": K,
         "entries": [{"A": A.reshape(-1).tolist(), "B": B.reshape(-1).tolist(), "r": A.shape[0], "scale": s, "off": off, "n": n}
                     for A, B, s, off, n in ents],
@@ -70,7 +79,7 @@ def host(tmp_path_factory):
         json.dump(job, f)
     p = subprocess.run(["node", CHECKS, jf], capture_output=True, text=True, timeout=120)
     assert p.returncode == 0, p.stderr
-    return json.loads(p.stdout), None, f16, ents, lora_dit, te_lora
+    return json.loads(p.stdout), stacked, f16, ents, lora_dit, te_lora
 
 
 def test_f16_rounding_matches_numpy(host):
@@ -86,6 +95,28 @@ def test_stacked_side_path(host):
     assert out["stack"]["R"] == R == 32
     assert np.allclose(np.asarray(out["stack"]["a"]).reshape(R, 256), la.numpy(), atol=1e-6)
     assert np.allclose(np.asarray(out["stack"]["b"]).reshape(48, R), lb.numpy(), atol=1e-5)
+
+
+def test_stacked_parts_split_into_windows(host):
+    """Nine rank-32 LoRAs on the nine parts of a stacked weight: the first eight parts share one
+    side path (rank 256), the ninth gets its own; each window's operands equal the oracle's
+    pack_lora over the window's entries, and the output rows of all windows together equal one
+    unlimited stacked side path (no LoRA lost or doubled)."""
+    out, stacked, *_ = host
+    SN, SK = 16, 32
+    wins = out["windows"]
+    assert [(w["off"], w["n"], w["R"]) for w in wins] == [(0, 8 * SN, 256), (8 * SN, SN, 32)]
+    for w, ents in ((wins[0], stacked[:8]), (wins[1], stacked[8:])):
+        la, lb, R = O.pack_lora([(A, B, s, off - w["off"], n) for A, B, s, off, n in ents], w["n"], SK)
+        assert np.allclose(np.asarray(w["a"]).reshape(R, SK), la.numpy(), atol=1e-6)
+        assert np.allclose(np.asarray(w["b"]).reshape(w["n"], R), lb.numpy(), atol=1e-5)
+    x = torch.randn(5, SK, generator=torch.Generator().manual_seed(4), dtype=torch.float64)
+    la, lb, _ = O.pack_lora(stacked, SN * 9, SK)
+    whole = (x @ la.T) @ lb.T
+    parts = torch.cat([(x @ torch.tensor(w["a"], dtype=torch.float64).reshape(w["R"], SK).T)
+                       @ torch.tensor(w["b"], dtype=torch.float64).reshape(w["n"], w["R"]).T for w in wins], 1)
+    assert torch.allclose(parts, whole, rtol=1e-5, atol=1e-4)
+    assert "blocks.0.attn.kv_y" in out["rankError"] and "260" in out["rankError"]
 
 
 def test_inspect_keys(host):

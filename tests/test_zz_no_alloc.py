@@ -4,6 +4,10 @@ then a smaller DiT-style call on a packed qkv buffer with fused head norms -- pl
 views that are not 16-byte aligned (its packed queries also come from the fixed array), the
 oracle on the small calls, and the size check that refuses a problem beyond the array."""
 
+import os
+import subprocess
+import sys
+
 import pytest
 import torch
 
@@ -104,3 +108,52 @@ def test_noalloc_refuses_beyond_the_array(ns2lib):
     with pytest.raises(ns2.NS2Error, match="needs .* bytes of scratch"):
         ns2lib.attention(q, k, k, o, Lq=L, Lk=Lk, H=16, D=96, ldq=1536, ldk=1536, ldv=1536, ldo=1536, batch=B,
                          qBatch=L * 1536, kBatch=Lk * 1536, vBatch=Lk * 1536, oBatch=L * 1536, noalloc=True)
+
+
+_FRESH = r"""
+import sys, torch
+sys.path[:0] = [sys.argv[1], sys.argv[2]]
+import ns2
+lib = ns2.load(0)
+lib.set_stream(torch.cuda.current_stream().cuda_stream)
+L, T, B = 76 * 52, 256, 2
+g = torch.Generator(device="cuda").manual_seed(3)
+q = torch.randn(B, L, 1536, device="cuda", generator=g)
+k = torch.randn(B, L + T, 1536, device="cuda", generator=g)
+o1 = torch.empty(B, L, 1536, device="cuda")
+o2 = torch.empty_like(o1)
+kw = dict(Lq=L, Lk=L + T, H=16, D=96, ldq=1536, ldk=1536, ldv=1536, ldo=1536, batch=B, qBatch=L * 1536,
+          kBatch=(L + T) * 1536, vBatch=(L + T) * 1536, oBatch=L * 1536)
+# a small call first, through the allocation-free entry too: the library's code objects are
+# loaded on its first kernel launch, which takes device memory of its own
+qs = torch.randn(1, 64, 1536, device="cuda", generator=g)
+os_ = torch.empty_like(qs)
+lib.attention(qs, qs, qs, os_, Lq=64, Lk=64, H=16, D=96, ldq=1536, ldk=1536, ldv=1536, ldo=1536, noalloc=True)
+torch.cuda.synchronize()
+free0 = torch.cuda.mem_get_info()[0]
+lib.attention(q, k, k, o1, noalloc=True, **kw)
+torch.cuda.synchronize()
+free1 = torch.cuda.mem_get_info()[0]
+lib.attention(q, k, k, o2, **kw)
+torch.cuda.synchronize()
+free2 = torch.cuda.mem_get_info()[0]
+print(free0, free1, free2, int(torch.equal(o1, o2)), flush=True)
+"""
+
+
+def test_noalloc_first_call_allocates_nothing():
+    """In a fresh process, where the library's workspace is still empty (only a small call
+    through ns2_attention_noalloc ran before, to load the code objects): the config-2 call
+    through ns2_attention_noalloc leaves the device's free memory unchanged, and the same call
+    through ns2_attention afterwards (which sizes its workspace for the packed K/V, ~52 MB)
+    lowers it, so the measurement would see an allocation. The two outputs are bit-identical."""
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    print("[noalloc] fresh process: noalloc first at 3952 x 4208 batch 2", flush=True)
+    p = subprocess.run([sys.executable, "-c", _FRESH, root, os.path.join(root, "nanosaur2-web_amd")],
+                       capture_output=True, text=True, timeout=300)
+    assert p.returncode == 0, p.stderr[-3000:]
+    free0, free1, free2, same = (int(t) for t in p.stdout.split()[-4:])
+    print(f"[noalloc] free bytes: before {free0}, after noalloc {free1}, after ns2_attention {free2}", flush=True)
+    assert free1 == free0, f"ns2_attention_noalloc changed free device memory by {free0 - free1} bytes"
+    assert free0 - free2 >= 32 << 20, "the allocating entry point's workspace did not show in free memory"
+    assert same == 1
