@@ -613,6 +613,10 @@ def main():
         "pass_tflop": flops / 1e12,
         "pass_tflops": (flops / (ms / 1e3) / 1e12) if ms else None,
         "pass_ms_wall": dit["ms_wall_median"] if dit else None,
+        # the same passes each queued behind a stream hold (every launch of the pass issued
+        # before the first one runs): the device time without the host's launch latency, as a
+        # pipelined sampler loop sees it; `value` keeps the unqueued time
+        "pass_ms_queued": dit.get("ms_device_queued_median") if dit else None,
         "pass_ms_host_to_host": dit["ms_host_to_host_median"] if dit else None,
         "weight_bytes": dit.get("weight_bytes") if dit else None,
         "joint_attention": attn,

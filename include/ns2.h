@@ -166,6 +166,19 @@ int ns2_tile_i8_weight_glu(const int8_t* W, int8_t* Wt, int N, int K);
 int ns2_linear_bf16(const float* A, int lda, const uint16_t* W, const float* bias,
                     const float* add, float* C, int M, int N, int K, int ldc, long long cOff,
                     float alpha, int act, int resid, const float* gate, long long gOff);
+/* The bf16 linear of ns2_linear_bf16 (gemm.js:98-118, ops.linear app/gpu/ops.js:46-66) on tiled
+ * operands, for many rows (the DiT's 3952-row patch embedder, SPRINT projection and final
+ * layer): At is the fp16 activation in the tiled layout of ns2_linear_i8_tiled (written by
+ * ns2_to_tiled_f16 or ns2_norm_mod_f16), Wt the weight re-tiled as fp16 by
+ * ns2_tile_bf16_weight. Epilogue as above without `add` (no row scale). N % 64 == 0,
+ * K % 64 == 0. The operands are the fp16 values the row-major kernel's loaders convert its
+ * fp32 activations and bf16 weights to. Additive to the reference interface. */
+int ns2_linear_f16w_tiled(const uint16_t* At, const uint16_t* Wt, const float* bias, float* C, int M, int N, int K,
+                          int ldc, long long cOff, float alpha, int act, int resid, const float* gate,
+                          long long gOff);
+/* Re-tile a bf16 weight [N, K] row-major into fp16 tiles Wt [N/64][K/64][8][64][8 halfs] for
+ * ns2_linear_f16w_tiled (round to nearest even; N % 64 == 0, K % 64 == 0). Done once at load. */
+int ns2_tile_bf16_weight(const uint16_t* W, uint16_t* Wt, int N, int K);
 
 /* ---- LoRA side path (ops.linear with W.lora, app/gpu/ops.js:50-87 loraDelta; app/lora.js) ---
  * The _lora variants compute the same linear plus the low-rank term
@@ -197,6 +210,9 @@ int ns2_linear_bf16_lora(const float* A, int lda, const uint16_t* W, const float
                          const float* add, float* C, int M, int N, int K, int ldc, long long cOff,
                          float alpha, int act, int resid, const float* gate, long long gOff,
                          const uint16_t* lora_a, const uint16_t* lora_b, int lora_r);
+int ns2_linear_f16w_tiled_lora(const uint16_t* At, const uint16_t* Wt, const float* bias, float* C, int M, int N,
+                               int K, int ldc, long long cOff, float alpha, int act, int resid, const float* gate,
+                               long long gOff, const uint16_t* lora_a, const uint16_t* lora_b, int lora_r);
 
 /* ---- attention without the fused kernel (ops.attention's materialized path, app/gpu/ops.js:
  *      211-241, softmaxShader) -----------------------------------------------------------
@@ -321,6 +337,17 @@ int ns2_norm_mod(const float* x, const float* mod, long long shiftOff, long long
 int ns2_norm_mod_rotate_f16(const float* x, const float* mod, long long shiftOff,
                             long long scaleOff, int rows, int cols, const float* weight,
                             float eps, uint16_t* y, int tiled);
+/* ns2_norm_mod without the rotation, written as fp16 (cols % 256 == 0, at most 4096): the
+ * input of a tiled fp16-weight linear (the DiT's final layer, app/models/nanosaur2.js:252-253),
+ * row-major or tiled as in ns2_norm_mod_rotate_f16. Additive to the reference interface. */
+int ns2_norm_mod_f16(const float* x, const float* mod, long long shiftOff, long long scaleOff, int rows, int cols,
+                     const float* weight, float eps, uint16_t* y, int tiled);
+/* y = x - sub (sub may be NULL: y = x) as the tiled fp16 operand of ns2_linear_f16w_tiled
+ * ([ceil(rows/64)][cols/64][8][64][8], padding rows zero; cols % 64 == 0): the input of the
+ * DiT's patch embedder (the latent tokens) and of its SPRINT projection (the difference of the
+ * two residual streams, app/models/nanosaur2.js:236-243, elementwise sub + linear).
+ * Additive to the reference interface. */
+int ns2_to_tiled_f16(const float* x, int ldx, const float* sub, int ldsub, uint16_t* y, int rows, int cols);
 /* ops.glu + gluShader (app/gpu/ops.js:141-148, app/gpu/kernels.js:344-360):
  * y[r, j] = act(x[r, j]) * x[r, I + j] for x [rows, 2I]. */
 int ns2_glu(const float* x, float* y, int rows, int I, int act);

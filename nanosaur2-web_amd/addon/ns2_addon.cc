@@ -429,6 +429,48 @@ napi_value LinearI8Tiled(napi_env env, napi_callback_info info) {
   return check(env, c, ns2_linear_i8_tiled_lora(At, Wt, scale, bias, C, M, N, K, ldc, cOff, alpha, act, resid, gate, gOff, la, lb, lr));
 }
 
+// tileBf16Weight(W, Wt, N, K)
+napi_value TileBf16Weight(napi_env env, napi_callback_info info) {
+  ARGS(4);
+  auto W = (const uint16_t*)c.ptr(0);
+  auto Wt = (uint16_t*)c.ptr(1);
+  int N = c.i32(2), K = c.i32(3);
+  return check(env, c, c.failed ? 0 : ns2_tile_bf16_weight(W, Wt, N, K));
+}
+
+// linearF16wTiled(At, Wt, bias, C, M, N, K, ldc, cOff, alpha, act, resid, gate, gOff[, loraA, loraB, loraR])
+napi_value LinearF16wTiled(napi_env env, napi_callback_info info) {
+  ARGS(17);
+  auto At = (const uint16_t*)c.ptr(0);
+  auto Wt = (const uint16_t*)c.ptr(1);
+  auto bias = (const float*)c.ptr(2);
+  auto C = (float*)c.ptr(3);
+  int M = c.i32(4), N = c.i32(5), K = c.i32(6), ldc = c.i32(7);
+  long long cOff = c.i64(8);
+  float alpha = c.f32(9);
+  int act = c.i32(10), resid = c.i32(11);
+  auto gate = (const float*)c.ptr(12);
+  long long gOff = c.i64(13);
+  auto la = (const uint16_t*)c.ptr(14);
+  auto lb = (const uint16_t*)c.ptr(15);
+  int lr = c.type(16) == napi_number ? c.i32(16) : 0;
+  if (c.failed) return nullptr;
+  return check(env, c, ns2_linear_f16w_tiled_lora(At, Wt, bias, C, M, N, K, ldc, cOff, alpha, act, resid, gate, gOff,
+                                                  la, lb, lr));
+}
+
+// toTiledF16(x, ldx, sub, ldsub, y, rows, cols)
+napi_value ToTiledF16(napi_env env, napi_callback_info info) {
+  ARGS(7);
+  auto x = (const float*)c.ptr(0);
+  int ldx = c.i32(1);
+  auto sub = (const float*)c.ptr(2);
+  int ldsub = c.i32(3);
+  auto y = (uint16_t*)c.ptr(4);
+  int rows = c.i32(5), cols = c.i32(6);
+  return check(env, c, c.failed ? 0 : ns2_to_tiled_f16(x, ldx, sub, ldsub, y, rows, cols));
+}
+
 // linearI8(A, aFmt, lda, W, scale, bias, add, C, M, N, K, ldc, cOff, alpha, act, resid, gate, gOff[, loraA, loraB, loraR])
 napi_value LinearI8(napi_env env, napi_callback_info info) {
   ARGS(21);
@@ -661,6 +703,21 @@ napi_value NormModT(napi_env env, napi_callback_info info) {
   return check(env, c, rc);
 }
 
+// normModF16(x, mod, shiftOff, scaleOff, rows, cols, weight, eps, y, tiled)
+napi_value NormModF16(napi_env env, napi_callback_info info) {
+  ARGS(10);
+  auto x = (const float*)c.ptr(0);
+  auto mod = (const float*)c.ptr(1);
+  long long sh = c.i64(2), sc = c.i64(3);
+  int rows = c.i32(4), cols = c.i32(5);
+  auto w = (const float*)c.ptr(6);
+  float eps = c.f32(7);
+  auto y = (uint16_t*)c.ptr(8);
+  int tiled = c.i32(9);
+  if (c.failed) return nullptr;
+  return check(env, c, ns2_norm_mod_f16(x, mod, sh, sc, rows, cols, w, eps, y, tiled));
+}
+
 // glu(x, y, rows, I, act) / gluRotateF16(x, y, rows, I, act, tiled)
 template <bool ROT>
 napi_value GluT(napi_env env, napi_callback_info info) {
@@ -819,6 +876,8 @@ napi_value Module(napi_env env, napi_value exports) {
       {"profileReport", ProfileReport}, {"hadamard256", Hadamard256}, {"rotateF16", RotateF16},
       {"tileI8Weight", TileI8Weight}, {"linearI8Tiled", LinearI8Tiled},
       {"tileI8WeightGlu", TileI8WeightGlu}, {"linearI8GluRotTiled", LinearI8GluRotTiled},
+      {"tileBf16Weight", TileBf16Weight}, {"linearF16wTiled", LinearF16wTiled}, {"toTiledF16", ToTiledF16},
+      {"normModF16", NormModF16},
       {"linearI8", LinearI8}, {"linearBf16", LinearBf16}, {"attention", Attention},
       {"attentionRows", AttentionRows}, {"attentionText", AttentionText},
       {"linearI8TiledVpack", LinearI8TiledVpack}, {"attentionVpackBytes", AttentionVpackBytes},

@@ -7,12 +7,17 @@
 //   W (int8 ConvRot weights), re-tiled once after upload (ns2_tile_i8_weight), each byte
 //   stored biased as u = w + 128:
 //     Wt[N/64][K/64][8 k-chunks][64 rows][8 bytes]            (4 KB per 64x64 tile)
+//   or W (bf16 weights of the plain linears), re-tiled once as fp16 (ns2_tile_bf16_weight) in
+//   the layout of A:
+//     Wt[N/64][K/64][8 k-chunks][64 rows][8 halfs]            (8 KB per 64x64 tile)
 // Tiles move into LDS as 1 KB blocks with direct global->LDS copies (no registers, no LDS
 // stores) into a ring of LDS stages, and the MFMA fragment reads are conflict-free: the 32
 // lanes of a half-wave read 32 consecutive 16-byte (A) or 8-byte (W) rows. The int8
 // weights are decoded to fp16 as they are read from LDS into the MFMA B operand (exact:
 // half(0x6400 | u) - 1152 = w for |w| <= 128), and the per-output-row scale is applied in
 // the epilogue, in the reference's order (app/gpu/gemm.js:159-164).
+#include <type_traits>
+
 #include "ns2_common.h"
 
 using namespace ns2dev;
@@ -142,7 +147,7 @@ __device__ __forceinline__ void store_plain(const TGemmArgs& p, const float16_t 
   for (int j = 0; j < TN; ++j) {
     const int n = nb + 32 * j + lq;
     if (n >= p.N) continue;
-    const float rs = p.scale[n];
+    const float rs = p.scale ? p.scale[n] : 1.0f;  // no per-row scale on fp16 weights
     const float bi = p.bias ? p.bias[n] : 0.0f;
     const float gt = RM == 2 ? p.gate[p.gOff + n] : 1.0f;
     float* cj = p.C + p.cOff + (long long)mb * p.ldc + n;
@@ -192,7 +197,7 @@ __device__ __forceinline__ void store_vpack(const TGemmArgs& p, const float16_t 
 #pragma unroll
   for (int j = 0; j < TN; ++j) {
     const int n = nb + 32 * j + lq;
-    const float rs = p.scale[n];
+    const float rs = p.scale ? p.scale[n] : 1.0f;
     const float bi = p.bias ? p.bias[n] : 0.0f;
     const int c = n - p.vcol0, h = c / p.vD, dd = c % p.vD;
 #pragma unroll
@@ -240,6 +245,8 @@ __device__ __forceinline__ void store_vpack(const TGemmArgs& p, const float16_t 
 // (ns2_tile_i8_weight_glu), so the 64 columns of a wave hold 32 columns of each GLU half; the
 // block's 512 columns give 256 consecutive outputs act(h1) * h2, one rotation group, which is
 // rotated and written to Y as the tiled fp16 operand of the next int8 linear.
+// WF16: fp16 weight tiles (the plain bf16 linears, re-tiled as fp16; no per-row scale unless
+// given): 8 KB per 64x64 weight tile, read straight into the MFMA B operand.
 // Waves per SIMD that a launch with the LoRA term keeps: the occupancy of the plain kernel of
 // the same shape (left free, the compiler spends a few more registers on the LoRA variants and
 // they lose a resident block: 128 -> 140 for the GLU launch).
@@ -251,21 +258,24 @@ constexpr int lora_waves_per_eu() {
   return 1;
 }
 
-template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int EPI, int ACT, int RM, bool LORA>
+template <int BM, int BN, int WAVES_M, int WAVES_N, int STAGES, int EPI, int ACT, int RM, bool LORA, bool WF16 = false>
 __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) __attribute__((amdgpu_waves_per_eu(lora_waves_per_eu<BM, BN, RM, LORA>())))
 void gemm_tiled_kernel(TGemmArgs p) {
   constexpr int NW = WAVES_M * WAVES_N;
   constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
   constexpr int TM = WTM / 32, TN = WTN / 32;
-  constexpr int A_BLOCKS = BM / 64 * 8, W_BLOCKS = BN / 64 * 4;  // 1 KB blocks per stage
+  constexpr int WCH = WF16 ? 8 : 4;  // 1 KB blocks per 64 weight rows of a k-tile
+  constexpr int WB = WF16 ? 2 : 1;   // bytes per weight element
+  constexpr int A_BLOCKS = BM / 64 * 8, W_BLOCKS = BN / 64 * WCH;  // 1 KB blocks per stage
   constexpr int BLOCKS = A_BLOCKS + W_BLOCKS;
   constexpr int PER_WAVE = BLOCKS / NW;
   static_assert(BM % 64 == 0 && BN % 64 == 0 && WTM % 32 == 0 && WTN % 32 == 0, "tile shape");
   static_assert(BLOCKS % NW == 0, "copies must split evenly over the waves");
 
   static_assert(STAGES == 2 || STAGES == 3, "two or three LDS stages");
+  static_assert(!WF16 || EPI == 0, "fp16 weights take the plain epilogue");
   __shared__ __attribute__((aligned(16))) half_t as[STAGES][BM * 64];
-  __shared__ __attribute__((aligned(16))) uint8_t ws[STAGES][BN * 64];
+  __shared__ __attribute__((aligned(16))) uint8_t ws[STAGES][BN * 64 * WB];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -280,7 +290,7 @@ void gemm_tiled_kernel(TGemmArgs p) {
   const int kt0 = p.part ? (int)blockIdx.y * p.ksplit : 0;
   const int kblocks = p.part ? (p.K / 64 - kt0 < p.ksplit ? p.K / 64 - kt0 : p.ksplit) : p.K / 64;
   const int kall = p.K / 64;
-  // Stage image: A blocks (8 k-chunks of 1 KB per 64-row block), then W blocks (4 per 64-row
+  // Stage image: A blocks (8 k-chunks of 1 KB per 64-row block), then W blocks (WCH per 64-row
   // block). Block ids past the last real 64-row block re-read the last one (their rows are
   // dropped). The per-wave sources and destinations are fixed up front; a k-tile adds its offset.
   const char* g_src[PER_WAVE];
@@ -301,13 +311,13 @@ void gemm_tiled_kernel(TGemmArgs p) {
         l_step[i] = BM * 64 * 2;
       } else {
         const int jw = j - A_BLOCKS;
-        const int nbi = jw / 4, c = jw % 4;
+        const int nbi = jw / WCH, c = jw % WCH;
         int nb = n0 / 64 + nbi;
         nb = nb < p.nblocks ? nb : p.nblocks - 1;
-        g_src[i] = reinterpret_cast<const char*>(p.Wt) + ((long long)nb * kall * 4 + (long long)kt0 * 4 + c) * 1024;
+        g_src[i] = reinterpret_cast<const char*>(p.Wt) + ((long long)nb * kall * WCH + (long long)kt0 * WCH + c) * 1024;
         l_dst[i] = ws_base + jw * 1024;
-        g_step[i] = 4 * 1024;
-        l_step[i] = BN * 64;
+        g_step[i] = WCH * 1024;
+        l_step[i] = BN * 64 * WB;
       }
     }
   }
@@ -337,16 +347,22 @@ void gemm_tiled_kernel(TGemmArgs p) {
   if (STAGES == 3 && kblocks > 1) dma(1, 1);
 
   // fragments of k-step s (16 k) of a stage: A rows wm*WTM + 32i + lq, k 16s + 8hi .. +7 (chunk
-  // 2s + hi); W columns wn*WTN + 32j + lq, the same k (8-byte chunk 2s + hi)
+  // 2s + hi); W columns wn*WTN + 32j + lq, the same k (8-byte chunk 2s + hi, or 16-byte chunk for
+  // fp16 weights, read as the B operand itself)
   auto read_a = [&](int st, int s, int i) {
     const int row = wm * WTM + 32 * i;
     const int mbi = row / 64, r0 = row % 64;
     return *reinterpret_cast<const half8_t*>(&as[st][((mbi * 8 + 2 * s + hi) * 64 + r0 + lq) * 8]);
   };
+  using WRaw = std::conditional_t<WF16, half8_t, uint2>;
   auto read_w = [&](int st, int s, int j) {
     const int col = wn * WTN + 32 * j;
     const int nbi = col / 64, c0 = col % 64;
-    return *reinterpret_cast<const uint2*>(&ws[st][((nbi * 8 + 2 * s + hi) * 64 + c0 + lq) * 8]);
+    return *reinterpret_cast<const WRaw*>(&ws[st][((nbi * 8 + 2 * s + hi) * 64 + c0 + lq) * 8 * WB]);
+  };
+  auto decode = [&](const WRaw& w) {
+    if constexpr (WF16) return w;
+    else return u8x8_to_h8(w);
   };
 
   for (int kt = 0; kt < kblocks; ++kt) {
@@ -363,7 +379,7 @@ void gemm_tiled_kernel(TGemmArgs p) {
     // one step ahead, behind the MFMAs; scheduling barriers pin the order (the default
     // scheduler would put every read right before its use to save registers)
     half8_t a[3][TM], b[2][TN];
-    uint2 w[3][TN];
+    WRaw w[3][TN];
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
 #pragma unroll
@@ -372,7 +388,7 @@ void gemm_tiled_kernel(TGemmArgs p) {
       for (int j = 0; j < TN; ++j) w[s][j] = read_w(st, s, j);
     }
 #pragma unroll
-    for (int j = 0; j < TN; ++j) b[0][j] = u8x8_to_h8(w[0][j]);
+    for (int j = 0; j < TN; ++j) b[0][j] = decode(w[0][j]);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       if (s + 2 < 4) {
@@ -389,7 +405,7 @@ void gemm_tiled_kernel(TGemmArgs p) {
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[s % 3][i], b[s & 1][j], acc[i][j], 0, 0, 0);
       if (s + 1 < 4) {
 #pragma unroll
-        for (int j = 0; j < TN; ++j) b[(s + 1) & 1][j] = u8x8_to_h8(w[(s + 1) % 3][j]);
+        for (int j = 0; j < TN; ++j) b[(s + 1) & 1][j] = decode(w[(s + 1) % 3][j]);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -513,7 +529,7 @@ __global__ __launch_bounds__(256) void tiled_splitk_reduce_kernel(TGemmArgs p, i
   for (int z = 0; z < splits; ++z) acc += p.part[z * mn + idx];
   const int m = (int)(idx / p.N), n = (int)(idx % p.N);
   float v = acc * p.alpha;
-  v *= p.scale[n];
+  if (p.scale) v *= p.scale[n];
   v += p.bias ? p.bias[n] : 0.0f;
   if (p.lr) v += lora_dot(p.lt, p.lb, p.lr, m, n);
   if (p.act == NS2_ACT_SILU) v = silu(v);
@@ -547,10 +563,32 @@ __global__ __launch_bounds__(256) void tile_w_kernel(const int8_t* __restrict__ 
   *reinterpret_cast<uint2*>(Wt + i * 8) = v;
 }
 
+// W [N, K] row-major bf16 -> Wt tiles [N/64][K/64][8 k-chunks of 8][64 rows][8 halfs] of fp16
+// (round to nearest even, as the row-major kernel's loader converts them); one thread per
+// 16-byte chunk.
+__global__ __launch_bounds__(256) void tile_w16_kernel(const uint16_t* __restrict__ W, uint16_t* __restrict__ Wt,
+                                                        int N, int K) {
+  const long long i = (long long)blockIdx.x * 256 + threadIdx.x;  // output chunk index
+  const long long chunks = (long long)N * K / 8;
+  if (i >= chunks) return;
+  const int row = (int)(i % 64);
+  const int c = (int)((i / 64) % 8);
+  const long long rest = i / 512;  // nb * (K/64) + kb
+  const int kb = (int)(rest % (K / 64));
+  const int nb = (int)(rest / (K / 64));
+  const uint4 v = *reinterpret_cast<const uint4*>(W + (long long)(nb * 64 + row) * K + kb * 64 + c * 8);
+  const uint32_t in[4] = {v.x, v.y, v.z, v.w};
+  uint32_t out[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    out[j] = pack_half2(__builtin_bit_cast(float, in[j] << 16), __builtin_bit_cast(float, in[j] & 0xffff0000u));
+  *reinterpret_cast<uint4*>(Wt + i * 8) = make_uint4(out[0], out[1], out[2], out[3]);
+}
+
 // Weight bytes per column band of the tile order: half of an XCD's 4 MB L2.
 constexpr long long kBandBytes = 2ll << 20;
 
-template <int BM, int BN, int WM, int WN, int STAGES = 2, int EPI = 0>
+template <int BM, int BN, int WM, int WN, int STAGES = 2, int EPI = 0, bool WF16 = false>
 int launch_tiled(TGemmArgs p, int splits = 1) {
   p.tiles_m = (p.M + BM - 1) / BM;
   p.tiles_n = (p.N + BN - 1) / BN;
@@ -561,7 +599,7 @@ int launch_tiled(TGemmArgs p, int splits = 1) {
   // with a few row tiles read each weight tile about once whatever the order.
   p.bands = 1;
   if (p.tiles_m >= 8) {
-    const double a_bytes = (double)p.tiles_m * BM * p.K * 2, w_bytes = (double)p.N * p.K;
+    const double a_bytes = (double)p.tiles_m * BM * p.K * 2, w_bytes = (double)p.N * p.K * (WF16 ? 2 : 1);
     double best = 0;
     for (int b = 1; b <= 8 && b <= p.tiles_n; b *= 2) {
       const double slice = w_bytes / b;
@@ -580,11 +618,11 @@ int launch_tiled(TGemmArgs p, int splits = 1) {
   do {                                                                                                \
     if constexpr (BM * BN < 256 * 256) {                                                              \
       if (p.lr) {                                                                                     \
-        gemm_tiled_kernel<BM, BN, WM, WN, STAGES, EPI, A, R, true><<<grid, block, 0, s>>>(p);         \
+        gemm_tiled_kernel<BM, BN, WM, WN, STAGES, EPI, A, R, true, WF16><<<grid, block, 0, s>>>(p);   \
         break;                                                                                        \
       }                                                                                               \
     }                                                                                                 \
-    gemm_tiled_kernel<BM, BN, WM, WN, STAGES, EPI, A, R, false><<<grid, block, 0, s>>>(p);            \
+    gemm_tiled_kernel<BM, BN, WM, WN, STAGES, EPI, A, R, false, WF16><<<grid, block, 0, s>>>(p);      \
   } while (0)
   if constexpr (EPI == 1) {
     if (p.act == NS2_ACT_SILU) NS2_TILED(NS2_ACT_SILU, 0);
@@ -654,19 +692,22 @@ inline bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 namespace {
 
-int linear_i8_tiled(const char* fn, const uint16_t* At, const int8_t* Wt, const float* scale, const float* bias,
-                    float* C, int M, int N, int K, int ldc, long long cOff, float alpha, int act, int resid,
-                    const float* gate, long long gOff, const uint16_t* lora_a, const uint16_t* lora_b, int lora_r,
-                    uint16_t* vpk = nullptr, int vcol0 = 0, int vD = 0, int vtiles = 0) {
+// wf16: Wt holds fp16 weight tiles (ns2_tile_bf16_weight) and scale may be null; otherwise
+// int8 ConvRot tiles with their per-row scales (K a whole number of rotation groups).
+int linear_tiled(const char* fn, bool wf16, const uint16_t* At, const void* Wt, const float* scale, const float* bias,
+                 float* C, int M, int N, int K, int ldc, long long cOff, float alpha, int act, int resid,
+                 const float* gate, long long gOff, const uint16_t* lora_a, const uint16_t* lora_b, int lora_r,
+                 uint16_t* vpk = nullptr, int vcol0 = 0, int vD = 0, int vtiles = 0) {
   NS2_READY();
   if (M == 0) return NS2_OK;
-  NS2_REQUIRE(At && Wt && scale && C, "%s: null At, Wt, scale or C", fn);
-  NS2_REQUIRE(M > 0 && N > 0 && N % 64 == 0 && K > 0 && K % 256 == 0,
-              "%s: M=%d N=%d K=%d (N %% 64 == 0, K %% 256 == 0 required)", fn, M, N, K);
+  NS2_REQUIRE(At && Wt && (scale || wf16) && C, "%s: null At, Wt, scale or C", fn);
+  const int kmul = wf16 ? 64 : 256;
+  NS2_REQUIRE(M > 0 && N > 0 && N % 64 == 0 && K > 0 && K % kmul == 0,
+              "%s: M=%d N=%d K=%d (N %% 64 == 0, K %% %d == 0 required)", fn, M, N, K, kmul);
   NS2_REQUIRE(ldc >= N && cOff >= 0 && gOff >= 0, "%s: bad ldc/offsets", fn);
   NS2_REQUIRE(aligned16(At) && aligned16(Wt), "%s: operands must be 16-byte aligned", fn);
   NS2_REQUIRE(act >= NS2_ACT_NONE && act <= NS2_ACT_GELU_TANH, "%s: unknown act %d", fn, act);
-  TGemmArgs p{reinterpret_cast<const half_t*>(At), reinterpret_cast<const uint8_t*>(Wt), scale, bias, C, nullptr, gate,
+  TGemmArgs p{reinterpret_cast<const half_t*>(At), static_cast<const uint8_t*>(Wt), scale, bias, C, nullptr, gate,
               cOff, gOff, M, N, K, ldc, (M + 63) / 64, N / 64, 0, 0, alpha, act, resid};
   p.vpk = reinterpret_cast<half_t*>(vpk);
   p.vcol0 = vcol0;
@@ -678,7 +719,7 @@ int linear_i8_tiled(const char* fn, const uint16_t* At, const int8_t* Wt, const 
     p.lb = reinterpret_cast<const half_t*>(lora_b);
     p.lr = lora_r;
   }
-  ns2::ProfScope prof_("gemm_i8_tiled");
+  ns2::ProfScope prof_(wf16 ? "gemm_f16_tiled" : "gemm_i8_tiled");
   // the 256x256 tiles (16 waves, 128 registers each) have no room for the LoRA term's registers
   int cfg = pick_config(M, N);
   if (lora_r && cfg == 0) cfg = 1;
@@ -699,6 +740,13 @@ int linear_i8_tiled(const char* fn, const uint16_t* At, const int8_t* Wt, const 
       splits = (kt + p.ksplit - 1) / p.ksplit;
       p.part = static_cast<float*>(ns2::workspace(5, (size_t)splits * M * N * sizeof(float)));
       if (!p.part) return ns2::set_error(NS2_ERR_OOM, "%s: split-K workspace allocation failed", fn);
+    }
+  }
+  if (wf16) {
+    switch (cfg) {
+      case 0: return launch_tiled<256, 256, 4, 4, 2, 0, true>(p);
+      case 1: return launch_tiled<64, 128, 1, 4, 2, 0, true>(p, splits);
+      default: return launch_tiled<64, 64, 2, 2, 2, 0, true>(p, splits);
     }
   }
   switch (cfg) {
@@ -766,7 +814,7 @@ int ns2_linear_i8_glu_rot_tiled_lora(const uint16_t* At, const int8_t* Wt, const
 int ns2_linear_i8_tiled(const uint16_t* At, const int8_t* Wt, const float* scale, const float* bias,
                         float* C, int M, int N, int K, int ldc, long long cOff, float alpha, int act,
                         int resid, const float* gate, long long gOff) {
-  return linear_i8_tiled("ns2_linear_i8_tiled", At, Wt, scale, bias, C, M, N, K, ldc, cOff, alpha, act, resid, gate,
+  return linear_tiled("ns2_linear_i8_tiled", false, At, Wt, scale, bias, C, M, N, K, ldc, cOff, alpha, act, resid, gate,
                          gOff, nullptr, nullptr, 0);
 }
 
@@ -774,8 +822,33 @@ int ns2_linear_i8_tiled_lora(const uint16_t* At, const int8_t* Wt, const float* 
                              float* C, int M, int N, int K, int ldc, long long cOff, float alpha, int act,
                              int resid, const float* gate, long long gOff, const uint16_t* lora_a,
                              const uint16_t* lora_b, int lora_r) {
-  return linear_i8_tiled("ns2_linear_i8_tiled_lora", At, Wt, scale, bias, C, M, N, K, ldc, cOff, alpha, act, resid,
+  return linear_tiled("ns2_linear_i8_tiled_lora", false, At, Wt, scale, bias, C, M, N, K, ldc, cOff, alpha, act, resid,
                          gate, gOff, lora_a, lora_b, lora_r);
+}
+
+int ns2_tile_bf16_weight(const uint16_t* W, uint16_t* Wt, int N, int K) {
+  NS2_READY();
+  NS2_REQUIRE(W && Wt && aligned16(W) && aligned16(Wt), "ns2_tile_bf16_weight: null or unaligned buffer");
+  NS2_REQUIRE(N > 0 && K > 0 && N % 64 == 0 && K % 64 == 0,
+              "ns2_tile_bf16_weight: N=%d and K=%d must be multiples of 64", N, K);
+  const long long chunks = (long long)N * K / 8;
+  ns2::ProfScope prof_("tile_bf16_weight");
+  tile_w16_kernel<<<(unsigned)((chunks + 255) / 256), 256, 0, ns2::stream()>>>(W, Wt, N, K);
+  NS2_LAUNCHED("tile_bf16_weight");
+  return NS2_OK;
+}
+
+int ns2_linear_f16w_tiled(const uint16_t* At, const uint16_t* Wt, const float* bias, float* C, int M, int N, int K,
+                          int ldc, long long cOff, float alpha, int act, int resid, const float* gate, long long gOff) {
+  return linear_tiled("ns2_linear_f16w_tiled", true, At, Wt, nullptr, bias, C, M, N, K, ldc, cOff, alpha, act, resid,
+                      gate, gOff, nullptr, nullptr, 0);
+}
+
+int ns2_linear_f16w_tiled_lora(const uint16_t* At, const uint16_t* Wt, const float* bias, float* C, int M, int N,
+                               int K, int ldc, long long cOff, float alpha, int act, int resid, const float* gate,
+                               long long gOff, const uint16_t* lora_a, const uint16_t* lora_b, int lora_r) {
+  return linear_tiled("ns2_linear_f16w_tiled_lora", true, At, Wt, nullptr, bias, C, M, N, K, ldc, cOff, alpha, act,
+                      resid, gate, gOff, lora_a, lora_b, lora_r);
 }
 
 int ns2_linear_i8_tiled_vpack(const uint16_t* At, const int8_t* Wt, const float* scale, const float* bias,
@@ -790,7 +863,7 @@ int ns2_linear_i8_tiled_vpack(const uint16_t* At, const int8_t* Wt, const float*
               "(vcol0=%d H=%d D=%d N=%d; vcol0 %% 64 == 0, D %% 32 == 0)", vcol0, H, D, N);
   NS2_REQUIRE(M % 16 == 0 && M <= Lk, "ns2_linear_i8_tiled_vpack: M=%d must be a multiple of 16 and at most Lk=%d",
               M, Lk);
-  return linear_i8_tiled("ns2_linear_i8_tiled_vpack", At, Wt, scale, bias, C, M, N, K, ldc, cOff, alpha, act, 0,
+  return linear_tiled("ns2_linear_i8_tiled_vpack", false, At, Wt, scale, bias, C, M, N, K, ldc, cOff, alpha, act, 0,
                          nullptr, 0, lora_a, lora_b, lora_r, vpk, vcol0, D, (Lk + 63) / 64);
 }
 

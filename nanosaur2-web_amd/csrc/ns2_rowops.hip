@@ -137,7 +137,8 @@ struct RotRowsArgs {
   int ldy, rows, tiled;
 };
 
-// [rows, 256 G] fp32 -> (normMod ->) rotated fp16, one wave per row and 8 rows per block.
+// [rows, 256 G] fp32 -> (normMod ->) rotated fp16, one wave per row and 8 rows per block
+// (ROT false: the fp16 operand of a plain fp16-weight linear, not rotated).
 // Each lane loads its 4 values of every group before any arithmetic (the whole row is in
 // flight at once), the row statistics are wave reductions, and the 8 rows of a block fill
 // whole 128-byte lines of the tiled layout (rows 8q..8q+7 of a k-chunk are adjacent 16-byte
@@ -146,7 +147,7 @@ struct RotRowsArgs {
 // any) in LDS once, in lane order (slot 64g + l holds the 4 columns lane l uses in group g, so
 // the waves' 16-byte reads are conflict-free), instead of every row's wave loading them from
 // L1: at 8 rows per block that is 3x the row's own bytes through L1 otherwise.
-template <int G, bool NORM>
+template <int G, bool NORM, bool ROT = true>
 __global__ __launch_bounds__(512) void rot_rows_kernel(RotRowsArgs a) {
   const int row = blockIdx.x * 8 + (threadIdx.x >> 6);
   constexpr int cols = 256 * G;
@@ -217,7 +218,7 @@ __global__ __launch_bounds__(512) void rot_rows_kernel(RotRowsArgs a) {
         v[g][2] = v[g][2] * r * s1.z + sh.z, v[g][3] = v[g][3] * r * s1.w + sh.w;
       }
     }
-    fwht256_mfma(v[g], h);
+    if (ROT) fwht256_mfma(v[g], h);
     if (!a.tiled || !TSTAGE) {
       if (active) store4_f16(a.y, row, g * 256 + lo, a.ldy, cols, a.tiled, v[g]);
     }
@@ -242,22 +243,56 @@ __global__ __launch_bounds__(512) void rot_rows_kernel(RotRowsArgs a) {
   }
 }
 
-template <bool NORM>
+template <bool NORM, bool ROT = true>
 void launch_rot_rows(const RotRowsArgs& a, int groups) {
   const dim3 grid((a.rows + 7) / 8), block(512);
   hipStream_t s = ns2::stream();
   switch (groups) {
 #define NS2_ROT_CASE(G) \
-    case G: rot_rows_kernel<G, NORM><<<grid, block, 0, s>>>(a); break;
+    case G: rot_rows_kernel<G, NORM, ROT><<<grid, block, 0, s>>>(a); break;
     NS2_ROT_CASE(1) NS2_ROT_CASE(2) NS2_ROT_CASE(3) NS2_ROT_CASE(4) NS2_ROT_CASE(5) NS2_ROT_CASE(6)
     NS2_ROT_CASE(7) NS2_ROT_CASE(8) NS2_ROT_CASE(9) NS2_ROT_CASE(10) NS2_ROT_CASE(11) NS2_ROT_CASE(12)
     NS2_ROT_CASE(13) NS2_ROT_CASE(14) NS2_ROT_CASE(15) NS2_ROT_CASE(16)
 #undef NS2_ROT_CASE
     // rotation only, rows up to 6144 columns (the widest block-linear input)
-    case 20: if constexpr (!NORM) rot_rows_kernel<20, NORM><<<grid, block, 0, s>>>(a); break;
-    case 24: if constexpr (!NORM) rot_rows_kernel<24, NORM><<<grid, block, 0, s>>>(a); break;
+    case 20: if constexpr (!NORM && ROT) rot_rows_kernel<20, NORM><<<grid, block, 0, s>>>(a); break;
+    case 24: if constexpr (!NORM && ROT) rot_rows_kernel<24, NORM><<<grid, block, 0, s>>>(a); break;
     default: break;
   }
+}
+
+// ---- fp16 operands of the plain linears ------------------------------------------------------
+
+// y = x (- sub) as the tiled fp16 operand [ceil(rows/64)][cols/64][8][64][8] of a tiled linear;
+// rows past the last one, up to the 64-row padding, are written as zeros. Thread i writes the
+// 16-byte chunk i of the tiled image (consecutive threads: consecutive rows of one 8-column
+// chunk), so the stores are contiguous; the 4 waves of a block read the 4 quarters of each
+// 128-byte line of the rows they cover.
+__global__ __launch_bounds__(256) void to_tiled_f16_kernel(const float* __restrict__ x, int ldx,
+                                                            const float* __restrict__ sub, int lds,
+                                                            uint16_t* __restrict__ y, int rows, int cols) {
+  const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+  const int cpr = cols / 8;  // 8-column chunks per row
+  const long long total = (long long)(rows + 63) / 64 * 64 * cpr;
+  if (i >= total) return;
+  const int rr = (int)(i % 64);
+  const long long rest = i / 64;  // 64-row block * cpr + chunk
+  const int kc = (int)(rest % cpr);
+  const int m = (int)(rest / cpr) * 64 + rr;
+  uint4 o = make_uint4(0u, 0u, 0u, 0u);
+  if (m < rows) {
+    const float4 a0 = *reinterpret_cast<const float4*>(x + (long long)m * ldx + kc * 8);
+    const float4 a1 = *reinterpret_cast<const float4*>(x + (long long)m * ldx + kc * 8 + 4);
+    float v[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+    if (sub) {
+      const float4 b0 = *reinterpret_cast<const float4*>(sub + (long long)m * lds + kc * 8);
+      const float4 b1 = *reinterpret_cast<const float4*>(sub + (long long)m * lds + kc * 8 + 4);
+      v[0] -= b0.x, v[1] -= b0.y, v[2] -= b0.z, v[3] -= b0.w;
+      v[4] -= b1.x, v[5] -= b1.y, v[6] -= b1.z, v[7] -= b1.w;
+    }
+    o = make_uint4(pack_half2(v[0], v[1]), pack_half2(v[2], v[3]), pack_half2(v[4], v[5]), pack_half2(v[6], v[7]));
+  }
+  *reinterpret_cast<uint4*>(y + i * 8) = o;
 }
 
 // ---- headNorm -------------------------------------------------------------------------------
@@ -523,6 +558,37 @@ int ns2_norm_mod_rotate_f16(const float* x, const float* mod, long long shiftOff
   RotRowsArgs a{x, cols, mod, shiftOff, scaleOff, weight, eps, y, cols, rows, tiled};
   launch_rot_rows<true>(a, cols / 256);
   NS2_LAUNCHED("norm_mod_rotate_f16");
+  return NS2_OK;
+}
+
+int ns2_norm_mod_f16(const float* x, const float* mod, long long shiftOff, long long scaleOff, int rows, int cols,
+                     const float* weight, float eps, uint16_t* y, int tiled) {
+  NS2_READY();
+  if (rows <= 0) return NS2_OK;
+  NS2_REQUIRE(cols % 256 == 0 && cols >= 256 && cols <= 4096,
+              "ns2_norm_mod_f16: cols=%d must be a multiple of 256 in [256, 4096]", cols);
+  NS2_REQUIRE(x && mod && y && aligned16(x) && aligned8(y) && shiftOff % 4 == 0 && scaleOff % 4 == 0 &&
+                  aligned16(mod) && (!weight || aligned16(weight)),
+              "ns2_norm_mod_f16: null or unaligned buffer/offset");
+  ns2::ProfScope prof_("norm_mod_f16");
+  RotRowsArgs a{x, cols, mod, shiftOff, scaleOff, weight, eps, y, cols, rows, tiled};
+  launch_rot_rows<true, false>(a, cols / 256);
+  NS2_LAUNCHED("norm_mod_f16");
+  return NS2_OK;
+}
+
+int ns2_to_tiled_f16(const float* x, int ldx, const float* sub, int ldsub, uint16_t* y, int rows, int cols) {
+  NS2_READY();
+  if (rows <= 0) return NS2_OK;
+  NS2_REQUIRE(cols > 0 && cols % 64 == 0, "ns2_to_tiled_f16: cols=%d must be a multiple of 64", cols);
+  NS2_REQUIRE(ldx >= cols && ldx % 4 == 0 && (!sub || (ldsub >= cols && ldsub % 4 == 0)),
+              "ns2_to_tiled_f16: ldx=%d / ldsub=%d must be multiples of 4 and >= cols", ldx, ldsub);
+  NS2_REQUIRE(x && y && aligned16(x) && aligned16(y) && (!sub || aligned16(sub)),
+              "ns2_to_tiled_f16: null or unaligned buffer");
+  const long long chunks = (long long)(rows + 63) / 64 * 64 * (cols / 8);
+  ns2::ProfScope prof_("to_tiled_f16");
+  to_tiled_f16_kernel<<<(unsigned)((chunks + 255) / 256), 256, 0, ns2::stream()>>>(x, ldx, sub, ldsub, y, rows, cols);
+  NS2_LAUNCHED("to_tiled_f16");
   return NS2_OK;
 }
 

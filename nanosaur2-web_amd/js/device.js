@@ -219,7 +219,7 @@ export class GPU {
 
   // Issue one op; with the profiler on, bracket it with timing events.
   run(name, flops, launch) {
-    if (!this.profiler) return launch();
+    if (!this.profiler || this.profiler.paused) return launch();
     const [a, b] = this.profiler.next({ name, flops });
     native.eventRecord(a);
     const r = launch();
@@ -231,6 +231,7 @@ export class GPU {
 // Per-op GPU timings aggregated by name (app/gpu/device.js:234-288).
 class Profiler {
   constructor() {
+    this.paused = false;  // ops issued while paused are not timed
     this.pending = [];
     this.spare = [];
     this.stats = new Map();

@@ -100,6 +100,30 @@ export class Nanosaur2DiT {
         ops.tileWeight(gpu, m.kvAll);
         ops.dropRowMajor(m.kvAll);
       }
+      // the adaLN projections that share an input run as one GEMV over a stacked weight: the text
+      // blocks' (all from the timestep embedding), and the shared and final ones (both from the
+      // conditioning vector); the parts keep their module names (LoRA targets)
+      const gemv = (Ws) => Ws.length > 1 && Ws.every((W) => W.kind === "bf16" && W.K === Ws[0].K);
+      if (gemv(m.text.map((b) => b.ada))) {
+        m.textAda = concatLinears(gpu, m.text.map((b) => b.ada));
+        m.text.forEach((b, i) => {
+          b.adaSlot = m.textAda.parts[i].off;
+          b.ada = null;
+        });
+      }
+      if (gemv([m.sharedAda, m.finalAda])) {
+        m.condAda = concatLinears(gpu, [m.sharedAda, m.finalAda]);
+        m.sharedAda = null;
+        m.finalAda = null;
+      }
+      // the 3952-row bf16 linears (patch embedder, SPRINT projection, final layer) take tiled
+      // fp16 operands over their weights re-tiled as fp16
+      for (const W of [m.sEmbed, m.sprintOut, m.finalLinear]) {
+        if (W && ops.tileablePlain(W)) {
+          ops.tileWeight(gpu, W);
+          ops.dropRowMajor(W);
+        }
+      }
       for (const b of m.text.concat(m.blocks)) {
         for (const W of [b.qkv, b.kvY, b.proj, b.w3]) if (W && ops.tileable(W)) ops.tileWeight(gpu, W);
         // the image blocks' MLP runs its first linear fused with the GLU and the rotation for w3;
@@ -120,7 +144,7 @@ export class Nanosaur2DiT {
   // Every linear weight of the model (LoRA targets, lora.js linearRegistry).
   linears() {
     const top = [this.sEmbed, this.t1, this.t2, this.yEmbed, this.yPool, this.sharedAda, this.sprintOut,
-      this.finalAda, this.finalLinear];
+      this.finalAda, this.finalLinear, this.condAda, this.textAda];
     const text = this.text.flatMap((b) => [b.ada, b.qkv, b.proj, b.w12, b.w3]);
     const blocks = this.blocks.flatMap((b) => [b.qkv, b.kvY, b.proj, b.w12, b.w3]);
     return top.concat(text, blocks, [this.kvAll]).filter((W) => W);
@@ -298,8 +322,10 @@ export class Nanosaur2DiT {
     const gpu = this.gpu;
     const L = text.L;
     const txt = ops.elementwise(gpu, "copy", text.y);
+    // every text block's modulation at once from the stacked adaLN weight
+    const mods = this.textAda ? ops.linear(gpu, tc, this.textAda, { name: "dit.text.ada" }) : null;
     for (const b of this.text) {
-      const mod = ops.linear(gpu, tc, b.ada, { name: "dit.text.ada" });
+      const mod = mods ? ops.colView(mods, b.adaSlot, 6 * D) : ops.linear(gpu, tc, b.ada, { name: "dit.text.ada" });
       const qkv = gpu.empty([L, 3 * D]);
       this.qkvProj(txt, mod, b, qkv, "dit.text.qkv");
       const a = this.attend(qkv, L, L, b);
@@ -309,6 +335,7 @@ export class Nanosaur2DiT {
       this.mlp(txt, b, mod);
       mod.release();
     }
+    if (mods) mods.release();
     return txt;
   }
 
@@ -347,8 +374,10 @@ export class Nanosaur2DiT {
     tc.release();
     const cond = ops.elementwise(gpu, "silu", t);
     t.release();
-    const mod = ops.linear(gpu, cond, this.sharedAda, { name: "dit.shared_ada" });
-    const final = ops.linear(gpu, cond, this.finalAda, { name: "dit.final_ada" });
+    // the shared block modulation and the final layer's, from one stacked GEMV when stacked
+    const ada = this.condAda ? ops.linear(gpu, cond, this.condAda, { name: "dit.shared_ada" }) : null;
+    const mod = ada ? ops.colView(ada, 0, 6 * D) : ops.linear(gpu, cond, this.sharedAda, { name: "dit.shared_ada" });
+    const final = ada ? ops.colView(ada, 6 * D, 2 * D) : ops.linear(gpu, cond, this.finalAda, { name: "dit.final_ada" });
     cond.release();
     // every block's modulation mod + offset_i (app/models/nanosaur2.js:190) at once
     const modAll = this.offsets ? ops.addRows(gpu, mod, this.offsets) : null;
@@ -360,6 +389,7 @@ export class Nanosaur2DiT {
         if (kvText) kvText.release();
         mod.release();
         final.release();
+        if (ada) ada.release();
         if (modAll) modAll.release();
       },
     };
@@ -404,7 +434,14 @@ export class Nanosaur2DiT {
   async forwardTokens(tokens, h, w, text, sigma, { pathDrop = false, onBlock } = {}) {
     const gpu = this.gpu;
     const L = h * w;
-    const x = ops.linear(gpu, tokens, this.sEmbed, { name: "dit.s_embed" });
+    let x;
+    if (this.sEmbed.tbuf) {
+      const tt = ops.toTiled(gpu, tokens);
+      x = ops.linear(gpu, null, this.sEmbed, { xr: tt, name: "dit.s_embed" });
+      tt.release();
+    } else {
+      x = ops.linear(gpu, tokens, this.sEmbed, { name: "dit.s_embed" });
+    }
     const cs = this.rope(h, w);
     let c = null;
     let g = null;
@@ -420,10 +457,13 @@ export class Nanosaur2DiT {
       if (!pathDrop) {
         g = ops.elementwise(gpu, "copy", x);
         for (let i = SPRINT_F; i < BLOCKS - SPRINT_H; i++) await run(i, g);
-        const d = ops.elementwise(gpu, "sub", g, x);
+        // x += (g - x) W^T; with the tiled weight the difference is formed as its fp16 operand
+        const tiled = !!this.sprintOut.tbuf;
+        const d = tiled ? ops.toTiled(gpu, g, x) : ops.elementwise(gpu, "sub", g, x);
         g.release();
         g = null;
-        ops.linear(gpu, d, this.sprintOut, { out: x, resid: true, name: "dit.sprint_out" });
+        ops.linear(gpu, tiled ? null : d, this.sprintOut, { xr: tiled ? d : undefined, out: x, resid: true,
+          name: "dit.sprint_out" });
         d.release();
       }
       for (let i = BLOCKS - SPRINT_H; i < BLOCKS; i++) await run(i, x);
@@ -433,10 +473,11 @@ export class Nanosaur2DiT {
       x.release();
       throw e;
     }
-    const n = ops.normMod(gpu, x, c.final, 0, D, D);
+    const tiled = !!this.finalLinear.tbuf;
+    const n = tiled ? ops.normModTiled(gpu, x, c.final, 0, D, D) : ops.normMod(gpu, x, c.final, 0, D, D);
     x.release();
     c.release();
-    const out = ops.linear(gpu, n, this.finalLinear, { name: "dit.final" });
+    const out = ops.linear(gpu, tiled ? null : n, this.finalLinear, { xr: tiled ? n : undefined, name: "dit.final" });
     n.release();
     return out;
   }

@@ -42,24 +42,50 @@ export function rotateHalf(gpu, x, cols = x.shape[x.shape.length - 1], tiled = f
   return y;
 }
 
-// Whether an int8 weight can take tiled operands (N % 64 == 0, K % 256 == 0).
+// Whether an int8 weight can take tiled (rotated) operands (N % 64 == 0, K % 256 == 0).
 export const tileable = (W) => W.kind === "i8" && W.N % 64 === 0 && W.K % 256 === 0;
+// Whether a bf16 weight can be re-tiled as fp16 for tiled plain operands (N, K % 64 == 0).
+export const tileablePlain = (W) => W.kind === "bf16" && W.N % 64 === 0 && W.K % 64 === 0;
 
-// Re-tile an int8 weight for tiled operands (W.tbuf, kept next to the row-major W.buf).
+// Re-tile a weight for tiled operands (W.tbuf, kept next to the row-major W.buf): int8 tiles of
+// biased bytes, or fp16 tiles of a bf16 weight.
 export function tileWeight(gpu, W) {
-  if (!tileable(W)) throw new Error(`${W.name}: [${W.N}, ${W.K}] int8 weight cannot be tiled`);
+  if (!tileable(W) && !tileablePlain(W)) throw new Error(`${W.name}: [${W.N}, ${W.K}] ${W.kind} weight cannot be tiled`);
   if (W.tbuf) return W;
-  const ptr = native.malloc(W.N * W.K);
-  W.tbuf = new DeviceBuffer(ptr, W.N * W.K, false);
-  gpu.run("tile_i8_weight", 0, () => native.tileI8Weight(addr(W.buf), addr(W.tbuf), W.N, W.K));
+  const bytes = W.N * W.K * (W.kind === "i8" ? 1 : 2);
+  W.tbuf = new DeviceBuffer(native.malloc(bytes), bytes, false);
+  if (W.kind === "i8") gpu.run("tile_i8_weight", 0, () => native.tileI8Weight(addr(W.buf), addr(W.tbuf), W.N, W.K));
+  else gpu.run("tile_bf16_weight", 0, () => native.tileBf16Weight(addr(W.buf), addr(W.tbuf), W.N, W.K));
   return W;
+}
+
+// x (- sub) as the tiled fp16 operand of a linear over a re-tiled bf16 weight ([rows, cols],
+// cols % 64 == 0): the DiT's patch-embedder input, and the SPRINT projection's input g - x
+// (app/models/nanosaur2.js:236-243: elementwise sub, then linear) without the fp32 difference.
+export function toTiled(gpu, x, sub = null) {
+  const cols = x.shape[x.shape.length - 1];
+  const rows = x.size / cols;
+  const y = rotatedOperand(gpu, rows, cols, true);
+  gpu.run(sub ? "sub_tiled_f16" : "to_tiled_f16", 0, () =>
+    native.toTiledF16(addr(x), cols, sub ? addr(sub) : null, cols, addr(y), rows, cols));
+  return y;
+}
+
+// normMod (below) written as the tiled fp16 operand of a linear over a re-tiled bf16 weight
+// (the final layer, app/models/nanosaur2.js:252-253), cols % 256 == 0.
+export function normModTiled(gpu, x, mod, shiftOff, scaleOff, cols, weight = null, eps = 1e-6) {
+  const rows = x.size / cols;
+  const y = rotatedOperand(gpu, rows, cols, true);
+  gpu.run(weight ? "rmsnorm_mod_f16" : "layernorm_mod_f16", 0, () =>
+    native.normModF16(addr(x), addr(mod), shiftOff, scaleOff, rows, cols, addr(weight), eps, addr(y), 1));
+  return y;
 }
 
 // Free the row-major int8 copy of a re-tiled weight when the caller only ever feeds it tiled
 // operands (the fused DiT path): the tiled copy alone then holds the weight, so the int8
 // model stays resident once instead of twice. linear() refuses a row-major launch afterwards.
 export function dropRowMajor(W) {
-  if (!W.tbuf && !W.tglu) throw new Error(`${W.name}: only a re-tiled int8 weight can drop its row-major copy`);
+  if (!W.tbuf && !W.tglu) throw new Error(`${W.name}: only a re-tiled weight can drop its row-major copy`);
   if (W.buf) W.buf.destroy();
   W.buf = null;
   return W;
@@ -126,7 +152,7 @@ export function linear(gpu, x, W, opts = {}) {
         cOff, 1, act, ...lora, addr(buf), col0, H, D, Lk));
     return out;
   }
-  if (W.kind === "i8" && src.tiled && !W.tbuf) throw new Error(`${W.name}: a tiled operand needs the tiled weight (tileWeight)`);
+  if (src.tiled && !W.tbuf) throw new Error(`${W.name}: a tiled operand needs the tiled weight (tileWeight)`);
   if (W.kind === "i8" && !src.tiled && !W.buf) {
     throw new Error(`${W.name}: the row-major int8 weight was freed after tiling; pass a tiled operand`);
   }
@@ -136,7 +162,7 @@ export function linear(gpu, x, W, opts = {}) {
   // stacked weight whose LoRAs need several side paths launches once per row window of W,
   // each into its own output columns.
   for (const { off, n, args: lora } of loraLaunches(gpu, W)) {
-    if (W.kind === "i8" && src.tiled && off % 64) throw new Error(`${W.name}: LoRA window at row ${off} is not tile aligned`);
+    if (src.tiled && off % 64) throw new Error(`${W.name}: LoRA window at row ${off} is not tile aligned`);
     const rowBytes = W.kind === "i8" ? W.K : 2 * W.K;
     const wAt = (buf) => addr(buf) + BigInt(off * rowBytes);
     const vAt = (t) => (t ? addr(t) + BigInt(4 * off) : null);
@@ -151,7 +177,12 @@ export function linear(gpu, x, W, opts = {}) {
       gpu.run(opts.name || "gemm.i8", flops, () =>
         native.linearI8(addr(src), aFmt, W.K, wAt(W.buf), vAt(W.scale), vAt(bias), null, addr(out),
           M, n, W.K, ldc, c0, 1, act, resid, addr(opts.gate), g0, ...lora));
+    } else if (src.tiled) {
+      gpu.run(opts.name || "gemm.bf16", flops, () =>
+        native.linearF16wTiled(addr(src), wAt(W.tbuf), vAt(bias), addr(out), M, n, W.K, ldc, c0, 1, act, resid,
+          addr(opts.gate), g0, ...lora));
     } else {
+      if (!W.buf) throw new Error(`${W.name}: the row-major bf16 weight was freed after tiling; pass a tiled operand`);
       gpu.run(opts.name || "gemm.bf16", flops, () =>
         native.linearBf16(addr(x), W.K, wAt(W.buf), vAt(bias), null, addr(out), M, n, W.K, ldc, c0,
           1, act, resid, addr(opts.gate), g0, ...lora));
@@ -311,6 +342,12 @@ export function addRows(gpu, a, b) {
 export function rowView(t, r) {
   const n = t.shape[t.shape.length - 1];
   return { buf: { ptr: addr(t) + BigInt(r * n * 4) }, shape: [1, n], size: n, release() {} };
+}
+
+// Columns [off, off + n) of a [1, N] tensor as a [1, n] view (no copy; valid while t is).
+export function colView(t, off, n) {
+  if (t.size !== t.shape[t.shape.length - 1] || off + n > t.size) throw new Error("colView: a [1, N] tensor and a window inside it");
+  return { buf: { ptr: addr(t) + BigInt(off * 4) }, shape: [1, n], size: n, release() {} };
 }
 
 export function rowSum(gpu, x, w, scale = 1) {

@@ -9,7 +9,12 @@
 // [T*640], weights.f32 [T]. --out writes the x0 prediction [64, h, w] as raw fp32.
 // With --reps, the pass is timed with the latent resident in device memory (stream events
 // and wall clock), and once more host-to-host (upload, pass, readback); one JSON line with
-// the timings (and the per-op profile with --profile) is printed. --lora attaches a LoRA file
+// the timings (and the per-op profile with --profile) is printed. The passes are timed twice:
+// one at a time (each waits for the previous to finish: `ms_device`), and queued (issued back
+// to back behind one untimed pass, with no wait between them: `ms_device_queued`), so that a
+// pass's launches are on the device before they run, as in a pipelined sampler loop (the host
+// issues a pass faster than the GPU runs it); the per-op profile is taken on queued passes, so
+// it times the ops' own execution rather than the host's launch latency between them. --lora attaches a LoRA file
 // (strength 1 by default; repeatable) to the model's linears (lora.js), as the pipeline does.
 // --abort-at K first runs a pass whose onBlock throws an AbortError after block K, as the
 // pipeline's cancel does, and reports the error, the blocks run and the pooled bytes in use
@@ -155,20 +160,42 @@ async function main() {
     for (let i = 0; i < a.warmup; i++) await pass();
     await gpu.sync();
     if (gpu.profiler) gpu.profiler.reset();
-    const evA = native.eventCreate();
-    const evB = native.eventCreate();
-    const dev = [];
-    const wall = [];
-    for (let i = 0; i < a.reps; i++) {
-      const w0 = process.hrtime.bigint();
-      native.eventRecord(evA);
+    const evs = [];
+    for (let i = 0; i < 2 * a.reps; i++) evs.push(native.eventCreate());
+    // one pass at a time: each waits for the previous one
+    const single = async () => {
+      const dev = [];
+      const wall = [];
+      for (let i = 0; i < a.reps; i++) {
+        const w0 = process.hrtime.bigint();
+        native.eventRecord(evs[0]);
+        await pass();
+        native.eventRecord(evs[1]);
+        await gpu.sync();
+        wall.push(Number(process.hrtime.bigint() - w0) / 1e6);
+        dev.push(native.eventElapsed(evs[0], evs[1]));
+        process.stderr.write(`[run_dit] pass ${i + 1}/${a.reps}: ${dev[dev.length - 1].toFixed(3)} ms\n`);
+      }
+      return { dev, wall };
+    };
+    // queued: one untimed pass, then the timed passes issued back to back, one wait at the end
+    const queued = async () => {
+      if (gpu.profiler) gpu.profiler.paused = true;
       await pass();
-      native.eventRecord(evB);
+      if (gpu.profiler) gpu.profiler.paused = false;
+      for (let i = 0; i < a.reps; i++) {
+        native.eventRecord(evs[2 * i]);
+        await pass();
+        native.eventRecord(evs[2 * i + 1]);
+      }
       await gpu.sync();
-      wall.push(Number(process.hrtime.bigint() - w0) / 1e6);
-      dev.push(native.eventElapsed(evA, evB));
-      process.stderr.write(`[run_dit] pass ${i + 1}/${a.reps}: ${dev[dev.length - 1].toFixed(3)} ms\n`);
-    }
+      const dev = [];
+      for (let i = 0; i < a.reps; i++) dev.push(native.eventElapsed(evs[2 * i], evs[2 * i + 1]));
+      process.stderr.write(`[run_dit] queued passes: ${dev.map((d) => d.toFixed(3)).join(" ")} ms\n`);
+      return dev;
+    };
+    const { dev, wall } = gpu.profiler ? { dev: [], wall: [] } : await single();
+    const devQ = await queued();
     if (gpu.profiler) {
       const rows = await gpu.profiler.report();
       report.profile = rows.map((r) => ({ name: r.name, count: r.count / a.reps, ms: r.ms / a.reps, tflops: r.flops ? r.flops / (r.ms / 1e3) / 1e12 : null }));
@@ -180,11 +207,11 @@ async function main() {
       host.push(Number(process.hrtime.bigint() - w0) / 1e6);
     }
     tokens.release();
-    native.eventDestroy(evA);
-    native.eventDestroy(evB);
+    for (const e of evs) native.eventDestroy(e);
     Object.assign(report, {
       reps: a.reps, warmup: a.warmup, ms_device: dev, ms_wall: wall, ms_host_to_host: host,
       ms_device_median: median(dev), ms_wall_median: median(wall), ms_host_to_host_median: median(host),
+      ms_device_queued: devQ, ms_device_queued_median: median(devQ),
     });
   }
   report.pool_peak_bytes = gpu.pool.peak;

@@ -67,6 +67,13 @@ SIGNATURES = {
                         c_float, c_int, c_int, c_vp, c_ll],
     "ns2_linear_bf16_lora": [c_vp, c_int, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_ll,
                         c_float, c_int, c_int, c_vp, c_ll, c_vp, c_vp, c_int],
+    "ns2_tile_bf16_weight": [c_vp, c_vp, c_int, c_int],
+    "ns2_linear_f16w_tiled": [c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_ll, c_float, c_int, c_int,
+                              c_vp, c_ll],
+    "ns2_linear_f16w_tiled_lora": [c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_ll, c_float, c_int, c_int,
+                                   c_vp, c_ll, c_vp, c_vp, c_int],
+    "ns2_norm_mod_f16": [c_vp, c_vp, c_ll, c_ll, c_int, c_int, c_vp, c_float, c_vp, c_int],
+    "ns2_to_tiled_f16": [c_vp, c_int, c_vp, c_int, c_vp, c_int, c_int],
     "ns2_attention": [c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
                       c_int, c_ll, c_ll, c_ll, c_ll, c_ll, c_ll, c_ll, c_ll, c_float, c_vp, c_int,
                       c_ll, c_vp, c_vp, c_float, c_vp, c_ll, c_int],
@@ -225,6 +232,22 @@ class Lib:
         args = [_ptr(At), _ptr(Wt), _ptr(scale), _ptr(bias), _ptr(C), M, N, K,
                 N if ldc is None else ldc, cOff, alpha, ACT[act], int(resid), _ptr(gate), gOff]
         self._linear("ns2_linear_i8_tiled", args, lora)
+
+    def tile_bf16_weight(self, W, Wt, N, K):
+        self.call("ns2_tile_bf16_weight", _ptr(W), _ptr(Wt), N, K)
+
+    def linear_f16w_tiled(self, At, Wt, C, M, N, K, *, bias=None, ldc=None, cOff=0, alpha=1.0, act="none",
+                          resid=False, gate=None, gOff=0, lora=None):
+        args = [_ptr(At), _ptr(Wt), _ptr(bias), _ptr(C), M, N, K, N if ldc is None else ldc, cOff, alpha, ACT[act],
+                int(resid), _ptr(gate), gOff]
+        self._linear("ns2_linear_f16w_tiled", args, lora)
+
+    def to_tiled_f16(self, x, ldx, y, rows, cols, *, sub=None, ldsub=0):
+        self.call("ns2_to_tiled_f16", _ptr(x), ldx, _ptr(sub), ldsub, _ptr(y), rows, cols)
+
+    def norm_mod_f16(self, x, mod, shiftOff, scaleOff, rows, cols, weight, y, eps=1e-6, tiled=True):
+        self.call("ns2_norm_mod_f16", _ptr(x), _ptr(mod), shiftOff, scaleOff, rows, cols, _ptr(weight), eps, _ptr(y),
+                  int(tiled))
 
     def linear_i8_tiled_vpack(self, At, Wt, scale, C, M, N, K, vpk, *, vcol0, H, D, Lk, bias=None, ldc=None,
                               cOff=0, alpha=1.0, act="none", lora=None):

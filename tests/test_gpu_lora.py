@@ -224,18 +224,31 @@ def test_gemma_encode_with_lora(lora_golden):
     assert_close(got, torch.from_numpy(z["te.out"]), TOL_PASS, "Gemma3 encoding with LoRA")
 
 
+# LoRAs on the linears the fused pass stacks or re-tiles: the two adaLN projections of the
+# conditioning vector (one stacked GEMV), a text block's adaLN projection (stacked with the
+# other block's), and the bf16 linears that take tiled fp16 operands
+STACKED_TARGETS = [
+    ("shared_encoder_adaLN.0", 6 * F.D, F.D, 8, "peft"),
+    ("final_layer.adaLN_modulation", 2 * F.D, F.D, 8, "kohya"),
+    ("text_refine_blocks.1.adaLN_modulation.0", 6 * F.D, F.D, 8, "peft"),
+    ("sprint_out_proj", F.D, F.D, 8, "peft"),
+    ("s_embedder.proj", F.D, 64, 8, "peft"),
+]
+
+
 @pytest.mark.parametrize("reference_ops", [False, True])
 def test_dit_pass_lora_on_every_joint_kv(tmp_path, reference_ops):
-    """A rank-32 LoRA on the kv_y of all 9 joint blocks (288 summed ranks). The fused pass runs
-    the 9 kv_y projections as one stacked weight, whose side paths then split into two row
-    windows (8 parts at rank 256, 1 at rank 32) and two launches; the reference op sequence
-    runs each kv_y with its own side path. Both against the oracle with the LoRA merged into
-    the weights (tools/reference.py:48-95), and closer to it than to the pass without the LoRA."""
+    """A rank-32 LoRA on the kv_y of all 9 joint blocks (288 summed ranks), plus LoRAs on the
+    stacked adaLN projections and the re-tiled bf16 linears. The fused pass runs the 9 kv_y
+    projections as one stacked weight, whose side paths then split into two row windows (8
+    parts at rank 256, 1 at rank 32) and two launches; the reference op sequence runs each kv_y
+    with its own side path. Both against the oracle with the LoRA merged into the weights
+    (tools/reference.py:48-95), and closer to it than to the pass without the LoRA."""
     from safetensors.torch import save_file
 
     I = 256
     tensors = F.make_weights(seed=5, I=I)
-    lora = F.make_lora(seed=14, I=I, b_std=0.3, targets=F.joint_kv_targets(32))
+    lora = F.make_lora(seed=14, I=I, b_std=0.3, targets=F.joint_kv_targets(32) + STACKED_TARGETS)
     wpath, lpath = str(tmp_path / "dit.safetensors"), str(tmp_path / "kv_lora.safetensors")
     F.save_weights(tensors, wpath)
     save_file(lora, lpath)
@@ -247,7 +260,7 @@ def test_dit_pass_lora_on_every_joint_kv(tmp_path, reference_ops):
     if reference_ops:
         args.append("--reference-ops")
     rep = F.run_node(args)
-    assert rep["loras"][0]["matched"] == 9 and rep["loras"][0]["skipped"] == 0
+    assert rep["loras"][0]["matched"] == 9 + len(STACKED_TARGETS) and rep["loras"][0]["skipped"] == 0
     got = torch.from_numpy(np.fromfile(out, dtype=np.float32).reshape(64, 5, 6))
     ref = F.oracle_forward(tensors, inp, loras=[(lora, 0.8)])
     assert_close(got, ref, TOL_PASS, f"DiT pass, rank-32 LoRA on all joint kv_y (reference ops {reference_ops})")

@@ -422,6 +422,71 @@ def test_linear_bf16_gemv_silu_resid(ns2lib):
     assert_close(outd.cpu(), O.linear_bf16(x.double(), w, out=base.double().clone(), resid=True), TOL_F32 * 10, "gemv resid")
 
 
+@pytest.mark.parametrize("M,N,K", [
+    (3952, 1536, 1536),   # the SPRINT projection (x += (g - x) W^T)
+    (3952, 1536, 64),     # the patch embedder (one k-tile)
+    (3952, 64, 1536),     # the final layer (one column tile: split K)
+    (97, 320, 512),       # ragged rows, N not a multiple of 128
+])
+def test_linear_f16w_tiled(ns2lib, M, N, K):
+    """bf16 weights re-tiled as fp16 (ns2_tile_bf16_weight) on tiled fp16 operands
+    (ns2_to_tiled_f16): a plain store with bias and SiLU, and the residual form with the input
+    formed as a difference of two fp32 streams, against the oracle's bf16 linear; the weight
+    tiles against the bf16 values rounded to fp16."""
+    g = gen(M + 3 * N + K)
+    x = torch.randn(M, K, generator=g)
+    x2 = torch.randn(M, K, generator=g)
+    w = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
+    bias = torch.randn(N, generator=g) * 0.1
+    wt = torch.empty(N * K, dtype=torch.int16, device=dev)
+    ns2lib.tile_bf16_weight(w.view(torch.int16).to(dev), wt, N, K)
+    torch.cuda.synchronize()
+    assert torch.equal(f16_as_float(untile_a(wt.cpu(), N, K)), w.float().half().float())
+    at = tiled_operand(M, K)
+    ns2lib.to_tiled_f16(x.to(dev), K, at, M, K)
+    torch.cuda.synchronize()
+    assert torch.equal(f16_as_float(untile_a(at.cpu(), M, K)), x.half().float())
+    out = torch.empty(M, N, device=dev)
+    ns2lib.linear_f16w_tiled(at, wt, out, M, N, K, bias=bias.to(dev), act="silu")
+    torch.cuda.synchronize()
+    assert_close(out.cpu(), O.linear_bf16(x.double(), w, bias=bias.double(), act="silu"), TOL,
+                 f"linear_f16w_tiled {M}x{N}x{K}")
+    # x += (x2 - x) W^T
+    ns2lib.to_tiled_f16(x2.to(dev), K, at, M, K, sub=x.to(dev), ldsub=K)
+    base = torch.randn(M, N, generator=g)
+    outd = base.to(dev)
+    ns2lib.linear_f16w_tiled(at, wt, outd, M, N, K, resid=True)
+    torch.cuda.synchronize()
+    ref = O.linear_bf16((x2 - x).double(), w, out=base.double().clone(), resid=True)
+    assert_close(outd.cpu(), ref, TOL, f"linear_f16w_tiled resid {M}x{N}x{K}")
+
+
+def test_to_tiled_f16_padding(ns2lib):
+    """Rows past M up to the 64-row padding are written as zeros."""
+    M, K = 70, 128
+    x = torch.randn(M, K, generator=gen(5))
+    at = torch.full(((M + 63) // 64 * 64, K), 0x3C00, dtype=torch.int16, device=dev)  # 1.0 everywhere
+    ns2lib.to_tiled_f16(x.to(dev), K, at, M, K)
+    torch.cuda.synchronize()
+    full = f16_as_float(untile_a(at.cpu(), 128, K))
+    assert torch.equal(full[:M], x.half().float()) and (full[M:] == 0).all()
+
+
+@pytest.mark.parametrize("rms", [False, True])
+def test_norm_mod_f16(ns2lib, rms):
+    """normMod written as the tiled fp16 operand, without the rotation (the final layer)."""
+    rows, cols = 300, 1536
+    g = gen(44 + rms)
+    x = torch.randn(rows, cols, generator=g) * 3 + 0.5
+    mod = torch.randn(2 * cols, generator=g) * 0.1
+    w = torch.randn(cols, generator=g) * 0.02 if rms else None
+    y = tiled_operand(rows, cols)
+    ns2lib.norm_mod_f16(x.to(dev), mod.to(dev), 0, cols, rows, cols, w.to(dev) if rms else None, y)
+    torch.cuda.synchronize()
+    ref = O.norm_mod(x.double(), mod.double(), 0, cols, w.double() if rms else None)
+    assert_close(f16_as_float(untile_a(y.cpu(), rows, cols)), ref, TOL_F16_OUT, f"norm_mod_f16 rms={rms}")
+
+
 # ----------------------------------------------------------------------------- attention
 
 def _attn_inputs(seed, Lq_img, T, heads=16, hd=96):
