@@ -527,6 +527,64 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemmArgs p) {
   }
 }
 
+// One-row bf16 GEMV (the adaLN and embedder projections of one conditioning vector) for
+// K = 512 KS: every wave owns CPW output columns and issues the loads of all its weight rows
+// (CPW x KS 16-byte chunks per lane) and of the input row before any arithmetic, so a wave keeps
+// CPW * K * 2 bytes in flight and the grid has CPW times fewer, longer-lived waves than one
+// wave per column. Sums over k in the order of gemv_kernel's lanes and steps.
+template <int CPW, int KS>
+__global__ __launch_bounds__(256) void gemv1_bf16_kernel(GemmArgs p) {
+  const int lane = threadIdx.x & 63;
+  const int n0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * CPW;
+  if (n0 >= p.N) return;
+  uint4 wq[CPW][KS];
+#pragma unroll
+  for (int c = 0; c < CPW; ++c) {
+    const int n = n0 + c < p.N ? n0 + c : p.N - 1;  // clamped: unconditional loads
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+      wq[c][s] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.W) + (long long)n * p.K + s * 512 + lane * 8);
+  }
+  float4 ar[KS][2];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    const float* ap = static_cast<const float*>(p.A) + s * 512 + lane * 8;
+    ar[s][0] = *reinterpret_cast<const float4*>(ap);
+    ar[s][1] = *reinterpret_cast<const float4*>(ap + 4);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  float acc[CPW];
+#pragma unroll
+  for (int c = 0; c < CPW; ++c) {
+    acc[c] = 0.f;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const uint32_t qq[4] = {wq[c][s].x, wq[c][s].y, wq[c][s].z, wq[c][s].w};
+      const float a[8] = {ar[s][0].x, ar[s][0].y, ar[s][0].z, ar[s][0].w, ar[s][1].x, ar[s][1].y, ar[s][1].z, ar[s][1].w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        acc[c] = fmaf(a[2 * j], __builtin_bit_cast(float, qq[j] << 16), acc[c]);
+        acc[c] = fmaf(a[2 * j + 1], __builtin_bit_cast(float, qq[j] & 0xffff0000u), acc[c]);
+      }
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < CPW; ++c) {
+    const int n = n0 + c;
+    const float sum = wave_sum(acc[c]);
+    float d = 0.f;
+    if (p.lr) {
+      for (int k = lane; k < p.lr; k += 64) d += p.lt[k] * (float)p.lb[(long long)(n < p.N ? n : p.N - 1) * p.lr + k];
+      d = wave_sum(d);
+    }
+    if (lane == 0 && n < p.N) {
+      const float bi = p.bias ? p.bias[n] : 0.0f;
+      const float gt = p.gate ? p.gate[p.gOff + n] : 1.0f;
+      epilogue_store(p, 0, n, sum, 1.0f, bi, gt, d);
+    }
+  }
+}
+
 // fp32 [rows, lda] (already rotated) -> fp16 [rows, cols]
 __global__ __launch_bounds__(256) void cast_f16_kernel(const float* __restrict__ x, int ldx,
                                                         uint16_t* __restrict__ y, int rows,
@@ -622,6 +680,8 @@ constexpr int kMaxSplits = 16;
 // the row kernel in place of the split-K reduce (a single split when K is short).
 // glu_y: a GLU post-op (y [M, N/2] = act(gate) * up, act glu_act), on the same split-K path.
 // hn: the per-head norms of a stacked q|k|v product (Gemma3), on the same split-K path.
+inline bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
 template <bool A_F32, bool W_BF16>
 int launch_gemm(const GemmArgs& p, const char* name, const RowNorm* rn = nullptr, float* glu_y = nullptr,
                 int glu_act = 0, const HeadNorm* hn = nullptr) {
@@ -630,7 +690,16 @@ int launch_gemm(const GemmArgs& p, const char* name, const RowNorm* rn = nullptr
   ns2::ProfScope prof_(rn ? "gemm_bf16_add_rmsnorm" : glu_y ? "gemm_bf16_glu" : hn ? "gemm_bf16_head_norm"
                           : p.M <= kGemvMaxM ? (W_BF16 ? "gemv_bf16" : "gemv_i8") : (W_BF16 ? "gemm_bf16" : "gemm_i8"));
   const long long big_tiles = (long long)((p.N + 127) / 128) * ((p.M + 127) / 128);
-  if (!post && p.M <= kGemvMaxM) {
+  if (!post && p.M == 1 && W_BF16 && A_F32 && p.K % 512 == 0 && p.K <= 2048 && aligned16(p.A)) {
+    constexpr int CPW = 4;
+    const dim3 grid((p.N + 4 * CPW - 1) / (4 * CPW));
+    switch (p.K / 512) {
+      case 1: gemv1_bf16_kernel<CPW, 1><<<grid, 256, 0, s>>>(p); break;
+      case 2: gemv1_bf16_kernel<CPW, 2><<<grid, 256, 0, s>>>(p); break;
+      case 3: gemv1_bf16_kernel<CPW, 3><<<grid, 256, 0, s>>>(p); break;
+      default: gemv1_bf16_kernel<CPW, 4><<<grid, 256, 0, s>>>(p); break;
+    }
+  } else if (!post && p.M <= kGemvMaxM) {
     // row count rounded up to 1, 2, 4 or 8: no duplicate A loads for the common M = 1
     const dim3 grid((p.N + 3) / 4);
     if (p.M == 1) gemv_kernel<W_BF16, 1><<<grid, 256, 0, s>>>(p);
@@ -682,8 +751,6 @@ int launch_gemm(const GemmArgs& p, const char* name, const RowNorm* rn = nullptr
   NS2_LAUNCHED(name);
   return NS2_OK;
 }
-
-inline bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 int check_common(const GemmArgs& p, const char* name) {
   NS2_REQUIRE(p.A && p.W && p.C, "%s: null A, W or C", name);

@@ -264,35 +264,42 @@ void launch_rot_rows(const RotRowsArgs& a, int groups) {
 // ---- fp16 operands of the plain linears ------------------------------------------------------
 
 // y = x (- sub) as the tiled fp16 operand [ceil(rows/64)][cols/64][8][64][8] of a tiled linear;
-// rows past the last one, up to the 64-row padding, are written as zeros. Thread i writes the
-// 16-byte chunk i of the tiled image (consecutive threads: consecutive rows of one 8-column
-// chunk), so the stores are contiguous; the 4 waves of a block read the 4 quarters of each
-// 128-byte line of the rows they cover.
+// rows past the last one, up to the 64-row padding, are written as zeros. One block per 64x64
+// tile: each wave reads 16 rows of 64 columns (256 contiguous bytes per row, 16 bytes per lane),
+// the block transposes the fp16 values through LDS into the tile's chunk-major image and writes
+// it out as 8 KB of contiguous 16-byte stores.
 __global__ __launch_bounds__(256) void to_tiled_f16_kernel(const float* __restrict__ x, int ldx,
                                                             const float* __restrict__ sub, int lds,
                                                             uint16_t* __restrict__ y, int rows, int cols) {
-  const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
-  const int cpr = cols / 8;  // 8-column chunks per row
-  const long long total = (long long)(rows + 63) / 64 * 64 * cpr;
-  if (i >= total) return;
-  const int rr = (int)(i % 64);
-  const long long rest = i / 64;  // 64-row block * cpr + chunk
-  const int kc = (int)(rest % cpr);
-  const int m = (int)(rest / cpr) * 64 + rr;
-  uint4 o = make_uint4(0u, 0u, 0u, 0u);
-  if (m < rows) {
-    const float4 a0 = *reinterpret_cast<const float4*>(x + (long long)m * ldx + kc * 8);
-    const float4 a1 = *reinterpret_cast<const float4*>(x + (long long)m * ldx + kc * 8 + 4);
-    float v[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-    if (sub) {
-      const float4 b0 = *reinterpret_cast<const float4*>(sub + (long long)m * lds + kc * 8);
-      const float4 b1 = *reinterpret_cast<const float4*>(sub + (long long)m * lds + kc * 8 + 4);
-      v[0] -= b0.x, v[1] -= b0.y, v[2] -= b0.z, v[3] -= b0.w;
-      v[4] -= b1.x, v[5] -= b1.y, v[6] -= b1.z, v[7] -= b1.w;
+  constexpr int CS = 64 * 8 + 8;  // halfs per chunk in LDS (16 bytes of padding: the 8 chunks of a
+                                 // row fall in different banks)
+  __shared__ __attribute__((aligned(16))) uint16_t t[8 * CS];
+  const int kb = blockIdx.x % (cols / 64), mb = blockIdx.x / (cols / 64);
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int q = tid + 256 * i;        // 4-column piece q of the 64x64 tile
+    const int r = q / 16, c4 = q % 16;  // row, first column / 4
+    const int m = mb * 64 + r;
+    uint2 o = make_uint2(0u, 0u);
+    if (m < rows) {
+      float4 v = *reinterpret_cast<const float4*>(x + (long long)m * ldx + kb * 64 + 4 * c4);
+      if (sub) {
+        const float4 b = *reinterpret_cast<const float4*>(sub + (long long)m * lds + kb * 64 + 4 * c4);
+        v.x -= b.x, v.y -= b.y, v.z -= b.z, v.w -= b.w;
+      }
+      o = make_uint2(pack_half2(v.x, v.y), pack_half2(v.z, v.w));
     }
-    o = make_uint4(pack_half2(v[0], v[1]), pack_half2(v[2], v[3]), pack_half2(v[4], v[5]), pack_half2(v[6], v[7]));
+    // chunk-major image: chunk c = column / 8 holds 64 rows of 8 halfs
+    *reinterpret_cast<uint2*>(&t[(c4 >> 1) * CS + r * 8 + 4 * (c4 & 1)]) = o;
   }
-  *reinterpret_cast<uint4*>(y + i * 8) = o;
+  __syncthreads();
+  uint4* dst = reinterpret_cast<uint4*>(y + ((long long)mb * (cols / 64) + kb) * 4096);
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int j = tid + 256 * i;  // 16-byte unit: chunk j / 64, row j % 64
+    dst[j] = *reinterpret_cast<const uint4*>(&t[(j >> 6) * CS + (j & 63) * 8]);
+  }
 }
 
 // ---- headNorm -------------------------------------------------------------------------------
@@ -585,9 +592,9 @@ int ns2_to_tiled_f16(const float* x, int ldx, const float* sub, int ldsub, uint1
               "ns2_to_tiled_f16: ldx=%d / ldsub=%d must be multiples of 4 and >= cols", ldx, ldsub);
   NS2_REQUIRE(x && y && aligned16(x) && aligned16(y) && (!sub || aligned16(sub)),
               "ns2_to_tiled_f16: null or unaligned buffer");
-  const long long chunks = (long long)(rows + 63) / 64 * 64 * (cols / 8);
+  const long long tiles = (long long)(rows + 63) / 64 * (cols / 64);
   ns2::ProfScope prof_("to_tiled_f16");
-  to_tiled_f16_kernel<<<(unsigned)((chunks + 255) / 256), 256, 0, ns2::stream()>>>(x, ldx, sub, ldsub, y, rows, cols);
+  to_tiled_f16_kernel<<<(unsigned)tiles, 256, 0, ns2::stream()>>>(x, ldx, sub, ldsub, y, rows, cols);
   NS2_LAUNCHED("to_tiled_f16");
   return NS2_OK;
 }

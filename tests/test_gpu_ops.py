@@ -487,6 +487,31 @@ def test_norm_mod_f16(ns2lib, rms):
     assert_close(f16_as_float(untile_a(y.cpu(), rows, cols)), ref, TOL_F16_OUT, f"norm_mod_f16 rms={rms}")
 
 
+@pytest.mark.parametrize("N,K", [(12288, 1536), (1000, 512), (77, 2048)])
+def test_linear_bf16_gemv_one_row(ns2lib, N, K):
+    """One-row bf16 linears with K a multiple of 512 (the adaLN projections, stacked): the
+    multi-column GEMV, plain with bias and SiLU, and a gated += into a column window; N not a
+    multiple of the 16 columns of a block."""
+    g = gen(N + K)
+    x = torch.randn(1, K, generator=g)
+    w = (torch.randn(N, K, generator=g) * 0.05).to(torch.bfloat16)
+    bias = torch.randn(N, generator=g) * 0.1
+    wd = w.view(torch.int16).to(dev)
+    out = torch.empty(1, N, device=dev)
+    ns2lib.linear_bf16(x.to(dev), K, wd, out, 1, N, K, bias=bias.to(dev), act="silu")
+    torch.cuda.synchronize()
+    assert_close(out.cpu(), O.linear_bf16(x.double(), w, bias=bias.double(), act="silu"), TOL_F32 * 10,
+                 f"gemv one row {N}x{K}")
+    base = torch.randn(1, N + 40, generator=g)
+    gate = torch.randn(N + 8, generator=g)
+    outd = base.to(dev)
+    ns2lib.linear_bf16(x.to(dev), K, wd, outd, 1, N, K, ldc=N + 40, cOff=24, resid=True, gate=gate.to(dev), gOff=8)
+    torch.cuda.synchronize()
+    ref = O.linear_bf16(x.double(), w, out=base.double().clone(), resid=True, gate=gate.double(), gOff=8,
+                        ldc=N + 40, cOff=24)
+    assert_close(outd.cpu(), ref, TOL_F32 * 10, f"gemv one row gated += {N}x{K}")
+
+
 # ----------------------------------------------------------------------------- attention
 
 def _attn_inputs(seed, Lq_img, T, heads=16, hd=96):
