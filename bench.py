@@ -177,9 +177,12 @@ def gemm_roofline(kernels):
 # ------------------------------------------------------------------------------ C ABI legs
 
 def timed(lib, call, reps, warmup):
-    """Mean ms per call over `reps` back-to-back calls (stream events), and the library profiler's
-    mean ms per launch of each kernel, after at least `warmup` calls and one second of untimed
-    calls (the clocks a busy GPU settles at)."""
+    """Mean ms per call three ways, after at least `warmup` calls and one second of untimed calls
+    (the clocks a busy GPU settles at): `graph_ms`, `reps` calls recorded as one HIP graph and
+    replayed (the device time of the op without the host's launch gaps); `eager_ms`, `reps`
+    back-to-back calls from Python (stream events around them); and the library profiler's mean
+    ms per launch of each kernel, from a third run with the profiler's events around every
+    launch. Returns (graph_ms, eager_ms, per-kernel profile)."""
     import torch
 
     t0 = time.perf_counter()
@@ -190,18 +193,35 @@ def timed(lib, call, reps, warmup):
         if n % 8 == 0:
             torch.cuda.synchronize()
     torch.cuda.synchronize()
-    lib.profile_reset()
-    lib.profile(True)
     a, b = lib.event(), lib.event()
     lib.record(a)
     for _ in range(reps):
         call()
     lib.record(b)
     torch.cuda.synchronize()
-    total_ms = lib.elapsed_ms(a, b) / reps
+    eager_ms = lib.elapsed_ms(a, b) / reps
+    lib.graph_begin()
+    for _ in range(reps):
+        call()
+    g = lib.graph_end()
+    lib.graph_launch(g)
+    torch.cuda.synchronize()
+    best = float("inf")
+    for _ in range(3):
+        lib.record(a)
+        lib.graph_launch(g)
+        lib.record(b)
+        torch.cuda.synchronize()
+        best = min(best, lib.elapsed_ms(a, b) / reps)
+    lib.graph_destroy(g)
+    lib.profile_reset()
+    lib.profile(True)
+    for _ in range(reps):
+        call()
+    torch.cuda.synchronize()
     prof = {k: {"count": v["count"], "ms": v["ms"] / max(1, v["count"])} for k, v in lib.profile_report().items()}
     lib.profile(False)
-    return total_ms, prof
+    return best, eager_ms, prof
 
 
 def rope_table(h, w):
@@ -247,7 +267,7 @@ def bench_attention(lib, h, w, T, B, reps, warmup):
                       qBatch=L * D, kBatch=Lk * D, vBatch=Lk * D, oBatch=L * D, key_bias=bias,
                       biasStart=L, biasBatch=T, rope_cs=cs, sin_off=L * HD // 2, rope_rows=L)
 
-    total_ms, prof = timed(lib, call, reps, warmup)
+    total_ms, eager_ms, prof = timed(lib, call, reps, warmup)
     flops = 4 * L * Lk * HD * HEADS * B
     flash_ms = prof["attn_flash"]["ms"]
     pack_ms = prof["attn_pack"]["ms"]
@@ -257,6 +277,8 @@ def bench_attention(lib, h, w, T, B, reps, warmup):
                   "2-D RoPE on image rows, log-weight bias on text keys, fp32 in/out",
         "gflop": flops / 1e9,
         "ms": total_ms, "tflops": tf(total_ms), "frac": tf(total_ms) / FP16_PEAK_TFLOPS,
+        "ms_eager": eager_ms, "ms_region": "ms: pack + flash, calls replayed as a HIP graph; ms_eager: "
+                                           "the same calls launched from Python",
         "flash_ms": flash_ms, "flash_tflops": tf(flash_ms), "flash_frac": tf(flash_ms) / FP16_PEAK_TFLOPS,
         "pack_ms": pack_ms, "flops_per_launch": flops,
     }
@@ -283,7 +305,7 @@ def bench_linear_cfg1(lib, reps, warmup):
             lib.rotate_f16(x, K, at, K, M, K, tiled=True)
             lib.linear_i8_tiled(at, wt, s, y, M, N, K)
 
-        total_ms, prof = timed(lib, call, reps, warmup)
+        total_ms, eager_ms, prof = timed(lib, call, reps, warmup)
         flops = 2 * M * N * K
         nbytes = N * K + 4 * N + 4 * M * K + 4 * M * N   # int8 W, scales, fp32 x in, fp32 y out
         gemm_ms, rot_ms = prof["gemm_i8_tiled"]["ms"], prof["rotate_f16"]["ms"]
@@ -291,7 +313,7 @@ def bench_linear_cfg1(lib, reps, warmup):
         out.append({
             "shape": f"{name}: M {M} x N {N} x K {K}", "gflop": flops / 1e9, "algorithmic_mb": nbytes / 1e6,
             "ms": total_ms, "tflops": tf(total_ms), "frac": tf(total_ms) / FP16_PEAK_TFLOPS,
-            "gbs": nbytes / (total_ms / 1e3) / 1e9,
+            "gbs": nbytes / (total_ms / 1e3) / 1e9, "ms_eager": eager_ms,
             "gemm_ms": gemm_ms, "gemm_tflops": tf(gemm_ms), "gemm_frac": tf(gemm_ms) / FP16_PEAK_TFLOPS,
             "rotate_ms": rot_ms, "rotate_gbs": M * K * 6 / (rot_ms / 1e3) / 1e9,
         })
@@ -550,7 +572,11 @@ def main():
     sys.path.insert(0, PKG)
     import ns2
 
-    lib = ns2.load(0, torch.cuda.current_stream().cuda_stream)
+    # the legs run on a stream of their own (default priority): a HIP graph cannot record the
+    # null stream; torch's allocations and fills of the legs go to the same stream
+    leg_stream = torch.cuda.Stream()
+    torch.cuda.set_stream(leg_stream)
+    lib = ns2.load(0, leg_stream.cuda_stream)
     reps = max(10, args.steps)
     attn = bench_attention(lib, H_IMG, W_IMG, T_TXT, 2, reps, max(2, args.warmup))
     log(f"attention 3952x4208 b2: {attn['ms']:.3f} ms/call, flash {attn['flash_ms']:.3f} ms "

@@ -149,7 +149,14 @@ struct RotRowsArgs {
 // L1: at 8 rows per block that is 3x the row's own bytes through L1 otherwise.
 template <int G, bool NORM, bool ROT = true>
 __global__ __launch_bounds__(512) void rot_rows_kernel(RotRowsArgs a) {
-  const int row = blockIdx.x * 8 + (threadIdx.x >> 6);
+  // rotation only, rows of an even number of groups from 6 on: each block takes half of its 8
+  // rows' groups (the two halves rotate independently), so the grid has twice the blocks and
+  // each block stages its whole part in LDS (2432 x 1536: 5.2 -> 4.7 us)
+  constexpr int GB = (!NORM && G >= 6 && G % 2 == 0) ? G / 2 : G;
+  constexpr int PARTS = G / GB;
+  static_assert(G % GB == 0 && GB <= 16, "groups per block");
+  const int part = PARTS > 1 ? blockIdx.x % PARTS : 0;
+  const int row = (blockIdx.x / PARTS) * 8 + (threadIdx.x >> 6);
   constexpr int cols = 256 * G;
   constexpr int NV = NORM ? 3 : 1;
   __shared__ __attribute__((aligned(16))) float4 mods[NV][NORM ? G * 64 : 1];  // [1 + scale, shift, w]
@@ -164,22 +171,23 @@ __global__ __launch_bounds__(512) void rot_rows_kernel(RotRowsArgs a) {
     __syncthreads();
   }
   // Tiled output goes through LDS (fp16, rows padded by 32 bytes: the 16 units of a quarter-wave
-  // write-out read, 2 chunks x 8 rows, fall in 16 different bank groups), up to 16 groups (66 KB;
-  // wider rows store directly and keep several blocks per CU). A wave past the last row still
-  // takes part in the block's barrier: it works on the last row, and its result is not written.
-  constexpr bool TSTAGE = G <= 16;
-  constexpr int TROW = cols + 16;
-  __shared__ __attribute__((aligned(16))) uint16_t tout[TSTAGE ? 8 * TROW : 8];
+  // write-out read, 2 chunks x 8 rows, fall in 16 different bank groups), at most 16 groups
+  // (66 KB), so every 128-byte line of the tiled layout is written whole (direct stores of
+  // 6144-column rows wrote each line in 8 pieces: 26.4 us at 2432 rows, 15.1 us staged in two
+  // column parts). A wave past the last row still takes part in the block's barrier: it works on the
+  // last row, and its result is not written.
+  constexpr int TROW = 256 * GB + 16;
+  __shared__ __attribute__((aligned(16))) uint16_t tout[8 * TROW];
   const bool active = row < a.rows;
-  if (!active && !(TSTAGE && a.tiled)) return;
+  if (!active && !a.tiled) return;
   // lane l holds elements 16(l%16) + 4(l/16) .. +3 of every group: the layout of the
   // matrix-core FWHT (its float4 loads still cover each group's 1 KB once per wave)
   const int lane = threadIdx.x & 63;
   const int lo = fwht_mfma_offset();
-  const float* src = a.x + (long long)(active ? row : a.rows - 1) * a.ldx + lo;
-  float v[G][4];
+  const float* src = a.x + (long long)(active ? row : a.rows - 1) * a.ldx + part * GB * 256 + lo;
+  float v[GB][4];
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
+  for (int g = 0; g < GB; ++g) {
     const float4 in = *reinterpret_cast<const float4*>(src + g * 256);
     v[g][0] = in.x, v[g][1] = in.y, v[g][2] = in.z, v[g][3] = in.w;
   }
@@ -189,12 +197,12 @@ __global__ __launch_bounds__(512) void rot_rows_kernel(RotRowsArgs a) {
     if (!a.w) {
       float s = 0.f;
 #pragma unroll
-      for (int g = 0; g < G; ++g) s += (v[g][0] + v[g][1]) + (v[g][2] + v[g][3]);
+      for (int g = 0; g < GB; ++g) s += (v[g][0] + v[g][1]) + (v[g][2] + v[g][3]);
       mean = wave_sum(s) / (float)cols;
     }
     float ss = 0.f;
 #pragma unroll
-    for (int g = 0; g < G; ++g)
+    for (int g = 0; g < GB; ++g)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         v[g][j] -= mean;
@@ -204,7 +212,7 @@ __global__ __launch_bounds__(512) void rot_rows_kernel(RotRowsArgs a) {
   }
   const half4v_t h = fwht_h16_fragment();
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
+  for (int g = 0; g < GB; ++g) {
     if (NORM) {
       // modulation of each element: y = ((v * r) * w) * (1 + scale) + shift, the reference's
       // order (kernels.js:82-117)
@@ -219,33 +227,33 @@ __global__ __launch_bounds__(512) void rot_rows_kernel(RotRowsArgs a) {
       }
     }
     if (ROT) fwht256_mfma(v[g], h);
-    if (!a.tiled || !TSTAGE) {
-      if (active) store4_f16(a.y, row, g * 256 + lo, a.ldy, cols, a.tiled, v[g]);
-    }
-    else {
+    if (!a.tiled) {
+      if (active) store4_f16(a.y, row, (part * GB + g) * 256 + lo, a.ldy, cols, a.tiled, v[g]);
+    } else {
       uint2 o;
       o.x = pack_half2(v[g][0], v[g][1]);
       o.y = pack_half2(v[g][2], v[g][3]);
       *reinterpret_cast<uint2*>(&tout[(threadIdx.x >> 6) * TROW + g * 256 + lo]) = o;
     }
   }
-  if (TSTAGE && a.tiled) {
+  if (a.tiled) {
     // write-out of the block's 8 rows: 16-byte unit u = (chunk u / 8, row u % 8), so the 8 units
     // of a chunk are one 128-byte line of the tiled layout and a wave writes 8 whole lines
     __syncthreads();
-    const int row0 = blockIdx.x * 8;
-    for (int u = threadIdx.x; u < G * 32 * 8; u += 512) {
+    const int row0 = (blockIdx.x / PARTS) * 8, c0 = part * GB * 32;
+    for (int u = threadIdx.x; u < GB * 32 * 8; u += 512) {
       const int c = u / 8, r = u % 8;
       if (row0 + r >= a.rows) continue;
       const uint4 q = *reinterpret_cast<const uint4*>(&tout[r * TROW + 8 * c]);
-      *reinterpret_cast<uint4*>(a.y + tiled_off(row0 + r, 8 * c, cols)) = q;
+      *reinterpret_cast<uint4*>(a.y + tiled_off(row0 + r, 8 * (c0 + c), cols)) = q;
     }
   }
 }
 
 template <bool NORM, bool ROT = true>
 void launch_rot_rows(const RotRowsArgs& a, int groups) {
-  const dim3 grid((a.rows + 7) / 8), block(512);
+  const int parts = (!NORM && groups >= 6 && groups % 2 == 0) ? 2 : 1;  // the kernel's column parts (GB)
+  const dim3 grid((a.rows + 7) / 8 * parts), block(512);
   hipStream_t s = ns2::stream();
   switch (groups) {
 #define NS2_ROT_CASE(G) \
