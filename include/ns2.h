@@ -76,7 +76,10 @@ int ns2_pool_trim(void);
 /* BufferPool.allocated / .peak (app/gpu/device.js:30-31). */
 int ns2_pool_stats(size_t* allocated, size_t* peak);
 
-/* GPU.write (app/gpu/device.js:122-131): host -> device, ordered on the stream. */
+/* GPU.write (app/gpu/device.js:122-131): host -> device, ordered on the stream; src may be
+ * reused when this returns. Copies up to 64 KB go through pinned staging slots and do not wait
+ * for the work queued before them (the queued write of the reference's writeBuffer); larger ones
+ * wait for the stream. Refused inside a graph capture. */
 int ns2_h2d(void* dst, const void* src, size_t bytes);
 /* GPU.read (app/gpu/device.js:141-154): device -> host, waits for prior work. */
 int ns2_d2h(void* dst, const void* src, size_t bytes);

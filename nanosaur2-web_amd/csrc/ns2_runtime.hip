@@ -27,6 +27,20 @@ static bool g_capturing = false;
 static int g_graphs = 0;
 static std::vector<void*> g_retired;
 
+// ---- staging of small host-to-device copies ------------------------------------------------
+// Pinned slots (allocated on first use, held until the process ends), each with the event of the
+// last copy that read it.
+constexpr size_t kStageBytes = 64 << 10;
+constexpr int kStageSlots = 16;
+struct Stage {
+  std::mutex mu;
+  void* base = nullptr;
+  hipEvent_t done[kStageSlots] = {};
+  bool used[kStageSlots] = {};
+  int next = 0;
+};
+static Stage g_stage;
+
 int set_error(int code, const char* fmt, ...) {
   va_list ap;
   va_start(ap, fmt);
@@ -294,6 +308,26 @@ int ns2_h2d(void* dst, const void* src, size_t bytes) {
   NS2_READY();
   if (!bytes) return NS2_OK;
   NS2_REQUIRE(dst && src, "ns2_h2d: null pointer");
+  NS2_REQUIRE(!g_capturing, "ns2_h2d: no uploads inside a graph capture");
+  if (bytes <= kStageBytes) {
+    // small copies (the per-pass timestep embedding): through a ring of pinned staging slots,
+    // queued on the stream without waiting for the work before it; a slot is reused once the
+    // copy that last read it has run
+    std::lock_guard<std::mutex> lock(g_stage.mu);
+    if (!g_stage.base) {
+      NS2_HIP(hipHostMalloc(&g_stage.base, kStageBytes * kStageSlots, hipHostMallocDefault));
+      for (int i = 0; i < kStageSlots; ++i) NS2_HIP(hipEventCreateWithFlags(&g_stage.done[i], hipEventDisableTiming));
+    }
+    const int i = g_stage.next;
+    g_stage.next = (i + 1) % kStageSlots;
+    if (g_stage.used[i]) NS2_HIP(hipEventSynchronize(g_stage.done[i]));
+    char* slot = static_cast<char*>(g_stage.base) + (size_t)i * kStageBytes;
+    memcpy(slot, src, bytes);
+    NS2_HIP(hipMemcpyAsync(dst, slot, bytes, hipMemcpyHostToDevice, g_stream));
+    NS2_HIP(hipEventRecord(g_stage.done[i], g_stream));
+    g_stage.used[i] = true;
+    return NS2_OK;
+  }
   // pageable source: the copy has completed reading src when this returns
   NS2_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, g_stream));
   NS2_HIP(hipStreamSynchronize(g_stream));
