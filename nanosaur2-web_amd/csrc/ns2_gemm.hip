@@ -673,6 +673,75 @@ __global__ __launch_bounds__(64 * lora_waves<RT>()) void lora_down_kernel(const 
     }
 }
 
+// The same on v_mfma_f32_16x16x32_f16 for K % 32 == 0: a block of 8 waves takes 16 rows and
+// 32 columns of t (blockIdx.y: columns 32y .. 32y+31 of R), so the 3952 image rows make 247
+// blocks at rank 32 and the 256 text rows 128 blocks at rank 256 (the 32-row kernel left CUs
+// idle: 10.6 us per call at rank 32, 46 us for 256 rows at rank 256). Lane l supplies row l%16
+// of x and of A with k = 32s + 8(l/16) .. +7; the accumulator element i of lane l is
+// t[4(l/16) + i][32y + 16j + l%16]. Every load of a wave's k-steps is issued before its products.
+template <int XFMT>
+__global__ __launch_bounds__(512) void lora_down16_kernel(const void* __restrict__ x, int ldx,
+                                                          const half_t* __restrict__ A, float* __restrict__ t,
+                                                          int M, int K, int R) {
+  constexpr int RB = 2, NWV = 8, NB = 6;
+  A += (long long)blockIdx.y * 32 * K;
+  t += blockIdx.y * 32;
+  __shared__ float red[NWV - 1][RB][4][64];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, l16 = lane & 15, kq = lane >> 4;
+  const int m0 = blockIdx.x * 16;
+  const int m = m0 + l16 < M ? m0 + l16 : M - 1;  // rows past M read the last row (not stored)
+  float4_t acc[RB];
+#pragma unroll
+  for (int j = 0; j < RB; ++j) acc[j] = float4_t{0.f, 0.f, 0.f, 0.f};
+  const int steps = K / 32;
+  const int mine = steps > wave ? (steps - wave + NWV - 1) / NWV : 0;
+  for (int j0 = 0; j0 < mine; j0 += NB) {
+    half8_t a[NB], b[NB][RB];
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+      const int sidx = wave + NWV * (j0 + u);
+      const int k = (sidx < steps ? sidx : steps - 1) * 32 + 8 * kq;
+      if constexpr (XFMT == 0) {
+        const float* xp = static_cast<const float*>(x) + (long long)m * ldx + k;
+        const float4 u0 = *reinterpret_cast<const float4*>(xp);
+        const float4 u1 = *reinterpret_cast<const float4*>(xp + 4);
+        a[u] = half8_t{(half_t)u0.x, (half_t)u0.y, (half_t)u0.z, (half_t)u0.w,
+                       (half_t)u1.x, (half_t)u1.y, (half_t)u1.z, (half_t)u1.w};
+      } else if constexpr (XFMT == 1) {
+        a[u] = *reinterpret_cast<const half8_t*>(static_cast<const half_t*>(x) + (long long)m * ldx + k);
+      } else {
+        a[u] = *reinterpret_cast<const half8_t*>(static_cast<const half_t*>(x) + tiled_off(m, k, K));
+      }
+#pragma unroll
+      for (int j = 0; j < RB; ++j) b[u][j] = *reinterpret_cast<const half8_t*>(A + (long long)(16 * j + l16) * K + k);
+    }
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+      if (j0 + u >= mine) a[u] = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+      for (int j = 0; j < RB; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[u], b[u][j], acc[j], 0, 0, 0);
+    }
+  }
+  if (wave > 0) {
+#pragma unroll
+    for (int j = 0; j < RB; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) red[wave - 1][j][i][lane] = acc[j][i];
+  }
+  __syncthreads();
+  if (wave > 0) return;
+#pragma unroll
+  for (int j = 0; j < RB; ++j)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float v = acc[j][i];
+#pragma unroll
+      for (int w = 0; w < NWV - 1; ++w) v += red[w][j][i][lane];
+      const int row = m0 + 4 * kq + i;
+      if (row < M) t[(long long)row * R + 16 * j + l16] = v;
+    }
+}
+
 constexpr int kGemvMaxM = 8;
 constexpr long long kSmallGridBlocks = 256;  // one block per CU
 constexpr int kMaxSplits = 16;
@@ -766,6 +835,10 @@ int check_common(const GemmArgs& p, const char* name) {
 
 template <int XFMT>
 void launch_lora_down(const void* x, int ldx, const half_t* A, float* t, int M, int K, int R, hipStream_t s) {
+  if (K % 32 == 0) {
+    lora_down16_kernel<XFMT><<<dim3((M + 15) / 16, R / 32), 512, 0, s>>>(x, ldx, A, t, M, K, R);
+    return;
+  }
   const dim3 grid((M + 31) / 32);
   switch (R / 32) {
 #define NS2_LORA_CASE(RT) \

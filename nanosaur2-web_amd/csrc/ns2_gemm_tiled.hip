@@ -540,6 +540,48 @@ __global__ __launch_bounds__(256) void tiled_splitk_reduce_kernel(TGemmArgs p, i
   else *c = *c + p.gate[p.gOff + n] * v;
 }
 
+// The same for launches with a LoRA term, one wave per 32x32 output tile: the lane sums the
+// splits of its 16 elements (the v_mfma_f32_32x32x16_f16 accumulator layout, rows 8(r/4) +
+// 4hi + r%4 of the tile, column lq), adds the tile's LoRA term on the matrix cores (lora_tile,
+// as the unsplit epilogues do) and applies the epilogue. An element-wise reduce would take the
+// LoRA term as R scalar products per element: 51.7 us for 256 x 3072 at rank 32.
+__global__ __launch_bounds__(256) void tiled_splitk_reduce_lora_kernel(TGemmArgs p, int splits) {
+  const int lane = threadIdx.x & 63, lq = lane & 31, hi = lane >> 5;
+  const int tn_count = p.N / 32;
+  const int tile = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (tile >= ((p.M + 31) / 32) * tn_count) return;  // uniform per wave
+  const int m0 = (tile / tn_count) * 32, n = (tile % tn_count) * 32 + lq;
+  const long long mn = (long long)p.M * p.N;
+  float acc[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int m = m0 + 8 * (r >> 2) + 4 * hi + (r & 3);
+    float a = 0.f;
+    if (m < p.M)
+      for (int z = 0; z < splits; ++z) a += p.part[z * mn + (long long)m * p.N + n];
+    acc[r] = a;
+  }
+  const int mrow = m0 + lq < p.M ? m0 + lq : p.M - 1;
+  const float16_t d = lora_tile(p.lt, p.lb, p.lr, mrow, n, hi);
+  const float rs = p.scale ? p.scale[n] : 1.0f;
+  const float bi = p.bias ? p.bias[n] : 0.0f;
+  const float gt = p.gate ? p.gate[p.gOff + n] : 1.0f;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int m = m0 + 8 * (r >> 2) + 4 * hi + (r & 3);
+    if (m >= p.M) continue;
+    float v = acc[r] * p.alpha;
+    v *= rs;
+    v += bi;
+    v += d[r];
+    if (p.act == NS2_ACT_SILU) v = silu(v);
+    else if (p.act == NS2_ACT_GELU_TANH) v = gelu_tanh(v);
+    float* c = p.C + p.cOff + (long long)m * p.ldc + n;
+    if (!p.resid) *c = v;
+    else *c = *c + gt * v;
+  }
+}
+
 // W [N, K] row-major int8 -> Wt tiles [N/64][K/64][8 k-chunks of 8][64 rows][8 bytes] of biased
 // bytes (w + 128); one thread per 8-byte chunk.
 __global__ __launch_bounds__(256) void tile_w_kernel(const int8_t* __restrict__ W, uint8_t* __restrict__ Wt,
@@ -645,7 +687,12 @@ int launch_tiled(TGemmArgs p, int splits = 1) {
   NS2_LAUNCHED("gemm_tiled");
   if (p.part) {
     const long long mn = (long long)p.M * p.N;
-    tiled_splitk_reduce_kernel<<<(unsigned)((mn + 255) / 256), 256, 0, s>>>(p, splits);
+    if (p.lr) {
+      const long long tiles32 = (long long)((p.M + 31) / 32) * (p.N / 32);
+      tiled_splitk_reduce_lora_kernel<<<(unsigned)((tiles32 + 3) / 4), 256, 0, s>>>(p, splits);
+    } else {
+      tiled_splitk_reduce_kernel<<<(unsigned)((mn + 255) / 256), 256, 0, s>>>(p, splits);
+    }
     NS2_LAUNCHED("gemm_tiled_splitk_reduce");
   }
   return NS2_OK;
