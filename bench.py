@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark: ms per 832x1216 int8 DiT pass + joint-attention TFLOP/s on one MI355X.
 
-  python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-dit] [--no-gemma] [--no-vendor]
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-dit] [--no-gemma] [--no-vendor] [--no-lora]
 
 Prints one JSON line. Legs, in order:
 
@@ -17,6 +17,8 @@ Prints one JSON line. Legs, in order:
    a profiled run of the same pass times every launch with stream events on the library's
    stream, and `roofline` is its algorithmic 2*M*N*K flops summed over the pass / its summed
    launch time, against the 2516.6 TFLOP/s dense fp16 MFMA peak.
+   `dit_lora` times the same pass with a synthetic rank-32 LoRA file on all 81 block linears
+   (the LoRA side path), beside it.
 2. Gemma3-270M text encoder (17 of 18 layers + final norm, 256 token ids, random-init bf16 weights
    of the real architecture) through the Node host (run_gemma.js), eager and replayed as a graph.
 3. Through the C ABI (ctypes), each after 1 s of back-to-back warm-up calls, timed with stream
@@ -130,6 +132,50 @@ def run_node(script, args, what, timeout=900):
 def run_dit(steps, warmup):
     return run_node(RUN_DIT, ["--synthetic", "3", "--shape", f"{H_IMG},{W_IMG},{T_TXT}",
                               "--warmup", str(warmup), "--reps", str(steps)], "run_dit.js")
+
+
+def write_lora(path, rank=32, seed=11):
+    """A synthetic LoRA file of the reference's PEFT format: rank `rank` on every block linear of
+    the pass (qkv_x, proj, w12 and w3 of the 18 blocks, kv_y of the 9 joint blocks: 81 modules),
+    bf16 A/B with std 0.05, alpha = rank / 2."""
+    import numpy as np
+    import torch
+    from safetensors.torch import save_file
+
+    rng = np.random.default_rng(seed)
+    mods = []
+    for b in range(BLOCKS):
+        mods += [(f"blocks.{b}.attn.qkv_x", 3 * D, D), (f"blocks.{b}.attn.proj", D, D),
+                 (f"blocks.{b}.mlp.w12", 2 * I_MLP, D), (f"blocks.{b}.mlp.w3", D, I_MLP)]
+        if b % 2 == 0:
+            mods.append((f"blocks.{b}.attn.kv_y", 2 * D, D))
+    out = {}
+    for name, n_out, n_in in mods:
+        base = "diffusion_model." + name
+        out[base + ".lora_A.weight"] = torch.from_numpy(
+            rng.standard_normal((rank, n_in), dtype=np.float32) * np.float32(0.05)).to(torch.bfloat16)
+        out[base + ".lora_B.weight"] = torch.from_numpy(
+            rng.standard_normal((n_out, rank), dtype=np.float32) * np.float32(0.05)).to(torch.bfloat16)
+        out[base + ".alpha"] = torch.tensor(rank / 2.0, dtype=torch.float32)
+    save_file(out, path)
+    return len(mods)
+
+
+def run_dit_lora(steps, warmup):
+    """The same pass with a rank-32 LoRA on all 81 block linears (the side path of
+    app/gpu/ops.js:70-87, attached as the pipeline attaches LoRA files)."""
+    import tempfile
+
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "lora_r32.safetensors")
+        n = write_lora(path)
+        r = run_node(RUN_DIT, ["--synthetic", "3", "--shape", f"{H_IMG},{W_IMG},{T_TXT}", "--warmup", str(warmup),
+                               "--reps", str(steps), "--lora", path], "run_dit.js --lora")
+    matched = sum(l["matched"] for l in r.get("loras", []))
+    if matched != n:
+        raise SystemExit(f"LoRA leg: {matched} of {n} modules matched")
+    return {"workload": f"the pass with a rank-32 LoRA (PEFT names, strength 1) on all {n} block linears",
+            "ms": r["ms_device_median"], "ms_queued": r.get("ms_device_queued_median"), "modules": n}
 
 
 def run_dit_profile():
@@ -543,6 +589,7 @@ def main():
     ap.add_argument("--no-dit", action="store_true", help="skip the DiT pass (kernels and CPU legs only)")
     ap.add_argument("--no-gemma", action="store_true", help="skip the text-encoder measurement")
     ap.add_argument("--no-vendor", action="store_true", help="skip the hipBLASLt / SDPA reference timings")
+    ap.add_argument("--no-lora", action="store_true", help="skip the pass with a rank-32 LoRA on every block linear")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a 256 MiB -> 256 MiB copy kernel (reference point for HBM counters)")
     args = ap.parse_args()
@@ -560,6 +607,11 @@ def main():
         gemm = gemm_roofline(kernels)
         log(f"DiT pass {dit['ms_device_median']:.3f} ms; int8 GEMMs {gemm['ms_per_pass']:.3f} ms/pass, "
             f"{gemm['tflops']:.1f} TFLOP/s")
+    dit_lora = None
+    if not args.no_dit and not args.no_lora:
+        dit_lora = run_dit_lora(args.steps, args.warmup)
+        dit_lora["overhead_ms"] = dit_lora["ms"] - dit["ms_device_median"]
+        log(f"DiT pass with LoRA {dit_lora['ms']:.3f} ms (+{dit_lora['overhead_ms']:.3f} ms)")
     gemma = None
     if not args.no_gemma:
         gemma = run_gemma(max(10, args.steps), max(3, args.warmup))
@@ -647,6 +699,7 @@ def main():
         "pass_ms_queued": dit.get("ms_device_queued_median") if dit else None,
         "pass_ms_host_to_host": dit["ms_host_to_host_median"] if dit else None,
         "weight_bytes": dit.get("weight_bytes") if dit else None,
+        "dit_lora": dit_lora,
         "joint_attention": attn,
         "joint_attention_768": attn0,
         "linear_int8_m2432": {"rows": lin1, "cpu_baseline": lin1_meta},
