@@ -805,7 +805,12 @@ int linear_tiled(const char* fn, bool wf16, const uint16_t* At, const void* Wt, 
   }
   switch (cfg) {
     case 0: return launch_tiled<256, 256, 4, 4>(p);
-    case 1: return launch_tiled<64, 128, 1, 4>(p, splits);
+    case 1:
+      // at most two blocks per CU (2432 x 1536 launches: 456 tiles) the copies' latency shows, and
+      // a third stage (48 KB, three blocks still fit) hides it: 2432 x 1536 x 6144 72.3 -> 69.6 us;
+      // at three blocks per CU (the DiT's 744-tile proj and w3) it costs more than it hides
+      if ((long long)((M + 63) / 64) * ((N + 127) / 128) <= 2 * kCUs) return launch_tiled<64, 128, 1, 4, 3>(p, splits);
+      return launch_tiled<64, 128, 1, 4>(p, splits);
     // three stages: at a few rows each block runs alone on its CU and its weights come from HBM,
     // so a deeper copy queue pays (text q/k/v 22.0 -> 17.0 us, text proj 15.4 -> 14.3 us in the
     // pass); LDS is no limit at one block per CU
