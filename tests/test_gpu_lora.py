@@ -53,8 +53,10 @@ def test_linear_i8_lora(ns2lib, M, N, K):
     assert_close(out.cpu(), ref, TOL, f"linear_i8_lora {M}x{N}x{K}")
 
 
-@pytest.mark.parametrize("M,N,K", [(300, 384, 768), (3952, 1536, 1536), (256, 3072, 1536)])
+@pytest.mark.parametrize("M,N,K", [(300, 384, 768), (3952, 1536, 1536), (256, 3072, 1536), (200, 1536, 1536)])
 def test_linear_i8_tiled_lora(ns2lib, M, N, K):
+    """(256, 3072) and (200, 1536) split K (fewer 64x64 tiles than CUs): the LoRA term is added
+    by the tile-wise reduce, 200 rows ending inside a 32-row tile."""
     g = gen(M + N + K + 2)
     x = torch.randn(M, K, generator=g)
     q, s = int8_weight(N, K, g)
@@ -105,7 +107,7 @@ def test_linear_i8_glu_rot_tiled_lora(ns2lib, M, N, K, act):
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 9216, 1536), (5, 1536, 256), (256, 640, 2048), (256, 1536, 640),
-                                   (3952, 1536, 1536)])
+                                   (3952, 1536, 1536), (17, 256, 80)])
 def test_linear_bf16_lora(ns2lib, M, N, K):
     """bf16 linears: GEMV (M <= 8), 64x64 tiles with K split over blocks (the LoRA term goes
     into the first split only), 128x128 tiles."""
@@ -122,6 +124,34 @@ def test_linear_bf16_lora(ns2lib, M, N, K):
     xd = x.double()
     ref = O.linear_bf16(xd, w, alpha=2.0, bias=bias.double(), add=O.lora_delta(xd, ents, N))
     assert_close(out.cpu(), ref, TOL, f"linear_bf16_lora {M}x{N}x{K}")
+
+
+@pytest.mark.parametrize("M,ranks", [(3952, (24, 40)), (250, (64, 100, 92))])
+def test_linear_i8_tiled_lora_ranks(ns2lib, M, ranks):
+    """Stacked ranks of 64 (3952 rows: 247 down-projection blocks of 16 rows, two 32-column slices
+    of t; the 64x128 launch with three stages) and 256 (250 rows: the rank split over eight
+    slices, rows ending inside a block; split K, the term added by the tile-wise reduce)."""
+    N, K = 768, 1536
+    g = gen(M + sum(ranks))
+    x = torch.randn(M, K, generator=g)
+    q, s = int8_weight(N, K, g)
+    ents = []
+    for i, r in enumerate(ranks):
+        n0, n = (0, N) if i == 0 else ((i * 128) % (N // 2), N // 2)
+        ents.append((torch.randn(r, K, generator=g) * 0.05, torch.randn(n, r, generator=g) * 0.3, 0.5 + 0.25 * i, n0, n))
+    la, lb, R = _packed(ents, N, K, rotate_a=True)
+    assert R == (64 if sum(ranks) <= 64 else 256)
+    xd, qd, sd = x.to(dev), q.to(dev), s.reshape(-1).to(dev)
+    wt = torch.empty(N * K, dtype=torch.int8, device=dev)
+    ns2lib.tile_i8_weight(qd, wt, N, K)
+    at = tiled_operand(M, K)
+    ns2lib.rotate_f16(xd, K, at, K, M, K, tiled=True)
+    out = torch.empty(M, N, device=dev)
+    ns2lib.linear_i8_tiled(at, wt, sd, out, M, N, K, lora=(la, lb, R))
+    torch.cuda.synchronize()
+    xr = x.double()
+    ref = O.linear_i8(xr, q, s.double(), add=O.lora_delta(xr, ents, N))
+    assert_close(out.cpu(), ref, TOL, f"linear_i8_tiled_lora ranks {ranks} at {M} rows")
 
 
 def test_lora_rank_errors(ns2lib):
