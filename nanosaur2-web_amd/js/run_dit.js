@@ -8,7 +8,8 @@
 // --inputs DIR holds inputs.json {h, w, sigma, T} and latent.f32 [64*h*w], context.f32
 // [T*640], weights.f32 [T]. --out writes the x0 prediction [64, h, w] as raw fp32.
 // With --reps, the pass is timed with the latent resident in device memory (stream events
-// and wall clock), and once more host-to-host (upload, pass, readback); one JSON line with
+// and wall clock), and as many times host-to-host (upload, pass, readback; the median, since a
+// lone host hiccup can double one sample); one JSON line with
 // the timings (and the per-op profile with --profile) is printed. The passes are timed twice:
 // one at a time (each waits for the previous to finish: `ms_device`), and queued (issued back
 // to back behind one untimed pass, with no wait between them: `ms_device_queued`), so that a
@@ -201,7 +202,7 @@ async function main() {
       report.profile = rows.map((r) => ({ name: r.name, count: r.count / a.reps, ms: r.ms / a.reps, tflops: r.flops ? r.flops / (r.ms / 1e3) / 1e12 : null }));
     }
     const host = [];
-    for (let i = 0; i < Math.min(3, a.reps); i++) {
+    for (let i = 0; i < a.reps; i++) {
       const w0 = process.hrtime.bigint();
       await dit.forward(inp.latent, h, w, text, sigma, { pathDrop: !!a.pathDrop });
       host.push(Number(process.hrtime.bigint() - w0) / 1e6);
