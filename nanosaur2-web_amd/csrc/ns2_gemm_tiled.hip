@@ -698,7 +698,7 @@ int launch_tiled(TGemmArgs p, int splits = 1) {
   return NS2_OK;
 }
 
-// Block-tile configurations (two LDS stages each, three for 64x64): BM x BN, the waves' layout, and two
+// Block-tile configurations: BM x BN, the waves' layout, and two
 // throughput figures fitted to measurements at the DiT shapes (3952 x {4608, 1536, 8192} x
 // {1536, 4096}, 256 x 3072 x 1536), in tile-area units per microsecond at K = 1536: `rate`
 // with the CUs full, `alone` for a CU that runs a single tile of this shape.

@@ -136,3 +136,49 @@ def test_js_copy_bounds(host):
     assert "released" in b["writeReleased"]
     assert "do not fit shape" in b["fromArrayShape"]
     assert "requested from a tensor of 6" in b["readCount"]
+
+
+def _bench_module():
+    import importlib.util
+
+    spec = importlib.util.spec_from_file_location("bench_under_test", os.path.join(ROOT, "bench.py"))
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def test_bench_refuses_several_gpus():
+    p = subprocess.run(["python3", os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                       timeout=120)
+    assert p.returncode == 2
+    assert "one GPU" in p.stderr
+
+
+def test_bench_lora_file(tmp_path):
+    """The LoRA file of bench.py's dit_lora leg: PEFT names of every block linear (qkv_x, proj,
+    w12, w3 of the 18 blocks, kv_y of the 9 joint blocks), rank 32, alpha 16, bf16 A/B of the
+    modules' shapes."""
+    from safetensors.torch import load_file
+
+    b = _bench_module()
+    path = str(tmp_path / "lora.safetensors")
+    n = b.write_lora(path)
+    assert n == 81
+    t = load_file(path)
+    assert len(t) == 3 * 81
+    D, I = b.D, b.I_MLP
+    shapes = {"attn.qkv_x": (3 * D, D), "attn.proj": (D, D), "mlp.w12": (2 * I, D), "mlp.w3": (D, I), "attn.kv_y": (2 * D, D)}
+    seen = set()
+    for key, v in t.items():
+        m = re.fullmatch(r"diffusion_model\.blocks\.(\d+)\.(attn\.\w+|mlp\.\w+)\.(lora_A\.weight|lora_B\.weight|alpha)", key)
+        assert m, key
+        blk, mod, part = int(m.group(1)), m.group(2), m.group(3)
+        assert 0 <= blk < b.BLOCKS and (mod != "attn.kv_y" or blk % 2 == 0), key
+        n_out, n_in = shapes[mod]
+        if part == "alpha":
+            assert v.dtype == torch.float32 and float(v) == 16.0
+        else:
+            assert v.dtype == torch.bfloat16
+            assert tuple(v.shape) == ((32, n_in) if part == "lora_A.weight" else (n_out, 32)), key
+        seen.add((blk, mod))
+    assert len(seen) == 81
