@@ -228,6 +228,14 @@ int ns2_linear_f16w_tiled_lora(const uint16_t* At, const uint16_t* Wt, const flo
 int ns2_attention_rows(const float* q, const float* k, const float* v, float* o, int Lq, int Lk,
                        int H, int D, int ldq, int ldk, int ldv, int ldo, long long qOff,
                        long long kOff, long long vOff, int group, int causal);
+/* ns2_attention_rows with K and V stored as fp16 (ldk, ldv, kOff, vOff counted in fp16
+ * elements), as ns2_linear_bf16_head_norm_f16kv writes them. The products take fp16 operands on
+ * either entry, so for K/V that are the fp16 roundings of ns2_attention_rows' fp32 K/V the
+ * outputs are the same bit for bit. D a multiple of 16 up to 256; q rows and the K/V rows
+ * 16-byte aligned. Additive to the reference interface. */
+int ns2_attention_rows_f16kv(const float* q, const uint16_t* k, const uint16_t* v, float* o, int Lq, int Lk,
+                             int H, int D, int ldq, int ldk, int ldv, int ldo, long long qOff,
+                             long long kOff, long long vOff, int group, int causal);
 
 /* ---- attention (ops.attention, app/gpu/ops.js:199-209; flashAttentionShader,
  *      app/gpu/kernels.js:119-305) ----------------------------------------------------------
@@ -395,6 +403,15 @@ int ns2_add_rmsnorm(float* x, const float* a, const float* w_add, const float* w
 int ns2_linear_bf16_head_norm(const float* A, int lda, const uint16_t* W, const float* bias, float* C, int M, int N,
                               int K, const float* w1, int H1, const float* w2, int H2, int D, const float* cs,
                               long long sin_off, int rope_rows, float eps);
+/* ns2_linear_bf16_head_norm with heads [H1, N/D) (the keys and values) stored as fp16 at
+ * kv16[m*ldkv + (h - H1)*D + i] (each fp32 result rounded to nearest once) instead of fp32 in
+ * C; C receives heads [0, H1) only. kv16 may point into C's rows past column H1*D (ldkv = 2*N):
+ * those fp32 columns are not written. Feeds ns2_attention_rows_f16kv. Additive to the reference
+ * interface. */
+int ns2_linear_bf16_head_norm_f16kv(const float* A, int lda, const uint16_t* W, const float* bias, float* C, int M,
+                                    int N, int K, const float* w1, int H1, const float* w2, int H2, int D,
+                                    const float* cs, long long sin_off, int rope_rows, float eps, uint16_t* kv16,
+                                    int ldkv);
 /* A gate/up projection and its GLU without the [M, N] product in HBM: t = A W^T (+ bias), then
  * Y[m][i] = act(t[m][i]) * t[m][N/2 + i] (ns2_linear_bf16 + ns2_glu; the Gemma3 MLP's fused
  * gate/up weight, app/models/gemma3.js:79-82). W bf16 [N, K] with the gate rows first; Y fp32

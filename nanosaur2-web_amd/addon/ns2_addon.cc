@@ -654,6 +654,23 @@ napi_value AttentionRows(napi_env env, napi_callback_info info) {
   return check(env, c, ns2_attention_rows(q, k, v, o, Lq, Lk, H, D, ldq, ldk, ldv, ldo, qOff, kOff, vOff, group, causal));
 }
 
+// attentionRowsF16kv(q, k, v, o, Lq, Lk, H, D, ldq, ldk, ldv, ldo, qOff, kOff, vOff, group, causal):
+// k and v fp16, their strides and offsets in fp16 elements
+napi_value AttentionRowsF16kv(napi_env env, napi_callback_info info) {
+  ARGS(17);
+  auto q = (const float*)c.ptr(0);
+  auto k = (const uint16_t*)c.ptr(1);
+  auto v = (const uint16_t*)c.ptr(2);
+  auto o = (float*)c.ptr(3);
+  int Lq = c.i32(4), Lk = c.i32(5), H = c.i32(6), D = c.i32(7);
+  int ldq = c.i32(8), ldk = c.i32(9), ldv = c.i32(10), ldo = c.i32(11);
+  long long qOff = c.i64(12), kOff = c.i64(13), vOff = c.i64(14);
+  int group = c.i32(15), causal = c.i32(16);
+  if (c.failed) return nullptr;
+  return check(env, c,
+               ns2_attention_rows_f16kv(q, k, v, o, Lq, Lk, H, D, ldq, ldk, ldv, ldo, qOff, kOff, vOff, group, causal));
+}
+
 // headNorm(X, w, L, H, D, ld, colOff, rowOff, cs, sinOff, eps)
 napi_value HeadNorm(napi_env env, napi_callback_info info) {
   ARGS(11);
@@ -845,6 +862,30 @@ napi_value LinearBf16HeadNorm(napi_env env, napi_callback_info info) {
   return check(env, c, ns2_linear_bf16_head_norm(A, lda, W, bias, C, M, N, K, w1, H1, w2, H2, D, cs, sinOff, ropeRows, eps));
 }
 
+// linearBf16HeadNormF16kv(A, lda, W, bias, C, M, N, K, w1, H1, w2, H2, D, cs, sinOff, ropeRows, eps, kv16, ldkv)
+napi_value LinearBf16HeadNormF16kv(napi_env env, napi_callback_info info) {
+  ARGS(19);
+  auto A = (const float*)c.ptr(0);
+  int lda = c.i32(1);
+  auto W = (const uint16_t*)c.ptr(2);
+  auto bias = (const float*)c.ptr(3);
+  auto C = (float*)c.ptr(4);
+  int M = c.i32(5), N = c.i32(6), K = c.i32(7);
+  auto w1 = (const float*)c.ptr(8);
+  int H1 = c.i32(9);
+  auto w2 = (const float*)c.ptr(10);
+  int H2 = c.i32(11), D = c.i32(12);
+  auto cs = (const float*)c.ptr(13);
+  long long sinOff = c.i64(14);
+  int ropeRows = c.i32(15);
+  float eps = c.f32(16);
+  auto kv16 = (uint16_t*)c.ptr(17);
+  int ldkv = c.i32(18);
+  if (c.failed) return nullptr;
+  return check(env, c, ns2_linear_bf16_head_norm_f16kv(A, lda, W, bias, C, M, N, K, w1, H1, w2, H2, D, cs, sinOff,
+                                                       ropeRows, eps, kv16, ldkv));
+}
+
 // linearBf16AddRmsnorm(A, lda, W, bias, x, wAdd, wOut, y, M, N, K, eps)
 napi_value LinearBf16AddRmsnorm(napi_env env, napi_callback_info info) {
   ARGS(12);
@@ -879,14 +920,15 @@ napi_value Module(napi_env env, napi_value exports) {
       {"tileBf16Weight", TileBf16Weight}, {"linearF16wTiled", LinearF16wTiled}, {"toTiledF16", ToTiledF16},
       {"normModF16", NormModF16},
       {"linearI8", LinearI8}, {"linearBf16", LinearBf16}, {"attention", Attention},
-      {"attentionRows", AttentionRows}, {"attentionText", AttentionText},
+      {"attentionRows", AttentionRows}, {"attentionRowsF16kv", AttentionRowsF16kv}, {"attentionText", AttentionText},
       {"linearI8TiledVpack", LinearI8TiledVpack}, {"attentionVpackBytes", AttentionVpackBytes},
       {"attentionVpacked", AttentionVpacked},
       {"headNorm", HeadNorm}, {"headNorm2", HeadNorm2}, {"normMod", NormModT<false>}, {"normModRotateF16", NormModT<true>},
       {"glu", GluT<false>}, {"gluRotateF16", GluT<true>}, {"elementwise", Elementwise},
       {"accumulate", Accumulate}, {"addRows", AddRows}, {"rowSum", RowSum}, {"rmsnorm", Rmsnorm},
       {"addRmsnorm", AddRmsnorm}, {"linearBf16AddRmsnorm", LinearBf16AddRmsnorm},
-      {"linearBf16Glu", LinearBf16Glu}, {"linearBf16HeadNorm", LinearBf16HeadNorm}, {"transpose", Transpose},
+      {"linearBf16Glu", LinearBf16Glu}, {"linearBf16HeadNorm", LinearBf16HeadNorm},
+      {"linearBf16HeadNormF16kv", LinearBf16HeadNormF16kv}, {"transpose", Transpose},
   };
   for (const Fn& f : fns) {
     napi_value fn;

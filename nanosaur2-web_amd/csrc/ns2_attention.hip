@@ -1442,6 +1442,197 @@ __global__ __launch_bounds__(64 * NW) void attn_rows_mfma_kernel(RowsArgs a) {
   }
 }
 
+// attn_rows_mfma_kernel with K and V stored as fp16 (the values its fp32 path converts before
+// every product, so the results are the same bit for bit): half the bytes per key, and each
+// wave issues the loads of two of its key blocks (kb and kb + NW) before it uses either, so a
+// query block at a few hundred keys costs one round trip to memory instead of two. The blocks
+// are then consumed in the order of the fp32 kernel, so every wave's online softmax sees the
+// same sequence. At D = 256 the K rows go through LDS: one direct copy of 512 bytes (32 lanes)
+// per key row, rows padded by 16 bytes, so the 8-byte fragment reads of 16 rows by 32 lanes fall
+// in 64 different banks.
+struct RowsArgsH {
+  const float* q;
+  const half_t* k;
+  const half_t* v;
+  float* o;
+  long long qOff, kOff, vOff;  // k, v offsets and strides in fp16 elements
+  int Lq, Lk, H, D, ldq, ldk, ldv, ldo, group, causal;
+  float scale;
+};
+
+template <int DB, int NW>
+__global__ __launch_bounds__(64 * NW) void attn_rows_h_kernel(RowsArgsH a) {
+  constexpr int D = 16 * DB;
+  constexpr bool KDMA = D == 256;
+  constexpr int RS = D * 2 + 16;                       // padded fp16 K row in LDS (bytes)
+  constexpr int KST = KDMA ? 2 * 16 * RS : 0;          // K rows of one wave's two key blocks
+  constexpr int OPB = NW * DB * 64 * 16;               // the partial outputs
+  constexpr int SM = NW * KST > OPB ? NW * KST : OPB;  // K rows in the loop, then o_part
+  __shared__ __attribute__((aligned(16))) char smem[SM];
+  float4(*o_part)[DB][64] = reinterpret_cast<float4(*)[DB][64]>(smem);
+  __shared__ float m_part[NW][16], l_part[NW][16];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int h = blockIdx.y;
+  const int q0 = (gridDim.x - 1 - blockIdx.x) * 16;
+  const int col = lane & 15, grp = lane >> 4;
+  const int g = h / a.group;
+  const int qi = q0 + col;
+  const bool qvalid = qi < a.Lq;
+
+  __shared__ half4_t q_lds[DB][64];
+  {
+    const float* qr = a.q + a.qOff + (long long)(qvalid ? qi : a.Lq - 1) * a.ldq + (long long)h * D + 4 * grp;
+    for (int t = wave; t < DB; t += NW) {
+      const float4 x = *reinterpret_cast<const float4*>(qr + 16 * t);
+      q_lds[t][lane] = half4_t{(half_t)(x.x * a.scale), (half_t)(x.y * a.scale), (half_t)(x.z * a.scale),
+                               (half_t)(x.w * a.scale)};
+    }
+  }
+  __syncthreads();
+  const half_t* kb0 = a.k + a.kOff + (long long)g * D;
+  const half_t* vb0 = a.v + a.vOff + (long long)g * D;
+
+  float4_t o[DB];
+#pragma unroll
+  for (int t = 0; t < DB; ++t) o[t] = float4_t{0.f, 0.f, 0.f, 0.f};
+  float m = -INFINITY, lsum = 0.f;
+
+  const int qlast = (q0 + 15 < a.Lq ? q0 + 15 : a.Lq - 1);
+  int nkb = (a.Lk + 15) / 16;
+  if (a.causal && qlast / 16 + 1 < nkb) nkb = qlast / 16 + 1;
+
+  // the loads of key block kb into slot u: K rows (LDS at D = 256, else registers) and the V^T
+  // operand values (row col: d = DB col + t of keys key0 + j)
+  auto load = [&](int kb, int u, half4_t (&kx)[DB], half_t (&vh)[4][DB]) {
+    if constexpr (KDMA) {
+      const uint32_t kst = lds_addr(smem) + wave * KST + u * 16 * RS;
+      if (lane < D / 8) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = kb * 16 + r;
+          dma16(kb0 + (long long)(key < a.Lk ? key : a.Lk - 1) * a.ldk + 8 * lane,
+                __builtin_amdgcn_readfirstlane(kst + r * RS));
+        }
+      }
+    } else {
+      const int kr = kb * 16 + col;
+      const half_t* krow = kb0 + (long long)(kr < a.Lk ? kr : a.Lk - 1) * a.ldk + 4 * grp;
+#pragma unroll
+      for (int t = 0; t < DB; ++t) kx[t] = *reinterpret_cast<const half4_t*>(krow + 16 * t);
+    }
+    const int key0 = kb * 16 + 4 * grp;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const half_t* vr = vb0 + DB * col + (long long)(key0 + j < a.Lk ? key0 + j : a.Lk - 1) * a.ldv;
+      if constexpr (DB % 8 == 0) {
+#pragma unroll
+        for (int t8 = 0; t8 < DB; t8 += 8) {
+          const half8_t x = *reinterpret_cast<const half8_t*>(vr + t8);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) vh[j][t8 + e] = x[e];
+        }
+      } else if constexpr (DB % 4 == 0) {
+#pragma unroll
+        for (int t4 = 0; t4 < DB; t4 += 4) {
+          const half4_t x = *reinterpret_cast<const half4_t*>(vr + t4);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) vh[j][t4 + e] = x[e];
+        }
+      } else {
+#pragma unroll
+        for (int t = 0; t < DB; ++t) vh[j][t] = vr[t];
+      }
+    }
+  };
+  // one key block's scores, softmax update and PV products (the arithmetic of the fp32 kernel)
+  auto consume = [&](int kb, int u, half4_t (&kx)[DB], const half_t (&vh)[4][DB]) {
+    if constexpr (KDMA) {
+      const char* kst_p = smem + wave * KST + u * 16 * RS;
+#pragma unroll
+      for (int t = 0; t < DB; ++t) kx[t] = *reinterpret_cast<const half4_t*>(kst_p + col * RS + (16 * t + 4 * grp) * 2);
+    }
+    float4_t s = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < DB; ++t) s = __builtin_amdgcn_mfma_f32_16x16x16f16(kx[t], q_lds[t][lane], s, 0, 0, 0);
+    const int key0 = kb * 16 + 4 * grp;
+    float bm = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int key = key0 + j;
+      if (key >= a.Lk || (a.causal && key > qi)) s[j] = -INFINITY;
+      bm = fmaxf(bm, s[j]);
+    }
+    bm = fmaxf(bm, __shfl_xor(bm, 16));
+    bm = fmaxf(bm, __shfl_xor(bm, 32));
+    const float mn = fmaxf(m, bm);
+    const float corr = mn == -INFINITY ? 1.f : exp2f(m - mn);
+    float p[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) p[j] = mn == -INFINITY ? 0.f : exp2f(s[j] - mn);
+    lsum = lsum * corr + ((p[0] + p[1]) + (p[2] + p[3]));
+    m = mn;
+    const half4_t pf = half4_t{(half_t)p[0], (half_t)p[1], (half_t)p[2], (half_t)p[3]};
+#pragma unroll
+    for (int t = 0; t < DB; ++t) {
+      const half4_t vf = half4_t{vh[0][t], vh[1][t], vh[2][t], vh[3][t]};
+      o[t] *= corr;
+      o[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(vf, pf, o[t], 0, 0, 0);
+    }
+  };
+
+  for (int kb = wave; kb < nkb; kb += 2 * NW) {
+    asm volatile("" ::: "memory");
+    const bool two = kb + NW < nkb;  // uniform per wave
+    half4_t kx0[DB], kx1[DB];
+    half_t vh0[4][DB], vh1[4][DB];
+    load(kb, 0, kx0, vh0);
+    if (two) load(kb + NW, 1, kx1, vh1);
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (KDMA) {
+      // this wave's K rows have landed (it alone reads them)
+      vm_wait<0>();
+      asm volatile("" ::: "memory");
+    }
+    consume(kb, 0, kx0, vh0);
+    if (two) consume(kb + NW, 1, kx1, vh1);
+  }
+  lsum += __shfl_xor(lsum, 16);
+  lsum += __shfl_xor(lsum, 32);
+  if constexpr (KDMA) __syncthreads();  // every wave is done with its K rows (o_part overlays them)
+
+#pragma unroll
+  for (int t = 0; t < DB; ++t) o_part[wave][t][lane] = make_float4(o[t][0], o[t][1], o[t][2], o[t][3]);
+  if (grp == 0) {
+    m_part[wave][col] = m;
+    l_part[wave][col] = lsum;
+  }
+  __syncthreads();
+  if (!qvalid) return;
+  float M = m_part[0][col];
+#pragma unroll
+  for (int w = 1; w < NW; ++w) M = fmaxf(M, m_part[w][col]);  // finite: wave 0 sees key 0
+  float sc[NW], L = 0.f;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    sc[w] = exp2f(m_part[w][col] - M);
+    L += sc[w] * l_part[w][col];
+  }
+  const float inv = 1.0f / L;
+  constexpr int F = 4 * DB, FW = (F + NW - 1) / NW;
+  float* orow = a.o + (long long)qi * a.ldo + (long long)h * D + F * grp;
+#pragma unroll
+  for (int u = 0; u < FW; ++u) {
+    const int f = wave * FW + u;
+    if (f < F) {
+      const int j = f / DB, t = f % DB;
+      float r = 0.f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) r += sc[w] * reinterpret_cast<const float*>(&o_part[w][t][lane])[j];
+      orow[f] = r * inv;
+    }
+  }
+}
+
 }  // namespace
 
 extern "C" int ns2_attention_rows(const float* q, const float* k, const float* v, float* o, int Lq, int Lk,
@@ -1487,6 +1678,41 @@ extern "C" int ns2_attention_rows(const float* q, const float* k, const float* v
   else if (dv == 3) attn_rows_kernel<3><<<grid, block, 0, s>>>(a);
   else attn_rows_kernel<4><<<grid, block, 0, s>>>(a);
   NS2_LAUNCHED("attn_rows");
+  return NS2_OK;
+}
+
+extern "C" int ns2_attention_rows_f16kv(const float* q, const uint16_t* k, const uint16_t* v, float* o, int Lq,
+                                        int Lk, int H, int D, int ldq, int ldk, int ldv, int ldo, long long qOff,
+                                        long long kOff, long long vOff, int group, int causal) {
+  NS2_READY();
+  if (Lq <= 0 || H <= 0) return NS2_OK;
+  NS2_REQUIRE(q && k && v && o, "ns2_attention_rows_f16kv: null q, k, v or o");
+  NS2_REQUIRE(D > 0 && D <= 256 && D % 16 == 0, "ns2_attention_rows_f16kv: head dim %d is not a multiple of 16 up to 256",
+              D);
+  NS2_REQUIRE(group > 0 && H % group == 0, "ns2_attention_rows_f16kv: H=%d is not a multiple of group=%d", H, group);
+  NS2_REQUIRE(Lk > 0 && ldq >= H * D && ldk >= H / group * D && ldv >= H / group * D && ldo >= H * D && qOff >= 0 &&
+                  kOff >= 0 && vOff >= 0,
+              "ns2_attention_rows_f16kv: bad sizes or strides");
+  // 16-byte rows: q as fp32 (strides and offset multiples of 4), k and v as fp16 (multiples of 8)
+  NS2_REQUIRE(aligned16(q) && aligned16(k) && aligned16(v) && ldq % 4 == 0 && qOff % 4 == 0 && ldk % 8 == 0 &&
+                  ldv % 8 == 0 && kOff % 8 == 0 && vOff % 8 == 0,
+              "ns2_attention_rows_f16kv: q, k and v rows must be 16-byte aligned");
+  RowsArgsH a{q, reinterpret_cast<const half_t*>(k), reinterpret_cast<const half_t*>(v), o, qOff, kOff, vOff, Lq, Lk,
+              H, D, ldq, ldk, ldv, ldo, group, causal ? 1 : 0, 1.0f / sqrtf((float)D) * kLog2e};
+  ns2::ProfScope prof_("attn_rows");
+  hipStream_t s = ns2::stream();
+  const dim3 grid((Lq + 15) / 16, H);
+  switch (D / 16) {
+#define NS2_ROWS_H_CASE(N) \
+  case N: attn_rows_h_kernel<N, kRowsWaves><<<grid, 64 * kRowsWaves, 0, s>>>(a); break;
+    NS2_ROWS_H_CASE(1) NS2_ROWS_H_CASE(2) NS2_ROWS_H_CASE(3) NS2_ROWS_H_CASE(4) NS2_ROWS_H_CASE(5)
+    NS2_ROWS_H_CASE(6) NS2_ROWS_H_CASE(7) NS2_ROWS_H_CASE(8) NS2_ROWS_H_CASE(9) NS2_ROWS_H_CASE(10)
+    NS2_ROWS_H_CASE(11) NS2_ROWS_H_CASE(12) NS2_ROWS_H_CASE(13) NS2_ROWS_H_CASE(14) NS2_ROWS_H_CASE(15)
+    NS2_ROWS_H_CASE(16)
+#undef NS2_ROWS_H_CASE
+    default: break;
+  }
+  NS2_LAUNCHED("attn_rows_h");
   return NS2_OK;
 }
 

@@ -365,6 +365,8 @@ __global__ __launch_bounds__(256) void splitk_add_rmsnorm_kernel(GemmArgs p, int
 // [H1, H1 + H2) with w2, then split-half RoPE on rows < rope_rows (pair i, i + D/2; cos at
 // cs[row*D/2 + i], sin at cs[sin_off + row*D/2 + i]); the remaining heads (the values) are stored
 // as summed. The splits are added in split order, as splitk_reduce_kernel adds them.
+// With kv16 set, heads h >= H1 (the keys and values) are stored as fp16 at
+// kv16[row*ldkv + (h - H1)*D + i] instead of fp32 in C: the fp32 value rounded once to nearest.
 struct HeadNorm {
   const float* w1;
   int H1;
@@ -374,6 +376,8 @@ struct HeadNorm {
   long long sin_off;
   int rope_rows;
   float eps;
+  half_t* kv16;
+  long long ldkv;
 };
 constexpr int kHeadNormMaxHeads = 8;
 template <int D>
@@ -415,7 +419,13 @@ __global__ __launch_bounds__(D) void splitk_head_norm_kernel(GemmArgs p, int spl
         __syncthreads();
       }
     }
-    out[(long long)h * D] = r;
+    if (hn.kv16 && h >= hn.H1) {  // uniform per block
+      // the fp32 value as the fp32 store would hold it (no multiply-add fused with the conversion)
+      asm volatile("" : "+v"(r));
+      hn.kv16[m * hn.ldkv + (long long)(h - hn.H1) * D + tid] = (half_t)r;
+    } else {
+      out[(long long)h * D] = r;
+    }
   }
 }
 
@@ -948,22 +958,44 @@ int ns2_linear_bf16_add_rmsnorm(const float* A, int lda, const uint16_t* W, cons
   return launch_gemm<true, true>(p, "linear_bf16_add_rmsnorm", &rn);
 }
 
+namespace {
+
+int linear_bf16_head_norm(const char* fn, const char* name, const float* A, int lda, const uint16_t* W, const float* bias, float* C,
+                          int M, int N, int K, const float* w1, int H1, const float* w2, int H2, int D, const float* cs,
+                          long long sin_off, int rope_rows, float eps, uint16_t* kv16, int ldkv) {
+  NS2_READY();
+  if (M == 0) return NS2_OK;
+  NS2_REQUIRE(D == 64 || D == 128 || D == 256, "%s: head dim %d is not 64, 128 or 256", fn, D);
+  NS2_REQUIRE(N % D == 0 && N / D <= kHeadNormMaxHeads && H1 >= 0 && H2 >= 0 && (H1 + H2) * D <= N &&
+                  (!H1 || w1) && (!H2 || w2),
+              "%s: N=%d (at most %d heads of %d), H1=%d, H2=%d or their weights", fn, N, kHeadNormMaxHeads, D, H1,
+              H2);
+  NS2_REQUIRE(C != A, "%s: C must not alias A", fn);
+  if (kv16) NS2_REQUIRE(ldkv >= N - H1 * D, "%s: ldkv=%d is below the %d fp16 key/value columns", fn, ldkv, N - H1 * D);
+  GemmArgs p{A, W, nullptr, bias, nullptr, C, nullptr, 0, 0, lda, N, M, N, K, 1.0f, NS2_ACT_NONE, 0};
+  int rc = check_common(p, fn);
+  if (rc) return rc;
+  const HeadNorm hn{w1, H1, w2, H2, D, cs, sin_off, cs ? rope_rows : 0, eps, reinterpret_cast<half_t*>(kv16), ldkv};
+  return launch_gemm<true, true>(p, name, nullptr, nullptr, 0, &hn);
+}
+
+}  // namespace
+
 int ns2_linear_bf16_head_norm(const float* A, int lda, const uint16_t* W, const float* bias, float* C, int M, int N,
                               int K, const float* w1, int H1, const float* w2, int H2, int D, const float* cs,
                               long long sin_off, int rope_rows, float eps) {
+  return linear_bf16_head_norm("ns2_linear_bf16_head_norm", "linear_bf16_head_norm", A, lda, W, bias, C, M, N, K, w1, H1, w2, H2, D, cs,
+                               sin_off, rope_rows, eps, nullptr, 0);
+}
+
+int ns2_linear_bf16_head_norm_f16kv(const float* A, int lda, const uint16_t* W, const float* bias, float* C, int M,
+                                    int N, int K, const float* w1, int H1, const float* w2, int H2, int D,
+                                    const float* cs, long long sin_off, int rope_rows, float eps, uint16_t* kv16,
+                                    int ldkv) {
   NS2_READY();
-  if (M == 0) return NS2_OK;
-  NS2_REQUIRE(D == 64 || D == 128 || D == 256, "ns2_linear_bf16_head_norm: head dim %d is not 64, 128 or 256", D);
-  NS2_REQUIRE(N % D == 0 && N / D <= kHeadNormMaxHeads && H1 >= 0 && H2 >= 0 && (H1 + H2) * D <= N &&
-                  (!H1 || w1) && (!H2 || w2),
-              "ns2_linear_bf16_head_norm: N=%d (at most %d heads of %d), H1=%d, H2=%d or their weights", N,
-              kHeadNormMaxHeads, D, H1, H2);
-  NS2_REQUIRE(C != A, "ns2_linear_bf16_head_norm: C must not alias A");
-  GemmArgs p{A, W, nullptr, bias, nullptr, C, nullptr, 0, 0, lda, N, M, N, K, 1.0f, NS2_ACT_NONE, 0};
-  int rc = check_common(p, "ns2_linear_bf16_head_norm");
-  if (rc) return rc;
-  const HeadNorm hn{w1, H1, w2, H2, D, cs, sin_off, cs ? rope_rows : 0, eps};
-  return launch_gemm<true, true>(p, "linear_bf16_head_norm", nullptr, nullptr, 0, &hn);
+  NS2_REQUIRE(kv16 || M == 0, "ns2_linear_bf16_head_norm_f16kv: null kv16");
+  return linear_bf16_head_norm("ns2_linear_bf16_head_norm_f16kv", "linear_bf16_head_norm", A, lda, W, bias, C, M, N, K, w1, H1, w2, H2, D,
+                               cs, sin_off, rope_rows, eps, kv16, ldkv);
 }
 
 int ns2_linear_bf16_glu(const float* A, int lda, const uint16_t* W, const float* bias, float* Y, int M, int N,

@@ -97,12 +97,18 @@ export class Gemma3 {
       const cs = l.global ? csGlobal : csLocal;
       // [Lt, q 1024 | k 256 | v 256], the q heads and then the k head normed and rotated in the
       // projection's split-K sum
-      const qkv = ops.linearHeadNorm(gpu, h, l.qkv, l.qn, H, l.kn, KH, { D: HD, cs });
+      // (on the fused path the k and v heads are stored as fp16, the attention's operand type)
+      const qkv = ops.linearHeadNorm(gpu, h, l.qkv, l.qn, H, l.kn, KH, { D: HD, cs, f16kv: true });
       h.release();
-      const a = ops.attention(gpu, {
-        q: qkv, k: qkv, v: qkv, Lq: Lt, Lk: Lt, H, D: HD, ldq: qkvW, ldk: qkvW, ldv: qkvW,
-        qOff: 0, kOff: H * HD, vOff: (H + KH) * HD, group: H / KH, causal: true,
-      });
+      const a = qkv.f16kv
+        ? ops.attentionRowsF16kv(gpu, {
+          q: qkv, kv: qkv, Lq: Lt, Lk: Lt, H, D: HD, ldq: qkvW, qOff: 0, kOff: qkv.f16kv.off,
+          vOff: qkv.f16kv.off + KH * HD, ldkv: qkv.f16kv.ld, group: H / KH, causal: true,
+        })
+        : ops.attention(gpu, {
+          q: qkv, k: qkv, v: qkv, Lq: Lt, Lk: Lt, H, D: HD, ldq: qkvW, ldk: qkvW, ldv: qkvW,
+          qOff: 0, kOff: H * HD, vOff: (H + KH) * HD, group: H / KH, causal: true,
+        });
       qkv.release();
       const h2 = ops.linearAddRmsnorm(gpu, a, l.o, x, l.postAttnNorm, l.preMlpNorm);
       a.release();

@@ -243,7 +243,11 @@ export function linearGlu(gpu, a, W, act) {
 // linear(a, W) of a stacked q|k|v weight followed by headNorm2 on its q and k heads (Gemma3,
 // app/models/gemma3.js:62-67; addition to the reference ops): for a bf16 weight without LoRA the
 // split-K sums are normed (and rotated) in the same row kernel, else the two ops run.
-export function linearHeadNorm(gpu, a, W, w1, H1, w2, H2, { D, cs = null, eps = 1e-6 }) {
+// f16kv: on the fused path, heads from H1 on (keys and values) are written as fp16 into the
+// front half of their own fp32 columns (fp16 column 2*H1*D + j of each row, row stride 2*W.N fp16
+// elements), and the result carries .f16kv = { off, ld } in fp16 elements for
+// attentionRowsF16kv; the fp32 columns of those heads are then not written.
+export function linearHeadNorm(gpu, a, W, w1, H1, w2, H2, { D, cs = null, eps = 1e-6, f16kv = false }) {
   const M = a.size / W.K;
   if (W.kind !== "bf16" || (W.lora && W.lora.length)) {
     const t = linear(gpu, a, W, { name: "te.qkv" });
@@ -251,10 +255,30 @@ export function linearHeadNorm(gpu, a, W, w1, H1, w2, H2, { D, cs = null, eps = 
     return t;
   }
   const y = gpu.empty([M, W.N]);
+  if (f16kv) {
+    const kv16 = addr(y) + BigInt(H1 * D * 4);
+    gpu.run("te.qkv+head_norm", 2 * M * W.N * W.K, () =>
+      native.linearBf16HeadNormF16kv(addr(a), W.K, addr(W.buf), addr(W.bias || null), addr(y), M, W.N, W.K,
+        addr(w1), H1, addr(w2), H2, D, cs ? addr(cs) : null, cs ? cs.sinOff : 0, cs ? M : 0, eps, kv16, 2 * W.N));
+    y.f16kv = { off: 2 * H1 * D, ld: 2 * W.N };
+    return y;
+  }
   gpu.run("te.qkv+head_norm", 2 * M * W.N * W.K, () =>
     native.linearBf16HeadNorm(addr(a), W.K, addr(W.buf), addr(W.bias || null), addr(y), M, W.N, W.K, addr(w1), H1,
       addr(w2), H2, D, cs ? addr(cs) : null, cs ? cs.sinOff : 0, cs ? M : 0, eps));
   return y;
+}
+
+// The materialized-path attention (causal / grouped, as attention() runs it) on fp16 keys and
+// values: kv is a Tensor whose bytes hold them, kOff / vOff / ldkv in fp16 elements (the
+// .f16kv layout of linearHeadNorm); q fp32 as in attention(). Output [Lq, H*D].
+export function attentionRowsF16kv(gpu, { q, kv, Lq, Lk, H, D, ldq, qOff = 0, kOff, vOff, ldkv, group = 1,
+  causal = false, out }) {
+  const o = out || gpu.empty([Lq, H * D]);
+  gpu.run("attn.rows", 4 * Lq * Lk * D * H, () =>
+    native.attentionRowsF16kv(addr(q), addr(kv), addr(kv), addr(o), Lq, Lk, H, D, ldq, ldkv, ldkv, H * D, qOff, kOff,
+      vOff, group, causal ? 1 : 0));
+  return o;
 }
 
 // linear(a, W) followed by addRmsnorm(x, ., wAdd, wOut) for a bf16 weight without LoRA: the

@@ -192,11 +192,14 @@ async function main() {
       await gpu.sync();
       const dev = [];
       for (let i = 0; i < a.reps; i++) dev.push(native.eventElapsed(evs[2 * i], evs[2 * i + 1]));
-      process.stderr.write(`[run_dit] queued passes: ${dev.map((d) => d.toFixed(3)).join(" ")} ms\n`);
-      return dev;
+      // the whole run of passes, first start to last end: any gap the host leaves between passes counts
+      const total = native.eventElapsed(evs[0], evs[2 * a.reps - 1]);
+      process.stderr.write(`[run_dit] queued passes: ${dev.map((d) => d.toFixed(3)).join(" ")} ms; ` +
+                           `${a.reps} passes in ${total.toFixed(3)} ms\n`);
+      return { devQ: dev, total };
     };
     const { dev, wall } = gpu.profiler ? { dev: [], wall: [] } : await single();
-    const devQ = await queued();
+    const { devQ, total } = await queued();
     if (gpu.profiler) {
       const rows = await gpu.profiler.report();
       report.profile = rows.map((r) => ({ name: r.name, count: r.count / a.reps, ms: r.ms / a.reps, tflops: r.flops ? r.flops / (r.ms / 1e3) / 1e12 : null }));
@@ -213,6 +216,7 @@ async function main() {
       reps: a.reps, warmup: a.warmup, ms_device: dev, ms_wall: wall, ms_host_to_host: host,
       ms_device_median: median(dev), ms_wall_median: median(wall), ms_host_to_host_median: median(host),
       ms_device_queued: devQ, ms_device_queued_median: median(devQ),
+      ms_device_queued_total: total, ms_device_queued_per_pass: total / a.reps,
     });
   }
   report.pool_peak_bytes = gpu.pool.peak;

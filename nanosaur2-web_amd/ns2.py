@@ -91,6 +91,8 @@ SIGNATURES = {
                                   c_vp, c_vp, c_int, c_vp, c_int, c_int, c_int, c_int],
     "ns2_attention_rows": [c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
                            c_ll, c_ll, c_ll, c_int, c_int],
+    "ns2_attention_rows_f16kv": [c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
+                                 c_ll, c_ll, c_ll, c_int, c_int],
     "ns2_head_norm": [c_vp, c_vp, c_int, c_int, c_int, c_int, c_ll, c_ll, c_vp, c_ll, c_float],
     "ns2_head_norm2": [c_vp, c_vp, c_int, c_vp, c_int, c_int, c_int, c_int, c_ll, c_ll, c_vp, c_ll, c_float],
     "ns2_norm_mod": [c_vp, c_vp, c_ll, c_ll, c_int, c_int, c_vp, c_float, c_vp],
@@ -107,6 +109,8 @@ SIGNATURES = {
     "ns2_linear_bf16_glu": [c_vp, c_int, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int],
     "ns2_linear_bf16_head_norm": [c_vp, c_int, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_vp, c_int, c_vp, c_int,
                                   c_int, c_vp, c_ll, c_int, c_float],
+    "ns2_linear_bf16_head_norm_f16kv": [c_vp, c_int, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_vp, c_int, c_vp,
+                                        c_int, c_int, c_vp, c_ll, c_int, c_float, c_vp, c_int],
     "ns2_linear_bf16_add_rmsnorm": [c_vp, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_float],
 }
 _RESTYPES = {"ns2_last_error": ctypes.c_char_p, "ns2_get_stream": c_vp, "ns2_pool_round": c_size,
@@ -322,6 +326,12 @@ class Lib:
         self.call("ns2_attention_rows", _ptr(q), _ptr(k), _ptr(v), _ptr(o), Lq, Lk, H, D, ldq, ldk, ldv,
                   ldo, qOff, kOff, vOff, group, int(causal))
 
+    def attention_rows_f16kv(self, q, k, v, o, *, Lq, Lk, H, D, ldq, ldk, ldv, ldo, qOff=0, kOff=0, vOff=0,
+                             group=1, causal=False):
+        """attention_rows with fp16 k and v (their strides and offsets in fp16 elements)."""
+        self.call("ns2_attention_rows_f16kv", _ptr(q), _ptr(k), _ptr(v), _ptr(o), Lq, Lk, H, D, ldq, ldk, ldv,
+                  ldo, qOff, kOff, vOff, group, int(causal))
+
     def head_norm(self, X, w, L, H, D, ld, colOff=0, rowOff=0, cs=None, sinOff=0, eps=1e-6):
         self.call("ns2_head_norm", _ptr(X), _ptr(w), L, H, D, ld, colOff, rowOff, _ptr(cs), sinOff, eps)
 
@@ -367,6 +377,13 @@ class Lib:
                               rope_rows=0, eps=1e-6):
         self.call("ns2_linear_bf16_head_norm", _ptr(A), lda, _ptr(W), _ptr(bias), _ptr(C), M, N, K, _ptr(w1), H1,
                   _ptr(w2), H2, D, _ptr(cs), sin_off, rope_rows, eps)
+
+    def linear_bf16_head_norm_f16kv(self, A, lda, W, bias, C, M, N, K, w1, H1, w2, H2, D, kv16, ldkv, cs=None,
+                                    sin_off=0, rope_rows=0, eps=1e-6):
+        """linear_bf16_head_norm with heads H1.. stored as fp16 in kv16 [M, ldkv] (a device address,
+        or a tensor)."""
+        self.call("ns2_linear_bf16_head_norm_f16kv", _ptr(A), lda, _ptr(W), _ptr(bias), _ptr(C), M, N, K,
+                  _ptr(w1), H1, _ptr(w2), H2, D, _ptr(cs), sin_off, rope_rows, eps, _ptr(kv16), ldkv)
 
     def linear_bf16_glu(self, A, lda, W, bias, Y, M, N, K, act="gelu_tanh"):
         self.call("ns2_linear_bf16_glu", _ptr(A), lda, _ptr(W), _ptr(bias), _ptr(Y), M, N, K, ACT[act])

@@ -1044,6 +1044,45 @@ def test_linear_bf16_head_norm(ns2lib, M, bias, rope):
     assert_close(y.cpu(), ref, TOL, f"linear_bf16_head_norm (M={M}, bias={bias}, rope={rope})")
 
 
+@pytest.mark.parametrize("M,bias,rope", [(256, False, True), (37, True, True), (5, False, False)])
+def test_linear_bf16_head_norm_f16kv(ns2lib, M, bias, rope):
+    """ns2_linear_bf16_head_norm_f16kv: the q heads bit-identical to ns2_linear_bf16_head_norm's,
+    the k and v heads its fp32 results rounded to nearest-even fp16 (torch's .half()), written into
+    the front half of their own fp32 columns (ldkv = 2N, as the Gemma3 encoder calls it) or into a
+    separate buffer with a wider row stride."""
+    N, K, D = 1536, 640, 256
+    g = gen(M + 5 * bias + 13 * rope)
+    a = torch.randn(M, K, generator=g)
+    w = (torch.randn(N, K, generator=g) * 0.05).to(torch.bfloat16)
+    b = torch.randn(N, generator=g) * 0.1 if bias else None
+    wq = (torch.randn(D, generator=g) * 0.3 + 1).to(dev)
+    wk = (torch.randn(D, generator=g) * 0.3 + 1).to(dev)
+    csd, sin_off = None, 0
+    if rope:
+        ang = torch.arange(M, dtype=torch.float64)[:, None] * torch.rand(D // 2, generator=g, dtype=torch.float64)[None]
+        csd = torch.cat([ang.cos().flatten(), ang.sin().flatten()]).float().to(dev)
+        sin_off = M * D // 2
+    ad, wd, bd = a.to(dev), w.view(torch.int16).to(dev), (b.to(dev) if bias else None)
+    y = torch.empty(M, N, device=dev)
+    ns2lib.linear_bf16_head_norm(ad, K, wd, bd, y, M, N, K, wq, 4, wk, 1, D, cs=csd, sin_off=sin_off, rope_rows=M)
+    z = torch.full((M, N), float("nan"), device=dev)
+    ns2lib.linear_bf16_head_norm_f16kv(ad, K, wd, bd, z, M, N, K, wq, 4, wk, 1, D, z.data_ptr() + 4 * D * 4, 2 * N,
+                                       cs=csd, sin_off=sin_off, rope_rows=M)
+    ld = 2 * D + 24
+    sep = torch.zeros(M, ld, dtype=torch.float16, device=dev)
+    zz = torch.empty(M, N, device=dev)
+    ns2lib.linear_bf16_head_norm_f16kv(ad, K, wd, bd, zz, M, N, K, wq, 4, wk, 1, D, sep, ld, cs=csd,
+                                       sin_off=sin_off, rope_rows=M)
+    torch.cuda.synchronize()
+    y, z, zz, sep = y.cpu(), z.cpu(), zz.cpu(), sep.cpu()
+    assert torch.equal(z[:, :4 * D], y[:, :4 * D]) and torch.equal(zz[:, :4 * D], y[:, :4 * D])
+    kv_ref = y[:, 4 * D:].half().view(torch.int16)
+    kv_in = z.view(torch.int16)[:, 8 * D:10 * D]
+    assert torch.equal(kv_in, kv_ref), "fp16 k/v in place"
+    assert torch.equal(sep[:, :2 * D].view(torch.int16), kv_ref), "fp16 k/v in a separate buffer"
+    assert (sep[:, 2 * D:] == 0).all(), "columns past the k/v heads untouched"
+
+
 @pytest.mark.parametrize("rows,cols", [(64, 3952), (3952, 64), (37, 100), (1, 5)])
 def test_transpose(ns2lib, rows, cols):
     """The latent <-> token layout change of forward() (exact)."""
@@ -1115,6 +1154,84 @@ def test_attention_rows_packed_qkv_view(ns2lib, pad):
     x = qkv.double()[:, pad:]
     ref = O.attention_rows(x[:, :H * D], x[:, H * D:(H + 1) * D], x[:, (H + 1) * D:], H, D, group=H, causal=True)
     assert_close(o.cpu(), ref, TOL_ROWS if pad else TOL, f"attention_rows packed qkv (pad {pad})")
+
+
+@pytest.mark.parametrize("D,H,group,causal,Lq,Lk", [
+    (256, 4, 4, True, 256, 256),  # the Gemma3 encoder's longest prompt: one pair of key blocks per wave
+    (256, 4, 4, True, 37, 37),
+    (256, 2, 1, False, 5, 300),   # 19 key blocks: waves with a pair and a lone third block
+    (256, 4, 2, True, 100, 37),   # more queries than keys under the causal mask
+    (128, 8, 2, True, 300, 300),  # K fragments from memory, 16-byte value loads
+    (64, 8, 1, False, 50, 70),    # 8-byte value loads
+    (96, 6, 2, True, 33, 33),     # six 16-dim steps: per-element value loads
+    (48, 3, 3, False, 9, 130),
+    (16, 2, 1, True, 1, 1),
+])
+def test_attention_rows_f16kv(ns2lib, D, H, group, causal, Lq, Lk):
+    """ns2_attention_rows_f16kv against ns2_attention_rows on the same K/V (fp16 values, given to
+    the fp32 entry as fp32): both run their products on the same fp16 operands and consume each
+    wave's key blocks in the same order, so the outputs are the same bit for bit; and against the
+    oracle at the matrix-core tolerance."""
+    g = gen(D * 5 + H + Lq + Lk)
+    KH = H // group
+    q = torch.randn(Lq, H * D, generator=g)
+    k = torch.randn(Lk, KH * D, generator=g).half()
+    v = torch.randn(Lk, KH * D, generator=g).half()
+    o32 = torch.empty(Lq, H * D, device=dev)
+    o16 = torch.empty(Lq, H * D, device=dev)
+    qd = q.to(dev)
+    ns2lib.attention_rows(qd, k.float().to(dev), v.float().to(dev), o32, Lq=Lq, Lk=Lk, H=H, D=D, ldq=H * D,
+                          ldk=KH * D, ldv=KH * D, ldo=H * D, group=group, causal=causal)
+    ns2lib.attention_rows_f16kv(qd, k.to(dev), v.to(dev), o16, Lq=Lq, Lk=Lk, H=H, D=D, ldq=H * D, ldk=KH * D,
+                                ldv=KH * D, ldo=H * D, group=group, causal=causal)
+    torch.cuda.synchronize()
+    assert torch.equal(o16.cpu(), o32.cpu()), f"attention_rows_f16kv vs fp32 K/V D={D} Lq={Lq} Lk={Lk}"
+    ref = O.attention_rows(q.double(), k.double(), v.double(), H, D, group=group, causal=causal)
+    assert_close(o16.cpu(), ref, TOL, f"attention_rows_f16kv D={D} H={H} group={group} causal={causal}")
+
+
+@pytest.mark.parametrize("L", [1, 37, 256])
+def test_gemma_qkv_f16kv_attention(ns2lib, L):
+    """The Gemma3 layer's q/k/v projection with fp16 k/v written in place, read by the fp16-K/V
+    attention (the encoder's path), against the fp32 projection and ns2_attention_rows: the same
+    output bit for bit."""
+    N, K, D, H = 1536, 640, 256, 4
+    g = gen(L + 901)
+    a = torch.randn(L, K, generator=g).to(dev)
+    w = (torch.randn(N, K, generator=g) * 0.05).to(torch.bfloat16).view(torch.int16).to(dev)
+    wq = (torch.randn(D, generator=g) * 0.3 + 1).to(dev)
+    wk = (torch.randn(D, generator=g) * 0.3 + 1).to(dev)
+    ang = torch.arange(L, dtype=torch.float64)[:, None] * torch.rand(D // 2, generator=g, dtype=torch.float64)[None]
+    cs = torch.cat([ang.cos().flatten(), ang.sin().flatten()]).float().to(dev)
+    y = torch.empty(L, N, device=dev)
+    ns2lib.linear_bf16_head_norm(a, K, w, None, y, L, N, K, wq, H, wk, 1, D, cs=cs, sin_off=L * D // 2, rope_rows=L)
+    z = torch.empty(L, N, device=dev)
+    ns2lib.linear_bf16_head_norm_f16kv(a, K, w, None, z, L, N, K, wq, H, wk, 1, D, z.data_ptr() + H * D * 4, 2 * N,
+                                       cs=cs, sin_off=L * D // 2, rope_rows=L)
+    # the fp32 reference path sees the fp16 roundings of its k/v, as the products do
+    y[:, H * D:] = y[:, H * D:].half().float()
+    o32 = torch.empty(L, H * D, device=dev)
+    o16 = torch.empty(L, H * D, device=dev)
+    ns2lib.attention_rows(y, y, y, o32, Lq=L, Lk=L, H=H, D=D, ldq=N, ldk=N, ldv=N, ldo=H * D, qOff=0, kOff=H * D,
+                          vOff=(H + 1) * D, group=H, causal=True)
+    ns2lib.attention_rows_f16kv(z, z, z, o16, Lq=L, Lk=L, H=H, D=D, ldq=N, ldk=2 * N, ldv=2 * N, ldo=H * D, qOff=0,
+                                kOff=2 * H * D, vOff=2 * H * D + D, group=H, causal=True)
+    torch.cuda.synchronize()
+    assert torch.equal(o16.cpu(), o32.cpu()), f"Gemma3 q/k/v -> attention with fp16 k/v in place (L={L})"
+
+
+def test_f16kv_errors(ns2lib):
+    import ns2
+
+    buf = torch.zeros(4096, device=dev)
+    with pytest.raises(ns2.NS2Error, match="16-byte aligned"):
+        ns2lib.attention_rows_f16kv(buf, buf, buf, buf, Lq=2, Lk=2, H=1, D=64, ldq=64, ldk=64, ldv=64, ldo=64,
+                                    kOff=4)
+    with pytest.raises(ns2.NS2Error, match="multiple of 16"):
+        ns2lib.attention_rows_f16kv(buf, buf, buf, buf, Lq=2, Lk=2, H=1, D=40, ldq=40, ldk=40, ldv=40, ldo=40)
+    out = torch.zeros(4096, device=dev)
+    with pytest.raises(ns2.NS2Error, match="ldkv"):
+        ns2lib.linear_bf16_head_norm_f16kv(buf, 64, buf, None, out, 2, 768, 64, buf, 1, buf, 1, 256, out, 256)
 
 
 @pytest.mark.parametrize("Lq,Lk,causal", [(100, 37, True), (5, 300, False), (300, 300, True)])
