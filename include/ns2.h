@@ -236,6 +236,15 @@ int ns2_attention_rows(const float* q, const float* k, const float* v, float* o,
 int ns2_attention_rows_f16kv(const float* q, const uint16_t* k, const uint16_t* v, float* o, int Lq, int Lk,
                              int H, int D, int ldq, int ldk, int ldv, int ldo, long long qOff,
                              long long kOff, long long vOff, int group, int causal);
+/* ns2_attention_rows_f16kv followed by the sublayer's output projection split over heads
+ * (Gemma3's attention and o_proj, app/models/gemma3.js:67-73): for each head h, with O_h its attention output
+ * [Lq, D] rounded to fp16 (as a linear rounds its input), part[h] [Lq, N] = O_h W_o[:, hD:(h+1)D]^T,
+ * fp32. wo_tiled: W_o [N, H*D] as ns2_tile_bf16_weight writes it. The H shares sum to the
+ * projection (without bias); ns2_parts_add_rmsnorm adds them. N and H*D multiples of 64.
+ * Additive to the reference interface. */
+int ns2_attention_rows_f16kv_oproj(const float* q, const uint16_t* k, const uint16_t* v, const uint16_t* wo_tiled,
+                                   float* part, int Lq, int Lk, int H, int D, int ldq, int ldk, int ldv,
+                                   long long qOff, long long kOff, long long vOff, int group, int causal, int N);
 
 /* ---- attention (ops.attention, app/gpu/ops.js:199-209; flashAttentionShader,
  *      app/gpu/kernels.js:119-305) ----------------------------------------------------------
@@ -421,6 +430,12 @@ int ns2_linear_bf16_glu(const float* A, int lda, const uint16_t* W, const float*
 int ns2_linear_bf16_add_rmsnorm(const float* A, int lda, const uint16_t* W, const float* bias, float* x,
                                 const float* w_add, const float* w_out, float* y, int M, int N, int K,
                                 float eps);
+/* The same sublayer norms on a product given as `splits` fp32 shares part [splits][M][N] (as
+ * ns2_attention_rows_f16kv_oproj writes them): t = sum of the shares in split order (+ bias), then
+ * x += rmsnorm(t) * w_add and, when y is not null, y = rmsnorm(x) * w_out (ns2_add_rmsnorm;
+ * app/models/gemma3.js:74-79). N <= 1024. Additive to the reference interface. */
+int ns2_parts_add_rmsnorm(const float* part, int splits, const float* bias, float* x, const float* w_add,
+                          const float* w_out, float* y, int M, int N, float eps);
 
 #ifdef __cplusplus
 }

@@ -671,6 +671,39 @@ napi_value AttentionRowsF16kv(napi_env env, napi_callback_info info) {
                ns2_attention_rows_f16kv(q, k, v, o, Lq, Lk, H, D, ldq, ldk, ldv, ldo, qOff, kOff, vOff, group, causal));
 }
 
+// attentionRowsF16kvOproj(q, k, v, woTiled, part, Lq, Lk, H, D, ldq, ldk, ldv, qOff, kOff, vOff, group, causal, N)
+napi_value AttentionRowsF16kvOproj(napi_env env, napi_callback_info info) {
+  ARGS(18);
+  auto q = (const float*)c.ptr(0);
+  auto k = (const uint16_t*)c.ptr(1);
+  auto v = (const uint16_t*)c.ptr(2);
+  auto wo = (const uint16_t*)c.ptr(3);
+  auto part = (float*)c.ptr(4);
+  int Lq = c.i32(5), Lk = c.i32(6), H = c.i32(7), D = c.i32(8);
+  int ldq = c.i32(9), ldk = c.i32(10), ldv = c.i32(11);
+  long long qOff = c.i64(12), kOff = c.i64(13), vOff = c.i64(14);
+  int group = c.i32(15), causal = c.i32(16), N = c.i32(17);
+  if (c.failed) return nullptr;
+  return check(env, c, ns2_attention_rows_f16kv_oproj(q, k, v, wo, part, Lq, Lk, H, D, ldq, ldk, ldv, qOff, kOff, vOff,
+                                                      group, causal, N));
+}
+
+// partsAddRmsnorm(part, splits, bias, x, wAdd, wOut, y, M, N, eps)
+napi_value PartsAddRmsnorm(napi_env env, napi_callback_info info) {
+  ARGS(10);
+  auto part = (const float*)c.ptr(0);
+  int splits = c.i32(1);
+  auto bias = (const float*)c.ptr(2);
+  auto x = (float*)c.ptr(3);
+  auto wAdd = (const float*)c.ptr(4);
+  auto wOut = (const float*)c.ptr(5);
+  auto y = (float*)c.ptr(6);
+  int M = c.i32(7), N = c.i32(8);
+  float eps = c.f32(9);
+  if (c.failed) return nullptr;
+  return check(env, c, ns2_parts_add_rmsnorm(part, splits, bias, x, wAdd, wOut, y, M, N, eps));
+}
+
 // headNorm(X, w, L, H, D, ld, colOff, rowOff, cs, sinOff, eps)
 napi_value HeadNorm(napi_env env, napi_callback_info info) {
   ARGS(11);
@@ -920,7 +953,8 @@ napi_value Module(napi_env env, napi_value exports) {
       {"tileBf16Weight", TileBf16Weight}, {"linearF16wTiled", LinearF16wTiled}, {"toTiledF16", ToTiledF16},
       {"normModF16", NormModF16},
       {"linearI8", LinearI8}, {"linearBf16", LinearBf16}, {"attention", Attention},
-      {"attentionRows", AttentionRows}, {"attentionRowsF16kv", AttentionRowsF16kv}, {"attentionText", AttentionText},
+      {"attentionRows", AttentionRows}, {"attentionRowsF16kv", AttentionRowsF16kv},
+      {"attentionRowsF16kvOproj", AttentionRowsF16kvOproj}, {"partsAddRmsnorm", PartsAddRmsnorm}, {"attentionText", AttentionText},
       {"linearI8TiledVpack", LinearI8TiledVpack}, {"attentionVpackBytes", AttentionVpackBytes},
       {"attentionVpacked", AttentionVpacked},
       {"headNorm", HeadNorm}, {"headNorm2", HeadNorm2}, {"normMod", NormModT<false>}, {"normModRotateF16", NormModT<true>},

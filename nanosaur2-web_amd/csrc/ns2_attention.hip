@@ -1458,9 +1458,20 @@ struct RowsArgsH {
   long long qOff, kOff, vOff;  // k, v offsets and strides in fp16 elements
   int Lq, Lk, H, D, ldq, ldk, ldv, ldo, group, causal;
   float scale;
+  // OPROJ: the output projection's share of each head instead of o (see attn_rows_h_kernel)
+  const half_t* wo;  // fp16 weight tiles of W_o [N][H*D] (tile_w16_kernel's layout)
+  float* part;       // [H][Lq][N] fp32
+  int N;
 };
 
-template <int DB, int NW>
+// OPROJ: the block goes on from its normalized output O_h (16 queries x D of head h, rounded to
+// fp16 as a linear's loader rounds its input) to O_h W_o[:, hD:(h+1)D]^T, head h's share of
+// the output projection, into part[h] (16 x N, fp32): the projection split over heads, its H
+// shares summed by the reduction that follows it, as a split-K linear's k-range shares are.
+// Each wave takes 16-column tiles n0 = 16w, 16(w + NW), ... with v_mfma_f32_16x16x16_f16: A = O_h
+// rows from LDS (row padded by 16 bytes), B = 4 consecutive k of weight row n0 + l%16 (8 bytes of
+// one tile chunk).
+template <int DB, int NW, bool OPROJ = false>
 __global__ __launch_bounds__(64 * NW) void attn_rows_h_kernel(RowsArgsH a) {
   constexpr int D = 16 * DB;
   constexpr bool KDMA = D == 256;
@@ -1598,6 +1609,24 @@ __global__ __launch_bounds__(64 * NW) void attn_rows_h_kernel(RowsArgsH a) {
   }
   lsum += __shfl_xor(lsum, 16);
   lsum += __shfl_xor(lsum, 32);
+  // OPROJ: the weight fragments of the wave's first JC column tiles are loaded here, so that
+  // their latency passes during the merge (they do not depend on the attention)
+  constexpr int JC = !OPROJ ? 1 : (DB == 14 || DB == 15) ? 1 : DB == 16 ? 5 : 3;
+  half4_t bf[JC][DB];
+  const int nt = OPROJ ? a.N / 16 : 0;
+  auto load_w = [&](int j0) {
+#pragma unroll
+    for (int c = 0; c < JC; ++c) {
+      const int j = j0 + c * NW;
+      if (j < nt) {  // uniform per wave
+        const int n = 16 * j + col;
+#pragma unroll
+        for (int t = 0; t < DB; ++t)
+          bf[c][t] = *reinterpret_cast<const half4_t*>(a.wo + tiled_off(n, h * D + 16 * t + 4 * grp, a.H * D));
+      }
+    }
+  };
+  if constexpr (OPROJ) load_w(wave);
   if constexpr (KDMA) __syncthreads();  // every wave is done with its K rows (o_part overlays them)
 
 #pragma unroll
@@ -1607,7 +1636,8 @@ __global__ __launch_bounds__(64 * NW) void attn_rows_h_kernel(RowsArgsH a) {
     l_part[wave][col] = lsum;
   }
   __syncthreads();
-  if (!qvalid) return;
+  if (!OPROJ && !qvalid) return;
+  // (rows past Lq repeat row Lq - 1's state: finite, and only OPROJ computes them)
   float M = m_part[0][col];
 #pragma unroll
   for (int w = 1; w < NW; ++w) M = fmaxf(M, m_part[w][col]);  // finite: wave 0 sees key 0
@@ -1619,16 +1649,63 @@ __global__ __launch_bounds__(64 * NW) void attn_rows_h_kernel(RowsArgsH a) {
   }
   const float inv = 1.0f / L;
   constexpr int F = 4 * DB, FW = (F + NW - 1) / NW;
-  float* orow = a.o + (long long)qi * a.ldo + (long long)h * D + F * grp;
+  float res[FW];
 #pragma unroll
   for (int u = 0; u < FW; ++u) {
     const int f = wave * FW + u;
+    res[u] = 0.f;
     if (f < F) {
       const int j = f / DB, t = f % DB;
       float r = 0.f;
 #pragma unroll
       for (int w = 0; w < NW; ++w) r += sc[w] * reinterpret_cast<const float*>(&o_part[w][t][lane])[j];
-      orow[f] = r * inv;
+      res[u] = r * inv;
+    }
+  }
+  if constexpr (!OPROJ) {
+    float* orow = a.o + (long long)qi * a.ldo + (long long)h * D + F * grp;
+#pragma unroll
+    for (int u = 0; u < FW; ++u)
+      if (wave * FW + u < F) orow[wave * FW + u] = res[u];
+  } else {
+    constexpr int OS = D + 8;  // fp16 row of O_h in LDS (16 bytes of padding)
+    half_t* o16 = reinterpret_cast<half_t*>(smem);
+    static_assert(16 * OS * 2 <= SM, "O_h fits the LDS of the loop");
+    __syncthreads();  // every wave is done reading o_part
+    if constexpr (FW == 8 && F % 8 == 0) {
+      // one 16-byte store: the row stride (2D + 16 bytes) and F grp + 8 wave keep it aligned
+      half8_t hv;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) hv[u] = (half_t)res[u];
+      *reinterpret_cast<half8_t*>(o16 + col * OS + F * grp + wave * FW) = hv;
+    } else {
+#pragma unroll
+      for (int u = 0; u < FW; ++u)
+        if (wave * FW + u < F) o16[col * OS + F * grp + wave * FW + u] = (half_t)res[u];
+    }
+    __syncthreads();
+    half4_t af[DB];
+#pragma unroll
+    for (int t = 0; t < DB; ++t) af[t] = *reinterpret_cast<const half4_t*>(o16 + col * OS + 16 * t + 4 * grp);
+    // the weight fragments of JC column tiles are loaded together (one round trip per JC tiles;
+    // one tile at a time where the loop's K/V registers leave no room: D = 224, 240)
+    for (int j0 = wave; j0 < nt; j0 += JC * NW) {
+      if (j0 != wave) load_w(j0);
+#pragma unroll
+      for (int c = 0; c < JC; ++c) {
+        const int j = j0 + c * NW;
+        if (j < nt) {
+          float4_t acc = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int t = 0; t < DB; ++t) acc = __builtin_amdgcn_mfma_f32_16x16x16f16(af[t], bf[c][t], acc, 0, 0, 0);
+          // acc[i]: query q0 + 4 grp + i, column 16 j + col
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int q = q0 + 4 * grp + i;
+            if (q < a.Lq) a.part[((long long)h * a.Lq + q) * a.N + 16 * j + col] = acc[i];
+          }
+        }
+      }
     }
   }
 }
@@ -1678,6 +1755,44 @@ extern "C" int ns2_attention_rows(const float* q, const float* k, const float* v
   else if (dv == 3) attn_rows_kernel<3><<<grid, block, 0, s>>>(a);
   else attn_rows_kernel<4><<<grid, block, 0, s>>>(a);
   NS2_LAUNCHED("attn_rows");
+  return NS2_OK;
+}
+
+extern "C" int ns2_attention_rows_f16kv_oproj(const float* q, const uint16_t* k, const uint16_t* v,
+                                              const uint16_t* wo_tiled, float* part, int Lq, int Lk, int H, int D,
+                                              int ldq, int ldk, int ldv, long long qOff, long long kOff,
+                                              long long vOff, int group, int causal, int N) {
+  NS2_READY();
+  if (Lq <= 0 || H <= 0) return NS2_OK;
+  const char* fn = "ns2_attention_rows_f16kv_oproj";
+  NS2_REQUIRE(q && k && v && wo_tiled && part, "%s: null q, k, v, wo_tiled or part", fn);
+  NS2_REQUIRE(D > 0 && D <= 256 && D % 16 == 0, "%s: head dim %d is not a multiple of 16 up to 256", fn, D);
+  NS2_REQUIRE(group > 0 && H % group == 0, "%s: H=%d is not a multiple of group=%d", fn, H, group);
+  NS2_REQUIRE(N > 0 && N % 64 == 0 && (H * D) % 64 == 0,
+              "%s: N=%d and H*D=%d must be multiples of 64 (the weight tiles)", fn, N, H * D);
+  NS2_REQUIRE(Lk > 0 && ldq >= H * D && ldk >= H / group * D && ldv >= H / group * D && qOff >= 0 && kOff >= 0 &&
+                  vOff >= 0,
+              "%s: bad sizes or strides", fn);
+  NS2_REQUIRE(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(wo_tiled) && ldq % 4 == 0 &&
+                  qOff % 4 == 0 && ldk % 8 == 0 && ldv % 8 == 0 && kOff % 8 == 0 && vOff % 8 == 0,
+              "%s: q, k, v rows and the weight tiles must be 16-byte aligned", fn);
+  RowsArgsH a{q, reinterpret_cast<const half_t*>(k), reinterpret_cast<const half_t*>(v), nullptr, qOff, kOff, vOff,
+              Lq, Lk, H, D, ldq, ldk, ldv, 0, group, causal ? 1 : 0, 1.0f / sqrtf((float)D) * kLog2e,
+              reinterpret_cast<const half_t*>(wo_tiled), part, N};
+  ns2::ProfScope prof_("attn_rows_oproj");
+  hipStream_t s = ns2::stream();
+  const dim3 grid((Lq + 15) / 16, H);
+  switch (D / 16) {
+#define NS2_ROWS_HO_CASE(N_) \
+  case N_: attn_rows_h_kernel<N_, kRowsWaves, true><<<grid, 64 * kRowsWaves, 0, s>>>(a); break;
+    NS2_ROWS_HO_CASE(1) NS2_ROWS_HO_CASE(2) NS2_ROWS_HO_CASE(3) NS2_ROWS_HO_CASE(4) NS2_ROWS_HO_CASE(5)
+    NS2_ROWS_HO_CASE(6) NS2_ROWS_HO_CASE(7) NS2_ROWS_HO_CASE(8) NS2_ROWS_HO_CASE(9) NS2_ROWS_HO_CASE(10)
+    NS2_ROWS_HO_CASE(11) NS2_ROWS_HO_CASE(12) NS2_ROWS_HO_CASE(13) NS2_ROWS_HO_CASE(14) NS2_ROWS_HO_CASE(15)
+    NS2_ROWS_HO_CASE(16)
+#undef NS2_ROWS_HO_CASE
+    default: break;
+  }
+  NS2_LAUNCHED("attn_rows_oproj");
   return NS2_OK;
 }
 

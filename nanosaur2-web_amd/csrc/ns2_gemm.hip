@@ -958,6 +958,23 @@ int ns2_linear_bf16_add_rmsnorm(const float* A, int lda, const uint16_t* W, cons
   return launch_gemm<true, true>(p, "linear_bf16_add_rmsnorm", &rn);
 }
 
+int ns2_parts_add_rmsnorm(const float* part, int splits, const float* bias, float* x, const float* w_add,
+                          const float* w_out, float* y, int M, int N, float eps) {
+  NS2_READY();
+  if (M == 0) return NS2_OK;
+  NS2_REQUIRE(part && x && w_add && (!y || w_out), "ns2_parts_add_rmsnorm: null part, x, w_add or w_out");
+  NS2_REQUIRE(splits > 0 && M > 0 && N > 0 && N <= kRowNormMaxN, "ns2_parts_add_rmsnorm: splits=%d M=%d N=%d (N <= %d)",
+              splits, M, N, kRowNormMaxN);
+  NS2_REQUIRE(y != x && part != x, "ns2_parts_add_rmsnorm: x must not alias part or y");
+  GemmArgs p{nullptr, nullptr, nullptr, bias, nullptr, x, nullptr, 0, 0, 0, N, M, N, 0, 1.0f, NS2_ACT_NONE, 0};
+  p.part = const_cast<float*>(part);
+  const RowNorm rn{x, w_add, w_out, y, eps};
+  ns2::ProfScope prof_("parts_add_rmsnorm");
+  splitk_add_rmsnorm_kernel<<<M, 256, 0, ns2::stream()>>>(p, splits, rn);
+  NS2_LAUNCHED("parts_add_rmsnorm");
+  return NS2_OK;
+}
+
 namespace {
 
 int linear_bf16_head_norm(const char* fn, const char* name, const float* A, int lda, const uint16_t* W, const float* bias, float* C,

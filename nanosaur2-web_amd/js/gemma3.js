@@ -51,7 +51,10 @@ export class Gemma3 {
     const m = new Gemma3(gpu, st);
     m.layers = [];
     for (let i = 0; i < RUN; i++) {
-      m.layers.push(await loadLayer(gpu, st, i));
+      const l = await loadLayer(gpu, st, i);
+      // o_proj re-tiled as fp16 (next to its row-major copy) for the attention's fused projection
+      if (ops.tileablePlain(l.o)) ops.tileWeight(gpu, l.o);
+      m.layers.push(l);
       if (onProgress) onProgress((i + 1) / RUN);
     }
     m.norm = await st.vector(gpu, "model.norm.weight", 1);
@@ -100,18 +103,31 @@ export class Gemma3 {
       // (on the fused path the k and v heads are stored as fp16, the attention's operand type)
       const qkv = ops.linearHeadNorm(gpu, h, l.qkv, l.qn, H, l.kn, KH, { D: HD, cs, f16kv: true });
       h.release();
-      const a = qkv.f16kv
-        ? ops.attentionRowsF16kv(gpu, {
+      let h2;
+      if (qkv.f16kv && l.o.tbuf && !(l.o.lora && l.o.lora.length)) {
+        // the attention and o_proj in one launch (each head's share of the projection), the
+        // shares summed by the post-norm's row kernel
+        const part = ops.attentionRowsF16kvOproj(gpu, {
           q: qkv, kv: qkv, Lq: Lt, Lk: Lt, H, D: HD, ldq: qkvW, qOff: 0, kOff: qkv.f16kv.off,
-          vOff: qkv.f16kv.off + KH * HD, ldkv: qkv.f16kv.ld, group: H / KH, causal: true,
-        })
-        : ops.attention(gpu, {
-          q: qkv, k: qkv, v: qkv, Lq: Lt, Lk: Lt, H, D: HD, ldq: qkvW, ldk: qkvW, ldv: qkvW,
-          qOff: 0, kOff: H * HD, vOff: (H + KH) * HD, group: H / KH, causal: true,
+          vOff: qkv.f16kv.off + KH * HD, ldkv: qkv.f16kv.ld, group: H / KH, causal: true, W: l.o,
         });
-      qkv.release();
-      const h2 = ops.linearAddRmsnorm(gpu, a, l.o, x, l.postAttnNorm, l.preMlpNorm);
-      a.release();
+        qkv.release();
+        h2 = ops.partsAddRmsnorm(gpu, part, H, l.o.bias, x, l.postAttnNorm, l.preMlpNorm);
+        part.release();
+      } else {
+        const a = qkv.f16kv
+          ? ops.attentionRowsF16kv(gpu, {
+            q: qkv, kv: qkv, Lq: Lt, Lk: Lt, H, D: HD, ldq: qkvW, qOff: 0, kOff: qkv.f16kv.off,
+            vOff: qkv.f16kv.off + KH * HD, ldkv: qkv.f16kv.ld, group: H / KH, causal: true,
+          })
+          : ops.attention(gpu, {
+            q: qkv, k: qkv, v: qkv, Lq: Lt, Lk: Lt, H, D: HD, ldq: qkvW, ldk: qkvW, ldv: qkvW,
+            qOff: 0, kOff: H * HD, vOff: (H + KH) * HD, group: H / KH, causal: true,
+          });
+        qkv.release();
+        h2 = ops.linearAddRmsnorm(gpu, a, l.o, x, l.postAttnNorm, l.preMlpNorm);
+        a.release();
+      }
       const g = ops.linearGlu(gpu, h2, l.gateUp, "gelu_tanh");
       h2.release();
       const next = i + 1 < this.layers.length ? this.layers[i + 1].inNorm : this.norm;

@@ -269,6 +269,31 @@ export function linearHeadNorm(gpu, a, W, w1, H1, w2, H2, { D, cs = null, eps = 
   return y;
 }
 
+// attentionRowsF16kv and the output projection after it (a Gemma3 layer's attention and o_proj,
+// app/models/gemma3.js:67-73; addition to the reference ops) without the attention output in
+// HBM: each head's block multiplies its normalized output by its D columns of W_o (a bf16 weight
+// re-tiled as fp16, W.tbuf) into its share part[h] [Lq, W.N]; the H shares sum to the projection
+// without bias (partsAddRmsnorm adds them and the bias). Returns the shares [H, Lq, W.N].
+export function attentionRowsF16kvOproj(gpu, { q, kv, Lq, Lk, H, D, ldq, qOff = 0, kOff, vOff, ldkv, group = 1,
+  causal = false, W }) {
+  if (!W.tbuf || W.kind !== "bf16" || W.K !== H * D) throw new Error(`${W.name}: the fused projection needs a re-tiled bf16 weight of K = H*D`);
+  const part = gpu.empty([H, Lq, W.N]);
+  gpu.run("attn.rows+o", 4 * Lq * Lk * D * H + 2 * Lq * W.N * W.K, () =>
+    native.attentionRowsF16kvOproj(addr(q), addr(kv), addr(kv), addr(W.tbuf), addr(part), Lq, Lk, H, D, ldq, ldkv,
+      ldkv, qOff, kOff, vOff, group, causal ? 1 : 0, W.N));
+  return part;
+}
+
+// addRmsnorm on a product given as `splits` shares [splits, M, N] (+ bias): x += rmsnorm(sum) *
+// wAdd, then y = rmsnorm(x) * wOut when wOut is given (returned).
+export function partsAddRmsnorm(gpu, part, splits, bias, x, wAdd, wOut, eps = 1e-6) {
+  const N = x.shape[x.shape.length - 1], M = x.size / N;
+  const y = wOut ? gpu.empty(x.shape) : null;
+  gpu.run("te.proj_norm", 0, () =>
+    native.partsAddRmsnorm(addr(part), splits, addr(bias || null), addr(x), addr(wAdd), addr(wOut), addr(y), M, N, eps));
+  return y;
+}
+
 // The materialized-path attention (causal / grouped, as attention() runs it) on fp16 keys and
 // values: kv is a Tensor whose bytes hold them, kOff / vOff / ldkv in fp16 elements (the
 // .f16kv layout of linearHeadNorm); q fp32 as in attention(). Output [Lq, H*D].

@@ -93,6 +93,9 @@ SIGNATURES = {
                            c_ll, c_ll, c_ll, c_int, c_int],
     "ns2_attention_rows_f16kv": [c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
                                  c_ll, c_ll, c_ll, c_int, c_int],
+    "ns2_attention_rows_f16kv_oproj": [c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_int,
+                                       c_int, c_ll, c_ll, c_ll, c_int, c_int, c_int],
+    "ns2_parts_add_rmsnorm": [c_vp, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_float],
     "ns2_head_norm": [c_vp, c_vp, c_int, c_int, c_int, c_int, c_ll, c_ll, c_vp, c_ll, c_float],
     "ns2_head_norm2": [c_vp, c_vp, c_int, c_vp, c_int, c_int, c_int, c_int, c_ll, c_ll, c_vp, c_ll, c_float],
     "ns2_norm_mod": [c_vp, c_vp, c_ll, c_ll, c_int, c_int, c_vp, c_float, c_vp],
@@ -325,6 +328,16 @@ class Lib:
                        group=1, causal=False):
         self.call("ns2_attention_rows", _ptr(q), _ptr(k), _ptr(v), _ptr(o), Lq, Lk, H, D, ldq, ldk, ldv,
                   ldo, qOff, kOff, vOff, group, int(causal))
+
+    def attention_rows_f16kv_oproj(self, q, k, v, wo_tiled, part, *, Lq, Lk, H, D, ldq, ldk, ldv, N, qOff=0,
+                                   kOff=0, vOff=0, group=1, causal=False):
+        """attention_rows_f16kv with each head's share of the output projection into part [H, Lq, N]."""
+        self.call("ns2_attention_rows_f16kv_oproj", _ptr(q), _ptr(k), _ptr(v), _ptr(wo_tiled), _ptr(part), Lq, Lk,
+                  H, D, ldq, ldk, ldv, qOff, kOff, vOff, group, int(causal), N)
+
+    def parts_add_rmsnorm(self, part, splits, bias, x, w_add, w_out, y, M, N, eps=1e-6):
+        self.call("ns2_parts_add_rmsnorm", _ptr(part), splits, _ptr(bias), _ptr(x), _ptr(w_add), _ptr(w_out),
+                  _ptr(y), M, N, eps)
 
     def attention_rows_f16kv(self, q, k, v, o, *, Lq, Lk, H, D, ldq, ldk, ldv, ldo, qOff=0, kOff=0, vOff=0,
                              group=1, causal=False):

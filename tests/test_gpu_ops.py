@@ -1220,6 +1220,80 @@ def test_gemma_qkv_f16kv_attention(ns2lib, L):
     assert torch.equal(o16.cpu(), o32.cpu()), f"Gemma3 q/k/v -> attention with fp16 k/v in place (L={L})"
 
 
+@pytest.mark.parametrize("L,H,group,D,N,causal", [
+    (256, 4, 4, 256, 640, True),  # the Gemma3 layer at its longest prompt
+    (37, 4, 4, 256, 640, True),
+    (1, 4, 4, 256, 640, True),
+    (100, 8, 2, 128, 256, False),  # other head dims, grouped K/V, several column rounds per wave
+    (50, 2, 1, 96, 192, True),
+])
+def test_attention_rows_f16kv_oproj(ns2lib, L, H, group, D, N, causal):
+    """ns2_attention_rows_f16kv_oproj: each head's share of the output projection, summed over the
+    heads, against ns2_attention_rows_f16kv followed by ns2_linear_bf16 of the output (the same fp16
+    roundings of the attention output and of W_o; the products summed over K in another order:
+    5e-5 where that linear runs its matrix-core path), and against the oracle's
+    attention and projection in fp64 (TOL)."""
+    g = gen(L * 7 + H + D + N)
+    KH = H // group
+    q = torch.randn(L, H * D, generator=g)
+    k = torch.randn(L, KH * D, generator=g).half()
+    v = torch.randn(L, KH * D, generator=g).half()
+    w = (torch.randn(N, H * D, generator=g) * 0.03).to(torch.bfloat16)
+    wd = w.view(torch.int16).to(dev)
+    wt = torch.empty(N * H * D, dtype=torch.int16, device=dev)
+    ns2lib.tile_bf16_weight(wd, wt, N, H * D)
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    part = torch.full((H, L, N), float("nan"), device=dev)
+    ns2lib.attention_rows_f16kv_oproj(qd, kd, vd, wt, part, Lq=L, Lk=L, H=H, D=D, ldq=H * D, ldk=KH * D,
+                                      ldv=KH * D, N=N, group=group, causal=causal)
+    o = torch.empty(L, H * D, device=dev)
+    ns2lib.attention_rows_f16kv(qd, kd, vd, o, Lq=L, Lk=L, H=H, D=D, ldq=H * D, ldk=KH * D, ldv=KH * D, ldo=H * D,
+                                group=group, causal=causal)
+    t = torch.empty(L, N, device=dev)
+    ns2lib.linear_bf16(o, H * D, wd, t, L, N, H * D)
+    torch.cuda.synchronize()
+    got = part.cpu().double().sum(0)
+    assert torch.isfinite(part.cpu()).all(), "every share written"
+    # fp32 sums of up to 1024 products in another association: 5e-5 of the largest output; at
+    # L <= 8 ns2_linear_bf16 runs its fp32 GEMV, which does not round its input to fp16
+    assert_close(got, t.cpu().double(), 5e-5 if L > 8 else TOL, f"attention + o_proj vs two launches (L={L}, D={D})")
+    ref = O.attention_rows(q.double(), k.double(), v.double(), H, D, group=group, causal=causal) @ w.double().t()
+    assert_close(got, ref, TOL, f"attention + o_proj vs the oracle (L={L}, D={D})")
+
+
+@pytest.mark.parametrize("M,splits,with_out,bias", [(256, 4, True, False), (37, 3, False, True), (1, 1, True, True)])
+def test_parts_add_rmsnorm(ns2lib, M, splits, with_out, bias):
+    """ns2_parts_add_rmsnorm: the sublayer norms (app/models/gemma3.js:74-79) on a product given as
+    fp32 shares, against ns2_add_rmsnorm of their sum taken in split order (bit-exact) and against
+    the oracle."""
+    N = 640
+    g = gen(M * 13 + splits)
+    part = torch.randn(splits, M, N, generator=g)
+    b = torch.randn(N, generator=g) * 0.1 if bias else None
+    x = torch.randn(M, N, generator=g) * 20
+    wa = torch.randn(N, generator=g) * 0.3 + 1
+    wo = torch.randn(N, generator=g) * 0.3 + 1
+    xd = x.to(dev)
+    y = torch.empty(M, N, device=dev) if with_out else None
+    ns2lib.parts_add_rmsnorm(part.to(dev), splits, b.to(dev) if bias else None, xd, wa.to(dev),
+                             wo.to(dev) if with_out else None, y, M, N)
+    t = part[0].clone()
+    for z in range(1, splits):
+        t += part[z]
+    if bias:
+        t += b
+    x2 = x.to(dev)
+    y2 = torch.empty(M, N, device=dev) if with_out else None
+    ns2lib.add_rmsnorm(x2, t.to(dev), wa.to(dev), wo.to(dev) if with_out else None, y2, M, N)
+    torch.cuda.synchronize()
+    assert torch.equal(xd.cpu(), x2.cpu()), "parts_add_rmsnorm x vs ns2_add_rmsnorm of the sum"
+    if with_out:
+        assert torch.equal(y.cpu(), y2.cpu()), "parts_add_rmsnorm y vs ns2_add_rmsnorm of the sum"
+    tr = part.double().sum(0) + (b.double() if bias else 0)
+    xr = x.double() + O.rms_norm(tr, wa.double())
+    assert_close(xd.cpu(), xr, TOL_F32, "parts_add_rmsnorm x")
+
+
 def test_f16kv_errors(ns2lib):
     import ns2
 
