@@ -919,6 +919,21 @@ napi_value LinearBf16HeadNormF16kv(napi_env env, napi_callback_info info) {
                                                        ropeRows, eps, kv16, ldkv));
 }
 
+// linearBf16GluDown(A, lda, W, bias, M, N, K, act, wdTiled, Nd, part)
+napi_value LinearBf16GluDown(napi_env env, napi_callback_info info) {
+  ARGS(11);
+  auto A = (const float*)c.ptr(0);
+  int lda = c.i32(1);
+  auto W = (const uint16_t*)c.ptr(2);
+  auto bias = (const float*)c.ptr(3);
+  int M = c.i32(4), N = c.i32(5), K = c.i32(6), act = c.i32(7);
+  auto wd = (const uint16_t*)c.ptr(8);
+  int Nd = c.i32(9);
+  auto part = (float*)c.ptr(10);
+  if (c.failed) return nullptr;
+  return check(env, c, ns2_linear_bf16_glu_down(A, lda, W, bias, M, N, K, act, wd, Nd, part));
+}
+
 // linearBf16AddRmsnorm(A, lda, W, bias, x, wAdd, wOut, y, M, N, K, eps)
 napi_value LinearBf16AddRmsnorm(napi_env env, napi_callback_info info) {
   ARGS(12);
@@ -961,7 +976,7 @@ napi_value Module(napi_env env, napi_value exports) {
       {"glu", GluT<false>}, {"gluRotateF16", GluT<true>}, {"elementwise", Elementwise},
       {"accumulate", Accumulate}, {"addRows", AddRows}, {"rowSum", RowSum}, {"rmsnorm", Rmsnorm},
       {"addRmsnorm", AddRmsnorm}, {"linearBf16AddRmsnorm", LinearBf16AddRmsnorm},
-      {"linearBf16Glu", LinearBf16Glu}, {"linearBf16HeadNorm", LinearBf16HeadNorm},
+      {"linearBf16Glu", LinearBf16Glu}, {"linearBf16GluDown", LinearBf16GluDown}, {"linearBf16HeadNorm", LinearBf16HeadNorm},
       {"linearBf16HeadNormF16kv", LinearBf16HeadNormF16kv}, {"transpose", Transpose},
   };
   for (const Fn& f : fns) {

@@ -456,6 +456,104 @@ __global__ __launch_bounds__(256) void splitk_glu_kernel(GemmArgs p, int splits,
   y[i] = apply_act(g, glu_act) * u;
 }
 
+// Split-K sum of a gate/up product, its GLU, and the linear after it split over the GLU
+// output's 256-column groups (Gemma3's MLP, app/models/gemma3.js:79-83). Block (16 rows, group r)
+// forms y = act(gate) * up for its rows and the group's columns with splitk_glu_kernel's
+// arithmetic, rounds y to fp16 into LDS (as the next linear's loader rounds its input) and
+// multiplies it by the next weight's 256 columns of group r (fp16 tiles, tile_w16_kernel's
+// layout) on v_mfma_f32_16x16x16_f16: share r of that product, out[r][m][n] fp32 for n < Nd.
+// The I/256 shares, summed in r order, are the product without bias. Each wave takes 16-column
+// tiles n0 = 16w, 16(w + 8), ...; the weight fragments of its first JC tiles are loaded before
+// the split sums are read (they do not depend on them), the rest JC tiles per round trip.
+struct GluDown {
+  const half_t* wd;  // the next weight [Nd][I] as fp16 tiles
+  float* out;        // [I/256][M][Nd]
+  int Nd, act;
+};
+__global__ __launch_bounds__(512) void splitk_glu_down_kernel(GemmArgs p, int splits, GluDown gd) {
+  constexpr int NW = 8, GS = 256, OS = GS + 8, DB = GS / 16, JC = 5;
+  __shared__ __attribute__((aligned(16))) half_t g16[16 * OS];
+  const int I = p.N / 2;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, col = lane & 15, grp = lane >> 4;
+  const int m0 = blockIdx.x * 16, j0 = blockIdx.y * GS, nt = gd.Nd / 16;
+  // lane's fragment t of column tile jt: tiled_off(16 jt + col, j0 + 16 t + 4 grp, I), which is
+  // the offset for t = 0 plus 1024 t (j0 and 16 t + 4 grp stay inside one 64-column k-tile
+  // pair of chunks: k >> 6 = j0/64 + t/4, chunk 2 (t % 4) + grp/2, element 4 (grp & 1))
+  half4_t bf[JC][DB];
+  auto load_w = [&](int jt0) {
+#pragma unroll
+    for (int c = 0; c < JC; ++c) {
+      const int jt = jt0 + c * NW;
+      if (jt < nt) {  // uniform per wave
+        const half_t* wrow = gd.wd + tiled_off(16 * jt + col, j0 + 4 * grp, I);
+#pragma unroll
+        for (int t = 0; t < DB; ++t) bf[c][t] = *reinterpret_cast<const half4_t*>(wrow + 1024 * t);
+      }
+    }
+  };
+  load_w(wave);
+  {
+    // thread: row rr, columns c8 .. c8 + 7 of the group (rows past M repeat the last row)
+    const int rr = tid >> 5, c8 = (tid & 31) * 8;
+    const long long m = m0 + rr < p.M ? m0 + rr : p.M - 1;
+    const long long mn = (long long)p.M * p.N;
+    const float* gp = p.part + m * p.N + j0 + c8;
+    float g[8], u[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) g[e] = u[e] = 0.f;
+    // two splits' loads in flight at a time (the weight fragments above hold most registers)
+#pragma unroll 2
+    for (int z = 0; z < splits; ++z) {
+      const float4 g0 = *reinterpret_cast<const float4*>(gp + z * mn), g1 = *reinterpret_cast<const float4*>(gp + z * mn + 4);
+      const float4 u0 = *reinterpret_cast<const float4*>(gp + z * mn + I);
+      const float4 u1 = *reinterpret_cast<const float4*>(gp + z * mn + I + 4);
+      g[0] += g0.x, g[1] += g0.y, g[2] += g0.z, g[3] += g0.w, g[4] += g1.x, g[5] += g1.y, g[6] += g1.z, g[7] += g1.w;
+      u[0] += u0.x, u[1] += u0.y, u[2] += u0.z, u[3] += u0.w, u[4] += u1.x, u[5] += u1.y, u[6] += u1.z, u[7] += u1.w;
+    }
+    half8_t hv;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int j = j0 + c8 + e;
+      float a = g[e] * p.alpha, b = u[e] * p.alpha;
+      if (p.scale) {
+        a *= p.scale[j];
+        b *= p.scale[j + I];
+      }
+      if (p.bias) {
+        a += p.bias[j];
+        b += p.bias[j + I];
+      }
+      float y = apply_act(a, gd.act) * b;
+      // the fp32 value first, as the GLU kernel stores it: no multiply fused into the conversion
+      asm volatile("" : "+v"(y));
+      hv[e] = (half_t)y;
+    }
+    *reinterpret_cast<half8_t*>(&g16[rr * OS + c8]) = hv;
+  }
+  __syncthreads();
+  half4_t af[DB];
+#pragma unroll
+  for (int t = 0; t < DB; ++t) af[t] = *reinterpret_cast<const half4_t*>(&g16[col * OS + 16 * t + 4 * grp]);
+  for (int jt0 = wave; jt0 < nt; jt0 += JC * NW) {
+    if (jt0 != wave) load_w(jt0);
+#pragma unroll
+    for (int c = 0; c < JC; ++c) {
+      const int jt = jt0 + c * NW;
+      if (jt < nt) {
+        float4_t acc = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int t = 0; t < DB; ++t) acc = __builtin_amdgcn_mfma_f32_16x16x16f16(af[t], bf[c][t], acc, 0, 0, 0);
+        // acc[i]: row m0 + 4 grp + i, column 16 jt + col
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int m = m0 + 4 * grp + i;
+          if (m < p.M) gd.out[((long long)blockIdx.y * p.M + m) * gd.Nd + 16 * jt + col] = acc[i];
+        }
+      }
+    }
+  }
+}
+
 // Small-M path: one wave per output column n, all M (<= MR <= 8) rows, fp32 FMA.
 // A: fp32 [M, lda] (bf16 layers) or rotated fp16 [M, lda] (int8 layers).
 template <bool W_BF16, int MR>
@@ -763,10 +861,10 @@ inline bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 template <bool A_F32, bool W_BF16>
 int launch_gemm(const GemmArgs& p, const char* name, const RowNorm* rn = nullptr, float* glu_y = nullptr,
-                int glu_act = 0, const HeadNorm* hn = nullptr) {
+                int glu_act = 0, const HeadNorm* hn = nullptr, const GluDown* gd = nullptr) {
   hipStream_t s = ns2::stream();
-  const bool post = rn || glu_y || hn;
-  ns2::ProfScope prof_(rn ? "gemm_bf16_add_rmsnorm" : glu_y ? "gemm_bf16_glu" : hn ? "gemm_bf16_head_norm"
+  const bool post = rn || glu_y || hn || gd;
+  ns2::ProfScope prof_(rn ? "gemm_bf16_add_rmsnorm" : glu_y ? "gemm_bf16_glu" : gd ? "gemm_bf16_glu_down" : hn ? "gemm_bf16_head_norm"
                           : p.M <= kGemvMaxM ? (W_BF16 ? "gemv_bf16" : "gemv_i8") : (W_BF16 ? "gemm_bf16" : "gemm_i8"));
   const long long big_tiles = (long long)((p.N + 127) / 128) * ((p.M + 127) / 128);
   if (!post && p.M == 1 && W_BF16 && A_F32 && p.K % 512 == 0 && p.K <= 2048 && aligned16(p.A)) {
@@ -819,6 +917,8 @@ int launch_gemm(const GemmArgs& p, const char* name, const RowNorm* rn = nullptr
       if (hn->D == 64) splitk_head_norm_kernel<64><<<p.M, 64, 0, s>>>(q, splits, *hn);
       else if (hn->D == 128) splitk_head_norm_kernel<128><<<p.M, 128, 0, s>>>(q, splits, *hn);
       else splitk_head_norm_kernel<256><<<p.M, 256, 0, s>>>(q, splits, *hn);
+    } else if (gd) {
+      splitk_glu_down_kernel<<<dim3((p.M + 15) / 16, p.N / 2 / 256), 512, 0, s>>>(q, splits, *gd);
     } else if (glu_y) {
       const long long n = (long long)p.M * (p.N / 2);
       splitk_glu_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(q, splits, glu_y, glu_act);
@@ -1027,6 +1127,24 @@ int ns2_linear_bf16_glu(const float* A, int lda, const uint16_t* W, const float*
   int rc = check_common(p, "ns2_linear_bf16_glu");
   if (rc) return rc;
   return launch_gemm<true, true>(p, "linear_bf16_glu", nullptr, Y, act);
+}
+
+int ns2_linear_bf16_glu_down(const float* A, int lda, const uint16_t* W, const float* bias, int M, int N, int K,
+                             int act, const uint16_t* wd_tiled, int Nd, float* part) {
+  NS2_READY();
+  if (M == 0) return NS2_OK;
+  const char* fn = "ns2_linear_bf16_glu_down";
+  NS2_REQUIRE(wd_tiled && part, "%s: null wd_tiled or part", fn);
+  NS2_REQUIRE(N % 512 == 0 && Nd > 0 && Nd % 64 == 0,
+              "%s: N=%d must be a multiple of 512 (256-column GLU groups) and Nd=%d of 64", fn, N, Nd);
+  NS2_REQUIRE(act >= NS2_ACT_NONE && act <= NS2_ACT_GELU_TANH, "%s: unknown act %d", fn, act);
+  NS2_REQUIRE(aligned16(wd_tiled) && part != A, "%s: wd_tiled must be 16-byte aligned and part must not alias A", fn);
+  // C is not written on this path; part stands in for the check
+  GemmArgs p{A, W, nullptr, bias, nullptr, part, nullptr, 0, 0, lda, N, M, N, K, 1.0f, NS2_ACT_NONE, 0};
+  int rc = check_common(p, fn);
+  if (rc) return rc;
+  const GluDown gd{reinterpret_cast<const half_t*>(wd_tiled), part, Nd, act};
+  return launch_gemm<true, true>(p, "linear_bf16_glu_down", nullptr, nullptr, 0, nullptr, &gd);
 }
 
 int ns2_linear_bf16_lora(const float* A, int lda, const uint16_t* W, const float* bias,

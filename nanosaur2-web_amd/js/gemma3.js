@@ -52,8 +52,10 @@ export class Gemma3 {
     m.layers = [];
     for (let i = 0; i < RUN; i++) {
       const l = await loadLayer(gpu, st, i);
-      // o_proj re-tiled as fp16 (next to its row-major copy) for the attention's fused projection
+      // o_proj and down re-tiled as fp16 (next to their row-major copies) for the fused
+      // projections of the attention and of the GLU
       if (ops.tileablePlain(l.o)) ops.tileWeight(gpu, l.o);
+      if (ops.tileablePlain(l.down)) ops.tileWeight(gpu, l.down);
       m.layers.push(l);
       if (onProgress) onProgress((i + 1) / RUN);
     }
@@ -128,11 +130,21 @@ export class Gemma3 {
         h2 = ops.linearAddRmsnorm(gpu, a, l.o, x, l.postAttnNorm, l.preMlpNorm);
         a.release();
       }
-      const g = ops.linearGlu(gpu, h2, l.gateUp, "gelu_tanh");
-      h2.release();
       const next = i + 1 < this.layers.length ? this.layers[i + 1].inNorm : this.norm;
-      h = ops.linearAddRmsnorm(gpu, g, l.down, x, l.postMlpNorm, next);
-      g.release();
+      const noLora = (W) => !(W.lora && W.lora.length);
+      if (l.gateUp.kind === "bf16" && noLora(l.gateUp) && l.gateUp.N % 512 === 0 && l.down.tbuf && noLora(l.down)) {
+        // the GLU's row kernel writes the down projection's shares per 256-column group, summed
+        // by the post-norm's row kernel
+        const part = ops.linearGluDown(gpu, h2, l.gateUp, l.down, "gelu_tanh");
+        h2.release();
+        h = ops.partsAddRmsnorm(gpu, part, l.gateUp.N / 512, l.down.bias, x, l.postMlpNorm, next);
+        part.release();
+      } else {
+        const g = ops.linearGlu(gpu, h2, l.gateUp, "gelu_tanh");
+        h2.release();
+        h = ops.linearAddRmsnorm(gpu, g, l.down, x, l.postMlpNorm, next);
+        g.release();
+      }
     });
     x.release();
     return h; // the final norm of the last layer's output

@@ -110,6 +110,7 @@ SIGNATURES = {
     "ns2_add_rmsnorm": [c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_float],
     "ns2_transpose": [c_vp, c_vp, c_int, c_int],
     "ns2_linear_bf16_glu": [c_vp, c_int, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int],
+    "ns2_linear_bf16_glu_down": [c_vp, c_int, c_vp, c_vp, c_int, c_int, c_int, c_int, c_vp, c_int, c_vp],
     "ns2_linear_bf16_head_norm": [c_vp, c_int, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_vp, c_int, c_vp, c_int,
                                   c_int, c_vp, c_ll, c_int, c_float],
     "ns2_linear_bf16_head_norm_f16kv": [c_vp, c_int, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_vp, c_int, c_vp,
@@ -400,6 +401,11 @@ class Lib:
 
     def linear_bf16_glu(self, A, lda, W, bias, Y, M, N, K, act="gelu_tanh"):
         self.call("ns2_linear_bf16_glu", _ptr(A), lda, _ptr(W), _ptr(bias), _ptr(Y), M, N, K, ACT[act])
+
+    def linear_bf16_glu_down(self, A, lda, W, bias, M, N, K, wd_tiled, Nd, part, act="gelu_tanh"):
+        """linear_bf16_glu and the next linear's shares per 256-column group into part [N/512, M, Nd]."""
+        self.call("ns2_linear_bf16_glu_down", _ptr(A), lda, _ptr(W), _ptr(bias), M, N, K, ACT[act], _ptr(wd_tiled), Nd,
+                  _ptr(part))
 
     def linear_bf16_add_rmsnorm(self, A, lda, W, bias, x, w_add, w_out, y, M, N, K, eps=1e-6):
         self.call("ns2_linear_bf16_add_rmsnorm", _ptr(A), lda, _ptr(W), _ptr(bias), _ptr(x), _ptr(w_add),

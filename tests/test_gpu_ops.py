@@ -1008,6 +1008,39 @@ def test_linear_bf16_glu(ns2lib, M, bias):
     assert_close(y.cpu(), ref, TOL, "linear_bf16_glu")
 
 
+@pytest.mark.parametrize("M,bias,Nd", [(256, False, 640), (37, True, 640), (1, False, 640), (100, True, 192)])
+def test_linear_bf16_glu_down(ns2lib, M, bias, Nd):
+    """ns2_linear_bf16_glu_down (Gemma3's gate/up, GELU-tanh gate and down projection,
+    app/models/gemma3.js:79-83): the shares per 256-column group, summed, against
+    ns2_linear_bf16_glu + ns2_linear_bf16 of its output (the same fp16 roundings of the GLU output
+    and of W_d, the products summed in another association: 5e-5 of the largest output where
+    that linear runs its matrix-core path; at M <= 8 it runs an fp32 GEMV: TOL), and against the
+    oracle in fp64 (TOL). The GLU output itself is bit-identical to ns2_linear_bf16_glu's."""
+    N, K, I = 4096, 640, 2048
+    g = gen(M * 3 + 5 * bias + Nd)
+    a = torch.randn(M, K, generator=g)
+    w = (torch.randn(N, K, generator=g) * 0.05).to(torch.bfloat16)
+    b = torch.randn(N, generator=g) * 0.1 if bias else None
+    wdn = (torch.randn(Nd, I, generator=g) * 0.03).to(torch.bfloat16)
+    ad, wd, bd = a.to(dev), w.view(torch.int16).to(dev), (b.to(dev) if bias else None)
+    wdd = wdn.view(torch.int16).to(dev)
+    wdt = torch.empty(Nd * I, dtype=torch.int16, device=dev)
+    ns2lib.tile_bf16_weight(wdd, wdt, Nd, I)
+    part = torch.full((I // 256, M, Nd), float("nan"), device=dev)
+    ns2lib.linear_bf16_glu_down(ad, K, wd, bd, M, N, K, wdt, Nd, part, "gelu_tanh")
+    y = torch.empty(M, I, device=dev)
+    ns2lib.linear_bf16_glu(ad, K, wd, bd, y, M, N, K, "gelu_tanh")
+    t = torch.empty(M, Nd, device=dev)
+    ns2lib.linear_bf16(y, I, wdd, t, M, Nd, I)
+    torch.cuda.synchronize()
+    assert torch.isfinite(part.cpu()).all(), "every share written"
+    got = part.cpu().double().sum(0)
+    assert_close(got, t.cpu().double(), 5e-5 if M > 8 else TOL, f"GLU + down vs two launches (M={M}, Nd={Nd})")
+    tr = O.linear_bf16(a.double(), w, bias=b.double() if bias else None)
+    ref = (torch.nn.functional.gelu(tr[:, :I], approximate="tanh") * tr[:, I:]) @ wdn.double().t()
+    assert_close(got, ref, TOL, f"GLU + down vs the oracle (M={M}, Nd={Nd})")
+
+
 @pytest.mark.parametrize("M,bias,rope", [(256, False, True), (37, True, True), (5, False, False)])
 def test_linear_bf16_head_norm(ns2lib, M, bias, rope):
     """Gemma3's q/k/v projection with the q and k head norms (and RoPE) in its split-K sum
