@@ -427,12 +427,12 @@ int ns2_linear_bf16_head_norm_f16kv(const float* A, int lda, const uint16_t* W, 
  * [M, N/2]. Additive to the reference interface. */
 int ns2_linear_bf16_glu(const float* A, int lda, const uint16_t* W, const float* bias, float* Y, int M, int N,
                         int K, int act);
-/* ns2_linear_bf16_glu followed by the next linear split over the GLU output's 256-column groups
+/* ns2_linear_bf16_glu followed by the next linear split over the GLU output's 128-column groups
  * (the Gemma3 MLP's down projection, app/models/gemma3.js:79-83), without the [M, N/2] GLU
- * output in HBM: for each group r, with y_r its [M, 256] columns rounded to fp16 (as a linear
- * rounds its input), part[r] [M, Nd] = y_r W_d[:, 256r:256(r+1)]^T, fp32. wd_tiled: W_d [Nd, N/2]
- * as ns2_tile_bf16_weight writes it. The N/512 shares sum to the product without bias;
- * ns2_parts_add_rmsnorm adds them. N % 512 == 0, Nd % 64 == 0. Additive to the reference
+ * output in HBM: for each group r, with y_r its [M, 128] columns rounded to fp16 (as a linear
+ * rounds its input), part[r] [M, Nd] = y_r W_d[:, 128r:128(r+1)]^T, fp32. wd_tiled: W_d [Nd, N/2]
+ * as ns2_tile_bf16_weight writes it. The N/256 shares sum to the product without bias;
+ * ns2_parts_add_rmsnorm adds them. N % 256 == 0, Nd % 64 == 0. Additive to the reference
  * interface. */
 int ns2_linear_bf16_glu_down(const float* A, int lda, const uint16_t* W, const float* bias, int M, int N, int K,
                              int act, const uint16_t* wd_tiled, int Nd, float* part);

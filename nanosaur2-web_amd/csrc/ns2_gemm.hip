@@ -457,21 +457,25 @@ __global__ __launch_bounds__(256) void splitk_glu_kernel(GemmArgs p, int splits,
 }
 
 // Split-K sum of a gate/up product, its GLU, and the linear after it split over the GLU
-// output's 256-column groups (Gemma3's MLP, app/models/gemma3.js:79-83). Block (16 rows, group r)
+// output's GS-column groups (Gemma3's MLP, app/models/gemma3.js:79-83). Block (16 rows, group r)
 // forms y = act(gate) * up for its rows and the group's columns with splitk_glu_kernel's
 // arithmetic, rounds y to fp16 into LDS (as the next linear's loader rounds its input) and
-// multiplies it by the next weight's 256 columns of group r (fp16 tiles, tile_w16_kernel's
+// multiplies it by the next weight's GS columns of group r (fp16 tiles, tile_w16_kernel's
 // layout) on v_mfma_f32_16x16x16_f16: share r of that product, out[r][m][n] fp32 for n < Nd.
-// The I/256 shares, summed in r order, are the product without bias. Each wave takes 16-column
+// The I/GS shares, summed in r order, are the product without bias. Each wave takes 16-column
 // tiles n0 = 16w, 16(w + 8), ...; the weight fragments of its first JC tiles are loaded before
 // the split sums are read (they do not depend on them), the rest JC tiles per round trip.
+// GLU output columns per share: 128 makes 16 x 16 = 256 blocks at 256 rows (one per CU), each
+// streaming 160 KB of the down weight from L2 (256: 128 blocks of 320 KB, 11.3 us per layer)
+constexpr int kGluDownGroup = 128;
 struct GluDown {
   const half_t* wd;  // the next weight [Nd][I] as fp16 tiles
-  float* out;        // [I/256][M][Nd]
+  float* out;        // [I/GS][M][Nd]
   int Nd, act;
 };
+template <int GS>
 __global__ __launch_bounds__(512) void splitk_glu_down_kernel(GemmArgs p, int splits, GluDown gd) {
-  constexpr int NW = 8, GS = 256, OS = GS + 8, DB = GS / 16, JC = 5;
+  constexpr int NW = 8, OS = GS + 8, DB = GS / 16, JC = 5, CPT = GS * 16 / 512;  // GLU columns per thread
   __shared__ __attribute__((aligned(16))) half_t g16[16 * OS];
   const int I = p.N / 2;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, col = lane & 15, grp = lane >> 4;
@@ -493,26 +497,29 @@ __global__ __launch_bounds__(512) void splitk_glu_down_kernel(GemmArgs p, int sp
   };
   load_w(wave);
   {
-    // thread: row rr, columns c8 .. c8 + 7 of the group (rows past M repeat the last row)
-    const int rr = tid >> 5, c8 = (tid & 31) * 8;
+    // thread: row rr, columns c8 .. c8 + CPT - 1 of the group (rows past M repeat the last row)
+    static_assert(CPT == 4 || CPT == 8, "4 or 8 GLU columns per thread");
+    const int rr = tid / (GS / CPT), c8 = (tid % (GS / CPT)) * CPT;
     const long long m = m0 + rr < p.M ? m0 + rr : p.M - 1;
     const long long mn = (long long)p.M * p.N;
     const float* gp = p.part + m * p.N + j0 + c8;
-    float g[8], u[8];
+    float g[CPT], u[CPT];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) g[e] = u[e] = 0.f;
+    for (int e = 0; e < CPT; ++e) g[e] = u[e] = 0.f;
     // two splits' loads in flight at a time (the weight fragments above hold most registers)
 #pragma unroll 2
     for (int z = 0; z < splits; ++z) {
-      const float4 g0 = *reinterpret_cast<const float4*>(gp + z * mn), g1 = *reinterpret_cast<const float4*>(gp + z * mn + 4);
-      const float4 u0 = *reinterpret_cast<const float4*>(gp + z * mn + I);
-      const float4 u1 = *reinterpret_cast<const float4*>(gp + z * mn + I + 4);
-      g[0] += g0.x, g[1] += g0.y, g[2] += g0.z, g[3] += g0.w, g[4] += g1.x, g[5] += g1.y, g[6] += g1.z, g[7] += g1.w;
-      u[0] += u0.x, u[1] += u0.y, u[2] += u0.z, u[3] += u0.w, u[4] += u1.x, u[5] += u1.y, u[6] += u1.z, u[7] += u1.w;
-    }
-    half8_t hv;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
+      for (int e4 = 0; e4 < CPT; e4 += 4) {
+        const float4 gv = *reinterpret_cast<const float4*>(gp + z * mn + e4);
+        const float4 uv = *reinterpret_cast<const float4*>(gp + z * mn + I + e4);
+        g[e4] += gv.x, g[e4 + 1] += gv.y, g[e4 + 2] += gv.z, g[e4 + 3] += gv.w;
+        u[e4] += uv.x, u[e4 + 1] += uv.y, u[e4 + 2] += uv.z, u[e4 + 3] += uv.w;
+      }
+    }
+    half_t hv[CPT];
+#pragma unroll
+    for (int e = 0; e < CPT; ++e) {
       const int j = j0 + c8 + e;
       float a = g[e] * p.alpha, b = u[e] * p.alpha;
       if (p.scale) {
@@ -528,7 +535,11 @@ __global__ __launch_bounds__(512) void splitk_glu_down_kernel(GemmArgs p, int sp
       asm volatile("" : "+v"(y));
       hv[e] = (half_t)y;
     }
-    *reinterpret_cast<half8_t*>(&g16[rr * OS + c8]) = hv;
+    if constexpr (CPT == 8) {
+      *reinterpret_cast<half8_t*>(&g16[rr * OS + c8]) = half8_t{hv[0], hv[1], hv[2], hv[3], hv[4], hv[5], hv[6], hv[7]};
+    } else {
+      *reinterpret_cast<half4_t*>(&g16[rr * OS + c8]) = half4_t{hv[0], hv[1], hv[2], hv[3]};
+    }
   }
   __syncthreads();
   half4_t af[DB];
@@ -918,7 +929,7 @@ int launch_gemm(const GemmArgs& p, const char* name, const RowNorm* rn = nullptr
       else if (hn->D == 128) splitk_head_norm_kernel<128><<<p.M, 128, 0, s>>>(q, splits, *hn);
       else splitk_head_norm_kernel<256><<<p.M, 256, 0, s>>>(q, splits, *hn);
     } else if (gd) {
-      splitk_glu_down_kernel<<<dim3((p.M + 15) / 16, p.N / 2 / 256), 512, 0, s>>>(q, splits, *gd);
+      splitk_glu_down_kernel<kGluDownGroup><<<dim3((p.M + 15) / 16, p.N / 2 / kGluDownGroup), 512, 0, s>>>(q, splits, *gd);
     } else if (glu_y) {
       const long long n = (long long)p.M * (p.N / 2);
       splitk_glu_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(q, splits, glu_y, glu_act);
@@ -1135,8 +1146,9 @@ int ns2_linear_bf16_glu_down(const float* A, int lda, const uint16_t* W, const f
   if (M == 0) return NS2_OK;
   const char* fn = "ns2_linear_bf16_glu_down";
   NS2_REQUIRE(wd_tiled && part, "%s: null wd_tiled or part", fn);
-  NS2_REQUIRE(N % 512 == 0 && Nd > 0 && Nd % 64 == 0,
-              "%s: N=%d must be a multiple of 512 (256-column GLU groups) and Nd=%d of 64", fn, N, Nd);
+  NS2_REQUIRE(N % (2 * kGluDownGroup) == 0 && Nd > 0 && Nd % 64 == 0,
+              "%s: N=%d must be a multiple of %d (%d-column GLU groups) and Nd=%d of 64", fn, N, 2 * kGluDownGroup,
+              kGluDownGroup, Nd);
   NS2_REQUIRE(act >= NS2_ACT_NONE && act <= NS2_ACT_GELU_TANH, "%s: unknown act %d", fn, act);
   NS2_REQUIRE(aligned16(wd_tiled) && part != A, "%s: wd_tiled must be 16-byte aligned and part must not alias A", fn);
   // C is not written on this path; part stands in for the check

@@ -132,12 +132,13 @@ export class Gemma3 {
       }
       const next = i + 1 < this.layers.length ? this.layers[i + 1].inNorm : this.norm;
       const noLora = (W) => !(W.lora && W.lora.length);
-      if (l.gateUp.kind === "bf16" && noLora(l.gateUp) && l.gateUp.N % 512 === 0 && l.down.tbuf && noLora(l.down)) {
-        // the GLU's row kernel writes the down projection's shares per 256-column group, summed
-        // by the post-norm's row kernel
+      const shares = l.gateUp.N / (2 * ops.GLU_DOWN_GROUP);
+      if (l.gateUp.kind === "bf16" && noLora(l.gateUp) && Number.isInteger(shares) && l.down.tbuf && noLora(l.down)) {
+        // the GLU's row kernel writes the down projection's shares per column group, summed by
+        // the post-norm's row kernel
         const part = ops.linearGluDown(gpu, h2, l.gateUp, l.down, "gelu_tanh");
         h2.release();
-        h = ops.partsAddRmsnorm(gpu, part, l.gateUp.N / 512, l.down.bias, x, l.postMlpNorm, next);
+        h = ops.partsAddRmsnorm(gpu, part, shares, l.down.bias, x, l.postMlpNorm, next);
         part.release();
       } else {
         const g = ops.linearGlu(gpu, h2, l.gateUp, "gelu_tanh");

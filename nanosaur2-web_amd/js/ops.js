@@ -284,15 +284,18 @@ export function attentionRowsF16kvOproj(gpu, { q, kv, Lq, Lk, H, D, ldq, qOff = 
   return part;
 }
 
+// GLU output columns per share of linearGluDown (the library's group width)
+export const GLU_DOWN_GROUP = 128;
+
 // linearGlu(a, W) and the linear by Wd after it (Gemma3's gate/up, GLU and down projection,
 // app/models/gemma3.js:79-83; addition to the reference ops) without the GLU output in HBM: the
-// GLU's row kernel multiplies each 256-column group of its output by Wd's matching columns
-// (a bf16 weight re-tiled as fp16, Wd.tbuf). Returns the shares [W.N/512, M, Wd.N]; they sum
+// GLU's row kernel multiplies each 128-column group of its output by Wd's matching columns
+// (a bf16 weight re-tiled as fp16, Wd.tbuf). Returns the shares [W.N/256, M, Wd.N]; they sum
 // to the product without bias (partsAddRmsnorm adds them and the bias).
 export function linearGluDown(gpu, a, W, Wd, act = "gelu_tanh") {
   if (!Wd.tbuf || Wd.kind !== "bf16" || Wd.K !== W.N / 2) throw new Error(`${Wd.name}: the fused down projection needs a re-tiled bf16 weight of K = N/2`);
   const M = a.size / W.K;
-  const part = gpu.empty([W.N / 512, M, Wd.N]);
+  const part = gpu.empty([W.N / (2 * GLU_DOWN_GROUP), M, Wd.N]);
   gpu.run("te.mlp+glu+down", 2 * M * W.N * W.K + 2 * M * Wd.N * Wd.K, () =>
     native.linearBf16GluDown(addr(a), W.K, addr(W.buf), addr(W.bias || null), M, W.N, W.K, ACT[act], addr(Wd.tbuf),
       Wd.N, addr(part)));

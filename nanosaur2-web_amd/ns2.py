@@ -403,7 +403,7 @@ class Lib:
         self.call("ns2_linear_bf16_glu", _ptr(A), lda, _ptr(W), _ptr(bias), _ptr(Y), M, N, K, ACT[act])
 
     def linear_bf16_glu_down(self, A, lda, W, bias, M, N, K, wd_tiled, Nd, part, act="gelu_tanh"):
-        """linear_bf16_glu and the next linear's shares per 256-column group into part [N/512, M, Nd]."""
+        """linear_bf16_glu and the next linear's shares per 128-column group into part [N/256, M, Nd]."""
         self.call("ns2_linear_bf16_glu_down", _ptr(A), lda, _ptr(W), _ptr(bias), M, N, K, ACT[act], _ptr(wd_tiled), Nd,
                   _ptr(part))
 

@@ -1011,7 +1011,7 @@ def test_linear_bf16_glu(ns2lib, M, bias):
 @pytest.mark.parametrize("M,bias,Nd", [(256, False, 640), (37, True, 640), (1, False, 640), (100, True, 192)])
 def test_linear_bf16_glu_down(ns2lib, M, bias, Nd):
     """ns2_linear_bf16_glu_down (Gemma3's gate/up, GELU-tanh gate and down projection,
-    app/models/gemma3.js:79-83): the shares per 256-column group, summed, against
+    app/models/gemma3.js:79-83): the shares per 128-column group, summed, against
     ns2_linear_bf16_glu + ns2_linear_bf16 of its output (the same fp16 roundings of the GLU output
     and of W_d, the products summed in another association: 5e-5 of the largest output where
     that linear runs its matrix-core path; at M <= 8 it runs an fp32 GEMV: TOL), and against the
@@ -1026,7 +1026,7 @@ def test_linear_bf16_glu_down(ns2lib, M, bias, Nd):
     wdd = wdn.view(torch.int16).to(dev)
     wdt = torch.empty(Nd * I, dtype=torch.int16, device=dev)
     ns2lib.tile_bf16_weight(wdd, wdt, Nd, I)
-    part = torch.full((I // 256, M, Nd), float("nan"), device=dev)
+    part = torch.full((I // 128, M, Nd), float("nan"), device=dev)
     ns2lib.linear_bf16_glu_down(ad, K, wd, bd, M, N, K, wdt, Nd, part, "gelu_tanh")
     y = torch.empty(M, I, device=dev)
     ns2lib.linear_bf16_glu(ad, K, wd, bd, y, M, N, K, "gelu_tanh")
