@@ -436,6 +436,18 @@ int ns2_linear_bf16_glu(const float* A, int lda, const uint16_t* W, const float*
  * interface. */
 int ns2_linear_bf16_glu_down(const float* A, int lda, const uint16_t* W, const float* bias, int M, int N, int K,
                              int act, const uint16_t* wd_tiled, int Nd, float* part);
+/* The Gemma3 layer's linears on the tiled fp16 path (the bf16 weights re-tiled as fp16 by
+ * ns2_tile_bf16_weight, the inputs as tiled fp16 operands [ceil(M/64)*64][K] as
+ * ns2_parts_add_rmsnorm_tiled or ns2_to_tiled_f16 write them): ns2_linear_bf16_head_norm_f16kv
+ * and ns2_linear_bf16_glu_down with the same outputs, up to the fp32 association of the K sums
+ * (the inputs and weights rounded to fp16 the same way). K % 64 == 0. Additive to the reference
+ * interface. */
+int ns2_linear_f16w_tiled_head_norm_f16kv(const uint16_t* At, const uint16_t* Wt, const float* bias, float* C, int M,
+                                          int N, int K, const float* w1, int H1, const float* w2, int H2, int D,
+                                          const float* cs, long long sin_off, int rope_rows, float eps,
+                                          uint16_t* kv16, int ldkv);
+int ns2_linear_f16w_tiled_glu_down(const uint16_t* At, const uint16_t* Wt, const float* bias, int M, int N, int K,
+                                   int act, const uint16_t* wd_tiled, int Nd, float* part);
 int ns2_linear_bf16_add_rmsnorm(const float* A, int lda, const uint16_t* W, const float* bias, float* x,
                                 const float* w_add, const float* w_out, float* y, int M, int N, int K,
                                 float eps);
@@ -445,6 +457,11 @@ int ns2_linear_bf16_add_rmsnorm(const float* A, int lda, const uint16_t* W, cons
  * app/models/gemma3.js:74-79). N <= 1024. Additive to the reference interface. */
 int ns2_parts_add_rmsnorm(const float* part, int splits, const float* bias, float* x, const float* w_add,
                           const float* w_out, float* y, int M, int N, float eps);
+/* ns2_parts_add_rmsnorm with y written as the tiled fp16 operand of the next linear
+ * ([ceil(M/64)*64][N], each value rounded once; rows past M untouched). N % 64 == 0. Additive to
+ * the reference interface. */
+int ns2_parts_add_rmsnorm_tiled(const float* part, int splits, const float* bias, float* x, const float* w_add,
+                                const float* w_out, uint16_t* yt, int M, int N, float eps);
 
 #ifdef __cplusplus
 }

@@ -934,6 +934,59 @@ napi_value LinearBf16GluDown(napi_env env, napi_callback_info info) {
   return check(env, c, ns2_linear_bf16_glu_down(A, lda, W, bias, M, N, K, act, wd, Nd, part));
 }
 
+// partsAddRmsnormTiled(part, splits, bias, x, wAdd, wOut, yt, M, N, eps)
+napi_value PartsAddRmsnormTiled(napi_env env, napi_callback_info info) {
+  ARGS(10);
+  auto part = (const float*)c.ptr(0);
+  int splits = c.i32(1);
+  auto bias = (const float*)c.ptr(2);
+  auto x = (float*)c.ptr(3);
+  auto wAdd = (const float*)c.ptr(4);
+  auto wOut = (const float*)c.ptr(5);
+  auto yt = (uint16_t*)c.ptr(6);
+  int M = c.i32(7), N = c.i32(8);
+  float eps = c.f32(9);
+  if (c.failed) return nullptr;
+  return check(env, c, ns2_parts_add_rmsnorm_tiled(part, splits, bias, x, wAdd, wOut, yt, M, N, eps));
+}
+
+// linearF16wTiledHeadNormF16kv(At, Wt, bias, C, M, N, K, w1, H1, w2, H2, D, cs, sinOff, ropeRows, eps, kv16, ldkv)
+napi_value LinearF16wTiledHeadNormF16kv(napi_env env, napi_callback_info info) {
+  ARGS(18);
+  auto At = (const uint16_t*)c.ptr(0);
+  auto Wt = (const uint16_t*)c.ptr(1);
+  auto bias = (const float*)c.ptr(2);
+  auto C = (float*)c.ptr(3);
+  int M = c.i32(4), N = c.i32(5), K = c.i32(6);
+  auto w1 = (const float*)c.ptr(7);
+  int H1 = c.i32(8);
+  auto w2 = (const float*)c.ptr(9);
+  int H2 = c.i32(10), D = c.i32(11);
+  auto cs = (const float*)c.ptr(12);
+  long long sinOff = c.i64(13);
+  int ropeRows = c.i32(14);
+  float eps = c.f32(15);
+  auto kv16 = (uint16_t*)c.ptr(16);
+  int ldkv = c.i32(17);
+  if (c.failed) return nullptr;
+  return check(env, c, ns2_linear_f16w_tiled_head_norm_f16kv(At, Wt, bias, C, M, N, K, w1, H1, w2, H2, D, cs, sinOff,
+                                                             ropeRows, eps, kv16, ldkv));
+}
+
+// linearF16wTiledGluDown(At, Wt, bias, M, N, K, act, wdTiled, Nd, part)
+napi_value LinearF16wTiledGluDown(napi_env env, napi_callback_info info) {
+  ARGS(10);
+  auto At = (const uint16_t*)c.ptr(0);
+  auto Wt = (const uint16_t*)c.ptr(1);
+  auto bias = (const float*)c.ptr(2);
+  int M = c.i32(3), N = c.i32(4), K = c.i32(5), act = c.i32(6);
+  auto wd = (const uint16_t*)c.ptr(7);
+  int Nd = c.i32(8);
+  auto part = (float*)c.ptr(9);
+  if (c.failed) return nullptr;
+  return check(env, c, ns2_linear_f16w_tiled_glu_down(At, Wt, bias, M, N, K, act, wd, Nd, part));
+}
+
 // linearBf16AddRmsnorm(A, lda, W, bias, x, wAdd, wOut, y, M, N, K, eps)
 napi_value LinearBf16AddRmsnorm(napi_env env, napi_callback_info info) {
   ARGS(12);
@@ -976,7 +1029,9 @@ napi_value Module(napi_env env, napi_value exports) {
       {"glu", GluT<false>}, {"gluRotateF16", GluT<true>}, {"elementwise", Elementwise},
       {"accumulate", Accumulate}, {"addRows", AddRows}, {"rowSum", RowSum}, {"rmsnorm", Rmsnorm},
       {"addRmsnorm", AddRmsnorm}, {"linearBf16AddRmsnorm", LinearBf16AddRmsnorm},
-      {"linearBf16Glu", LinearBf16Glu}, {"linearBf16GluDown", LinearBf16GluDown}, {"linearBf16HeadNorm", LinearBf16HeadNorm},
+      {"linearBf16Glu", LinearBf16Glu}, {"linearBf16GluDown", LinearBf16GluDown},
+      {"partsAddRmsnormTiled", PartsAddRmsnormTiled}, {"linearF16wTiledHeadNormF16kv", LinearF16wTiledHeadNormF16kv},
+      {"linearF16wTiledGluDown", LinearF16wTiledGluDown}, {"linearBf16HeadNorm", LinearBf16HeadNorm},
       {"linearBf16HeadNormF16kv", LinearBf16HeadNormF16kv}, {"transpose", Transpose},
   };
   for (const Fn& f : fns) {

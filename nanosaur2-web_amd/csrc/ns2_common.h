@@ -30,6 +30,11 @@ void* noalloc_scratch();
 // tiled operand layout of the int8 GEMM (K columns). Returns a status code.
 int lora_prepare(const float** t, const uint16_t* lora_a, const uint16_t* lora_b, int R, const void* x, int x_fmt,
                  int ldx, int M, int K, const char* name);
+// The tiled linear over a re-tiled fp16 weight without its epilogue: the raw products of At Wt^T
+// split over K into *splits fp32 partials *part ([*splits][M][N], library scratch slot 5, summed
+// in split order by the caller's row kernel). At fp16 tiled [ceil(M/64)*64][K]. Returns a status code.
+int linear_f16w_tiled_raw(const char* fn, const uint16_t* At, const uint16_t* Wt, int M, int N, int K, float** part,
+                          int* splits);
 
 // Kernel profiler (ns2_profile_*): when enabled, stream events bracket every launch and are
 // aggregated by kernel name on ns2_profile_report.

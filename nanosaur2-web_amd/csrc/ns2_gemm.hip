@@ -302,6 +302,9 @@ struct RowNorm {
   const float* w_out;
   float* y;
   float eps;
+  // y as the tiled fp16 operand of the next linear (K = N columns) instead of fp32: each value
+  // rounded once to nearest
+  uint16_t* yt;
 };
 __global__ __launch_bounds__(256) void splitk_add_rmsnorm_kernel(GemmArgs p, int splits, RowNorm rn) {
   constexpr int C = kRowNormCols;
@@ -352,11 +355,19 @@ __global__ __launch_bounds__(256) void splitk_add_rmsnorm_kernel(GemmArgs p, int
       sx += v * v;
     }
   }
-  if (!rn.y) return;
+  if (!rn.y && !rn.yt) return;
   const float r2 = rsqrtf(block_sum(sx, red) / (float)N + rn.eps);
 #pragma unroll
   for (int j = 0; j < C; ++j)
-    if (tid + 256 * j < N) rn.y[row + col[j]] = t[j] * r2 * rn.w_out[col[j]];
+    if (tid + 256 * j < N) {
+      float v = t[j] * r2 * rn.w_out[col[j]];
+      if (rn.yt) {
+        asm volatile("" : "+v"(v));  // the fp32 value, then one rounding (no fused conversion)
+        reinterpret_cast<half_t*>(rn.yt)[tiled_off(blockIdx.x, col[j], N)] = (half_t)v;
+      } else {
+        rn.y[row + col[j]] = v;
+      }
+    }
 }
 
 // Split-K sum of a stacked q|k|v product followed by the per-head norms of app/gpu/ops.js:
@@ -1157,6 +1168,79 @@ int ns2_linear_bf16_glu_down(const float* A, int lda, const uint16_t* W, const f
   if (rc) return rc;
   const GluDown gd{reinterpret_cast<const half_t*>(wd_tiled), part, Nd, act};
   return launch_gemm<true, true>(p, "linear_bf16_glu_down", nullptr, nullptr, 0, nullptr, &gd);
+}
+
+int ns2_parts_add_rmsnorm_tiled(const float* part, int splits, const float* bias, float* x, const float* w_add,
+                                const float* w_out, uint16_t* yt, int M, int N, float eps) {
+  NS2_READY();
+  if (M == 0) return NS2_OK;
+  const char* fn = "ns2_parts_add_rmsnorm_tiled";
+  NS2_REQUIRE(part && x && w_add && w_out && yt, "%s: null part, x, w_add, w_out or yt", fn);
+  NS2_REQUIRE(splits > 0 && M > 0 && N > 0 && N % 64 == 0 && N <= kRowNormMaxN,
+              "%s: splits=%d M=%d N=%d (N %% 64 == 0, N <= %d)", fn, splits, M, N, kRowNormMaxN);
+  NS2_REQUIRE(part != x && aligned16(yt), "%s: x must not alias part; yt 16-byte aligned", fn);
+  GemmArgs p{nullptr, nullptr, nullptr, bias, nullptr, x, nullptr, 0, 0, 0, N, M, N, 0, 1.0f, NS2_ACT_NONE, 0};
+  p.part = const_cast<float*>(part);
+  const RowNorm rn{x, w_add, w_out, nullptr, eps, yt};
+  ns2::ProfScope prof_("parts_add_rmsnorm");
+  splitk_add_rmsnorm_kernel<<<M, 256, 0, ns2::stream()>>>(p, splits, rn);
+  NS2_LAUNCHED("parts_add_rmsnorm");
+  return NS2_OK;
+}
+
+int ns2_linear_f16w_tiled_head_norm_f16kv(const uint16_t* At, const uint16_t* Wt, const float* bias, float* C, int M,
+                                          int N, int K, const float* w1, int H1, const float* w2, int H2, int D,
+                                          const float* cs, long long sin_off, int rope_rows, float eps,
+                                          uint16_t* kv16, int ldkv) {
+  NS2_READY();
+  if (M == 0) return NS2_OK;
+  const char* fn = "ns2_linear_f16w_tiled_head_norm_f16kv";
+  NS2_REQUIRE(C && kv16, "%s: null C or kv16", fn);
+  NS2_REQUIRE(D == 64 || D == 128 || D == 256, "%s: head dim %d is not 64, 128 or 256", fn, D);
+  NS2_REQUIRE(N % D == 0 && N / D <= kHeadNormMaxHeads && H1 >= 0 && H2 >= 0 && (H1 + H2) * D <= N &&
+                  (!H1 || w1) && (!H2 || w2),
+              "%s: N=%d (at most %d heads of %d), H1=%d, H2=%d or their weights", fn, N, kHeadNormMaxHeads, D, H1,
+              H2);
+  NS2_REQUIRE(ldkv >= N - H1 * D, "%s: ldkv=%d is below the %d fp16 key/value columns", fn, ldkv, N - H1 * D);
+  float* part = nullptr;
+  int splits = 1;
+  int rc = ns2::linear_f16w_tiled_raw(fn, At, Wt, M, N, K, &part, &splits);
+  if (rc) return rc;
+  GemmArgs q{nullptr, nullptr, nullptr, bias, nullptr, C, nullptr, 0, 0, 0, N, M, N, K, 1.0f, NS2_ACT_NONE, 0};
+  q.part = part;
+  const HeadNorm hn{w1, H1, w2, H2, D, cs, sin_off, cs ? rope_rows : 0, eps, reinterpret_cast<half_t*>(kv16), ldkv};
+  ns2::ProfScope prof_("head_norm_f16kv");
+  hipStream_t s = ns2::stream();
+  if (D == 64) splitk_head_norm_kernel<64><<<M, 64, 0, s>>>(q, splits, hn);
+  else if (D == 128) splitk_head_norm_kernel<128><<<M, 128, 0, s>>>(q, splits, hn);
+  else splitk_head_norm_kernel<256><<<M, 256, 0, s>>>(q, splits, hn);
+  NS2_LAUNCHED("head_norm_f16kv");
+  return NS2_OK;
+}
+
+int ns2_linear_f16w_tiled_glu_down(const uint16_t* At, const uint16_t* Wt, const float* bias, int M, int N, int K,
+                                   int act, const uint16_t* wd_tiled, int Nd, float* part) {
+  NS2_READY();
+  if (M == 0) return NS2_OK;
+  const char* fn = "ns2_linear_f16w_tiled_glu_down";
+  NS2_REQUIRE(wd_tiled && part, "%s: null wd_tiled or part", fn);
+  NS2_REQUIRE(N % (2 * kGluDownGroup) == 0 && Nd > 0 && Nd % 64 == 0,
+              "%s: N=%d must be a multiple of %d (%d-column GLU groups) and Nd=%d of 64", fn, N, 2 * kGluDownGroup,
+              kGluDownGroup, Nd);
+  NS2_REQUIRE(act >= NS2_ACT_NONE && act <= NS2_ACT_GELU_TANH, "%s: unknown act %d", fn, act);
+  NS2_REQUIRE(aligned16(wd_tiled), "%s: wd_tiled must be 16-byte aligned", fn);
+  float* gu = nullptr;
+  int splits = 1;
+  int rc = ns2::linear_f16w_tiled_raw(fn, At, Wt, M, N, K, &gu, &splits);
+  if (rc) return rc;
+  GemmArgs q{nullptr, nullptr, nullptr, bias, nullptr, part, nullptr, 0, 0, 0, N, M, N, K, 1.0f, NS2_ACT_NONE, 0};
+  q.part = gu;
+  const GluDown gd{reinterpret_cast<const half_t*>(wd_tiled), part, Nd, act};
+  ns2::ProfScope prof_("glu_down");
+  splitk_glu_down_kernel<kGluDownGroup>
+      <<<dim3((M + 15) / 16, N / 2 / kGluDownGroup), 512, 0, ns2::stream()>>>(q, splits, gd);
+  NS2_LAUNCHED("glu_down");
+  return NS2_OK;
 }
 
 int ns2_linear_bf16_lora(const float* A, int lda, const uint16_t* W, const float* bias,

@@ -631,7 +631,7 @@ __global__ __launch_bounds__(256) void tile_w16_kernel(const uint16_t* __restric
 constexpr long long kBandBytes = 2ll << 20;
 
 template <int BM, int BN, int WM, int WN, int STAGES = 2, int EPI = 0, bool WF16 = false>
-int launch_tiled(TGemmArgs p, int splits = 1) {
+int launch_tiled(TGemmArgs p, int splits = 1, bool reduce = true) {
   p.tiles_m = (p.M + BM - 1) / BM;
   p.tiles_n = (p.N + BN - 1) / BN;
   // column bands (1, 2, 4 or 8) by an estimate of the bytes the XCDs' L2s miss: with b bands
@@ -685,7 +685,7 @@ int launch_tiled(TGemmArgs p, int splits = 1) {
   }
 #undef NS2_TILED
   NS2_LAUNCHED("gemm_tiled");
-  if (p.part) {
+  if (p.part && reduce) {
     const long long mn = (long long)p.M * p.N;
     if (p.lr) {
       const long long tiles32 = (long long)((p.M + 31) / 32) * (p.N / 32);
@@ -819,6 +819,30 @@ int linear_tiled(const char* fn, bool wf16, const uint16_t* At, const void* Wt, 
 }
 
 }  // namespace
+
+int ns2::linear_f16w_tiled_raw(const char* fn, const uint16_t* At, const uint16_t* Wt, int M, int N, int K,
+                               float** part, int* splits) {
+  NS2_REQUIRE(At && Wt && M > 0 && N > 0 && N % 64 == 0 && K > 0 && K % 64 == 0 && aligned16(At) && aligned16(Wt),
+              "%s: At, Wt, M=%d, N=%d (N %% 64 == 0), K=%d (K %% 64 == 0) or alignment", fn, M, N, K);
+  TGemmArgs p{reinterpret_cast<const half_t*>(At), reinterpret_cast<const uint8_t*>(Wt), nullptr, nullptr, nullptr,
+              nullptr, nullptr, 0, 0, M, N, K, N, (M + 63) / 64, N / 64, 0, 0, 1.0f, NS2_ACT_NONE, 0};
+  // 64x64 tiles (the few-row launches this serves); K split until about one block per CU, at
+  // least 4 k-tiles per split
+  const long long tiles = (long long)((M + 63) / 64) * (N / 64);
+  const int kt = K / 64;
+  int s = (int)(kCUs / tiles);
+  if (s > kt / 4) s = kt / 4;
+  if (s > 8) s = 8;
+  if (s < 1) s = 1;
+  p.ksplit = (kt + s - 1) / s;
+  s = (kt + p.ksplit - 1) / p.ksplit;
+  p.part = static_cast<float*>(ns2::workspace(5, (size_t)s * M * N * sizeof(float)));
+  if (!p.part) return ns2::set_error(NS2_ERR_OOM, "%s: split-K workspace allocation failed", fn);
+  *part = p.part;
+  *splits = s;
+  ns2::ProfScope prof_("gemm_f16_tiled");
+  return launch_tiled<64, 64, 2, 2, 3, 0, true>(p, s, false);
+}
 
 extern "C" {
 

@@ -52,10 +52,10 @@ export class Gemma3 {
     m.layers = [];
     for (let i = 0; i < RUN; i++) {
       const l = await loadLayer(gpu, st, i);
-      // o_proj and down re-tiled as fp16 (next to their row-major copies) for the fused
-      // projections of the attention and of the GLU
-      if (ops.tileablePlain(l.o)) ops.tileWeight(gpu, l.o);
-      if (ops.tileablePlain(l.down)) ops.tileWeight(gpu, l.down);
+      // every linear re-tiled as fp16 (next to its row-major copy): q/k/v and gate/up take the
+      // tiled operands the row kernels write, o_proj and down the fused projections of the
+      // attention and of the GLU
+      for (const W of [l.qkv, l.o, l.gateUp, l.down]) if (ops.tileablePlain(W)) ops.tileWeight(gpu, W);
       m.layers.push(l);
       if (onProgress) onProgress((i + 1) / RUN);
     }
@@ -97,16 +97,39 @@ export class Gemma3 {
     const Lt = x.shape[0];
     const qkvW = (H + 2 * KH) * HD;
     const [csLocal, csGlobal] = this.ropeTables(Lt);
+    const noLora = (W) => !(W.lora && W.lora.length);
+    // a linear whose input the previous row kernel can write as the tiled fp16 operand takes
+    // the tiled path (a LoRA on it keeps the row-major path and its fp32 input)
+    const tiled = ops.tiledPathOk;
+    const mlpFused = (l) => Number.isInteger(l.gateUp.N / (2 * ops.GLU_DOWN_GROUP)) && l.down.tbuf && noLora(l.down) &&
+      l.gateUp.kind === "bf16" && noLora(l.gateUp);
+    // the layer input: fp32 h, or hT as the tiled operand of its q/k/v projection
     let h = ops.rmsnorm(gpu, x, this.layers[0].inNorm, D);
+    let hT = null;
+    if (tiled(this.layers[0].qkv)) {
+      hT = ops.toTiled(gpu, h);
+      h.release();
+      h = null;
+    }
     this.layers.forEach((l, i) => {
       const cs = l.global ? csGlobal : csLocal;
       // [Lt, q 1024 | k 256 | v 256], the q heads and then the k head normed and rotated in the
-      // projection's split-K sum
-      // (on the fused path the k and v heads are stored as fp16, the attention's operand type)
-      const qkv = ops.linearHeadNorm(gpu, h, l.qkv, l.qn, H, l.kn, KH, { D: HD, cs, f16kv: true });
-      h.release();
-      let h2;
-      if (qkv.f16kv && l.o.tbuf && !(l.o.lora && l.o.lora.length)) {
+      // projection's split-K sum (on the fused paths the k and v heads are stored as fp16, the
+      // attention's operand type)
+      let qkv;
+      if (hT) {
+        qkv = ops.linearHeadNormTiled(gpu, hT, l.qkv, l.qn, H, l.kn, KH, { D: HD, cs });
+        hT.release();
+        hT = null;
+      } else {
+        qkv = ops.linearHeadNorm(gpu, h, l.qkv, l.qn, H, l.kn, KH, { D: HD, cs, f16kv: true });
+        h.release();
+        h = null;
+      }
+      const mlpTiled = mlpFused(l) && tiled(l.gateUp);
+      let h2 = null;
+      let h2T = null;
+      if (qkv.f16kv && l.o.tbuf && noLora(l.o)) {
         // the attention and o_proj in one launch (each head's share of the projection), the
         // shares summed by the post-norm's row kernel
         const part = ops.attentionRowsF16kvOproj(gpu, {
@@ -114,7 +137,8 @@ export class Gemma3 {
           vOff: qkv.f16kv.off + KH * HD, ldkv: qkv.f16kv.ld, group: H / KH, causal: true, W: l.o,
         });
         qkv.release();
-        h2 = ops.partsAddRmsnorm(gpu, part, H, l.o.bias, x, l.postAttnNorm, l.preMlpNorm);
+        if (mlpTiled) h2T = ops.partsAddRmsnormTiled(gpu, part, H, l.o.bias, x, l.postAttnNorm, l.preMlpNorm);
+        else h2 = ops.partsAddRmsnorm(gpu, part, H, l.o.bias, x, l.postAttnNorm, l.preMlpNorm);
         part.release();
       } else {
         const a = qkv.f16kv
@@ -129,22 +153,37 @@ export class Gemma3 {
         qkv.release();
         h2 = ops.linearAddRmsnorm(gpu, a, l.o, x, l.postAttnNorm, l.preMlpNorm);
         a.release();
+        if (mlpTiled) {
+          h2T = ops.toTiled(gpu, h2);
+          h2.release();
+          h2 = null;
+        }
       }
-      const next = i + 1 < this.layers.length ? this.layers[i + 1].inNorm : this.norm;
-      const noLora = (W) => !(W.lora && W.lora.length);
-      const shares = l.gateUp.N / (2 * ops.GLU_DOWN_GROUP);
-      if (l.gateUp.kind === "bf16" && noLora(l.gateUp) && Number.isInteger(shares) && l.down.tbuf && noLora(l.down)) {
+      const last = i + 1 === this.layers.length;
+      const next = last ? this.norm : this.layers[i + 1].inNorm;
+      // the next layer's q/k/v input as its tiled operand, or fp32 (and the final norm's output)
+      const nextTiled = !last && tiled(this.layers[i + 1].qkv);
+      if (mlpFused(l)) {
         // the GLU's row kernel writes the down projection's shares per column group, summed by
         // the post-norm's row kernel
-        const part = ops.linearGluDown(gpu, h2, l.gateUp, l.down, "gelu_tanh");
-        h2.release();
-        h = ops.partsAddRmsnorm(gpu, part, shares, l.down.bias, x, l.postMlpNorm, next);
+        const shares = l.gateUp.N / (2 * ops.GLU_DOWN_GROUP);
+        const part = h2T ? ops.linearGluDownTiled(gpu, h2T, l.gateUp, l.down, "gelu_tanh")
+          : ops.linearGluDown(gpu, h2, l.gateUp, l.down, "gelu_tanh");
+        if (h2T) h2T.release();
+        if (h2) h2.release();
+        if (nextTiled) hT = ops.partsAddRmsnormTiled(gpu, part, shares, l.down.bias, x, l.postMlpNorm, next);
+        else h = ops.partsAddRmsnorm(gpu, part, shares, l.down.bias, x, l.postMlpNorm, next);
         part.release();
       } else {
         const g = ops.linearGlu(gpu, h2, l.gateUp, "gelu_tanh");
         h2.release();
         h = ops.linearAddRmsnorm(gpu, g, l.down, x, l.postMlpNorm, next);
         g.release();
+        if (nextTiled) {
+          hT = ops.toTiled(gpu, h);
+          h.release();
+          h = null;
+        }
       }
     });
     x.release();

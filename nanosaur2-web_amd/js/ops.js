@@ -302,6 +302,43 @@ export function linearGluDown(gpu, a, W, Wd, act = "gelu_tanh") {
   return part;
 }
 
+// Whether a bf16 weight takes the encoder's tiled fp16 path (re-tiled, no LoRA attached).
+export const tiledPathOk = (W) => W.kind === "bf16" && !!W.tbuf && !(W.lora && W.lora.length);
+
+// linearHeadNorm with f16kv on a tiled fp16 operand (aT, rows aT.rows) over W.tbuf: the same
+// result and .f16kv layout.
+export function linearHeadNormTiled(gpu, aT, W, w1, H1, w2, H2, { D, cs = null, eps = 1e-6 }) {
+  const M = aT.rows;
+  const y = gpu.empty([M, W.N]);
+  const kv16 = addr(y) + BigInt(H1 * D * 4);
+  gpu.run("te.qkv+head_norm", 2 * M * W.N * W.K, () =>
+    native.linearF16wTiledHeadNormF16kv(addr(aT), addr(W.tbuf), addr(W.bias || null), addr(y), M, W.N, W.K,
+      addr(w1), H1, addr(w2), H2, D, cs ? addr(cs) : null, cs ? cs.sinOff : 0, cs ? M : 0, eps, kv16, 2 * W.N));
+  y.f16kv = { off: 2 * H1 * D, ld: 2 * W.N };
+  return y;
+}
+
+// linearGluDown on a tiled fp16 operand (aT, rows aT.rows) with W.tbuf: the same shares.
+export function linearGluDownTiled(gpu, aT, W, Wd, act = "gelu_tanh") {
+  if (!Wd.tbuf || Wd.kind !== "bf16" || Wd.K !== W.N / 2) throw new Error(`${Wd.name}: the fused down projection needs a re-tiled bf16 weight of K = N/2`);
+  const M = aT.rows;
+  const part = gpu.empty([W.N / (2 * GLU_DOWN_GROUP), M, Wd.N]);
+  gpu.run("te.mlp+glu+down", 2 * M * W.N * W.K + 2 * M * Wd.N * Wd.K, () =>
+    native.linearF16wTiledGluDown(addr(aT), addr(W.tbuf), addr(W.bias || null), M, W.N, W.K, ACT[act],
+      addr(Wd.tbuf), Wd.N, addr(part)));
+  return part;
+}
+
+// partsAddRmsnorm with y written as the tiled fp16 operand of the next linear (returned).
+export function partsAddRmsnormTiled(gpu, part, splits, bias, x, wAdd, wOut, eps = 1e-6) {
+  const N = x.shape[x.shape.length - 1], M = x.size / N;
+  const yt = rotatedOperand(gpu, M, N, true);
+  gpu.run("te.proj_norm", 0, () =>
+    native.partsAddRmsnormTiled(addr(part), splits, addr(bias || null), addr(x), addr(wAdd), addr(wOut), addr(yt), M,
+      N, eps));
+  return yt;
+}
+
 // addRmsnorm on a product given as `splits` shares [splits, M, N] (+ bias): x += rmsnorm(sum) *
 // wAdd, then y = rmsnorm(x) * wOut when wOut is given (returned).
 export function partsAddRmsnorm(gpu, part, splits, bias, x, wAdd, wOut, eps = 1e-6) {

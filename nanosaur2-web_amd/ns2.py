@@ -96,6 +96,10 @@ SIGNATURES = {
     "ns2_attention_rows_f16kv_oproj": [c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_int, c_int,
                                        c_int, c_ll, c_ll, c_ll, c_int, c_int, c_int],
     "ns2_parts_add_rmsnorm": [c_vp, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_float],
+    "ns2_parts_add_rmsnorm_tiled": [c_vp, c_int, c_vp, c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_float],
+    "ns2_linear_f16w_tiled_head_norm_f16kv": [c_vp, c_vp, c_vp, c_vp, c_int, c_int, c_int, c_vp, c_int, c_vp, c_int,
+                                              c_int, c_vp, c_ll, c_int, c_float, c_vp, c_int],
+    "ns2_linear_f16w_tiled_glu_down": [c_vp, c_vp, c_vp, c_int, c_int, c_int, c_int, c_vp, c_int, c_vp],
     "ns2_head_norm": [c_vp, c_vp, c_int, c_int, c_int, c_int, c_ll, c_ll, c_vp, c_ll, c_float],
     "ns2_head_norm2": [c_vp, c_vp, c_int, c_vp, c_int, c_int, c_int, c_int, c_ll, c_ll, c_vp, c_ll, c_float],
     "ns2_norm_mod": [c_vp, c_vp, c_ll, c_ll, c_int, c_int, c_vp, c_float, c_vp],
@@ -335,6 +339,19 @@ class Lib:
         """attention_rows_f16kv with each head's share of the output projection into part [H, Lq, N]."""
         self.call("ns2_attention_rows_f16kv_oproj", _ptr(q), _ptr(k), _ptr(v), _ptr(wo_tiled), _ptr(part), Lq, Lk,
                   H, D, ldq, ldk, ldv, qOff, kOff, vOff, group, int(causal), N)
+
+    def parts_add_rmsnorm_tiled(self, part, splits, bias, x, w_add, w_out, yt, M, N, eps=1e-6):
+        self.call("ns2_parts_add_rmsnorm_tiled", _ptr(part), splits, _ptr(bias), _ptr(x), _ptr(w_add), _ptr(w_out),
+                  _ptr(yt), M, N, eps)
+
+    def linear_f16w_tiled_head_norm_f16kv(self, At, Wt, bias, C, M, N, K, w1, H1, w2, H2, D, kv16, ldkv, cs=None,
+                                          sin_off=0, rope_rows=0, eps=1e-6):
+        self.call("ns2_linear_f16w_tiled_head_norm_f16kv", _ptr(At), _ptr(Wt), _ptr(bias), _ptr(C), M, N, K,
+                  _ptr(w1), H1, _ptr(w2), H2, D, _ptr(cs), sin_off, rope_rows, eps, _ptr(kv16), ldkv)
+
+    def linear_f16w_tiled_glu_down(self, At, Wt, bias, M, N, K, wd_tiled, Nd, part, act="gelu_tanh"):
+        self.call("ns2_linear_f16w_tiled_glu_down", _ptr(At), _ptr(Wt), _ptr(bias), M, N, K, ACT[act],
+                  _ptr(wd_tiled), Nd, _ptr(part))
 
     def parts_add_rmsnorm(self, part, splits, bias, x, w_add, w_out, y, M, N, eps=1e-6):
         self.call("ns2_parts_add_rmsnorm", _ptr(part), splits, _ptr(bias), _ptr(x), _ptr(w_add), _ptr(w_out),

@@ -1041,6 +1041,110 @@ def test_linear_bf16_glu_down(ns2lib, M, bias, Nd):
     assert_close(got, ref, TOL, f"GLU + down vs the oracle (M={M}, Nd={Nd})")
 
 
+def to_tiled_dev(ns2lib, a):
+    """fp32 [M, K] -> the tiled fp16 operand through ns2_to_tiled_f16 (padding rows zero)."""
+    M, K = a.shape
+    at = tiled_operand(M, K)
+    ns2lib.call("ns2_to_tiled_f16", a.data_ptr(), K, None, K, at.data_ptr(), M, K)
+    return at
+
+
+@pytest.mark.parametrize("M,bias", [(256, False), (37, True), (1, False)])
+def test_linear_f16w_tiled_head_norm_f16kv(ns2lib, M, bias):
+    """The Gemma3 q/k/v projection on the tiled fp16 path (tiled operand, fp16 weight tiles, raw
+    split-K products into the head-norm row kernel) against the row-major
+    ns2_linear_bf16_head_norm_f16kv: the same fp16 roundings of input and weight, the K sums in
+    another association (q heads within 5e-5; the fp16 k/v within one rounding step), and
+    against the oracle (TOL)."""
+    N, K, D = 1536, 640, 256
+    g = gen(M * 11 + bias)
+    a = torch.randn(M, K, generator=g)
+    w = (torch.randn(N, K, generator=g) * 0.05).to(torch.bfloat16)
+    b = torch.randn(N, generator=g) * 0.1 if bias else None
+    wq = (torch.randn(D, generator=g) * 0.3 + 1).to(dev)
+    wk = (torch.randn(D, generator=g) * 0.3 + 1).to(dev)
+    ang = torch.arange(M, dtype=torch.float64)[:, None] * torch.rand(D // 2, generator=g, dtype=torch.float64)[None]
+    cs = torch.cat([ang.cos().flatten(), ang.sin().flatten()]).float()
+    csd, sin_off = cs.to(dev), M * D // 2
+    ad, wd, bd = a.to(dev), w.view(torch.int16).to(dev), (b.to(dev) if bias else None)
+    wt = torch.empty(N * K, dtype=torch.int16, device=dev)
+    ns2lib.tile_bf16_weight(wd, wt, N, K)
+    at = to_tiled_dev(ns2lib, ad)
+    y1 = torch.empty(M, N, device=dev)
+    ns2lib.linear_bf16_head_norm_f16kv(ad, K, wd, bd, y1, M, N, K, wq, 4, wk, 1, D, y1.data_ptr() + 4 * D * 4, 2 * N,
+                                       cs=csd, sin_off=sin_off, rope_rows=M)
+    y2 = torch.empty(M, N, device=dev)
+    ns2lib.linear_f16w_tiled_head_norm_f16kv(at, wt, bd, y2, M, N, K, wq, 4, wk, 1, D, y2.data_ptr() + 4 * D * 4,
+                                             2 * N, cs=csd, sin_off=sin_off, rope_rows=M)
+    torch.cuda.synchronize()
+    y1, y2 = y1.cpu(), y2.cpu()
+    q1, q2 = y1[:, :4 * D].double(), y2[:, :4 * D].double()
+    kv1 = y1.view(torch.float16)[:, 8 * D:10 * D].double()
+    kv2 = y2.view(torch.float16)[:, 8 * D:10 * D].double()
+    # (the row-major path's fp32 GEMV at M <= 8 does not round its input to fp16)
+    assert_close(q2, q1, 5e-5 if M > 8 else TOL, f"tiled vs row-major q heads (M={M})")
+    assert_close(kv2, kv1, 2e-3, f"tiled vs row-major fp16 k/v (M={M})")
+    ref = O.linear_bf16(a.double(), w, bias=b.double() if bias else None)
+    O.head_norm_rope(ref, wq.double().cpu(), M, 4, D, N, colOff=0, cs=cs, sinOff=sin_off)
+    O.head_norm_rope(ref, wk.double().cpu(), M, 1, D, N, colOff=4 * D, cs=cs, sinOff=sin_off)
+    assert_close(q2, ref[:, :4 * D], TOL, f"tiled q heads vs the oracle (M={M})")
+    assert_close(kv2, ref[:, 4 * D:], TOL, f"tiled fp16 k/v vs the oracle (M={M})")
+
+
+@pytest.mark.parametrize("M,bias", [(256, False), (37, True), (1, True)])
+def test_linear_f16w_tiled_glu_down(ns2lib, M, bias):
+    """The Gemma3 gate/up, GLU and down shares on the tiled fp16 path against the row-major
+    ns2_linear_bf16_glu_down (5e-4: the K sums in another association, then the GLU output's
+    fp16 rounding) and the oracle (TOL)."""
+    N, K, I, Nd = 4096, 640, 2048, 640
+    g = gen(M * 17 + bias)
+    a = torch.randn(M, K, generator=g)
+    w = (torch.randn(N, K, generator=g) * 0.05).to(torch.bfloat16)
+    b = torch.randn(N, generator=g) * 0.1 if bias else None
+    wdn = (torch.randn(Nd, I, generator=g) * 0.03).to(torch.bfloat16)
+    ad, wd, bd = a.to(dev), w.view(torch.int16).to(dev), (b.to(dev) if bias else None)
+    wt = torch.empty(N * K, dtype=torch.int16, device=dev)
+    ns2lib.tile_bf16_weight(wd, wt, N, K)
+    wdd = wdn.view(torch.int16).to(dev)
+    wdt = torch.empty(Nd * I, dtype=torch.int16, device=dev)
+    ns2lib.tile_bf16_weight(wdd, wdt, Nd, I)
+    at = to_tiled_dev(ns2lib, ad)
+    p1 = torch.empty(I // 128, M, Nd, device=dev)
+    ns2lib.linear_bf16_glu_down(ad, K, wd, bd, M, N, K, wdt, Nd, p1, "gelu_tanh")
+    p2 = torch.full((I // 128, M, Nd), float("nan"), device=dev)
+    ns2lib.linear_f16w_tiled_glu_down(at, wt, bd, M, N, K, wdt, Nd, p2, "gelu_tanh")
+    torch.cuda.synchronize()
+    s1, s2 = p1.cpu().double().sum(0), p2.cpu().double().sum(0)
+    assert torch.isfinite(s2).all(), "every share written"
+    # the GLU output is rounded to fp16 before the down product: where the two gate/up K sums
+    # differ in their last bits a value can round the other way (one fp16 step, 2^-11)
+    assert_close(s2, s1, 5e-4 if M > 8 else TOL, f"tiled vs row-major GLU + down (M={M})")
+    tr = O.linear_bf16(a.double(), w, bias=b.double() if bias else None)
+    ref = (torch.nn.functional.gelu(tr[:, :I], approximate="tanh") * tr[:, I:]) @ wdn.double().t()
+    assert_close(s2, ref, TOL, f"tiled GLU + down vs the oracle (M={M})")
+
+
+@pytest.mark.parametrize("M,splits", [(256, 16), (37, 4), (1, 1)])
+def test_parts_add_rmsnorm_tiled(ns2lib, M, splits):
+    """ns2_parts_add_rmsnorm_tiled: x as ns2_parts_add_rmsnorm updates it (bit-exact) and y as
+    its fp32 y rounded once to fp16 in the tiled operand layout (bit-exact)."""
+    N = 640
+    g = gen(M * 19 + splits)
+    part = torch.randn(splits, M, N, generator=g).to(dev)
+    x = torch.randn(M, N, generator=g) * 20
+    wa = (torch.randn(N, generator=g) * 0.3 + 1).to(dev)
+    wo = (torch.randn(N, generator=g) * 0.3 + 1).to(dev)
+    x1, x2 = x.to(dev), x.to(dev)
+    y1 = torch.empty(M, N, device=dev)
+    ns2lib.parts_add_rmsnorm(part, splits, None, x1, wa, wo, y1, M, N)
+    yt = tiled_operand(M, N)
+    ns2lib.parts_add_rmsnorm_tiled(part, splits, None, x2, wa, wo, yt, M, N)
+    torch.cuda.synchronize()
+    assert torch.equal(x1.cpu(), x2.cpu()), "x"
+    got = untile_a(yt.cpu(), M, N).view(torch.float16)
+    assert torch.equal(got.view(torch.int16), y1.cpu().half().view(torch.int16)), "tiled fp16 y"
+
+
 @pytest.mark.parametrize("M,bias,rope", [(256, False, True), (37, True, True), (5, False, False)])
 def test_linear_bf16_head_norm(ns2lib, M, bias, rope):
     """Gemma3's q/k/v projection with the q and k head norms (and RoPE) in its split-K sum
