@@ -160,16 +160,6 @@ __global__ __launch_bounds__(512) void rot_rows_kernel(RotRowsArgs a) {
   constexpr int cols = 256 * G;
   constexpr int NV = NORM ? 3 : 1;
   __shared__ __attribute__((aligned(16))) float4 mods[NV][NORM ? G * 64 : 1];  // [1 + scale, shift, w]
-  if (NORM) {
-    for (int i = threadIdx.x; i < G * 64; i += 512) {
-      const int c = (i / 64) * 256 + 16 * (i % 16) + 4 * ((i % 64) / 16);
-      const float4 sc = *reinterpret_cast<const float4*>(a.mod + a.scaleOff + c);
-      mods[0][i] = make_float4(1.0f + sc.x, 1.0f + sc.y, 1.0f + sc.z, 1.0f + sc.w);
-      mods[1][i] = *reinterpret_cast<const float4*>(a.mod + a.shiftOff + c);
-      if (a.w) mods[NV - 1][i] = *reinterpret_cast<const float4*>(a.w + c);
-    }
-    __syncthreads();
-  }
   // Tiled output goes through LDS (fp16, rows padded by 32 bytes: the 16 units of a quarter-wave
   // write-out read, 2 chunks x 8 rows, fall in 16 different bank groups), at most 16 groups
   // (66 KB), so every 128-byte line of the tiled layout is written whole (direct stores of
@@ -179,9 +169,10 @@ __global__ __launch_bounds__(512) void rot_rows_kernel(RotRowsArgs a) {
   constexpr int TROW = 256 * GB + 16;
   __shared__ __attribute__((aligned(16))) uint16_t tout[8 * TROW];
   const bool active = row < a.rows;
-  if (!active && !a.tiled) return;
   // lane l holds elements 16(l%16) + 4(l/16) .. +3 of every group: the layout of the
-  // matrix-core FWHT (its float4 loads still cover each group's 1 KB once per wave)
+  // matrix-core FWHT (its float4 loads still cover each group's 1 KB once per wave). The row's
+  // loads are issued first, so that they are in flight while the block stages the modulation
+  // (a barrier waits for LDS operations only; a wave past the last row loads the last row).
   const int lane = threadIdx.x & 63;
   const int lo = fwht_mfma_offset();
   const float* src = a.x + (long long)(active ? row : a.rows - 1) * a.ldx + part * GB * 256 + lo;
@@ -191,6 +182,20 @@ __global__ __launch_bounds__(512) void rot_rows_kernel(RotRowsArgs a) {
     const float4 in = *reinterpret_cast<const float4*>(src + g * 256);
     v[g][0] = in.x, v[g][1] = in.y, v[g][2] = in.z, v[g][3] = in.w;
   }
+  if (NORM) {
+    for (int i = threadIdx.x; i < G * 64; i += 512) {
+      const int c = (i / 64) * 256 + 16 * (i % 16) + 4 * ((i % 64) / 16);
+      // the three loads go out together (one wait for all)
+      const float4 sc = *reinterpret_cast<const float4*>(a.mod + a.scaleOff + c);
+      const float4 sh = *reinterpret_cast<const float4*>(a.mod + a.shiftOff + c);
+      const float4 ww = a.w ? *reinterpret_cast<const float4*>(a.w + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+      mods[0][i] = make_float4(1.0f + sc.x, 1.0f + sc.y, 1.0f + sc.z, 1.0f + sc.w);
+      mods[1][i] = sh;
+      if (a.w) mods[NV - 1][i] = ww;
+    }
+    __syncthreads();
+  }
+  if (!active && !a.tiled) return;
   float r = 1.f;
   if (NORM) {
     float mean = 0.f;
