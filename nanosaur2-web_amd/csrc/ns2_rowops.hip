@@ -137,7 +137,7 @@ struct RotRowsArgs {
   int ldy, rows, tiled;
 };
 
-// [rows, 256 G] fp32 -> (normMod ->) rotated fp16, one wave per row and 8 rows per block
+// [rows, 256 G] fp32 -> (normMod ->) rotated fp16, 8 rows per block
 // (ROT false: the fp16 operand of a plain fp16-weight linear, not rotated).
 // Each lane loads its 4 values of every group before any arithmetic (the whole row is in
 // flight at once), the row statistics are wave reductions, and the 8 rows of a block fill
@@ -146,17 +146,31 @@ struct RotRowsArgs {
 // normMod: the block stages the modulation vectors (1 + scale, shift and the norm weight, if
 // any) in LDS once, in lane order (slot 64g + l holds the 4 columns lane l uses in group g, so
 // the waves' 16-byte reads are conflict-free), instead of every row's wave loading them from
-// L1: at 8 rows per block that is 3x the row's own bytes through L1 otherwise.
+// L1: at 8 rows per block that is 3x the row's own bytes through L1 otherwise. Rows of an even
+// number of groups from 4 on take two waves each (16 waves per block), each wave half of the
+// row's groups, the two halves' sums added through LDS: twice the waves in flight and half the
+// per-wave chain of rotations.
+template <int G, bool NORM>
+constexpr bool rot_two_waves() { return NORM && G >= 4 && G % 2 == 0; }
+template <int G, bool NORM>
+constexpr int rot_threads() { return rot_two_waves<G, NORM>() ? 1024 : 512; }
+
 template <int G, bool NORM, bool ROT = true>
-__global__ __launch_bounds__(512) void rot_rows_kernel(RotRowsArgs a) {
+__global__ __launch_bounds__((rot_threads<G, NORM>())) void rot_rows_kernel(RotRowsArgs a) {
+  constexpr bool WS = rot_two_waves<G, NORM>();
+  constexpr int WPR = WS ? 2 : 1;  // waves per row
   // rotation only, rows of an even number of groups from 6 on: each block takes half of its 8
   // rows' groups (the two halves rotate independently), so the grid has twice the blocks and
   // each block stages its whole part in LDS (2432 x 1536: 5.2 -> 4.7 us)
-  constexpr int GB = (!NORM && G >= 6 && G % 2 == 0) ? G / 2 : G;
-  constexpr int PARTS = G / GB;
-  static_assert(G % GB == 0 && GB <= 16, "groups per block");
+  constexpr int PARTS = (!NORM && G >= 6 && G % 2 == 0) ? 2 : 1;  // column parts per block
+  constexpr int GBLK = G / PARTS;                                  // groups of a row per block
+  constexpr int GB = GBLK / WPR;                                   // groups per wave
+  static_assert(G % (PARTS * WPR) == 0 && GBLK <= 16, "groups per block");
   const int part = PARTS > 1 ? blockIdx.x % PARTS : 0;
-  const int row = (blockIdx.x / PARTS) * 8 + (threadIdx.x >> 6);
+  const int wave = threadIdx.x >> 6, rl = wave / WPR;
+  const int half = WS ? wave % WPR : 0;  // this wave's half of the block's groups
+  const int row = (blockIdx.x / PARTS) * 8 + rl;
+  const int gb0 = half * GB;             // the wave's first group within the block's part
   constexpr int cols = 256 * G;
   constexpr int NV = NORM ? 3 : 1;
   __shared__ __attribute__((aligned(16))) float4 mods[NV][NORM ? G * 64 : 1];  // [1 + scale, shift, w]
@@ -164,9 +178,9 @@ __global__ __launch_bounds__(512) void rot_rows_kernel(RotRowsArgs a) {
   // write-out read, 2 chunks x 8 rows, fall in 16 different bank groups), at most 16 groups
   // (66 KB), so every 128-byte line of the tiled layout is written whole (direct stores of
   // 6144-column rows wrote each line in 8 pieces: 26.4 us at 2432 rows, 15.1 us staged in two
-  // column parts). A wave past the last row still takes part in the block's barrier: it works on the
-  // last row, and its result is not written.
-  constexpr int TROW = 256 * GB + 16;
+  // column parts). A wave past the last row still takes part in the block's barriers: it works
+  // on the last row, and its result is not written.
+  constexpr int TROW = 256 * GBLK + 16;
   __shared__ __attribute__((aligned(16))) uint16_t tout[8 * TROW];
   const bool active = row < a.rows;
   // lane l holds elements 16(l%16) + 4(l/16) .. +3 of every group: the layout of the
@@ -175,7 +189,7 @@ __global__ __launch_bounds__(512) void rot_rows_kernel(RotRowsArgs a) {
   // (a barrier waits for LDS operations only; a wave past the last row loads the last row).
   const int lane = threadIdx.x & 63;
   const int lo = fwht_mfma_offset();
-  const float* src = a.x + (long long)(active ? row : a.rows - 1) * a.ldx + part * GB * 256 + lo;
+  const float* src = a.x + (long long)(active ? row : a.rows - 1) * a.ldx + (part * GBLK + gb0) * 256 + lo;
   float v[GB][4];
 #pragma unroll
   for (int g = 0; g < GB; ++g) {
@@ -183,7 +197,7 @@ __global__ __launch_bounds__(512) void rot_rows_kernel(RotRowsArgs a) {
     v[g][0] = in.x, v[g][1] = in.y, v[g][2] = in.z, v[g][3] = in.w;
   }
   if (NORM) {
-    for (int i = threadIdx.x; i < G * 64; i += 512) {
+    for (int i = threadIdx.x; i < G * 64; i += rot_threads<G, NORM>()) {
       const int c = (i / 64) * 256 + 16 * (i % 16) + 4 * ((i % 64) / 16);
       // the three loads go out together (one wait for all)
       const float4 sc = *reinterpret_cast<const float4*>(a.mod + a.scaleOff + c);
@@ -195,15 +209,25 @@ __global__ __launch_bounds__(512) void rot_rows_kernel(RotRowsArgs a) {
     }
     __syncthreads();
   }
-  if (!active && !a.tiled) return;
+  // with two waves per row every wave reaches the barriers below
+  if (!WS && !active && !a.tiled) return;
   float r = 1.f;
   if (NORM) {
+    // the two halves' sums of a row meet in LDS (separate slots for the two sums, so no
+    // barrier is needed between reading the first and writing the second)
+    __shared__ float red[2][8][WPR];
     float mean = 0.f;
     if (!a.w) {
       float s = 0.f;
 #pragma unroll
       for (int g = 0; g < GB; ++g) s += (v[g][0] + v[g][1]) + (v[g][2] + v[g][3]);
-      mean = wave_sum(s) / (float)cols;
+      s = wave_sum(s);
+      if (WS) {
+        if (lane == 0) red[0][rl][half] = s;
+        __syncthreads();
+        s = red[0][rl][0] + red[0][rl][WPR - 1];
+      }
+      mean = s / (float)cols;
     }
     float ss = 0.f;
 #pragma unroll
@@ -213,17 +237,24 @@ __global__ __launch_bounds__(512) void rot_rows_kernel(RotRowsArgs a) {
         v[g][j] -= mean;
         ss += v[g][j] * v[g][j];
       }
-    r = rsqrtf(wave_sum(ss) / (float)cols + a.eps);
+    ss = wave_sum(ss);
+    if (WS) {
+      if (lane == 0) red[1][rl][half] = ss;
+      __syncthreads();
+      ss = red[1][rl][0] + red[1][rl][WPR - 1];
+    }
+    r = rsqrtf(ss / (float)cols + a.eps);
   }
   const half4v_t h = fwht_h16_fragment();
 #pragma unroll
   for (int g = 0; g < GB; ++g) {
+    const int gg = part * GBLK + gb0 + g;  // group of the row
     if (NORM) {
       // modulation of each element: y = ((v * r) * w) * (1 + scale) + shift, the reference's
       // order (kernels.js:82-117)
-      const float4 s1 = mods[0][g * 64 + lane], sh = mods[1][g * 64 + lane];
+      const float4 s1 = mods[0][gg * 64 + lane], sh = mods[1][gg * 64 + lane];
       if (a.w) {
-        const float4 ww = mods[NV - 1][g * 64 + lane];
+        const float4 ww = mods[NV - 1][gg * 64 + lane];
         v[g][0] = v[g][0] * r * ww.x * s1.x + sh.x, v[g][1] = v[g][1] * r * ww.y * s1.y + sh.y;
         v[g][2] = v[g][2] * r * ww.z * s1.z + sh.z, v[g][3] = v[g][3] * r * ww.w * s1.w + sh.w;
       } else {
@@ -233,20 +264,20 @@ __global__ __launch_bounds__(512) void rot_rows_kernel(RotRowsArgs a) {
     }
     if (ROT) fwht256_mfma(v[g], h);
     if (!a.tiled) {
-      if (active) store4_f16(a.y, row, (part * GB + g) * 256 + lo, a.ldy, cols, a.tiled, v[g]);
+      if (active) store4_f16(a.y, row, gg * 256 + lo, a.ldy, cols, a.tiled, v[g]);
     } else {
       uint2 o;
       o.x = pack_half2(v[g][0], v[g][1]);
       o.y = pack_half2(v[g][2], v[g][3]);
-      *reinterpret_cast<uint2*>(&tout[(threadIdx.x >> 6) * TROW + g * 256 + lo]) = o;
+      *reinterpret_cast<uint2*>(&tout[rl * TROW + (gb0 + g) * 256 + lo]) = o;
     }
   }
   if (a.tiled) {
     // write-out of the block's 8 rows: 16-byte unit u = (chunk u / 8, row u % 8), so the 8 units
     // of a chunk are one 128-byte line of the tiled layout and a wave writes 8 whole lines
     __syncthreads();
-    const int row0 = (blockIdx.x / PARTS) * 8, c0 = part * GB * 32;
-    for (int u = threadIdx.x; u < GB * 32 * 8; u += 512) {
+    const int row0 = (blockIdx.x / PARTS) * 8, c0 = part * GBLK * 32;
+    for (int u = threadIdx.x; u < GBLK * 32 * 8; u += rot_threads<G, NORM>()) {
       const int c = u / 8, r = u % 8;
       if (row0 + r >= a.rows) continue;
       const uint4 q = *reinterpret_cast<const uint4*>(&tout[r * TROW + 8 * c]);
@@ -257,19 +288,19 @@ __global__ __launch_bounds__(512) void rot_rows_kernel(RotRowsArgs a) {
 
 template <bool NORM, bool ROT = true>
 void launch_rot_rows(const RotRowsArgs& a, int groups) {
-  const int parts = (!NORM && groups >= 6 && groups % 2 == 0) ? 2 : 1;  // the kernel's column parts (GB)
-  const dim3 grid((a.rows + 7) / 8 * parts), block(512);
+  const int parts = (!NORM && groups >= 6 && groups % 2 == 0) ? 2 : 1;  // the kernel's column parts
+  const dim3 grid((a.rows + 7) / 8 * parts);
   hipStream_t s = ns2::stream();
   switch (groups) {
 #define NS2_ROT_CASE(G) \
-    case G: rot_rows_kernel<G, NORM, ROT><<<grid, block, 0, s>>>(a); break;
+    case G: rot_rows_kernel<G, NORM, ROT><<<grid, rot_threads<G, NORM>(), 0, s>>>(a); break;
     NS2_ROT_CASE(1) NS2_ROT_CASE(2) NS2_ROT_CASE(3) NS2_ROT_CASE(4) NS2_ROT_CASE(5) NS2_ROT_CASE(6)
     NS2_ROT_CASE(7) NS2_ROT_CASE(8) NS2_ROT_CASE(9) NS2_ROT_CASE(10) NS2_ROT_CASE(11) NS2_ROT_CASE(12)
     NS2_ROT_CASE(13) NS2_ROT_CASE(14) NS2_ROT_CASE(15) NS2_ROT_CASE(16)
 #undef NS2_ROT_CASE
     // rotation only, rows up to 6144 columns (the widest block-linear input)
-    case 20: if constexpr (!NORM && ROT) rot_rows_kernel<20, NORM><<<grid, block, 0, s>>>(a); break;
-    case 24: if constexpr (!NORM && ROT) rot_rows_kernel<24, NORM><<<grid, block, 0, s>>>(a); break;
+    case 20: if constexpr (!NORM && ROT) rot_rows_kernel<20, NORM><<<grid, 512, 0, s>>>(a); break;
+    case 24: if constexpr (!NORM && ROT) rot_rows_kernel<24, NORM><<<grid, 512, 0, s>>>(a); break;
     default: break;
   }
 }
