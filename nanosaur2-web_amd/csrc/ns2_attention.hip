@@ -1462,6 +1462,7 @@ struct RowsArgsH {
   const half_t* wo;  // fp16 weight tiles of W_o [N][H*D] (tile_w16_kernel's layout)
   float* part;       // [H][Lq][N] fp32
   int N;
+  int ncs;           // OPROJ: blocks per (query block, head), blockIdx.z, each a range of N's 16-column tiles
 };
 
 // OPROJ: the block goes on from its normalized output O_h (16 queries x D of head h, rounded to
@@ -1470,7 +1471,9 @@ struct RowsArgsH {
 // shares summed by the reduction that follows it, as a split-K linear's k-range shares are.
 // Each wave takes 16-column tiles n0 = 16w, 16(w + NW), ... with v_mfma_f32_16x16x16_f16: A = O_h
 // rows from LDS (row padded by 16 bytes), B = 4 consecutive k of weight row n0 + l%16 (8 bytes of
-// one tile chunk).
+// one tile chunk). With ncs > 1, block z of a (query block, head) takes the z-th of ncs ranges of
+// the column tiles (and repeats the attention): the grid fills CUs the attention alone leaves
+// idle, and each block streams 1/ncs of the head's W_o slice.
 template <int DB, int NW, bool OPROJ = false>
 __global__ __launch_bounds__(64 * NW) void attn_rows_h_kernel(RowsArgsH a) {
   constexpr int D = 16 * DB;
@@ -1614,11 +1617,12 @@ __global__ __launch_bounds__(64 * NW) void attn_rows_h_kernel(RowsArgsH a) {
   constexpr int JC = !OPROJ ? 1 : (DB == 14 || DB == 15) ? 1 : DB == 16 ? 5 : 3;
   half4_t bf[JC][DB];
   const int nt = OPROJ ? a.N / 16 : 0;
+  const int j_lo = OPROJ ? (int)blockIdx.z * nt / a.ncs : 0, j_hi = OPROJ ? ((int)blockIdx.z + 1) * nt / a.ncs : 0;
   auto load_w = [&](int j0) {
 #pragma unroll
     for (int c = 0; c < JC; ++c) {
       const int j = j0 + c * NW;
-      if (j < nt) {  // uniform per wave
+      if (j < j_hi) {  // uniform per wave
         const int n = 16 * j + col;
 #pragma unroll
         for (int t = 0; t < DB; ++t)
@@ -1626,7 +1630,7 @@ __global__ __launch_bounds__(64 * NW) void attn_rows_h_kernel(RowsArgsH a) {
       }
     }
   };
-  if constexpr (OPROJ) load_w(wave);
+  if constexpr (OPROJ) load_w(j_lo + wave);
   if constexpr (KDMA) __syncthreads();  // every wave is done with its K rows (o_part overlays them)
 
 #pragma unroll
@@ -1689,12 +1693,12 @@ __global__ __launch_bounds__(64 * NW) void attn_rows_h_kernel(RowsArgsH a) {
     for (int t = 0; t < DB; ++t) af[t] = *reinterpret_cast<const half4_t*>(o16 + col * OS + 16 * t + 4 * grp);
     // the weight fragments of JC column tiles are loaded together (one round trip per JC tiles;
     // one tile at a time where the loop's K/V registers leave no room: D = 224, 240)
-    for (int j0 = wave; j0 < nt; j0 += JC * NW) {
-      if (j0 != wave) load_w(j0);
+    for (int j0 = j_lo + wave; j0 < j_hi; j0 += JC * NW) {
+      if (j0 != j_lo + wave) load_w(j0);
 #pragma unroll
       for (int c = 0; c < JC; ++c) {
         const int j = j0 + c * NW;
-        if (j < nt) {
+        if (j < j_hi) {
           float4_t acc = float4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
           for (int t = 0; t < DB; ++t) acc = __builtin_amdgcn_mfma_f32_16x16x16f16(af[t], bf[c][t], acc, 0, 0, 0);
@@ -1778,10 +1782,14 @@ extern "C" int ns2_attention_rows_f16kv_oproj(const float* q, const uint16_t* k,
               "%s: q, k, v rows and the weight tiles must be 16-byte aligned", fn);
   RowsArgsH a{q, reinterpret_cast<const half_t*>(k), reinterpret_cast<const half_t*>(v), nullptr, qOff, kOff, vOff,
               Lq, Lk, H, D, ldq, ldk, ldv, 0, group, causal ? 1 : 0, 1.0f / sqrtf((float)D) * kLog2e,
-              reinterpret_cast<const half_t*>(wo_tiled), part, N};
+              reinterpret_cast<const half_t*>(wo_tiled), part, N, 1};
+  // column ranges per (query block, head): up to 4, while the grid stays within one block per CU
+  // (256 tokens, 4 heads: 64 -> 256 blocks)
+  const int units = (Lq + 15) / 16 * H;
+  while (a.ncs < 4 && units * a.ncs * 2 <= kChipCUs && N / 16 >= a.ncs * 2) a.ncs *= 2;
   ns2::ProfScope prof_("attn_rows_oproj");
   hipStream_t s = ns2::stream();
-  const dim3 grid((Lq + 15) / 16, H);
+  const dim3 grid((Lq + 15) / 16, H, a.ncs);
   switch (D / 16) {
 #define NS2_ROWS_HO_CASE(N_) \
   case N_: attn_rows_h_kernel<N_, kRowsWaves, true><<<grid, 64 * kRowsWaves, 0, s>>>(a); break;
