@@ -291,10 +291,12 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs p, int spli
 
 // Split-K sum of one output row followed by the Gemma3 sublayer norms of that row (one block
 // per row): t = epilogue(sum of the splits), x += rmsnorm(t) * w_add, y = rmsnorm(x) * w_out
-// (y optional). Thread i owns columns i + 256 j (j < kRowNormCols); the splits are read four
-// at a time (16 loads in flight per thread) from clamped addresses and added in split order, as
-// splitk_reduce_kernel adds them.
+// (y optional). Thread i owns columns i + 256 j (j < C, C = ceil(N / 256)); the loads of 16
+// splits go out together (one round trip for the 16 down-projection shares of the encoder's MLP)
+// from clamped addresses, and the splits are added in split order, as splitk_reduce_kernel adds
+// them.
 constexpr int kRowNormCols = 4;
+constexpr int kRowNormSplitsInFlight = 16;
 constexpr int kRowNormMaxN = 256 * kRowNormCols;
 struct RowNorm {
   float* x;
@@ -306,8 +308,9 @@ struct RowNorm {
   // rounded once to nearest
   uint16_t* yt;
 };
+template <int C>
 __global__ __launch_bounds__(256) void splitk_add_rmsnorm_kernel(GemmArgs p, int splits, RowNorm rn) {
-  constexpr int C = kRowNormCols;
+  constexpr int ZB = kRowNormSplitsInFlight;
   __shared__ float red[4];
   const int N = p.N, tid = threadIdx.x;
   const long long mn = (long long)p.M * N, row = (long long)blockIdx.x * N;
@@ -320,16 +323,16 @@ __global__ __launch_bounds__(256) void splitk_add_rmsnorm_kernel(GemmArgs p, int
     acc[j] = 0.f;
     xv[j] = rn.x[row + col[j]];
   }
-  for (int z0 = 0; z0 < splits; z0 += 4) {
-    float v[4][C];
+  for (int z0 = 0; z0 < splits; z0 += ZB) {
+    float v[ZB][C];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
+    for (int k = 0; k < ZB; ++k) {
       const long long zo = (long long)(z0 + k < splits ? z0 + k : splits - 1) * mn + row;
 #pragma unroll
       for (int j = 0; j < C; ++j) v[k][j] = p.part[zo + col[j]];
     }
 #pragma unroll
-    for (int k = 0; k < 4; ++k)
+    for (int k = 0; k < ZB; ++k)
 #pragma unroll
       for (int j = 0; j < C; ++j)
         if (z0 + k < splits) acc[j] += v[k][j];
@@ -368,6 +371,13 @@ __global__ __launch_bounds__(256) void splitk_add_rmsnorm_kernel(GemmArgs p, int
         rn.y[row + col[j]] = v;
       }
     }
+}
+
+// The row kernel with as many column slots per thread as N needs (N <= kRowNormMaxN).
+void launch_add_rmsnorm(const GemmArgs& p, int splits, const RowNorm& rn, hipStream_t s) {
+  if (p.N <= 512) splitk_add_rmsnorm_kernel<2><<<p.M, 256, 0, s>>>(p, splits, rn);
+  else if (p.N <= 768) splitk_add_rmsnorm_kernel<3><<<p.M, 256, 0, s>>>(p, splits, rn);
+  else splitk_add_rmsnorm_kernel<kRowNormCols><<<p.M, 256, 0, s>>>(p, splits, rn);
 }
 
 // Split-K sum of a stacked q|k|v product followed by the per-head norms of app/gpu/ops.js:
@@ -934,7 +944,7 @@ int launch_gemm(const GemmArgs& p, const char* name, const RowNorm* rn = nullptr
     if (q.lr) gemm_mfma_kernel<BM, BN, WM, WN, A_F32, W_BF16, true><<<grid, (BM / WM) * (BN / WN) * 64, 0, s>>>(q);
     else gemm_mfma_kernel<BM, BN, WM, WN, A_F32, W_BF16, false><<<grid, (BM / WM) * (BN / WN) * 64, 0, s>>>(q);
     if (rn) {
-      splitk_add_rmsnorm_kernel<<<p.M, 256, 0, s>>>(q, splits, *rn);
+      launch_add_rmsnorm(q, splits, *rn, s);
     } else if (hn) {
       if (hn->D == 64) splitk_head_norm_kernel<64><<<p.M, 64, 0, s>>>(q, splits, *hn);
       else if (hn->D == 128) splitk_head_norm_kernel<128><<<p.M, 128, 0, s>>>(q, splits, *hn);
@@ -1092,7 +1102,7 @@ int ns2_parts_add_rmsnorm(const float* part, int splits, const float* bias, floa
   p.part = const_cast<float*>(part);
   const RowNorm rn{x, w_add, w_out, y, eps};
   ns2::ProfScope prof_("parts_add_rmsnorm");
-  splitk_add_rmsnorm_kernel<<<M, 256, 0, ns2::stream()>>>(p, splits, rn);
+  launch_add_rmsnorm(p, splits, rn, ns2::stream());
   NS2_LAUNCHED("parts_add_rmsnorm");
   return NS2_OK;
 }
@@ -1183,7 +1193,7 @@ int ns2_parts_add_rmsnorm_tiled(const float* part, int splits, const float* bias
   p.part = const_cast<float*>(part);
   const RowNorm rn{x, w_add, w_out, nullptr, eps, yt};
   ns2::ProfScope prof_("parts_add_rmsnorm");
-  splitk_add_rmsnorm_kernel<<<M, 256, 0, ns2::stream()>>>(p, splits, rn);
+  launch_add_rmsnorm(p, splits, rn, ns2::stream());
   NS2_LAUNCHED("parts_add_rmsnorm");
   return NS2_OK;
 }
