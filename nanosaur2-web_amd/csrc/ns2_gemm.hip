@@ -404,8 +404,8 @@ constexpr int kHeadNormMaxHeads = 8;
 template <int D>
 __global__ __launch_bounds__(D) void splitk_head_norm_kernel(GemmArgs p, int splits, HeadNorm hn) {
   constexpr int MH = kHeadNormMaxHeads;
-  __shared__ float red[D / 64];
-  __shared__ float row_buf[D];
+  __shared__ float red[D / 64 * MH];
+  __shared__ float row_buf[MH * D];
   const int tid = threadIdx.x, heads = p.N / D;
   const long long mn = (long long)p.M * p.N, m = blockIdx.x;
   // every load of the row first (unconditional, from clamped addresses): the split partials
@@ -423,29 +423,54 @@ __global__ __launch_bounds__(D) void splitk_head_norm_kernel(GemmArgs p, int spl
   const bool rope = hn.cs && m < hn.rope_rows;  // uniform per block
   const float c = rope ? hn.cs[m * half + i] : 1.f, sn = rope ? hn.cs[hn.sin_off + m * half + i] : 0.f;
   float* out = p.C + p.cOff + m * p.ldc + tid;
+  const int normed = hn.H1 + hn.H2;
+  float r[MH];
+#pragma unroll
+  for (int h = 0; h < MH; ++h) {
+    r[h] = acc[h] * p.alpha;
+    if (p.scale) r[h] *= p.scale[(h < heads ? h : heads - 1) * D + tid];
+    if (p.bias) r[h] += p.bias[(h < heads ? h : heads - 1) * D + tid];
+  }
+  // the normed heads' sums of squares together: wave sums, one barrier, then each thread adds
+  // the waves' partials in wave order (block_sum's order)
+  const int lane = tid & 63, wv = tid >> 6;
+#pragma unroll
+  for (int h = 0; h < MH; ++h) {
+    if (h >= normed) break;
+    const float ws = wave_sum(r[h] * r[h]);
+    if (lane == 0) red[wv * MH + h] = ws;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int h = 0; h < MH; ++h) {
+    if (h >= normed) break;
+    float t = 0.f;
+    for (int w = 0; w < D / 64; ++w) t += red[w * MH + h];
+    r[h] = r[h] * rsqrtf(t / (float)D + hn.eps) * (h < hn.H1 ? w1 : w2);
+  }
+  if (rope) {
+    // split-half RoPE of every normed head, the partners through LDS (one barrier)
+#pragma unroll
+    for (int h = 0; h < MH; ++h)
+      if (h < normed) row_buf[h * D + tid] = r[h];
+    __syncthreads();
+#pragma unroll
+    for (int h = 0; h < MH; ++h) {
+      if (h >= normed) break;
+      const float other = row_buf[h * D + (tid < half ? tid + half : tid - half)];
+      r[h] = tid < half ? r[h] * c - other * sn : r[h] * c + other * sn;
+    }
+  }
 #pragma unroll
   for (int h = 0; h < MH; ++h) {
     if (h >= heads) break;
-    float r = acc[h] * p.alpha;
-    if (p.scale) r *= p.scale[h * D + tid];
-    if (p.bias) r += p.bias[h * D + tid];
-    if (h < hn.H1 + hn.H2) {  // uniform per block
-      const float rs = rsqrtf(block_sum(r * r, red) / (float)D + hn.eps);
-      r = r * rs * (h < hn.H1 ? w1 : w2);
-      if (rope) {
-        row_buf[tid] = r;
-        __syncthreads();
-        const float other = row_buf[tid < half ? tid + half : tid - half];
-        r = tid < half ? r * c - other * sn : r * c + other * sn;
-        __syncthreads();
-      }
-    }
+    float v = r[h];
     if (hn.kv16 && h >= hn.H1) {  // uniform per block
       // the fp32 value as the fp32 store would hold it (no multiply-add fused with the conversion)
-      asm volatile("" : "+v"(r));
-      hn.kv16[m * hn.ldkv + (long long)(h - hn.H1) * D + tid] = (half_t)r;
+      asm volatile("" : "+v"(v));
+      hn.kv16[m * hn.ldkv + (long long)(h - hn.H1) * D + tid] = (half_t)v;
     } else {
-      out[(long long)h * D] = r;
+      out[(long long)h * D] = v;
     }
   }
 }
