@@ -518,7 +518,17 @@ struct GluDown {
   const half_t* wd;  // the next weight [Nd][I] as fp16 tiles
   float* out;        // [I/GS][M][Nd]
   int Nd, act;
+  // blocks per (16 rows, group), blockIdx.z, each a range of the Nd/16 column tiles (each repeats
+  // the group's GLU): at 256 rows two blocks per CU, each streaming half the group's weight slice
+  int ncs;
 };
+// Column ranges per (16 rows, group): doubled while the grid stays within two blocks per CU.
+inline int glu_down_ranges(int M, int N, int Nd) {
+  const long long blocks = (long long)((M + 15) / 16) * (N / 2 / kGluDownGroup);
+  int ncs = 1;
+  while (ncs < 4 && blocks * ncs * 2 <= 512 && Nd / 16 >= ncs * 2 * 8) ncs *= 2;
+  return ncs;
+}
 template <int GS>
 __global__ __launch_bounds__(512) void splitk_glu_down_kernel(GemmArgs p, int splits, GluDown gd) {
   constexpr int NW = 8, OS = GS + 8, DB = GS / 16, JC = 5, CPT = GS * 16 / 512;  // GLU columns per thread
@@ -526,6 +536,7 @@ __global__ __launch_bounds__(512) void splitk_glu_down_kernel(GemmArgs p, int sp
   const int I = p.N / 2;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, col = lane & 15, grp = lane >> 4;
   const int m0 = blockIdx.x * 16, j0 = blockIdx.y * GS, nt = gd.Nd / 16;
+  const int jlo = (int)blockIdx.z * nt / gd.ncs, jhi = ((int)blockIdx.z + 1) * nt / gd.ncs;
   // lane's fragment t of column tile jt: tiled_off(16 jt + col, j0 + 16 t + 4 grp, I), which is
   // the offset for t = 0 plus 1024 t (j0 and 16 t + 4 grp stay inside one 64-column k-tile
   // pair of chunks: k >> 6 = j0/64 + t/4, chunk 2 (t % 4) + grp/2, element 4 (grp & 1))
@@ -534,14 +545,14 @@ __global__ __launch_bounds__(512) void splitk_glu_down_kernel(GemmArgs p, int sp
 #pragma unroll
     for (int c = 0; c < JC; ++c) {
       const int jt = jt0 + c * NW;
-      if (jt < nt) {  // uniform per wave
+      if (jt < jhi) {  // uniform per wave
         const half_t* wrow = gd.wd + tiled_off(16 * jt + col, j0 + 4 * grp, I);
 #pragma unroll
         for (int t = 0; t < DB; ++t) bf[c][t] = *reinterpret_cast<const half4_t*>(wrow + 1024 * t);
       }
     }
   };
-  load_w(wave);
+  load_w(jlo + wave);
   {
     // thread: row rr, columns c8 .. c8 + CPT - 1 of the group (rows past M repeat the last row)
     static_assert(CPT == 4 || CPT == 8, "4 or 8 GLU columns per thread");
@@ -591,12 +602,12 @@ __global__ __launch_bounds__(512) void splitk_glu_down_kernel(GemmArgs p, int sp
   half4_t af[DB];
 #pragma unroll
   for (int t = 0; t < DB; ++t) af[t] = *reinterpret_cast<const half4_t*>(&g16[col * OS + 16 * t + 4 * grp]);
-  for (int jt0 = wave; jt0 < nt; jt0 += JC * NW) {
-    if (jt0 != wave) load_w(jt0);
+  for (int jt0 = jlo + wave; jt0 < jhi; jt0 += JC * NW) {
+    if (jt0 != jlo + wave) load_w(jt0);
 #pragma unroll
     for (int c = 0; c < JC; ++c) {
       const int jt = jt0 + c * NW;
-      if (jt < nt) {
+      if (jt < jhi) {
         float4_t acc = float4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int t = 0; t < DB; ++t) acc = __builtin_amdgcn_mfma_f32_16x16x16f16(af[t], bf[c][t], acc, 0, 0, 0);
@@ -975,7 +986,8 @@ int launch_gemm(const GemmArgs& p, const char* name, const RowNorm* rn = nullptr
       else if (hn->D == 128) splitk_head_norm_kernel<128><<<p.M, 128, 0, s>>>(q, splits, *hn);
       else splitk_head_norm_kernel<256><<<p.M, 256, 0, s>>>(q, splits, *hn);
     } else if (gd) {
-      splitk_glu_down_kernel<kGluDownGroup><<<dim3((p.M + 15) / 16, p.N / 2 / kGluDownGroup), 512, 0, s>>>(q, splits, *gd);
+      splitk_glu_down_kernel<kGluDownGroup>
+          <<<dim3((p.M + 15) / 16, p.N / 2 / kGluDownGroup, gd->ncs), 512, 0, s>>>(q, splits, *gd);
     } else if (glu_y) {
       const long long n = (long long)p.M * (p.N / 2);
       splitk_glu_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(q, splits, glu_y, glu_act);
@@ -1201,7 +1213,7 @@ int ns2_linear_bf16_glu_down(const float* A, int lda, const uint16_t* W, const f
   GemmArgs p{A, W, nullptr, bias, nullptr, part, nullptr, 0, 0, lda, N, M, N, K, 1.0f, NS2_ACT_NONE, 0};
   int rc = check_common(p, fn);
   if (rc) return rc;
-  const GluDown gd{reinterpret_cast<const half_t*>(wd_tiled), part, Nd, act};
+  const GluDown gd{reinterpret_cast<const half_t*>(wd_tiled), part, Nd, act, glu_down_ranges(M, N, Nd)};
   return launch_gemm<true, true>(p, "linear_bf16_glu_down", nullptr, nullptr, 0, nullptr, &gd);
 }
 
@@ -1270,10 +1282,10 @@ int ns2_linear_f16w_tiled_glu_down(const uint16_t* At, const uint16_t* Wt, const
   if (rc) return rc;
   GemmArgs q{nullptr, nullptr, nullptr, bias, nullptr, part, nullptr, 0, 0, 0, N, M, N, K, 1.0f, NS2_ACT_NONE, 0};
   q.part = gu;
-  const GluDown gd{reinterpret_cast<const half_t*>(wd_tiled), part, Nd, act};
+  const GluDown gd{reinterpret_cast<const half_t*>(wd_tiled), part, Nd, act, glu_down_ranges(M, N, Nd)};
   ns2::ProfScope prof_("glu_down");
   splitk_glu_down_kernel<kGluDownGroup>
-      <<<dim3((M + 15) / 16, N / 2 / kGluDownGroup), 512, 0, ns2::stream()>>>(q, splits, gd);
+      <<<dim3((M + 15) / 16, N / 2 / kGluDownGroup, gd.ncs), 512, 0, ns2::stream()>>>(q, splits, gd);
   NS2_LAUNCHED("glu_down");
   return NS2_OK;
 }
