@@ -1008,7 +1008,8 @@ def test_linear_bf16_glu(ns2lib, M, bias):
     assert_close(y.cpu(), ref, TOL, "linear_bf16_glu")
 
 
-@pytest.mark.parametrize("M,bias,Nd", [(256, False, 640), (37, True, 640), (1, False, 640), (100, True, 192)])
+@pytest.mark.parametrize("M,bias,Nd", [(256, False, 640), (37, True, 640), (1, False, 640), (100, True, 192),
+                                       (300, False, 640)])  # 304 blocks: one per (16 rows, group), all columns
 def test_linear_bf16_glu_down(ns2lib, M, bias, Nd):
     """ns2_linear_bf16_glu_down (Gemma3's gate/up, GELU-tanh gate and down projection,
     app/models/gemma3.js:79-83): the shares per 128-column group, summed, against
@@ -1361,6 +1362,8 @@ def test_gemma_qkv_f16kv_attention(ns2lib, L):
     (256, 4, 4, 256, 640, True),  # the Gemma3 layer at its longest prompt
     (37, 4, 4, 256, 640, True),
     (1, 4, 4, 256, 640, True),
+    (500, 4, 4, 256, 640, True),   # 128 (query block, head) units: two blocks each, half the columns
+    (600, 4, 4, 256, 640, True),   # 152 units: one block each, all the columns
     (100, 8, 2, 128, 256, False),  # other head dims, grouped K/V, several column rounds per wave
     (50, 2, 1, 96, 192, True),
 ])
@@ -1398,12 +1401,16 @@ def test_attention_rows_f16kv_oproj(ns2lib, L, H, group, D, N, causal):
     assert_close(got, ref, TOL, f"attention + o_proj vs the oracle (L={L}, D={D})")
 
 
-@pytest.mark.parametrize("M,splits,with_out,bias", [(256, 4, True, False), (37, 3, False, True), (1, 1, True, True)])
-def test_parts_add_rmsnorm(ns2lib, M, splits, with_out, bias):
+@pytest.mark.parametrize("M,splits,with_out,bias,N", [
+    (256, 4, True, False, 640), (37, 3, False, True, 640), (1, 1, True, True, 640),
+    (64, 20, True, False, 640),   # more shares than the 16 whose loads go out together
+    (40, 5, True, True, 512),     # two columns per thread
+    (40, 16, True, False, 1024),  # four columns per thread
+])
+def test_parts_add_rmsnorm(ns2lib, M, splits, with_out, bias, N):
     """ns2_parts_add_rmsnorm: the sublayer norms (app/models/gemma3.js:74-79) on a product given as
     fp32 shares, against ns2_add_rmsnorm of their sum taken in split order (bit-exact) and against
     the oracle."""
-    N = 640
     g = gen(M * 13 + splits)
     part = torch.randn(splits, M, N, generator=g)
     b = torch.randn(N, generator=g) * 0.1 if bias else None
