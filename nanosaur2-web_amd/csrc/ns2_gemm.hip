@@ -511,8 +511,9 @@ __global__ __launch_bounds__(256) void splitk_glu_kernel(GemmArgs p, int splits,
 // The I/GS shares, summed in r order, are the product without bias. Each wave takes 16-column
 // tiles n0 = 16w, 16(w + 8), ...; the weight fragments of its first JC tiles are loaded before
 // the split sums are read (they do not depend on them), the rest JC tiles per round trip.
-// GLU output columns per share: 128 makes 16 x 16 = 256 blocks at 256 rows (one per CU), each
-// streaming 160 KB of the down weight from L2 (256: 128 blocks of 320 KB, 11.3 us per layer)
+// GLU output columns per share: 128 makes 16 x 16 = 256 (16 rows, group) units at 256 rows, each
+// streaming 160 KB of the down weight from L2 (256: 128 units of 320 KB, 11.3 us per layer
+// before the column ranges below)
 constexpr int kGluDownGroup = 128;
 struct GluDown {
   const half_t* wd;  // the next weight [Nd][I] as fp16 tiles
@@ -522,11 +523,13 @@ struct GluDown {
   // the group's GLU): at 256 rows two blocks per CU, each streaming half the group's weight slice
   int ncs;
 };
-// Column ranges per (16 rows, group): doubled while the grid stays within two blocks per CU.
+// Column ranges per (16 rows, group): doubled while the grid stays within two blocks per CU
+// and every block keeps at least 8 of the 16-column tiles (one per wave).
+constexpr long long kGluDownMaxBlocks = 2 * 256;
 inline int glu_down_ranges(int M, int N, int Nd) {
   const long long blocks = (long long)((M + 15) / 16) * (N / 2 / kGluDownGroup);
   int ncs = 1;
-  while (ncs < 4 && blocks * ncs * 2 <= 512 && Nd / 16 >= ncs * 2 * 8) ncs *= 2;
+  while (ncs < 4 && blocks * ncs * 2 <= kGluDownMaxBlocks && Nd / 16 >= ncs * 2 * 8) ncs *= 2;
   return ncs;
 }
 template <int GS>
